@@ -1,0 +1,293 @@
+// ref_driver.cpp -- TEST INFRASTRUCTURE ONLY.
+//
+// A small C-ABI shim over the *real* ggml CPU backend, compiled from the sources
+// under /root/reference/third_party/ggml by oracle/Makefile.ref into
+// oracle/_ref/libqwref.so.  It is this repository's own code and calls only
+// ggml's public API.  It exists to (1) pin the CPU restatement in
+// oracle/qwmoe_oracle.cpp against the reference bit for bit, (2) write the
+// golden fixtures under tests/golden/, and (3) serve as the timed CPU baseline
+// ("kind": "reference") in bench.py.  The product library never links it.
+//
+// The MoE layer graph below is the op sequence of
+// core/runtime.cpp:861-974 (Runtime::Impl::build_moe, non-cache path):
+//   router mul_mat (869) -> soft_max (883) -> argsort_top_k (885) ->
+//   get_rows/sum_rows/clamp/div (887-897) -> 3x mul_mat_id + swiglu_split
+//   (935-938) -> weighted sum: transposed mul_mat for T=1 (940-945) or
+//   mul + add chain for T>1 (947-959).
+// An optional ggml_rms_norm (ggml/src/ggml-cpu/ops.cpp:3795-3860) follows it so
+// layers can be stacked the way the 48-layer decode benchmark does.
+
+#include "ggml.h"
+#include "ggml-cpu.h"
+
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <vector>
+
+extern "C" {
+
+// ggml_cpu_init fills the CPU backend's lookup tables (fp16 table, type
+// traits); it is idempotent and cheap after the first call.
+static void ensure_init() {
+    static bool done = false;
+    if (!done) { ggml_cpu_init(); done = true; }
+}
+
+// ggml_quantize_chunk with imatrix = NULL (ggml/src/ggml.c:7919-8000).
+size_t qwref_quantize(int type, const float * src, void * dst, int64_t nrows, int64_t n_per_row) {
+    ensure_init();
+    return ggml_quantize_chunk((enum ggml_type) type, src, dst, 0, nrows, n_per_row, nullptr);
+}
+
+// type_traits_cpu[type].from_float: the activation quantizer mul_mat_id uses.
+int qwref_from_float(int type, const float * x, void * y, int64_t n) {
+    ensure_init();
+    const struct ggml_type_traits_cpu * t = ggml_get_type_traits_cpu((enum ggml_type) type);
+    if (!t || !t->from_float) return -1;
+    t->from_float(x, y, n);
+    return 0;
+}
+
+// type_traits_cpu[type].vec_dot on one (weight row, quantized activation row).
+int qwref_vec_dot(int type, int n, const void * x, const void * y, float * s) {
+    ensure_init();
+    const struct ggml_type_traits_cpu * t = ggml_get_type_traits_cpu((enum ggml_type) type);
+    if (!t || !t->vec_dot) return -1;
+    t->vec_dot(n, s, 0, x, 0, y, 0, 1);
+    return 0;
+}
+
+int qwref_vec_dot_type(int type) {
+    ensure_init();
+    return (int) ggml_get_type_traits_cpu((enum ggml_type) type)->vec_dot_type;
+}
+
+int qwref_dequantize(int type, const void * x, float * y, int64_t n) {
+    ensure_init();
+    const struct ggml_type_traits * t = ggml_get_type_traits((enum ggml_type) type);
+    if (!t || !t->to_float) return -1;
+    t->to_float(x, y, n);
+    return 0;
+}
+
+size_t qwref_row_size(int type, int64_t n) { return ggml_row_size((enum ggml_type) type, n); }
+
+// ---------------------------------------------------------------------------
+// One MoE FFN layer on the CPU backend, built once and evaluated many times.
+
+struct qwref_layer {
+    ggml_context * wctx = nullptr;   // weights: no_alloc, data owned by the caller
+    ggml_context * ctx  = nullptr;   // activations and intermediates
+    ggml_cgraph  * gf   = nullptr;
+    ggml_tensor * x = nullptr, * logits = nullptr, * probs = nullptr, * selected = nullptr,
+                * weights = nullptr, * up = nullptr, * gate = nullptr, * act = nullptr,
+                * experts = nullptr, * out = nullptr, * xnext = nullptr;
+    std::vector<uint8_t> work;
+    int n_threads = 1;
+    int64_t H = 0, E = 0, K = 0, F = 0, T = 0;
+};
+
+// types: ggml type ids for gate/up/down expert tensors [K=H,N=F,E] / [K=F,N=H,E].
+// w_router: f32 [H, E] (ne0 = H).  rms_eps < 0 disables the trailing RMSNorm.
+qwref_layer * qwref_layer_create(int64_t H, int64_t E, int64_t k, int64_t F, int64_t T,
+                                 int type_gate, int type_up, int type_down,
+                                 const float * w_router, const void * w_gate, const void * w_up,
+                                 const void * w_down, float expert_weights_scale, float rms_eps,
+                                 int n_threads) {
+    ensure_init();
+    qwref_layer * L = new qwref_layer();
+    L->H = H; L->E = E; L->K = k; L->F = F; L->T = T; L->n_threads = n_threads;
+
+    ggml_init_params wp = { ggml_tensor_overhead() * 8, nullptr, true };
+    L->wctx = ggml_init(wp);
+    ggml_tensor * Wr = ggml_new_tensor_2d(L->wctx, GGML_TYPE_F32, H, E);
+    ggml_tensor * Wg = ggml_new_tensor_3d(L->wctx, (ggml_type) type_gate, H, F, E);
+    ggml_tensor * Wu = ggml_new_tensor_3d(L->wctx, (ggml_type) type_up, H, F, E);
+    ggml_tensor * Wd = ggml_new_tensor_3d(L->wctx, (ggml_type) type_down, F, H, E);
+    Wr->data = (void *) w_router; Wg->data = (void *) w_gate;
+    Wu->data = (void *) w_up;     Wd->data = (void *) w_down;
+
+    // intermediates: generous bound, all f32 except ids
+    size_t act_bytes = sizeof(float) * (size_t) T * (size_t) (
+        H * 4 + E * 4 + k * 8 + F * k * 4 + H * k * 4 + H * k * 2);
+    ggml_init_params ip = { act_bytes + ggml_tensor_overhead() * 256 + ggml_graph_overhead() + (1 << 20),
+                            nullptr, false };
+    L->ctx = ggml_init(ip);
+    ggml_context * ctx = L->ctx;
+
+    L->x = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, H, T);
+    ggml_tensor * logits = ggml_mul_mat(ctx, Wr, L->x);                       // [E, T]
+    ggml_tensor * probs  = ggml_soft_max(ctx, logits);
+    ggml_tensor * selected = ggml_argsort_top_k(ctx, probs, (int) k);         // [k, T] i32 view
+    ggml_tensor * probs3 = ggml_reshape_3d(ctx, probs, 1, E, T);
+    ggml_tensor * weights = ggml_get_rows(ctx, probs3, selected);             // [1, k, T]
+    weights = ggml_reshape_2d(ctx, weights, k, T);
+    ggml_tensor * wsum = ggml_sum_rows(ctx, weights);
+    wsum = ggml_clamp(ctx, wsum, 6.103515625e-5f, INFINITY);
+    weights = ggml_div(ctx, weights, wsum);
+    weights = ggml_reshape_3d(ctx, weights, 1, k, T);
+    if (expert_weights_scale != 0.0f && expert_weights_scale != 1.0f)
+        weights = ggml_scale(ctx, weights, expert_weights_scale);
+
+    ggml_tensor * x3 = ggml_reshape_3d(ctx, L->x, H, 1, T);
+    ggml_tensor * up   = ggml_mul_mat_id(ctx, Wu, x3, selected);
+    ggml_tensor * gate = ggml_mul_mat_id(ctx, Wg, x3, selected);
+    ggml_tensor * act  = ggml_swiglu_split(ctx, gate, up);
+    ggml_tensor * experts = ggml_mul_mat_id(ctx, Wd, act, selected);          // [H, k, T]
+
+    L->gf = ggml_new_graph(ctx);
+    ggml_build_forward_expand(L->gf, weights);
+    ggml_tensor * moe_out;
+    if (T == 1) {
+        ggml_tensor * et = ggml_cont(ctx, ggml_transpose(ctx, ggml_reshape_2d(ctx, experts, H, k)));
+        ggml_tensor * w  = ggml_reshape_2d(ctx, weights, k, 1);
+        moe_out = ggml_mul_mat(ctx, et, w);
+    } else {
+        ggml_tensor * ew = ggml_mul(ctx, experts, weights);
+        ggml_build_forward_expand(L->gf, ew);
+        std::vector<ggml_tensor *> cur(k);
+        for (int i = 0; i < k; ++i) {
+            cur[i] = ggml_view_2d(ctx, ew, H, T, ew->nb[2], (size_t) i * ew->nb[1]);
+            ggml_build_forward_expand(L->gf, cur[i]);
+        }
+        moe_out = cur[0];
+        for (int i = 1; i < k; ++i) {
+            moe_out = ggml_add(ctx, moe_out, cur[i]);
+            ggml_build_forward_expand(L->gf, moe_out);
+        }
+        if (k == 1) moe_out = ggml_cont(ctx, moe_out);
+    }
+    ggml_build_forward_expand(L->gf, moe_out);
+    ggml_tensor * xnext = nullptr;
+    if (rms_eps >= 0.0f) {
+        xnext = ggml_rms_norm(ctx, moe_out, rms_eps);
+        ggml_build_forward_expand(L->gf, xnext);
+    }
+    // keep intermediates observable
+    ggml_build_forward_expand(L->gf, up);
+    ggml_build_forward_expand(L->gf, gate);
+    ggml_build_forward_expand(L->gf, act);
+    ggml_build_forward_expand(L->gf, experts);
+
+    L->logits = logits; L->probs = probs; L->selected = selected; L->weights = weights;
+    L->up = up; L->gate = gate; L->act = act; L->experts = experts; L->out = moe_out; L->xnext = xnext;
+
+    ggml_cplan plan = ggml_graph_plan(L->gf, n_threads, nullptr);
+    L->work.resize(plan.work_size + 64);
+    return L;
+}
+
+void qwref_layer_free(qwref_layer * L) {
+    if (!L) return;
+    ggml_free(L->ctx);
+    ggml_free(L->wctx);
+    delete L;
+}
+
+static void copy_2d(const ggml_tensor * t, void * dst, size_t elt) {
+    // copies a (possibly strided in dim 1) 2-D tensor to a dense buffer
+    const int64_t n0 = t->ne[0], n1 = t->ne[1] * t->ne[2] * t->ne[3];
+    for (int64_t i1 = 0; i1 < n1; ++i1) {
+        memcpy((char *) dst + i1 * n0 * elt, (const char *) t->data + i1 * t->nb[1], n0 * elt);
+    }
+}
+
+// Evaluates the layer on x [T, H] (row-major == ggml [H, T]).  Any output
+// pointer may be NULL.  ids/weights are [T, k]; logits/probs [T, E];
+// gate/up/act [T, k, F]; experts [T, k, H]; out / xnext [T, H].
+int qwref_layer_eval(qwref_layer * L, const float * x, float * out, float * xnext,
+                     int32_t * ids, float * weights, float * logits, float * probs,
+                     float * gate, float * up, float * act, float * experts, int n_threads) {
+    memcpy(L->x->data, x, sizeof(float) * L->H * L->T);
+    ggml_cplan plan = ggml_graph_plan(L->gf, n_threads > 0 ? n_threads : L->n_threads, nullptr);
+    if (plan.work_size + 64 > L->work.size()) L->work.resize(plan.work_size + 64);
+    plan.work_data = L->work.data();
+    if (ggml_graph_compute(L->gf, &plan) != GGML_STATUS_SUCCESS) return -1;
+    if (out)     copy_2d(L->out, out, 4);
+    if (xnext && L->xnext) copy_2d(L->xnext, xnext, 4);
+    if (ids)     copy_2d(L->selected, ids, 4);
+    if (weights) copy_2d(L->weights, weights, 4);
+    if (logits)  copy_2d(L->logits, logits, 4);
+    if (probs)   copy_2d(L->probs, probs, 4);
+    if (gate)    copy_2d(L->gate, gate, 4);
+    if (up)      copy_2d(L->up, up, 4);
+    if (act)     copy_2d(L->act, act, 4);
+    if (experts) copy_2d(L->experts, experts, 4);
+    return 0;
+}
+
+// ggml_mul_mat_id alone on the CPU backend (ggml.c:3329-3356,
+// ggml-cpu.c:1534-1707): as [K, N, n_as] of `type`, b f32 [K, b_ne1, T]
+// (dense), ids i32 [n_ids, T] (dense) -> dst f32 [N, n_ids, T].
+int qwref_mul_mat_id(int type, int64_t K, int64_t N, int64_t n_as, const void * as,
+                     int64_t b_ne1, int64_t T, const float * b, int64_t n_ids,
+                     const int32_t * ids, float * dst, int n_threads) {
+    ensure_init();
+    ggml_init_params wp = { ggml_tensor_overhead() * 4, nullptr, true };
+    ggml_context * wctx = ggml_init(wp);
+    ggml_tensor * A = ggml_new_tensor_3d(wctx, (ggml_type) type, K, N, n_as);
+    A->data = (void *) as;
+    size_t bytes = sizeof(float) * (size_t) (K * b_ne1 * T + N * n_ids * T) + sizeof(int32_t) * n_ids * T;
+    ggml_init_params ip = { bytes + ggml_tensor_overhead() * 16 + ggml_graph_overhead() + (1 << 20), nullptr, false };
+    ggml_context * ctx = ggml_init(ip);
+    ggml_tensor * B = ggml_new_tensor_3d(ctx, GGML_TYPE_F32, K, b_ne1, T);
+    ggml_tensor * I = ggml_new_tensor_2d(ctx, GGML_TYPE_I32, n_ids, T);
+    memcpy(B->data, b, sizeof(float) * K * b_ne1 * T);
+    memcpy(I->data, ids, sizeof(int32_t) * n_ids * T);
+    ggml_tensor * C = ggml_mul_mat_id(ctx, A, B, I);
+    ggml_cgraph * gf = ggml_new_graph(ctx);
+    ggml_build_forward_expand(gf, C);
+    ggml_cplan plan = ggml_graph_plan(gf, n_threads, nullptr);
+    std::vector<uint8_t> work(plan.work_size + 64);
+    plan.work_data = work.data();
+    int rc = ggml_graph_compute(gf, &plan) == GGML_STATUS_SUCCESS ? 0 : -1;
+    if (rc == 0) memcpy(dst, C->data, sizeof(float) * N * n_ids * T);
+    ggml_free(ctx);
+    ggml_free(wctx);
+    return rc;
+}
+
+// Single-op helpers on the CPU backend, used to pin the oracle op by op.
+// op: 0 soft_max rows [E, T]; 1 argsort DESC rows (i32 out); 2 rms_norm rows
+// (param = eps); 3 swiglu_split(a = gate, b = up); 4 vec_dot_f32 via mul_mat
+// of a [n, rows] by b [n, 1].
+int qwref_unary(int op, const float * a, const float * b, int64_t ne0, int64_t ne1, float param,
+                void * dst, int n_threads) {
+    ensure_init();
+    size_t bytes = sizeof(float) * (size_t) ne0 * ne1 * 4;
+    ggml_init_params ip = { bytes + ggml_tensor_overhead() * 16 + ggml_graph_overhead() + (1 << 20), nullptr, false };
+    ggml_context * ctx = ggml_init(ip);
+    ggml_tensor * A = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, ne0, ne1);
+    memcpy(A->data, a, sizeof(float) * ne0 * ne1);
+    ggml_tensor * R = nullptr;
+    switch (op) {
+        case 0: R = ggml_soft_max(ctx, A); break;
+        case 1: R = ggml_argsort(ctx, A, GGML_SORT_ORDER_DESC); break;
+        case 2: R = ggml_rms_norm(ctx, A, param); break;
+        case 3: {
+            ggml_tensor * B = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, ne0, ne1);
+            memcpy(B->data, b, sizeof(float) * ne0 * ne1);
+            R = ggml_swiglu_split(ctx, A, B);
+            break;
+        }
+        case 4: {
+            ggml_tensor * B = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, ne0, 1);
+            memcpy(B->data, b, sizeof(float) * ne0);
+            R = ggml_mul_mat(ctx, A, B);   // [ne1, 1]
+            break;
+        }
+        default: ggml_free(ctx); return -2;
+    }
+    ggml_cgraph * gf = ggml_new_graph(ctx);
+    ggml_build_forward_expand(gf, R);
+    ggml_cplan plan = ggml_graph_plan(gf, n_threads, nullptr);
+    std::vector<uint8_t> work(plan.work_size + 64);
+    plan.work_data = work.data();
+    int rc = ggml_graph_compute(gf, &plan) == GGML_STATUS_SUCCESS ? 0 : -1;
+    if (rc == 0) memcpy(dst, R->data, ggml_nbytes(R));
+    ggml_free(ctx);
+    return rc;
+}
+
+} // extern "C"

@@ -1,0 +1,352 @@
+"""ctypes bindings for the test oracles (test infrastructure only).
+
+* ``Oracle``  -- oracle/liboracle.so, the CPU restatement of the reference path
+  (oracle/qwmoe_oracle.cpp).
+* ``RefGGML`` -- oracle/_ref/libqwref.so, the real ggml CPU backend compiled from
+  /root/reference sources plus oracle/ref_driver.cpp.  Present only where it was
+  built; tests that need it skip otherwise.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use these.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parents[1]
+ORACLE_SO = ROOT / "oracle" / "liboracle.so"
+REF_SO = ROOT / "oracle" / "_ref" / "libqwref.so"
+
+F32, Q8_0, Q4_K, Q6_K, Q8_K, I32 = 0, 8, 12, 14, 15, 26
+BLOCK = {Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210), Q8_K: (256, 292), F32: (1, 4)}
+
+
+def row_size(t: int, n: int) -> int:
+    qk, bs = BLOCK[t]
+    assert n % qk == 0, (t, n)
+    return n // qk * bs
+
+
+def vec_dot_type(t: int) -> int:
+    return Q8_0 if t == Q8_0 else Q8_K
+
+
+def _p(a: np.ndarray | None):
+    return None if a is None else C.c_void_p(a.ctypes.data)
+
+
+class Oracle:
+    def __init__(self, path: Path = ORACLE_SO):
+        if not path.exists():
+            raise FileNotFoundError(f"{path} not built (run make -C oracle)")
+        L = self.lib = C.CDLL(str(path))
+        L.orc_f32_to_f16.restype = C.c_uint16
+        L.orc_f32_to_f16.argtypes = [C.c_float]
+        L.orc_f16_to_f32.restype = C.c_float
+        L.orc_f16_to_f32.argtypes = [C.c_uint16]
+        L.orc_quantize.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_int64]
+        L.orc_from_float.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int64]
+        L.orc_dequantize.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int64]
+        L.orc_vec_dot.argtypes = [C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
+        L.orc_dot_lanes.argtypes = [C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
+        L.orc_vec_dot_f32.restype = C.c_float
+        L.orc_vec_dot_f32.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int]
+        L.orc_v_expf.restype = C.c_float
+        L.orc_v_expf.argtypes = [C.c_float]
+        L.orc_swiglu.argtypes = [C.c_int64, C.c_void_p, C.c_void_p, C.c_void_p]
+        L.orc_soft_max.argtypes = [C.c_int64, C.c_int64, C.c_void_p, C.c_void_p]
+        L.orc_argsort_desc.argtypes = [C.c_int64, C.c_int64, C.c_void_p, C.c_void_p]
+        L.orc_rms_norm.argtypes = [C.c_int64, C.c_int64, C.c_void_p, C.c_void_p, C.c_float]
+        L.orc_group_by_expert.argtypes = [C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_int64,
+                                          C.c_void_p, C.c_void_p, C.c_void_p]
+        L.orc_mul_mat_id.argtypes = [C.c_int, C.c_int64, C.c_int64, C.c_int64, C.c_void_p, C.c_size_t,
+                                     C.c_size_t, C.c_int64, C.c_int64, C.c_void_p, C.c_int64, C.c_void_p,
+                                     C.c_int64, C.c_void_p, C.c_int64, C.c_void_p]
+        L.orc_router.argtypes = [C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p,
+                                 C.c_float, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
+        L.orc_moe_layer.argtypes = ([C.c_int64] * 5 + [C.c_int] * 3 + [C.c_void_p] * 4 + [C.c_int64]
+                                    + [C.c_void_p] * 3 + [C.c_float, C.c_float] + [C.c_void_p] * 9)
+
+    # -- quantization -------------------------------------------------------
+    def quantize(self, t: int, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        n_per_row = x.shape[-1]
+        nrows = x.size // n_per_row
+        out = np.zeros(nrows * row_size(t, n_per_row), np.uint8)
+        assert self.lib.orc_quantize(t, _p(x), _p(out), nrows, n_per_row) == 0
+        return out
+
+    def from_float(self, t: int, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.zeros(row_size(t, x.size), np.uint8)
+        assert self.lib.orc_from_float(t, _p(x), _p(out), x.size) == 0
+        return out
+
+    def dequantize(self, t: int, q: np.ndarray, n: int) -> np.ndarray:
+        out = np.zeros(n, np.float32)
+        assert self.lib.orc_dequantize(t, _p(np.ascontiguousarray(q)), _p(out), n) == 0
+        return out
+
+    def vec_dot(self, t: int, n: int, xq: np.ndarray, yq: np.ndarray) -> np.float32:
+        s = np.zeros(1, np.float32)
+        self.lib.orc_vec_dot(t, n, _p(xq), _p(yq), _p(s))
+        return s[0]
+
+    def dot_lanes(self, t: int, n: int, xq: np.ndarray, yq: np.ndarray):
+        nb = n // BLOCK[t][0]
+        lanes = np.zeros((nb, 8), np.int32)
+        mins = np.zeros((nb, 4), np.int32)
+        assert self.lib.orc_dot_lanes(t, n, _p(xq), _p(yq), _p(lanes), _p(mins)) == 0
+        return lanes, mins
+
+    # -- float ops ------------------------------------------------------------
+    def vec_dot_f32(self, x, y, tail_mode=2) -> float:
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.ascontiguousarray(y, np.float32)
+        return np.float32(self.lib.orc_vec_dot_f32(x.size, _p(x), _p(y), int(tail_mode)))
+
+    def soft_max(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.zeros_like(x)
+        self.lib.orc_soft_max(x.shape[-1], x.size // x.shape[-1], _p(x), _p(y))
+        return y
+
+    def argsort_desc(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.zeros(x.shape, np.int32)
+        self.lib.orc_argsort_desc(x.shape[-1], x.size // x.shape[-1], _p(x), _p(y))
+        return y
+
+    def rms_norm(self, x: np.ndarray, eps: float) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.zeros_like(x)
+        self.lib.orc_rms_norm(x.shape[-1], x.size // x.shape[-1], _p(x), _p(y), eps)
+        return y
+
+    def swiglu(self, gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+        g = np.ascontiguousarray(gate, np.float32)
+        u = np.ascontiguousarray(up, np.float32)
+        y = np.zeros_like(g)
+        # rows are independent; the AVX2 8-lane split restarts per row
+        n = g.shape[-1]
+        for r in range(g.size // n):
+            self.lib.orc_swiglu(n, C.c_void_p(g.ctypes.data + 4 * r * n), C.c_void_p(u.ctypes.data + 4 * r * n),
+                                C.c_void_p(y.ctypes.data + 4 * r * n))
+        return y
+
+    # -- path ----------------------------------------------------------------
+    def group_by_expert(self, ids: np.ndarray, n_as: int):
+        ids = np.ascontiguousarray(ids, np.int32)
+        T, k = ids.shape
+        counts = np.zeros(n_as, np.int32)
+        offsets = np.zeros(n_as + 1, np.int32)
+        rows = np.zeros((T * k, 2), np.int32)
+        assert self.lib.orc_group_by_expert(_p(ids), k, T, k, n_as, _p(counts), _p(offsets), _p(rows)) == 0
+        return counts, offsets, rows
+
+    def mul_mat_id(self, t: int, K: int, N: int, n_as: int, w: np.ndarray, b: np.ndarray,
+                   ids: np.ndarray, slot_of: np.ndarray | None = None, n_logical: int = 0) -> np.ndarray:
+        """b: f32 [T, b_ne1, K]; ids: i32 [T, k] -> dst f32 [T, k, N]."""
+        b = np.ascontiguousarray(b, np.float32)
+        ids = np.ascontiguousarray(ids, np.int32)
+        T, b_ne1, _ = b.shape
+        k = ids.shape[1]
+        rs = row_size(t, K)
+        dst = np.zeros((T, k, N), np.float32)
+        so = None if slot_of is None else np.ascontiguousarray(slot_of, np.int32)
+        rc = self.lib.orc_mul_mat_id(t, K, N, n_as, _p(w), rs, rs * N, b_ne1, T, _p(b), k, _p(ids), k,
+                                     _p(so), n_logical, _p(dst))
+        assert rc == 0
+        return dst
+
+    def router(self, W: np.ndarray, x: np.ndarray, k: int, scale: float = 0.0):
+        E, H = W.shape
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, H)
+        T = x.shape[0]
+        ids = np.zeros((T, k), np.int32)
+        w = np.zeros((T, k), np.float32)
+        logits = np.zeros((T, E), np.float32)
+        probs = np.zeros((T, E), np.float32)
+        self.lib.orc_router(H, E, k, T, _p(np.ascontiguousarray(W, np.float32)), _p(x), scale, _p(ids),
+                            _p(w), _p(logits), _p(probs))
+        return ids, w, logits, probs
+
+    def moe_layer(self, layer: "LayerWeights", x: np.ndarray, rms_eps: float = -1.0, scale: float = 0.0):
+        H, E, k, F = layer.H, layer.E, layer.k, layer.F
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, H)
+        T = x.shape[0]
+        out = np.zeros((T, H), np.float32)
+        xnext = np.zeros((T, H), np.float32)
+        ids = np.zeros((T, k), np.int32)
+        w = np.zeros((T, k), np.float32)
+        gate = np.zeros((T, k, F), np.float32)
+        up = np.zeros((T, k, F), np.float32)
+        act = np.zeros((T, k, F), np.float32)
+        ex = np.zeros((T, k, H), np.float32)
+        sg, su, sd = (None, None, None) if layer.slot_of is None else layer.slot_of
+        rc = self.lib.orc_moe_layer(H, E, k, F, T, layer.type_gate, layer.type_up, layer.type_down,
+                                    _p(layer.router), _p(layer.gate), _p(layer.up), _p(layer.down),
+                                    layer.n_slots, _p(sg), _p(su), _p(sd), scale, rms_eps, _p(x), _p(out),
+                                    _p(xnext), _p(ids), _p(w), _p(gate), _p(up), _p(act), _p(ex))
+        assert rc == 0
+        return dict(out=out, xnext=xnext, ids=ids, weights=w, gate=gate, up=up, act=act, experts=ex)
+
+
+class LayerWeights:
+    """One MoE layer's synthetic weights, quantized on the CPU.
+
+    gate/up: [n_slots] matrices of F rows x H; down: [n_slots] matrices of H rows x F.
+    With ``permute`` the logical experts are stored at a seeded random slot
+    permutation and ``slot_of`` holds the (gate, up, down) logical->slot tables.
+    """
+
+    def __init__(self, H, E, k, F, type_gate=Q4_K, type_up=Q4_K, type_down=Q4_K, seed=0,
+                 oracle: Oracle | None = None, permute=False, zipf_skew: float = 0.0):
+        self.H, self.E, self.k, self.F = H, E, k, F
+        self.type_gate, self.type_up, self.type_down = type_gate, type_up, type_down
+        rng = np.random.default_rng(seed)
+        orc = oracle or Oracle()
+        self.router = (rng.standard_normal((E, H), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+        if zipf_skew > 0:
+            self.router *= zipf_row_scales(E, zipf_skew)[:, None]
+        wg = rng.standard_normal((E, F, H), dtype=np.float32) * np.float32(0.02)
+        wu = rng.standard_normal((E, F, H), dtype=np.float32) * np.float32(0.02)
+        wd = rng.standard_normal((E, H, F), dtype=np.float32) * np.float32(0.02)
+        self.n_slots = E
+        self.slot_of = None
+        qg = orc.quantize(type_gate, wg.reshape(-1, H)).reshape(E, -1)
+        qu = orc.quantize(type_up, wu.reshape(-1, H)).reshape(E, -1)
+        qd = orc.quantize(type_down, wd.reshape(-1, F)).reshape(E, -1)
+        if permute:
+            perms = [rng.permutation(E).astype(np.int32) for _ in range(3)]
+            pools = []
+            for q, p in zip((qg, qu, qd), perms):
+                pool = np.empty_like(q)
+                pool[p] = q          # logical expert e lives in slot p[e]
+                pools.append(pool)
+            qg, qu, qd = pools
+            self.slot_of = tuple(perms)
+        self.gate = np.ascontiguousarray(qg.reshape(-1))
+        self.up = np.ascontiguousarray(qu.reshape(-1))
+        self.down = np.ascontiguousarray(qd.reshape(-1))
+
+
+def zipf_row_scales(E: int, s: float) -> np.ndarray:
+    """Per-expert router row scales that skew top-k popularity towards low ids.
+
+    Larger logit variance for popular experts makes them win the top-k more
+    often; the scale follows a Zipf(s) rank profile, normalised to mean 1.
+    """
+    ranks = np.arange(1, E + 1, dtype=np.float64)
+    w = ranks ** (-s)
+    return (1.0 + 1.5 * w / w.max()).astype(np.float32)
+
+
+class RefGGML:
+    def __init__(self, path: Path = REF_SO):
+        if not path.exists():
+            raise FileNotFoundError(f"{path} not built (run make -C oracle ref)")
+        L = self.lib = C.CDLL(str(path))
+        L.qwref_quantize.restype = C.c_size_t
+        L.qwref_quantize.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_int64]
+        L.qwref_from_float.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int64]
+        L.qwref_vec_dot.argtypes = [C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
+        L.qwref_dequantize.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int64]
+        L.qwref_layer_create.restype = C.c_void_p
+        L.qwref_layer_create.argtypes = ([C.c_int64] * 5 + [C.c_int] * 3 + [C.c_void_p] * 4
+                                         + [C.c_float, C.c_float, C.c_int])
+        L.qwref_layer_free.argtypes = [C.c_void_p]
+        L.qwref_layer_eval.argtypes = [C.c_void_p] + [C.c_void_p] * 11 + [C.c_int]
+        L.qwref_mul_mat_id.argtypes = [C.c_int, C.c_int64, C.c_int64, C.c_int64, C.c_void_p, C.c_int64,
+                                       C.c_int64, C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p, C.c_int]
+        L.qwref_unary.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_float,
+                                  C.c_void_p, C.c_int]
+
+    def quantize(self, t, x):
+        x = np.ascontiguousarray(x, np.float32)
+        n_per_row = x.shape[-1]
+        nrows = x.size // n_per_row
+        out = np.zeros(nrows * row_size(t, n_per_row), np.uint8)
+        self.lib.qwref_quantize(t, _p(x), _p(out), nrows, n_per_row)
+        return out
+
+    def from_float(self, t, x):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros(row_size(t, x.size), np.uint8)
+        assert self.lib.qwref_from_float(t, _p(x), _p(out), x.size) == 0
+        return out
+
+    def dequantize(self, t, q, n):
+        out = np.zeros(n, np.float32)
+        assert self.lib.qwref_dequantize(t, _p(np.ascontiguousarray(q)), _p(out), n) == 0
+        return out
+
+    def vec_dot(self, t, n, xq, yq):
+        s = np.zeros(1, np.float32)
+        assert self.lib.qwref_vec_dot(t, n, _p(xq), _p(yq), _p(s)) == 0
+        return s[0]
+
+    def unary(self, op, a, b=None, param=0.0, n_threads=1):
+        a = np.ascontiguousarray(a, np.float32)
+        ne0 = a.shape[-1]
+        ne1 = a.size // ne0
+        bb = None if b is None else np.ascontiguousarray(b, np.float32)
+        if op == 1:
+            out = np.zeros(a.shape, np.int32)
+        elif op == 4:
+            out = np.zeros(ne1, np.float32)
+        else:
+            out = np.zeros(a.shape, np.float32)
+        assert self.lib.qwref_unary(op, _p(a), _p(bb), ne0, ne1, param, _p(out), n_threads) == 0
+        return out
+
+    def mul_mat_id(self, t, K, N, n_as, w, b, ids, n_threads=4):
+        b = np.ascontiguousarray(b, np.float32)
+        ids = np.ascontiguousarray(ids, np.int32)
+        T, b_ne1, _ = b.shape
+        k = ids.shape[1]
+        dst = np.zeros((T, k, N), np.float32)
+        assert self.lib.qwref_mul_mat_id(t, K, N, n_as, _p(w), b_ne1, T, _p(b), k, _p(ids), _p(dst),
+                                         n_threads) == 0
+        return dst
+
+    def layer(self, lw: LayerWeights, T: int, rms_eps: float = -1.0, scale: float = 0.0, n_threads: int = 4):
+        return RefLayer(self, lw, T, rms_eps, scale, n_threads)
+
+
+class RefLayer:
+    def __init__(self, ref: RefGGML, lw: LayerWeights, T, rms_eps, scale, n_threads):
+        assert lw.slot_of is None, "the reference graph indexes experts directly"
+        self.ref, self.lw, self.T = ref, lw, T
+        self.h = ref.lib.qwref_layer_create(lw.H, lw.E, lw.k, lw.F, T, lw.type_gate, lw.type_up,
+                                            lw.type_down, _p(lw.router), _p(lw.gate), _p(lw.up),
+                                            _p(lw.down), scale, rms_eps, n_threads)
+        assert self.h
+
+    def __call__(self, x, n_threads=0):
+        lw, T = self.lw, self.T
+        H, k, F, E = lw.H, lw.k, lw.F, lw.E
+        x = np.ascontiguousarray(x, np.float32).reshape(T, H)
+        r = dict(out=np.zeros((T, H), np.float32), xnext=np.zeros((T, H), np.float32),
+                 ids=np.zeros((T, k), np.int32), weights=np.zeros((T, k), np.float32),
+                 logits=np.zeros((T, E), np.float32), probs=np.zeros((T, E), np.float32),
+                 gate=np.zeros((T, k, F), np.float32), up=np.zeros((T, k, F), np.float32),
+                 act=np.zeros((T, k, F), np.float32), experts=np.zeros((T, k, H), np.float32))
+        rc = self.ref.lib.qwref_layer_eval(self.h, _p(x), _p(r["out"]), _p(r["xnext"]), _p(r["ids"]),
+                                           _p(r["weights"]), _p(r["logits"]), _p(r["probs"]), _p(r["gate"]),
+                                           _p(r["up"]), _p(r["act"]), _p(r["experts"]), n_threads)
+        assert rc == 0
+        return r
+
+    def __del__(self):
+        try:
+            self.ref.lib.qwref_layer_free(self.h)
+        except Exception:
+            pass
+
+
+def have_ref() -> bool:
+    return REF_SO.exists()
