@@ -1,0 +1,204 @@
+#!/usr/bin/env python3
+"""Benchmark: Qwen3-30B-A3B-shaped Q4_K MoE FFN decode on one MI355X.
+
+Workload: 48 MoE FFN layers (H=2048, E=128, top-8,
+F=768), Q4_K gate/up/down experts quantized on the GPU from seeded N(0, 0.02)
+fp32, fp32 routers N(0, 0.02), RMSNorm (eps 1e-6) between layers; batch-1
+decode, each step a fresh N(0, 1) token input pushed through all 48 layers.
+A step = one token through the whole 48-layer stack.
+
+Prints one JSON line: decode tok/s (whole job), the roofline of the dominant
+kernel measured with HIP events on its own stream, and the reference ggml CPU
+path timed on this host's cores on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+H, E, K_USED, F, N_LAYER = 2048, 128, 8, 768, 48
+RMS_EPS = 1e-6
+HBM_PEAK_GBS = 8000.0
+
+
+def algorithmic_bytes_per_token() -> int:
+    from questwend_amd import Q4_K, row_size
+    expert = 2 * F * row_size(Q4_K, H) + H * row_size(Q4_K, F)        # gate + up + down of one expert
+    router = E * H * 4
+    return N_LAYER * (K_USED * expert + router)                        # activations are negligible
+
+
+def make_weights(torch, ops, Q4_K, seed: int):
+    """Per layer: router f32 [E, H]; gate/up [E*F, row(H)]; down [E*H, row(F)] (uint8)."""
+    from questwend_amd import row_size
+    dev = "cuda:0"
+    layers = []
+    chunk = 16  # experts generated + quantized per step (bounded fp32 scratch)
+    tmp = torch.empty(chunk * F * H, dtype=torch.float32, device=dev)
+    for l in range(N_LAYER):
+        router = torch.empty((E, H), dtype=torch.float32, device=dev)
+        ops.randn_(router, seed * 1000 + l * 10 + 0, 0.0, 0.02)
+        mats = []
+        for role, (rows, cols) in enumerate(((F, H), (F, H), (H, F))):
+            q = torch.empty((E * rows, row_size(Q4_K, cols)), dtype=torch.uint8, device=dev)
+            for e0 in range(0, E, chunk):
+                n = chunk * rows * cols
+                ops.randn_(tmp[:n], seed * 1000 + l * 10 + 1 + role * 100000 + e0, 0.0, 0.02)
+                ops.quantize_chunk_into(Q4_K, tmp[:n].view(chunk * rows, cols), q[e0 * rows:(e0 + chunk) * rows])
+            mats.append(q)
+        layers.append((router, *mats))
+    torch.cuda.synchronize()
+    del tmp
+    return layers
+
+
+def cpu_baseline(layers_host, xs, budget_s: float = 15.0):
+    """Reference ggml CPU backend (oracle/_ref) on a bounded sample: the first
+    two layers' weights copied to host, decode steps until the time budget is
+    spent; scaled to the 48-layer stack."""
+    import numpy as np
+    sys.path.insert(0, str(ROOT / "tests"))
+    from oracle_lib import Q4_K, REF_SO, LayerWeights, Oracle, RefGGML
+    n_thr = min(16, os.cpu_count() or 1)
+    lws = []
+    for (router, gate, up, down) in layers_host:
+        lw = LayerWeights.__new__(LayerWeights)
+        lw.H, lw.E, lw.k, lw.F = H, E, K_USED, F
+        lw.type_gate = lw.type_up = lw.type_down = Q4_K
+        lw.router, lw.gate, lw.up, lw.down = router, gate.reshape(-1), up.reshape(-1), down.reshape(-1)
+        lw.n_slots, lw.slot_of = E, None
+        lws.append(lw)
+    if REF_SO.exists():
+        ref = RefGGML()
+        runners = [ref.layer(lw, 1, rms_eps=RMS_EPS, n_threads=n_thr) for lw in lws]
+        kind, cores = "reference", n_thr
+        step = lambda r, x: r(x, n_threads=n_thr)["xnext"]  # noqa: E731
+    else:
+        orc = Oracle()
+        runners = lws
+        kind, cores = "port", 1
+        step = lambda lw, x: orc.moe_layer(lw, x, rms_eps=RMS_EPS)["xnext"]  # noqa: E731
+    x = xs[0:1]
+    for r in runners:           # warm-up
+        x = step(r, x)
+    n_layers_run, t0 = 0, time.perf_counter()
+    i = 0
+    while time.perf_counter() - t0 < budget_s:
+        x = xs[i % len(xs): i % len(xs) + 1]
+        for r in runners:
+            x = step(r, x)
+            n_layers_run += 1
+        i += 1
+    dt = time.perf_counter() - t0
+    per_layer = dt / n_layers_run
+    return {"value": round(1.0 / (per_layer * N_LAYER), 3), "unit": "tok/s", "cores": cores, "kind": kind,
+            "sample": f"{n_layers_run} layer evaluations ({len(runners)} distinct layers, T=1) in {dt:.1f}s, "
+                      f"scaled to the 48-layer stack"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--seed", type=int, default=1)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (see DESIGN.md, sharding)",
+              file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+    from questwend_amd import Q4_K, ops, row_size
+
+    ops.init(0, 256 << 20)
+    t_gen = time.perf_counter()
+    layers = make_weights(torch, ops, Q4_K, args.seed)
+    t_gen = time.perf_counter() - t_gen
+    Ls = [ops.make_layer(H, E, K_USED, F, r, g, u, d, (Q4_K,) * 3) for (r, g, u, d) in layers]
+    n_steps = args.steps + args.warmup
+    xs = torch.empty((n_steps, H), dtype=torch.float32, device="cuda:0")
+    ops.randn_(xs, args.seed + 777, 0.0, 1.0)
+    # ping-pong activation buffers
+    buf = [torch.empty((1, H), dtype=torch.float32, device="cuda:0") for _ in range(2)]
+    out = torch.empty((1, H), dtype=torch.float32, device="cuda:0")
+    ids = torch.empty((1, K_USED), dtype=torch.int32, device="cuda:0")
+    wts = torch.empty((1, K_USED), dtype=torch.float32, device="cuda:0")
+    lib = __import__("questwend_amd").lib()
+    st = ops.stream()
+
+    def step(i: int) -> None:
+        x = xs[i:i + 1]
+        for l, L in enumerate(Ls):
+            xn = buf[l & 1]
+            rc = lib.qwmoe_ffn_layer(st, C.byref(L), x.data_ptr(), 1, out.data_ptr(), RMS_EPS, xn.data_ptr(),
+                                     ids.data_ptr(), wts.data_ptr())
+            if rc:
+                raise RuntimeError(f"qwmoe_ffn_layer failed: {rc}")
+            x = xn
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for i in range(args.steps):
+        step(args.warmup + i)
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = ev0.elapsed_time(ev1)
+    ms_per_step = wall * 1000.0 / args.steps
+    tok_s = args.steps / wall
+    abytes = algorithmic_bytes_per_token()
+    achieved = abytes * args.steps / (gpu_ms / 1000.0) / 1e9
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        host_layers = []
+        for (r, g, u, d) in layers[:2]:
+            host_layers.append((r.cpu().numpy(), g.cpu().numpy(), u.cpu().numpy(), d.cpu().numpy()))
+        cpu = cpu_baseline(host_layers, xs[: min(n_steps, 32)].cpu().numpy())
+
+    line = {
+        "metric": "decode tok/s + achieved HBM GB/s (% of 8 TB/s), Q4_K MoE FFN 30B-A3B",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_K x q8_K -> int32 -> f32",
+        "data": "synthetic (seeded N(0,0.02) weights quantized to Q4_K on the GPU; N(0,1) token inputs)",
+        "config": {"workload": "Qwen3-30B-A3B MoE FFN stack, 48 layers, batch-1 decode (configs[1])",
+                   "n_embd": H, "n_expert": E, "n_expert_used": K_USED, "n_ff_exp": F, "n_layer": N_LAYER,
+                   "weights": "Q4_K", "rms_eps": RMS_EPS, "path": "qwmoe_ffn_layer per layer"},
+        "hbm_gbs": round(achieved, 1),
+        "hbm_frac": round(achieved / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "whole decode step (qwmoe_ffn_layer x 48)",
+                     "bytes_per_launch": abytes},
+        "cpu_baseline": cpu,
+        "weight_gen_s": round(t_gen, 2),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

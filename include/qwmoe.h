@@ -1,0 +1,214 @@
+/*
+ * qwmoe.h -- C ABI of the MI355X (gfx950) quantized MoE expert-FFN library.
+ *
+ * The library replaces, for QuestWend's MoE FFN path, what the ggml backend
+ * executes for the graph that core/runtime.cpp builds per layer
+ * (Runtime::Impl::build_moe, core/runtime.cpp:861-974; build_moe_cached
+ * 1857-1887; the seg-B lambda of decode_cached_batch 2061-2089).  Paths below
+ * are relative to the reference tree; ggml sources are under
+ * third_party/ggml/.
+ *
+ * Conventions
+ *   - ggml ne/nb conventions: ne0 is the contiguous dimension, nb* are byte
+ *     strides.  Quantized block layouts are ggml's, byte for byte
+ *     (ggml/src/ggml-common.h:252-255 Q8_0, 327-337 Q4_K, 362-367 Q6_K,
+ *     371-375 Q8_K).  Type ids are ggml's (ggml/include/ggml.h:390-416).
+ *   - Every pointer argument named as data (weights, activations, ids,
+ *     outputs) is device memory owned by the caller.  The library owns only the
+ *     workspace it allocates in qwmoe_init and frees in qwmoe_shutdown; no
+ *     entry point allocates device memory.
+ *   - `stream` is a hipStream_t (NULL = the default stream).  All compute calls
+ *     are asynchronous and stream-ordered; none synchronises with the host.
+ *     Calls that use the workspace must not run concurrently on two streams.
+ *   - Results are bit-identical to ggml's CPU backend in its x86 AVX2+FMA
+ *     build for the same inputs: router ids and weights, token grouping,
+ *     quantized activations, integer block sums and fp32 outputs.
+ *   - Every function returns QWMOE_OK (0) or a negative status and never
+ *     aborts.  Errors a kernel can only see on the device (an expert id out of
+ *     range) set bits of a device status word read by qwmoe_device_status().
+ */
+#ifndef QWMOE_H
+#define QWMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QWMOE_OK 0
+#define QWMOE_ERR_INVALID_ARG (-1)
+#define QWMOE_ERR_UNSUPPORTED (-2)
+#define QWMOE_ERR_HIP (-3)
+#define QWMOE_ERR_WORKSPACE (-4)
+#define QWMOE_ERR_NOT_INITIALIZED (-5)
+
+/* ggml_type values used on the path (ggml/include/ggml.h:390-416). */
+enum qwmoe_type {
+    QWMOE_TYPE_F32 = 0,
+    QWMOE_TYPE_Q8_0 = 8,
+    QWMOE_TYPE_Q4_K = 12,
+    QWMOE_TYPE_Q6_K = 14,
+    QWMOE_TYPE_Q8_K = 15,
+    QWMOE_TYPE_I32 = 26
+};
+
+/* Device status bits (qwmoe_device_status). */
+#define QWMOE_STATUS_TOPK_TIE_SORT 1   /* a top-k tie was resolved by the exact std::sort replay (informational) */
+#define QWMOE_STATUS_BAD_ID 2          /* an ids entry was outside [0, n_as) and was skipped */
+#define QWMOE_STATUS_BAD_SLOT 4        /* a slot table entry was outside [0, n_slots) and was skipped */
+
+/* ---- library ------------------------------------------------------------ */
+
+/* Selects `device`, allocates the workspace (workspace_bytes == 0: 256 MiB).
+ * Replaces backend initialisation (ggml_backend_reg_i, ggml/src/ggml-backend-impl.h:214-227). */
+int qwmoe_init(int device, size_t workspace_bytes);
+int qwmoe_shutdown(void);
+const char * qwmoe_strerror(int status);
+/* Bytes used by the workspace of the most demanding call so far. */
+size_t qwmoe_workspace_high_water(void);
+
+/* ggml_row_size (ggml/src/ggml.c) for the supported types; 0 if unsupported. */
+size_t qwmoe_row_size(int type, int64_t ne);
+/* type_traits_cpu[type].vec_dot_type (ggml/src/ggml-cpu/ggml-cpu.c:271-335): Q8_0 -> Q8_0, Q4_K/Q6_K -> Q8_K. */
+int qwmoe_vec_dot_type(int type);
+
+/* Synchronises `stream`, returns the OR of the device status bits raised since
+ * the last clear, and clears them when `clear` != 0. */
+int qwmoe_device_status(void * stream, int32_t * status_out, int clear);
+
+/* ---- quantization --------------------------------------------------------- */
+
+/* Activation quantizer used by mul_mat_id (type_traits_cpu[vdt].from_float,
+ * ggml/src/ggml-cpu/ggml-cpu.c:1585-1620): vdt = Q8_K -> quantize_row_q8_K_ref
+ * (ggml/src/ggml-quants.c:2768-2803); vdt = Q8_0 -> the x86 AVX2
+ * quantize_row_q8_0 (ggml/src/ggml-cpu/arch/x86/quants.c:302-404).
+ * src: f32 [ne0, ne1, ne2] with byte strides nb1, nb2; dst: dense rows,
+ * row (i1 + i2 * ne1) at dst + row * qwmoe_row_size(vdt, ne0). */
+int qwmoe_quantize_act(void * stream, int vdt, const float * src, int64_t ne0, int64_t ne1, int64_t ne2,
+                       size_t nb1, size_t nb2, void * dst);
+
+/* Weight quantizer: ggml_quantize_chunk(type, src, dst, 0, nrows, n_per_row, NULL)
+ * (ggml/src/ggml.c:7919-8000) for type Q4_K (quantize_row_q4_K_ref,
+ * ggml-quants.c:1457-1527), Q6_K (quantize_row_q6_K_ref, 1869-1937) and Q8_0
+ * (quantize_row_q8_0_ref, 276-297).  Bit-identical to the CPU code. */
+int qwmoe_quantize_chunk(void * stream, int type, const float * src, void * dst, int64_t nrows, int64_t n_per_row);
+
+/* type_traits[type].to_float: dequantize_row_q8_0 / _q4_K / _q6_K
+ * (ggml-quants.c:553-566, 1529-1551, 1939-1968). */
+int qwmoe_dequantize(void * stream, int type, const void * x, float * y, int64_t n);
+
+/* Seeded synthetic N(mean, stddev) f32 data (no reference counterpart; the
+ * benchmark's weight/input generator). */
+int qwmoe_fill_randn(void * stream, float * y, int64_t n, uint64_t seed, float mean, float stddev);
+
+/* ---- the op: ggml_mul_mat_id ------------------------------------------- */
+
+/* dst[:, e, t] = as[:, :, a(ids[e, t])] . b[:, e % ne11, t]
+ * Replaces GGML_OP_MUL_MAT_ID as constructed by ggml_mul_mat_id
+ * (ggml/include/ggml.h:1445-1449, ggml/src/ggml.c:3315-3356) and computed by
+ * ggml_compute_forward_mul_mat_id (ggml/src/ggml-cpu/ggml-cpu.c:1534-1707).
+ *   as   : [ne00 = K, ne01 = N, ne02 = n_as] of `type` (Q4_K, Q6_K, Q8_0), strides nb01, nb02
+ *   b    : f32 [K, ne11, ne12 = T], strides nb11, nb12
+ *   ids  : i32 [n_ids, T], row stride ids_nb1 bytes (the strided view argsort_top_k returns is fine)
+ *   slot_of : optional [n_slot_of] table: a(id) = slot_of[id] (the in-graph
+ *          remap of core/runtime.cpp:913-919 / ExpertCache::slot_of_row,
+ *          core/expert_cache.cpp:694-697); NULL: a(id) = id
+ *   dst  : f32 [N, n_ids, T], strides nb1, nb2 (nb0 = 4)
+ * Requirements: K a multiple of 256 (Q4_K, Q6_K) or 64 (Q8_0). */
+int qwmoe_mul_mat_id(void * stream, int type, const void * as, int64_t ne00, int64_t ne01, int64_t ne02,
+                     size_t nb01, size_t nb02, const float * b, int64_t ne11, int64_t ne12, size_t nb11,
+                     size_t nb12, const int32_t * ids, int64_t n_ids, size_t ids_nb1, const int32_t * slot_of,
+                     int64_t n_slot_of, float * dst, size_t nb1, size_t nb2);
+
+/* Per-expert grouping of the (slot e, token t) pairs, in the order of
+ * ggml-cpu.c:1622-1637 (token outer, slot inner): counts[n_as],
+ * offsets[n_as + 1] (exclusive prefix sum), rows[T * n_ids][2] = (e, t). */
+int qwmoe_group_by_expert(void * stream, const int32_t * ids, int64_t n_ids, int64_t T, size_t ids_nb1,
+                          int64_t n_as, int32_t * counts, int32_t * offsets, int32_t * rows);
+
+/* ---- router and FFN tail ---------------------------------------------------- */
+
+/* Router of core/runtime.cpp:869-897: logits = mul_mat(W, x) -> soft_max ->
+ * argsort_top_k(k) -> get_rows / sum_rows / clamp(clamp_min, inf) / div
+ * (/ scale when scale is neither 0 nor 1).
+ *   W: f32 [H, E] (row e contiguous); x: f32 [H, T] with row stride x_nb1 bytes
+ *   ids, weights: [k, T] dense; probs: optional [E, T] dense.
+ * Requirements: E % 8 == 0, E <= 512, H % 4 == 0. */
+int qwmoe_router_topk(void * stream, const float * W, const float * x, int64_t H, int64_t E, int64_t k,
+                      int64_t T, size_t x_nb1, float clamp_min, float scale, int32_t * ids, float * weights,
+                      float * probs);
+
+/* ggml_swiglu_split(gate, up) = silu(gate) * up (ggml/src/ggml.c:3060-3065,
+ * ggml/src/ggml-cpu/ops.cpp:3182-3238): `rows` rows of n values, n % 8 == 0. */
+int qwmoe_swiglu(void * stream, const float * gate, const float * up, float * out, int64_t n, int64_t rows);
+
+/* Weighted expert sum of core/runtime.cpp:940-959.  experts: [H, k, T];
+ * weights: [k, T]; out: [H, T]. */
+int qwmoe_weighted_sum(void * stream, const float * experts, const float * weights, float * out, int64_t H,
+                       int64_t k, int64_t T);
+
+/* ggml_rms_norm (ggml/src/ggml-cpu/ops.cpp:3795-3860) over `rows` rows of n. */
+int qwmoe_rms_norm(void * stream, const float * x, float * y, int64_t n, int64_t rows, float eps);
+
+/* ---- fused layer ------------------------------------------------------------ */
+
+/* One MoE FFN layer's tensors: the ggml graph inputs of build_moe
+ * (core/runtime.cpp:861-974).  Expert tensors are either the full
+ * blk.N.ffn_{gate,up,down}_exps.weight [K, N, n_expert] or ExpertCache slot
+ * pools [K, N, n_slots] (core/expert_cache.h:53-62) addressed through the
+ * logical-expert -> slot rows slot_{gate,up,down} (NULL: identity). */
+typedef struct qwmoe_layer {
+    int64_t n_embd;            /* H */
+    int64_t n_expert;          /* E */
+    int64_t n_expert_used;     /* k */
+    int64_t n_ff;              /* F (n_ff_exp) */
+    float expert_weights_scale;
+    const float * router;      /* f32 [H, E]: blk.N.ffn_gate_inp.weight */
+    int type_gate, type_up, type_down;
+    const void * gate;         /* [H, F, n_slots_gate] */
+    const void * up;           /* [H, F, n_slots_up] */
+    const void * down;         /* [F, H, n_slots_down] */
+    size_t gate_nb1, gate_nb2, up_nb1, up_nb2, down_nb1, down_nb2;
+    int64_t n_slots_gate, n_slots_up, n_slots_down;
+    const int32_t * slot_gate; /* [E] or NULL */
+    const int32_t * slot_up;
+    const int32_t * slot_down;
+} qwmoe_layer;
+
+/* The whole layer for T tokens: router -> 3x mul_mat_id + swiglu -> weighted
+ * sum, then (rms_eps >= 0) x_next = rms_norm(out, rms_eps).
+ * x, out, x_next: f32 [H, T] dense.  ids_out / weights_out: optional [k, T]. */
+int qwmoe_ffn_layer(void * stream, const qwmoe_layer * layer, const float * x, int64_t T, float * out,
+                    float rms_eps, float * x_next, int32_t * ids_out, float * weights_out);
+
+/* ---- expert slot table (host) ------------------------------------------------ */
+
+/* Resident-only counterpart of ExpertCache's slot bookkeeping
+ * (core/expert_cache.h:39-166; key = layer * n_expert + expert,
+ * core/expert_cache.cpp:691-721): one (role, layer) row maps logical expert ids
+ * to slots of that role's pool.  Tables live in host memory; copy a row to the
+ * device for qwmoe_layer.slot_*.  role: 0 gate, 1 up, 2 down (ExpertCache::Role). */
+typedef struct qwmoe_slot_table qwmoe_slot_table;
+qwmoe_slot_table * qwmoe_slot_table_create(int n_layer, int n_expert);
+void qwmoe_slot_table_free(qwmoe_slot_table * t);
+/* Places every (layer, expert) of every role: identity (seed == 0) or a seeded
+ * random permutation of the n_layer * n_expert slots of each role's pool. */
+int qwmoe_slot_table_fill(qwmoe_slot_table * t, uint64_t seed);
+int qwmoe_slot_table_set(qwmoe_slot_table * t, int role, int layer, int expert, int32_t slot);
+int32_t qwmoe_slot_table_slot_of(const qwmoe_slot_table * t, int role, int layer, int expert);
+/* Dense row for (role, layer): n_expert entries (ExpertCache::slot_of_row). */
+const int32_t * qwmoe_slot_table_row(const qwmoe_slot_table * t, int role, int layer);
+
+/* ---- host-side checks (no GPU needed) ---------------------------------------- */
+
+/* The std::sort replay the router uses when top-k ties occur, run on the host:
+ * idx[0..n) = argsort of values, descending, in exactly std::sort's order. */
+int qwmoe_host_argsort_desc(const float * values, int n, int32_t * idx);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QWMOE_H */

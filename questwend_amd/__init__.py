@@ -1,0 +1,109 @@
+"""questwend_amd -- MI355X-native quantized MoE expert-FFN path for QuestWend.
+
+The product is the C-ABI library ``libqwmoe.so`` (declared in include/qwmoe.h,
+built from questwend_amd/csrc by ``questwend_amd.build``).  This module is a
+thin ctypes binding over it for Python callers, tests and the benchmark; it
+takes device pointers (e.g. ``torch.Tensor.data_ptr()``) and never falls back
+to a CPU implementation: if the library is missing it raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+LIB_PATH = PKG / "libqwmoe.so"
+
+F32, Q8_0, Q4_K, Q6_K, Q8_K, I32 = 0, 8, 12, 14, 15, 26
+BLOCK = {Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210), Q8_K: (256, 292), F32: (1, 4)}
+
+STATUS_TOPK_TIE_SORT, STATUS_BAD_ID, STATUS_BAD_SLOT = 1, 2, 4
+
+
+class QwmoeError(RuntimeError):
+    pass
+
+
+class Layer(C.Structure):
+    """Mirror of ``qwmoe_layer`` (include/qwmoe.h)."""
+
+    _fields_ = [
+        ("n_embd", C.c_int64), ("n_expert", C.c_int64), ("n_expert_used", C.c_int64), ("n_ff", C.c_int64),
+        ("expert_weights_scale", C.c_float),
+        ("router", C.c_void_p),
+        ("type_gate", C.c_int), ("type_up", C.c_int), ("type_down", C.c_int),
+        ("gate", C.c_void_p), ("up", C.c_void_p), ("down", C.c_void_p),
+        ("gate_nb1", C.c_size_t), ("gate_nb2", C.c_size_t), ("up_nb1", C.c_size_t), ("up_nb2", C.c_size_t),
+        ("down_nb1", C.c_size_t), ("down_nb2", C.c_size_t),
+        ("n_slots_gate", C.c_int64), ("n_slots_up", C.c_int64), ("n_slots_down", C.c_int64),
+        ("slot_gate", C.c_void_p), ("slot_up", C.c_void_p), ("slot_down", C.c_void_p),
+    ]
+
+
+# name -> (restype, argtypes); every exported symbol of include/qwmoe.h
+P, I64, SZ, I, F, U64 = C.c_void_p, C.c_int64, C.c_size_t, C.c_int, C.c_float, C.c_uint64
+SIGNATURES = {
+    "qwmoe_init": (I, [I, SZ]),
+    "qwmoe_shutdown": (I, []),
+    "qwmoe_strerror": (C.c_char_p, [I]),
+    "qwmoe_workspace_high_water": (SZ, []),
+    "qwmoe_row_size": (SZ, [I, I64]),
+    "qwmoe_vec_dot_type": (I, [I]),
+    "qwmoe_device_status": (I, [P, P, I]),
+    "qwmoe_quantize_act": (I, [P, I, P, I64, I64, I64, SZ, SZ, P]),
+    "qwmoe_quantize_chunk": (I, [P, I, P, P, I64, I64]),
+    "qwmoe_dequantize": (I, [P, I, P, P, I64]),
+    "qwmoe_fill_randn": (I, [P, P, I64, U64, F, F]),
+    "qwmoe_mul_mat_id": (I, [P, I, P, I64, I64, I64, SZ, SZ, P, I64, I64, SZ, SZ, P, I64, SZ, P, I64, P, SZ, SZ]),
+    "qwmoe_group_by_expert": (I, [P, P, I64, I64, SZ, I64, P, P, P]),
+    "qwmoe_router_topk": (I, [P, P, P, I64, I64, I64, I64, SZ, F, F, P, P, P]),
+    "qwmoe_swiglu": (I, [P, P, P, P, I64, I64]),
+    "qwmoe_weighted_sum": (I, [P, P, P, P, I64, I64, I64]),
+    "qwmoe_rms_norm": (I, [P, P, P, I64, I64, F]),
+    "qwmoe_ffn_layer": (I, [P, P, P, I64, P, F, P, P, P]),
+    "qwmoe_slot_table_create": (P, [I, I]),
+    "qwmoe_slot_table_free": (None, [P]),
+    "qwmoe_slot_table_fill": (I, [P, U64]),
+    "qwmoe_slot_table_set": (I, [P, I, I, I, C.c_int32]),
+    "qwmoe_slot_table_slot_of": (C.c_int32, [P, I, I, I]),
+    "qwmoe_slot_table_row": (P, [P, I, I]),
+    "qwmoe_host_argsort_desc": (I, [P, I, P]),
+}
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """Loads libqwmoe.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise QwmoeError(f"{LIB_PATH} is missing: build it with `python -m questwend_amd.build`")
+        L = C.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc: int, what: str = "") -> None:
+    if rc != 0:
+        msg = lib().qwmoe_strerror(rc).decode()
+        raise QwmoeError(f"{what}: {msg} ({rc})")
+
+
+def row_size(t: int, n: int) -> int:
+    qk, bs = BLOCK[t]
+    if n % qk:
+        raise ValueError(f"row of {n} values is not a multiple of the {qk}-value block")
+    return n // qk * bs
+
+
+def vec_dot_type(t: int) -> int:
+    return Q8_0 if t == Q8_0 else Q8_K
+
+
+from . import ops  # noqa: E402,F401  (torch-facing wrappers)

@@ -1,0 +1,395 @@
+// api.cpp -- the extern "C" boundary (include/qwmoe.h): argument validation,
+// workspace carving and dispatch to the HIP kernels.  Host code only.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <random>
+#include <vector>
+
+#include "../../include/qwmoe.h"
+#include "qw_kernels.hpp"
+#include "qw_sort.hpp"
+
+namespace {
+
+struct Library {
+    bool ready = false;
+    int device = -1;
+    uint8_t* ws = nullptr;       // device workspace arena
+    size_t ws_bytes = 0;
+    size_t high_water = 0;
+    int32_t* status = nullptr;   // device status word (first 256 bytes of the arena)
+};
+
+Library g_lib;
+std::mutex g_mu;
+
+// Bump allocator over the workspace for one call.
+struct Arena {
+    uint8_t* base;
+    size_t cap, off;
+    explicit Arena(size_t reserved) : base(g_lib.ws), cap(g_lib.ws_bytes), off(reserved) {}
+    template <typename T>
+    T* take(size_t count) {
+        off = (off + 255) & ~(size_t) 255;
+        if (off + count * sizeof(T) + 64 > cap) return nullptr;
+        T* p = (T*) (base + off);
+        off += count * sizeof(T) + 64;  // + slack: kernels may read a few bytes past a row end
+        return p;
+    }
+    ~Arena() {
+        if (off > g_lib.high_water) g_lib.high_water = off;
+    }
+};
+
+constexpr size_t kReserved = 256;  // status word lives here
+
+inline hipStream_t S(void* s) { return (hipStream_t) s; }
+
+bool weight_type_ok(int t) { return t == qw::T_Q4_K || t == qw::T_Q6_K || t == qw::T_Q8_0; }
+
+int check_k(int type, int64_t K) {
+    if (K <= 0) return QWMOE_ERR_INVALID_ARG;
+    if ((type == qw::T_Q4_K || type == qw::T_Q6_K) && K % 256 != 0) return QWMOE_ERR_UNSUPPORTED;
+    if (type == qw::T_Q8_0 && K % 64 != 0) return QWMOE_ERR_UNSUPPORTED;
+    return QWMOE_OK;
+}
+
+// Shared implementation of mul_mat_id once b is quantized and ids are grouped.
+int mmid_grouped(hipStream_t st, int type, const void* as, int64_t K, int64_t N, int64_t n_as, size_t nb01,
+                 size_t nb02, const uint8_t* bq, int64_t ne11, size_t bq_row, const int32_t* rows,
+                 const int32_t* active, const int32_t* active_off, const int32_t* n_active, int64_t max_active,
+                 const int32_t* slot_of, int64_t n_slot_of, float* dst, size_t nb1, size_t nb2) {
+    qw::MmidArgs m{};
+    m.type = type;
+    m.w = (const uint8_t*) as;
+    m.nb1 = nb01;
+    m.nb2 = nb02;
+    m.K = K;
+    m.N = N;
+    m.n_as = n_as;
+    m.act_q = bq;
+    m.b_ne1 = ne11;
+    m.act_row_bytes = bq_row;
+    m.rows = rows;
+    m.active = active;
+    m.active_off = active_off;
+    m.n_active = n_active;
+    m.slot_of = slot_of;
+    m.n_slot_of = n_slot_of;
+    m.dst = dst;
+    m.dst_nb1 = nb1;
+    m.dst_nb2 = nb2;
+    m.status = g_lib.status;
+    m.max_active = max_active;
+    return qw::launch_mmid_gemv(m, st);
+}
+
+struct Grouping {
+    int32_t *rows, *active, *active_off, *n_active, *counts, *offsets;
+    int64_t max_active;
+};
+
+int group(hipStream_t st, Arena& ar, const int32_t* ids, int64_t n_ids, int64_t T, size_t ids_nb1, int64_t n_bins,
+          int32_t* counts, int32_t* offsets, int32_t* rows_out, Grouping& G) {
+    const int64_t P = n_ids * T;
+    G.max_active = std::min<int64_t>(n_bins, P);
+    G.rows = rows_out ? rows_out : ar.take<int32_t>((size_t) (2 * P + 2));
+    G.active = ar.take<int32_t>((size_t) G.max_active + 1);
+    G.active_off = ar.take<int32_t>((size_t) G.max_active + 2);
+    G.n_active = ar.take<int32_t>(1);
+    int32_t* hist = ar.take<int32_t>((size_t) qw::GROUP_WAVES * (size_t) n_bins);
+    if (!G.rows || !G.active || !G.active_off || !G.n_active || !hist) return QWMOE_ERR_WORKSPACE;
+    G.counts = counts;
+    G.offsets = offsets;
+    qw::GroupArgs g{};
+    g.ids = ids;
+    g.n_ids = n_ids;
+    g.T = T;
+    g.ids_stride = (int64_t) (ids_nb1 / sizeof(int32_t));
+    g.n_bins = n_bins;
+    g.counts = counts;
+    g.offsets = offsets;
+    g.rows = G.rows;
+    g.active = G.active;
+    g.active_off = G.active_off;
+    g.n_active = G.n_active;
+    g.status = g_lib.status;
+    g.hist_ws = hist;
+    return qw::launch_group(g, st);
+}
+
+}  // namespace
+
+extern "C" {
+
+int qwmoe_init(int device, size_t workspace_bytes) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (g_lib.ready) {
+        if (g_lib.device == device && (workspace_bytes == 0 || workspace_bytes <= g_lib.ws_bytes)) return QWMOE_OK;
+        (void) hipFree(g_lib.ws);
+        g_lib = Library{};
+    }
+    if (hipSetDevice(device) != hipSuccess) return QWMOE_ERR_HIP;
+    const size_t bytes = workspace_bytes ? workspace_bytes : ((size_t) 256 << 20);
+    void* p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) return QWMOE_ERR_HIP;
+    if (hipMemset(p, 0, kReserved) != hipSuccess) return QWMOE_ERR_HIP;
+    if (hipDeviceSynchronize() != hipSuccess) return QWMOE_ERR_HIP;
+    g_lib.ws = (uint8_t*) p;
+    g_lib.ws_bytes = bytes;
+    g_lib.status = (int32_t*) p;
+    g_lib.device = device;
+    g_lib.ready = true;
+    return QWMOE_OK;
+}
+
+int qwmoe_shutdown(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!g_lib.ready) return QWMOE_OK;
+    (void) hipDeviceSynchronize();
+    (void) hipFree(g_lib.ws);
+    g_lib = Library{};
+    return QWMOE_OK;
+}
+
+const char* qwmoe_strerror(int status) {
+    switch (status) {
+        case QWMOE_OK: return "ok";
+        case QWMOE_ERR_INVALID_ARG: return "invalid argument";
+        case QWMOE_ERR_UNSUPPORTED: return "unsupported type or shape";
+        case QWMOE_ERR_HIP: return "HIP runtime error";
+        case QWMOE_ERR_WORKSPACE: return "workspace too small";
+        case QWMOE_ERR_NOT_INITIALIZED: return "qwmoe_init has not been called";
+    }
+    return "unknown status";
+}
+
+size_t qwmoe_workspace_high_water(void) { return g_lib.high_water; }
+
+size_t qwmoe_row_size(int type, int64_t ne) {
+    const int be = qw::block_elems(type), bb = qw::block_bytes(type);
+    if (bb == 0 || ne < 0 || ne % be != 0) return 0;
+    return (size_t) (ne / be) * (size_t) bb;
+}
+
+int qwmoe_vec_dot_type(int type) { return weight_type_ok(type) ? qw::vec_dot_type(type) : QWMOE_ERR_UNSUPPORTED; }
+
+int qwmoe_device_status(void* stream, int32_t* status_out, int clear) {
+    if (!g_lib.ready) return QWMOE_ERR_NOT_INITIALIZED;
+    int32_t v = 0;
+    if (hipStreamSynchronize(S(stream)) != hipSuccess) return QWMOE_ERR_HIP;
+    if (hipMemcpy(&v, g_lib.status, sizeof(v), hipMemcpyDeviceToHost) != hipSuccess) return QWMOE_ERR_HIP;
+    if (clear && hipMemset(g_lib.status, 0, sizeof(int32_t)) != hipSuccess) return QWMOE_ERR_HIP;
+    if (status_out) *status_out = v;
+    return QWMOE_OK;
+}
+
+int qwmoe_quantize_act(void* stream, int vdt, const float* src, int64_t ne0, int64_t ne1, int64_t ne2, size_t nb1,
+                       size_t nb2, void* dst) {
+    if (!src || !dst || ne0 <= 0 || ne1 < 0 || ne2 < 0) return QWMOE_ERR_INVALID_ARG;
+    if (vdt != qw::T_Q8_K && vdt != qw::T_Q8_0) return QWMOE_ERR_UNSUPPORTED;
+    if (ne0 % qw::block_elems(vdt) != 0) return QWMOE_ERR_UNSUPPORTED;
+    if (nb1 % 16 != 0 || nb2 % 16 != 0 || ((uintptr_t) src & 15)) return QWMOE_ERR_UNSUPPORTED;
+    return qw::launch_quantize_act(vdt, src, ne0, ne1 ? ne1 : 1, ne1 * ne2, nb1, nb2, dst, S(stream));
+}
+
+int qwmoe_quantize_chunk(void* stream, int type, const float* src, void* dst, int64_t nrows, int64_t n_per_row) {
+    if (!src || !dst || nrows < 0 || n_per_row <= 0) return QWMOE_ERR_INVALID_ARG;
+    if (!weight_type_ok(type)) return QWMOE_ERR_UNSUPPORTED;
+    if (n_per_row % qw::block_elems(type) != 0) return QWMOE_ERR_INVALID_ARG;
+    return qw::launch_quantize_weights(type, src, nrows * n_per_row, dst, S(stream));
+}
+
+int qwmoe_dequantize(void* stream, int type, const void* x, float* y, int64_t n) {
+    if (!x || !y || n < 0) return QWMOE_ERR_INVALID_ARG;
+    if (!weight_type_ok(type)) return QWMOE_ERR_UNSUPPORTED;
+    if (n % qw::block_elems(type) != 0) return QWMOE_ERR_INVALID_ARG;
+    return qw::launch_dequantize(type, x, y, n, S(stream));
+}
+
+int qwmoe_fill_randn(void* stream, float* y, int64_t n, uint64_t seed, float mean, float stddev) {
+    if (!y || n < 0) return QWMOE_ERR_INVALID_ARG;
+    return qw::launch_randn(y, n, seed, mean, stddev, S(stream));
+}
+
+int qwmoe_group_by_expert(void* stream, const int32_t* ids, int64_t n_ids, int64_t T, size_t ids_nb1, int64_t n_as,
+                          int32_t* counts, int32_t* offsets, int32_t* rows) {
+    if (!g_lib.ready) return QWMOE_ERR_NOT_INITIALIZED;
+    if (!ids || !rows || n_ids <= 0 || T < 0 || n_as <= 0 || ids_nb1 < (size_t) n_ids * 4 || ids_nb1 % 4)
+        return QWMOE_ERR_INVALID_ARG;
+    Arena ar(kReserved);
+    Grouping G{};
+    return group(S(stream), ar, ids, n_ids, T, ids_nb1, n_as, counts, offsets, rows, G);
+}
+
+int qwmoe_mul_mat_id(void* stream, int type, const void* as, int64_t ne00, int64_t ne01, int64_t ne02, size_t nb01,
+                     size_t nb02, const float* b, int64_t ne11, int64_t ne12, size_t nb11, size_t nb12,
+                     const int32_t* ids, int64_t n_ids, size_t ids_nb1, const int32_t* slot_of, int64_t n_slot_of,
+                     float* dst, size_t nb1, size_t nb2) {
+    if (!g_lib.ready) return QWMOE_ERR_NOT_INITIALIZED;
+    if (!as || !b || !ids || !dst || ne01 <= 0 || ne02 <= 0 || ne11 <= 0 || ne12 < 0 || n_ids <= 0)
+        return QWMOE_ERR_INVALID_ARG;
+    if (!weight_type_ok(type)) return QWMOE_ERR_UNSUPPORTED;
+    int rc = check_k(type, ne00);
+    if (rc) return rc;
+    const size_t rs = qwmoe_row_size(type, ne00);
+    if (nb01 < rs || nb02 < nb01 * (size_t) ne01) return QWMOE_ERR_INVALID_ARG;
+    if (ids_nb1 < (size_t) n_ids * 4 || ids_nb1 % 4) return QWMOE_ERR_INVALID_ARG;
+    if (nb1 < (size_t) ne01 * 4 || nb2 < nb1 * (size_t) n_ids) return QWMOE_ERR_INVALID_ARG;
+    if (slot_of && n_slot_of <= 0) return QWMOE_ERR_INVALID_ARG;
+    if (ne11 != 1 && ne11 != n_ids) return QWMOE_ERR_UNSUPPORTED;  // the broadcast rule e % ne11 needs ne11 | n_ids
+    if (ne12 == 0) return QWMOE_OK;
+    const int vdt = qw::vec_dot_type(type);
+    const size_t qrow = qwmoe_row_size(vdt, ne00);
+    if (qrow % 4) return QWMOE_ERR_UNSUPPORTED;
+    hipStream_t st = S(stream);
+    Arena ar(kReserved);
+    uint8_t* bq = ar.take<uint8_t>(qrow * (size_t) (ne11 * ne12) + 64);
+    if (!bq) return QWMOE_ERR_WORKSPACE;
+    rc = qwmoe_quantize_act(stream, vdt, b, ne00, ne11, ne12, nb11, nb12, bq);
+    if (rc) return rc;
+    Grouping G{};
+    const int64_t n_bins = slot_of ? n_slot_of : ne02;
+    rc = group(st, ar, ids, n_ids, ne12, ids_nb1, n_bins, nullptr, nullptr, nullptr, G);
+    if (rc) return rc;
+    return mmid_grouped(st, type, as, ne00, ne01, ne02, nb01, nb02, bq, ne11, qrow, G.rows, G.active, G.active_off,
+                        G.n_active, G.max_active, slot_of, n_slot_of, dst, nb1, nb2);
+}
+
+int qwmoe_router_topk(void* stream, const float* W, const float* x, int64_t H, int64_t E, int64_t k, int64_t T,
+                      size_t x_nb1, float clamp_min, float scale, int32_t* ids, float* weights, float* probs) {
+    if (!g_lib.ready) return QWMOE_ERR_NOT_INITIALIZED;
+    if (!W || !x || !ids || !weights || H <= 0 || E <= 0 || k <= 0 || k > E || T < 0) return QWMOE_ERR_INVALID_ARG;
+    if (E % 8 || E > 512 || H % 4 || x_nb1 % 16 || ((uintptr_t) x & 15) || ((uintptr_t) W & 15) || x_nb1 < (size_t) H * 4)
+        return QWMOE_ERR_UNSUPPORTED;
+    Arena ar(kReserved);
+    float* logits = ar.take<float>((size_t) (E * T) + 1);
+    if (!logits) return QWMOE_ERR_WORKSPACE;
+    qw::RouterArgs a{};
+    a.W = W;
+    a.x = x;
+    a.x_stride = (int64_t) (x_nb1 / 4);
+    a.H = H;
+    a.E = E;
+    a.k = k;
+    a.T = T;
+    a.clamp_min = clamp_min;
+    a.scale = scale;
+    a.ids = ids;
+    a.weights = weights;
+    a.probs = probs;
+    a.logits = nullptr;
+    a.status = g_lib.status;
+    return qw::launch_router(a, logits, S(stream));
+}
+
+int qwmoe_swiglu(void* stream, const float* gate, const float* up, float* out, int64_t n, int64_t rows) {
+    if (!gate || !up || !out || n <= 0 || rows < 0) return QWMOE_ERR_INVALID_ARG;
+    return qw::launch_swiglu(gate, up, out, rows, n, (size_t) n * 4, (size_t) n * 4, (size_t) n * 4, S(stream));
+}
+
+int qwmoe_weighted_sum(void* stream, const float* experts, const float* weights, float* out, int64_t H, int64_t k,
+                       int64_t T) {
+    if (!experts || !weights || !out || H <= 0 || k <= 0 || T < 0) return QWMOE_ERR_INVALID_ARG;
+    return qw::launch_weighted_sum(experts, weights, out, H, k, T, S(stream));
+}
+
+int qwmoe_rms_norm(void* stream, const float* x, float* y, int64_t n, int64_t rows, float eps) {
+    if (!x || !y || n <= 0 || rows < 0 || !(eps >= 0.0f)) return QWMOE_ERR_INVALID_ARG;
+    return qw::launch_rms_norm(x, y, n, rows, eps, S(stream));
+}
+
+int qwmoe_ffn_layer(void* stream, const qwmoe_layer* L, const float* x, int64_t T, float* out, float rms_eps,
+                    float* x_next, int32_t* ids_out, float* weights_out) {
+    if (!g_lib.ready) return QWMOE_ERR_NOT_INITIALIZED;
+    if (!L || !x || !out || T < 0) return QWMOE_ERR_INVALID_ARG;
+    const int64_t H = L->n_embd, E = L->n_expert, k = L->n_expert_used, F = L->n_ff;
+    if (H <= 0 || E <= 0 || k <= 0 || k > E || F <= 0 || !L->router || !L->gate || !L->up || !L->down)
+        return QWMOE_ERR_INVALID_ARG;
+    if (!weight_type_ok(L->type_gate) || !weight_type_ok(L->type_up) || !weight_type_ok(L->type_down))
+        return QWMOE_ERR_UNSUPPORTED;
+    int rc;
+    if ((rc = check_k(L->type_gate, H)) || (rc = check_k(L->type_up, H)) || (rc = check_k(L->type_down, F))) return rc;
+    if (F % 8) return QWMOE_ERR_UNSUPPORTED;
+    if (rms_eps >= 0.0f && !x_next) return QWMOE_ERR_INVALID_ARG;
+    if (T == 0) return QWMOE_OK;
+    hipStream_t st = S(stream);
+    Arena ar(kReserved);
+    int32_t* ids = ar.take<int32_t>((size_t) (k * T));
+    float* w = ar.take<float>((size_t) (k * T));
+    float* logits = ar.take<float>((size_t) (E * T));
+    float* upo = ar.take<float>((size_t) (F * k * T));
+    float* gateo = ar.take<float>((size_t) (F * k * T));
+    float* act = ar.take<float>((size_t) (F * k * T));
+    float* ex = ar.take<float>((size_t) (H * k * T));
+    if (!ids || !w || !logits || !upo || !gateo || !act || !ex) return QWMOE_ERR_WORKSPACE;
+    // router
+    qw::RouterArgs ra{};
+    ra.W = L->router;
+    ra.x = x;
+    ra.x_stride = H;
+    ra.H = H;
+    ra.E = E;
+    ra.k = k;
+    ra.T = T;
+    ra.clamp_min = 6.103515625e-5f;
+    ra.scale = L->expert_weights_scale;
+    ra.ids = ids;
+    ra.weights = w;
+    ra.status = g_lib.status;
+    if (E % 8 || E > 512 || H % 4) return QWMOE_ERR_UNSUPPORTED;
+    if ((rc = qw::launch_router(ra, logits, st))) return rc;
+    // grouping by logical expert (slot rows are injective for resident layers)
+    Grouping G{};
+    if ((rc = group(st, ar, ids, k, T, (size_t) k * 4, E, nullptr, nullptr, nullptr, G))) return rc;
+    // x quantized once per distinct activation type of gate / up
+    const int vg = qw::vec_dot_type(L->type_gate), vu = qw::vec_dot_type(L->type_up);
+    const size_t qg = qwmoe_row_size(vg, H), qu = qwmoe_row_size(vu, H);
+    uint8_t* xg = ar.take<uint8_t>(qg * (size_t) T + 64);
+    uint8_t* xu = (vu == vg) ? xg : ar.take<uint8_t>(qu * (size_t) T + 64);
+    if (!xg || !xu) return QWMOE_ERR_WORKSPACE;
+    if ((rc = qw::launch_quantize_act(vg, x, H, 1, T, (size_t) H * 4, (size_t) H * 4, xg, st))) return rc;
+    if (xu != xg && (rc = qw::launch_quantize_act(vu, x, H, 1, T, (size_t) H * 4, (size_t) H * 4, xu, st))) return rc;
+    const size_t dnb1 = (size_t) F * 4, dnb2 = (size_t) F * 4 * (size_t) k;
+    if ((rc = mmid_grouped(st, L->type_up, L->up, H, F, L->n_slots_up, L->up_nb1, L->up_nb2, xu, 1, qu, G.rows,
+                           G.active, G.active_off, G.n_active, G.max_active, L->slot_up, L->slot_up ? E : 0, upo,
+                           dnb1, dnb2)))
+        return rc;
+    if ((rc = mmid_grouped(st, L->type_gate, L->gate, H, F, L->n_slots_gate, L->gate_nb1, L->gate_nb2, xg, 1, qg,
+                           G.rows, G.active, G.active_off, G.n_active, G.max_active, L->slot_gate,
+                           L->slot_gate ? E : 0, gateo, dnb1, dnb2)))
+        return rc;
+    if ((rc = qw::launch_swiglu(gateo, upo, act, k * T, F, (size_t) F * 4, (size_t) F * 4, (size_t) F * 4, st)))
+        return rc;
+    const int vd = qw::vec_dot_type(L->type_down);
+    const size_t qd = qwmoe_row_size(vd, F);
+    uint8_t* aq = ar.take<uint8_t>(qd * (size_t) (k * T) + 64);
+    if (!aq) return QWMOE_ERR_WORKSPACE;
+    if ((rc = qw::launch_quantize_act(vd, act, F, k, k * T, (size_t) F * 4, (size_t) F * 4 * (size_t) k, aq, st)))
+        return rc;
+    if ((rc = mmid_grouped(st, L->type_down, L->down, F, H, L->n_slots_down, L->down_nb1, L->down_nb2, aq, k, qd,
+                           G.rows, G.active, G.active_off, G.n_active, G.max_active, L->slot_down,
+                           L->slot_down ? E : 0, ex, (size_t) H * 4, (size_t) H * 4 * (size_t) k)))
+        return rc;
+    if ((rc = qw::launch_weighted_sum(ex, w, out, H, k, T, st))) return rc;
+    if (rms_eps >= 0.0f && (rc = qw::launch_rms_norm(out, x_next, H, T, rms_eps, st))) return rc;
+    if (ids_out && hipMemcpyAsync(ids_out, ids, sizeof(int32_t) * k * T, hipMemcpyDeviceToDevice, st) != hipSuccess)
+        return QWMOE_ERR_HIP;
+    if (weights_out && hipMemcpyAsync(weights_out, w, sizeof(float) * k * T, hipMemcpyDeviceToDevice, st) != hipSuccess)
+        return QWMOE_ERR_HIP;
+    return QWMOE_OK;
+}
+
+int qwmoe_host_argsort_desc(const float* values, int n, int32_t* idx) {
+    if (!values || !idx || n < 0) return QWMOE_ERR_INVALID_ARG;
+    for (int i = 0; i < n; ++i) idx[i] = i;
+    qw::libstdcxx_sort_desc(idx, n, values);
+    return QWMOE_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,111 @@
+// ffn.hip -- the element-wise tail of the MoE FFN, bit-identical to the
+// reference CPU path.
+//   swiglu_split(gate, up)   ggml/src/ggml-cpu/ops.cpp:3182-3238, vec.cpp:417-445 (AVX2 ggml_v_silu)
+//   weighted expert sum      core/runtime.cpp:940-959: T == 1 -> mul_mat of the
+//                            transposed experts by the weights (ggml_vec_dot_f32 of
+//                            length k); T > 1 -> mul by the weights, then an add
+//                            chain in slot order
+//   rms_norm                 ggml/src/ggml-cpu/ops.cpp:3795-3860
+#include "qw_kernels.hpp"
+
+namespace qw {
+
+// Rows of n values; n % 8 == 0 so every value takes the 8-lane SIMD path.
+__global__ void k_swiglu(const float* __restrict__ gate, const float* __restrict__ up, float* __restrict__ out,
+                         int64_t n_rows, int64_t n, size_t gs, size_t us, size_t os) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_rows * n) return;
+    const int64_t r = i / n, c = i % n;
+    const float g = ((const float*) ((const char*) gate + r * gs))[c];
+    const float u = ((const float*) ((const char*) up + r * us))[c];
+    ((float*) ((char*) out + r * os))[c] = v_silu(g) * u;
+}
+
+int launch_swiglu(const float* gate, const float* up, float* out, int64_t n_rows, int64_t n, size_t g_stride,
+                  size_t u_stride, size_t o_stride, hipStream_t stream) {
+    if (n % 8 != 0) return -2;
+    const int64_t tot = n_rows * n;
+    if (tot == 0) return 0;
+    hipLaunchKernelGGL(k_swiglu, dim3((unsigned) ((tot + 255) / 256)), dim3(256), 0, stream, gate, up, out, n_rows, n,
+                       g_stride, u_stride, o_stride);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+// ggml_vec_dot_f32 (AVX, vec.cpp:11-140) of x (stride xs) and y, one thread.
+__device__ __forceinline__ float vec_dot_f32_avx(int64_t n, const float* x, int64_t xs, const float* y) {
+    const int64_t np = n & ~(int64_t) 31;
+    float sumf;
+    if (np > 0) {
+        float c[32];
+        for (int i = 0; i < 32; ++i) c[i] = 0.0f;
+        for (int64_t s = 0; s < np; s += 32)
+            for (int i = 0; i < 32; ++i) c[i] = __builtin_fmaf(x[(s + i) * xs], y[s + i], c[i]);
+        float s8[8];
+        for (int l = 0; l < 8; ++l) s8[l] = (c[l] + c[16 + l]) + (c[8 + l] + c[24 + l]);
+        float t0[4];
+        for (int l = 0; l < 4; ++l) t0[l] = s8[l] + s8[l + 4];
+        sumf = (t0[0] + t0[1]) + (t0[2] + t0[3]);
+    } else {
+        sumf = 0.0f;
+    }
+    const int64_t nv = np + ((n - np) & ~(int64_t) 3);
+    for (int64_t i = np; i < n; ++i)
+        sumf = (i < nv) ? sumf + x[i * xs] * y[i] : __builtin_fmaf(x[i * xs], y[i], sumf);
+    return sumf;
+}
+
+// experts: [T][k][H]; weights: [T][k]; out: [T][H]
+__global__ void k_weighted_sum(const float* __restrict__ ex, const float* __restrict__ w, float* __restrict__ out,
+                               int64_t H, int64_t k, int64_t T) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= H * T) return;
+    const int64_t t = i / H, h = i % H;
+    const float* e = ex + t * k * H + h;
+    const float* wt = w + t * k;
+    if (T == 1) {
+        out[i] = vec_dot_f32_avx(k, e, H, wt);
+    } else {
+        float acc = e[0] * wt[0];
+        for (int64_t s = 1; s < k; ++s) acc = acc + e[s * H] * wt[s];
+        out[i] = acc;
+    }
+}
+
+int launch_weighted_sum(const float* experts, const float* weights, float* out, int64_t H, int64_t k, int64_t T,
+                        hipStream_t stream) {
+    const int64_t tot = H * T;
+    if (tot == 0) return 0;
+    hipLaunchKernelGGL(k_weighted_sum, dim3((unsigned) ((tot + 255) / 256)), dim3(256), 0, stream, experts, weights,
+                       out, H, k, T);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+// One row per 256-thread block.  The reference sums x*x in double, in order;
+// the tree order used here can only differ after the final rounding to float
+// when the sum lies within ~1e-13 (relative) of a float rounding boundary.
+__global__ void __launch_bounds__(256) k_rms_norm(const float* __restrict__ x, float* __restrict__ y, int64_t n,
+                                                  float eps) {
+    __shared__ double part[4];
+    const float* xr = x + (int64_t) blockIdx.x * n;
+    float* yr = y + (int64_t) blockIdx.x * n;
+    double s = 0.0;
+    for (int64_t i = threadIdx.x; i < n; i += 256) {
+        const float v = xr[i];
+        s += (double) (v * v);
+    }
+    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    const double tot = (part[0] + part[1]) + (part[2] + part[3]);
+    const float mean = (float) (tot / (double) n);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    for (int64_t i = threadIdx.x; i < n; i += 256) yr[i] = xr[i] * scale;
+}
+
+int launch_rms_norm(const float* x, float* y, int64_t n, int64_t rows, float eps, hipStream_t stream) {
+    if (rows == 0) return 0;
+    hipLaunchKernelGGL(k_rms_norm, dim3((unsigned) rows), dim3(256), 0, stream, x, y, n, eps);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+}  // namespace qw

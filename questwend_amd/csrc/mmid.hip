@@ -1,0 +1,353 @@
+// mmid.hip -- ggml_mul_mat_id on the GPU: per-expert grouping and the
+// quantized GEMV over grouped rows.
+//
+// Contract (ggml/src/ggml.c:3315-3328):  dst[:, e, t] = as[:, :, ids[e, t]] . b[:, e % b_ne1, t]
+// CPU semantics reproduced (ggml/src/ggml-cpu/ggml-cpu.c:1534-1707):
+//   * b is quantized to the weight type's vec_dot_type first (quantize.hip);
+//   * rows are grouped per expert with token outer, slot inner (1622-1637);
+//   * each output is vec_dot(row, quantized column); here every output equals the
+//     AVX2 vec_dot bit for bit (arch/x86/quants.c:1308-1370, 2038-2115, 2426-2508):
+//     the same 8 integer lanes per super-block, the same fma chain over blocks and
+//     the same horizontal-sum tree.
+#include "qw_kernels.hpp"
+
+namespace qw {
+
+// ---------------------------------------------------------------------------
+// Grouping: stable counting sort of the (e, t) pairs by bin (= ids value).
+// One workgroup of GROUP_WAVES waves; wave w owns a contiguous slice of the
+// flattened pair index f = t * n_ids + e, so slice order == ggml row order.
+
+__device__ __forceinline__ uint64_t lanemask_lt() {
+    const int lane = threadIdx.x & 63;
+    return lane == 0 ? 0ull : (~0ull >> (64 - lane));
+}
+
+__global__ void __launch_bounds__(GROUP_WAVES * 64) k_group(GroupArgs g) {
+    const int lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6;
+    const int64_t P = g.T * g.n_ids;
+    const int64_t S = (P + GROUP_WAVES - 1) / GROUP_WAVES;
+    const int64_t f0 = w * S, f1 = (f0 + S < P) ? f0 + S : P;
+    // Per-slice counters live in global memory and are only touched through
+    // L2 atomics, so no lane ever reads a stale per-CU cached copy.
+    int32_t* hist = g.hist_ws + (int64_t) w * g.n_bins;
+    for (int64_t a = lane; a < g.n_bins; a += 64) __hip_atomic_store(hist + a, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    // phase A: per-slice histogram by peeling equal keys within each 64-chunk
+    for (int64_t c = f0; c < f1; c += 64) {
+        const int64_t f = c + lane;
+        int key = -1;
+        if (f < f1) {
+            const int64_t t = f / g.n_ids, e = f % g.n_ids;
+            key = g.ids[t * g.ids_stride + e];
+            if (key < 0 || key >= g.n_bins) {
+                if (g.status) atomicOr(g.status, 2);
+                key = -1;
+            }
+        }
+        uint64_t pending = __ballot(key >= 0);
+        while (pending) {
+            const int leader = __ffsll((unsigned long long) pending) - 1;
+            const int k = __shfl(key, leader);
+            const uint64_t m = __ballot(key == k);
+            if (lane == leader) atomicAdd(hist + k, (int32_t) __popcll(m));
+            pending &= ~m;
+        }
+    }
+    __syncthreads();
+    // phase B: totals, exclusive scan over bins, per-slice bases, active list.
+    // Each thread scans a contiguous chunk of bins; chunk sums are scanned in LDS.
+    __shared__ int32_t part_cnt[GROUP_WAVES * 64];
+    __shared__ int32_t part_act[GROUP_WAVES * 64];
+    const int nthr = GROUP_WAVES * 64;
+    const int64_t per = (g.n_bins + nthr - 1) / nthr;
+    const int64_t b0 = threadIdx.x * per, b1 = (b0 + per < g.n_bins) ? b0 + per : g.n_bins;
+    int32_t csum = 0, asum = 0;
+    for (int64_t a = b0; a < b1; ++a) {
+        int32_t tot = 0;
+        for (int ww = 0; ww < GROUP_WAVES; ++ww)
+            tot += __hip_atomic_load(g.hist_ws + (int64_t) ww * g.n_bins + a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        csum += tot;
+        asum += tot > 0;
+    }
+    part_cnt[threadIdx.x] = csum;
+    part_act[threadIdx.x] = asum;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int32_t rc = 0, ra = 0;
+        for (int i = 0; i < nthr; ++i) {
+            const int32_t c = part_cnt[i], q = part_act[i];
+            part_cnt[i] = rc;
+            part_act[i] = ra;
+            rc += c;
+            ra += q;
+        }
+        if (g.n_active) *g.n_active = ra;
+        if (g.offsets) g.offsets[g.n_bins] = rc;
+        if (g.active_off) g.active_off[ra] = rc;
+    }
+    __syncthreads();
+    int32_t off = part_cnt[threadIdx.x], aidx = part_act[threadIdx.x];
+    for (int64_t a = b0; a < b1; ++a) {
+        int32_t run = off, tot = 0;
+        for (int ww = 0; ww < GROUP_WAVES; ++ww) {
+            int32_t* h = g.hist_ws + (int64_t) ww * g.n_bins + a;
+            const int32_t c = __hip_atomic_exchange(h, run, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // -> write cursor
+            run += c;
+            tot += c;
+        }
+        if (g.counts) g.counts[a] = tot;
+        if (g.offsets) g.offsets[a] = off;
+        if (tot > 0) {
+            g.active[aidx] = (int32_t) a;
+            g.active_off[aidx] = off;
+            ++aidx;
+        }
+        off += tot;
+    }
+    __syncthreads();
+    // phase C: stable scatter of (e, t) pairs
+    for (int64_t c = f0; c < f1; c += 64) {
+        const int64_t f = c + lane;
+        int key = -1;
+        int64_t t = 0, e = 0;
+        if (f < f1) {
+            t = f / g.n_ids;
+            e = f % g.n_ids;
+            key = g.ids[t * g.ids_stride + e];
+            if (key < 0 || key >= g.n_bins) key = -1;
+        }
+        uint64_t pending = __ballot(key >= 0);
+        while (pending) {
+            const int leader = __ffsll((unsigned long long) pending) - 1;
+            const int k = __shfl(key, leader);
+            const uint64_t m = __ballot(key == k);
+            int32_t base = 0;
+            if (lane == leader) base = atomicAdd(hist + k, (int32_t) __popcll(m));
+            base = __shfl(base, leader);
+            if (key == k) {
+                const int32_t pos = base + __popcll(m & lanemask_lt());
+                g.rows[2 * pos] = (int32_t) e;
+                g.rows[2 * pos + 1] = (int32_t) t;
+            }
+            pending &= ~m;
+        }
+    }
+}
+
+int launch_group(const GroupArgs& g, hipStream_t stream) {
+    if (g.n_bins <= 0) return -2;
+    hipLaunchKernelGGL(k_group, dim3(1), dim3(GROUP_WAVES * 64), 0, stream, g);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+// ---------------------------------------------------------------------------
+// GEMV over grouped rows.  Workgroup = 4 waves = MMID_ROWS weight rows of one
+// expert matrix, staged once in LDS and applied to every token routed to it.
+// Lane (row, n): n is the AVX2 lane index 0..7 of the reference reduction.
+
+constexpr int MMID_ROWS = 32;   // rows per workgroup (8 per wave)
+constexpr int MMID_CT = 8;      // activation rows staged per pass
+
+__device__ __forceinline__ uint32_t lds_u32(const uint32_t* lds, uint32_t byte_off) {
+    const uint32_t lo = lds[byte_off >> 2], hi = lds[(byte_off >> 2) + 1];
+    return __builtin_amdgcn_alignbyte(hi, lo, byte_off & 3);
+}
+__device__ __forceinline__ uint32_t lds_u32a(const uint32_t* lds, uint32_t byte_off) { return lds[byte_off >> 2]; }
+__device__ __forceinline__ uint16_t lds_u16(const uint32_t* lds, uint32_t byte_off) {
+    return (uint16_t) (lds_u32(lds, byte_off) & 0xffff);
+}
+__device__ __forceinline__ float lds_f32(const uint32_t* lds, uint32_t byte_off) { return bitsf(lds_u32(lds, byte_off)); }
+
+// Row dot products from LDS for one (row, n) lane.  Returns the lane's
+// contribution after the 8-lane reduction (valid in lane n == 0 of the group).
+template <int TYPE>
+__device__ __forceinline__ float row_dot_lds(const uint32_t* lds, uint32_t wbase, uint32_t abase, int nb, int n);
+
+template <>
+__device__ __forceinline__ float row_dot_lds<T_Q4_K>(const uint32_t* lds, uint32_t wbase, uint32_t abase, int nb, int n) {
+    float acc = 0.0f, accm = 0.0f;
+    for (int b = 0; b < nb; ++b) {
+        const uint32_t blk = wbase + 144u * b;
+        const uint32_t yb = abase + 292u * b;
+        const uint32_t h0 = lds_u32(lds, blk);
+        const uint32_t s0 = lds_u32(lds, blk + 4), s1 = lds_u32(lds, blk + 8), s2 = lds_u32(lds, blk + 12);
+        const uint8_t q[12] = {(uint8_t) s0, (uint8_t) (s0 >> 8), (uint8_t) (s0 >> 16), (uint8_t) (s0 >> 24),
+                               (uint8_t) s1, (uint8_t) (s1 >> 8), (uint8_t) (s1 >> 16), (uint8_t) (s1 >> 24),
+                               (uint8_t) s2, (uint8_t) (s2 >> 8), (uint8_t) (s2 >> 16), (uint8_t) (s2 >> 24)};
+        int sc[8], mn[8];
+        for (int j = 0; j < 8; ++j) scale_min_k4(j, q, sc[j], mn[j]);
+        int sumi = 0;
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t wq = lds_u32(lds, blk + 16 + 32 * j + 4 * n);
+            const int lo = (int) (wq & 0x0F0F0F0Fu), hi = (int) ((wq >> 4) & 0x0F0F0F0Fu);
+            const int alo = (int) lds_u32(lds, yb + 4 + 64 * j + 4 * n);
+            const int ahi = (int) lds_u32(lds, yb + 4 + 64 * j + 32 + 4 * n);
+            sumi += sc[2 * j] * sdot4(lo, alo, 0) + sc[2 * j + 1] * sdot4(hi, ahi, 0);
+        }
+        const float yd = lds_f32(lds, yb);
+        const float d = yd * h2f((uint16_t) (h0 & 0xffff));
+        acc = __builtin_fmaf(d, (float) sumi, acc);
+        if (n < 4) {
+            const uint32_t bs01 = lds_u32(lds, yb + 260 + 8 * n), bs23 = lds_u32(lds, yb + 260 + 8 * n + 4);
+            const int q8s0 = (int) (int16_t) (bs01 & 0xffff) + (int) (int16_t) (bs01 >> 16);
+            const int q8s1 = (int) (int16_t) (bs23 & 0xffff) + (int) (int16_t) (bs23 >> 16);
+            const int prod = mn[2 * n] * q8s0 + mn[2 * n + 1] * q8s1;
+            const float dmin = -yd * h2f((uint16_t) (h0 >> 16));
+            accm = __builtin_fmaf(dmin, (float) prod, accm);
+        }
+    }
+    // hsum_float_8(acc) + ((m0 + m2) + (m1 + m3))
+    float a = acc;
+    a = a + __shfl_down(a, 4, 8);
+    a = a + __shfl_down(a, 2, 8);
+    a = a + __shfl_down(a, 1, 8);
+    float m = accm;
+    m = m + __shfl_down(m, 2, 8);
+    m = m + __shfl_down(m, 1, 8);
+    return a + m;
+}
+
+template <>
+__device__ __forceinline__ float row_dot_lds<T_Q6_K>(const uint32_t* lds, uint32_t wbase, uint32_t abase, int nb, int n) {
+    float acc = 0.0f;
+    const int g = n >= 4 ? 1 : 0;
+    for (int b = 0; b < nb; ++b) {
+        const uint32_t blk = wbase + 210u * b;
+        const uint32_t yb = abase + 292u * b;
+        int sc[16];
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t s = lds_u32(lds, blk + 192 + 4 * i);
+            sc[4 * i + 0] = (int) (int8_t) (s & 0xff);
+            sc[4 * i + 1] = (int) (int8_t) ((s >> 8) & 0xff);
+            sc[4 * i + 2] = (int) (int8_t) ((s >> 16) & 0xff);
+            sc[4 * i + 3] = (int) (int8_t) (s >> 24);
+        }
+        int sumi = 0;
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t qa = lds_u32(lds, blk + 64 * j + 4 * n);
+            const uint32_t qb = lds_u32(lds, blk + 64 * j + 32 + 4 * n);
+            const uint32_t qh = lds_u32(lds, blk + 128 + 32 * j + 4 * n);
+            const int q0 = (int) ((qa & 0x0F0F0F0Fu) | ((qh & 0x03030303u) << 4));
+            const int q1 = (int) ((qb & 0x0F0F0F0Fu) | ((qh & 0x0C0C0C0Cu) << 2));
+            const int q2 = (int) (((qa >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u));
+            const int q3 = (int) (((qb >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u));
+            const uint32_t y = yb + 4 + 128 * j + 4 * n;
+            sumi += sc[8 * j + 0 + g] * sdot4(q0, (int) lds_u32(lds, y), 0);
+            sumi += sc[8 * j + 2 + g] * sdot4(q1, (int) lds_u32(lds, y + 32), 0);
+            sumi += sc[8 * j + 4 + g] * sdot4(q2, (int) lds_u32(lds, y + 64), 0);
+            sumi += sc[8 * j + 6 + g] * sdot4(q3, (int) lds_u32(lds, y + 96), 0);
+        }
+        const uint32_t bs = lds_u32(lds, yb + 260 + 4 * n);
+        sumi -= 32 * ((int) (int16_t) (bs & 0xffff) * sc[2 * n] + (int) (int16_t) (bs >> 16) * sc[2 * n + 1]);
+        const float d = lds_f32(lds, yb) * h2f(lds_u16(lds, blk + 208));
+        acc = __builtin_fmaf(d, (float) sumi, acc);
+    }
+    float a = acc;
+    a = a + __shfl_down(a, 4, 8);
+    a = a + __shfl_down(a, 2, 8);
+    a = a + __shfl_down(a, 1, 8);
+    return a;
+}
+
+template <>
+__device__ __forceinline__ float row_dot_lds<T_Q8_0>(const uint32_t* lds, uint32_t wbase, uint32_t abase, int nb, int n) {
+    float acc = 0.0f;
+    for (int b = 0; b < nb; ++b) {
+        const uint32_t blk = wbase + 34u * b;
+        const uint32_t yb = abase + 34u * b;
+        const int sumi = sdot4((int) lds_u32(lds, blk + 2 + 4 * n), (int) lds_u32(lds, yb + 2 + 4 * n), 0);
+        const float d = h2f(lds_u16(lds, blk)) * h2f(lds_u16(lds, yb));
+        acc = __builtin_fmaf(d, (float) sumi, acc);
+    }
+    float a = acc;
+    a = a + __shfl_down(a, 4, 8);
+    a = a + __shfl_down(a, 2, 8);
+    a = a + __shfl_down(a, 1, 8);
+    return a;
+}
+
+__host__ __device__ inline uint32_t mmid_slot_bytes(size_t row_bytes) {
+    return (uint32_t) (((row_bytes + 15 + 15) / 16) * 16 + 16);
+}
+
+template <int TYPE>
+__global__ void __launch_bounds__(256) k_mmid_gemv(MmidArgs m) {
+    extern __shared__ uint32_t lds[];
+    const int g = blockIdx.y;
+    if (g >= *m.n_active) return;
+    const int bin = m.active[g];
+    int64_t mat = bin;
+    if (m.slot_of) mat = (bin < m.n_slot_of) ? m.slot_of[bin] : -1;
+    if (mat < 0 || mat >= m.n_as) {
+        if (threadIdx.x == 0 && m.status) atomicOr(m.status, 4);
+        return;
+    }
+    const int64_t r0 = (int64_t) blockIdx.x * MMID_ROWS;
+    if (r0 >= m.N) return;
+    const int nrows = (int) ((m.N - r0) < MMID_ROWS ? (m.N - r0) : MMID_ROWS);
+    const size_t row_bytes = (size_t) (m.K / block_elems(TYPE)) * block_bytes(TYPE);
+    const uint32_t RS = mmid_slot_bytes(row_bytes);
+    const uint8_t* wmat = m.w + (size_t) mat * m.nb2;
+    // stage the weight rows: each row as its 16-byte aligned superset
+    const int nchmax = (int) ((row_bytes + 15) / 16) + 1;
+    for (int idx = threadIdx.x; idx < nrows * nchmax; idx += 256) {
+        const int r = idx / nchmax, c = idx % nchmax;
+        const uint8_t* src = wmat + (size_t) (r0 + r) * m.nb1;
+        const uintptr_t s0 = (uintptr_t) src & ~(uintptr_t) 15;
+        const uintptr_t s1 = ((uintptr_t) src + row_bytes + 15) & ~(uintptr_t) 15;
+        if (c < (int) ((s1 - s0) / 16)) ((uint4*) (lds + (r * RS) / 4))[c] = ((const uint4*) s0)[c];
+    }
+    const uint32_t ABASE = RS * MMID_ROWS;  // activation staging follows the weights
+    const uint32_t ARS = (uint32_t) (((m.act_row_bytes + 3) / 4) * 4 + 16);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int rl = wave * 8 + (lane >> 3);  // row within the tile
+    const int n = lane & 7;
+    const bool rvalid = rl < nrows;
+    const int rrow = rvalid ? rl : 0;
+    const uint32_t wbase = rrow * RS + (uint32_t) ((uintptr_t) (wmat + (size_t) (r0 + rrow) * m.nb1) & 15);
+    const int nb = (int) (m.K / block_elems(TYPE));
+    const int p0 = m.active_off[g], p1 = m.active_off[g + 1];
+    for (int pc = p0; pc < p1; pc += MMID_CT) {
+        const int cnt = (p1 - pc) < MMID_CT ? (p1 - pc) : MMID_CT;
+        __syncthreads();  // weights staged / previous chunk consumed
+        for (int tk = 0; tk < cnt; ++tk) {
+            const int e = m.rows[2 * (pc + tk)], t = m.rows[2 * (pc + tk) + 1];
+            const int64_t arow = (int64_t) (e % m.b_ne1) + (int64_t) t * m.b_ne1;
+            const uint32_t* src = (const uint32_t*) (m.act_q + (size_t) arow * m.act_row_bytes);
+            uint32_t* dst = lds + (ABASE + tk * ARS) / 4;
+            const int nw = (int) ((m.act_row_bytes + 3) / 4);
+            for (int c = threadIdx.x; c < nw; c += 256) dst[c] = src[c];
+        }
+        __syncthreads();
+        for (int tk = 0; tk < cnt; ++tk) {
+            const float v = row_dot_lds<TYPE>(lds, wbase, ABASE + tk * ARS, nb, n);
+            if (rvalid && n == 0) {
+                const int e = m.rows[2 * (pc + tk)], t = m.rows[2 * (pc + tk) + 1];
+                float* d = (float*) ((char*) m.dst + (size_t) e * m.dst_nb1 + (size_t) t * m.dst_nb2);
+                d[r0 + rl] = v;
+            }
+        }
+    }
+}
+
+int launch_mmid_gemv(const MmidArgs& m, hipStream_t stream) {
+    const size_t row_bytes = (size_t) (m.K / block_elems(m.type)) * block_bytes(m.type);
+    const size_t lds_bytes = (size_t) mmid_slot_bytes(row_bytes) * MMID_ROWS +
+                             (size_t) MMID_CT * (((m.act_row_bytes + 3) / 4) * 4 + 16);
+    if (lds_bytes > 160 * 1024) return -2;
+    dim3 grid((unsigned) ((m.N + MMID_ROWS - 1) / MMID_ROWS), (unsigned) m.max_active);
+    if (grid.y == 0) return 0;
+    switch (m.type) {
+        case T_Q4_K: hipLaunchKernelGGL(k_mmid_gemv<T_Q4_K>, grid, dim3(256), lds_bytes, stream, m); break;
+        case T_Q6_K: hipLaunchKernelGGL(k_mmid_gemv<T_Q6_K>, grid, dim3(256), lds_bytes, stream, m); break;
+        case T_Q8_0: hipLaunchKernelGGL(k_mmid_gemv<T_Q8_0>, grid, dim3(256), lds_bytes, stream, m); break;
+        default: return -2;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+int launch_mmid_mfma(const MmidArgs& m, hipStream_t stream) { return launch_mmid_gemv(m, stream); }
+
+}  // namespace qw

@@ -1,0 +1,114 @@
+// qw_common.hpp -- device-side building blocks shared by every qwmoe kernel.
+//
+// Block layouts are byte-identical to ggml's (ggml/src/ggml-common.h:252-255,
+// 327-337, 362-367, 371-375 of the reference tree); the arithmetic helpers
+// reproduce, lane for lane, the float order of ggml's x86 AVX2+FMA CPU backend,
+// which is what makes the GPU results bit-identical to it.  All sources are
+// compiled with -ffp-contract=off: every fused multiply-add below is explicit.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qw {
+
+constexpr int QK_K = 256;
+constexpr int QK8_0 = 32;
+constexpr int WAVE = 64;
+
+enum Type : int { T_F32 = 0, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14, T_Q8_K = 15, T_I32 = 26 };
+
+struct __attribute__((packed)) BlockQ8_0 { uint16_t d; int8_t qs[QK8_0]; };
+struct __attribute__((packed)) BlockQ4_K { uint16_t d; uint16_t dmin; uint8_t scales[12]; uint8_t qs[QK_K / 2]; };
+struct __attribute__((packed)) BlockQ6_K { uint8_t ql[QK_K / 2]; uint8_t qh[QK_K / 4]; int8_t scales[QK_K / 16]; uint16_t d; };
+struct __attribute__((packed)) BlockQ8_K { float d; int8_t qs[QK_K]; int16_t bsums[QK_K / 16]; };
+static_assert(sizeof(BlockQ8_0) == 34, "q8_0 layout");
+static_assert(sizeof(BlockQ4_K) == 144, "q4_K layout");
+static_assert(sizeof(BlockQ6_K) == 210, "q6_K layout");
+static_assert(sizeof(BlockQ8_K) == 292, "q8_K layout");
+
+__host__ __device__ constexpr int block_elems(int t) { return (t == T_Q8_0) ? QK8_0 : (t == T_F32 ? 1 : QK_K); }
+__host__ __device__ constexpr int block_bytes(int t) {
+    return t == T_Q8_0 ? 34 : t == T_Q4_K ? 144 : t == T_Q6_K ? 210 : t == T_Q8_K ? 292 : t == T_F32 ? 4 : 0;
+}
+__host__ __device__ constexpr int vec_dot_type(int t) { return t == T_Q8_0 ? T_Q8_0 : T_Q8_K; }
+
+__device__ __forceinline__ uint32_t fbits(float f) { return __float_as_uint(f); }
+__device__ __forceinline__ float bitsf(uint32_t u) { return __uint_as_float(u); }
+
+// binary16 <-> binary32, round to nearest even (F16C _cvtss_sh(x, 0) semantics).
+__device__ __forceinline__ float h2f(uint16_t h) {
+    _Float16 v;
+    __builtin_memcpy(&v, &h, 2);
+    return (float) v;
+}
+__device__ __forceinline__ uint16_t f2h(float f) {
+    const _Float16 v = (_Float16) f;
+    uint16_t h;
+    __builtin_memcpy(&h, &v, 2);
+    return h;
+}
+
+// ggml-quants.c:621-626: 1.5*2^23 magic add == round half to even for |x| < 2^22.
+__device__ __forceinline__ int nearest_int(float fval) {
+    float val = fval + 12582912.f;
+    int i = (int) fbits(val);
+    return (i & 0x007fffff) - 0x00400000;
+}
+
+// hsum_float_8 (ggml-cpu/arch/x86/quants.c:42-48): ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)).
+__device__ __forceinline__ float hsum8(const float a[8]) {
+    const float r0 = a[4] + a[0], r1 = a[5] + a[1], r2 = a[6] + a[2], r3 = a[7] + a[3];
+    return (r0 + r2) + (r1 + r3);
+}
+
+// One lane of ggml_v_expf, AVX2+FMA branch (ggml-cpu/vec.h:1215-1254).  The
+// constants and step order are ggml's; every fma here is one the AVX2 code does.
+__device__ __forceinline__ float v_expf(float x) {
+    const float r = 0x1.8p23f;
+    const float z = __builtin_fmaf(x, 0x1.715476p+0f, r);
+    const float n = z - r;
+    const float b = __builtin_fmaf(-n, 0x1.7f7d1cp-20f, __builtin_fmaf(-n, 0x1.62e4p-1f, x));
+    const uint32_t e = fbits(z) << 23;
+    const float k = bitsf(e + 0x3f800000u);
+    const float u = b * b;
+    const float j = __builtin_fmaf(__builtin_fmaf(__builtin_fmaf(0x1.0e4020p-7f, b, 0x1.573e2ep-5f), u,
+                                                  __builtin_fmaf(0x1.555e66p-3f, b, 0x1.fffdb6p-2f)),
+                                   u, 0x1.ffffecp-1f * b);
+    const float an = __builtin_fabsf(n);
+    if (!(an > 126.0f)) return __builtin_fmaf(k, j, k);
+    const uint32_t g = (n <= 0.0f) ? 0x82000000u : 0u;
+    const float s1 = bitsf(g + 0x7f000000u);
+    const float s2 = bitsf(e - g);
+    if (an > 192.0f) return s1 * s1;
+    return __builtin_fmaf(s2, j, s2) * s1;
+}
+
+// ggml_v_silu (vec.h:1256-1263): x / (1 + exp(0 - x)), IEEE division.
+__device__ __forceinline__ float v_silu(float x) {
+    const float e = v_expf(0.0f - x);
+    return x / (1.0f + e);
+}
+
+// get_scale_min_k4 (ggml-quants.c:880-887).
+__device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, int& d, int& m) {
+    if (j < 4) {
+        d = q[j] & 63;
+        m = q[j + 4] & 63;
+    } else {
+        d = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        m = (q[j + 4] >> 4) | ((q[j - 0] >> 6) << 4);
+    }
+}
+
+__device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+// Unaligned little-endian reads (compiler splits them to what the alignment allows).
+template <typename T>
+__device__ __forceinline__ T ld_unaligned(const void* p) {
+    T v;
+    __builtin_memcpy(&v, p, sizeof(T));
+    return v;
+}
+
+}  // namespace qw

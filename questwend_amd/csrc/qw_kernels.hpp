@@ -1,0 +1,79 @@
+// qw_kernels.hpp -- launch wrappers exported by each kernel translation unit and
+// used by the C-ABI layer (api.cpp).  All launches are stream-ordered and
+// asynchronous; each returns 0 or a negative status (see include/qwmoe.h).
+#pragma once
+
+#include "qw_common.hpp"
+
+namespace qw {
+
+// quantize.hip
+int launch_quantize_act(int vdt, const float* src, int64_t K, int64_t ne1, int64_t nrows, size_t nb1, size_t nb2,
+                        void* dst, hipStream_t stream);
+int launch_quantize_weights(int type, const float* src, int64_t n, void* dst, hipStream_t stream);
+int launch_dequantize(int type, const void* x, float* y, int64_t n, hipStream_t stream);
+int launch_randn(float* y, int64_t n, uint64_t seed, float mean, float stddev, hipStream_t stream);
+
+// router.hip
+struct RouterArgs {
+    const float* W;       // [E][H] fp32 (ggml [H, E])
+    const float* x;       // token t at x + t * x_stride (floats)
+    int64_t x_stride;
+    int64_t H, E, k, T;
+    float clamp_min;      // 6.103515625e-5 in the reference
+    float scale;          // expert_weights_scale (applied when != 0 and != 1)
+    int32_t* ids;         // [T][k]
+    float* weights;       // [T][k]
+    float* logits;        // optional [T][E]
+    float* probs;         // optional [T][E]
+    int32_t* status;      // optional device word: bit 0 set when a top-k tie needed the exact sort
+};
+int launch_router(const RouterArgs& a, float* logits_ws, hipStream_t stream);
+
+// mmid.hip
+struct GroupArgs {
+    const int32_t* ids;   // [T][ids_stride]
+    int64_t n_ids, T, ids_stride;
+    int64_t n_bins;       // number of matrices (or logical experts)
+    int32_t* counts;      // [n_bins]        (optional)
+    int32_t* offsets;     // [n_bins + 1]    (optional)
+    int32_t* rows;        // [T * n_ids][2]  (e, t) pairs grouped by bin, ggml order
+    int32_t* active;      // [min(n_bins, T*n_ids)] bins with count > 0, ascending
+    int32_t* active_off;  // [n_active + 1]  offsets into rows for each active bin
+    int32_t* n_active;    // [1]
+    int32_t* status;      // bit 1 set on an out-of-range id
+    int32_t* hist_ws;     // workspace: GROUP_WAVES * n_bins ints
+};
+constexpr int GROUP_WAVES = 8;
+int launch_group(const GroupArgs& g, hipStream_t stream);
+
+struct MmidArgs {
+    int type;                 // weight type
+    const uint8_t* w;         // matrix a at w + a * nb2, row r at + r * nb1
+    size_t nb1, nb2;
+    int64_t K, N, n_as;
+    const uint8_t* act_q;     // quantized activation rows, row (e % b_ne1) + t * b_ne1
+    int64_t b_ne1;
+    size_t act_row_bytes;
+    const int32_t* rows;      // grouped (e, t) pairs
+    const int32_t* active;    // active bins
+    const int32_t* active_off;
+    const int32_t* n_active;
+    const int32_t* slot_of;   // optional bin -> matrix index
+    int64_t n_slot_of;
+    float* dst;               // dst[r] of pair (e, t) at dst + e * dst_nb1 + t * dst_nb2 (bytes)
+    size_t dst_nb1, dst_nb2;
+    int32_t* status;          // bit 2 set on an out-of-range slot
+    int64_t max_active;       // grid bound on active bins
+};
+int launch_mmid_gemv(const MmidArgs& m, hipStream_t stream);
+int launch_mmid_mfma(const MmidArgs& m, hipStream_t stream);
+
+// ffn.hip
+int launch_swiglu(const float* gate, const float* up, float* out, int64_t n_rows, int64_t n, size_t g_stride,
+                  size_t u_stride, size_t o_stride, hipStream_t stream);
+int launch_weighted_sum(const float* experts, const float* weights, float* out, int64_t H, int64_t k, int64_t T,
+                        hipStream_t stream);
+int launch_rms_norm(const float* x, float* y, int64_t n, int64_t rows, float eps, hipStream_t stream);
+
+}  // namespace qw

@@ -1,0 +1,146 @@
+// router.hip -- MoE router on the GPU, bit-identical to the reference CPU path.
+//
+// Reference op sequence (core/runtime.cpp:869-897, Runtime::Impl::build_moe):
+//   logits = mul_mat(W_gate_inp, x)     ggml_vec_dot_f32, vec.cpp:11-140 (AVX: 4 x 8-lane
+//                                       fma accumulators, GGML_F32x8_REDUCE simd-mappings.h:579-629)
+//   probs  = soft_max(logits)           ops.cpp:5455-5566, vec.cpp:531- (ggml_v_expf, double sum)
+//   ids    = argsort_top_k(probs, k)    ggml.c:5344-5361 -> ARGSORT DESC ops.cpp:8332-8382 (std::sort)
+//   w      = get_rows / sum_rows / clamp(6.103515625e-5, inf) / div (/ scale)
+#include "qw_kernels.hpp"
+#include "qw_sort.hpp"
+
+namespace qw {
+
+constexpr int ROUTER_TT = 4;  // tokens per wave in the logits kernel
+
+// logits[t][e] = vec_dot_f32(H, W[e], x[t]).  One wave = 8 experts x ROUTER_TT
+// tokens; lane (g, m) owns the four fma chains c = 4m..4m+3 of expert g, i.e.
+// elements i == c (mod 32), exactly the 32 chains of the AVX reduction.
+__global__ void __launch_bounds__(64) k_router_logits(const float* __restrict__ W, const float* __restrict__ x,
+                                                      int64_t x_stride, int64_t H, int64_t E, int64_t T,
+                                                      float* __restrict__ logits) {
+    const int lane = threadIdx.x;
+    const int g = lane >> 3, m = lane & 7;
+    const int64_t e = (int64_t) blockIdx.x * 8 + g;
+    const int64_t t0 = (int64_t) blockIdx.y * ROUTER_TT;
+    const int64_t np = H & ~(int64_t) 31;
+    const bool ev = e < E;
+    const float* w = W + (ev ? e : 0) * H;
+    float acc[ROUTER_TT][4];
+    for (int tt = 0; tt < ROUTER_TT; ++tt)
+        for (int r = 0; r < 4; ++r) acc[tt][r] = 0.0f;
+    for (int64_t s = 0; s < np; s += 32) {
+        const float4 wv = *(const float4*) (w + s + 4 * m);
+        for (int tt = 0; tt < ROUTER_TT; ++tt) {
+            const int64_t t = t0 + tt < T ? t0 + tt : T - 1;
+            const float4 xv = *(const float4*) (x + t * x_stride + s + 4 * m);
+            acc[tt][0] = __builtin_fmaf(wv.x, xv.x, acc[tt][0]);
+            acc[tt][1] = __builtin_fmaf(wv.y, xv.y, acc[tt][1]);
+            acc[tt][2] = __builtin_fmaf(wv.z, xv.z, acc[tt][2]);
+            acc[tt][3] = __builtin_fmaf(wv.w, xv.w, acc[tt][3]);
+        }
+    }
+    // Chain c_l (l < 8) lives in lanes m = 0,1; c_{8+l} in 2,3; c_{16+l} in 4,5; c_{24+l} in 6,7.
+    for (int tt = 0; tt < ROUTER_TT; ++tt) {
+        float v[4];
+        for (int r = 0; r < 4; ++r) {
+            float a = acc[tt][r];
+            a = a + __shfl_down(a, 4, 8);   // (c_l + c_{16+l})            lanes 0..3
+            a = a + __shfl_down(a, 2, 8);   // + (c_{8+l} + c_{24+l}) = s_l  lanes 0,1
+            a = a + __shfl_down(a, 1, 8);   // s_l + s_{l+4} = t0_r          lane 0
+            v[r] = a;
+        }
+        const int64_t t = t0 + tt;
+        if (m == 0 && ev && t < T) {
+            float sumf = (v[0] + v[1]) + (v[2] + v[3]);   // two _mm_hadd_ps
+            // scalar tail (n % 32): 4-wide multiply + in-order add per full group of 4, fma for the rest
+            const float* xt = x + t * x_stride;
+            const int64_t nv = np + ((H - np) & ~(int64_t) 3);
+            for (int64_t i = np; i < H; ++i)
+                sumf = (i < nv) ? sumf + w[i] * xt[i] : __builtin_fmaf(w[i], xt[i], sumf);
+            logits[t * E + e] = sumf;
+        }
+    }
+}
+
+// Softmax, exact top-k and weight normalisation for one token per wave.
+// Supports E % 8 == 0 and E <= 64 * ROUTER_EPL.
+constexpr int ROUTER_EPL = 8;
+__global__ void __launch_bounds__(64) k_router_topk(const float* __restrict__ logits, int64_t E, int64_t k,
+                                                    int64_t T, float clamp_min, float scale, int32_t* __restrict__ ids,
+                                                    float* __restrict__ weights, float* __restrict__ probs_out,
+                                                    int32_t* __restrict__ status) {
+    __shared__ float p[64 * ROUTER_EPL];
+    __shared__ float gsum[64 * ROUTER_EPL / 8];
+    __shared__ int32_t order[64 * ROUTER_EPL];
+    __shared__ int need_sort;
+    const int lane = threadIdx.x;
+    const int64_t t = blockIdx.x;
+    const float* l = logits + t * E;
+    float mx = -INFINITY;
+    for (int64_t i = lane; i < E; i += 64) mx = fmaxf(mx, l[i]);
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    for (int64_t i = lane; i < E; i += 64) p[i] = v_expf(l[i] - mx);
+    if (lane == 0) need_sort = 0;
+    __syncthreads();
+    const int64_t ng = E / 8;
+    for (int64_t gi = lane; gi < ng; gi += 64) gsum[gi] = hsum8(&p[8 * gi]);
+    __syncthreads();
+    double sum = 0.0;
+    if (lane == 0)
+        for (int64_t gi = 0; gi < ng; ++gi) sum += (double) gsum[gi];
+    sum = __shfl(sum, 0);
+    const float inv = (float) (1.0 / sum);
+    for (int64_t i = lane; i < E; i += 64) p[i] = p[i] * inv;
+    __syncthreads();
+    if (probs_out)
+        for (int64_t i = lane; i < E; i += 64) probs_out[t * E + i] = p[i];
+    // rank of every element; a tie group that reaches into the first k places
+    // leaves the order to std::sort's algorithm, which is then replayed exactly
+    for (int64_t i = lane; i < E; i += 64) {
+        const float pi = p[i];
+        int gt = 0, eq = 0;
+        for (int64_t j = 0; j < E; ++j) {
+            gt += p[j] > pi;
+            eq += p[j] == pi;
+        }
+        if (gt < k) {
+            if (eq > 1) need_sort = 1;
+            else order[gt] = (int32_t) i;
+        }
+    }
+    __syncthreads();
+    if (need_sort) {
+        if (lane == 0) {
+            for (int64_t i = 0; i < E; ++i) order[i] = (int32_t) i;
+            libstdcxx_sort_desc(order, (int) E, p);
+            if (status) atomicOr(status, 1);
+        }
+        __syncthreads();
+    }
+    if (lane == 0) {
+        double s = 0.0;
+        for (int64_t i = 0; i < k; ++i) s += (double) p[order[i]];
+        float wsum = (float) s;
+        wsum = fmaxf(fminf(wsum, INFINITY), clamp_min);
+        for (int64_t i = 0; i < k; ++i) {
+            float wi = p[order[i]] / wsum;
+            if (scale != 0.0f && scale != 1.0f) wi = wi * scale;
+            ids[t * k + i] = order[i];
+            weights[t * k + i] = wi;
+        }
+    }
+}
+
+int launch_router(const RouterArgs& a, float* logits_ws, hipStream_t stream) {
+    if (a.E % 8 != 0 || a.E > 64 * ROUTER_EPL || a.k < 1 || a.k > a.E || a.H < 1) return -2;
+    if (a.T == 0) return 0;
+    float* logits = a.logits ? a.logits : logits_ws;
+    dim3 g1((unsigned) ((a.E + 7) / 8), (unsigned) ((a.T + ROUTER_TT - 1) / ROUTER_TT));
+    hipLaunchKernelGGL(k_router_logits, g1, dim3(64), 0, stream, a.W, a.x, a.x_stride, a.H, a.E, a.T, logits);
+    hipLaunchKernelGGL(k_router_topk, dim3((unsigned) a.T), dim3(64), 0, stream, logits, a.E, a.k, a.T, a.clamp_min,
+                       a.scale, a.ids, a.weights, a.probs, a.status);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+}  // namespace qw
