@@ -183,6 +183,28 @@ typedef struct qwmoe_layer {
 int qwmoe_ffn_layer(void * stream, const qwmoe_layer * layer, const float * x, int64_t T, float * out,
                     float rms_eps, float * x_next, int32_t * ids_out, float * weights_out);
 
+/* ---- persistent multi-layer decode ------------------------------------------ */
+
+/* A stack of MoE FFN layers decoded one token per launch, all layers in a
+ * single persistent kernel (one workgroup per CU).  Replaces, for the MoE FFN
+ * layers, the per-token graph the reference builds and replays in
+ * Runtime::decode -> decode_reuse / build_graph (core/runtime.cpp:1768-1829,
+ * 976-1100), with ggml_rms_norm between layers as in the benchmark stack.
+ * All layers must share n_embd, n_expert, n_expert_used, n_ff, types
+ * (Q4_K gate/up, Q4_K or Q6_K down) and expert_weights_scale; row strides must
+ * be multiples of 16 bytes.  Creation allocates (descriptor table and exchange
+ * buffers); running does not. */
+typedef struct qwmoe_decode_stack qwmoe_decode_stack;
+int qwmoe_decode_stack_create(const qwmoe_layer * layers, int n_layer, float rms_eps, qwmoe_decode_stack ** out);
+/* One token: x [H] -> out [H] (MoE output of the last layer) and, when
+ * non-NULL, x_out [H] = rms_norm(out); ids_out / weights_out [n_layer][k]. */
+int qwmoe_decode_stack_run(void * stream, qwmoe_decode_stack * s, const float * x, float * out, float * x_out,
+                           int32_t * ids_out, float * weights_out);
+/* Synchronises `stream`; status bits: 1 top-k tie replayed, 8 a wait timed out
+ * (launch abandoned), 16 a slot table entry was out of range. */
+int qwmoe_decode_stack_status(void * stream, qwmoe_decode_stack * s, int32_t * status_out, int clear);
+void qwmoe_decode_stack_free(qwmoe_decode_stack * s);
+
 /* ---- expert slot table (host) ------------------------------------------------ */
 
 /* Resident-only counterpart of ExpertCache's slot bookkeeping

@@ -62,6 +62,10 @@ SIGNATURES = {
     "qwmoe_weighted_sum": (I, [P, P, P, P, I64, I64, I64]),
     "qwmoe_rms_norm": (I, [P, P, P, I64, I64, F]),
     "qwmoe_ffn_layer": (I, [P, P, P, I64, P, F, P, P, P]),
+    "qwmoe_decode_stack_create": (I, [P, I, F, P]),
+    "qwmoe_decode_stack_run": (I, [P, P, P, P, P, P, P]),
+    "qwmoe_decode_stack_status": (I, [P, P, P, I]),
+    "qwmoe_decode_stack_free": (None, [P]),
     "qwmoe_slot_table_create": (P, [I, I]),
     "qwmoe_slot_table_free": (None, [P]),
     "qwmoe_slot_table_fill": (I, [P, U64]),

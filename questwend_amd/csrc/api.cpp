@@ -13,6 +13,7 @@
 #include "../../include/qwmoe.h"
 #include "qw_kernels.hpp"
 #include "qw_sort.hpp"
+#include "qw_decode.hpp"
 
 namespace {
 
@@ -385,10 +386,138 @@ int qwmoe_ffn_layer(void* stream, const qwmoe_layer* L, const float* x, int64_t 
     return QWMOE_OK;
 }
 
+}  // extern "C"
+
+struct qwmoe_decode_stack {
+    qw::DecodeStackDesc d;
+};
+
+extern "C" {
+
+int qwmoe_decode_stack_create(const qwmoe_layer* layers, int n_layer, float rms_eps, qwmoe_decode_stack** out) {
+    if (!g_lib.ready) return QWMOE_ERR_NOT_INITIALIZED;
+    if (!layers || n_layer <= 0 || !out || !(rms_eps >= 0.0f)) return QWMOE_ERR_INVALID_ARG;
+    *out = nullptr;
+    const qwmoe_layer& L0 = layers[0];
+    for (int l = 0; l < n_layer; ++l) {
+        const qwmoe_layer& L = layers[l];
+        if (L.n_embd != L0.n_embd || L.n_expert != L0.n_expert || L.n_expert_used != L0.n_expert_used ||
+            L.n_ff != L0.n_ff || L.type_gate != L0.type_gate || L.type_up != L0.type_up ||
+            L.type_down != L0.type_down || L.expert_weights_scale != L0.expert_weights_scale)
+            return QWMOE_ERR_INVALID_ARG;
+        if (!L.router || !L.gate || !L.up || !L.down) return QWMOE_ERR_INVALID_ARG;
+        if (L.type_gate != qw::T_Q4_K || L.type_up != qw::T_Q4_K) return QWMOE_ERR_UNSUPPORTED;
+        if (L.gate_nb1 % 16 || L.gate_nb2 % 16 || L.up_nb1 % 16 || L.up_nb2 % 16 || ((uintptr_t) L.gate & 15) ||
+            ((uintptr_t) L.up & 15) || ((uintptr_t) L.router & 15))
+            return QWMOE_ERR_UNSUPPORTED;
+        if (L.n_slots_gate <= 0 || L.n_slots_up <= 0 || L.n_slots_down <= 0) return QWMOE_ERR_INVALID_ARG;
+    }
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return QWMOE_ERR_HIP;
+    auto* s = new (std::nothrow) qwmoe_decode_stack();
+    if (!s) return QWMOE_ERR_INVALID_ARG;
+    qw::DecodeStackDesc& d = s->d;
+    d.n_layer = n_layer;
+    d.H = L0.n_embd;
+    d.E = L0.n_expert;
+    d.k = L0.n_expert_used;
+    d.F = L0.n_ff;
+    d.type_down = L0.type_down;
+    d.scale = L0.expert_weights_scale;
+    d.rms_eps = rms_eps;
+    int rc = qw::plan_decode_stack(d, cus);
+    if (rc) {
+        delete s;
+        return rc;
+    }
+    // one device block: layer table | act | y | logits | status, abort
+    const size_t n_layers_b = sizeof(qw::DecodeLayer) * (size_t) n_layer;
+    const size_t off_xa = (n_layers_b + 255) & ~(size_t) 255;
+    const size_t off_xy = off_xa + (((size_t) (d.k * d.F) * 8 + 255) & ~(size_t) 255);
+    const size_t off_xl = off_xy + (((size_t) d.H * 8 + 255) & ~(size_t) 255);
+    const size_t off_st = off_xl + (((size_t) d.E * 8 + 255) & ~(size_t) 255);
+    const size_t total = off_st + 256;
+    void* blk = nullptr;
+    if (hipMalloc(&blk, total) != hipSuccess) {
+        delete s;
+        return QWMOE_ERR_HIP;
+    }
+    std::vector<qw::DecodeLayer> host((size_t) n_layer);
+    for (int l = 0; l < n_layer; ++l) {
+        const qwmoe_layer& L = layers[l];
+        qw::DecodeLayer& D = host[(size_t) l];
+        D.router = L.router;
+        D.gate = (const uint8_t*) L.gate;
+        D.up = (const uint8_t*) L.up;
+        D.down = (const uint8_t*) L.down;
+        D.gate_nb1 = L.gate_nb1;
+        D.gate_nb2 = L.gate_nb2;
+        D.up_nb1 = L.up_nb1;
+        D.up_nb2 = L.up_nb2;
+        D.down_nb1 = L.down_nb1;
+        D.down_nb2 = L.down_nb2;
+        D.slot_gate = L.slot_gate;
+        D.slot_up = L.slot_up;
+        D.slot_down = L.slot_down;
+        D.n_slots_gate = L.n_slots_gate;
+        D.n_slots_up = L.n_slots_up;
+        D.n_slots_down = L.n_slots_down;
+    }
+    uint8_t* base = (uint8_t*) blk;
+    if (hipMemset(blk, 0, total) != hipSuccess ||
+        hipMemcpy(base, host.data(), n_layers_b, hipMemcpyHostToDevice) != hipSuccess ||
+        hipDeviceSynchronize() != hipSuccess) {
+        (void) hipFree(blk);
+        delete s;
+        return QWMOE_ERR_HIP;
+    }
+    d.dev_block = blk;
+    d.layers_dev = (qw::DecodeLayer*) base;
+    d.xa = (uint64_t*) (base + off_xa);
+    d.xy = (uint64_t*) (base + off_xy);
+    d.xl = (uint64_t*) (base + off_xl);
+    d.status = (int32_t*) (base + off_st);
+    d.abort_flag = (int32_t*) (base + off_st + 128);
+    d.epoch = 1;
+    *out = s;
+    return QWMOE_OK;
+}
+
+int qwmoe_decode_stack_run(void* stream, qwmoe_decode_stack* s, const float* x, float* out, float* x_out,
+                           int32_t* ids_out, float* weights_out) {
+    if (!s || !x || !out) return QWMOE_ERR_INVALID_ARG;
+    if ((ids_out == nullptr) != (weights_out == nullptr)) return QWMOE_ERR_INVALID_ARG;
+    qw::DecodeStackDesc& d = s->d;
+    if (d.epoch > 0x7fffffffu - (uint32_t) d.n_layer) return QWMOE_ERR_UNSUPPORTED;  // epoch space exhausted
+    const uint32_t e0 = d.epoch;
+    d.epoch += (uint32_t) d.n_layer;
+    return qw::launch_decode_stack(d, x, out, x_out, ids_out, weights_out, e0, S(stream));
+}
+
+int qwmoe_decode_stack_status(void* stream, qwmoe_decode_stack* s, int32_t* status_out, int clear) {
+    if (!s) return QWMOE_ERR_INVALID_ARG;
+    int32_t v = 0;
+    if (hipStreamSynchronize(S(stream)) != hipSuccess) return QWMOE_ERR_HIP;
+    if (hipMemcpy(&v, s->d.status, sizeof(v), hipMemcpyDeviceToHost) != hipSuccess) return QWMOE_ERR_HIP;
+    if (clear && hipMemset(s->d.status, 0, sizeof(int32_t)) != hipSuccess) return QWMOE_ERR_HIP;
+    if (status_out) *status_out = v;
+    return QWMOE_OK;
+}
+
+void qwmoe_decode_stack_free(qwmoe_decode_stack* s) {
+    if (!s) return;
+    (void) hipDeviceSynchronize();
+    (void) hipFree(s->d.dev_block);
+    delete s;
+}
+
 int qwmoe_host_argsort_desc(const float* values, int n, int32_t* idx) {
     if (!values || !idx || n < 0) return QWMOE_ERR_INVALID_ARG;
     for (int i = 0; i < n; ++i) idx[i] = i;
-    qw::libstdcxx_sort_desc(idx, n, values);
+    qw::SortRange stack[qw::SORT_STACK];
+    qw::libstdcxx_sort_desc(idx, n, values, stack);
     return QWMOE_OK;
 }
 

@@ -10,6 +10,7 @@
 //     the same 8 integer lanes per super-block, the same fma chain over blocks and
 //     the same horizontal-sum tree.
 #include "qw_kernels.hpp"
+#include "qw_rowdot.hpp"
 
 namespace qw {
 
@@ -149,124 +150,6 @@ int launch_group(const GroupArgs& g, hipStream_t stream) {
 
 constexpr int MMID_ROWS = 32;   // rows per workgroup (8 per wave)
 constexpr int MMID_CT = 8;      // activation rows staged per pass
-
-__device__ __forceinline__ uint32_t lds_u32(const uint32_t* lds, uint32_t byte_off) {
-    const uint32_t lo = lds[byte_off >> 2], hi = lds[(byte_off >> 2) + 1];
-    return __builtin_amdgcn_alignbyte(hi, lo, byte_off & 3);
-}
-__device__ __forceinline__ uint32_t lds_u32a(const uint32_t* lds, uint32_t byte_off) { return lds[byte_off >> 2]; }
-__device__ __forceinline__ uint16_t lds_u16(const uint32_t* lds, uint32_t byte_off) {
-    return (uint16_t) (lds_u32(lds, byte_off) & 0xffff);
-}
-__device__ __forceinline__ float lds_f32(const uint32_t* lds, uint32_t byte_off) { return bitsf(lds_u32(lds, byte_off)); }
-
-// Row dot products from LDS for one (row, n) lane.  Returns the lane's
-// contribution after the 8-lane reduction (valid in lane n == 0 of the group).
-template <int TYPE>
-__device__ __forceinline__ float row_dot_lds(const uint32_t* lds, uint32_t wbase, uint32_t abase, int nb, int n);
-
-template <>
-__device__ __forceinline__ float row_dot_lds<T_Q4_K>(const uint32_t* lds, uint32_t wbase, uint32_t abase, int nb, int n) {
-    float acc = 0.0f, accm = 0.0f;
-    for (int b = 0; b < nb; ++b) {
-        const uint32_t blk = wbase + 144u * b;
-        const uint32_t yb = abase + 292u * b;
-        const uint32_t h0 = lds_u32(lds, blk);
-        const uint32_t s0 = lds_u32(lds, blk + 4), s1 = lds_u32(lds, blk + 8), s2 = lds_u32(lds, blk + 12);
-        const uint8_t q[12] = {(uint8_t) s0, (uint8_t) (s0 >> 8), (uint8_t) (s0 >> 16), (uint8_t) (s0 >> 24),
-                               (uint8_t) s1, (uint8_t) (s1 >> 8), (uint8_t) (s1 >> 16), (uint8_t) (s1 >> 24),
-                               (uint8_t) s2, (uint8_t) (s2 >> 8), (uint8_t) (s2 >> 16), (uint8_t) (s2 >> 24)};
-        int sc[8], mn[8];
-        for (int j = 0; j < 8; ++j) scale_min_k4(j, q, sc[j], mn[j]);
-        int sumi = 0;
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t wq = lds_u32(lds, blk + 16 + 32 * j + 4 * n);
-            const int lo = (int) (wq & 0x0F0F0F0Fu), hi = (int) ((wq >> 4) & 0x0F0F0F0Fu);
-            const int alo = (int) lds_u32(lds, yb + 4 + 64 * j + 4 * n);
-            const int ahi = (int) lds_u32(lds, yb + 4 + 64 * j + 32 + 4 * n);
-            sumi += sc[2 * j] * sdot4(lo, alo, 0) + sc[2 * j + 1] * sdot4(hi, ahi, 0);
-        }
-        const float yd = lds_f32(lds, yb);
-        const float d = yd * h2f((uint16_t) (h0 & 0xffff));
-        acc = __builtin_fmaf(d, (float) sumi, acc);
-        if (n < 4) {
-            const uint32_t bs01 = lds_u32(lds, yb + 260 + 8 * n), bs23 = lds_u32(lds, yb + 260 + 8 * n + 4);
-            const int q8s0 = (int) (int16_t) (bs01 & 0xffff) + (int) (int16_t) (bs01 >> 16);
-            const int q8s1 = (int) (int16_t) (bs23 & 0xffff) + (int) (int16_t) (bs23 >> 16);
-            const int prod = mn[2 * n] * q8s0 + mn[2 * n + 1] * q8s1;
-            const float dmin = -yd * h2f((uint16_t) (h0 >> 16));
-            accm = __builtin_fmaf(dmin, (float) prod, accm);
-        }
-    }
-    // hsum_float_8(acc) + ((m0 + m2) + (m1 + m3))
-    float a = acc;
-    a = a + __shfl_down(a, 4, 8);
-    a = a + __shfl_down(a, 2, 8);
-    a = a + __shfl_down(a, 1, 8);
-    float m = accm;
-    m = m + __shfl_down(m, 2, 8);
-    m = m + __shfl_down(m, 1, 8);
-    return a + m;
-}
-
-template <>
-__device__ __forceinline__ float row_dot_lds<T_Q6_K>(const uint32_t* lds, uint32_t wbase, uint32_t abase, int nb, int n) {
-    float acc = 0.0f;
-    const int g = n >= 4 ? 1 : 0;
-    for (int b = 0; b < nb; ++b) {
-        const uint32_t blk = wbase + 210u * b;
-        const uint32_t yb = abase + 292u * b;
-        int sc[16];
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t s = lds_u32(lds, blk + 192 + 4 * i);
-            sc[4 * i + 0] = (int) (int8_t) (s & 0xff);
-            sc[4 * i + 1] = (int) (int8_t) ((s >> 8) & 0xff);
-            sc[4 * i + 2] = (int) (int8_t) ((s >> 16) & 0xff);
-            sc[4 * i + 3] = (int) (int8_t) (s >> 24);
-        }
-        int sumi = 0;
-        for (int j = 0; j < 2; ++j) {
-            const uint32_t qa = lds_u32(lds, blk + 64 * j + 4 * n);
-            const uint32_t qb = lds_u32(lds, blk + 64 * j + 32 + 4 * n);
-            const uint32_t qh = lds_u32(lds, blk + 128 + 32 * j + 4 * n);
-            const int q0 = (int) ((qa & 0x0F0F0F0Fu) | ((qh & 0x03030303u) << 4));
-            const int q1 = (int) ((qb & 0x0F0F0F0Fu) | ((qh & 0x0C0C0C0Cu) << 2));
-            const int q2 = (int) (((qa >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u));
-            const int q3 = (int) (((qb >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u));
-            const uint32_t y = yb + 4 + 128 * j + 4 * n;
-            sumi += sc[8 * j + 0 + g] * sdot4(q0, (int) lds_u32(lds, y), 0);
-            sumi += sc[8 * j + 2 + g] * sdot4(q1, (int) lds_u32(lds, y + 32), 0);
-            sumi += sc[8 * j + 4 + g] * sdot4(q2, (int) lds_u32(lds, y + 64), 0);
-            sumi += sc[8 * j + 6 + g] * sdot4(q3, (int) lds_u32(lds, y + 96), 0);
-        }
-        const uint32_t bs = lds_u32(lds, yb + 260 + 4 * n);
-        sumi -= 32 * ((int) (int16_t) (bs & 0xffff) * sc[2 * n] + (int) (int16_t) (bs >> 16) * sc[2 * n + 1]);
-        const float d = lds_f32(lds, yb) * h2f(lds_u16(lds, blk + 208));
-        acc = __builtin_fmaf(d, (float) sumi, acc);
-    }
-    float a = acc;
-    a = a + __shfl_down(a, 4, 8);
-    a = a + __shfl_down(a, 2, 8);
-    a = a + __shfl_down(a, 1, 8);
-    return a;
-}
-
-template <>
-__device__ __forceinline__ float row_dot_lds<T_Q8_0>(const uint32_t* lds, uint32_t wbase, uint32_t abase, int nb, int n) {
-    float acc = 0.0f;
-    for (int b = 0; b < nb; ++b) {
-        const uint32_t blk = wbase + 34u * b;
-        const uint32_t yb = abase + 34u * b;
-        const int sumi = sdot4((int) lds_u32(lds, blk + 2 + 4 * n), (int) lds_u32(lds, yb + 2 + 4 * n), 0);
-        const float d = h2f(lds_u16(lds, blk)) * h2f(lds_u16(lds, yb));
-        acc = __builtin_fmaf(d, (float) sumi, acc);
-    }
-    float a = acc;
-    a = a + __shfl_down(a, 4, 8);
-    a = a + __shfl_down(a, 2, 8);
-    a = a + __shfl_down(a, 1, 8);
-    return a;
-}
 
 __host__ __device__ inline uint32_t mmid_slot_bytes(size_t row_bytes) {
     return (uint32_t) (((row_bytes + 15 + 15) / 16) * 16 + 16);

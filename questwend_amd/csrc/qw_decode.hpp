@@ -1,0 +1,47 @@
+// qw_decode.hpp -- host/device descriptors of the persistent decode stack.
+#pragma once
+
+#include <stdint.h>
+
+#include "qw_common.hpp"
+
+namespace qw {
+
+// Per-layer tensors as the kernel sees them (device memory).
+struct DecodeLayer {
+    const float* router;          // [E][H]
+    const uint8_t* gate;
+    const uint8_t* up;
+    const uint8_t* down;
+    uint64_t gate_nb1, gate_nb2, up_nb1, up_nb2, down_nb1, down_nb2;
+    const int32_t* slot_gate;     // logical -> slot, or null
+    const int32_t* slot_up;
+    const int32_t* slot_down;
+    int64_t n_slots_gate, n_slots_up, n_slots_down;
+};
+
+struct DecodeStackDesc {
+    DecodeLayer* layers_dev = nullptr;
+    int n_layer = 0;
+    int64_t H = 0, E = 0, k = 0, F = 0;
+    int type_down = 0;
+    float scale = 0.0f, rms_eps = 1e-6f;
+    uint64_t* xa = nullptr;       // exchange words
+    uint64_t* xy = nullptr;
+    uint64_t* xl = nullptr;
+    int32_t* status = nullptr;
+    int32_t* abort_flag = nullptr;
+    uint32_t epoch = 1;           // next launch's first layer epoch
+    int grid = 0;
+    int pa_per = 0, hb_per = 0;
+    uint32_t lds_rw = 0, lds_a = 0, lds_b = 0, lds_xq = 0, lds_aq = 0, lds_x = 0, lds_act = 0, lds_res = 0,
+             lds_total = 0;
+    uint32_t rs_a = 0, rs_b = 0;
+    void* dev_block = nullptr;    // one allocation holding everything above
+};
+
+int plan_decode_stack(DecodeStackDesc& d, int grid);
+int launch_decode_stack(const DecodeStackDesc& d, const float* x_in, float* out, float* x_out, int32_t* ids_out,
+                        float* w_out, uint32_t epoch0, hipStream_t stream);
+
+}  // namespace qw

@@ -144,21 +144,23 @@ __host__ __device__ inline void insert_unguarded_(int32_t* first, int32_t* last,
     }
 }
 
+// Pending right-hand ranges: at most one per level, and there are at most
+// 2*floor(log2 n) + 1 levels before the heapsort fallback takes over.
+constexpr int SORT_STACK = 66;
+struct SortRange { int first, last, depth; };
+
 // Sorts idx[0..n) so that the order equals libstdc++ std::sort(idx, idx+n, less).
+// `stack` holds SORT_STACK entries (LDS on the device, so it never spills).
 template <typename Cmp>
-__host__ __device__ inline void libstdcxx_sort(int32_t* idx, int n, const Cmp& less) {
+__host__ __device__ inline void libstdcxx_sort(int32_t* idx, int n, const Cmp& less, SortRange* stack) {
     if (n <= 1) return;
     constexpr int kThreshold = 16;
     int lg = 0;
     while ((2 << lg) <= n) ++lg;  // floor(log2 n)
-    // pending right-hand ranges: at most one per level, and there are at most
-    // 2*floor(log2 n) + 1 levels before the heapsort fallback takes over
-    struct Range { int first, last, depth; };
-    Range stack[66];
     int sp = 0;
     stack[sp++] = {0, n, 2 * lg};
     while (sp > 0) {
-        const Range r = stack[--sp];
+        const SortRange r = stack[--sp];
         int32_t* first = idx + r.first;
         int32_t* last = idx + r.last;
         int depth = r.depth;
@@ -173,7 +175,7 @@ __host__ __device__ inline void libstdcxx_sort(int32_t* idx, int n, const Cmp& l
             int32_t* cut = hoare_unguarded_(first + 1, last, first, less);
             // the right part is sorted independently of the left one, so the order
             // in which the two are processed does not change the result
-            if (sp < 66) stack[sp++] = {(int) (cut - idx), (int) (last - idx), depth};
+            if (sp < SORT_STACK) stack[sp++] = {(int) (cut - idx), (int) (last - idx), depth};
             last = cut;
         }
     }
@@ -185,8 +187,8 @@ __host__ __device__ inline void libstdcxx_sort(int32_t* idx, int n, const Cmp& l
     }
 }
 
-__host__ __device__ inline void libstdcxx_sort_desc(int32_t* idx, int n, const float* values) {
-    libstdcxx_sort(idx, n, DescByValue{values});
+__host__ __device__ inline void libstdcxx_sort_desc(int32_t* idx, int n, const float* values, SortRange* stack) {
+    libstdcxx_sort(idx, n, DescByValue{values}, stack);
 }
 
 }  // namespace qw

@@ -73,6 +73,7 @@ __global__ void __launch_bounds__(64) k_router_topk(const float* __restrict__ lo
     __shared__ float p[64 * ROUTER_EPL];
     __shared__ float gsum[64 * ROUTER_EPL / 8];
     __shared__ int32_t order[64 * ROUTER_EPL];
+    __shared__ SortRange sort_stack[SORT_STACK];
     __shared__ int need_sort;
     const int lane = threadIdx.x;
     const int64_t t = blockIdx.x;
@@ -113,7 +114,7 @@ __global__ void __launch_bounds__(64) k_router_topk(const float* __restrict__ lo
     if (need_sort) {
         if (lane == 0) {
             for (int64_t i = 0; i < E; ++i) order[i] = (int32_t) i;
-            libstdcxx_sort_desc(order, (int) E, p);
+            libstdcxx_sort_desc(order, (int) E, p, sort_stack);
             if (status) atomicOr(status, 1);
         }
         __syncthreads();

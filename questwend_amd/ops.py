@@ -165,6 +165,50 @@ def make_layer(H, E, k, F, router, gate, up, down, types, n_slots=None, slots=No
     return L
 
 
+class DecodeStack:
+    """A persistent-kernel decode stack over ``layers`` (qwmoe_decode_stack_*).
+
+    Keeps references to the layer tensors it points at; ``run`` pushes one
+    token through every layer in a single launch."""
+
+    def __init__(self, layers: list[Layer], rms_eps: float = 1e-6, keepalive=None):
+        arr = (Layer * len(layers))(*layers)
+        h = C.c_void_p()
+        check(lib().qwmoe_decode_stack_create(C.cast(arr, C.c_void_p), len(layers), rms_eps, C.byref(h)),
+              "decode_stack_create")
+        self.h, self.n_layer, self._keep = h, len(layers), (arr, keepalive)
+        self.H, self.k = layers[0].n_embd, layers[0].n_expert_used
+
+    def run(self, x, out, x_out=None, ids=None, weights=None) -> None:
+        check(lib().qwmoe_decode_stack_run(stream(), self.h, _ptr(x), _ptr(out), _ptr(x_out), _ptr(ids),
+                                           _ptr(weights)), "decode_stack_run")
+
+    def __call__(self, x, want_ids: bool = True):
+        torch = _torch()
+        out = torch.empty(self.H, dtype=torch.float32, device=x.device)
+        xo = torch.empty(self.H, dtype=torch.float32, device=x.device)
+        ids = torch.empty((self.n_layer, self.k), dtype=torch.int32, device=x.device) if want_ids else None
+        w = torch.empty((self.n_layer, self.k), dtype=torch.float32, device=x.device) if want_ids else None
+        self.run(x, out, xo, ids, w)
+        return out, xo, ids, w
+
+    def status(self, clear: bool = True) -> int:
+        v = C.c_int32(0)
+        check(lib().qwmoe_decode_stack_status(stream(), self.h, C.byref(v), int(clear)), "decode_stack_status")
+        return v.value
+
+    def close(self) -> None:
+        if self.h:
+            lib().qwmoe_decode_stack_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 def ffn_layer(layer: Layer, x, rms_eps: float = -1.0):
     """One MoE FFN layer.  x: f32 [T, H] -> (out, x_next or None, ids, weights)."""
     torch = _torch()
