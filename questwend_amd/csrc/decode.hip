@@ -153,26 +153,39 @@ __device__ void quant_q8K_lds(uint32_t* lds, const float* src, int nblocks, uint
     }
 }
 
-template <int TYPE_DOWN>
+// global_load_lds_dwordx4: lane i of the wave lands at lds + off + 16 * i.
+__device__ __forceinline__ void dma16(uint32_t* lds, uint32_t lds_off, const void* src) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*) ((uint8_t*) lds + lds_off), 16, 0, 0);
+}
+// One wave copies nch 16-byte chunks starting at the 16-byte aligned src to
+// LDS at lds_off (no VGPRs held; completion via vmcnt).
+__device__ __forceinline__ void dma_row(uint32_t* lds, uint32_t lds_off, const uint8_t* src, int nch, int lane) {
+    for (int it = 0; it * 64 < nch; ++it)
+        if (it * 64 + lane < nch) dma16(lds, lds_off + (uint32_t) it * 1024u, src + (size_t) (it * 64 + lane) * 16);
+}
+__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+template <int NBH, int NBF, int TYPE_DOWN>
 __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
     extern __shared__ uint32_t lds[];
     __shared__ int32_t s_ids[32];
     __shared__ float s_w[32];
     __shared__ int32_t s_order[512];
     __shared__ float s_p[512];
+    __shared__ float s_e[512];
     __shared__ float s_gsum[64];
     __shared__ double s_red[DEC_WAVES];
     __shared__ SortRange s_stack[SORT_STACK];
     __shared__ int s_need_sort;
 
-    const int G = gridDim.x, b = blockIdx.x, tid = threadIdx.x;
+    const int b = blockIdx.x, tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int H = a.H, E = a.E, k = a.k, F = a.F;
-    const int nbH = H / QK_K, nbF = F / QK_K;
+    const int nbH = NBH > 0 ? NBH : H / QK_K, nbF = NBF > 0 ? NBF : F / QK_K;
     const uint32_t rowA = (uint32_t) nbH * 144u;                                   // gate/up row bytes (Q4_K)
     const uint32_t rowB = (uint32_t) nbF * (TYPE_DOWN == T_Q4_K ? 144u : 210u);   // down row bytes
     float* xs = (float*) ((uint8_t*) lds + a.lds_x);       // x (fp32) of the current layer
-    float* res = (float*) ((uint8_t*) lds + a.lds_res);    // per-row results / act / y staging
+    float* res = (float*) ((uint8_t*) lds + a.lds_res);    // per-row results, then y
     const int P = k * F;
     const int pa0 = b * a.pa_per < P ? b * a.pa_per : P;
     const int pa1 = pa0 + a.pa_per < P ? pa0 + a.pa_per : P;
@@ -180,67 +193,73 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
     const int h0 = b * a.hb_per < H ? b * a.hb_per : H;
     const int h1 = h0 + a.hb_per < H ? h0 + a.hb_per : H;
     const int nh = h1 - h0;
+    const int chA = (int) (rowA / 16);
 
-    // ---- layer 0 input and router row preload -------------------------------
+    // ---- layer 0 input and router row ----------------------------------------
     for (int i = tid; i < H; i += DEC_THREADS) xs[i] = a.x_in[i];
-    if (b < E) copy_chunks(lds, a.lds_rw, (const uint8_t*) (a.layers[0].router + (size_t) b * H), H * 4 / 16);
+    if (b < E && wave == 0) dma_row(lds, a.lds_rw, (const uint8_t*) (a.layers[0].router + (size_t) b * H), H / 4, lane);
+    wait_dma();
     __syncthreads();
 
     for (int l = 0; l < a.n_layer; ++l) {
         const DecodeLayer& L = a.layers[l];
         const uint32_t ep = a.epoch0 + (uint32_t) l;
         const uint32_t rw_cur = a.lds_rw + (uint32_t) (l & 1) * (uint32_t) H * 4u;
-        // ---- C(l-1)/router(l): logit e = b from the LDS router row -----------
+        // ---- router(l): logit e = b from the LDS router row ---------------------
         if (b < E && wave == 0) {
-            // lanes 0..31 = the 32 fma chains of the AVX2 ggml_vec_dot_f32 (np = H, H % 32 == 0)
+            // lanes 0..31 = the 32 fma chains of the AVX2 ggml_vec_dot_f32 (H % 32 == 0)
             const float* w = (const float*) ((uint8_t*) lds + rw_cur);
             float acc = 0.0f;
             if (lane < 32)
                 for (int s = 0; s < H; s += 32) acc = __builtin_fmaf(w[s + lane], xs[s + lane], acc);
-            // chains c_l (l<8) | c_{8+l} | c_{16+l} | c_{24+l} : lanes l, 8+l, 16+l, 24+l
-            float t = acc + __shfl_down(acc, 16, 32);   // c_l + c_{16+l}  (l < 16)
-            t = t + __shfl_down(t, 8, 32);               // (c_l+c_{16+l}) + (c_{8+l}+c_{24+l}) = s_l, l < 8
-            t = t + __shfl_down(t, 4, 32);               // s_l + s_{l+4} = t0_l, l < 4
-            // (t0_0 + t0_1) + (t0_2 + t0_3)
+            float t = acc + __shfl_down(acc, 16, 32);   // c_l + c_{16+l}
+            t = t + __shfl_down(t, 8, 32);               // s_l = (c_l + c_{16+l}) + (c_{8+l} + c_{24+l})
+            t = t + __shfl_down(t, 4, 32);               // t0_l = s_l + s_{l+4}
             const float u = t + __shfl_down(t, 1, 32);
-            const float logit = u + __shfl_down(u, 2, 32);
+            const float logit = u + __shfl_down(u, 2, 32);   // (t0_0 + t0_1) + (t0_2 + t0_3)
             if (lane == 0) st_dev64(a.xl + b, tagged(logit, ep));
         }
-        // prefetch the next layer's router row into the other buffer
-        if (b < E && l + 1 < a.n_layer)
-            copy_chunks(lds, a.lds_rw + (uint32_t) ((l + 1) & 1) * (uint32_t) H * 4u,
-                        (const uint8_t*) (a.layers[l + 1].router + (size_t) b * H), H * 4 / 16);
-        // Q8_K(x) for the gate/up rows
+        // the next layer's router row streams in behind everything else
+        if (b < E && wave == 1 && l + 1 < a.n_layer)
+            dma_row(lds, a.lds_rw + (uint32_t) ((l + 1) & 1) * (uint32_t) H * 4u,
+                    (const uint8_t*) (a.layers[l + 1].router + (size_t) b * H), H / 4, lane);
         quant_q8K_lds(lds, xs, nbH, a.lds_xq);
-        // ---- top-k (every WG) ----------------------------------------------
-        if (!gather_tagged<1>(a, a.xl, E, ep, s_p)) return;
+        // ---- softmax and exact top-k (every WG) ----------------------------------
+        if (!gather_tagged<1>(a, a.xl, E, ep, s_p)) { wait_dma(); return; }
         {
-            // softmax with ggml_v_expf, double sum of 8-lane groups in order
             float mx = -INFINITY;
-            for (int i = 0; i < E; ++i) mx = fmaxf(mx, s_p[i]);
+            for (int i = lane; i < E; i += 64) mx = fmaxf(mx, s_p[i]);
+            for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+            for (int i = tid; i < E; i += DEC_THREADS) s_e[i] = v_expf(s_p[i] - mx);
             __syncthreads();
-            for (int i = tid; i < E; i += DEC_THREADS) s_p[i] = v_expf(s_p[i] - mx);
-            if (tid == 0) s_need_sort = 0;
-            __syncthreads();
-            for (int g = tid; g < E / 8; g += DEC_THREADS) s_gsum[g] = hsum8(&s_p[8 * g]);
+            for (int g = tid; g < E / 8; g += DEC_THREADS) s_gsum[g] = hsum8(&s_e[8 * g]);
             __syncthreads();
             double sum = 0.0;
             for (int g = 0; g < E / 8; ++g) sum += (double) s_gsum[g];
             const float inv = (float) (1.0 / sum);
+            for (int i = tid; i < E; i += DEC_THREADS) s_p[i] = s_e[i] * inv;
             __syncthreads();
-            for (int i = tid; i < E; i += DEC_THREADS) s_p[i] = s_p[i] * inv;
-            __syncthreads();
-            for (int i = tid; i < E; i += DEC_THREADS) {
-                const float pi = s_p[i];
-                int gt = 0, eq = 0;
-                for (int j = 0; j < E; ++j) {
-                    gt += s_p[j] > pi;
-                    eq += s_p[j] == pi;
+            if (wave == 0) {
+                // k rounds of wave arg-max; a second element equal to a selected
+                // value means std::sort's tie order decides -> exact replay below
+                float v[8];
+                for (int j = 0; j < 8; ++j) v[j] = (lane + 64 * j < E) ? s_p[lane + 64 * j] : -1.0f;
+                bool tie = false;
+                for (int r = 0; r < k; ++r) {
+                    float m = v[0];
+                    for (int j = 1; j < 8; ++j) m = fmaxf(m, v[j]);
+                    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+                    int cnt = 0, sel = -1;
+                    for (int j = 0; j < 8; ++j) {
+                        const uint64_t msk = __ballot(v[j] == m);
+                        cnt += __popcll(msk);
+                        if (sel < 0 && msk) sel = 64 * j + __ffsll((unsigned long long) msk) - 1;
+                    }
+                    tie = tie || cnt > 1;
+                    if (lane == 0) s_order[r] = sel;
+                    if (lane == (sel & 63)) v[sel >> 6] = -1.0f;
                 }
-                if (gt < k) {
-                    if (eq > 1) s_need_sort = 1;
-                    else s_order[gt] = i;
-                }
+                if (lane == 0) s_need_sort = tie;
             }
             __syncthreads();
             if (s_need_sort) {
@@ -269,43 +288,44 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
             }
             __syncthreads();
         }
-        // ---- stream this WG's rows: gate/up pairs and down rows ------------
-        // pair p -> slot i = p / F, row f = p % F; LDS row slot 2*(p-pa0) gate, +1 up
-        for (int c = tid; c < np * 2 * (int) (rowA / 16); c += DEC_THREADS) {
-            const int per = (int) (rowA / 16);
-            const int r = c / per, ch = c % per;
+        // ---- stream this WG's gate/up rows (pair p: slot p / F, row p % F) -------
+        for (int r = wave; r < 2 * np; r += DEC_WAVES) {
             const int p = pa0 + (r >> 1);
             const int i = p / F, f = p % F;
             const int e = s_ids[i];
             const bool up = r & 1;
             const int32_t* so = up ? L.slot_up : L.slot_gate;
             int64_t mat = so ? so[e] : e;
-            const int64_t nsl = up ? L.n_slots_up : L.n_slots_gate;
-            if (mat < 0 || mat >= nsl) { atomicOr(a.status, 16); mat = 0; }
+            if (mat < 0 || mat >= (up ? L.n_slots_up : L.n_slots_gate)) {
+                if (lane == 0) atomicOr(a.status, 16);
+                mat = 0;
+            }
             const uint8_t* src = (up ? L.up : L.gate) + (size_t) mat * (up ? L.up_nb2 : L.gate_nb2) +
                                  (size_t) f * (up ? L.up_nb1 : L.gate_nb1);
-            ((uint4*) ((uint8_t*) lds + a.lds_a + (uint32_t) r * a.rs_a))[ch] = ((const uint4*) src)[ch];
+            dma_row(lds, a.lds_a + (uint32_t) r * a.rs_a, src, chA, lane);
         }
-        {
-            const int perB = (int) ((rowB + 30) / 16);   // row plus up to 15 bytes of misalignment
-            for (int c = tid; c < k * nh * perB; c += DEC_THREADS) {
-                const int r = c / perB, ch = c % perB;
-                const int i = r / nh, hh = r % nh;
-                const int e = s_ids[i];
-                int64_t mat = L.slot_down ? L.slot_down[e] : e;
-                if (mat < 0 || mat >= L.n_slots_down) { atomicOr(a.status, 16); mat = 0; }
-                const uint8_t* rowp = L.down + (size_t) mat * L.down_nb2 + (size_t) (h0 + hh) * L.down_nb1;
-                const uint8_t* base = (const uint8_t*) ((uintptr_t) rowp & ~(uintptr_t) 15);
-                if ((uint32_t) ch * 16u < (uint32_t) ((rowp + rowB) - base))
-                    ((uint4*) ((uint8_t*) lds + a.lds_b + (uint32_t) r * a.rs_b))[ch] = ((const uint4*) base)[ch];
-            }
-        }
+        wait_dma();
         __syncthreads();
-        // ---- A: gate / up rows, SwiGLU ---------------------------------------
+        // ---- and the down rows, which land while A computes and act is exchanged -
+        for (int r = wave; r < k * nh; r += DEC_WAVES) {
+            const int i = r / nh, hh = r % nh;
+            const int e = s_ids[i];
+            int64_t mat = L.slot_down ? L.slot_down[e] : e;
+            if (mat < 0 || mat >= L.n_slots_down) {
+                if (lane == 0) atomicOr(a.status, 16);
+                mat = 0;
+            }
+            const uint8_t* rowp = L.down + (size_t) mat * L.down_nb2 + (size_t) (h0 + hh) * L.down_nb1;
+            const uint8_t* base = (const uint8_t*) ((uintptr_t) rowp & ~(uintptr_t) 15);
+            dma_row(lds, a.lds_b + (uint32_t) r * a.rs_b, base, (int) ((rowp + rowB - base + 15) / 16), lane);
+        }
+        // ---- A: gate / up rows, SwiGLU ---------------------------------------------
         for (int r0 = 0; r0 < np * 2; r0 += DEC_WAVES * 8) {
             const int r = r0 + wave * 8 + (lane >> 3);
             const int rr = r < np * 2 ? r : 0;
-            const float v = row_dot_lds<T_Q4_K>(lds, a.lds_a + (uint32_t) rr * a.rs_a, a.lds_xq, nbH, lane & 7);
+            float v;
+            if constexpr (NBH > 0) v = row_dot_q4k_a<NBH>(lds, a.lds_a + (uint32_t) rr * a.rs_a, a.lds_xq, lane & 7);
+            else v = row_dot_lds<T_Q4_K>(lds, a.lds_a + (uint32_t) rr * a.rs_a, a.lds_xq, nbH, lane & 7);
             if (r < np * 2 && (lane & 7) == 0) res[r] = v;
         }
         __syncthreads();
@@ -313,10 +333,11 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
             const float act = v_silu(res[2 * j]) * res[2 * j + 1];
             st_dev64(a.xa + pa0 + j, tagged(act, ep));
         }
-        // ---- B: all act -> Q8_K per slot; down rows; weighted sum -----------
-        float* actf = (float*) ((uint8_t*) lds + a.lds_act);   // k*F floats (reuses the gate/up rows' space)
-        if (!gather_tagged<12>(a, a.xa, P, ep, actf)) return;
+        // ---- B: all act -> Q8_K per slot; down rows; weighted sum ------------------
+        float* actf = (float*) ((uint8_t*) lds + a.lds_act);
+        if (!gather_tagged<12>(a, a.xa, P, ep, actf)) { wait_dma(); return; }
         quant_q8K_lds(lds, actf, k * nbF, a.lds_aq);
+        wait_dma();
         __syncthreads();
         for (int r0 = 0; r0 < k * nh; r0 += DEC_WAVES * 8) {
             const int r = r0 + wave * 8 + (lane >> 3);
@@ -327,13 +348,20 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
             if (mat < 0 || mat >= L.n_slots_down) mat = 0;
             const uint8_t* rowp = L.down + (size_t) mat * L.down_nb2 + (size_t) (h0 + hh) * L.down_nb1;
             const uint32_t wb = a.lds_b + (uint32_t) rr * a.rs_b + (uint32_t) ((uintptr_t) rowp & 15);
-            const float v = row_dot_lds<TYPE_DOWN>(lds, wb, a.lds_aq + (uint32_t) (i * nbF) * 292u, nbF, lane & 7);
+            const uint32_t ab = a.lds_aq + (uint32_t) (i * nbF) * 292u;
+            float v;
+            if constexpr (TYPE_DOWN == T_Q4_K && NBF > 0) {
+                v = (wb & 3) == 0 ? row_dot_q4k_a<NBF>(lds, wb, ab, lane & 7)
+                                  : row_dot_lds<TYPE_DOWN>(lds, wb, ab, nbF, lane & 7);
+            } else {
+                v = row_dot_lds<TYPE_DOWN>(lds, wb, ab, nbF, lane & 7);
+            }
             if (r < k * nh && (lane & 7) == 0) res[r] = v;
         }
         __syncthreads();
         for (int hh = tid; hh < nh; hh += DEC_THREADS) {
-            // ggml_vec_dot_f32(k, experts^T row, w): k < 32 -> scalar tail, groups of
-            // four as mul+add, the remainder fused
+            // ggml_vec_dot_f32(k, experts^T row, w): k < 32 -> scalar tail: groups of
+            // four as mul + add, the remainder fused
             float sumf = 0.0f;
             const int nv = k & ~3;
             for (int i = 0; i < k; ++i) {
@@ -342,10 +370,10 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
             }
             st_dev64(a.xy + h0 + hh, tagged(sumf, ep));
         }
-        // ---- C: all y -> RMSNorm -> x of the next layer -----------------------
-        float* ys = res;   // reuse (H floats): every thread must be done with the down results
+        // ---- C: all y -> RMSNorm -> x of the next layer ----------------------------
+        float* ys = res;   // reused: every thread must be done with the down results
         __syncthreads();
-        if (!gather_tagged<4>(a, a.xy, H, ep, ys)) return;
+        if (!gather_tagged<4>(a, a.xy, H, ep, ys)) { wait_dma(); return; }
         {
             double s = 0.0;
             for (int i = tid; i < H; i += DEC_THREADS) {
@@ -408,7 +436,10 @@ int launch_decode_stack(const DecodeStackDesc& d, const float* x_in, float* out,
     a.rs_a = d.rs_a;
     a.rs_b = d.rs_b;
     void* args[] = {&a};
-    const void* fn = d.type_down == T_Q6_K ? (const void*) k_decode_stack<T_Q6_K> : (const void*) k_decode_stack<T_Q4_K>;
+    const void* fn;
+    if (d.type_down == T_Q4_K && d.H == 2048 && d.F == 768) fn = (const void*) k_decode_stack<8, 3, T_Q4_K>;
+    else if (d.type_down == T_Q6_K) fn = (const void*) k_decode_stack<0, 0, T_Q6_K>;
+    else fn = (const void*) k_decode_stack<0, 0, T_Q4_K>;
     hipError_t e = hipLaunchCooperativeKernel(fn, dim3((unsigned) d.grid), dim3(DEC_THREADS), args, d.lds_total, stream);
     return e == hipSuccess ? 0 : -3;
 }

@@ -103,6 +103,26 @@ __device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, int& d, in
 
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
+// DPP lane exchanges inside a row of 16 lanes (VALU latency, no LDS round trip).
+// xor1 / xor2 are exact lane-xor patterns; half_mirror (i <-> 7-i in each 8) and
+// mirror (i <-> 15-i) pair lanes across 4- and 8-lane groups, which is all a
+// reduction needs once the smaller groups already agree.
+enum : int { DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140 };
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// LDS-only workgroup barrier: orders LDS traffic but, unlike __syncthreads,
+// does not wait for outstanding global stores to be acknowledged.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Unaligned little-endian reads (compiler splits them to what the alignment allows).
 template <typename T>
 __device__ __forceinline__ T ld_unaligned(const void* p) {

@@ -68,6 +68,55 @@ __device__ __forceinline__ float row_dot_lds<T_Q4_K>(const uint32_t* lds, uint32
     return a + m;
 }
 
+// Q4_K x Q8_K for 4-byte aligned weight and activation rows, NB super-blocks
+// known at compile time (fully unrolled: all LDS reads can be issued early).
+// Same integer lanes and float order as row_dot_lds<T_Q4_K>.
+template <int NB>
+__device__ __forceinline__ float row_dot_q4k_a(const uint32_t* lds, uint32_t wbase, uint32_t abase, int n) {
+    float acc = 0.0f, accm = 0.0f;
+    const uint32_t* w = lds + (wbase >> 2);
+    const uint32_t* y = lds + (abase >> 2);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const uint32_t* blk = w + 36 * b;   // 144 bytes
+        const uint32_t* yb = y + 73 * b;    // 292 bytes
+        const uint32_t h0 = blk[0], s0 = blk[1], s1 = blk[2], s2 = blk[3];
+        // the 8 six-bit scales and mins as bytes (the utmp shuffle of quants.c:2067-2072)
+        const uint32_t sc_lo = s0 & 0x3f3f3f3fu;
+        const uint32_t sc_hi = (s2 & 0x0f0f0f0fu) | (((s0 >> 6) & 0x03030303u) << 4);
+        const uint32_t mn_lo = s1 & 0x3f3f3f3fu;
+        const uint32_t mn_hi = ((s2 >> 4) & 0x0f0f0f0fu) | (((s1 >> 6) & 0x03030303u) << 4);
+        int sumi = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t scw = j < 2 ? sc_lo : sc_hi;
+            const int sl = (int) ((scw >> (16 * (j & 1))) & 0xff);
+            const int sh = (int) ((scw >> (16 * (j & 1) + 8)) & 0xff);
+            const uint32_t wq = blk[4 + 8 * j + n];
+            const int lo = (int) (wq & 0x0F0F0F0Fu), hi = (int) ((wq >> 4) & 0x0F0F0F0Fu);
+            sumi += sl * sdot4(lo, (int) yb[1 + 16 * j + n], 0) + sh * sdot4(hi, (int) yb[1 + 16 * j + 8 + n], 0);
+        }
+        const float yd = bitsf(yb[0]);
+        acc = __builtin_fmaf(yd * h2f((uint16_t) (h0 & 0xffff)), (float) sumi, acc);
+        if (n < 4) {
+            const uint32_t bs01 = yb[65 + 2 * n], bs23 = yb[66 + 2 * n];
+            const int q8s0 = (int) (int16_t) (bs01 & 0xffff) + (int) (int16_t) (bs01 >> 16);
+            const int q8s1 = (int) (int16_t) (bs23 & 0xffff) + (int) (int16_t) (bs23 >> 16);
+            const uint32_t mw = n < 2 ? mn_lo : mn_hi;
+            const int m0 = (int) ((mw >> (16 * (n & 1))) & 0xff), m1 = (int) ((mw >> (16 * (n & 1) + 8)) & 0xff);
+            accm = __builtin_fmaf(-yd * h2f((uint16_t) (h0 >> 16)), (float) (m0 * q8s0 + m1 * q8s1), accm);
+        }
+    }
+    float a = acc;
+    a = a + __shfl_down(a, 4, 8);
+    a = a + __shfl_down(a, 2, 8);
+    a = a + __shfl_down(a, 1, 8);
+    float m = accm;
+    m = m + __shfl_down(m, 2, 8);
+    m = m + __shfl_down(m, 1, 8);
+    return a + m;
+}
+
 template <>
 __device__ __forceinline__ float row_dot_lds<T_Q6_K>(const uint32_t* lds, uint32_t wbase, uint32_t abase, int nb, int n) {
     float acc = 0.0f;
