@@ -3,18 +3,19 @@
 // build_moe per layer inside one graph, decode() -> build_graph, 976-1100).
 //
 // One workgroup per CU, all co-resident (cooperative launch).  Per layer:
-//   A  every WG: top-k from the layer's logits; Q8_K(x); stream its slice of the
-//      selected experts' gate/up rows into LDS (and, already, its down rows);
-//      gate, up, SwiGLU for its row pairs -> act
-//   B  every WG: all act -> Q8_K per expert; its H/G output rows of all k experts'
-//      down projections; weighted expert sum -> y rows
-//   C  every WG: all y -> RMSNorm -> x of the next layer; WG e computes router
-//      logit e of the next layer from its LDS copy of that router row
+//   top-k  every WG: softmax + exact top-k from the layer's E logits
+//   A      every WG: Q8_K(x); its slice of the selected experts' gate/up row
+//          pairs (loaded to LDS) -> gate, up, SwiGLU -> act words
+//   B      every WG: all act -> Q8_K per expert; its H/G output rows of all k
+//          experts' down projections (loads issued before A computes, held in
+//          registers while act is exchanged); weighted expert sum -> y words
+//   C      every WG: all y -> RMSNorm -> x of the next layer; WG e computes
+//          router logit e of the next layer from its LDS copy of that row
 // Cross-WG data (act, y, logits) moves through device memory as 64-bit words
 // {value, epoch}; consumers poll the words themselves, so one memory round
-// trip both carries the data and signals it.  All such accesses are
-// device-scope relaxed atomics; producers order their writes with a wait for
-// store completion before anything that depends on them.
+// trip both carries the data and signals it.  Those accesses are device-scope
+// relaxed atomics.  Inside a WG all sharing goes through LDS, so the barriers
+// order LDS traffic only and never wait for global stores to be acknowledged.
 //
 // Every float operation reproduces ggml's AVX2 CPU order (qw_rowdot.hpp,
 // router/ffn semantics), so ids and outputs are bit-identical to the reference.
@@ -27,7 +28,9 @@ namespace qw {
 
 constexpr int DEC_THREADS = 512;
 constexpr int DEC_WAVES = DEC_THREADS / 64;
-constexpr long DEC_SPIN_LIMIT = 1L << 22;   // ~seconds: a stuck wait aborts the launch
+constexpr long DEC_SPIN_LIMIT = 1L << 22;   // ~seconds: a stuck wait abandons the launch
+constexpr int MAXJ_A = 8;                    // 16-byte gate/up chunks per thread per round
+constexpr int MAXJ_B = 4;                    // 16-byte down chunks held per thread
 
 struct DecodeArgs {
     const DecodeLayer* layers;
@@ -49,7 +52,7 @@ struct DecodeArgs {
     // partition / LDS layout (host computed)
     int pa_per;               // row pairs per WG (ceil(k*F / G))
     int hb_per;               // down rows per WG (multiple of 4)
-    uint32_t lds_rw, lds_a, lds_b, lds_xq, lds_aq, lds_x, lds_act, lds_res, lds_total;
+    uint32_t lds_rw, lds_a, lds_b, lds_xq, lds_aq, lds_x, lds_act, lds_res, lds_y, lds_total;
     uint32_t rs_a;            // LDS stride of a gate/up row
     uint32_t rs_b;            // LDS stride of a down row (16-aligned)
 };
@@ -74,96 +77,120 @@ __device__ __forceinline__ void raise_abort(const DecodeArgs& a, int bit) {
 }
 
 // Polls n tagged words (this thread's share: idx = tid + j * DEC_THREADS) until
-// all carry `epoch`, storing the float payloads to dst[idx].  Loads of one
-// round are independent, so a round costs one memory round trip.  Returns
-// false on abort.
+// all carry `epoch`, storing the float payloads to dst[idx] (LDS).  Loads of one
+// round are independent, so a round costs one memory round trip.  A thread
+// that gives up sets *fail (LDS); the caller reads it after its next barrier.
 template <int MAXJ>
-__device__ bool gather_tagged(const DecodeArgs& a, const uint64_t* src, int n, uint32_t epoch, float* dst) {
+__device__ void gather_tagged(const DecodeArgs& a, const uint64_t* src, int n, uint32_t epoch, float* dst,
+                              int* fail) {
     const int tid = threadIdx.x;
-    bool ok = true;
-    for (int base = 0; base < n && ok; base += MAXJ * DEC_THREADS) {
+    for (int base = 0; base < n; base += MAXJ * DEC_THREADS) {
         uint64_t v[MAXJ];
         long spins = 0;
+        bool ok;
         do {
             ok = true;
+#pragma unroll
             for (int j = 0; j < MAXJ; ++j) {
                 const int idx = base + tid + j * DEC_THREADS;
                 v[j] = idx < n ? ld_dev64(src + idx) : ((uint64_t) epoch << 32);
             }
+#pragma unroll
             for (int j = 0; j < MAXJ; ++j) ok = ok && ((uint32_t) (v[j] >> 32) == epoch);
             if (!ok) {
                 if (++spins > DEC_SPIN_LIMIT) { raise_abort(a, 8); break; }
                 if ((spins & 255) == 0 && aborted(a)) break;
             }
         } while (!ok);
+        if (!ok) {
+            *fail = 1;
+            return;
+        }
+#pragma unroll
         for (int j = 0; j < MAXJ; ++j) {
             const int idx = base + tid + j * DEC_THREADS;
             if (idx < n) dst[idx] = bitsf((uint32_t) v[j]);
         }
     }
-    return __syncthreads_or(!ok) == 0;
 }
 
-// 16-byte chunks from global to LDS (each thread a strided subset).
-__device__ __forceinline__ void copy_chunks(uint32_t* lds, uint32_t lds_off, const uint8_t* g, int nchunks) {
-    uint4* d = (uint4*) ((uint8_t*) lds + lds_off);
-    const uint4* s = (const uint4*) g;
-    for (int c = threadIdx.x; c < nchunks; c += DEC_THREADS) d[c] = s[c];
-}
-
-// Q8_K of n fp32 values in LDS (n % 256 == 0) into blocks at lds byte offset q.
-// One wave per block; the reduction follows quantize_row_q8_K_ref exactly.
-__device__ void quant_q8K_lds(uint32_t* lds, const float* src, int nblocks, uint32_t q) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    for (int b = wave; b < nblocks; b += DEC_WAVES) {
-        const float* x = src + b * QK_K;
-        float v[4];
-        for (int i = 0; i < 4; ++i) v[i] = x[4 * lane + i];
+// Q8_K (quantize_row_q8_K_ref, ggml-quants.c) of nblocks x 256 fp32 values in
+// LDS into blocks at LDS byte offset q.  Sixteen lanes (one DPP row) per block,
+// sixteen consecutive values per lane: the first-index max |x| is a four-step
+// row reduction and each lane's values form exactly one bsums group.
+__device__ void quant_q8K_lds16(uint32_t* lds, const float* src, int nblocks, uint32_t q) {
+    const int grp = threadIdx.x >> 4, l = threadIdx.x & 15;
+    for (int b = grp; b < nblocks; b += DEC_THREADS / 16) {
+        const float* x = src + b * QK_K + 16 * l;
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 16; i += 4) {
+            const float4 t = *(const float4*) (x + i);
+            v[i] = t.x;
+            v[i + 1] = t.y;
+            v[i + 2] = t.z;
+            v[i + 3] = t.w;
+        }
         float am = 0.0f;
         int ai = 0x7fffffff;
-        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
             const float t = __builtin_fabsf(v[i]);
-            if (t > am) { am = t; ai = 4 * lane + i; }
+            if (t > am) { am = t; ai = 16 * l + i; }
         }
-        for (int off = 32; off >= 1; off >>= 1) {
-            const float om = __shfl_xor(am, off);
-            const int oi = __shfl_xor(ai, off);
-            if (om > am || (om == am && oi < ai)) { am = om; ai = oi; }
-        }
+#define QW_AMAX_STEP(C)                                             \
+    {                                                               \
+        const float om = dpp_f<C>(am);                              \
+        const int oi = dpp_i<C>(ai);                                \
+        if (om > am || (om == am && oi < ai)) { am = om; ai = oi; } \
+    }
+        QW_AMAX_STEP(DPP_XOR1)
+        QW_AMAX_STEP(DPP_XOR2)
+        QW_AMAX_STEP(DPP_HALF_MIRROR)
+        QW_AMAX_STEP(DPP_MIRROR)
+#undef QW_AMAX_STEP
         uint8_t* blk = (uint8_t*) lds + q + (uint32_t) b * 292u;
+        uint32_t* qw = (uint32_t*) (blk + 4 + 16 * l);
         if (!(am > 0.0f)) {
-            *(uint32_t*) (blk + 4 + 4 * lane) = 0;
-            if (lane < 16) *(int16_t*) (blk + 260 + 2 * lane) = 0;
-            if (lane == 0) *(float*) blk = 0.0f;
+            qw[0] = qw[1] = qw[2] = qw[3] = 0;
+            *(int16_t*) (blk + 260 + 2 * l) = 0;
+            if (l == 0) *(float*) blk = 0.0f;
             continue;
         }
-        const float iscale = -127.f / x[ai];
-        int qv[4], s = 0;
-        for (int i = 0; i < 4; ++i) {
-            const int t = nearest_int(iscale * v[i]);
-            qv[i] = t < 127 ? t : 127;
-            s += qv[i];
+        const float iscale = -127.f / src[b * QK_K + ai];
+        int s = 0;
+        uint32_t words[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            int t = nearest_int(iscale * v[i]);
+            t = t < 127 ? t : 127;
+            s += t;
+            words[i >> 2] |= (uint32_t) (t & 0xff) << (8 * (i & 3));
         }
-        *(uint32_t*) (blk + 4 + 4 * lane) = (uint32_t) (qv[0] & 0xff) | ((uint32_t) (qv[1] & 0xff) << 8) |
-                                            ((uint32_t) (qv[2] & 0xff) << 16) | ((uint32_t) (qv[3] & 0xff) << 24);
-        s += __shfl_xor(s, 1);
-        s += __shfl_xor(s, 2);
-        if ((lane & 3) == 0) *(int16_t*) (blk + 260 + 2 * (lane >> 2)) = (int16_t) s;
-        if (lane == 0) *(float*) blk = 1.0f / iscale;
+        qw[0] = words[0];
+        qw[1] = words[1];
+        qw[2] = words[2];
+        qw[3] = words[3];
+        *(int16_t*) (blk + 260 + 2 * l) = (int16_t) s;
+        if (l == 0) *(float*) blk = 1.0f / iscale;
     }
 }
 
-// global_load_lds_dwordx4: lane i of the wave lands at lds + off + 16 * i.
-__device__ __forceinline__ void dma16(uint32_t* lds, uint32_t lds_off, const void* src) {
-    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*) ((uint8_t*) lds + lds_off), 16, 0, 0);
+// 16-byte global loads through the global address space (a generic pointer
+// would become a flat load, which also occupies the LDS counter).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) const u32x4 g_u32x4;
+__device__ __forceinline__ u32x4 ldg16(const void* p) { return *(g_u32x4*) p; }
+__device__ __forceinline__ void sts16(uint32_t* lds, uint32_t byte_off, u32x4 v) {
+    *(u32x4*) ((uint8_t*) lds + byte_off) = v;
 }
-// One wave copies nch 16-byte chunks starting at the 16-byte aligned src to
-// LDS at lds_off (no VGPRs held; completion via vmcnt).
-__device__ __forceinline__ void dma_row(uint32_t* lds, uint32_t lds_off, const uint8_t* src, int nch, int lane) {
-    for (int it = 0; it * 64 < nch; ++it)
-        if (it * 64 + lane < nch) dma16(lds, lds_off + (uint32_t) it * 1024u, src + (size_t) (it * 64 + lane) * 16);
+
+// 16-byte chunk ch of a down row starting at rowp (any alignment): the chunk of
+// the row's 16-aligned base, or null past the row's end.
+__device__ __forceinline__ const u32x4* down_chunk(const uint8_t* rowp, uint32_t rowB, int ch) {
+    const uint8_t* base = (const uint8_t*) ((uintptr_t) rowp & ~(uintptr_t) 15);
+    return (uint32_t) ch * 16u < (uint32_t) (rowp + rowB - base) ? (const u32x4*) base + ch : nullptr;
 }
-__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 template <int NBH, int NBF, int TYPE_DOWN>
 __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
@@ -171,21 +198,26 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
     __shared__ int32_t s_ids[32];
     __shared__ float s_w[32];
     __shared__ int32_t s_order[512];
-    __shared__ float s_p[512];
+    __shared__ __align__(16) float s_p[512];
     __shared__ float s_e[512];
     __shared__ float s_gsum[64];
     __shared__ double s_red[DEC_WAVES];
+    __shared__ const uint8_t* s_rowA[96];
+    __shared__ const uint8_t* s_rowB[256];
     __shared__ SortRange s_stack[SORT_STACK];
     __shared__ int s_need_sort;
+    __shared__ int s_fail;
 
-    const int b = blockIdx.x, tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63;
+    const int b = blockIdx.x, tid0 = threadIdx.x;
     const int H = a.H, E = a.E, k = a.k, F = a.F;
     const int nbH = NBH > 0 ? NBH : H / QK_K, nbF = NBF > 0 ? NBF : F / QK_K;
-    const uint32_t rowA = (uint32_t) nbH * 144u;                                   // gate/up row bytes (Q4_K)
+    const int chA = 9 * nbH;                                                       // 144-byte blocks / 16
     const uint32_t rowB = (uint32_t) nbF * (TYPE_DOWN == T_Q4_K ? 144u : 210u);   // down row bytes
+    const int chB = (int) ((rowB + 30) / 16);                                     // incl. misalignment
     float* xs = (float*) ((uint8_t*) lds + a.lds_x);       // x (fp32) of the current layer
-    float* res = (float*) ((uint8_t*) lds + a.lds_res);    // per-row results, then y
+    float* res = (float*) ((uint8_t*) lds + a.lds_res);    // per-row dot results
+    float* ys = (float*) ((uint8_t*) lds + a.lds_y);       // gathered y
+    float* actf = (float*) ((uint8_t*) lds + a.lds_act);   // gathered act
     const int P = k * F;
     const int pa0 = b * a.pa_per < P ? b * a.pa_per : P;
     const int pa1 = pa0 + a.pa_per < P ? pa0 + a.pa_per : P;
@@ -193,22 +225,27 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
     const int h0 = b * a.hb_per < H ? b * a.hb_per : H;
     const int h1 = h0 + a.hb_per < H ? h0 + a.hb_per : H;
     const int nh = h1 - h0;
-    const int chA = (int) (rowA / 16);
+    const int nA = 2 * np * chA;            // gate/up chunks of this WG
+    const int nB = k * nh * chB;            // down chunks (upper bound)
+    const bool b_fits = nB <= MAXJ_B * DEC_THREADS;
 
     // ---- layer 0 input and router row ----------------------------------------
-    for (int i = tid; i < H; i += DEC_THREADS) xs[i] = a.x_in[i];
-    if (b < E && wave == 0) dma_row(lds, a.lds_rw, (const uint8_t*) (a.layers[0].router + (size_t) b * H), H / 4, lane);
-    wait_dma();
-    __syncthreads();
+    if (tid0 == 0) s_fail = 0;
+    for (int i = tid0; i < H; i += DEC_THREADS) xs[i] = a.x_in[i];
+    if (b < E)
+        for (int c = tid0; c < H / 4; c += DEC_THREADS)
+            sts16(lds, a.lds_rw + 16u * c, ldg16(a.layers[0].router + (size_t) b * H + 4 * c));
+    lds_barrier();
 
     for (int l = 0; l < a.n_layer; ++l) {
         const DecodeLayer& L = a.layers[l];
         const uint32_t ep = a.epoch0 + (uint32_t) l;
-        const uint32_t rw_cur = a.lds_rw + (uint32_t) (l & 1) * (uint32_t) H * 4u;
+        const int tid = opaque(tid0);   // per-thread addresses are rebuilt every layer
+        const int wave = tid >> 6, lane = tid & 63;
         // ---- router(l): logit e = b from the LDS router row ---------------------
         if (b < E && wave == 0) {
             // lanes 0..31 = the 32 fma chains of the AVX2 ggml_vec_dot_f32 (H % 32 == 0)
-            const float* w = (const float*) ((uint8_t*) lds + rw_cur);
+            const float* w = (const float*) ((uint8_t*) lds + a.lds_rw + (uint32_t) (l & 1) * (uint32_t) H * 4u);
             float acc = 0.0f;
             if (lane < 32)
                 for (int s = 0; s < H; s += 32) acc = __builtin_fmaf(w[s + lane], xs[s + lane], acc);
@@ -219,77 +256,91 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
             const float logit = u + __shfl_down(u, 2, 32);   // (t0_0 + t0_1) + (t0_2 + t0_3)
             if (lane == 0) st_dev64(a.xl + b, tagged(logit, ep));
         }
-        // the next layer's router row streams in behind everything else
-        if (b < E && wave == 1 && l + 1 < a.n_layer)
-            dma_row(lds, a.lds_rw + (uint32_t) ((l + 1) & 1) * (uint32_t) H * 4u,
-                    (const uint8_t*) (a.layers[l + 1].router + (size_t) b * H), H / 4, lane);
-        quant_q8K_lds(lds, xs, nbH, a.lds_xq);
+        quant_q8K_lds16(lds, xs, nbH, a.lds_xq);
+        // the next layer's router row: loaded now, written to LDS after the logit wait
+        const bool rw_next = b < E && l + 1 < a.n_layer;
+        const float* rw_src = rw_next ? a.layers[l + 1].router + (size_t) b * H : nullptr;
+        const uint32_t rw_dst = a.lds_rw + (uint32_t) ((l + 1) & 1) * (uint32_t) H * 4u;
+        const bool rw0 = rw_next && tid < H / 4, rw1 = rw_next && tid + DEC_THREADS < H / 4;
+        u32x4 rwv0, rwv1;
+        if (rw0) rwv0 = ldg16(rw_src + 4 * tid);
+        if (rw1) rwv1 = ldg16(rw_src + 4 * (tid + DEC_THREADS));
         // ---- softmax and exact top-k (every WG) ----------------------------------
-        if (!gather_tagged<1>(a, a.xl, E, ep, s_p)) { wait_dma(); return; }
+        gather_tagged<1>(a, a.xl, E, ep, s_p, &s_fail);
+        if (rw0) sts16(lds, rw_dst + 16u * tid, rwv0);
+        if (rw1) sts16(lds, rw_dst + 16u * (tid + DEC_THREADS), rwv1);
+        if (tid == 0) s_need_sort = 0;
+        lds_barrier();
+        if (s_fail) return;
         {
+            // ggml_soft_max (ggml-cpu/ops.cpp): max, ggml_vec_soft_max_f32 (exp in
+            // AVX2 groups of 8, double sum), scale by 1/sum
             float mx = -INFINITY;
             for (int i = lane; i < E; i += 64) mx = fmaxf(mx, s_p[i]);
-            for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+            mx = fmaxf(mx, dpp_f<DPP_XOR1>(mx));
+            mx = fmaxf(mx, dpp_f<DPP_XOR2>(mx));
+            mx = fmaxf(mx, dpp_f<DPP_HALF_MIRROR>(mx));
+            mx = fmaxf(mx, dpp_f<DPP_MIRROR>(mx));
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
             for (int i = tid; i < E; i += DEC_THREADS) s_e[i] = v_expf(s_p[i] - mx);
-            __syncthreads();
+            lds_barrier();
             for (int g = tid; g < E / 8; g += DEC_THREADS) s_gsum[g] = hsum8(&s_e[8 * g]);
-            __syncthreads();
+            lds_barrier();
             double sum = 0.0;
             for (int g = 0; g < E / 8; ++g) sum += (double) s_gsum[g];
             const float inv = (float) (1.0 / sum);
             for (int i = tid; i < E; i += DEC_THREADS) s_p[i] = s_e[i] * inv;
-            __syncthreads();
-            if (wave == 0) {
-                // k rounds of wave arg-max; a second element equal to a selected
-                // value means std::sort's tie order decides -> exact replay below
-                float v[8];
-                for (int j = 0; j < 8; ++j) v[j] = (lane + 64 * j < E) ? s_p[lane + 64 * j] : -1.0f;
-                bool tie = false;
-                for (int r = 0; r < k; ++r) {
-                    float m = v[0];
-                    for (int j = 1; j < 8; ++j) m = fmaxf(m, v[j]);
-                    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-                    int cnt = 0, sel = -1;
-                    for (int j = 0; j < 8; ++j) {
-                        const uint64_t msk = __ballot(v[j] == m);
-                        cnt += __popcll(msk);
-                        if (sel < 0 && msk) sel = 64 * j + __ffsll((unsigned long long) msk) - 1;
-                    }
-                    tie = tie || cnt > 1;
-                    if (lane == 0) s_order[r] = sel;
-                    if (lane == (sel & 63)) v[sel >> 6] = -1.0f;
+            lds_barrier();
+            // argsort (descending) by ranks: with no value tied (or unordered)
+            // inside the first k places the order is unique; otherwise std::sort's
+            // own tie order decides -> exact replay below
+            for (int i = tid; i < E; i += DEC_THREADS) {
+                const float pi = s_p[i];
+                int gt = 0, eq = 0;
+#pragma unroll 4
+                for (int j = 0; j < E; j += 4) {
+                    const float4 q = *(const float4*) (s_p + j);
+                    gt += (q.x > pi) + (q.y > pi) + (q.z > pi) + (q.w > pi);
+                    eq += (q.x == pi) + (q.y == pi) + (q.z == pi) + (q.w == pi);
                 }
-                if (lane == 0) s_need_sort = tie;
+                if (gt < k) {
+                    if (eq != 1) s_need_sort = 1;
+                    else s_order[gt] = i;
+                }
             }
-            __syncthreads();
+            lds_barrier();
             if (s_need_sort) {
                 if (tid == 0) {
                     for (int i = 0; i < E; ++i) s_order[i] = i;
                     libstdcxx_sort_desc(s_order, E, s_p, s_stack);
                     if (b == 0) atomicOr(a.status, 1);
                 }
-                __syncthreads();
+                lds_barrier();
             }
-            if (tid == 0) {
+            if (tid < k) {
+                const int id = s_order[tid];
+                s_ids[tid] = id;
+                s_e[tid] = s_p[id];
+            }
+            lds_barrier();
+            // weights: selected probabilities / clamp(sum) (* scale)
+            if (tid < k) {
                 double s = 0.0;
-                for (int i = 0; i < k; ++i) s += (double) s_p[s_order[i]];
+                for (int i = 0; i < k; ++i) s += (double) s_e[i];
                 float wsum = (float) s;
                 wsum = fmaxf(fminf(wsum, INFINITY), 6.103515625e-5f);
-                for (int i = 0; i < k; ++i) {
-                    float wi = s_p[s_order[i]] / wsum;
-                    if (a.scale != 0.0f && a.scale != 1.0f) wi = wi * a.scale;
-                    s_ids[i] = s_order[i];
-                    s_w[i] = wi;
-                    if (b == 0 && a.ids_out) {
-                        a.ids_out[l * k + i] = s_order[i];
-                        a.w_out[l * k + i] = wi;
-                    }
+                float wi = s_e[tid] / wsum;
+                if (a.scale != 0.0f && a.scale != 1.0f) wi = wi * a.scale;
+                s_w[tid] = wi;
+                if (b == 0 && a.ids_out) {
+                    a.ids_out[l * k + tid] = s_ids[tid];
+                    a.w_out[l * k + tid] = wi;
                 }
             }
-            __syncthreads();
         }
-        // ---- stream this WG's gate/up rows (pair p: slot p / F, row p % F) -------
-        for (int r = wave; r < 2 * np; r += DEC_WAVES) {
+        // ---- row addresses of this WG's gate/up pairs and down rows -------------
+        for (int r = tid; r < 2 * np; r += DEC_THREADS) {
             const int p = pa0 + (r >> 1);
             const int i = p / F, f = p % F;
             const int e = s_ids[i];
@@ -297,28 +348,38 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
             const int32_t* so = up ? L.slot_up : L.slot_gate;
             int64_t mat = so ? so[e] : e;
             if (mat < 0 || mat >= (up ? L.n_slots_up : L.n_slots_gate)) {
-                if (lane == 0) atomicOr(a.status, 16);
+                atomicOr(a.status, 16);
                 mat = 0;
             }
-            const uint8_t* src = (up ? L.up : L.gate) + (size_t) mat * (up ? L.up_nb2 : L.gate_nb2) +
-                                 (size_t) f * (up ? L.up_nb1 : L.gate_nb1);
-            dma_row(lds, a.lds_a + (uint32_t) r * a.rs_a, src, chA, lane);
+            s_rowA[r] = (up ? L.up : L.gate) + (size_t) mat * (up ? L.up_nb2 : L.gate_nb2) +
+                        (size_t) f * (up ? L.up_nb1 : L.gate_nb1);
         }
-        wait_dma();
-        __syncthreads();
-        // ---- and the down rows, which land while A computes and act is exchanged -
-        for (int r = wave; r < k * nh; r += DEC_WAVES) {
+        for (int r = tid; r < k * nh; r += DEC_THREADS) {
             const int i = r / nh, hh = r % nh;
             const int e = s_ids[i];
             int64_t mat = L.slot_down ? L.slot_down[e] : e;
             if (mat < 0 || mat >= L.n_slots_down) {
-                if (lane == 0) atomicOr(a.status, 16);
+                atomicOr(a.status, 16);
                 mat = 0;
             }
-            const uint8_t* rowp = L.down + (size_t) mat * L.down_nb2 + (size_t) (h0 + hh) * L.down_nb1;
-            const uint8_t* base = (const uint8_t*) ((uintptr_t) rowp & ~(uintptr_t) 15);
-            dma_row(lds, a.lds_b + (uint32_t) r * a.rs_b, base, (int) ((rowp + rowB - base + 15) / 16), lane);
+            s_rowB[r] = L.down + (size_t) mat * L.down_nb2 + (size_t) (h0 + hh) * L.down_nb1;
         }
+        lds_barrier();
+        // ---- gate/up rows to LDS: every load of a round in flight at once --------
+        for (int base = 0; base < nA; base += MAXJ_A * DEC_THREADS) {
+            u32x4 t[MAXJ_A];
+#pragma unroll
+            for (int j = 0; j < MAXJ_A; ++j) {
+                const int c = base + tid + j * DEC_THREADS;
+                if (c < nA) t[j] = ldg16(s_rowA[c / chA] + 16 * (c % chA));
+            }
+#pragma unroll
+            for (int j = 0; j < MAXJ_A; ++j) {
+                const int c = base + tid + j * DEC_THREADS;
+                if (c < nA) sts16(lds, a.lds_a + (uint32_t) (c / chA) * a.rs_a + 16u * (c % chA), t[j]);
+            }
+        }
+        lds_barrier();
         // ---- A: gate / up rows, SwiGLU ---------------------------------------------
         for (int r0 = 0; r0 < np * 2; r0 += DEC_WAVES * 8) {
             const int r = r0 + wave * 8 + (lane >> 3);
@@ -328,26 +389,47 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
             else v = row_dot_lds<T_Q4_K>(lds, a.lds_a + (uint32_t) rr * a.rs_a, a.lds_xq, nbH, lane & 7);
             if (r < np * 2 && (lane & 7) == 0) res[r] = v;
         }
-        __syncthreads();
+        lds_barrier();
+        // ---- down rows: issued now, held in registers while act is exchanged --------
+        u32x4 tb[MAXJ_B];
+        if (b_fits) {
+#pragma unroll
+            for (int j = 0; j < MAXJ_B; ++j) {
+                const int c = tid + j * DEC_THREADS;
+                const u32x4* src = c < nB ? down_chunk(s_rowB[c / chB], rowB, c % chB) : nullptr;
+                if (src) tb[j] = ldg16(src);
+            }
+        }
         for (int j = tid; j < np; j += DEC_THREADS) {
             const float act = v_silu(res[2 * j]) * res[2 * j + 1];
             st_dev64(a.xa + pa0 + j, tagged(act, ep));
         }
         // ---- B: all act -> Q8_K per slot; down rows; weighted sum ------------------
-        float* actf = (float*) ((uint8_t*) lds + a.lds_act);
-        if (!gather_tagged<12>(a, a.xa, P, ep, actf)) { wait_dma(); return; }
-        quant_q8K_lds(lds, actf, k * nbF, a.lds_aq);
-        wait_dma();
-        __syncthreads();
+        // (act lands where the gate/up rows were: every thread is past the A
+        // barrier, so they are consumed)
+        gather_tagged<12>(a, a.xa, P, ep, actf, &s_fail);
+        if (b_fits) {
+#pragma unroll
+            for (int j = 0; j < MAXJ_B; ++j) {
+                const int c = tid + j * DEC_THREADS;
+                if (c < nB && down_chunk(s_rowB[c / chB], rowB, c % chB))
+                    sts16(lds, a.lds_b + (uint32_t) (c / chB) * a.rs_b + 16u * (c % chB), tb[j]);
+            }
+        } else {
+            for (int c = tid; c < nB; c += DEC_THREADS) {
+                const u32x4* src = down_chunk(s_rowB[c / chB], rowB, c % chB);
+                if (src) sts16(lds, a.lds_b + (uint32_t) (c / chB) * a.rs_b + 16u * (c % chB), ldg16(src));
+            }
+        }
+        lds_barrier();
+        if (s_fail) return;
+        quant_q8K_lds16(lds, actf, k * nbF, a.lds_aq);
+        lds_barrier();
         for (int r0 = 0; r0 < k * nh; r0 += DEC_WAVES * 8) {
             const int r = r0 + wave * 8 + (lane >> 3);
             const int rr = r < k * nh ? r : 0;
-            const int i = rr / nh, hh = rr % nh;
-            const int e = s_ids[i];
-            int64_t mat = L.slot_down ? L.slot_down[e] : e;
-            if (mat < 0 || mat >= L.n_slots_down) mat = 0;
-            const uint8_t* rowp = L.down + (size_t) mat * L.down_nb2 + (size_t) (h0 + hh) * L.down_nb1;
-            const uint32_t wb = a.lds_b + (uint32_t) rr * a.rs_b + (uint32_t) ((uintptr_t) rowp & 15);
+            const int i = rr / nh;
+            const uint32_t wb = a.lds_b + (uint32_t) rr * a.rs_b + (uint32_t) ((uintptr_t) s_rowB[rr] & 15);
             const uint32_t ab = a.lds_aq + (uint32_t) (i * nbF) * 292u;
             float v;
             if constexpr (TYPE_DOWN == T_Q4_K && NBF > 0) {
@@ -358,7 +440,7 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
             }
             if (r < k * nh && (lane & 7) == 0) res[r] = v;
         }
-        __syncthreads();
+        lds_barrier();
         for (int hh = tid; hh < nh; hh += DEC_THREADS) {
             // ggml_vec_dot_f32(k, experts^T row, w): k < 32 -> scalar tail: groups of
             // four as mul + add, the remainder fused
@@ -371,9 +453,9 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
             st_dev64(a.xy + h0 + hh, tagged(sumf, ep));
         }
         // ---- C: all y -> RMSNorm -> x of the next layer ----------------------------
-        float* ys = res;   // reused: every thread must be done with the down results
-        __syncthreads();
-        if (!gather_tagged<4>(a, a.xy, H, ep, ys)) { wait_dma(); return; }
+        gather_tagged<4>(a, a.xy, H, ep, ys, &s_fail);
+        lds_barrier();
+        if (s_fail) return;
         {
             double s = 0.0;
             for (int i = tid; i < H; i += DEC_THREADS) {
@@ -382,7 +464,7 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
             }
             for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
             if (lane == 0) s_red[wave] = s;
-            __syncthreads();
+            lds_barrier();
             double tot = 0.0;
             for (int w = 0; w < DEC_WAVES; ++w) tot += s_red[w];
             const float mean = (float) (tot / (double) H);
@@ -394,7 +476,7 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
                     if (a.x_out) a.x_out[i] = xs[i];
                 }
             }
-            __syncthreads();
+            lds_barrier();
         }
     }
 }
@@ -432,6 +514,7 @@ int launch_decode_stack(const DecodeStackDesc& d, const float* x_in, float* out,
     a.lds_x = d.lds_x;
     a.lds_act = d.lds_act;
     a.lds_res = d.lds_res;
+    a.lds_y = d.lds_y;
     a.lds_total = d.lds_total;
     a.rs_a = d.rs_a;
     a.rs_b = d.rs_b;
@@ -447,14 +530,16 @@ int launch_decode_stack(const DecodeStackDesc& d, const float* x_in, float* out,
 int plan_decode_stack(DecodeStackDesc& d, int grid) {
     if (d.H % 256 || d.F % 256 || d.E % 8 || d.E > 512 || d.k < 1 || d.k > 32 || d.k > d.E) return -2;
     if (d.type_down != T_Q4_K && d.type_down != T_Q6_K) return -2;
+    if (d.H > 2 * 4 * DEC_THREADS) return -2;          // router row held in two uint4 per thread
     d.grid = grid;
     const int P = (int) (d.k * d.F);
     d.pa_per = (P + grid - 1) / grid;
     d.hb_per = (int) (((d.H + grid - 1) / grid + 3) / 4 * 4);
-    if (d.E > grid) return -2;                        // one router row per WG
+    if (d.E > grid) return -2;                         // one router row per WG
+    if (2 * d.pa_per > 96 || d.k * d.hb_per > 256) return -2;   // row address tables
     const uint32_t rowA = (uint32_t) (d.H / 256) * 144u;
     const uint32_t rowB = (uint32_t) (d.F / 256) * (d.type_down == T_Q4_K ? 144u : 210u);
-    d.rs_a = rowA + 32;                               // stride = 8 (mod 32) dwords for 144-byte rows
+    d.rs_a = rowA + 32;                                // stride = 8 (mod 32) dwords for 144-byte rows
     d.rs_b = ((rowB + 15) / 16 + 1) * 16;
     uint32_t off = 0;
     auto take = [&](uint32_t bytes) { const uint32_t o = off; off += (bytes + 15) / 16 * 16; return o; };
@@ -467,9 +552,10 @@ int plan_decode_stack(DecodeStackDesc& d, int grid) {
     // act (fp32, k*F) is gathered after the gate/up rows are consumed: reuse their space if it fits
     const uint32_t act_bytes = (uint32_t) (d.k * d.F) * 4u;
     d.lds_act = act_bytes <= (uint32_t) (2 * d.pa_per) * d.rs_a ? d.lds_a : take(act_bytes);
-    d.lds_res = take((uint32_t) std::max<int64_t>(d.H, std::max<int64_t>(2 * d.pa_per, d.k * d.hb_per)) * 4u);
+    d.lds_res = take((uint32_t) std::max<int64_t>(2 * d.pa_per, d.k * d.hb_per) * 4u);
+    d.lds_y = take((uint32_t) d.H * 4u);
     d.lds_total = off;
-    if (d.lds_total > 160 * 1024 - 8 * 1024) return -2;   // static shared arrays need ~6 KB
+    if (d.lds_total > 160 * 1024 - 12 * 1024) return -2;   // static shared arrays take ~11 KB
     return 0;
 }
 

@@ -123,6 +123,14 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// Returns v unchanged, but hides where it came from: per-thread addresses
+// derived from the result are recomputed where they are used instead of being
+// hoisted out of (and kept live across) an enclosing loop.
+__device__ __forceinline__ int opaque(int v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
 // Unaligned little-endian reads (compiler splits them to what the alignment allows).
 template <typename T>
 __device__ __forceinline__ T ld_unaligned(const void* p) {

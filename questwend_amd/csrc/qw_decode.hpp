@@ -35,7 +35,7 @@ struct DecodeStackDesc {
     int grid = 0;
     int pa_per = 0, hb_per = 0;
     uint32_t lds_rw = 0, lds_a = 0, lds_b = 0, lds_xq = 0, lds_aq = 0, lds_x = 0, lds_act = 0, lds_res = 0,
-             lds_total = 0;
+             lds_y = 0, lds_total = 0;
     uint32_t rs_a = 0, rs_b = 0;
     void* dev_block = nullptr;    // one allocation holding everything above
 };

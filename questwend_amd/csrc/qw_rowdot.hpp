@@ -69,14 +69,15 @@ __device__ __forceinline__ float row_dot_lds<T_Q4_K>(const uint32_t* lds, uint32
 }
 
 // Q4_K x Q8_K for 4-byte aligned weight and activation rows, NB super-blocks
-// known at compile time (fully unrolled: all LDS reads can be issued early).
+// known at compile time (unrolled by 4: the LDS reads of four blocks are issued
+// together, within the register budget of a 512-thread persistent kernel).
 // Same integer lanes and float order as row_dot_lds<T_Q4_K>.
 template <int NB>
 __device__ __forceinline__ float row_dot_q4k_a(const uint32_t* lds, uint32_t wbase, uint32_t abase, int n) {
     float acc = 0.0f, accm = 0.0f;
     const uint32_t* w = lds + (wbase >> 2);
     const uint32_t* y = lds + (abase >> 2);
-#pragma unroll
+#pragma unroll 4
     for (int b = 0; b < NB; ++b) {
         const uint32_t* blk = w + 36 * b;   // 144 bytes
         const uint32_t* yb = y + 73 * b;    // 292 bytes
