@@ -27,6 +27,18 @@ sys.path.insert(0, str(ROOT))
 H, E, K_USED, F, N_LAYER = 2048, 128, 8, 768, 48
 RMS_EPS = 1e-6
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = ROOT / "profiles" / "decode_stack_q4k_30b_pmc.txt"
+
+
+def measured_traffic(path: str):
+    """HBM bytes per decode launch from a committed rocprofv3 counter summary, or None."""
+    try:
+        for line in Path(path).read_text().splitlines():
+            if line.strip().startswith("hbm_bytes_per_launch"):
+                return int(float(line.split("=", 1)[1].split()[0]))
+    except (OSError, ValueError, IndexError):
+        pass
+    return None
 
 
 def algorithmic_bytes_per_token() -> int:
@@ -104,6 +116,22 @@ def cpu_baseline(layers_host, xs, budget_s: float = 15.0):
                       f"scaled to the 48-layer stack"}
 
 
+def copy_probe(mib: int = 1024, reps: int = 4) -> int:
+    """A plain device copy of known size (torch's copy kernel): run under
+    ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE`` it gives the factor between
+    those counters and the bytes a kernel actually moves."""
+    import torch
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes_read": n * 4, "copy_probe_bytes_written": n * 4, "reps": reps}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -111,11 +139,17 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--traffic", default=str(TRAFFIC_FILE),
+                    help="text file whose 'hbm_bytes_per_launch = N' line is the HBM traffic of one decode "
+                         "launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (copy-calibrated)")
+    ap.add_argument("--copy-probe", action="store_true", help="run only the copy-kernel calibration probe")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (see DESIGN.md, sharding)",
-              file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (the sharding plan is "
+              "documented, not built)", file=sys.stderr)
         return 2
+    if args.copy_probe:
+        return copy_probe()
 
     import numpy as np
     import torch
@@ -192,8 +226,8 @@ def main() -> int:
         "hbm_gbs": round(abytes * tok_s / 1e9, 1),
         "hbm_frac": round(abytes * tok_s / 1e9 / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_decode_stack<12> (one token, 48 layers)",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.traffic),
+                     "kernel": "k_decode_stack<8,3,Q4_K> (one launch = one token through 48 layers)",
                      "bytes_per_launch": abytes, "avg_launch_ms": round(kern_ms, 4)},
         "cpu_baseline": cpu,
         "parity_check_vs_per_layer_path": same,

@@ -428,6 +428,7 @@ int qwmoe_decode_stack_create(const qwmoe_layer* layers, int n_layer, float rms_
     d.scale = L0.expert_weights_scale;
     d.rms_eps = rms_eps;
     int rc = qw::plan_decode_stack(d, cus);
+    if (rc == 0) rc = qw::check_decode_residency(d);
     if (rc) {
         delete s;
         return rc;

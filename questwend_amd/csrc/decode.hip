@@ -2,13 +2,14 @@
 // token through every layer of a stack (the work core/runtime.cpp schedules as
 // build_moe per layer inside one graph, decode() -> build_graph, 976-1100).
 //
-// One workgroup per CU, all co-resident (cooperative launch).  Per layer:
+// One workgroup per CU, all co-resident (the LDS footprint admits one per CU).
+// Per layer:
 //   top-k  every WG: softmax + exact top-k from the layer's E logits
 //   A      every WG: Q8_K(x); its slice of the selected experts' gate/up row
 //          pairs (loaded to LDS) -> gate, up, SwiGLU -> act words
 //   B      every WG: all act -> Q8_K per expert; its H/G output rows of all k
-//          experts' down projections (loads issued before A computes, held in
-//          registers while act is exchanged); weighted expert sum -> y words
+//          experts' down projections (loads issued once A has computed, held
+//          in registers while act is exchanged); weighted expert sum -> y words
 //   C      every WG: all y -> RMSNorm -> x of the next layer; WG e computes
 //          router logit e of the next layer from its LDS copy of that row
 // Cross-WG data (act, y, logits) moves through device memory as 64-bit words
@@ -519,12 +520,27 @@ int launch_decode_stack(const DecodeStackDesc& d, const float* x_in, float* out,
     a.rs_a = d.rs_a;
     a.rs_b = d.rs_b;
     void* args[] = {&a};
-    const void* fn;
-    if (d.type_down == T_Q4_K && d.H == 2048 && d.F == 768) fn = (const void*) k_decode_stack<8, 3, T_Q4_K>;
-    else if (d.type_down == T_Q6_K) fn = (const void*) k_decode_stack<0, 0, T_Q6_K>;
-    else fn = (const void*) k_decode_stack<0, 0, T_Q4_K>;
-    hipError_t e = hipLaunchCooperativeKernel(fn, dim3((unsigned) d.grid), dim3(DEC_THREADS), args, d.lds_total, stream);
+    // A plain launch: one WG per CU, and the LDS footprint admits only one per
+    // CU, so on a device this process is not sharing every WG is resident at
+    // once (checked at create time by check_decode_residency).  If some WG is
+    // held back, the others' bounded waits end the launch with status bit 3.
+    hipError_t e = hipLaunchKernel(decode_kernel(d), dim3((unsigned) d.grid), dim3(DEC_THREADS), args, d.lds_total,
+                                   stream);
     return e == hipSuccess ? 0 : -3;
+}
+
+const void* decode_kernel(const DecodeStackDesc& d) {
+    if (d.type_down == T_Q4_K && d.H == 2048 && d.F == 768) return (const void*) k_decode_stack<8, 3, T_Q4_K>;
+    if (d.type_down == T_Q6_K) return (const void*) k_decode_stack<0, 0, T_Q6_K>;
+    return (const void*) k_decode_stack<0, 0, T_Q4_K>;
+}
+
+int check_decode_residency(const DecodeStackDesc& d) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel(d), DEC_THREADS, d.lds_total) !=
+        hipSuccess)
+        return -3;
+    return per_cu >= 1 ? 0 : -2;
 }
 
 int plan_decode_stack(DecodeStackDesc& d, int grid) {

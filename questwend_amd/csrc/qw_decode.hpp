@@ -41,6 +41,9 @@ struct DecodeStackDesc {
 };
 
 int plan_decode_stack(DecodeStackDesc& d, int grid);
+const void* decode_kernel(const DecodeStackDesc& d);
+// 0 if one WG of the planned kernel fits on a CU (grid = CU count => all resident).
+int check_decode_residency(const DecodeStackDesc& d);
 int launch_decode_stack(const DecodeStackDesc& d, const float* x_in, float* out, float* x_out, int32_t* ids_out,
                         float* w_out, uint32_t epoch0, hipStream_t stream);
 
