@@ -92,12 +92,10 @@ __device__ void gather_tagged(const DecodeArgs& a, const uint64_t* src, int n, u
         do {
             ok = true;
 #pragma unroll
-            for (int j = 0; j < MAXJ; ++j) {
-                const int idx = base + tid + j * DEC_THREADS;
-                v[j] = idx < n ? ld_dev64(src + idx) : ((uint64_t) epoch << 32);
-            }
+            for (int j = 0; j < MAXJ; ++j) v[j] = ld_dev64(src + min(base + tid + j * DEC_THREADS, n - 1));
 #pragma unroll
-            for (int j = 0; j < MAXJ; ++j) ok = ok && ((uint32_t) (v[j] >> 32) == epoch);
+            for (int j = 0; j < MAXJ; ++j)
+                ok = ok && (base + tid + j * DEC_THREADS >= n || (uint32_t) (v[j] >> 32) == epoch);
             if (!ok) {
                 if (++spins > DEC_SPIN_LIMIT) { raise_abort(a, 8); break; }
                 if ((spins & 255) == 0 && aborted(a)) break;
@@ -186,11 +184,16 @@ __device__ __forceinline__ void sts16(uint32_t* lds, uint32_t byte_off, u32x4 v)
     *(u32x4*) ((uint8_t*) lds + byte_off) = v;
 }
 
-// 16-byte chunk ch of a down row starting at rowp (any alignment): the chunk of
-// the row's 16-aligned base, or null past the row's end.
-__device__ __forceinline__ const u32x4* down_chunk(const uint8_t* rowp, uint32_t rowB, int ch) {
+// 16-byte chunk ch of a down row starting at rowp (any alignment), counted
+// from the row's 16-aligned base.  Past the row's end it returns the row's last
+// chunk (the load stays where the row is) and sets ok = false.  Loads in this
+// kernel are unconditional with clamped addresses: a load inside a divergent
+// branch makes the compiler wait for it at the join, one load at a time.
+__device__ __forceinline__ const u32x4* down_chunk(const uint8_t* rowp, uint32_t rowB, int ch, bool& ok) {
     const uint8_t* base = (const uint8_t*) ((uintptr_t) rowp & ~(uintptr_t) 15);
-    return (uint32_t) ch * 16u < (uint32_t) (rowp + rowB - base) ? (const u32x4*) base + ch : nullptr;
+    const int last = (int) ((uint32_t) (rowp + rowB - base - 1) / 16u);
+    ok = ch <= last;
+    return (const u32x4*) base + (ok ? ch : last);
 }
 
 template <int NBH, int NBF, int TYPE_DOWN>
@@ -260,12 +263,14 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
         quant_q8K_lds16(lds, xs, nbH, a.lds_xq);
         // the next layer's router row: loaded now, written to LDS after the logit wait
         const bool rw_next = b < E && l + 1 < a.n_layer;
-        const float* rw_src = rw_next ? a.layers[l + 1].router + (size_t) b * H : nullptr;
+        // (loads are unconditional, from clamped addresses -- a WG without a next
+        // row reads x_in, an L2 hit -- so that none of them waits for another)
+        const float* rw_src = rw_next ? a.layers[l + 1].router + (size_t) b * H : a.x_in;
         const uint32_t rw_dst = a.lds_rw + (uint32_t) ((l + 1) & 1) * (uint32_t) H * 4u;
         const bool rw0 = rw_next && tid < H / 4, rw1 = rw_next && tid + DEC_THREADS < H / 4;
-        u32x4 rwv0, rwv1;
-        if (rw0) rwv0 = ldg16(rw_src + 4 * tid);
-        if (rw1) rwv1 = ldg16(rw_src + 4 * (tid + DEC_THREADS));
+        const u32x4 rwv0 = ldg16(rw_src + 4 * min(tid, H / 4 - 1));
+        u32x4 rwv1 = rwv0;
+        if (H / 4 > DEC_THREADS) rwv1 = ldg16(rw_src + 4 * min(tid + DEC_THREADS, H / 4 - 1));
         // ---- softmax and exact top-k (every WG) ----------------------------------
         gather_tagged<1>(a, a.xl, E, ep, s_p, &s_fail);
         if (rw0) sts16(lds, rw_dst + 16u * tid, rwv0);
@@ -371,8 +376,8 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
             u32x4 t[MAXJ_A];
 #pragma unroll
             for (int j = 0; j < MAXJ_A; ++j) {
-                const int c = base + tid + j * DEC_THREADS;
-                if (c < nA) t[j] = ldg16(s_rowA[c / chA] + 16 * (c % chA));
+                const int c = min(base + tid + j * DEC_THREADS, nA - 1);
+                t[j] = ldg16(s_rowA[c / chA] + 16 * (c % chA));
             }
 #pragma unroll
             for (int j = 0; j < MAXJ_A; ++j) {
@@ -391,19 +396,22 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
             if (r < np * 2 && (lane & 7) == 0) res[r] = v;
         }
         lds_barrier();
-        // ---- down rows: issued now, held in registers while act is exchanged --------
-        u32x4 tb[MAXJ_B];
-        if (b_fits) {
-#pragma unroll
-            for (int j = 0; j < MAXJ_B; ++j) {
-                const int c = tid + j * DEC_THREADS;
-                const u32x4* src = c < nB ? down_chunk(s_rowB[c / chB], rowB, c % chB) : nullptr;
-                if (src) tb[j] = ldg16(src);
-            }
-        }
-        for (int j = tid; j < np; j += DEC_THREADS) {
+        if (tid < np) {   // np <= 48 (plan)
+            const int j = tid;
             const float act = v_silu(res[2 * j]) * res[2 * j + 1];
             st_dev64(a.xa + pa0 + j, tagged(act, ep));
+        }
+        // ---- down rows: issued now, held in registers while act is exchanged --------
+        // (after the act stores: issued before them, the compiler waits for these
+        // loads inside the SwiGLU block)
+        u32x4 tb[MAXJ_B];
+        if (b_fits && nB > 0) {
+#pragma unroll
+            for (int j = 0; j < MAXJ_B; ++j) {
+                const int c = min(tid + j * DEC_THREADS, nB - 1);
+                bool ok;
+                tb[j] = ldg16(down_chunk(s_rowB[c / chB], rowB, c % chB, ok));
+            }
         }
         // ---- B: all act -> Q8_K per slot; down rows; weighted sum ------------------
         // (act lands where the gate/up rows were: every thread is past the A
@@ -413,13 +421,15 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
 #pragma unroll
             for (int j = 0; j < MAXJ_B; ++j) {
                 const int c = tid + j * DEC_THREADS;
-                if (c < nB && down_chunk(s_rowB[c / chB], rowB, c % chB))
-                    sts16(lds, a.lds_b + (uint32_t) (c / chB) * a.rs_b + 16u * (c % chB), tb[j]);
+                bool ok = false;
+                if (c < nB) down_chunk(s_rowB[c / chB], rowB, c % chB, ok);
+                if (ok) sts16(lds, a.lds_b + (uint32_t) (c / chB) * a.rs_b + 16u * (c % chB), tb[j]);
             }
         } else {
             for (int c = tid; c < nB; c += DEC_THREADS) {
-                const u32x4* src = down_chunk(s_rowB[c / chB], rowB, c % chB);
-                if (src) sts16(lds, a.lds_b + (uint32_t) (c / chB) * a.rs_b + 16u * (c % chB), ldg16(src));
+                bool ok;
+                const u32x4 v = ldg16(down_chunk(s_rowB[c / chB], rowB, c % chB, ok));
+                if (ok) sts16(lds, a.lds_b + (uint32_t) (c / chB) * a.rs_b + 16u * (c % chB), v);
             }
         }
         lds_barrier();
@@ -442,7 +452,8 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
             if (r < k * nh && (lane & 7) == 0) res[r] = v;
         }
         lds_barrier();
-        for (int hh = tid; hh < nh; hh += DEC_THREADS) {
+        if (tid < nh) {   // nh <= 256 (plan)
+            const int hh = tid;
             // ggml_vec_dot_f32(k, experts^T row, w): k < 32 -> scalar tail: groups of
             // four as mul + add, the remainder fused
             float sumf = 0.0f;
