@@ -24,6 +24,7 @@ struct Library {
     size_t ws_bytes = 0;
     size_t high_water = 0;
     int32_t* status = nullptr;   // device status word (first 256 bytes of the arena)
+    int mfma_min_rows = 32;      // experts with this many routed rows use the matrix-core kernel (0: never)
 };
 
 Library g_lib;
@@ -64,7 +65,7 @@ int check_k(int type, int64_t K) {
 int mmid_grouped(hipStream_t st, int type, const void* as, int64_t K, int64_t N, int64_t n_as, size_t nb01,
                  size_t nb02, const uint8_t* bq, int64_t ne11, size_t bq_row, const int32_t* rows,
                  const int32_t* active, const int32_t* active_off, const int32_t* n_active, int64_t max_active,
-                 const int32_t* slot_of, int64_t n_slot_of, float* dst, size_t nb1, size_t nb2) {
+                 const int32_t* slot_of, int64_t n_slot_of, float* dst, size_t nb1, size_t nb2, int64_t max_rows) {
     qw::MmidArgs m{};
     m.type = type;
     m.w = (const uint8_t*) as;
@@ -87,7 +88,15 @@ int mmid_grouped(hipStream_t st, int type, const void* as, int64_t K, int64_t N,
     m.dst_nb2 = nb2;
     m.status = g_lib.status;
     m.max_active = max_active;
-    return qw::launch_mmid_gemv(m, st);
+    // experts with at least mfma_min_rows routed rows (possible only when the
+    // batch holds that many pairs) go to the int8 matrix-core kernel; the rest
+    // stay on the bit-exact GEMV
+    m.mfma_min_rows = 0;
+    const bool mfma = g_lib.mfma_min_rows > 0 && max_rows >= g_lib.mfma_min_rows && qw::mmid_mfma_supported(m);
+    if (mfma) m.mfma_min_rows = g_lib.mfma_min_rows;
+    int rc = qw::launch_mmid_gemv(m, st);
+    if (rc == 0 && mfma) rc = qw::launch_mmid_mfma(m, st);
+    return rc;
 }
 
 struct Grouping {
@@ -169,6 +178,15 @@ const char* qwmoe_strerror(int status) {
     }
     return "unknown status";
 }
+
+int qwmoe_set_mfma_min_rows(int rows) {
+    if (rows < 0) return QWMOE_ERR_INVALID_ARG;
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_lib.mfma_min_rows = rows;
+    return QWMOE_OK;
+}
+
+int qwmoe_get_mfma_min_rows(void) { return g_lib.mfma_min_rows; }
 
 size_t qwmoe_workspace_high_water(void) { return g_lib.high_water; }
 
@@ -259,7 +277,7 @@ int qwmoe_mul_mat_id(void* stream, int type, const void* as, int64_t ne00, int64
     rc = group(st, ar, ids, n_ids, ne12, ids_nb1, n_bins, nullptr, nullptr, nullptr, G);
     if (rc) return rc;
     return mmid_grouped(st, type, as, ne00, ne01, ne02, nb01, nb02, bq, ne11, qrow, G.rows, G.active, G.active_off,
-                        G.n_active, G.max_active, slot_of, n_slot_of, dst, nb1, nb2);
+                        G.n_active, G.max_active, slot_of, n_slot_of, dst, nb1, nb2, n_ids * ne12);
 }
 
 int qwmoe_router_topk(void* stream, const float* W, const float* x, int64_t H, int64_t E, int64_t k, int64_t T,
@@ -359,11 +377,11 @@ int qwmoe_ffn_layer(void* stream, const qwmoe_layer* L, const float* x, int64_t 
     const size_t dnb1 = (size_t) F * 4, dnb2 = (size_t) F * 4 * (size_t) k;
     if ((rc = mmid_grouped(st, L->type_up, L->up, H, F, L->n_slots_up, L->up_nb1, L->up_nb2, xu, 1, qu, G.rows,
                            G.active, G.active_off, G.n_active, G.max_active, L->slot_up, L->slot_up ? E : 0, upo,
-                           dnb1, dnb2)))
+                           dnb1, dnb2, T)))
         return rc;
     if ((rc = mmid_grouped(st, L->type_gate, L->gate, H, F, L->n_slots_gate, L->gate_nb1, L->gate_nb2, xg, 1, qg,
                            G.rows, G.active, G.active_off, G.n_active, G.max_active, L->slot_gate,
-                           L->slot_gate ? E : 0, gateo, dnb1, dnb2)))
+                           L->slot_gate ? E : 0, gateo, dnb1, dnb2, T)))
         return rc;
     if ((rc = qw::launch_swiglu(gateo, upo, act, k * T, F, (size_t) F * 4, (size_t) F * 4, (size_t) F * 4, st)))
         return rc;
@@ -375,7 +393,7 @@ int qwmoe_ffn_layer(void* stream, const qwmoe_layer* L, const float* x, int64_t 
         return rc;
     if ((rc = mmid_grouped(st, L->type_down, L->down, F, H, L->n_slots_down, L->down_nb1, L->down_nb2, aq, k, qd,
                            G.rows, G.active, G.active_off, G.n_active, G.max_active, L->slot_down,
-                           L->slot_down ? E : 0, ex, (size_t) H * 4, (size_t) H * 4 * (size_t) k)))
+                           L->slot_down ? E : 0, ex, (size_t) H * 4, (size_t) H * 4 * (size_t) k, T)))
         return rc;
     if ((rc = qw::launch_weighted_sum(ex, w, out, H, k, T, st))) return rc;
     if (rms_eps >= 0.0f && (rc = qw::launch_rms_norm(out, x_next, H, T, rms_eps, st))) return rc;

@@ -160,6 +160,7 @@ __global__ void __launch_bounds__(256) k_mmid_gemv(MmidArgs m) {
     extern __shared__ uint32_t lds[];
     const int g = blockIdx.y;
     if (g >= *m.n_active) return;
+    if (m.mfma_min_rows > 0 && m.active_off[g + 1] - m.active_off[g] >= m.mfma_min_rows) return;   // matrix cores take it
     const int bin = m.active[g];
     int64_t mat = bin;
     if (m.slot_of) mat = (bin < m.n_slot_of) ? m.slot_of[bin] : -1;
@@ -230,7 +231,5 @@ int launch_mmid_gemv(const MmidArgs& m, hipStream_t stream) {
     }
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
-
-int launch_mmid_mfma(const MmidArgs& m, hipStream_t stream) { return launch_mmid_gemv(m, stream); }
 
 }  // namespace qw

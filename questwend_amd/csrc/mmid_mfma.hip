@@ -1,0 +1,204 @@
+// mmid_mfma.hip -- ggml_mul_mat_id for experts with many routed rows (prefill,
+// large verify batches): the Q4_K x Q8_K block products as int8 matrix-core
+// (MFMA) contractions over staged super-block tiles, bit-identical to ggml.
+//
+// Reference: ggml_vec_dot_q4_K_q8_K, AVX2 branch (ggml/src/ggml-cpu/arch/x86/
+// quants.c:2038-2115).  Per (weight row, activation row, super-block) it keeps
+// eight int32 lanes, lane L holding
+//     sumi_L = sum_{j=0..7} sc_j * sum_{e=0..3} q4[32 j + 4 L + e] * q8[32 j + 4 L + e]
+// (maddubs pairs, madd with the sub-block scale), four min lanes
+//     prod_m = mins[2m] * q8s[2m] + mins[2m+1] * q8s[2m+1],  q8s[j] = sum of q8 over sub-block j
+// and then, over the super-blocks i in order, acc_L = fma(d_i, sumi_L, acc_L),
+// accm_m = fma(dmin_i, prod_m, accm_m) with d = y.d * fp16(x.d),
+// dmin = -y.d * fp16(x.dmin); the result is hsum_float_8(acc) + ((m0+m2)+(m1+m3)).
+// This kernel computes exactly those integers on the matrix cores and replays
+// the float steps lane for lane, so its outputs equal ggml's bit for bit.
+//
+// Matrix-core mapping.  v_mfma_i32_16x16x32_i8 (D = A x B + C, 16 x 16 x 32):
+// A lane l holds weight row l % 16 and k-slots 8 (l/16) .. +8; B lane l holds
+// activation row l % 16 and the same k-slots; D lane l, register r is row
+// 4 (l/16) + r, activation row l % 16.  For AVX lane L the 32 k-slots are the
+// 32 positions of that lane: slot 8 g + 4 h + e is sub-block j = 2 g + h,
+// element 4 L + e, i.e. nibble h of qs byte 32 g + 4 L + e -- one qs dword per
+// MFMA lane gives both of its sub-blocks.  The scale goes into A: with
+// sc = 8 sc_hi + sc_lo (sc_hi, sc_lo <= 7), A_lo = sc_lo * q4 and
+// A_hi = sc_hi * q4 fit int8 and the byte-wise products never carry, and
+// sumi_L = 8 (A_hi . q8) + (A_lo . q8).  The min lanes use
+// v_mfma_i32_16x16x64_i8 over the 64 positions of sub-blocks 2m and 2m+1 with
+// every A byte equal to that sub-block's min.  20 MFMAs per 16 x 16 tile and
+// super-block.
+#include "qw_kernels.hpp"
+
+namespace qw {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4m __attribute__((ext_vector_type(4)));
+
+constexpr int MF_M = 64;          // weight rows per workgroup (4 waves x 16)
+constexpr int MF_TILES = 2;       // 16-row activation tiles per wave and pass
+constexpr int MF_N = 16 * MF_TILES;
+constexpr uint32_t MF_WS = 144;   // LDS stride of a staged Q4_K block (9 x 16 B)
+constexpr uint32_t MF_AS = 272;   // LDS stride of a staged Q8_K block: d at 0, qs at 16 (16-aligned)
+
+__device__ __forceinline__ long pack2(uint32_t lo, uint32_t hi) { return (long) (((uint64_t) hi << 32) | lo); }
+
+__global__ void __launch_bounds__(256) k_mmid_mfma_q4k(MmidArgs m) {
+    __shared__ __align__(16) uint8_t s_w[MF_M * MF_WS];
+    __shared__ __align__(16) uint8_t s_a[MF_N * MF_AS];
+    __shared__ int32_t s_et[MF_N][2];
+    const int g = blockIdx.y;
+    if (g >= *m.n_active) return;
+    const int p0 = m.active_off[g], p1 = m.active_off[g + 1];
+    if (p1 - p0 < m.mfma_min_rows) return;   // light expert: the GEMV kernel's
+    const int bin = m.active[g];
+    int64_t mat = bin;
+    if (m.slot_of) mat = (bin < m.n_slot_of) ? m.slot_of[bin] : -1;
+    if (mat < 0 || mat >= m.n_as) {
+        if (threadIdx.x == 0 && m.status) atomicOr(m.status, 4);
+        return;
+    }
+    const int64_t r0 = (int64_t) blockIdx.x * MF_M;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int lr = lane & 15, gq = lane >> 4;   // A row / B row within a tile; k-slot group
+    const int nb = (int) (m.K / QK_K);
+    const uint8_t* wtile = m.w + (size_t) mat * m.nb2 + (size_t) r0 * m.nb1;
+    const int arow_l = 16 * wave + lr;          // this lane's A row in the staged tile
+
+    for (int pc = p0; pc < p1; pc += MF_N) {
+        const int ntok = (p1 - pc) < MF_N ? (p1 - pc) : MF_N;
+        lds_barrier();   // the previous pass is done with s_et / s_a
+        if (tid < MF_N) {
+            const int pp = pc + (tid < ntok ? tid : 0);
+            s_et[tid][0] = m.rows[2 * pp];
+            s_et[tid][1] = m.rows[2 * pp + 1];
+        }
+        // per output (tile t, D register r): the eight AVX lanes and four min lanes
+        float acc[MF_TILES][4][8], accm[MF_TILES][4][4];
+#pragma unroll
+        for (int t = 0; t < MF_TILES; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+#pragma unroll
+                for (int L = 0; L < 8; ++L) acc[t][r][L] = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) accm[t][r][q] = 0.0f;
+            }
+        lds_barrier();
+        for (int i = 0; i < nb; ++i) {
+            // stage super-block i: 64 weight rows (16-byte chunks) and the pass's
+            // activation blocks (d and the 256 quants, as dwords: rows are 4-aligned)
+            for (int z = tid; z < MF_M * 9; z += 256) {
+                const int r = z / 9, c = z - r * 9;
+                const u32x4m v = *(const __attribute__((address_space(1))) u32x4m*) (wtile + (size_t) r * m.nb1 +
+                                                                                   (size_t) i * 144 + 16 * c);
+                *(u32x4m*) (s_w + r * MF_WS + 16 * c) = v;
+            }
+            for (int z = tid; z < ntok * 65; z += 256) {
+                const int n = z / 65, c = z - n * 65;
+                const int e = s_et[n][0], t = s_et[n][1];
+                const int64_t arow = (int64_t) (e % m.b_ne1) + (int64_t) t * m.b_ne1;
+                const uint32_t* src = (const uint32_t*) (m.act_q + (size_t) arow * m.act_row_bytes + (size_t) i * 292);
+                *(uint32_t*) (s_a + n * MF_AS + (c == 0 ? 0 : 12 + 4 * c)) = src[c];
+            }
+            lds_barrier();
+            // this lane's A row: the 6-bit scales and mins of the 8 sub-blocks
+            // (the utmp shuffle of quants.c:2067-2072), as bytes
+            const u32x4m hdr = *(const u32x4m*) (s_w + arow_l * MF_WS);
+            const uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;
+            const uint32_t sc_lo = s0 & 0x3f3f3f3fu;
+            const uint32_t sc_hi = (s2 & 0x0f0f0f0fu) | (((s0 >> 6) & 0x03030303u) << 4);
+            const uint32_t mn_lo = s1 & 0x3f3f3f3fu;
+            const uint32_t mn_hi = ((s2 >> 4) & 0x0f0f0f0fu) | (((s1 >> 6) & 0x03030303u) << 4);
+            // sub-blocks 2 gq (low nibbles) and 2 gq + 1 (high nibbles) of this lane's k-slots
+            const uint32_t scw = gq < 2 ? sc_lo : sc_hi;
+            const uint32_t sa = (scw >> (16 * (gq & 1))) & 0xffu, sb = (scw >> (16 * (gq & 1) + 8)) & 0xffu;
+            // block scales of the D rows 4 gq + r and the B rows of each tile
+            float dx[4], dmx[4], dy[MF_TILES];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t h0 = *(const uint32_t*) (s_w + (16 * wave + 4 * gq + r) * MF_WS);
+                dx[r] = h2f((uint16_t) (h0 & 0xffff));
+                dmx[r] = h2f((uint16_t) (h0 >> 16));
+            }
+#pragma unroll
+            for (int t = 0; t < MF_TILES; ++t) dy[t] = *(const float*) (s_a + (16 * t + lr) * MF_AS);
+            // AVX lanes
+#pragma unroll
+            for (int L = 0; L < 8; ++L) {
+                const uint32_t w = *(const uint32_t*) (s_w + arow_l * MF_WS + 16 + 32 * gq + 4 * L);
+                const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+                const long a_lo = pack2(lo * (sa & 7u), hi * (sb & 7u));
+                const long a_hi = pack2(lo * (sa >> 3), hi * (sb >> 3));
+#pragma unroll
+                for (int t = 0; t < MF_TILES; ++t) {
+                    const uint8_t* ab = s_a + (16 * t + lr) * MF_AS + 16 + 64 * gq + 4 * L;
+                    const long bq = pack2(*(const uint32_t*) ab, *(const uint32_t*) (ab + 32));
+                    const v4i z4 = v4i{0, 0, 0, 0};
+                    const v4i dlo = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_lo, bq, z4, 0, 0, 0);
+                    const v4i dhi = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_hi, bq, z4, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float d = dy[t] * dx[r];
+                        acc[t][r][L] = __builtin_fmaf(d, (float) (8 * dhi[r] + dlo[r]), acc[t][r][L]);
+                    }
+                }
+            }
+            // min lanes: sub-blocks 2q (k-slots of lane groups 0, 1) and 2q + 1 (groups 2, 3)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int sbk = 2 * q + (gq >> 1);
+                const uint32_t mnw = sbk < 4 ? mn_lo : mn_hi;
+                const int mb = (int) (((mnw >> (8 * (sbk & 3))) & 0xffu) * 0x01010101u);
+                const v4i a_mn = v4i{mb, mb, mb, mb};
+#pragma unroll
+                for (int t = 0; t < MF_TILES; ++t) {
+                    const v4i bq = *(const v4i*) (s_a + (16 * t + lr) * MF_AS + 16 + 64 * q + 16 * gq);
+                    const v4i dm = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_mn, bq, v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float dmin = -dy[t] * dmx[r];
+                        accm[t][r][q] = __builtin_fmaf(dmin, (float) dm[r], accm[t][r][q]);
+                    }
+                }
+            }
+            lds_barrier();   // staged tiles consumed
+        }
+        // hsum_float_8(acc) + ((m0 + m2) + (m1 + m3)); rows r0 + 16 wave + 4 gq .. +3
+#pragma unroll
+        for (int t = 0; t < MF_TILES; ++t) {
+            const int n = 16 * t + lr;
+            float o[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float* a = acc[t][r];
+                const float hs = ((a[4] + a[0]) + (a[6] + a[2])) + ((a[5] + a[1]) + (a[7] + a[3]));
+                const float* mm = accm[t][r];
+                o[r] = hs + ((mm[0] + mm[2]) + (mm[1] + mm[3]));
+            }
+            if (n < ntok) {
+                const int e = s_et[n][0], tt = s_et[n][1];
+                float* d = (float*) ((char*) m.dst + (size_t) e * m.dst_nb1 + (size_t) tt * m.dst_nb2) + r0 +
+                           16 * wave + 4 * gq;
+                *(float4*) d = float4{o[0], o[1], o[2], o[3]};
+            }
+        }
+    }
+}
+
+// Whether the matrix-core kernel can take (type, shape, strides): Q4_K rows of
+// 16-byte aligned super-blocks, 64-row tiles, 16-byte aligned output rows.
+bool mmid_mfma_supported(const MmidArgs& m) {
+    return m.type == T_Q4_K && m.N % MF_M == 0 && m.K % QK_K == 0 && m.nb1 % 16 == 0 && m.nb2 % 16 == 0 &&
+           ((uintptr_t) m.w & 15) == 0 && m.dst_nb1 % 16 == 0 && m.dst_nb2 % 16 == 0 && ((uintptr_t) m.dst & 15) == 0 &&
+           m.act_row_bytes % 4 == 0 && ((uintptr_t) m.act_q & 3) == 0;
+}
+
+int launch_mmid_mfma(const MmidArgs& m, hipStream_t stream) {
+    if (!mmid_mfma_supported(m)) return -2;
+    dim3 grid((unsigned) (m.N / MF_M), (unsigned) m.max_active);
+    if (grid.y == 0) return 0;
+    hipLaunchKernelGGL(k_mmid_mfma_q4k, grid, dim3(256), 0, stream, m);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+}  // namespace qw

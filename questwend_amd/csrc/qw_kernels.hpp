@@ -65,8 +65,11 @@ struct MmidArgs {
     size_t dst_nb1, dst_nb2;
     int32_t* status;          // bit 2 set on an out-of-range slot
     int64_t max_active;       // grid bound on active bins
+    int mfma_min_rows;        // bins with at least this many rows go to the matrix-core kernel (0: none do)
 };
 int launch_mmid_gemv(const MmidArgs& m, hipStream_t stream);
+// mmid_mfma.hip
+bool mmid_mfma_supported(const MmidArgs& m);
 int launch_mmid_mfma(const MmidArgs& m, hipStream_t stream);
 
 // ffn.hip

@@ -28,6 +28,14 @@ def shutdown() -> None:
     check(lib().qwmoe_shutdown(), "qwmoe_shutdown")
 
 
+def set_mfma_min_rows(rows: int) -> int:
+    """Experts with at least ``rows`` routed rows use the int8 matrix-core
+    kernel (0: never; every output bit-exact).  Returns the previous value."""
+    prev = lib().qwmoe_get_mfma_min_rows()
+    check(lib().qwmoe_set_mfma_min_rows(rows), "set_mfma_min_rows")
+    return prev
+
+
 def device_status(clear: bool = True) -> int:
     v = C.c_int32(0)
     check(lib().qwmoe_device_status(stream(), C.byref(v), int(clear)), "qwmoe_device_status")

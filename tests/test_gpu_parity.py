@@ -36,8 +36,10 @@ def lib_init():
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     ops.init(0, 512 << 20)
+    prev = ops.set_mfma_min_rows(0)   # every expert on the bit-exact GEMV (the matrix cores: test_gpu_prefill.py)
     yield
     torch.cuda.synchronize()
+    ops.set_mfma_min_rows(prev)
 
 
 @pytest.fixture(scope="module")

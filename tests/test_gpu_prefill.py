@@ -1,0 +1,222 @@
+"""GPU parity of the grouped prefill path: mul_mat_id over many routed rows.
+
+Experts with at least ``mfma_min_rows`` routed rows go to the int8 matrix-core
+kernel (v_mfma_i32_16x16x64_i8), lighter ones to the bit-exact GEMV.  The bar:
+router ids and the per-expert grouping exact (test_gpu_parity.py covers them at
+T up to 1024), the integer block sums exact, and fp32 outputs within 1e-3 of
+the CPU reference, measured as max|gpu - cpu| / max(max|cpu|, 1e-30).
+
+The matrix-core path computes ggml's eight AVX2 lane sums and four min lanes
+per super-block exactly and replays the float steps in ggml's order, so its
+outputs are bit-identical to the reference as well.  Its integer core is also
+pinned on its own with inputs for which every fp32 operation is exact (block
+scales d = dmin = 1, activations that quantize to themselves with d = -1, sums
+below 2^24).
+"""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+from questwend_amd import ops  # noqa: E402
+from oracle_lib import Q4_K, LayerWeights, Oracle, RefGGML, have_ref, row_size  # noqa: E402
+
+DEV = "cuda:0"
+TOL = 1e-3
+
+
+def note(msg: str) -> None:
+    print(f"[gpu-prefill] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def lib_init():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    ops.init(0, 512 << 20)
+    prev = ops.set_mfma_min_rows(32)
+    yield
+    torch.cuda.synchronize()
+    ops.set_mfma_min_rows(prev)
+
+
+@pytest.fixture(scope="module")
+def orc():
+    return Oracle()
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def bits(a):
+    return np.asarray(a, np.float32).view(np.uint32)
+
+
+def rel_err(got, want) -> float:
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    return float(np.max(np.abs(got - want)) / max(np.max(np.abs(want)), 1e-30))
+
+
+def encode_q4k_scales(sc: np.ndarray, mn: np.ndarray) -> np.ndarray:
+    """The 12 scale bytes of a Q4_K block from 8 six-bit scales and mins: the
+    inverse of get_scale_min_k4 (ggml-quants.c:880-887)."""
+    out = np.zeros(sc.shape[:-1] + (12,), np.uint8)
+    for j in range(4):
+        out[..., j] = (sc[..., j] & 63) | ((sc[..., j + 4] >> 4) << 6)
+        out[..., j + 4] = (mn[..., j] & 63) | ((mn[..., j + 4] >> 4) << 6)
+        out[..., j + 8] = (sc[..., j + 4] & 15) | ((mn[..., j + 4] & 15) << 4)
+    return out
+
+
+def exact_q4k(rng, rows: int, K: int, max_scale: int) -> np.ndarray:
+    """Q4_K rows with d = dmin = 1.0 and small scales: dequantized weights are
+    small integers, so every fp32 operation of the block dot is exact."""
+    nb = K // 256
+    blk = np.zeros((rows, nb, 144), np.uint8)
+    blk[..., 0:4] = np.array([0x00, 0x3C, 0x00, 0x3C], np.uint8)   # fp16 1.0, 1.0
+    sc = rng.integers(0, max_scale + 1, (rows, nb, 8)).astype(np.uint8)
+    mn = rng.integers(0, 64, (rows, nb, 8)).astype(np.uint8)
+    blk[..., 4:16] = encode_q4k_scales(sc, mn)
+    blk[..., 16:] = rng.integers(0, 256, (rows, nb, 128)).astype(np.uint8)
+    return blk.reshape(-1)
+
+
+def exact_acts(rng, shape, K: int) -> np.ndarray:
+    """f32 activations that Q8_K quantizes to themselves (negated, d = -1): small
+    integers with one 127 per 256-block as the unique largest magnitude."""
+    x = rng.integers(-31, 32, shape + (K,)).astype(np.float32)
+    x[..., ::256] = 127.0
+    return x
+
+
+def zipf_ids(rng, T: int, k: int, n_as: int, s: float = 1.1) -> np.ndarray:
+    p = np.arange(1, n_as + 1, dtype=np.float64) ** -s
+    p /= p.sum()
+    return np.stack([rng.choice(n_as, k, replace=False, p=p) for _ in range(T)]).astype(np.int32)
+
+
+def test_exact_inputs_pin_the_crafted_blocks(orc):
+    """The crafted blocks dequantize to d*sc*q - dmin*m with d = dmin = 1 (the
+    oracle's dequantizer, itself pinned against ggml), i.e. small integers."""
+    rng = np.random.default_rng(0)
+    w = exact_q4k(rng, 4, 512, max_scale=7)
+    deq = orc.dequantize(Q4_K, w, 4 * 512)
+    assert np.all(deq == np.round(deq)) and np.max(np.abs(deq)) <= 7 * 15 + 63
+
+
+@pytest.mark.parametrize("K,N,ne11,min_rows", [(2048, 128, 1, 16), (768, 256, 2, 1), (4096, 64, 1, 8)])
+def test_mfma_integer_core_bit_exact(orc, K, N, ne11, min_rows):
+    note(f"matrix-core mul_mat_id, exact inputs: K={K} N={N} ne11={ne11} min_rows={min_rows}")
+    rng = np.random.default_rng(K + N)
+    n_as, T, n_ids = 5, 70, 2
+    w = exact_q4k(rng, n_as * N, K, max_scale=7)
+    b = exact_acts(rng, (T, ne11), K)
+    ids = np.stack([[0, 1 + (t % 4)] for t in range(T)]).astype(np.int32)   # expert 0 takes all 70 tokens
+    want = orc.mul_mat_id(Q4_K, K, N, n_as, w, b, ids)
+    prev = ops.set_mfma_min_rows(min_rows)
+    try:
+        got = host(ops.mul_mat_id(Q4_K, dev(w), K, N, n_as, dev(b), dev(ids)))
+    finally:
+        ops.set_mfma_min_rows(prev)
+    assert np.array_equal(bits(got), bits(want))
+    assert ops.device_status(clear=True) == 0
+
+
+@pytest.mark.parametrize("K,N,T,k,n_as,ne11", [(2048, 768, 256, 8, 32, 1), (768, 2048, 128, 8, 16, 8),
+                                              (2048, 512, 97, 4, 8, 1)])
+def test_mfma_random_bit_exact(orc, K, N, T, k, n_as, ne11):
+    note(f"matrix-core mul_mat_id, random data: K={K} N={N} T={T} k={k} n_as={n_as} ne11={ne11}")
+    rng = np.random.default_rng(T + N)
+    w = orc.quantize(Q4_K, (rng.standard_normal((n_as * N, K)) * 0.02).astype(np.float32))
+    b = rng.standard_normal((T, ne11, K)).astype(np.float32)
+    ids = zipf_ids(rng, T, k, n_as)
+    want = orc.mul_mat_id(Q4_K, K, N, n_as, w, b, ids)
+    counts = np.bincount(ids.reshape(-1), minlength=n_as)
+    assert counts.max() >= 32, "the case must route some expert to the matrix cores"
+    got = host(ops.mul_mat_id(Q4_K, dev(w), K, N, n_as, dev(b), dev(ids)))
+    note(f"  heavy experts {int((counts >= 32).sum())}/{n_as}, max rows {counts.max()}, "
+         f"rel err {rel_err(got, want):.3e}")
+    assert np.array_equal(bits(got), bits(want))
+    assert ops.device_status(clear=True) == 0
+
+
+def test_mfma_disabled_is_bit_exact(orc):
+    note("mul_mat_id with the matrix cores disabled: every expert on the GEMV, bit-exact")
+    rng = np.random.default_rng(11)
+    K, N, T, k, n_as = 2048, 256, 96, 4, 8
+    w = orc.quantize(Q4_K, (rng.standard_normal((n_as * N, K)) * 0.02).astype(np.float32))
+    b = rng.standard_normal((T, 1, K)).astype(np.float32)
+    ids = zipf_ids(rng, T, k, n_as)
+    prev = ops.set_mfma_min_rows(0)
+    try:
+        got = host(ops.mul_mat_id(Q4_K, dev(w), K, N, n_as, dev(b), dev(ids)))
+    finally:
+        ops.set_mfma_min_rows(prev)
+    assert np.array_equal(bits(got), bits(orc.mul_mat_id(Q4_K, K, N, n_as, w, b, ids)))
+
+
+class GpuLayerQ4K:
+    """A Q4_K layer generated and quantized on the GPU, with a host copy for the
+    CPU reference.  Router rows scaled by a Zipf profile skew expert popularity."""
+
+    def __init__(self, H, E, k, F, seed, zipf_skew=1.1):
+        from oracle_lib import zipf_row_scales
+        self.router = torch.empty((E, H), dtype=torch.float32, device=DEV)
+        ops.randn_(self.router, seed * 10 + 1, 0.0, 0.02)
+        self.router *= dev(zipf_row_scales(E, zipf_skew))[:, None]
+        mats = []
+        tmp = torch.empty(E * F * H, dtype=torch.float32, device=DEV)
+        for j, (rows, cols) in enumerate(((F, H), (F, H), (H, F))):
+            ops.randn_(tmp, seed * 10 + 2 + j, 0.0, 0.02)
+            mats.append(ops.quantize_chunk(Q4_K, tmp.view(E * rows, cols)).view(E, -1))
+        del tmp
+        self.gate, self.up, self.down = mats
+        self.layer = ops.make_layer(H, E, k, F, self.router, self.gate, self.up, self.down, (Q4_K,) * 3)
+        torch.cuda.synchronize()
+        lw = LayerWeights.__new__(LayerWeights)
+        lw.H, lw.E, lw.k, lw.F = H, E, k, F
+        lw.type_gate = lw.type_up = lw.type_down = Q4_K
+        lw.router = self.router.cpu().numpy()
+        lw.gate, lw.up, lw.down = (m.cpu().numpy().reshape(-1) for m in mats)
+        lw.n_slots, lw.slot_of = E, None
+        self.host = lw
+
+
+@pytest.mark.parametrize("T", [512])
+def test_prefill_layer_30b_shape(orc, T):
+    """a Q4_K layer at the 30B-A3B shape, T tokens of N(0,1), Zipf-skewed
+    routing: ids, weights and the layer output bit-identical to the CPU reference;
+    its RMSNorm within 1e-3 (double sum in another order, rounding identical
+    except within ~2^-29 of a float boundary)."""
+    H, E, k, F = 2048, 128, 8, 768
+    note(f"prefill layer 30B shape T={T} (reference: {'ggml' if have_ref() else 'oracle'})")
+    g = GpuLayerQ4K(H, E, k, F, seed=77)
+    rng = np.random.default_rng(T)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    out, xn, ids, w = ops.ffn_layer(g.layer, dev(x), rms_eps=1e-6)
+    out, xn, ids, w = host(out), host(xn), host(ids), host(w)
+    if have_ref():
+        r = RefGGML().layer(g.host, T, rms_eps=1e-6, n_threads=16)(x)
+    else:
+        r = orc.moe_layer(g.host, x, rms_eps=1e-6)
+    counts = np.bincount(r["ids"].reshape(-1), minlength=E)
+    note(f"  rows per expert: max {counts.max()}, experts >= 32 rows: {int((counts >= 32).sum())}, "
+         f"unused: {int((counts == 0).sum())}")
+    assert np.array_equal(ids, r["ids"])
+    assert np.array_equal(bits(w), bits(r["weights"]))
+    note(f"  output rel err {rel_err(out, r['out']):.3e}, rms_norm rel err {rel_err(xn, r['xnext']):.3e}")
+    assert np.array_equal(bits(out), bits(r["out"]))
+    assert rel_err(xn, r["xnext"]) < TOL
