@@ -116,6 +116,123 @@ def cpu_baseline(layers_host, xs, budget_s: float = 15.0):
                       f"scaled to the 48-layer stack"}
 
 
+def zipf_row_scales(E: int, s: float):
+    """Router row scales following a Zipf(s) rank profile (mean about 1): experts
+    with larger logit variance win the top-k more often, which skews the
+    per-expert row counts of a prefill batch towards low ids."""
+    import numpy as np
+    w = np.arange(1, E + 1, dtype=np.float64) ** (-s)
+    return (1.0 + 1.5 * w / w.max()).astype(np.float32)
+
+
+def prefill(args) -> int:
+    """one Qwen3-30B-A3B-shaped Q4_K MoE FFN layer, a prefill batch
+    of T=512 N(0,1) tokens, router rows skewed so expert popularity follows
+    Zipf(1.1).  A step = the whole layer (router, grouping, quantization,
+    gate/up/down mul_mat_id, SwiGLU, weighted sum, RMSNorm) for the 512 tokens."""
+    import numpy as np
+    import torch
+    from questwend_amd import Q4_K, ops, row_size
+
+    T = args.tokens
+    ops.init(0, 512 << 20)
+    dev = "cuda:0"
+    router = torch.empty((E, H), dtype=torch.float32, device=dev)
+    ops.randn_(router, args.seed * 1000 + 1, 0.0, 0.02)
+    router *= torch.from_numpy(zipf_row_scales(E, 1.1)).to(dev)[:, None]
+    mats = []
+    tmp = torch.empty(16 * F * H, dtype=torch.float32, device=dev)
+    for role, (rows, cols) in enumerate(((F, H), (F, H), (H, F))):
+        q = torch.empty((E * rows, row_size(Q4_K, cols)), dtype=torch.uint8, device=dev)
+        for e0 in range(0, E, 16):
+            ops.randn_(tmp[:16 * rows * cols], args.seed * 1000 + 2 + role * 100000 + e0, 0.0, 0.02)
+            ops.quantize_chunk_into(Q4_K, tmp[:16 * rows * cols].view(16 * rows, cols), q[e0 * rows:(e0 + 16) * rows])
+        mats.append(q)
+    del tmp
+    L = ops.make_layer(H, E, K_USED, F, router, *mats, (Q4_K,) * 3)
+    x = torch.empty((T, H), dtype=torch.float32, device=dev)
+    ops.randn_(x, args.seed + 555, 0.0, 1.0)
+    torch.cuda.synchronize()
+
+    def timed(min_rows: int):
+        prev = ops.set_mfma_min_rows(min_rows)
+        try:
+            for _ in range(args.warmup):
+                ops.ffn_layer(L, x, rms_eps=RMS_EPS)
+            torch.cuda.synchronize()
+            evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                   for _ in range(args.steps)]
+            t0 = time.perf_counter()
+            for a, b in evs:
+                a.record()
+                r = ops.ffn_layer(L, x, rms_eps=RMS_EPS)
+                b.record()
+            torch.cuda.synchronize()
+            wall = time.perf_counter() - t0
+            return wall / args.steps, sum(a.elapsed_time(b) for a, b in evs) / args.steps / 1000.0, r
+        finally:
+            ops.set_mfma_min_rows(prev)
+
+    step_s, ev_s, (out, xn, ids, w) = timed(args.mfma_min_rows)
+    gemv_s, _, (out_g, _, _, _) = timed(0)
+    same = bool(torch.equal(out.view(torch.int32), out_g.view(torch.int32)))
+    counts = np.bincount(ids.cpu().numpy().reshape(-1), minlength=E)
+    expert_bytes = 2 * F * row_size(Q4_K, H) + H * row_size(Q4_K, F)
+    wbytes = int((counts > 0).sum()) * expert_bytes + E * H * 4          # unique weights touched + router
+    macs = T * K_USED * (2 * F * H + H * F)                               # int8 MACs of the three projections
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = prefill_cpu_baseline(L, mats, router, x, T)
+    line = {
+        "metric": "prefill tok/s + achieved HBM GB/s and int8 MFMA rate, Q4_K MoE FFN layer 30B-A3B",
+        "value": round(T / step_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(step_s * 1e3, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q4_K x q8_K -> int32 (MFMA i8) -> f32", "data": "synthetic (seeded, router Zipf(1.1)-skewed)",
+        "config": {"workload": "Qwen3-30B-A3B MoE FFN layer, prefill T=512 (configs[2])", "n_embd": H,
+                   "n_expert": E, "n_expert_used": K_USED, "n_ff_exp": F, "tokens": T, "weights": "Q4_K",
+                   "path": f"qwmoe_ffn_layer (mfma_min_rows {args.mfma_min_rows})"},
+        "rows_per_expert": {"max": int(counts.max()), "ge32": int((counts >= 32).sum()), "unused": int((counts == 0).sum())},
+        "roofline": {"bound": "hbm", "achieved": round(wbytes / ev_s / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(wbytes / ev_s / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_step": wbytes, "avg_step_ms": round(ev_s * 1e3, 4),
+                     "int8_mac_rate_tops": round(macs / ev_s / 1e12, 2),
+                     "int8_mac_frac_of_2500_tmacs": round(macs / ev_s / 2.5e15, 4)},
+        "gemv_only_ms_per_step": round(gemv_s * 1e3, 4),
+        "mfma_equals_gemv_bitwise": same,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def prefill_cpu_baseline(L, mats, router, x, T: int):
+    """The reference ggml CPU backend (oracle/_ref) on the same layer and batch:
+    one evaluation of the T-token graph on 16 host threads."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    from oracle_lib import REF_SO, LayerWeights, RefGGML
+    from questwend_amd import Q4_K
+    if not REF_SO.exists():
+        return None
+    lw = LayerWeights.__new__(LayerWeights)
+    lw.H, lw.E, lw.k, lw.F = H, E, K_USED, F
+    lw.type_gate = lw.type_up = lw.type_down = Q4_K
+    lw.router = router.cpu().numpy()
+    lw.gate, lw.up, lw.down = (m.cpu().numpy().reshape(-1) for m in mats)
+    lw.n_slots, lw.slot_of = E, None
+    n_thr = min(16, os.cpu_count() or 1)
+    run = RefGGML().layer(lw, T, rms_eps=RMS_EPS, n_threads=n_thr)
+    xh = x.cpu().numpy()
+    run(xh, n_threads=n_thr)
+    t0 = time.perf_counter()
+    reps = 0
+    while time.perf_counter() - t0 < 10.0 or reps == 0:
+        run(xh, n_threads=n_thr)
+        reps += 1
+    dt = (time.perf_counter() - t0) / reps
+    return {"value": round(T / dt, 2), "unit": "tok/s", "cores": n_thr, "kind": "reference",
+            "sample": f"{reps} evaluations of the T={T} layer graph in {dt * reps:.1f}s"}
+
+
 def copy_probe(mib: int = 1024, reps: int = 4) -> int:
     """A plain device copy of known size (torch's copy kernel): run under
     ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE`` it gives the factor between
@@ -143,6 +260,10 @@ def main() -> int:
                     help="text file whose 'hbm_bytes_per_launch = N' line is the HBM traffic of one decode "
                          "launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (copy-calibrated)")
     ap.add_argument("--copy-probe", action="store_true", help="run only the copy-kernel calibration probe")
+    ap.add_argument("--workload", choices=["decode", "prefill"], default="decode",
+                    help="decode: configs[1] (the headline line); prefill: configs[2]")
+    ap.add_argument("--tokens", type=int, default=512, help="prefill batch size")
+    ap.add_argument("--mfma-min-rows", type=int, default=1, help="prefill: experts with this many rows use MFMA")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the sharding plan is "
@@ -150,6 +271,8 @@ def main() -> int:
         return 2
     if args.copy_probe:
         return copy_probe()
+    if args.workload == "prefill":
+        return prefill(args)
 
     import numpy as np
     import torch

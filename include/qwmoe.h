@@ -68,11 +68,12 @@ int qwmoe_shutdown(void);
 const char * qwmoe_strerror(int status);
 /* Experts that receive at least `rows` rows in one mul_mat_id (prefill and
  * large verify batches) are computed on the int8 matrix cores
- * (v_mfma_i32_16x16x64_i8) when the weight type is Q4_K: the integer block sums
- * are exact, the fp32 accumulation order differs from the AVX2 one (outputs
- * agree with ggml's to a few ulps).  Lighter experts, and every expert when
- * rows == 0, use the bit-exact GEMV.  Default 32.  No reference counterpart:
- * ggml's CPU backend has a single dot product (ggml-cpu.c:1463-1524). */
+ * (v_mfma_i32_16x16x32_i8 / 16x16x64_i8) when the weight type is Q4_K; lighter
+ * experts, and every expert when rows == 0, use the LDS-tiled GEMV.  Both are
+ * bit-identical to ggml (the matrix-core kernel forms the eight AVX2 lane sums
+ * and four min lanes exactly and replays their float steps).  Default 8.  No
+ * reference counterpart: ggml's CPU backend has one dot product per type
+ * (ggml-cpu.c:1463-1524); this only selects the GPU kernel. */
 int qwmoe_set_mfma_min_rows(int rows);
 int qwmoe_get_mfma_min_rows(void);
 /* Bytes used by the workspace of the most demanding call so far. */

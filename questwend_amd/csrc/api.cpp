@@ -24,7 +24,7 @@ struct Library {
     size_t ws_bytes = 0;
     size_t high_water = 0;
     int32_t* status = nullptr;   // device status word (first 256 bytes of the arena)
-    int mfma_min_rows = 32;      // experts with this many routed rows use the matrix-core kernel (0: never)
+    int mfma_min_rows = 8;       // experts with this many routed rows use the matrix-core kernel (0: never)
 };
 
 Library g_lib;

@@ -24,16 +24,41 @@ __device__ __forceinline__ uint64_t lanemask_lt() {
     return lane == 0 ? 0ull : (~0ull >> (64 - lane));
 }
 
+// Per-slice counters: in LDS when GROUP_WAVES * n_bins fits (GROUP_LDS_BINS),
+// else in global memory touched only through L2 atomics (so no lane ever reads
+// a stale per-CU cached copy).
+constexpr int GROUP_LDS_BINS = 2048;
+
+template <bool IN_LDS>
+__device__ __forceinline__ int32_t hist_add(int32_t* h, int32_t v) {
+    if constexpr (IN_LDS) return atomicAdd(h, v);
+    else return __hip_atomic_fetch_add(h, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <bool IN_LDS>
+__device__ __forceinline__ int32_t hist_load(int32_t* h) {
+    if constexpr (IN_LDS) return *(volatile int32_t*) h;
+    else return __hip_atomic_load(h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <bool IN_LDS>
+__device__ __forceinline__ int32_t hist_exchange(int32_t* h, int32_t v) {
+    if constexpr (IN_LDS) return atomicExch(h, v);
+    else return __hip_atomic_exchange(h, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <bool IN_LDS>
 __global__ void __launch_bounds__(GROUP_WAVES * 64) k_group(GroupArgs g) {
+    __shared__ int32_t s_hist[IN_LDS ? GROUP_WAVES * GROUP_LDS_BINS : 1];
     const int lane = threadIdx.x & 63;
     const int w = threadIdx.x >> 6;
     const int64_t P = g.T * g.n_ids;
     const int64_t S = (P + GROUP_WAVES - 1) / GROUP_WAVES;
     const int64_t f0 = w * S, f1 = (f0 + S < P) ? f0 + S : P;
-    // Per-slice counters live in global memory and are only touched through
-    // L2 atomics, so no lane ever reads a stale per-CU cached copy.
-    int32_t* hist = g.hist_ws + (int64_t) w * g.n_bins;
-    for (int64_t a = lane; a < g.n_bins; a += 64) __hip_atomic_store(hist + a, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    int32_t* hist_base = IN_LDS ? s_hist : g.hist_ws;
+    int32_t* hist = hist_base + (int64_t) w * g.n_bins;
+    for (int64_t a = lane; a < g.n_bins; a += 64) {
+        if constexpr (IN_LDS) hist[a] = 0;
+        else __hip_atomic_store(hist + a, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     __syncthreads();
     // phase A: per-slice histogram by peeling equal keys within each 64-chunk
     for (int64_t c = f0; c < f1; c += 64) {
@@ -52,7 +77,7 @@ __global__ void __launch_bounds__(GROUP_WAVES * 64) k_group(GroupArgs g) {
             const int leader = __ffsll((unsigned long long) pending) - 1;
             const int k = __shfl(key, leader);
             const uint64_t m = __ballot(key == k);
-            if (lane == leader) atomicAdd(hist + k, (int32_t) __popcll(m));
+            if (lane == leader) hist_add<IN_LDS>(hist + k, (int32_t) __popcll(m));
             pending &= ~m;
         }
     }
@@ -67,8 +92,7 @@ __global__ void __launch_bounds__(GROUP_WAVES * 64) k_group(GroupArgs g) {
     int32_t csum = 0, asum = 0;
     for (int64_t a = b0; a < b1; ++a) {
         int32_t tot = 0;
-        for (int ww = 0; ww < GROUP_WAVES; ++ww)
-            tot += __hip_atomic_load(g.hist_ws + (int64_t) ww * g.n_bins + a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int ww = 0; ww < GROUP_WAVES; ++ww) tot += hist_load<IN_LDS>(hist_base + (int64_t) ww * g.n_bins + a);
         csum += tot;
         asum += tot > 0;
     }
@@ -93,8 +117,8 @@ __global__ void __launch_bounds__(GROUP_WAVES * 64) k_group(GroupArgs g) {
     for (int64_t a = b0; a < b1; ++a) {
         int32_t run = off, tot = 0;
         for (int ww = 0; ww < GROUP_WAVES; ++ww) {
-            int32_t* h = g.hist_ws + (int64_t) ww * g.n_bins + a;
-            const int32_t c = __hip_atomic_exchange(h, run, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // -> write cursor
+            int32_t* h = hist_base + (int64_t) ww * g.n_bins + a;
+            const int32_t c = hist_exchange<IN_LDS>(h, run);  // -> write cursor
             run += c;
             tot += c;
         }
@@ -125,7 +149,7 @@ __global__ void __launch_bounds__(GROUP_WAVES * 64) k_group(GroupArgs g) {
             const int k = __shfl(key, leader);
             const uint64_t m = __ballot(key == k);
             int32_t base = 0;
-            if (lane == leader) base = atomicAdd(hist + k, (int32_t) __popcll(m));
+            if (lane == leader) base = hist_add<IN_LDS>(hist + k, (int32_t) __popcll(m));
             base = __shfl(base, leader);
             if (key == k) {
                 const int32_t pos = base + __popcll(m & lanemask_lt());
@@ -139,7 +163,8 @@ __global__ void __launch_bounds__(GROUP_WAVES * 64) k_group(GroupArgs g) {
 
 int launch_group(const GroupArgs& g, hipStream_t stream) {
     if (g.n_bins <= 0) return -2;
-    hipLaunchKernelGGL(k_group, dim3(1), dim3(GROUP_WAVES * 64), 0, stream, g);
+    if (g.n_bins <= GROUP_LDS_BINS) hipLaunchKernelGGL(k_group<true>, dim3(1), dim3(GROUP_WAVES * 64), 0, stream, g);
+    else hipLaunchKernelGGL(k_group<false>, dim3(1), dim3(GROUP_WAVES * 64), 0, stream, g);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 

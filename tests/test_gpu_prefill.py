@@ -40,7 +40,7 @@ def lib_init():
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     ops.init(0, 512 << 20)
-    prev = ops.set_mfma_min_rows(32)
+    prev = ops.set_mfma_min_rows(8)
     yield
     torch.cuda.synchronize()
     ops.set_mfma_min_rows(prev)
