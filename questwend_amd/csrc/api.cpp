@@ -92,6 +92,7 @@ int mmid_grouped(hipStream_t st, int type, const void* as, int64_t K, int64_t N,
     // batch holds that many pairs) go to the int8 matrix-core kernel; the rest
     // stay on the bit-exact GEMV
     m.mfma_min_rows = 0;
+    m.max_rows = max_rows;
     const bool mfma = g_lib.mfma_min_rows > 0 && max_rows >= g_lib.mfma_min_rows && qw::mmid_mfma_supported(m);
     if (mfma) m.mfma_min_rows = g_lib.mfma_min_rows;
     int rc = qw::launch_mmid_gemv(m, st);

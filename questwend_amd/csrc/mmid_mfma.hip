@@ -27,6 +27,8 @@
 // v_mfma_i32_16x16x64_i8 over the 64 positions of sub-blocks 2m and 2m+1 with
 // every A byte equal to that sub-block's min.  20 MFMAs per 16 x 16 tile and
 // super-block.
+#include <algorithm>
+
 #include "qw_kernels.hpp"
 
 namespace qw {
@@ -35,21 +37,27 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4m __attribute__((ext_vector_type(4)));
 
 constexpr int MF_M = 64;          // weight rows per workgroup (4 waves x 16)
-constexpr int MF_TILES = 2;       // 16-row activation tiles per wave and pass
-constexpr int MF_N = 16 * MF_TILES;
+constexpr int MF_N = 16;          // activation rows per workgroup (one 16-row tile per wave)
 constexpr uint32_t MF_WS = 144;   // LDS stride of a staged Q4_K block (9 x 16 B)
 constexpr uint32_t MF_AS = 272;   // LDS stride of a staged Q8_K block: d at 0, qs at 16 (16-aligned)
+constexpr int MF_WCH = (MF_M * 9 + 255) / 256;    // 16-byte weight chunks per thread and super-block
+constexpr int MF_ACH = (MF_N * 65 + 255) / 256;   // activation dwords per thread and super-block
 
 __device__ __forceinline__ long pack2(uint32_t lo, uint32_t hi) { return (long) (((uint64_t) hi << 32) | lo); }
 
-__global__ void __launch_bounds__(256) k_mmid_mfma_q4k(MmidArgs m) {
-    __shared__ __align__(16) uint8_t s_w[MF_M * MF_WS];
-    __shared__ __align__(16) uint8_t s_a[MF_N * MF_AS];
+// Workgroup (row tile x, active expert y, pass z): weight rows r0 .. r0 + 63 of the
+// expert's matrix against its routed activation rows 16 z .. 16 z + 15.  Super-block
+// i + 1 is loaded into registers while super-block i is computed from LDS.
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) k_mmid_mfma_q4k(MmidArgs m) {
+    __shared__ __align__(16) uint8_t s_w[2][MF_M * MF_WS];
+    __shared__ __align__(16) uint8_t s_a[2][MF_N * MF_AS];
+    __shared__ int32_t s_arow[MF_N];
     __shared__ int32_t s_et[MF_N][2];
     const int g = blockIdx.y;
     if (g >= *m.n_active) return;
     const int p0 = m.active_off[g], p1 = m.active_off[g + 1];
     if (p1 - p0 < m.mfma_min_rows) return;   // light expert: the GEMV kernel's
+    if (p0 + MF_N * (int) blockIdx.z >= p1) return;
     const int bin = m.active[g];
     int64_t mat = bin;
     if (m.slot_of) mat = (bin < m.n_slot_of) ? m.slot_of[bin] : -1;
@@ -59,129 +67,143 @@ __global__ void __launch_bounds__(256) k_mmid_mfma_q4k(MmidArgs m) {
     }
     const int64_t r0 = (int64_t) blockIdx.x * MF_M;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int lr = lane & 15, gq = lane >> 4;   // A row / B row within a tile; k-slot group
+    const int lr = lane & 15, gq = lane >> 4;   // A row / B row within the tile; k-slot group
     const int nb = (int) (m.K / QK_K);
     const uint8_t* wtile = m.w + (size_t) mat * m.nb2 + (size_t) r0 * m.nb1;
     const int arow_l = 16 * wave + lr;          // this lane's A row in the staged tile
+    for (int pass = blockIdx.z;; pass += gridDim.z) {
+    const int pc = p0 + MF_N * pass;
+    if (pc >= p1) break;
+    const int ntok = (p1 - pc) < MF_N ? (p1 - pc) : MF_N;
+    lds_barrier();   // the previous pass is done with the staged tiles
+    if (tid < MF_N) {
+        const int pp = pc + (tid < ntok ? tid : 0);
+        const int e = m.rows[2 * pp], t = m.rows[2 * pp + 1];
+        s_et[tid][0] = e;
+        s_et[tid][1] = t;
+        s_arow[tid] = (int) ((int64_t) (e % m.b_ne1) + (int64_t) t * m.b_ne1);
+    }
+    lds_barrier();
 
-    for (int pc = p0; pc < p1; pc += MF_N) {
-        const int ntok = (p1 - pc) < MF_N ? (p1 - pc) : MF_N;
-        lds_barrier();   // the previous pass is done with s_et / s_a
-        if (tid < MF_N) {
-            const int pp = pc + (tid < ntok ? tid : 0);
-            s_et[tid][0] = m.rows[2 * pp];
-            s_et[tid][1] = m.rows[2 * pp + 1];
+    // staging: this thread's weight chunks and activation dwords of super-block i
+    u32x4m wreg[MF_WCH];
+    uint32_t areg[MF_ACH];
+    auto load = [&](int i) {
+#pragma unroll
+        for (int j = 0; j < MF_WCH; ++j) {
+            const int z = min(tid + 256 * j, MF_M * 9 - 1);
+            const int r = z / 9, c = z - r * 9;
+            wreg[j] = *(const __attribute__((address_space(1))) u32x4m*) (wtile + (size_t) r * m.nb1 +
+                                                                        (size_t) i * 144 + 16 * c);
         }
-        // per output (tile t, D register r): the eight AVX lanes and four min lanes
-        float acc[MF_TILES][4][8], accm[MF_TILES][4][4];
 #pragma unroll
-        for (int t = 0; t < MF_TILES; ++t)
+        for (int j = 0; j < MF_ACH; ++j) {
+            const int z = min(tid + 256 * j, ntok * 65 - 1);
+            const int n = z / 65, c = z - n * 65;
+            const uint32_t* src = (const uint32_t*) (m.act_q + (size_t) s_arow[n] * m.act_row_bytes + (size_t) i * 292);
+            areg[j] = *(const __attribute__((address_space(1))) uint32_t*) (src + c);
+        }
+    };
+    auto store = [&](int buf) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-#pragma unroll
-                for (int L = 0; L < 8; ++L) acc[t][r][L] = 0.0f;
-#pragma unroll
-                for (int q = 0; q < 4; ++q) accm[t][r][q] = 0.0f;
-            }
-        lds_barrier();
-        for (int i = 0; i < nb; ++i) {
-            // stage super-block i: 64 weight rows (16-byte chunks) and the pass's
-            // activation blocks (d and the 256 quants, as dwords: rows are 4-aligned)
-            for (int z = tid; z < MF_M * 9; z += 256) {
+        for (int j = 0; j < MF_WCH; ++j) {
+            const int z = tid + 256 * j;
+            if (z < MF_M * 9) {
                 const int r = z / 9, c = z - r * 9;
-                const u32x4m v = *(const __attribute__((address_space(1))) u32x4m*) (wtile + (size_t) r * m.nb1 +
-                                                                                   (size_t) i * 144 + 16 * c);
-                *(u32x4m*) (s_w + r * MF_WS + 16 * c) = v;
+                *(u32x4m*) (s_w[buf] + r * MF_WS + 16 * c) = wreg[j];
             }
-            for (int z = tid; z < ntok * 65; z += 256) {
+        }
+#pragma unroll
+        for (int j = 0; j < MF_ACH; ++j) {
+            const int z = tid + 256 * j;
+            if (z < ntok * 65) {
                 const int n = z / 65, c = z - n * 65;
-                const int e = s_et[n][0], t = s_et[n][1];
-                const int64_t arow = (int64_t) (e % m.b_ne1) + (int64_t) t * m.b_ne1;
-                const uint32_t* src = (const uint32_t*) (m.act_q + (size_t) arow * m.act_row_bytes + (size_t) i * 292);
-                *(uint32_t*) (s_a + n * MF_AS + (c == 0 ? 0 : 12 + 4 * c)) = src[c];
-            }
-            lds_barrier();
-            // this lane's A row: the 6-bit scales and mins of the 8 sub-blocks
-            // (the utmp shuffle of quants.c:2067-2072), as bytes
-            const u32x4m hdr = *(const u32x4m*) (s_w + arow_l * MF_WS);
-            const uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;
-            const uint32_t sc_lo = s0 & 0x3f3f3f3fu;
-            const uint32_t sc_hi = (s2 & 0x0f0f0f0fu) | (((s0 >> 6) & 0x03030303u) << 4);
-            const uint32_t mn_lo = s1 & 0x3f3f3f3fu;
-            const uint32_t mn_hi = ((s2 >> 4) & 0x0f0f0f0fu) | (((s1 >> 6) & 0x03030303u) << 4);
-            // sub-blocks 2 gq (low nibbles) and 2 gq + 1 (high nibbles) of this lane's k-slots
-            const uint32_t scw = gq < 2 ? sc_lo : sc_hi;
-            const uint32_t sa = (scw >> (16 * (gq & 1))) & 0xffu, sb = (scw >> (16 * (gq & 1) + 8)) & 0xffu;
-            // block scales of the D rows 4 gq + r and the B rows of each tile
-            float dx[4], dmx[4], dy[MF_TILES];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t h0 = *(const uint32_t*) (s_w + (16 * wave + 4 * gq + r) * MF_WS);
-                dx[r] = h2f((uint16_t) (h0 & 0xffff));
-                dmx[r] = h2f((uint16_t) (h0 >> 16));
-            }
-#pragma unroll
-            for (int t = 0; t < MF_TILES; ++t) dy[t] = *(const float*) (s_a + (16 * t + lr) * MF_AS);
-            // AVX lanes
-#pragma unroll
-            for (int L = 0; L < 8; ++L) {
-                const uint32_t w = *(const uint32_t*) (s_w + arow_l * MF_WS + 16 + 32 * gq + 4 * L);
-                const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
-                const long a_lo = pack2(lo * (sa & 7u), hi * (sb & 7u));
-                const long a_hi = pack2(lo * (sa >> 3), hi * (sb >> 3));
-#pragma unroll
-                for (int t = 0; t < MF_TILES; ++t) {
-                    const uint8_t* ab = s_a + (16 * t + lr) * MF_AS + 16 + 64 * gq + 4 * L;
-                    const long bq = pack2(*(const uint32_t*) ab, *(const uint32_t*) (ab + 32));
-                    const v4i z4 = v4i{0, 0, 0, 0};
-                    const v4i dlo = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_lo, bq, z4, 0, 0, 0);
-                    const v4i dhi = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_hi, bq, z4, 0, 0, 0);
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const float d = dy[t] * dx[r];
-                        acc[t][r][L] = __builtin_fmaf(d, (float) (8 * dhi[r] + dlo[r]), acc[t][r][L]);
-                    }
-                }
-            }
-            // min lanes: sub-blocks 2q (k-slots of lane groups 0, 1) and 2q + 1 (groups 2, 3)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int sbk = 2 * q + (gq >> 1);
-                const uint32_t mnw = sbk < 4 ? mn_lo : mn_hi;
-                const int mb = (int) (((mnw >> (8 * (sbk & 3))) & 0xffu) * 0x01010101u);
-                const v4i a_mn = v4i{mb, mb, mb, mb};
-#pragma unroll
-                for (int t = 0; t < MF_TILES; ++t) {
-                    const v4i bq = *(const v4i*) (s_a + (16 * t + lr) * MF_AS + 16 + 64 * q + 16 * gq);
-                    const v4i dm = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_mn, bq, v4i{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const float dmin = -dy[t] * dmx[r];
-                        accm[t][r][q] = __builtin_fmaf(dmin, (float) dm[r], accm[t][r][q]);
-                    }
-                }
-            }
-            lds_barrier();   // staged tiles consumed
-        }
-        // hsum_float_8(acc) + ((m0 + m2) + (m1 + m3)); rows r0 + 16 wave + 4 gq .. +3
-#pragma unroll
-        for (int t = 0; t < MF_TILES; ++t) {
-            const int n = 16 * t + lr;
-            float o[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float* a = acc[t][r];
-                const float hs = ((a[4] + a[0]) + (a[6] + a[2])) + ((a[5] + a[1]) + (a[7] + a[3]));
-                const float* mm = accm[t][r];
-                o[r] = hs + ((mm[0] + mm[2]) + (mm[1] + mm[3]));
-            }
-            if (n < ntok) {
-                const int e = s_et[n][0], tt = s_et[n][1];
-                float* d = (float*) ((char*) m.dst + (size_t) e * m.dst_nb1 + (size_t) tt * m.dst_nb2) + r0 +
-                           16 * wave + 4 * gq;
-                *(float4*) d = float4{o[0], o[1], o[2], o[3]};
+                *(uint32_t*) (s_a[buf] + n * MF_AS + (c == 0 ? 0 : 12 + 4 * c)) = areg[j];
             }
         }
+    };
+
+    // per output (D register r): the eight AVX lanes and four min lanes
+    float acc[4][8], accm[4][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+#pragma unroll
+        for (int L = 0; L < 8; ++L) acc[r][L] = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) accm[r][q] = 0.0f;
+    }
+    load(0);
+    store(0);
+    lds_barrier();
+    for (int i = 0; i < nb; ++i) {
+        const int buf = i & 1;
+        if (i + 1 < nb) load(i + 1);
+        const uint8_t* sw = s_w[buf];
+        const uint8_t* sa = s_a[buf];
+        // this lane's A row: the 6-bit scales and mins of the 8 sub-blocks
+        // (the utmp shuffle of quants.c:2067-2072), as bytes
+        const u32x4m hdr = *(const u32x4m*) (sw + arow_l * MF_WS);
+        const uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;
+        const uint32_t sc_lo = s0 & 0x3f3f3f3fu;
+        const uint32_t sc_hi = (s2 & 0x0f0f0f0fu) | (((s0 >> 6) & 0x03030303u) << 4);
+        const uint32_t mn_lo = s1 & 0x3f3f3f3fu;
+        const uint32_t mn_hi = ((s2 >> 4) & 0x0f0f0f0fu) | (((s1 >> 6) & 0x03030303u) << 4);
+        // sub-blocks 2 gq (low nibbles) and 2 gq + 1 (high nibbles) of this lane's k-slots
+        const uint32_t scw = gq < 2 ? sc_lo : sc_hi;
+        const uint32_t sa_ = (scw >> (16 * (gq & 1))) & 0xffu, sb_ = (scw >> (16 * (gq & 1) + 8)) & 0xffu;
+        // block scales of the D rows 4 gq + r and of this lane's B row
+        float d[4], dmin[4];
+        const float dy = *(const float*) (sa + lr * MF_AS);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t h0 = *(const uint32_t*) (sw + (16 * wave + 4 * gq + r) * MF_WS);
+            d[r] = dy * h2f((uint16_t) (h0 & 0xffff));
+            dmin[r] = -dy * h2f((uint16_t) (h0 >> 16));
+        }
+        // AVX lanes
+#pragma unroll
+        for (int L = 0; L < 8; ++L) {
+            const uint32_t w = *(const uint32_t*) (sw + arow_l * MF_WS + 16 + 32 * gq + 4 * L);
+            const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+            const long a_lo = pack2(lo * (sa_ & 7u), hi * (sb_ & 7u));
+            const long a_hi = pack2(lo * (sa_ >> 3), hi * (sb_ >> 3));
+            const uint8_t* ab = sa + lr * MF_AS + 16 + 64 * gq + 4 * L;
+            const long bq = pack2(*(const uint32_t*) ab, *(const uint32_t*) (ab + 32));
+            const v4i z4 = v4i{0, 0, 0, 0};
+            const v4i dlo = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_lo, bq, z4, 0, 0, 0);
+            const v4i dhi = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_hi, bq, z4, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[r][L] = __builtin_fmaf(d[r], (float) (8 * dhi[r] + dlo[r]), acc[r][L]);
+        }
+        // min lanes: sub-blocks 2q (k-slots of lane groups 0, 1) and 2q + 1 (groups 2, 3)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int sbk = 2 * q + (gq >> 1);
+            const uint32_t mnw = sbk < 4 ? mn_lo : mn_hi;
+            const int mb = (int) (((mnw >> (8 * (sbk & 3))) & 0xffu) * 0x01010101u);
+            const v4i a_mn = v4i{mb, mb, mb, mb};
+            const v4i bq = *(const v4i*) (sa + lr * MF_AS + 16 + 64 * q + 16 * gq);
+            const v4i dm = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_mn, bq, v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) accm[r][q] = __builtin_fmaf(dmin[r], (float) dm[r], accm[r][q]);
+        }
+        if (i + 1 < nb) store(buf ^ 1);   // the other buffer was last read before the previous barrier
+        lds_barrier();
+    }
+    // hsum_float_8(acc) + ((m0 + m2) + (m1 + m3)); rows r0 + 16 wave + 4 gq .. +3 of B row lr
+    float o[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float* a = acc[r];
+        const float hs = ((a[4] + a[0]) + (a[6] + a[2])) + ((a[5] + a[1]) + (a[7] + a[3]));
+        const float* mm = accm[r];
+        o[r] = hs + ((mm[0] + mm[2]) + (mm[1] + mm[3]));
+    }
+    if (lr < ntok) {
+        const int e = s_et[lr][0], tt = s_et[lr][1];
+        float* dp = (float*) ((char*) m.dst + (size_t) e * m.dst_nb1 + (size_t) tt * m.dst_nb2) + r0 + 16 * wave + 4 * gq;
+        *(float4*) dp = float4{o[0], o[1], o[2], o[3]};
+    }
     }
 }
 
@@ -195,7 +217,11 @@ bool mmid_mfma_supported(const MmidArgs& m) {
 
 int launch_mmid_mfma(const MmidArgs& m, hipStream_t stream) {
     if (!mmid_mfma_supported(m)) return -2;
-    dim3 grid((unsigned) (m.N / MF_M), (unsigned) m.max_active);
+    // passes of 16 rows (an expert receives at most max_rows rows); workgroup z
+    // takes passes z, z + gridDim.z, ...
+    const int64_t passes = (m.max_rows + MF_N - 1) / MF_N;
+    const unsigned gz = (unsigned) std::min<int64_t>(std::max<int64_t>(passes, 1), 16);
+    dim3 grid((unsigned) (m.N / MF_M), (unsigned) m.max_active, gz);
     if (grid.y == 0) return 0;
     hipLaunchKernelGGL(k_mmid_mfma_q4k, grid, dim3(256), 0, stream, m);
     return hipGetLastError() == hipSuccess ? 0 : -3;

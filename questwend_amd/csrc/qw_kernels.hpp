@@ -66,6 +66,7 @@ struct MmidArgs {
     int32_t* status;          // bit 2 set on an out-of-range slot
     int64_t max_active;       // grid bound on active bins
     int mfma_min_rows;        // bins with at least this many rows go to the matrix-core kernel (0: none do)
+    int64_t max_rows;         // bound on the rows of one bin
 };
 int launch_mmid_gemv(const MmidArgs& m, hipStream_t stream);
 // mmid_mfma.hip
