@@ -19,15 +19,11 @@ namespace qw {
 // One workgroup of GROUP_WAVES waves; wave w owns a contiguous slice of the
 // flattened pair index f = t * n_ids + e, so slice order == ggml row order.
 
-__device__ __forceinline__ uint64_t lanemask_lt() {
-    const int lane = threadIdx.x & 63;
-    return lane == 0 ? 0ull : (~0ull >> (64 - lane));
-}
-
 // Per-slice counters: in LDS when GROUP_WAVES * n_bins fits (GROUP_LDS_BINS),
 // else in global memory touched only through L2 atomics (so no lane ever reads
 // a stale per-CU cached copy).
-constexpr int GROUP_LDS_BINS = 2048;
+constexpr int GROUP_LDS_BINS = 1024;
+constexpr int GROUP_UNROLL = 4;  // 64-pair chunks whose ids are loaded together
 
 template <bool IN_LDS>
 __device__ __forceinline__ int32_t hist_add(int32_t* h, int32_t v) {
@@ -36,56 +32,88 @@ __device__ __forceinline__ int32_t hist_add(int32_t* h, int32_t v) {
 }
 template <bool IN_LDS>
 __device__ __forceinline__ int32_t hist_load(int32_t* h) {
-    if constexpr (IN_LDS) return *(volatile int32_t*) h;
+    if constexpr (IN_LDS) return *h;
     else return __hip_atomic_load(h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Replaces a counter that only the calling thread touches in this phase.
 template <bool IN_LDS>
 __device__ __forceinline__ int32_t hist_exchange(int32_t* h, int32_t v) {
-    if constexpr (IN_LDS) return atomicExch(h, v);
-    else return __hip_atomic_exchange(h, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if constexpr (IN_LDS) {
+        const int32_t old = *h;
+        *h = v;
+        return old;
+    } else {
+        return __hip_atomic_exchange(h, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// Ranks the keys of one 64-pair chunk without serialising over distinct keys:
+// the lanes holding a lane's key (its peers) are found bit by bit from one
+// ballot per key bit (keys < 2^nbits); rank = earlier peers, cnt = peers, first
+// = lowest peer.  Lanes with key < 0 are nobody's peers and are ignored.
+struct ChunkRank {
+    int rank, cnt, first;
+};
+__device__ __forceinline__ ChunkRank chunk_rank(int key, int nbits) {
+    const int lane = threadIdx.x & 63;
+    uint64_t peers = __ballot(key >= 0);
+    for (int b = 0; b < nbits; ++b) {
+        const bool bit = (key >> b) & 1;
+        const uint64_t m = __ballot(bit);
+        peers &= bit ? m : ~m;
+    }
+    const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    return ChunkRank{(int) __popcll(peers & lt), (int) __popcll(peers), __ffsll((unsigned long long) peers) - 1};
+}
+
+// Key of pair f = t * n_ids + e (-1 past the slice end or out of range).
+__device__ __forceinline__ int pair_key(const GroupArgs& g, int f, int f1, int& t, int& e, bool flag) {
+    t = 0;
+    e = 0;
+    if (f >= f1) return -1;
+    t = (int) ((uint32_t) f / (uint32_t) g.n_ids);
+    e = f - t * (int) g.n_ids;
+    int key = g.ids[(int64_t) t * g.ids_stride + e];
+    if (key < 0 || key >= g.n_bins) {
+        if (flag && g.status) atomicOr(g.status, 2);
+        key = -1;
+    }
+    return key;
 }
 
 template <bool IN_LDS>
 __global__ void __launch_bounds__(GROUP_WAVES * 64) k_group(GroupArgs g) {
     __shared__ int32_t s_hist[IN_LDS ? GROUP_WAVES * GROUP_LDS_BINS : 1];
+    __shared__ int32_t s_wsum[2][GROUP_WAVES];
     const int lane = threadIdx.x & 63;
     const int w = threadIdx.x >> 6;
-    const int64_t P = g.T * g.n_ids;
-    const int64_t S = (P + GROUP_WAVES - 1) / GROUP_WAVES;
-    const int64_t f0 = w * S, f1 = (f0 + S < P) ? f0 + S : P;
+    const int P = (int) (g.T * g.n_ids);
+    const int S = (P + GROUP_WAVES - 1) / GROUP_WAVES;
+    const int f0 = w * S, f1 = (f0 + S < P) ? f0 + S : P;
     int32_t* hist_base = IN_LDS ? s_hist : g.hist_ws;
     int32_t* hist = hist_base + (int64_t) w * g.n_bins;
+    const int nbits = g.n_bins > 1 ? 32 - __clz((int) (g.n_bins - 1)) : 0;
     for (int64_t a = lane; a < g.n_bins; a += 64) {
         if constexpr (IN_LDS) hist[a] = 0;
         else __hip_atomic_store(hist + a, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
-    // phase A: per-slice histogram by peeling equal keys within each 64-chunk
-    for (int64_t c = f0; c < f1; c += 64) {
-        const int64_t f = c + lane;
-        int key = -1;
-        if (f < f1) {
-            const int64_t t = f / g.n_ids, e = f % g.n_ids;
-            key = g.ids[t * g.ids_stride + e];
-            if (key < 0 || key >= g.n_bins) {
-                if (g.status) atomicOr(g.status, 2);
-                key = -1;
-            }
-        }
-        uint64_t pending = __ballot(key >= 0);
-        while (pending) {
-            const int leader = __ffsll((unsigned long long) pending) - 1;
-            const int k = __shfl(key, leader);
-            const uint64_t m = __ballot(key == k);
-            if (lane == leader) hist_add<IN_LDS>(hist + k, (int32_t) __popcll(m));
-            pending &= ~m;
+    // phase A: per-slice histogram; the first lane of each key in a chunk adds
+    // the chunk's count for it
+    for (int c = f0; c < f1; c += GROUP_UNROLL * 64) {
+        int t[GROUP_UNROLL], e[GROUP_UNROLL], key[GROUP_UNROLL];
+#pragma unroll
+        for (int u = 0; u < GROUP_UNROLL; ++u) key[u] = pair_key(g, c + 64 * u + lane, f1, t[u], e[u], true);
+#pragma unroll
+        for (int u = 0; u < GROUP_UNROLL; ++u) {
+            const ChunkRank r = chunk_rank(key[u], nbits);
+            if (key[u] >= 0 && r.rank == 0) hist_add<IN_LDS>(hist + key[u], r.cnt);
         }
     }
     __syncthreads();
     // phase B: totals, exclusive scan over bins, per-slice bases, active list.
-    // Each thread scans a contiguous chunk of bins; chunk sums are scanned in LDS.
-    __shared__ int32_t part_cnt[GROUP_WAVES * 64];
-    __shared__ int32_t part_act[GROUP_WAVES * 64];
+    // Each thread takes a contiguous run of bins; run sums are scanned across
+    // the workgroup (wave prefix sums, then the wave totals).
     const int nthr = GROUP_WAVES * 64;
     const int64_t per = (g.n_bins + nthr - 1) / nthr;
     const int64_t b0 = threadIdx.x * per, b1 = (b0 + per < g.n_bins) ? b0 + per : g.n_bins;
@@ -96,29 +124,39 @@ __global__ void __launch_bounds__(GROUP_WAVES * 64) k_group(GroupArgs g) {
         csum += tot;
         asum += tot > 0;
     }
-    part_cnt[threadIdx.x] = csum;
-    part_act[threadIdx.x] = asum;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        int32_t rc = 0, ra = 0;
-        for (int i = 0; i < nthr; ++i) {
-            const int32_t c = part_cnt[i], q = part_act[i];
-            part_cnt[i] = rc;
-            part_act[i] = ra;
-            rc += c;
-            ra += q;
+    int32_t ic = csum, ia = asum;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int32_t uc = __shfl_up(ic, d), ua = __shfl_up(ia, d);
+        if (lane >= d) {
+            ic += uc;
+            ia += ua;
         }
-        if (g.n_active) *g.n_active = ra;
-        if (g.offsets) g.offsets[g.n_bins] = rc;
-        if (g.active_off) g.active_off[ra] = rc;
+    }
+    if (lane == 63) {
+        s_wsum[0][w] = ic;
+        s_wsum[1][w] = ia;
     }
     __syncthreads();
-    int32_t off = part_cnt[threadIdx.x], aidx = part_act[threadIdx.x];
+    int32_t off = ic - csum, aidx = ia - asum, tc = 0, ta = 0;
+    for (int ww = 0; ww < GROUP_WAVES; ++ww) {
+        const int32_t wc = s_wsum[0][ww], wa = s_wsum[1][ww];
+        if (ww < w) {
+            off += wc;
+            aidx += wa;
+        }
+        tc += wc;
+        ta += wa;
+    }
+    if (threadIdx.x == 0) {
+        if (g.n_active) *g.n_active = ta;
+        if (g.offsets) g.offsets[g.n_bins] = tc;
+        if (g.active_off) g.active_off[ta] = tc;
+    }
     for (int64_t a = b0; a < b1; ++a) {
         int32_t run = off, tot = 0;
         for (int ww = 0; ww < GROUP_WAVES; ++ww) {
-            int32_t* h = hist_base + (int64_t) ww * g.n_bins + a;
-            const int32_t c = hist_exchange<IN_LDS>(h, run);  // -> write cursor
+            const int32_t c = hist_exchange<IN_LDS>(hist_base + (int64_t) ww * g.n_bins + a, run);  // -> write cursor
             run += c;
             tot += c;
         }
@@ -132,37 +170,30 @@ __global__ void __launch_bounds__(GROUP_WAVES * 64) k_group(GroupArgs g) {
         off += tot;
     }
     __syncthreads();
-    // phase C: stable scatter of (e, t) pairs
-    for (int64_t c = f0; c < f1; c += 64) {
-        const int64_t f = c + lane;
-        int key = -1;
-        int64_t t = 0, e = 0;
-        if (f < f1) {
-            t = f / g.n_ids;
-            e = f % g.n_ids;
-            key = g.ids[t * g.ids_stride + e];
-            if (key < 0 || key >= g.n_bins) key = -1;
-        }
-        uint64_t pending = __ballot(key >= 0);
-        while (pending) {
-            const int leader = __ffsll((unsigned long long) pending) - 1;
-            const int k = __shfl(key, leader);
-            const uint64_t m = __ballot(key == k);
+    // phase C: stable scatter of (e, t) pairs: the first lane of each key takes
+    // the chunk's positions from the slice cursor, the others offset by rank
+    for (int c = f0; c < f1; c += GROUP_UNROLL * 64) {
+        int t[GROUP_UNROLL], e[GROUP_UNROLL], key[GROUP_UNROLL];
+#pragma unroll
+        for (int u = 0; u < GROUP_UNROLL; ++u) key[u] = pair_key(g, c + 64 * u + lane, f1, t[u], e[u], false);
+#pragma unroll
+        for (int u = 0; u < GROUP_UNROLL; ++u) {
+            const ChunkRank r = chunk_rank(key[u], nbits);
             int32_t base = 0;
-            if (lane == leader) base = hist_add<IN_LDS>(hist + k, (int32_t) __popcll(m));
-            base = __shfl(base, leader);
-            if (key == k) {
-                const int32_t pos = base + __popcll(m & lanemask_lt());
-                g.rows[2 * pos] = (int32_t) e;
-                g.rows[2 * pos + 1] = (int32_t) t;
+            if (key[u] >= 0 && r.rank == 0) base = hist_add<IN_LDS>(hist + key[u], r.cnt);
+            base = __shfl(base, r.first & 63);
+            if (key[u] >= 0) {
+                const int32_t pos = base + r.rank;
+                g.rows[2 * pos] = (int32_t) e[u];
+                g.rows[2 * pos + 1] = (int32_t) t[u];
             }
-            pending &= ~m;
         }
     }
 }
 
 int launch_group(const GroupArgs& g, hipStream_t stream) {
-    if (g.n_bins <= 0) return -2;
+    if (g.n_bins <= 0 || g.n_bins >= (int64_t(1) << 30) || g.n_ids <= 0 || g.T < 0 || g.T * g.n_ids >= (int64_t(1) << 31))
+        return -2;
     if (g.n_bins <= GROUP_LDS_BINS) hipLaunchKernelGGL(k_group<true>, dim3(1), dim3(GROUP_WAVES * 64), 0, stream, g);
     else hipLaunchKernelGGL(k_group<false>, dim3(1), dim3(GROUP_WAVES * 64), 0, stream, g);
     return hipGetLastError() == hipSuccess ? 0 : -3;

@@ -44,7 +44,7 @@ struct GroupArgs {
     int32_t* status;      // bit 1 set on an out-of-range id
     int32_t* hist_ws;     // workspace: GROUP_WAVES * n_bins ints
 };
-constexpr int GROUP_WAVES = 8;
+constexpr int GROUP_WAVES = 16;
 int launch_group(const GroupArgs& g, hipStream_t stream);
 
 struct MmidArgs {

@@ -178,13 +178,18 @@ def test_mul_mat_id_bad_id_sets_status(orc):
 
 # ---------------------------------------------------------------- grouping
 
-@pytest.mark.parametrize("T,k,n_as", [(1, 8, 128), (5, 8, 128), (512, 8, 128), (1024, 8, 128), (3, 2, 5000)])
-def test_group_by_expert(orc, T, k, n_as):
-    note(f"group_by_expert T={T} k={k} n_as={n_as}")
+@pytest.mark.parametrize("T,k,n_as,dup", [(1, 8, 128, False), (5, 8, 128, False), (512, 8, 128, False),
+                                          (1024, 8, 128, False), (4096, 8, 128, False), (3, 2, 5000, False),
+                                          (700, 6, 1500, False), (333, 7, 3, True), (257, 5, 64, True)])
+def test_group_by_expert(orc, T, k, n_as, dup):
+    """Stable grouping (token outer, slot inner) bit-exact; dup routes one token to
+    the same matrix several times, as ggml_mul_mat_id allows, so one 64-pair chunk
+    holds long runs of equal keys; n_as above 1024 keeps the counters in global memory."""
+    note(f"group_by_expert T={T} k={k} n_as={n_as} dup={dup}")
     rng = np.random.default_rng(T + n_as)
     p = np.arange(1, n_as + 1, dtype=np.float64) ** -1.1
     p /= p.sum()
-    ids = np.stack([rng.choice(n_as, k, replace=False, p=p) for _ in range(T)]).astype(np.int32)
+    ids = np.stack([rng.choice(n_as, k, replace=dup, p=p) for _ in range(T)]).astype(np.int32)
     cnt, off, rows = (host(x) for x in ops.group_by_expert(dev(ids), n_as))
     c2, o2, r2 = orc.group_by_expert(ids, n_as)
     assert np.array_equal(cnt, c2)
