@@ -32,6 +32,9 @@ constexpr int DEC_WAVES = DEC_THREADS / 64;
 constexpr long DEC_SPIN_LIMIT = 1L << 22;   // ~seconds: a stuck wait abandons the launch
 constexpr int MAXJ_A = 8;                    // 16-byte gate/up chunks per thread per round
 constexpr int MAXJ_B = 4;                    // 16-byte down chunks held per thread
+constexpr int TOPK_TPV = 4;                  // lanes ranking one logit
+constexpr int LAYER_WORDS = sizeof(DecodeLayer) / 8;
+static_assert(sizeof(DecodeLayer) % 8 == 0, "layer descriptors are copied as 64-bit words");
 
 struct DecodeArgs {
     const DecodeLayer* layers;
@@ -180,6 +183,17 @@ __device__ void quant_q8K_lds16(uint32_t* lds, const float* src, int nblocks, ui
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(1))) const u32x4 g_u32x4;
 __device__ __forceinline__ u32x4 ldg16(const void* p) { return *(g_u32x4*) p; }
+// After a gather the polls were this thread's newest loads and have returned,
+// so every older load has too.  Saying so (at a point every thread reaches)
+// keeps the compiler's per-register load tracking from carrying loads whose use
+// was conditional into later code, where it would wait for every load since.
+__device__ __forceinline__ void loads_returned() { __builtin_amdgcn_s_waitcnt(0x0F70); }   // vmcnt(0)
+__device__ __forceinline__ uint64_t ldg_u64(const uint64_t* p) {
+    return *(const __attribute__((address_space(1))) uint64_t*) p;
+}
+__device__ __forceinline__ int32_t ldg_i32(const int32_t* p) {
+    return *(const __attribute__((address_space(1))) int32_t*) p;
+}
 __device__ __forceinline__ void sts16(uint32_t* lds, uint32_t byte_off, u32x4 v) {
     *(u32x4*) ((uint8_t*) lds + byte_off) = v;
 }
@@ -209,7 +223,11 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
     __shared__ const uint8_t* s_rowA[96];
     __shared__ const uint8_t* s_rowB[256];
     __shared__ SortRange s_stack[SORT_STACK];
+    __shared__ int32_t s_spec[32];
+    __shared__ uint64_t s_L[2][LAYER_WORDS];   // descriptors of layers l (slot l & 1) and l + 1
     __shared__ int s_need_sort;
+    __shared__ int s_bad;
+    __shared__ int s_reload;
     __shared__ int s_fail;
 
     const int b = blockIdx.x, tid0 = threadIdx.x;
@@ -235,14 +253,18 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
 
     // ---- layer 0 input and router row ----------------------------------------
     if (tid0 == 0) s_fail = 0;
+    if (tid0 < 32) s_spec[tid0] = 0;
+    if (tid0 < 2 * LAYER_WORDS && tid0 / LAYER_WORDS < a.n_layer)
+        s_L[tid0 / LAYER_WORDS][tid0 % LAYER_WORDS] = ldg_u64((const uint64_t*) a.layers + tid0);
     for (int i = tid0; i < H; i += DEC_THREADS) xs[i] = a.x_in[i];
     if (b < E)
         for (int c = tid0; c < H / 4; c += DEC_THREADS)
             sts16(lds, a.lds_rw + 16u * c, ldg16(a.layers[0].router + (size_t) b * H + 4 * c));
     lds_barrier();
+    loads_returned();   // (each was stored to LDS above)
 
     for (int l = 0; l < a.n_layer; ++l) {
-        const DecodeLayer& L = a.layers[l];
+        const DecodeLayer& L = *(const DecodeLayer*) s_L[l & 1];
         const uint32_t ep = a.epoch0 + (uint32_t) l;
         const int tid = opaque(tid0);   // per-thread addresses are rebuilt every layer
         const int wave = tid >> 6, lane = tid & 63;
@@ -251,8 +273,22 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
             // lanes 0..31 = the 32 fma chains of the AVX2 ggml_vec_dot_f32 (H % 32 == 0)
             const float* w = (const float*) ((uint8_t*) lds + a.lds_rw + (uint32_t) (l & 1) * (uint32_t) H * 4u);
             float acc = 0.0f;
-            if (lane < 32)
-                for (int s = 0; s < H; s += 32) acc = __builtin_fmaf(w[s + lane], xs[s + lane], acc);
+            if (lane < 32) {
+                // the chain is serial; its LDS reads are not (unrolled so they are in flight together)
+                const int Hc = NBH > 0 ? NBH * QK_K : H;
+                for (int s0 = 0; s0 < Hc; s0 += 16 * 32) {
+                    float wv[16], xv[16];
+#pragma unroll
+                    for (int u = 0; u < 16; ++u) {
+                        const int s = min(s0 + 32 * u, Hc - 32);   // (past Hc: never used)
+                        wv[u] = w[s + lane];
+                        xv[u] = xs[s + lane];
+                    }
+#pragma unroll
+                    for (int u = 0; u < 16; ++u)
+                        if (s0 + 32 * u < Hc) acc = __builtin_fmaf(wv[u], xv[u], acc);
+                }
+            }
             float t = acc + __shfl_down(acc, 16, 32);   // c_l + c_{16+l}
             t = t + __shfl_down(t, 8, 32);               // s_l = (c_l + c_{16+l}) + (c_{8+l} + c_{24+l})
             t = t + __shfl_down(t, 4, 32);               // t0_l = s_l + s_{l+4}
@@ -265,19 +301,86 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
         const bool rw_next = b < E && l + 1 < a.n_layer;
         // (loads are unconditional, from clamped addresses -- a WG without a next
         // row reads x_in, an L2 hit -- so that none of them waits for another)
-        const float* rw_src = rw_next ? a.layers[l + 1].router + (size_t) b * H : a.x_in;
+        const float* rw_src = rw_next ? ((const DecodeLayer*) s_L[(l + 1) & 1])->router + (size_t) b * H : a.x_in;
         const uint32_t rw_dst = a.lds_rw + (uint32_t) ((l + 1) & 1) * (uint32_t) H * 4u;
         const bool rw0 = rw_next && tid < H / 4, rw1 = rw_next && tid + DEC_THREADS < H / 4;
         const u32x4 rwv0 = ldg16(rw_src + 4 * min(tid, H / 4 - 1));
-        u32x4 rwv1 = rwv0;
-        if (H / 4 > DEC_THREADS) rwv1 = ldg16(rw_src + 4 * min(tid + DEC_THREADS, H / 4 - 1));
-        // ---- softmax and exact top-k (every WG) ----------------------------------
+        const u32x4 rwv1 = ldg16(rw_src + 4 * min(tid + DEC_THREADS, H / 4 - 1));
+        // ---- top-k (every WG) -----------------------------------------------------
+        // The order by logit (ties by index) is the order by probability unless the
+        // softmax rounds two of the first k + 1 places together.  The gate/up rows of
+        // that order are loaded while the softmax runs; the exact order is then
+        // checked against it and, on a difference, the rows are loaded again.
         gather_tagged<1>(a, a.xl, E, ep, s_p, &s_fail);
         if (rw0) sts16(lds, rw_dst + 16u * tid, rwv0);
         if (rw1) sts16(lds, rw_dst + 16u * (tid + DEC_THREADS), rwv1);
-        if (tid == 0) s_need_sort = 0;
+        if (tid == 0) {
+            s_need_sort = 0;
+            s_bad = 0;
+            s_reload = 0;
+        }
         lds_barrier();
         if (s_fail) return;
+        loads_returned();
+        // logit ranks: rank = number of strictly larger logits, TOPK_TPV lanes per
+        // value, lane sub taking the float4 groups c = sub (mod TOPK_TPV).  Equal
+        // logits share a rank, so the losing one fails the check below, as does a
+        // NaN; either sends the layer to the exact order.  E % 8 == 0, so the groups
+        // of a lane come in whole batches of 8 when E % 128 == 0 (else clamped).
+        // (s_order holds rank[i] until the check.)
+        for (int i0 = 0; i0 < E; i0 += DEC_THREADS / TOPK_TPV) {
+            const int i = i0 + tid / TOPK_TPV, sub = tid % TOPK_TPV;
+            const float li = s_p[i < E ? i : 0];
+            int rank = 0;
+            for (int c0 = sub; c0 < E / 4; c0 += 8 * TOPK_TPV) {
+                float4 q[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) q[u] = *(const float4*) (s_p + 4 * min(c0 + u * TOPK_TPV, E / 4 - 1));
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int gt = (q[u].x > li) + (q[u].y > li) + (q[u].z > li) + (q[u].w > li);
+                    rank += c0 + u * TOPK_TPV < E / 4 ? gt : 0;   // (a clamped repeat counts 0)
+                }
+            }
+#pragma unroll
+            for (int o = 1; o < TOPK_TPV; o <<= 1) rank += __shfl_xor(rank, o);
+            if (i < E && sub == 0) {
+                s_order[i] = rank;
+                if (rank < k) s_spec[rank] = i;
+                if (li != li) s_bad = 1;
+            }
+        }
+        lds_barrier();
+        // gate/up rows of the speculative experts: one round of loads, in flight
+        // through the softmax (a slot that does not map is read as slot 0 here and
+        // reported below only if the expert is really selected)
+        const bool spec = nA > 0 && nA <= MAXJ_A * DEC_THREADS;
+        auto table_a = [&](const int32_t* ids, bool report) {
+            for (int r = tid; r < 2 * np; r += DEC_THREADS) {
+                const int p = pa0 + (r >> 1);
+                const int i = p / F, f = p % F;
+                const int e = ids[i];
+                const bool up = r & 1;
+                const int32_t* so = up ? L.slot_up : L.slot_gate;
+                int64_t mat = so ? ldg_i32(so + e) : e;
+                if (mat < 0 || mat >= (up ? L.n_slots_up : L.n_slots_gate)) {
+                    if (report) atomicOr(a.status, 16);
+                    mat = 0;
+                }
+                s_rowA[r] = (up ? L.up : L.gate) + (size_t) mat * (up ? L.up_nb2 : L.gate_nb2) +
+                            (size_t) f * (up ? L.up_nb1 : L.gate_nb1);
+            }
+        };
+        u32x4 t[MAXJ_A];
+        if (spec) {
+            table_a(s_spec, false);
+            lds_barrier();
+#pragma unroll
+            for (int j = 0; j < MAXJ_A; ++j) {
+                const int c = min(tid + j * DEC_THREADS, nA - 1);
+                t[j] = ldg16(s_rowA[c / chA] + 16 * (c % chA));
+            }
+        }
         {
             // ggml_soft_max (ggml-cpu/ops.cpp): max, ggml_vec_soft_max_f32 (exp in
             // AVX2 groups of 8, double sum), scale by 1/sum
@@ -298,36 +401,54 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
             const float inv = (float) (1.0 / sum);
             for (int i = tid; i < E; i += DEC_THREADS) s_p[i] = s_e[i] * inv;
             lds_barrier();
-            // argsort (descending) by ranks: with no value tied (or unordered)
-            // inside the first k places the order is unique; otherwise std::sort's
-            // own tie order decides -> exact replay below
-            for (int i = tid; i < E; i += DEC_THREADS) {
-                const float pi = s_p[i];
-                int gt = 0, eq = 0;
-#pragma unroll 4
-                for (int j = 0; j < E; j += 4) {
-                    const float4 q = *(const float4*) (s_p + j);
-                    gt += (q.x > pi) + (q.y > pi) + (q.z > pi) + (q.w > pi);
-                    eq += (q.x == pi) + (q.y == pi) + (q.z == pi) + (q.w == pi);
-                }
-                if (gt < k) {
-                    if (eq != 1) s_need_sort = 1;
-                    else s_order[gt] = i;
+            // The speculative order is the exact argsort's first k iff its
+            // probabilities strictly decrease and every other one is strictly
+            // below the k-th (then no tie or NaN can reorder them).
+            {
+                const float q = s_p[s_spec[k - 1]];
+                for (int i = tid; i < E; i += DEC_THREADS) {
+                    const int r = s_order[i];
+                    const float pi = s_p[i];
+                    const bool ok = r >= k ? (pi < q) : (s_spec[r] == i && (r == 0 || s_p[s_spec[r - 1]] > pi));
+                    if (!ok) s_bad = 1;
                 }
             }
             lds_barrier();
-            if (s_need_sort) {
-                if (tid == 0) {
-                    for (int i = 0; i < E; ++i) s_order[i] = i;
-                    libstdcxx_sort_desc(s_order, E, s_p, s_stack);
-                    if (b == 0) atomicOr(a.status, 1);
+            if (!s_bad) {
+                if (tid < k) s_order[tid] = s_spec[tid];
+            } else {
+                // argsort (descending) by ranks: with no value tied (or unordered)
+                // inside the first k places the order is unique; otherwise std::sort's
+                // own tie order decides -> exact replay below
+                for (int i = tid; i < E; i += DEC_THREADS) {
+                    const float pi = s_p[i];
+                    int gt = 0, eq = 0;
+#pragma unroll 4
+                    for (int j = 0; j < E; j += 4) {
+                        const float4 q = *(const float4*) (s_p + j);
+                        gt += (q.x > pi) + (q.y > pi) + (q.z > pi) + (q.w > pi);
+                        eq += (q.x == pi) + (q.y == pi) + (q.z == pi) + (q.w == pi);
+                    }
+                    if (gt < k) {
+                        if (eq != 1) s_need_sort = 1;
+                        else s_order[gt] = i;
+                    }
                 }
                 lds_barrier();
+                if (s_need_sort) {
+                    if (tid == 0) {
+                        for (int i = 0; i < E; ++i) s_order[i] = i;
+                        libstdcxx_sort_desc(s_order, E, s_p, s_stack);
+                        if (b == 0) atomicOr(a.status, 1);
+                    }
+                }
             }
+            lds_barrier();
             if (tid < k) {
                 const int id = s_order[tid];
                 s_ids[tid] = id;
                 s_e[tid] = s_p[id];
+                if (id != s_spec[tid]) s_reload = 1;
             }
             lds_barrier();
             // weights: selected probabilities / clamp(sum) (* scale)
@@ -345,44 +466,48 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
                 }
             }
         }
-        // ---- row addresses of this WG's gate/up pairs and down rows -------------
-        for (int r = tid; r < 2 * np; r += DEC_THREADS) {
-            const int p = pa0 + (r >> 1);
-            const int i = p / F, f = p % F;
-            const int e = s_ids[i];
-            const bool up = r & 1;
-            const int32_t* so = up ? L.slot_up : L.slot_gate;
-            int64_t mat = so ? so[e] : e;
-            if (mat < 0 || mat >= (up ? L.n_slots_up : L.n_slots_gate)) {
-                atomicOr(a.status, 16);
-                mat = 0;
-            }
-            s_rowA[r] = (up ? L.up : L.gate) + (size_t) mat * (up ? L.up_nb2 : L.gate_nb2) +
-                        (size_t) f * (up ? L.up_nb1 : L.gate_nb1);
-        }
+        // ---- down row addresses; slot checks of the selected experts ------------
         for (int r = tid; r < k * nh; r += DEC_THREADS) {
             const int i = r / nh, hh = r % nh;
             const int e = s_ids[i];
-            int64_t mat = L.slot_down ? L.slot_down[e] : e;
+            int64_t mat = L.slot_down ? ldg_i32(L.slot_down + e) : e;
             if (mat < 0 || mat >= L.n_slots_down) {
                 atomicOr(a.status, 16);
                 mat = 0;
             }
             s_rowB[r] = L.down + (size_t) mat * L.down_nb2 + (size_t) (h0 + hh) * L.down_nb1;
         }
-        lds_barrier();
-        // ---- gate/up rows to LDS: every load of a round in flight at once --------
-        for (int base = 0; base < nA; base += MAXJ_A * DEC_THREADS) {
-            u32x4 t[MAXJ_A];
+        const bool reload = !spec || s_reload;
+        if (!reload && tid < 2 * k) {   // the gate/up table was built without reporting
+            const int e = s_ids[tid >> 1];
+            const bool up = tid & 1;
+            const int32_t* so = up ? L.slot_up : L.slot_gate;
+            const int64_t mat = so ? ldg_i32(so + e) : e;
+            if (mat < 0 || mat >= (up ? L.n_slots_up : L.n_slots_gate)) atomicOr(a.status, 16);
+        }
+        // ---- gate/up rows to LDS --------------------------------------------------
+        if (!reload) {
 #pragma unroll
             for (int j = 0; j < MAXJ_A; ++j) {
-                const int c = min(base + tid + j * DEC_THREADS, nA - 1);
-                t[j] = ldg16(s_rowA[c / chA] + 16 * (c % chA));
-            }
-#pragma unroll
-            for (int j = 0; j < MAXJ_A; ++j) {
-                const int c = base + tid + j * DEC_THREADS;
+                const int c = tid + j * DEC_THREADS;
                 if (c < nA) sts16(lds, a.lds_a + (uint32_t) (c / chA) * a.rs_a + 16u * (c % chA), t[j]);
+            }
+        } else {
+            table_a(s_ids, true);
+            lds_barrier();
+            // every load of a round in flight at once
+            for (int base = 0; base < nA; base += MAXJ_A * DEC_THREADS) {
+                u32x4 t2[MAXJ_A];
+#pragma unroll
+                for (int j = 0; j < MAXJ_A; ++j) {
+                    const int c = min(base + tid + j * DEC_THREADS, nA - 1);
+                    t2[j] = ldg16(s_rowA[c / chA] + 16 * (c % chA));
+                }
+#pragma unroll
+                for (int j = 0; j < MAXJ_A; ++j) {
+                    const int c = base + tid + j * DEC_THREADS;
+                    if (c < nA) sts16(lds, a.lds_a + (uint32_t) (c / chA) * a.rs_a + 16u * (c % chA), t2[j]);
+                }
             }
         }
         lds_barrier();
@@ -434,6 +559,7 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
         }
         lds_barrier();
         if (s_fail) return;
+        loads_returned();
         quant_q8K_lds16(lds, actf, k * nbF, a.lds_aq);
         lds_barrier();
         for (int r0 = 0; r0 < k * nh; r0 += DEC_WAVES * 8) {
@@ -464,10 +590,16 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
             }
             st_dev64(a.xy + h0 + hh, tagged(sumf, ep));
         }
+        // the descriptor of layer l + 2 replaces this layer's (its loads return
+        // before the y polls that follow them)
+        const bool next2 = l + 2 < a.n_layer && tid < LAYER_WORDS;
+        const uint64_t lw = ldg_u64((const uint64_t*) (a.layers + (next2 ? l + 2 : l)) + (tid % LAYER_WORDS));
         // ---- C: all y -> RMSNorm -> x of the next layer ----------------------------
         gather_tagged<4>(a, a.xy, H, ep, ys, &s_fail);
+        if (next2) s_L[l & 1][tid] = lw;
         lds_barrier();
         if (s_fail) return;
+        loads_returned();
         {
             double s = 0.0;
             for (int i = tid; i < H; i += DEC_THREADS) {

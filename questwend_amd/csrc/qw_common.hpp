@@ -102,6 +102,8 @@ __device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, int& d, in
 }
 
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+// a * b for |a|, |b| < 2^23 (v_mul_i32_i24, full rate; a 32-bit multiply is quarter rate)
+__device__ __forceinline__ int mul24(int a, int b) { return __mul24(a, b); }
 
 // DPP lane exchanges inside a row of 16 lanes (VALU latency, no LDS round trip).
 // xor1 / xor2 are exact lane-xor patterns; half_mirror (i <-> 7-i in each 8) and

@@ -43,7 +43,7 @@ __device__ __forceinline__ float row_dot_lds<T_Q4_K>(const uint32_t* lds, uint32
             const int lo = (int) (wq & 0x0F0F0F0Fu), hi = (int) ((wq >> 4) & 0x0F0F0F0Fu);
             const int alo = (int) lds_u32(lds, yb + 4 + 64 * j + 4 * n);
             const int ahi = (int) lds_u32(lds, yb + 4 + 64 * j + 32 + 4 * n);
-            sumi += sc[2 * j] * sdot4(lo, alo, 0) + sc[2 * j + 1] * sdot4(hi, ahi, 0);
+            sumi += mul24(sc[2 * j], sdot4(lo, alo, 0)) + mul24(sc[2 * j + 1], sdot4(hi, ahi, 0));
         }
         const float yd = lds_f32(lds, yb);
         const float d = yd * h2f((uint16_t) (h0 & 0xffff));
@@ -52,7 +52,7 @@ __device__ __forceinline__ float row_dot_lds<T_Q4_K>(const uint32_t* lds, uint32
             const uint32_t bs01 = lds_u32(lds, yb + 260 + 8 * n), bs23 = lds_u32(lds, yb + 260 + 8 * n + 4);
             const int q8s0 = (int) (int16_t) (bs01 & 0xffff) + (int) (int16_t) (bs01 >> 16);
             const int q8s1 = (int) (int16_t) (bs23 & 0xffff) + (int) (int16_t) (bs23 >> 16);
-            const int prod = mn[2 * n] * q8s0 + mn[2 * n + 1] * q8s1;
+            const int prod = mul24(mn[2 * n], q8s0) + mul24(mn[2 * n + 1], q8s1);
             const float dmin = -yd * h2f((uint16_t) (h0 >> 16));
             accm = __builtin_fmaf(dmin, (float) prod, accm);
         }
@@ -95,7 +95,7 @@ __device__ __forceinline__ float row_dot_q4k_a(const uint32_t* lds, uint32_t wba
             const int sh = (int) ((scw >> (16 * (j & 1) + 8)) & 0xff);
             const uint32_t wq = blk[4 + 8 * j + n];
             const int lo = (int) (wq & 0x0F0F0F0Fu), hi = (int) ((wq >> 4) & 0x0F0F0F0Fu);
-            sumi += sl * sdot4(lo, (int) yb[1 + 16 * j + n], 0) + sh * sdot4(hi, (int) yb[1 + 16 * j + 8 + n], 0);
+            sumi += mul24(sl, sdot4(lo, (int) yb[1 + 16 * j + n], 0)) + mul24(sh, sdot4(hi, (int) yb[1 + 16 * j + 8 + n], 0));
         }
         const float yd = bitsf(yb[0]);
         acc = __builtin_fmaf(yd * h2f((uint16_t) (h0 & 0xffff)), (float) sumi, acc);
@@ -105,7 +105,7 @@ __device__ __forceinline__ float row_dot_q4k_a(const uint32_t* lds, uint32_t wba
             const int q8s1 = (int) (int16_t) (bs23 & 0xffff) + (int) (int16_t) (bs23 >> 16);
             const uint32_t mw = n < 2 ? mn_lo : mn_hi;
             const int m0 = (int) ((mw >> (16 * (n & 1))) & 0xff), m1 = (int) ((mw >> (16 * (n & 1) + 8)) & 0xff);
-            accm = __builtin_fmaf(-yd * h2f((uint16_t) (h0 >> 16)), (float) (m0 * q8s0 + m1 * q8s1), accm);
+            accm = __builtin_fmaf(-yd * h2f((uint16_t) (h0 >> 16)), (float) (mul24(m0, q8s0) + mul24(m1, q8s1)), accm);
         }
     }
     float a = acc;
@@ -143,10 +143,10 @@ __device__ __forceinline__ float row_dot_lds<T_Q6_K>(const uint32_t* lds, uint32
             const int q2 = (int) (((qa >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u));
             const int q3 = (int) (((qb >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u));
             const uint32_t y = yb + 4 + 128 * j + 4 * n;
-            sumi += sc[8 * j + 0 + g] * sdot4(q0, (int) lds_u32(lds, y), 0);
-            sumi += sc[8 * j + 2 + g] * sdot4(q1, (int) lds_u32(lds, y + 32), 0);
-            sumi += sc[8 * j + 4 + g] * sdot4(q2, (int) lds_u32(lds, y + 64), 0);
-            sumi += sc[8 * j + 6 + g] * sdot4(q3, (int) lds_u32(lds, y + 96), 0);
+            sumi += mul24(sc[8 * j + 0 + g], sdot4(q0, (int) lds_u32(lds, y), 0));
+            sumi += mul24(sc[8 * j + 2 + g], sdot4(q1, (int) lds_u32(lds, y + 32), 0));
+            sumi += mul24(sc[8 * j + 4 + g], sdot4(q2, (int) lds_u32(lds, y + 64), 0));
+            sumi += mul24(sc[8 * j + 6 + g], sdot4(q3, (int) lds_u32(lds, y + 96), 0));
         }
         const uint32_t bs = lds_u32(lds, yb + 260 + 4 * n);
         sumi -= 32 * ((int) (int16_t) (bs & 0xffff) * sc[2 * n] + (int) (int16_t) (bs >> 16) * sc[2 * n + 1]);

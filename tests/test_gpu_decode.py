@@ -50,10 +50,12 @@ class GpuLayer:
     """One layer's synthetic weights generated and quantized on the GPU, plus a
     host copy of the same bytes in the oracle's LayerWeights form."""
 
-    def __init__(self, H, E, k, F, types, seed, permute=False):
+    def __init__(self, H, E, k, F, types, seed, permute=False, dup_router=False):
         tg, tu, td = types
         self.router = torch.empty((E, H), dtype=torch.float32, device=DEV)
         ops.randn_(self.router, seed * 10 + 1, 0.0, 0.02)
+        if dup_router:   # experts 2j and 2j+1 get equal logits: every top-k has ties
+            self.router[1::2] = self.router[0::2]
         mats = []
         tmp = torch.empty(E * F * H, dtype=torch.float32, device=DEV)
         for j, (t, rows, cols) in enumerate(((tg, F, H), (tu, F, H), (td, H, F))):
@@ -125,6 +127,18 @@ def test_decode_stack_q6k_down_permuted_slots(orc):
     layers = [GpuLayer(1024, 16, 8, 512, (Q4_K, Q4_K, Q6_K), seed=500 + i, permute=True) for i in range(2)]
     rng = np.random.default_rng(2)
     run_and_compare(orc, layers, [rng.standard_normal(1024).astype(np.float32) for _ in range(2)])
+
+
+def test_decode_stack_router_ties(orc):
+    """Router rows equal in pairs: every layer's probabilities tie in pairs, inside
+    the first k places and (k odd) across the k-th place, so the kernel's
+    speculative order (by logit, ties by index) fails its check and the exact
+    order comes from the std::sort replay; where that order differs from the
+    speculative one the gate/up rows are loaded again."""
+    note("decode stack: tied router logits, 3 layers H=1024 E=16 k=3 F=512, 3 tokens")
+    layers = [GpuLayer(1024, 16, 3, 512, (Q4_K,) * 3, seed=700 + i, dup_router=True) for i in range(3)]
+    rng = np.random.default_rng(3)
+    run_and_compare(orc, layers, [rng.standard_normal(1024).astype(np.float32) for _ in range(3)])
 
 
 def test_decode_stack_equals_per_layer_path():
