@@ -27,8 +27,6 @@
 // v_mfma_i32_16x16x64_i8 over the 64 positions of sub-blocks 2m and 2m+1 with
 // every A byte equal to that sub-block's min.  20 MFMAs per 16 x 16 tile and
 // super-block.
-#include <algorithm>
-
 #include "qw_kernels.hpp"
 
 namespace qw {
@@ -45,19 +43,24 @@ constexpr int MF_ACH = (MF_N * 65 + 255) / 256;   // activation dwords per threa
 
 __device__ __forceinline__ long pack2(uint32_t lo, uint32_t hi) { return (long) (((uint64_t) hi << 32) | lo); }
 
-// Workgroup (row tile x, active expert y, pass z): weight rows r0 .. r0 + 63 of the
-// expert's matrix against its routed activation rows 16 z .. 16 z + 15.  Super-block
-// i + 1 is loaded into registers while super-block i is computed from LDS.
+// Workgroup b = (active expert g, row tile): weight rows r0 .. r0 + 63 of the
+// expert's matrix against all its routed activation rows, 16 per pass.  Super-
+// block i + 1 is loaded into registers while super-block i is computed from LDS.
+// One workgroup walks all passes of its tile, so the workgroups in flight hold
+// distinct tiles and a tile's re-reads come from the caches of its CU.  (Measured
+// on the T=512 30B layer: 117 us per projection; one workgroup per pass: 124 us
+// with 2.6x the weight bytes fetched; a tile's passes placed on one XCD: 202 us.)
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) k_mmid_mfma_q4k(MmidArgs m) {
     __shared__ __align__(16) uint8_t s_w[2][MF_M * MF_WS];
     __shared__ __align__(16) uint8_t s_a[2][MF_N * MF_AS];
     __shared__ int32_t s_arow[MF_N];
     __shared__ int32_t s_et[MF_N][2];
-    const int g = blockIdx.y;
+    const int tiles = (int) (m.N / MF_M);
+    const int tile = (int) (blockIdx.x % (uint32_t) tiles);
+    const int g = (int) (blockIdx.x / (uint32_t) tiles);
     if (g >= *m.n_active) return;
     const int p0 = m.active_off[g], p1 = m.active_off[g + 1];
     if (p1 - p0 < m.mfma_min_rows) return;   // light expert: the GEMV kernel's
-    if (p0 + MF_N * (int) blockIdx.z >= p1) return;
     const int bin = m.active[g];
     int64_t mat = bin;
     if (m.slot_of) mat = (bin < m.n_slot_of) ? m.slot_of[bin] : -1;
@@ -65,13 +68,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
         if (threadIdx.x == 0 && m.status) atomicOr(m.status, 4);
         return;
     }
-    const int64_t r0 = (int64_t) blockIdx.x * MF_M;
+    const int64_t r0 = (int64_t) tile * MF_M;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int lr = lane & 15, gq = lane >> 4;   // A row / B row within the tile; k-slot group
     const int nb = (int) (m.K / QK_K);
     const uint8_t* wtile = m.w + (size_t) mat * m.nb2 + (size_t) r0 * m.nb1;
     const int arow_l = 16 * wave + lr;          // this lane's A row in the staged tile
-    for (int pass = blockIdx.z;; pass += gridDim.z) {
+    for (int pass = 0;; ++pass) {
     const int pc = p0 + MF_N * pass;
     if (pc >= p1) break;
     const int ntok = (p1 - pc) < MF_N ? (p1 - pc) : MF_N;
@@ -217,13 +220,12 @@ bool mmid_mfma_supported(const MmidArgs& m) {
 
 int launch_mmid_mfma(const MmidArgs& m, hipStream_t stream) {
     if (!mmid_mfma_supported(m)) return -2;
-    // passes of 16 rows (an expert receives at most max_rows rows); workgroup z
-    // takes passes z, z + gridDim.z, ...
-    const int64_t passes = (m.max_rows + MF_N - 1) / MF_N;
-    const unsigned gz = (unsigned) std::min<int64_t>(std::max<int64_t>(passes, 1), 16);
-    dim3 grid((unsigned) (m.N / MF_M), (unsigned) m.max_active, gz);
-    if (grid.y == 0) return 0;
-    hipLaunchKernelGGL(k_mmid_mfma_q4k, grid, dim3(256), 0, stream, m);
+    // one workgroup per (active expert, row tile)
+    const int64_t groups = m.max_active * (m.N / MF_M);
+    if (groups == 0) return 0;
+    if (groups > (int64_t(1) << 30)) return -2;
+    const unsigned grid = (unsigned) groups;
+    hipLaunchKernelGGL(k_mmid_mfma_q4k, dim3(grid), dim3(256), 0, stream, m);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
