@@ -43,6 +43,20 @@ constexpr int MF_ACH = (MF_N * 65 + 255) / 256;   // activation dwords per threa
 
 __device__ __forceinline__ long pack2(uint32_t lo, uint32_t hi) { return (long) (((uint64_t) hi << 32) | lo); }
 
+// Byte-wise products of four bytes b (each <= 15) with s (<= 7), as one packed
+// 16-bit multiply: each half holds b0 + 256 b1 and b0 s < 256 never carries.
+typedef unsigned short u16x2m __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t mul_bytes(uint32_t b, uint32_t s) {
+    const u16x2m ss = {(unsigned short) s, (unsigned short) s};
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2m, b) * ss);
+}
+
+// Raw buffer resource over [base, base + bytes): 32-bit offsets, loads past the
+// end return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short) 0, (int) bytes, 0x00020000);
+}
+
 // Workgroup b = (active expert g, row tile): weight rows r0 .. r0 + 63 of the
 // expert's matrix against all its routed activation rows, 16 per pass.  Super-
 // block i + 1 is loaded into registers while super-block i is computed from LDS.
@@ -73,6 +87,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int lr = lane & 15, gq = lane >> 4;   // A row / B row within the tile; k-slot group
     const int nb = (int) (m.K / QK_K);
     const uint8_t* wtile = m.w + (size_t) mat * m.nb2 + (size_t) r0 * m.nb1;
+    const __amdgpu_buffer_rsrc_t wrsrc = buffer_rsrc(wtile, (uint32_t) (MF_M * m.nb1));
+    const __amdgpu_buffer_rsrc_t arsrc = buffer_rsrc(m.act_q, 0x7fffffffu);
     const int arow_l = 16 * wave + lr;          // this lane's A row in the staged tile
     for (int pass = 0;; ++pass) {
     const int pc = p0 + MF_N * pass;
@@ -88,42 +104,43 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
     lds_barrier();
 
-    // staging: this thread's weight chunks and activation dwords of super-block i
+    // staging: this thread's weight chunks and activation dwords of super-block i,
+    // through buffer loads (32-bit offsets from a uniform base; a load past the
+    // buffer's end returns zeros instead of reading out of bounds).  Offsets and
+    // LDS destinations are fixed for the pass; a super-block adds i * 144 / i * 292.
+    uint32_t woff[MF_WCH], wdst[MF_WCH], aoff[MF_ACH], adst[MF_ACH];
+#pragma unroll
+    for (int j = 0; j < MF_WCH; ++j) {
+        const int z = tid + 256 * j;
+        const int zc = min(z, MF_M * 9 - 1);
+        const int r = zc / 9, c = zc - r * 9;
+        woff[j] = (uint32_t) r * (uint32_t) m.nb1 + 16u * (uint32_t) c;
+        wdst[j] = z < MF_M * 9 ? (uint32_t) (r * MF_WS + 16 * c) : 0xffffffffu;
+    }
+#pragma unroll
+    for (int j = 0; j < MF_ACH; ++j) {
+        const int z = tid + 256 * j;
+        const int zc = min(z, ntok * 65 - 1);
+        const int n = zc / 65, c = zc - n * 65;
+        aoff[j] = (uint32_t) s_arow[n] * (uint32_t) m.act_row_bytes + 4u * (uint32_t) c;
+        adst[j] = z < ntok * 65 ? (uint32_t) (n * MF_AS + (c == 0 ? 0 : 12 + 4 * c)) : 0xffffffffu;
+    }
     u32x4m wreg[MF_WCH];
     uint32_t areg[MF_ACH];
     auto load = [&](int i) {
 #pragma unroll
-        for (int j = 0; j < MF_WCH; ++j) {
-            const int z = min(tid + 256 * j, MF_M * 9 - 1);
-            const int r = z / 9, c = z - r * 9;
-            wreg[j] = *(const __attribute__((address_space(1))) u32x4m*) (wtile + (size_t) r * m.nb1 +
-                                                                        (size_t) i * 144 + 16 * c);
-        }
+        for (int j = 0; j < MF_WCH; ++j)
+            wreg[j] = __builtin_bit_cast(u32x4m, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, woff[j] + (uint32_t) i * 144u, 0, 0));
 #pragma unroll
-        for (int j = 0; j < MF_ACH; ++j) {
-            const int z = min(tid + 256 * j, ntok * 65 - 1);
-            const int n = z / 65, c = z - n * 65;
-            const uint32_t* src = (const uint32_t*) (m.act_q + (size_t) s_arow[n] * m.act_row_bytes + (size_t) i * 292);
-            areg[j] = *(const __attribute__((address_space(1))) uint32_t*) (src + c);
-        }
+        for (int j = 0; j < MF_ACH; ++j) areg[j] = __builtin_amdgcn_raw_buffer_load_b32(arsrc, aoff[j] + (uint32_t) i * 292u, 0, 0);
     };
     auto store = [&](int buf) {
 #pragma unroll
-        for (int j = 0; j < MF_WCH; ++j) {
-            const int z = tid + 256 * j;
-            if (z < MF_M * 9) {
-                const int r = z / 9, c = z - r * 9;
-                *(u32x4m*) (s_w[buf] + r * MF_WS + 16 * c) = wreg[j];
-            }
-        }
+        for (int j = 0; j < MF_WCH; ++j)
+            if (wdst[j] != 0xffffffffu) *(u32x4m*) (s_w[buf] + wdst[j]) = wreg[j];
 #pragma unroll
-        for (int j = 0; j < MF_ACH; ++j) {
-            const int z = tid + 256 * j;
-            if (z < ntok * 65) {
-                const int n = z / 65, c = z - n * 65;
-                *(uint32_t*) (s_a[buf] + n * MF_AS + (c == 0 ? 0 : 12 + 4 * c)) = areg[j];
-            }
-        }
+        for (int j = 0; j < MF_ACH; ++j)
+            if (adst[j] != 0xffffffffu) *(uint32_t*) (s_a[buf] + adst[j]) = areg[j];
     };
 
     // per output (D register r): the eight AVX lanes and four min lanes
@@ -168,8 +185,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
         for (int L = 0; L < 8; ++L) {
             const uint32_t w = *(const uint32_t*) (sw + arow_l * MF_WS + 16 + 32 * gq + 4 * L);
             const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
-            const long a_lo = pack2(lo * (sa_ & 7u), hi * (sb_ & 7u));
-            const long a_hi = pack2(lo * (sa_ >> 3), hi * (sb_ >> 3));
+            const long a_lo = pack2(mul_bytes(lo, sa_ & 7u), mul_bytes(hi, sb_ & 7u));
+            const long a_hi = pack2(mul_bytes(lo, sa_ >> 3), mul_bytes(hi, sb_ >> 3));
             const uint8_t* ab = sa + lr * MF_AS + 16 + 64 * gq + 4 * L;
             const long bq = pack2(*(const uint32_t*) ab, *(const uint32_t*) (ab + 32));
             const v4i z4 = v4i{0, 0, 0, 0};
