@@ -24,7 +24,7 @@ pytestmark = pytest.mark.gpu
 
 torch = pytest.importorskip("torch")
 from questwend_amd import ops  # noqa: E402
-from oracle_lib import Q4_K, LayerWeights, Oracle, RefGGML, have_ref, row_size  # noqa: E402
+from oracle_lib import Q4_K, Q6_K, LayerWeights, Oracle, RefGGML, have_ref, row_size  # noqa: E402
 
 DEV = "cuda:0"
 TOL = 1e-3
@@ -220,3 +220,96 @@ def test_prefill_layer_30b_shape(orc, T):
     note(f"  output rel err {rel_err(out, r['out']):.3e}, rms_norm rel err {rel_err(xn, r['xnext']):.3e}")
     assert np.array_equal(bits(out), bits(r["out"]))
     assert rel_err(xn, r["xnext"]) < TOL
+
+
+class GpuLayerTyped:
+    """A layer of any weight types generated and quantized on the GPU, with a host
+    copy for the CPU reference.  Optional Zipf-scaled router rows skew expert
+    popularity; optional permuted slot pools (logical expert e lives in slot p[e])."""
+
+    def __init__(self, H, E, k, F, types, seed, zipf_skew=None, permute=False):
+        from oracle_lib import zipf_row_scales
+        tg, tu, td = types
+        self.router = torch.empty((E, H), dtype=torch.float32, device=DEV)
+        ops.randn_(self.router, seed * 10 + 1, 0.0, 0.02)
+        if zipf_skew is not None:
+            self.router *= dev(zipf_row_scales(E, zipf_skew))[:, None]
+        mats = []
+        tmp = torch.empty(E * F * H, dtype=torch.float32, device=DEV)
+        for j, (t, rows, cols) in enumerate(((tg, F, H), (tu, F, H), (td, H, F))):
+            ops.randn_(tmp, seed * 10 + 2 + j, 0.0, 0.02)
+            mats.append(ops.quantize_chunk(t, tmp.view(E * rows, cols)).view(E, -1))
+        del tmp
+        slots = None
+        if permute:
+            g = torch.Generator().manual_seed(seed)
+            perms = [torch.randperm(E, generator=g).to(torch.int32) for _ in range(3)]
+            pools = []
+            for m, p in zip(mats, perms):
+                pool = torch.empty_like(m)
+                pool[p.long().to(DEV)] = m
+                pools.append(pool)
+            mats = pools
+            slots = tuple(p.to(DEV) for p in perms)
+        self.mats, self.slots = mats, slots
+        self.layer = ops.make_layer(H, E, k, F, self.router, *mats, types, n_slots=(E, E, E), slots=slots)
+        torch.cuda.synchronize()
+        lw = LayerWeights.__new__(LayerWeights)
+        lw.H, lw.E, lw.k, lw.F = H, E, k, F
+        lw.type_gate, lw.type_up, lw.type_down = types
+        lw.router = self.router.cpu().numpy()
+        lw.gate, lw.up, lw.down = (m.cpu().numpy().reshape(-1) for m in mats)
+        lw.n_slots = E
+        lw.slot_of = None if slots is None else tuple(s.cpu().numpy() for s in slots)
+        self.host = lw
+
+
+C5 = (4096, 128, 8, 1536, (Q4_K, Q4_K, Q6_K))   # configs[4]: large experts, Q6_K down
+
+
+@pytest.mark.parametrize("T", [1, 5])
+def test_layer_config5_shape_permuted_slots(orc, T):
+    """configs[4] shape (H=4096, F=1536, Q4_K gate/up, Q6_K down, E=128) read
+    through permuted slot pools: ids, weights, output and RMSNorm bit-identical
+    to the oracle (whose slot handling the parity tests pin at smaller shapes)."""
+    H, E, k, F, types = C5
+    note(f"ffn_layer config-5 shape T={T}, permuted slots")
+    g = GpuLayerTyped(H, E, k, F, types, seed=900 + T, permute=True)
+    x = np.random.default_rng(T + 50).standard_normal((T, H)).astype(np.float32)
+    out, xn, ids, w = ops.ffn_layer(g.layer, dev(x), rms_eps=1e-6)
+    out, xn, ids, w = host(out), host(xn), host(ids), host(w)
+    r = orc.moe_layer(g.host, x, rms_eps=1e-6)
+    assert np.array_equal(ids, r["ids"])
+    assert np.array_equal(bits(w), bits(r["weights"]))
+    assert np.array_equal(bits(out), bits(r["out"]))
+    assert np.array_equal(bits(xn), bits(r["xnext"]))
+    assert ops.device_status(clear=True) == 0
+
+
+def test_prefill_layer_config5_shape():
+    """configs[4] prefill: T=1024 at the large-expert shape, Zipf-skewed routing.
+    Q4_K gate/up of the heavy experts run on the matrix cores, the Q6_K down on
+    the GEMV.  Against the reference ggml (16 threads) when it is built; else
+    tokens are independent, so a sample of 24 tokens is checked against the
+    oracle."""
+    H, E, k, F, types = C5
+    T = 1024
+    note(f"prefill layer config-5 shape T={T} (reference: {'ggml' if have_ref() else 'oracle, 24 tokens'})")
+    g = GpuLayerTyped(H, E, k, F, types, seed=950, zipf_skew=1.1)
+    x = np.random.default_rng(T).standard_normal((T, H)).astype(np.float32)
+    out, xn, ids, w = ops.ffn_layer(g.layer, dev(x), rms_eps=1e-6)
+    out, xn, ids, w = host(out), host(xn), host(ids), host(w)
+    counts = np.bincount(ids.reshape(-1), minlength=E)
+    note(f"  rows per expert: max {counts.max()}, experts >= 8 rows: {int((counts >= 8).sum())}")
+    assert counts.max() >= 64, "the case must route heavy experts to the matrix cores"
+    if have_ref():
+        r = RefGGML().layer(g.host, T, rms_eps=1e-6, n_threads=16)(x)
+        sel = np.arange(T)
+    else:
+        sel = np.r_[0:8, 500:508, T - 8:T]
+        r = Oracle().moe_layer(g.host, x[sel], rms_eps=1e-6)
+    assert np.array_equal(ids[sel], r["ids"])
+    assert np.array_equal(bits(w[sel]), bits(r["weights"]))
+    assert np.array_equal(bits(out[sel]), bits(r["out"]))
+    assert rel_err(xn[sel], r["xnext"]) < TOL
+    assert ops.device_status(clear=True) == 0
