@@ -206,6 +206,7 @@ int launch_group(const GroupArgs& g, hipStream_t stream) {
 
 constexpr int MMID_ROWS = 32;   // rows per workgroup (8 per wave)
 constexpr int MMID_CT = 8;      // activation rows staged per pass
+constexpr int MMID_NT = 4;      // activation rows per row-dot call
 
 __host__ __device__ inline uint32_t mmid_slot_bytes(size_t row_bytes) {
     return (uint32_t) (((row_bytes + 15 + 15) / 16) * 16 + 16);
@@ -214,6 +215,7 @@ __host__ __device__ inline uint32_t mmid_slot_bytes(size_t row_bytes) {
 template <int TYPE>
 __global__ void __launch_bounds__(256) k_mmid_gemv(MmidArgs m) {
     extern __shared__ uint32_t lds[];
+    __shared__ int s_chunk[MMID_CT][3];   // (e, t, activation row) of the staged chunk
     const int g = blockIdx.y;
     if (g >= *m.n_active) return;
     if (m.mfma_min_rows > 0 && m.active_off[g + 1] - m.active_off[g] >= m.mfma_min_rows) return;   // matrix cores take it
@@ -249,24 +251,41 @@ __global__ void __launch_bounds__(256) k_mmid_gemv(MmidArgs m) {
     const uint32_t wbase = rrow * RS + (uint32_t) ((uintptr_t) (wmat + (size_t) (r0 + rrow) * m.nb1) & 15);
     const int nb = (int) (m.K / block_elems(TYPE));
     const int p0 = m.active_off[g], p1 = m.active_off[g + 1];
+    const int nw = (int) ((m.act_row_bytes + 3) / 4);
     for (int pc = p0; pc < p1; pc += MMID_CT) {
         const int cnt = (p1 - pc) < MMID_CT ? (p1 - pc) : MMID_CT;
         __syncthreads();  // weights staged / previous chunk consumed
-        for (int tk = 0; tk < cnt; ++tk) {
-            const int e = m.rows[2 * (pc + tk)], t = m.rows[2 * (pc + tk) + 1];
-            const int64_t arow = (int64_t) (e % m.b_ne1) + (int64_t) t * m.b_ne1;
-            const uint32_t* src = (const uint32_t*) (m.act_q + (size_t) arow * m.act_row_bytes);
-            uint32_t* dst = lds + (ABASE + tk * ARS) / 4;
-            const int nw = (int) ((m.act_row_bytes + 3) / 4);
-            for (int c = threadIdx.x; c < nw; c += 256) dst[c] = src[c];
+        if (threadIdx.x < cnt) {
+            const int e = m.rows[2 * (pc + threadIdx.x)], t = m.rows[2 * (pc + threadIdx.x) + 1];
+            s_chunk[threadIdx.x][0] = e;
+            s_chunk[threadIdx.x][1] = t;
+            s_chunk[threadIdx.x][2] = (int) ((int64_t) (e % m.b_ne1) + (int64_t) t * m.b_ne1);
         }
         __syncthreads();
-        for (int tk = 0; tk < cnt; ++tk) {
-            const float v = row_dot_lds<TYPE>(lds, wbase, ABASE + tk * ARS, nb, n);
+        // all activation rows of the chunk in one cooperative pass
+        for (int idx = threadIdx.x; idx < cnt * nw; idx += 256) {
+            const int tk = idx / nw, c = idx - tk * nw;
+            const uint32_t* src = (const uint32_t*) (m.act_q + (size_t) s_chunk[tk][2] * m.act_row_bytes);
+            lds[(ABASE + tk * ARS) / 4 + c] = src[c];
+        }
+        __syncthreads();
+        // MMID_NT activation rows per row-dot call: the weight bits are unpacked
+        // once per block (rows past cnt repeat the last one and are not stored)
+        for (int tk0 = 0; tk0 < cnt; tk0 += MMID_NT) {
+            uint32_t ab[MMID_NT];
+#pragma unroll
+            for (int u = 0; u < MMID_NT; ++u) ab[u] = ABASE + (uint32_t) min(tk0 + u, cnt - 1) * ARS;
+            float v[MMID_NT];
+            row_dot_lds_mt<TYPE, MMID_NT>(lds, wbase, ab, nb, n, v);
             if (rvalid && n == 0) {
-                const int e = m.rows[2 * (pc + tk)], t = m.rows[2 * (pc + tk) + 1];
-                float* d = (float*) ((char*) m.dst + (size_t) e * m.dst_nb1 + (size_t) t * m.dst_nb2);
-                d[r0 + rl] = v;
+#pragma unroll
+                for (int u = 0; u < MMID_NT; ++u) {
+                    if (tk0 + u < cnt) {
+                        const int e = s_chunk[tk0 + u][0], t = s_chunk[tk0 + u][1];
+                        float* d = (float*) ((char*) m.dst + (size_t) e * m.dst_nb1 + (size_t) t * m.dst_nb2);
+                        d[r0 + rl] = v[u];
+                    }
+                }
             }
         }
     }

@@ -149,7 +149,7 @@ __device__ __forceinline__ float row_dot_lds<T_Q6_K>(const uint32_t* lds, uint32
             sumi += mul24(sc[8 * j + 6 + g], sdot4(q3, (int) lds_u32(lds, y + 96), 0));
         }
         const uint32_t bs = lds_u32(lds, yb + 260 + 4 * n);
-        sumi -= 32 * ((int) (int16_t) (bs & 0xffff) * sc[2 * n] + (int) (int16_t) (bs >> 16) * sc[2 * n + 1]);
+        sumi -= 32 * (mul24((int) (int16_t) (bs & 0xffff), sc[2 * n]) + mul24((int) (int16_t) (bs >> 16), sc[2 * n + 1]));
         const float d = lds_f32(lds, yb) * h2f(lds_u16(lds, blk + 208));
         acc = __builtin_fmaf(d, (float) sumi, acc);
     }
@@ -175,6 +175,155 @@ __device__ __forceinline__ float row_dot_lds<T_Q8_0>(const uint32_t* lds, uint32
     a = a + __shfl_down(a, 2, 8);
     a = a + __shfl_down(a, 1, 8);
     return a;
+}
+
+// The same row dots for NT activation rows at once: each block's weight bits
+// are unpacked once and applied to every row, and the NT chains are independent.
+// Per activation row the integers and the float sequence are those above.
+template <int TYPE, int NT>
+__device__ __forceinline__ void row_dot_lds_mt(const uint32_t* lds, uint32_t wbase, const uint32_t* abase, int nb, int n,
+                                               float* out);
+
+template <int NT>
+__device__ __forceinline__ void reduce8_mt(const float* acc, float* out) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        float a = acc[t];
+        a = a + __shfl_down(a, 4, 8);
+        a = a + __shfl_down(a, 2, 8);
+        a = a + __shfl_down(a, 1, 8);
+        out[t] = a;
+    }
+}
+
+template <>
+__device__ __forceinline__ void row_dot_lds_mt<T_Q4_K, 4>(const uint32_t* lds, uint32_t wbase, const uint32_t* abase,
+                                                          int nb, int n, float* out) {
+    constexpr int NT = 4;
+    float acc[NT], accm[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = accm[t] = 0.0f;
+    for (int b = 0; b < nb; ++b) {
+        const uint32_t blk = wbase + 144u * b;
+        const uint32_t h0 = lds_u32(lds, blk);
+        const uint32_t s0 = lds_u32(lds, blk + 4), s1 = lds_u32(lds, blk + 8), s2 = lds_u32(lds, blk + 12);
+        const uint8_t q[12] = {(uint8_t) s0, (uint8_t) (s0 >> 8), (uint8_t) (s0 >> 16), (uint8_t) (s0 >> 24),
+                               (uint8_t) s1, (uint8_t) (s1 >> 8), (uint8_t) (s1 >> 16), (uint8_t) (s1 >> 24),
+                               (uint8_t) s2, (uint8_t) (s2 >> 8), (uint8_t) (s2 >> 16), (uint8_t) (s2 >> 24)};
+        int sc[8], mn[8];
+        for (int j = 0; j < 8; ++j) scale_min_k4(j, q, sc[j], mn[j]);
+        int lo[4], hi[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t wq = lds_u32(lds, blk + 16 + 32 * j + 4 * n);
+            lo[j] = (int) (wq & 0x0F0F0F0Fu);
+            hi[j] = (int) ((wq >> 4) & 0x0F0F0F0Fu);
+        }
+        const float wd = h2f((uint16_t) (h0 & 0xffff)), wdm = h2f((uint16_t) (h0 >> 16));
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const uint32_t yb = abase[t] + 292u * b;
+            int sumi = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int alo = (int) lds_u32(lds, yb + 4 + 64 * j + 4 * n);
+                const int ahi = (int) lds_u32(lds, yb + 4 + 64 * j + 32 + 4 * n);
+                sumi += mul24(sc[2 * j], sdot4(lo[j], alo, 0)) + mul24(sc[2 * j + 1], sdot4(hi[j], ahi, 0));
+            }
+            const float yd = lds_f32(lds, yb);
+            acc[t] = __builtin_fmaf(yd * wd, (float) sumi, acc[t]);
+            const int nn = n & 3;
+            const uint32_t bs01 = lds_u32(lds, yb + 260 + 8 * nn), bs23 = lds_u32(lds, yb + 260 + 8 * nn + 4);
+            const int q8s0 = (int) (int16_t) (bs01 & 0xffff) + (int) (int16_t) (bs01 >> 16);
+            const int q8s1 = (int) (int16_t) (bs23 & 0xffff) + (int) (int16_t) (bs23 >> 16);
+            const int prod = mul24(mn[2 * nn], q8s0) + mul24(mn[2 * nn + 1], q8s1);
+            const float pm = __builtin_fmaf(-yd * wdm, (float) prod, accm[t]);
+            accm[t] = n < 4 ? pm : accm[t];
+        }
+    }
+    float a[NT], m[NT];
+    reduce8_mt<NT>(acc, a);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        float mm = accm[t];
+        mm = mm + __shfl_down(mm, 2, 8);
+        mm = mm + __shfl_down(mm, 1, 8);
+        m[t] = mm;
+        out[t] = a[t] + m[t];
+    }
+}
+
+template <>
+__device__ __forceinline__ void row_dot_lds_mt<T_Q6_K, 4>(const uint32_t* lds, uint32_t wbase, const uint32_t* abase,
+                                                          int nb, int n, float* out) {
+    constexpr int NT = 4;
+    float acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
+    const int g = n >= 4 ? 1 : 0;
+    for (int b = 0; b < nb; ++b) {
+        const uint32_t blk = wbase + 210u * b;
+        int sc[16];
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t s = lds_u32(lds, blk + 192 + 4 * i);
+            sc[4 * i + 0] = (int) (int8_t) (s & 0xff);
+            sc[4 * i + 1] = (int) (int8_t) ((s >> 8) & 0xff);
+            sc[4 * i + 2] = (int) (int8_t) ((s >> 16) & 0xff);
+            sc[4 * i + 3] = (int) (int8_t) (s >> 24);
+        }
+        int q6[2][4];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t qa = lds_u32(lds, blk + 64 * j + 4 * n);
+            const uint32_t qb = lds_u32(lds, blk + 64 * j + 32 + 4 * n);
+            const uint32_t qh = lds_u32(lds, blk + 128 + 32 * j + 4 * n);
+            q6[j][0] = (int) ((qa & 0x0F0F0F0Fu) | ((qh & 0x03030303u) << 4));
+            q6[j][1] = (int) ((qb & 0x0F0F0F0Fu) | ((qh & 0x0C0C0C0Cu) << 2));
+            q6[j][2] = (int) (((qa >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u));
+            q6[j][3] = (int) (((qb >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u));
+        }
+        const float wd = h2f(lds_u16(lds, blk + 208));
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const uint32_t yb = abase[t] + 292u * b;
+            int sumi = 0;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const uint32_t y = yb + 4 + 128 * j + 4 * n;
+                sumi += mul24(sc[8 * j + 0 + g], sdot4(q6[j][0], (int) lds_u32(lds, y), 0));
+                sumi += mul24(sc[8 * j + 2 + g], sdot4(q6[j][1], (int) lds_u32(lds, y + 32), 0));
+                sumi += mul24(sc[8 * j + 4 + g], sdot4(q6[j][2], (int) lds_u32(lds, y + 64), 0));
+                sumi += mul24(sc[8 * j + 6 + g], sdot4(q6[j][3], (int) lds_u32(lds, y + 96), 0));
+            }
+            const uint32_t bs = lds_u32(lds, yb + 260 + 4 * n);
+            sumi -= 32 * (mul24((int) (int16_t) (bs & 0xffff), sc[2 * n]) + mul24((int) (int16_t) (bs >> 16), sc[2 * n + 1]));
+            const float d = lds_f32(lds, yb) * wd;
+            acc[t] = __builtin_fmaf(d, (float) sumi, acc[t]);
+        }
+    }
+    reduce8_mt<NT>(acc, out);
+}
+
+template <>
+__device__ __forceinline__ void row_dot_lds_mt<T_Q8_0, 4>(const uint32_t* lds, uint32_t wbase, const uint32_t* abase,
+                                                          int nb, int n, float* out) {
+    constexpr int NT = 4;
+    float acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
+    for (int b = 0; b < nb; ++b) {
+        const uint32_t blk = wbase + 34u * b;
+        const int wq = (int) lds_u32(lds, blk + 2 + 4 * n);
+        const float wd = h2f(lds_u16(lds, blk));
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const uint32_t yb = abase[t] + 34u * b;
+            const int sumi = sdot4(wq, (int) lds_u32(lds, yb + 2 + 4 * n), 0);
+            const float d = wd * h2f(lds_u16(lds, yb));
+            acc[t] = __builtin_fmaf(d, (float) sumi, acc[t]);
+        }
+    }
+    reduce8_mt<NT>(acc, out);
 }
 
 }  // namespace qw
