@@ -205,7 +205,7 @@ int launch_group(const GroupArgs& g, hipStream_t stream) {
 // Lane (row, n): n is the AVX2 lane index 0..7 of the reference reduction.
 
 constexpr int MMID_ROWS = 32;   // rows per workgroup (8 per wave)
-constexpr int MMID_CT = 8;      // activation rows staged per pass
+constexpr int MMID_CT = 16;     // activation rows staged per pass
 constexpr int MMID_NT = 4;      // activation rows per row-dot call
 
 __host__ __device__ inline uint32_t mmid_slot_bytes(size_t row_bytes) {
