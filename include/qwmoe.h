@@ -43,6 +43,8 @@ extern "C" {
 #define QWMOE_ERR_HIP (-3)
 #define QWMOE_ERR_WORKSPACE (-4)
 #define QWMOE_ERR_NOT_INITIALIZED (-5)
+#define QWMOE_ERR_FORMAT (-6)          /* malformed or unsupported GGUF file */
+#define QWMOE_ERR_IO (-7)              /* a file could not be opened or read */
 
 /* ggml_type values used on the path (ggml/include/ggml.h:390-416). */
 enum qwmoe_type {
@@ -232,6 +234,69 @@ int qwmoe_slot_table_set(qwmoe_slot_table * t, int role, int layer, int expert, 
 int32_t qwmoe_slot_table_slot_of(const qwmoe_slot_table * t, int role, int layer, int expert);
 /* Dense row for (role, layer): n_expert entries (ExpertCache::slot_of_row). */
 const int32_t * qwmoe_slot_table_row(const qwmoe_slot_table * t, int role, int layer);
+
+/* ---- GGUF models --------------------------------------------------------------- */
+
+/* GGUF metadata of a model file, or of a "<name>-00001-of-0000N.gguf" shard set
+ * (KV from the first shard, tensors from all).  Replaces gguf_init_from_file
+ * with no_alloc per shard (ggml/src/gguf.cpp:451-906) and Model::load's unified
+ * tensor map with per-tensor (shard file, absolute offset) sources
+ * (core/model.cpp:400-502).  Opening reads metadata only (host memory); the
+ * same files the reference rejects are rejected with QWMOE_ERR_FORMAT. */
+typedef struct qwmoe_gguf qwmoe_gguf;
+typedef struct qwmoe_gguf_tensor_info {
+    char name[64];
+    int32_t type;              /* ggml type id */
+    int32_t n_dims;
+    int64_t ne[4];
+    uint64_t offset;           /* within its shard's data section (gguf_get_tensor_offset) */
+    uint64_t file_offset;      /* absolute, in its shard file (Model::src_) */
+    uint64_t nbytes;           /* gguf_get_tensor_size */
+    int32_t shard;
+} qwmoe_gguf_tensor_info;
+/* Hyperparameters of the MoE FFN path, read as Model::load_hparams does
+ * (core/model.cpp:504-548): "<arch>.block_count", ".embedding_length",
+ * ".expert_count", ".expert_used_count", ".expert_feed_forward_length",
+ * ".expert_weights_scale" (default 1). */
+typedef struct qwmoe_moe_hparams {
+    char arch[32];
+    int32_t n_layer, n_embd, n_expert, n_expert_used, n_ff_exp;
+    float expert_weights_scale;
+} qwmoe_moe_hparams;
+
+int qwmoe_gguf_open(const char * path, qwmoe_gguf ** out);
+void qwmoe_gguf_close(qwmoe_gguf * g);
+int qwmoe_gguf_n_shards(const qwmoe_gguf * g);
+int qwmoe_gguf_shard_info(const qwmoe_gguf * g, int shard, uint32_t * version, uint64_t * alignment,
+                          uint64_t * data_offset);
+/* KV pairs (gguf_get_n_kv, gguf_find_key -> index or -1, gguf_get_kv_type /
+ * gguf_get_arr_type / gguf_get_arr_n, gguf_get_arr_data / gguf_get_val_data:
+ * `data` is the raw little-endian payload of fixed-size values, NULL for
+ * strings, which qwmoe_gguf_kv_str returns element by element). */
+int qwmoe_gguf_n_kv(const qwmoe_gguf * g);
+int qwmoe_gguf_find_key(const qwmoe_gguf * g, const char * key);
+int qwmoe_gguf_kv(const qwmoe_gguf * g, int idx, const char ** key, int32_t * type, int32_t * arr_type, uint64_t * n,
+                  const void ** data);
+int qwmoe_gguf_kv_str(const qwmoe_gguf * g, int idx, uint64_t i, const char ** out);
+/* Typed lookups with a default, with the conversions of core/gguf_util.cpp:21-51
+ * (u32 accepts UINT32/INT32/UINT64/INT64, f32 accepts FLOAT32/FLOAT64). */
+int qwmoe_gguf_get_u32(const qwmoe_gguf * g, const char * key, uint32_t def, uint32_t * out);
+int qwmoe_gguf_get_f32(const qwmoe_gguf * g, const char * key, float def, float * out);
+int qwmoe_gguf_get_str(const qwmoe_gguf * g, const char * key, const char * def, const char ** out);
+int qwmoe_gguf_n_tensors(const qwmoe_gguf * g);
+int qwmoe_gguf_tensor_at(const qwmoe_gguf * g, int idx, qwmoe_gguf_tensor_info * out);
+/* index of `name`, or -1 (gguf_find_tensor) */
+int qwmoe_gguf_find_tensor(const qwmoe_gguf * g, const char * name, qwmoe_gguf_tensor_info * out);
+int qwmoe_gguf_moe_hparams(const qwmoe_gguf * g, qwmoe_moe_hparams * hp);
+/* Device bytes layer `il`'s blk.il.ffn_gate_inp / ffn_{gate,up,down}_exps
+ * tensors take in qwmoe_gguf_load_moe_layer's layout (each 256-byte aligned). */
+int qwmoe_gguf_moe_layer_bytes(const qwmoe_gguf * g, int il, size_t * out);
+/* Reads layer `il`'s router and expert tensors into the caller's device buffer
+ * `dev` (dev_bytes >= qwmoe_gguf_moe_layer_bytes) through pinned host staging
+ * (the handle keeps two 16 MiB pinned buffers from its first load until close),
+ * and fills `out` with pointers into it (identity slots).  Returns once the
+ * copies on `stream` are complete.  Expert types: Q4_K, Q6_K, Q8_0; router: F32. */
+int qwmoe_gguf_load_moe_layer(void * stream, qwmoe_gguf * g, int il, void * dev, size_t dev_bytes, qwmoe_layer * out);
 
 /* ---- host-side checks (no GPU needed) ---------------------------------------- */
 

@@ -75,7 +75,38 @@ SIGNATURES = {
     "qwmoe_slot_table_slot_of": (C.c_int32, [P, I, I, I]),
     "qwmoe_slot_table_row": (P, [P, I, I]),
     "qwmoe_host_argsort_desc": (I, [P, I, P]),
+    "qwmoe_gguf_open": (I, [C.c_char_p, P]),
+    "qwmoe_gguf_close": (None, [P]),
+    "qwmoe_gguf_n_shards": (I, [P]),
+    "qwmoe_gguf_shard_info": (I, [P, I, P, P, P]),
+    "qwmoe_gguf_n_kv": (I, [P]),
+    "qwmoe_gguf_find_key": (I, [P, C.c_char_p]),
+    "qwmoe_gguf_kv": (I, [P, I, P, P, P, P, P]),
+    "qwmoe_gguf_kv_str": (I, [P, I, U64, P]),
+    "qwmoe_gguf_get_u32": (I, [P, C.c_char_p, C.c_uint32, P]),
+    "qwmoe_gguf_get_f32": (I, [P, C.c_char_p, F, P]),
+    "qwmoe_gguf_get_str": (I, [P, C.c_char_p, C.c_char_p, P]),
+    "qwmoe_gguf_n_tensors": (I, [P]),
+    "qwmoe_gguf_tensor_at": (I, [P, I, P]),
+    "qwmoe_gguf_find_tensor": (I, [P, C.c_char_p, P]),
+    "qwmoe_gguf_moe_hparams": (I, [P, P]),
+    "qwmoe_gguf_moe_layer_bytes": (I, [P, I, P]),
+    "qwmoe_gguf_load_moe_layer": (I, [P, P, I, P, SZ, P]),
 }
+
+
+class GgufTensorInfo(C.Structure):
+    """Mirror of ``qwmoe_gguf_tensor_info``."""
+
+    _fields_ = [("name", C.c_char * 64), ("type", C.c_int32), ("n_dims", C.c_int32), ("ne", C.c_int64 * 4),
+                ("offset", C.c_uint64), ("file_offset", C.c_uint64), ("nbytes", C.c_uint64), ("shard", C.c_int32)]
+
+
+class MoeHparams(C.Structure):
+    """Mirror of ``qwmoe_moe_hparams``."""
+
+    _fields_ = [("arch", C.c_char * 32), ("n_layer", C.c_int32), ("n_embd", C.c_int32), ("n_expert", C.c_int32),
+                ("n_expert_used", C.c_int32), ("n_ff_exp", C.c_int32), ("expert_weights_scale", C.c_float)]
 
 _lib = None
 
@@ -98,7 +129,9 @@ def lib() -> C.CDLL:
 def check(rc: int, what: str = "") -> None:
     if rc != 0:
         msg = lib().qwmoe_strerror(rc).decode()
-        raise QwmoeError(f"{what}: {msg} ({rc})")
+        err = QwmoeError(f"{what}: {msg} ({rc})")
+        err.status = rc
+        raise err
 
 
 def row_size(t: int, n: int) -> int:

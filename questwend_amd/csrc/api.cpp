@@ -176,6 +176,8 @@ const char* qwmoe_strerror(int status) {
         case QWMOE_ERR_HIP: return "HIP runtime error";
         case QWMOE_ERR_WORKSPACE: return "workspace too small";
         case QWMOE_ERR_NOT_INITIALIZED: return "qwmoe_init has not been called";
+        case QWMOE_ERR_FORMAT: return "malformed or unsupported GGUF file";
+        case QWMOE_ERR_IO: return "file could not be opened or read";
     }
     return "unknown status";
 }

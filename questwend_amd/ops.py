@@ -8,7 +8,7 @@ from __future__ import annotations
 
 import ctypes as C
 
-from . import BLOCK, Q8_0, Q8_K, Layer, check, lib, row_size, vec_dot_type
+from . import BLOCK, Q8_0, Q8_K, GgufTensorInfo, Layer, MoeHparams, check, lib, row_size, vec_dot_type
 
 
 def _torch():
@@ -229,3 +229,114 @@ def ffn_layer(layer: Layer, x, rms_eps: float = -1.0):
     check(lib().qwmoe_ffn_layer(stream(), C.byref(layer), _ptr(x), T, _ptr(out), rms_eps, _ptr(xn), _ptr(ids),
                                 _ptr(w)), "ffn_layer")
     return out, xn, ids, w
+
+
+class Gguf:
+    """A GGUF model file (or shard set) opened through qwmoe_gguf_*: metadata on
+    the host, MoE layers loaded into device memory on request."""
+
+    _SCALAR = {0: "B", 1: "b", 2: "H", 3: "h", 4: "I", 5: "i", 6: "f", 7: "?", 10: "Q", 11: "q", 12: "d"}
+
+    def __init__(self, path):
+        h = C.c_void_p()
+        check(lib().qwmoe_gguf_open(str(path).encode(), C.byref(h)), "gguf_open")
+        self.h = h
+
+    def close(self) -> None:
+        if self.h:
+            lib().qwmoe_gguf_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def shards(self) -> list[dict]:
+        out = []
+        for i in range(lib().qwmoe_gguf_n_shards(self.h)):
+            v, a, d = C.c_uint32(), C.c_uint64(), C.c_uint64()
+            check(lib().qwmoe_gguf_shard_info(self.h, i, C.byref(v), C.byref(a), C.byref(d)), "gguf_shard_info")
+            out.append({"version": v.value, "alignment": a.value, "data_offset": d.value})
+        return out
+
+    def kv(self) -> list[dict]:
+        import struct
+        out = []
+        for i in range(lib().qwmoe_gguf_n_kv(self.h)):
+            key, t, at, n, data = C.c_char_p(), C.c_int32(), C.c_int32(), C.c_uint64(), C.c_void_p()
+            check(lib().qwmoe_gguf_kv(self.h, i, C.byref(key), C.byref(t), C.byref(at), C.byref(n), C.byref(data)),
+                  "gguf_kv")
+            e = {"key": key.value.decode(), "type": t.value}
+            et = at.value if t.value == 9 else t.value
+            if t.value == 9:
+                e.update(arr_type=at.value, n=n.value)
+            if et == 8:
+                vals = []
+                for j in range(n.value):
+                    s = C.c_char_p()
+                    check(lib().qwmoe_gguf_kv_str(self.h, i, j, C.byref(s)), "gguf_kv_str")
+                    vals.append(s.value.decode())
+            else:
+                f = self._SCALAR[et]
+                sz = struct.calcsize("<" + f)
+                raw = C.string_at(data.value, n.value * sz) if n.value else b""
+                vals = list(struct.unpack(f"<{n.value}{f}", raw))
+            e["value"] = vals if t.value == 9 else vals[0]
+            out.append(e)
+        return out
+
+    def tensors(self) -> list[dict]:
+        out = []
+        for i in range(lib().qwmoe_gguf_n_tensors(self.h)):
+            ti = GgufTensorInfo()
+            check(lib().qwmoe_gguf_tensor_at(self.h, i, C.byref(ti)), "gguf_tensor_at")
+            out.append(self._info(ti))
+        return out
+
+    def tensor(self, name: str):
+        ti = GgufTensorInfo()
+        idx = lib().qwmoe_gguf_find_tensor(self.h, name.encode(), C.byref(ti))
+        return None if idx < 0 else self._info(ti)
+
+    @staticmethod
+    def _info(ti) -> dict:
+        return {"name": ti.name.decode(), "type": ti.type, "n_dims": ti.n_dims, "ne": list(ti.ne),
+                "offset": ti.offset, "file_offset": ti.file_offset, "size": ti.nbytes, "shard": ti.shard}
+
+    def get_u32(self, key: str, default: int = 0) -> int:
+        v = C.c_uint32()
+        check(lib().qwmoe_gguf_get_u32(self.h, key.encode(), default, C.byref(v)), "gguf_get_u32")
+        return v.value
+
+    def get_f32(self, key: str, default: float = 0.0) -> float:
+        v = C.c_float()
+        check(lib().qwmoe_gguf_get_f32(self.h, key.encode(), default, C.byref(v)), "gguf_get_f32")
+        return v.value
+
+    def get_str(self, key: str, default: str = ""):
+        v = C.c_char_p()
+        check(lib().qwmoe_gguf_get_str(self.h, key.encode(), default.encode(), C.byref(v)), "gguf_get_str")
+        return v.value.decode()
+
+    def hparams(self) -> dict:
+        hp = MoeHparams()
+        check(lib().qwmoe_gguf_moe_hparams(self.h, C.byref(hp)), "gguf_moe_hparams")
+        return {"arch": hp.arch.decode(), "n_layer": hp.n_layer, "n_embd": hp.n_embd, "n_expert": hp.n_expert,
+                "n_expert_used": hp.n_expert_used, "n_ff_exp": hp.n_ff_exp,
+                "expert_weights_scale": hp.expert_weights_scale}
+
+    def layer_bytes(self, il: int) -> int:
+        n = C.c_size_t()
+        check(lib().qwmoe_gguf_moe_layer_bytes(self.h, il, C.byref(n)), "gguf_moe_layer_bytes")
+        return n.value
+
+    def load_layer(self, il: int, device="cuda:0"):
+        """Layer il's router and experts in a new device buffer -> (Layer, buffer)."""
+        torch = _torch()
+        buf = torch.empty(self.layer_bytes(il), dtype=torch.uint8, device=device)
+        L = Layer()
+        check(lib().qwmoe_gguf_load_moe_layer(stream(), self.h, il, _ptr(buf), buf.numel(), C.byref(L)),
+              "gguf_load_moe_layer")
+        return L, buf
