@@ -273,6 +273,8 @@ int qwmoe_gguf_shard_info(const qwmoe_gguf * g, int shard, uint32_t * version, u
  * gguf_get_arr_type / gguf_get_arr_n, gguf_get_arr_data / gguf_get_val_data:
  * `data` is the raw little-endian payload of fixed-size values, NULL for
  * strings, which qwmoe_gguf_kv_str returns element by element). */
+/* Path of shard `shard` (the file Model::tensor_file names, core/model.cpp:300-304). */
+int qwmoe_gguf_shard_path(const qwmoe_gguf * g, int shard, const char ** out);
 int qwmoe_gguf_n_kv(const qwmoe_gguf * g);
 int qwmoe_gguf_find_key(const qwmoe_gguf * g, const char * key);
 int qwmoe_gguf_kv(const qwmoe_gguf * g, int idx, const char ** key, int32_t * type, int32_t * arr_type, uint64_t * n,
@@ -297,6 +299,114 @@ int qwmoe_gguf_moe_layer_bytes(const qwmoe_gguf * g, int il, size_t * out);
  * and fills `out` with pointers into it (identity slots).  Returns once the
  * copies on `stream` are complete.  Expert types: Q4_K, Q6_K, Q8_0; router: F32. */
 int qwmoe_gguf_load_moe_layer(void * stream, qwmoe_gguf * g, int il, void * dev, size_t dev_bytes, qwmoe_layer * out);
+
+/* ---- expert cache: slot pools fed from a slower tier ------------------------- */
+
+/* ExpertCache (core/expert_cache.h:39-166, core/expert_cache.cpp:90-832): when
+ * not every expert fits in HBM, slot pools hold the hot (layer, expert) slabs
+ * and the rest are fetched on demand.  One pool per (role, type, ne0, ne1)
+ * signature, shared by the layers that have it (cpp:128-152); every pool gets
+ * the same residency fraction budget / total expert bytes, at least n_used and
+ * at most n_layer_of_pool * n_expert slots (cpp:155-186); LRU victim = the first
+ * slot with the smallest access stamp (cpp:374-391); key = layer * n_expert +
+ * expert.  Slot rows use 0 as the non-resident sentinel, as slot_of_row does
+ * (cpp:694-697): a kernel run on rows with absent experts reads slot 0, so a
+ * caller that speculates checks residency of the ids it got back afterwards
+ * (core/runtime.cpp:2921-2933) and repairs with ensure_resident.
+ *
+ * Tiers: host memory (each (role, layer) tensor's n_expert slabs back to back,
+ * the RAM tier of cpp:355-364; pinned memory makes every fetch an asynchronous
+ * DMA) or a file (slabs read with pread by a pool of worker threads into
+ * pinned staging, then copied asynchronously: the SSD tier of cpp:297-352 and
+ * 412-687, without the opt-in coalescing).  Every copy and row upload is
+ * issued on the cache's stream, so work the caller issues on that stream
+ * afterwards sees the slabs; calls on one cache must not overlap. */
+typedef struct qwmoe_expert_cache qwmoe_expert_cache;
+
+typedef struct qwmoe_expert_src {
+    int32_t type;              /* ggml type: Q4_K, Q6_K or Q8_0 */
+    int64_t ne0, ne1;          /* one expert's slab is [ne0, ne1]; the tensor is [ne0, ne1, n_expert] */
+    const void * host;         /* host tier: n_expert slabs back to back, or NULL for the file tier */
+    const char * path;         /* file tier: the file holding the same bytes ... */
+    uint64_t file_offset;      /* ... from this absolute offset */
+} qwmoe_expert_src;
+
+#define QWMOE_CACHE_DRY_RUN 1  /* bookkeeping only: no device pools, no copies, no file reads (planning, tests) */
+
+typedef struct qwmoe_expert_cache_config {
+    size_t vram_budget;        /* bytes the slot pools may take (core/expert_cache.h:43-45) */
+    int32_t n_used;            /* experts per token: every pool holds at least this many slots */
+    int32_t io_threads;        /* file tier read workers (0: 8, core/expert_cache.cpp:100) */
+    int32_t flags;             /* QWMOE_CACHE_DRY_RUN */
+} qwmoe_expert_cache_config;
+
+typedef struct qwmoe_expert_cache_stats {  /* ExpertCache::Stats, core/expert_cache.h:86-88 */
+    uint64_t hits, misses, evictions;
+    double fetch_ms;           /* host time spent reading files and issuing copies */
+    uint64_t fetch_bytes;
+} qwmoe_expert_cache_stats;
+
+/* srcs: [3][n_layer] (role-major: gate, up, down), copied at creation; host
+ * sources must stay valid for the cache's lifetime.  Allocates the pools and
+ * a device row table [3][n_layer][n_expert] with one hipMalloc. */
+int qwmoe_expert_cache_create(void * stream, int n_layer, int n_expert, const qwmoe_expert_src * srcs,
+                              const qwmoe_expert_cache_config * cfg, qwmoe_expert_cache ** out);
+/* From a GGUF model's blk.N.ffn_{gate,up,down}_exps.weight tensors (the
+ * expert tensors ExpertCache's constructor looks up, cpp:76-89, 110-122).
+ * tier 0: host RAM -- every expert tensor is read once into pinned host memory
+ * the cache owns (the CPU expert buffer Model keeps for the RAM tier);
+ * tier 1: file -- slabs are read from the shard files on each miss.
+ * cfg->n_used == 0 takes n_expert_used from the metadata. */
+int qwmoe_expert_cache_create_gguf(void * stream, const qwmoe_gguf * g, int tier, const qwmoe_expert_cache_config * cfg,
+                                   qwmoe_expert_cache ** out);
+void qwmoe_expert_cache_free(qwmoe_expert_cache * c);
+
+int qwmoe_expert_cache_n_pools(const qwmoe_expert_cache * c);
+/* One pool: its role, type, slab shape, slots, slab bytes and device base
+ * (NULL in a dry run). */
+int qwmoe_expert_cache_pool_info(const qwmoe_expert_cache * c, int pool, int32_t * role, int32_t * type, int64_t * ne0,
+                                 int64_t * ne1, int64_t * n_slots, uint64_t * slab_bytes, void ** base);
+/* Pool serving (role, layer) (ExpertCache::layer_pool_). */
+int qwmoe_expert_cache_pool_of(const qwmoe_expert_cache * c, int role, int layer);
+int qwmoe_expert_cache_min_slots(const qwmoe_expert_cache * c);          /* cpp:282-286 */
+int qwmoe_expert_cache_capacity(const qwmoe_expert_cache * c, int layer); /* cpp:288-293 */
+
+/* ExpertCache::ensure (cpp:790-832): make `layer`'s experts ids[0..n) resident
+ * for all three roles, fetching the misses, and write their slot ids (host
+ * arrays of n; any may be NULL).  Rejects, before changing anything, a call
+ * naming more distinct experts than capacity(layer) (the reference leaves that
+ * to its callers, core/runtime.cpp:2131-2146: such a call would evict its own
+ * slots). */
+int qwmoe_expert_cache_ensure(qwmoe_expert_cache * c, int layer, const int32_t * ids, int n, int32_t * slot_gate,
+                              int32_t * slot_up, int32_t * slot_down);
+/* ExpertCache::ensure_resident (cpp:779-788): fetch what is absent of
+ * (layer, expert) in the three pools, counting misses only. */
+int qwmoe_expert_cache_ensure_resident(qwmoe_expert_cache * c, int layer, int expert);
+/* ExpertCache::touch (cpp:699-707): a resident access; no-op when absent. */
+int qwmoe_expert_cache_touch(qwmoe_expert_cache * c, int role, int layer, int expert);
+/* 1 resident, 0 absent, < 0 error (cpp:689-692). */
+int qwmoe_expert_cache_resident(const qwmoe_expert_cache * c, int role, int layer, int expert);
+/* Host row for (role, layer): n_expert slot ids, 0 when absent (cpp:694-697). */
+const int32_t * qwmoe_expert_cache_slot_of_row(const qwmoe_expert_cache * c, int role, int layer);
+/* Device copy of that row, kept current on the cache's stream by every call
+ * that changes residency (the in-graph remap table g2s_all,
+ * core/runtime.cpp:2877-2884).  NULL in a dry run. */
+const int32_t * qwmoe_expert_cache_device_row(const qwmoe_expert_cache * c, int role, int layer);
+/* Fills L's expert fields (types, pool bases, strides, slot counts, device
+ * rows) for `layer`; the caller sets shapes, router and scale. */
+int qwmoe_expert_cache_layer(const qwmoe_expert_cache * c, int layer, qwmoe_layer * L);
+int qwmoe_expert_cache_get_stats(const qwmoe_expert_cache * c, qwmoe_expert_cache_stats * out);
+/* Hot-expert profile in the reference's text format (cpp:723-741):
+ * "QWENEXPCACHE 1", "<n_layer> <n_expert>", then "<role> <layer> <expert> <count>"
+ * lines; keys are written in ascending order per pool. */
+int qwmoe_expert_cache_save_profile(const qwmoe_expert_cache * c, const char * path);
+/* ExpertCache::load_prefetch (cpp:743-777): installs the most-accessed keys
+ * until each pool is full; equal counts keep file order (the reference's
+ * std::sort leaves their order unspecified).  A missing or incompatible file
+ * prefetches nothing and is not an error.  *n_prefetched may be NULL. */
+int qwmoe_expert_cache_load_prefetch(qwmoe_expert_cache * c, const char * path, uint64_t * n_prefetched);
+/* Waits for every copy the cache issued. */
+int qwmoe_expert_cache_sync(qwmoe_expert_cache * c);
 
 /* ---- host-side checks (no GPU needed) ---------------------------------------- */
 

@@ -92,6 +92,26 @@ SIGNATURES = {
     "qwmoe_gguf_moe_hparams": (I, [P, P]),
     "qwmoe_gguf_moe_layer_bytes": (I, [P, I, P]),
     "qwmoe_gguf_load_moe_layer": (I, [P, P, I, P, SZ, P]),
+    "qwmoe_gguf_shard_path": (I, [P, I, P]),
+    "qwmoe_expert_cache_create": (I, [P, I, I, P, P, P]),
+    "qwmoe_expert_cache_create_gguf": (I, [P, P, I, P, P]),
+    "qwmoe_expert_cache_free": (None, [P]),
+    "qwmoe_expert_cache_n_pools": (I, [P]),
+    "qwmoe_expert_cache_pool_info": (I, [P, I, P, P, P, P, P, P, P]),
+    "qwmoe_expert_cache_pool_of": (I, [P, I, I]),
+    "qwmoe_expert_cache_min_slots": (I, [P]),
+    "qwmoe_expert_cache_capacity": (I, [P, I]),
+    "qwmoe_expert_cache_ensure": (I, [P, I, P, I, P, P, P]),
+    "qwmoe_expert_cache_ensure_resident": (I, [P, I, I]),
+    "qwmoe_expert_cache_touch": (I, [P, I, I, I]),
+    "qwmoe_expert_cache_resident": (I, [P, I, I, I]),
+    "qwmoe_expert_cache_slot_of_row": (P, [P, I, I]),
+    "qwmoe_expert_cache_device_row": (P, [P, I, I]),
+    "qwmoe_expert_cache_layer": (I, [P, I, P]),
+    "qwmoe_expert_cache_get_stats": (I, [P, P]),
+    "qwmoe_expert_cache_save_profile": (I, [P, C.c_char_p]),
+    "qwmoe_expert_cache_load_prefetch": (I, [P, C.c_char_p, P]),
+    "qwmoe_expert_cache_sync": (I, [P]),
 }
 
 
@@ -107,6 +127,30 @@ class MoeHparams(C.Structure):
 
     _fields_ = [("arch", C.c_char * 32), ("n_layer", C.c_int32), ("n_embd", C.c_int32), ("n_expert", C.c_int32),
                 ("n_expert_used", C.c_int32), ("n_ff_exp", C.c_int32), ("expert_weights_scale", C.c_float)]
+
+
+
+class ExpertSrc(C.Structure):
+    """Mirror of ``qwmoe_expert_src``."""
+
+    _fields_ = [("type", C.c_int32), ("ne0", C.c_int64), ("ne1", C.c_int64), ("host", C.c_void_p),
+                ("path", C.c_char_p), ("file_offset", C.c_uint64)]
+
+
+class ExpertCacheConfig(C.Structure):
+    """Mirror of ``qwmoe_expert_cache_config``."""
+
+    _fields_ = [("vram_budget", C.c_size_t), ("n_used", C.c_int32), ("io_threads", C.c_int32), ("flags", C.c_int32)]
+
+
+class ExpertCacheStats(C.Structure):
+    """Mirror of ``qwmoe_expert_cache_stats``."""
+
+    _fields_ = [("hits", C.c_uint64), ("misses", C.c_uint64), ("evictions", C.c_uint64), ("fetch_ms", C.c_double),
+                ("fetch_bytes", C.c_uint64)]
+
+
+CACHE_DRY_RUN = 1
 
 _lib = None
 

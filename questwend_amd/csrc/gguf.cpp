@@ -380,6 +380,12 @@ int qwmoe_gguf_shard_info(const qwmoe_gguf* g, int shard, uint32_t* version, uin
     return QWMOE_OK;
 }
 
+int qwmoe_gguf_shard_path(const qwmoe_gguf* g, int shard, const char** out) {
+    if (!g || !out || shard < 0 || shard >= (int) g->shards.size()) return QWMOE_ERR_INVALID_ARG;
+    *out = g->shards[shard].path.c_str();
+    return QWMOE_OK;
+}
+
 int qwmoe_gguf_n_kv(const qwmoe_gguf* g) { return g ? (int) g->kv.size() : QWMOE_ERR_INVALID_ARG; }
 
 int qwmoe_gguf_find_key(const qwmoe_gguf* g, const char* key) {

@@ -97,7 +97,9 @@ __global__ void __launch_bounds__(64) k_router_topk(const float* __restrict__ lo
     if (probs_out)
         for (int64_t i = lane; i < E; i += 64) probs_out[t * E + i] = p[i];
     // rank of every element; a tie group that reaches into the first k places
-    // leaves the order to std::sort's algorithm, which is then replayed exactly
+    // leaves the order to std::sort's algorithm, which is then replayed exactly.
+    // A NaN (eq == 0) goes to the replay too: softmax makes every probability NaN
+    // then, which std::sort treats as all equivalent.
     for (int64_t i = lane; i < E; i += 64) {
         const float pi = p[i];
         int gt = 0, eq = 0;
@@ -106,7 +108,7 @@ __global__ void __launch_bounds__(64) k_router_topk(const float* __restrict__ lo
             eq += p[j] == pi;
         }
         if (gt < k) {
-            if (eq > 1) need_sort = 1;
+            if (eq != 1) need_sort = 1;
             else order[gt] = (int32_t) i;
         }
     }

@@ -8,7 +8,8 @@ from __future__ import annotations
 
 import ctypes as C
 
-from . import BLOCK, Q8_0, Q8_K, GgufTensorInfo, Layer, MoeHparams, check, lib, row_size, vec_dot_type
+from . import (BLOCK, CACHE_DRY_RUN, Q8_0, Q8_K, ExpertCacheConfig, ExpertCacheStats, ExpertSrc, GgufTensorInfo, Layer,
+               MoeHparams, check, lib, row_size, vec_dot_type)
 
 
 def _torch():
@@ -340,3 +341,135 @@ class Gguf:
         check(lib().qwmoe_gguf_load_moe_layer(stream(), self.h, il, _ptr(buf), buf.numel(), C.byref(L)),
               "gguf_load_moe_layer")
         return L, buf
+
+
+class ExpertCache:
+    """Expert slot pools in device memory fed from host memory or a file,
+    through qwmoe_expert_cache_* (ExpertCache, core/expert_cache.h:39-166).
+
+    Construct with ``sources`` = [role][layer] dicts {type, ne0, ne1, host (an
+    address) or path + file_offset}, or with ``ExpertCache.from_gguf``.  Every
+    copy goes on ``stream`` (torch's current stream by default); a dry run keeps
+    the bookkeeping only."""
+
+    ROLES = ("gate", "up", "down")
+
+    def __init__(self, n_layer: int, n_expert: int, sources, vram_budget: int, n_used: int, io_threads: int = 0,
+                 dry_run: bool = False, stream_handle=None, _handle=None):
+        self.n_layer, self.n_expert = n_layer, n_expert
+        self._keep = []
+        if _handle is not None:
+            self.h = _handle
+            return
+        arr = (ExpertSrc * (3 * n_layer))()
+        for r in range(3):
+            for il in range(n_layer):
+                s = sources[r][il]
+                e = arr[r * n_layer + il]
+                e.type, e.ne0, e.ne1 = s["type"], s["ne0"], s["ne1"]
+                e.host = s.get("host")
+                if s.get("path") is not None:
+                    b = str(s["path"]).encode()
+                    self._keep.append(b)
+                    e.path = b
+                    e.file_offset = s.get("file_offset", 0)
+        cfg = ExpertCacheConfig(vram_budget, n_used, io_threads, CACHE_DRY_RUN if dry_run else 0)
+        h = C.c_void_p()
+        st = None if dry_run else (stream_handle if stream_handle is not None else stream())
+        check(lib().qwmoe_expert_cache_create(st, n_layer, n_expert, arr, C.byref(cfg), C.byref(h)),
+              "expert_cache_create")
+        self.h = h
+
+    @classmethod
+    def from_gguf(cls, g: "Gguf", tier: int, vram_budget: int, n_used: int = 0, io_threads: int = 0,
+                  dry_run: bool = False, stream_handle=None):
+        cfg = ExpertCacheConfig(vram_budget, n_used, io_threads, CACHE_DRY_RUN if dry_run else 0)
+        h = C.c_void_p()
+        st = None if dry_run else (stream_handle if stream_handle is not None else stream())
+        check(lib().qwmoe_expert_cache_create_gguf(st, g.h, tier, C.byref(cfg), C.byref(h)), "expert_cache_create_gguf")
+        hp = g.hparams()
+        return cls(hp["n_layer"], hp["n_expert"], None, 0, 0, _handle=h)
+
+    def close(self) -> None:
+        if self.h:
+            lib().qwmoe_expert_cache_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001  (interpreter shutdown)
+            pass
+
+    def pools(self) -> list[dict]:
+        out = []
+        for i in range(lib().qwmoe_expert_cache_n_pools(self.h)):
+            role, t, ne0, ne1, ns, slab, base = (C.c_int32(), C.c_int32(), C.c_int64(), C.c_int64(), C.c_int64(),
+                                                 C.c_uint64(), C.c_void_p())
+            check(lib().qwmoe_expert_cache_pool_info(self.h, i, C.byref(role), C.byref(t), C.byref(ne0), C.byref(ne1),
+                                                     C.byref(ns), C.byref(slab), C.byref(base)), "pool_info")
+            out.append({"role": role.value, "type": t.value, "ne0": ne0.value, "ne1": ne1.value,
+                        "n_slots": ns.value, "slab": slab.value, "base": base.value})
+        return out
+
+    def pool_of(self, role: int, layer: int) -> int:
+        r = lib().qwmoe_expert_cache_pool_of(self.h, role, layer)
+        check(min(r, 0), "pool_of")
+        return r
+
+    def min_slots(self) -> int:
+        return lib().qwmoe_expert_cache_min_slots(self.h)
+
+    def capacity(self, layer: int) -> int:
+        r = lib().qwmoe_expert_cache_capacity(self.h, layer)
+        check(min(r, 0), "capacity")
+        return r
+
+    def ensure(self, layer: int, ids) -> tuple[list[int], list[int], list[int]]:
+        n = len(ids)
+        a = (C.c_int32 * max(n, 1))(*ids)
+        g, u, d = ((C.c_int32 * max(n, 1))() for _ in range(3))
+        check(lib().qwmoe_expert_cache_ensure(self.h, layer, a, n, g, u, d), "expert_cache_ensure")
+        return list(g[:n]), list(u[:n]), list(d[:n])
+
+    def ensure_resident(self, layer: int, expert: int) -> None:
+        check(lib().qwmoe_expert_cache_ensure_resident(self.h, layer, expert), "expert_cache_ensure_resident")
+
+    def touch(self, role: int, layer: int, expert: int) -> None:
+        check(lib().qwmoe_expert_cache_touch(self.h, role, layer, expert), "expert_cache_touch")
+
+    def resident(self, role: int, layer: int, expert: int) -> bool:
+        r = lib().qwmoe_expert_cache_resident(self.h, role, layer, expert)
+        check(min(r, 0), "expert_cache_resident")
+        return r == 1
+
+    def slot_of_row(self, role: int, layer: int) -> list[int]:
+        p = lib().qwmoe_expert_cache_slot_of_row(self.h, role, layer)
+        if not p:
+            raise ValueError("role/layer out of range")
+        return list((C.c_int32 * self.n_expert).from_address(p))
+
+    def device_row(self, role: int, layer: int) -> int:
+        return lib().qwmoe_expert_cache_device_row(self.h, role, layer) or 0
+
+    def layer(self, layer: int, L: Layer | None = None) -> Layer:
+        L = L if L is not None else Layer()
+        check(lib().qwmoe_expert_cache_layer(self.h, layer, C.byref(L)), "expert_cache_layer")
+        return L
+
+    def stats(self) -> dict:
+        s = ExpertCacheStats()
+        check(lib().qwmoe_expert_cache_get_stats(self.h, C.byref(s)), "expert_cache_stats")
+        return {"hits": s.hits, "misses": s.misses, "evictions": s.evictions, "fetch_ms": s.fetch_ms,
+                "fetch_bytes": s.fetch_bytes}
+
+    def save_profile(self, path) -> None:
+        check(lib().qwmoe_expert_cache_save_profile(self.h, str(path).encode()), "expert_cache_save_profile")
+
+    def load_prefetch(self, path) -> int:
+        n = C.c_uint64()
+        check(lib().qwmoe_expert_cache_load_prefetch(self.h, str(path).encode(), C.byref(n)), "expert_cache_load_prefetch")
+        return n.value
+
+    def sync(self) -> None:
+        check(lib().qwmoe_expert_cache_sync(self.h), "expert_cache_sync")

@@ -233,6 +233,34 @@ def test_router_ties_replay_std_sort(orc):
     assert ops.device_status(clear=True) & qa.STATUS_TOPK_TIE_SORT
 
 
+def test_router_non_finite_input(orc):
+    """A NaN or +Inf in a token's input makes every logit of that token
+    non-finite and softmax makes every probability NaN; std::sort then sees
+    all-equivalent values, and the replay must give its permutation (the other
+    tokens are unaffected)."""
+    note("router with NaN / +Inf inputs")
+    rng = np.random.default_rng(23)
+    H, E, k, T = 512, 64, 6, 4
+    W = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    x[1, 7] = np.nan
+    x[3, 100] = np.inf
+    ops.device_status(clear=True)
+    ids, w, probs = ops.router_topk(dev(W), dev(x), k, want_probs=True)
+    i2, w2, _, p2 = orc.router(W, x, k)
+    ids, w, probs = host(ids), host(w), host(probs)
+    for t in (0, 2):
+        assert np.array_equal(ids[t], i2[t])
+        assert np.array_equal(bits(w[t]), bits(w2[t]))
+    want = np.empty(E, np.int32)
+    qa.lib().qwmoe_host_argsort_desc(np.full(E, np.nan, np.float32).ctypes.data, E, want.ctypes.data)
+    for t in (1, 3):
+        assert np.isnan(probs[t]).all() and np.isnan(p2[t]).all()
+        assert np.array_equal(ids[t], want[:k]) and np.array_equal(i2[t], want[:k]), f"token {t}"
+        assert np.isnan(w[t]).all()
+    assert ops.device_status(clear=True) == qa.STATUS_TOPK_TIE_SORT
+
+
 # ---------------------------------------------------------------- FFN tail
 
 def test_swiglu_and_weighted_sum(orc):
