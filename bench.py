@@ -233,6 +233,141 @@ def prefill_cpu_baseline(L, mats, router, x, T: int):
             "sample": f"{reps} evaluations of the T={T} layer graph in {dt * reps:.1f}s"}
 
 
+def expert_cache_bench(args) -> int:
+    """The configs[1] decode stack (48 Q4_K layers of the 30B-A3B shape) with
+    its experts in pinned host memory and a fraction ``--resident`` of them in
+    HBM slot pools fed by qwmoe_expert_cache (the RAM tier of
+    core/expert_cache.cpp:355-364).  A step = one token: the whole-stack kernel
+    speculating on the resident set, the ids it used checked against the
+    residency (qwmoe_expert_cache_verify), and on a miss the per-layer path
+    (router -> ensure -> layer, core/runtime.cpp:2458-2662).  Router rows are
+    Zipf(--zipf)-skewed (0: unskewed).  Every timed token's output is compared
+    bitwise with the all-resident stack afterwards."""
+    import numpy as np
+    import torch
+    from questwend_amd import Q4_K, ops, row_size
+
+    ops.init(0, 256 << 20)
+    dev = "cuda:0"
+    layers = make_weights(torch, ops, Q4_K, args.seed)
+    if args.zipf > 0:
+        sc = torch.from_numpy(zipf_row_scales(E, args.zipf)).to(dev)[:, None]
+        for lay in layers:
+            lay[0].mul_(sc)
+    # the RAM tier: every expert tensor in pinned host memory
+    host = [[None] * N_LAYER for _ in range(3)]
+    for l, lay in enumerate(layers):
+        for r in range(3):
+            m = lay[1 + r]
+            h = torch.empty(m.numel(), dtype=torch.uint8, pin_memory=True)
+            h.copy_(m.view(-1))
+            host[r][l] = h
+    torch.cuda.synchronize()
+    # plain H2D probe: one 1 GiB pinned -> device copy
+    probe_h = torch.empty(1 << 30, dtype=torch.uint8, pin_memory=True)
+    probe_d = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    probe_d.copy_(probe_h, non_blocking=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(3):
+        probe_d.copy_(probe_h, non_blocking=True)
+    torch.cuda.synchronize()
+    h2d_probe = 3 * (1 << 30) / (time.perf_counter() - t0) / 1e9
+    del probe_h, probe_d
+
+    shapes = ((H, F), (H, F), (F, H))
+    slab = [row_size(Q4_K, shapes[r][0]) * shapes[r][1] for r in range(3)]
+    total = sum(slab) * E * N_LAYER
+    budget = int(total * args.resident)
+    srcs = [[{"type": Q4_K, "ne0": shapes[r][0], "ne1": shapes[r][1], "host": host[r][l].data_ptr()}
+             for l in range(N_LAYER)] for r in range(3)]
+    cache = ops.ExpertCache(N_LAYER, E, srcs, budget, K_USED, copy_engine=args.copy_engine)
+    resident = [ops.make_layer(H, E, K_USED, F, r, g, u, d, (Q4_K,) * 3) for (r, g, u, d) in layers]
+    cached = []
+    for l, (r, g, u, d) in enumerate(layers):
+        L = ops.make_layer(H, E, K_USED, F, r, g, u, d, (Q4_K,) * 3)
+        cache.layer(l, L)
+        cached.append(L)
+    spec = ops.DecodeStack(cached, RMS_EPS, keepalive=(layers, host))
+    n_per_layer = min(E, cache.capacity(0) // N_LAYER)
+
+    # cold fill: the first n_per_layer experts of every layer (the Zipf-hot ones)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for l in range(N_LAYER):
+        cache.ensure(l, list(range(n_per_layer)))
+    cache.sync()
+    fill_s = time.perf_counter() - t0
+    fill_bytes = cache.stats()["fetch_bytes"]
+
+    n_steps = args.steps + args.warmup
+    xs = torch.empty((n_steps, H), dtype=torch.float32, device=dev)
+    ops.randn_(xs, args.seed + 777, 0.0, 1.0)
+    outs = torch.empty((n_steps, H), dtype=torch.float32, device=dev)
+    routers = [lay[0] for lay in layers]
+
+    def step(i):
+        x = xs[i]
+        out, _, ids, _ = spec(x)
+        if cache.verify(ids.cpu()) == 0:          # accepted (touches every used expert)
+            outs[i].copy_(out)
+            return True
+        xl = x.view(1, H)
+        for l in range(N_LAYER):                    # decode_cached: router, ensure, layer
+            lid, _ = ops.router_topk(routers[l], xl, K_USED)
+            cache.ensure(l, lid.cpu().numpy().reshape(-1).tolist())
+            o, xl, _, _ = ops.ffn_layer(cached[l], xl, rms_eps=RMS_EPS)
+        outs[i].copy_(o.view(-1))
+        return False
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    st0 = cache.stats()
+    t0 = time.perf_counter()
+    accepted = sum(step(args.warmup + i) for i in range(args.steps))
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    st1 = cache.stats()
+
+    # the same tokens through the all-resident stack
+    ref = ops.DecodeStack(resident, RMS_EPS, keepalive=layers)
+    same = True
+    for i in range(args.warmup, n_steps):
+        o, _, _, _ = ref(xs[i], want_ids=False)
+        same &= bool(torch.equal(o.view(torch.int32), outs[i].view(torch.int32)))
+    torch.cuda.synchronize()
+    fetched = st1["fetch_bytes"] - st0["fetch_bytes"]
+    miss = st1["misses"] - st0["misses"]
+    line = {
+        "metric": "offloaded decode tok/s, 30B-A3B Q4_K MoE FFN stack, experts in pinned host memory, "
+                  f"{args.resident:.0%} of them in HBM slot pools",
+        "value": round(args.steps / wall, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(wall * 1e3 / args.steps, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "q4_K x q8_K -> f32",
+        "data": f"synthetic (seeded; router rows Zipf({args.zipf})-skewed)" if args.zipf > 0 else "synthetic (seeded)",
+        "config": {"workload": "configs[1] decode stack through the expert cache (RAM tier)", "n_layer": N_LAYER,
+                   "n_embd": H, "n_expert": E, "n_expert_used": K_USED, "n_ff_exp": F, "weights": "Q4_K",
+                   "resident_fraction": args.resident, "pool_slots": [p["n_slots"] for p in cache.pools()],
+                   "zipf": args.zipf, "scattered_fetch": "copy engine" if args.copy_engine else "gather kernel"},
+        "accepted_speculative": accepted, "repaired_per_layer": args.steps - accepted,
+        "misses_per_token": round(miss / args.steps, 2), "fetched_mb_per_token": round(fetched / args.steps / 1e6, 2),
+        "fetch_gbps_during_run": round(fetched / wall / 1e9, 2),
+        "cold_fill": {"bytes": fill_bytes, "seconds": round(fill_s, 4), "gbps": round(fill_bytes / fill_s / 1e9, 2)},
+        "h2d_probe_gbps": round(h2d_probe, 2),
+        "roofline": {"bound": "pcie", "achieved": round(fill_bytes / fill_s / 1e9, 2), "peak": 64.0, "unit": "GB/s",
+                     "frac": round(fill_bytes / fill_s / 1e9 / 64.0, 4), "traffic": None,
+                     "note": "cold fill of the pools through ensure(); peak = PCIe 5.0 x16 per direction"},
+        "matches_all_resident_bitwise": same,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+    spec.close()
+    ref.close()
+    cache.close()
+    return 0
+
+
 def copy_probe(mib: int = 1024, reps: int = 4) -> int:
     """A plain device copy of known size (torch's copy kernel): run under
     ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE`` it gives the factor between
@@ -260,8 +395,13 @@ def main() -> int:
                     help="text file whose 'hbm_bytes_per_launch = N' line is the HBM traffic of one decode "
                          "launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (copy-calibrated)")
     ap.add_argument("--copy-probe", action="store_true", help="run only the copy-kernel calibration probe")
-    ap.add_argument("--workload", choices=["decode", "prefill"], default="decode",
-                    help="decode: configs[1] (the headline line); prefill: configs[2]")
+    ap.add_argument("--workload", choices=["decode", "prefill", "expert_cache"], default="decode",
+                    help="decode: configs[1] (the headline line); prefill: configs[2]; expert_cache: configs[1] "
+                         "decode with the experts offloaded to pinned host memory")
+    ap.add_argument("--resident", type=float, default=0.5, help="expert_cache: fraction of experts in HBM")
+    ap.add_argument("--zipf", type=float, default=1.1, help="expert_cache: router skew (0: none)")
+    ap.add_argument("--copy-engine", action="store_true",
+                    help="expert_cache: every fetch by hipMemcpyAsync (no slab gather kernel)")
     ap.add_argument("--tokens", type=int, default=512, help="prefill batch size")
     ap.add_argument("--mfma-min-rows", type=int, default=1, help="prefill: experts with this many rows use MFMA")
     args = ap.parse_args()
@@ -273,6 +413,8 @@ def main() -> int:
         return copy_probe()
     if args.workload == "prefill":
         return prefill(args)
+    if args.workload == "expert_cache":
+        return expert_cache_bench(args)
 
     import numpy as np
     import torch

@@ -315,8 +315,9 @@ int qwmoe_gguf_load_moe_layer(void * stream, qwmoe_gguf * g, int il, void * dev,
  * (core/runtime.cpp:2921-2933) and repairs with ensure_resident.
  *
  * Tiers: host memory (each (role, layer) tensor's n_expert slabs back to back,
- * the RAM tier of cpp:355-364; pinned memory makes every fetch an asynchronous
- * DMA) or a file (slabs read with pread by a pool of worker threads into
+ * the RAM tier of cpp:355-364; from pinned memory, runs of consecutive slabs
+ * are copied by the copy engine and scattered slabs by one gather kernel per
+ * call, both asynchronous) or a file (slabs read with pread by a pool of worker threads into
  * pinned staging, then copied asynchronously: the SSD tier of cpp:297-352 and
  * 412-687, without the opt-in coalescing).  Every copy and row upload is
  * issued on the cache's stream, so work the caller issues on that stream
@@ -332,6 +333,7 @@ typedef struct qwmoe_expert_src {
 } qwmoe_expert_src;
 
 #define QWMOE_CACHE_DRY_RUN 1  /* bookkeeping only: no device pools, no copies, no file reads (planning, tests) */
+#define QWMOE_CACHE_COPY_ENGINE 2  /* host tier: every fetch by hipMemcpyAsync (no slab gather kernel) */
 
 typedef struct qwmoe_expert_cache_config {
     size_t vram_budget;        /* bytes the slot pools may take (core/expert_cache.h:43-45) */
@@ -392,6 +394,13 @@ const int32_t * qwmoe_expert_cache_slot_of_row(const qwmoe_expert_cache * c, int
  * that changes residency (the in-graph remap table g2s_all,
  * core/runtime.cpp:2877-2884).  NULL in a dry run. */
 const int32_t * qwmoe_expert_cache_device_row(const qwmoe_expert_cache * c, int role, int layer);
+/* The residency check of a speculative run (decode_cached_fast's verify and
+ * accept, core/runtime.cpp:2922-2934, 2959-2972): ids [n_layer][k] are the experts a
+ * whole-stack decode used (qwmoe_decode_stack_run's ids_out).  Returns how
+ * many (layer, id) entries miss in at least one role; when none does and
+ * `touch` is set, touches every role of every entry (hits, LRU stamps,
+ * counts).  Changes nothing otherwise. */
+int qwmoe_expert_cache_verify(qwmoe_expert_cache * c, const int32_t * ids, int n_layer, int k, int touch);
 /* Fills L's expert fields (types, pool bases, strides, slot counts, device
  * rows) for `layer`; the caller sets shapes, router and scale. */
 int qwmoe_expert_cache_layer(const qwmoe_expert_cache * c, int layer, qwmoe_layer * L);

@@ -130,6 +130,18 @@ class ExpertCachePolicy:
         p.clk[p.key2slot[key]] = self.clock
         self.hits += 1
 
+    def verify(self, ids, touch: bool = True) -> int:
+        """decode_cached_fast's residency check and accept (core/runtime.cpp:2922-2934,
+        2959-2972): ids [n_layer][k]; entries absent in any role, touching all when none is."""
+        missing = sum(1 for l, row in enumerate(ids) for e in row
+                      if not all(self.resident(r, l, e) for r in range(3)))
+        if missing == 0 and touch:
+            for l, row in enumerate(ids):
+                for e in row:
+                    for r in range(3):
+                        self.touch(r, l, e)
+        return missing
+
     def resident(self, role: int, layer: int, expert: int) -> bool:
         return layer * self.n_expert + expert in self.pool(role, layer).key2slot
 

@@ -105,6 +105,7 @@ SIGNATURES = {
     "qwmoe_expert_cache_ensure_resident": (I, [P, I, I]),
     "qwmoe_expert_cache_touch": (I, [P, I, I, I]),
     "qwmoe_expert_cache_resident": (I, [P, I, I, I]),
+    "qwmoe_expert_cache_verify": (I, [P, P, I, I, I]),
     "qwmoe_expert_cache_slot_of_row": (P, [P, I, I]),
     "qwmoe_expert_cache_device_row": (P, [P, I, I]),
     "qwmoe_expert_cache_layer": (I, [P, I, P]),
@@ -150,7 +151,7 @@ class ExpertCacheStats(C.Structure):
                 ("fetch_bytes", C.c_uint64)]
 
 
-CACHE_DRY_RUN = 1
+CACHE_DRY_RUN, CACHE_COPY_ENGINE = 1, 2
 
 _lib = None
 

@@ -15,9 +15,10 @@
 //
 // Mechanics, MI355X-first:
 //   * pools and the device row table [3][n_layer][n_expert] are one hipMalloc;
-//   * host tier: a miss is one hipMemcpyAsync from the (pinned) source slab into
-//     its slot on the cache's stream, as the RAM tier's ggml_backend_tensor_set_async
-//     (cpp:355-364);
+//   * host tier: misses go to their slots asynchronously on the cache's stream,
+//     as the RAM tier's ggml_backend_tensor_set_async (cpp:355-364): runs of
+//     consecutive slabs by the copy engine, scattered slabs of pinned sources by
+//     one gather kernel launch per call (slab_copy.hip);
 //   * file tier: misses of one call are read with pread by a persistent worker
 //     pool into one of two pinned 64 MiB stages while the other stage's slabs
 //     are being copied (cpp:412-687 reads into a pinned batch and uploads it);
@@ -46,6 +47,7 @@
 #include <vector>
 
 #include "../../include/qwmoe.h"
+#include "qw_slab_copy.hpp"
 
 namespace {
 
@@ -80,6 +82,7 @@ struct Pool {
 
 struct Source {
     const uint8_t* host = nullptr;            // host tier
+    const uint8_t* mapped = nullptr;          // its device-visible address when it is pinned, else null
     int file = -1;                            // file tier: index into the cache's files
     uint64_t offset = 0;
 };
@@ -192,6 +195,7 @@ struct qwmoe_expert_cache {
     bool row_pending[2] = {false, false};
     int row_next = 0;
     int io_threads = DEFAULT_IO_THREADS;
+    bool copy_engine_only = false;            // QWMOE_CACHE_COPY_ENGINE: no slab gather kernel
     Workers* workers = nullptr;
 
     ~qwmoe_expert_cache() {
@@ -275,15 +279,48 @@ struct qwmoe_expert_cache {
         set_row(p.role, key, 0);
     }
 
-    int fetch_host(const std::vector<Job>& js) {
-        for (const Job& j : js) {
-            const Pool& p = pools[j.pool];
-            const uint8_t* s = src[j.role][j.layer].host + (size_t) j.expert * p.slab;
-            if (hipMemcpyAsync(p.dev + (size_t) j.slot * p.slab, s, p.slab, hipMemcpyHostToDevice, stream) !=
-                hipSuccess)
+    // Host tier.  Installs whose source slabs and destination slots are both
+    // consecutive go as one copy-engine copy per run (a cold fill of a layer's
+    // experts is one copy per role).  The remaining single slabs of a pool go
+    // through the slab gather kernel, up to 64 per launch, when their source is
+    // pinned (device-mapped) memory; otherwise one copy each.
+    int fetch_host(std::vector<Job> js) {
+        std::sort(js.begin(), js.end(), [](const Job& a, const Job& b) {
+            return a.pool != b.pool ? a.pool < b.pool : a.slot < b.slot;
+        });
+        qw::SlabCopyArgs g{};
+        int g_pool = -1;
+        auto flush_gather = [&]() -> int {
+            if (g.n == 0) return QWMOE_OK;
+            const int rc = qw::launch_slab_copy(g, stream);
+            g.n = 0;
+            return rc == 0 ? QWMOE_OK : QWMOE_ERR_HIP;
+        };
+        for (size_t i = 0; i < js.size();) {
+            size_t n = 1;
+            while (i + n < js.size() && js[i + n].pool == js[i].pool && js[i + n].layer == js[i].layer &&
+                   js[i + n].slot == js[i].slot + (int) n && js[i + n].expert == js[i].expert + (int) n)
+                ++n;
+            const Pool& p = pools[js[i].pool];
+            const Source& sr = src[js[i].role][js[i].layer];
+            uint8_t* dst = p.dev + (size_t) js[i].slot * p.slab;
+            const size_t off = (size_t) js[i].expert * p.slab;
+            if (n == 1 && sr.mapped && !copy_engine_only && p.slab % 16 == 0) {
+                if (g_pool != js[i].pool || g.n == (uint32_t) qw::SLAB_COPY_MAX) {
+                    const int rc = flush_gather();
+                    if (rc != QWMOE_OK) return rc;
+                    g_pool = js[i].pool;
+                    g.bytes = p.slab;
+                }
+                g.src[g.n] = sr.mapped + off;
+                g.dst[g.n] = dst;
+                g.n++;
+            } else if (hipMemcpyAsync(dst, sr.host + off, n * p.slab, hipMemcpyHostToDevice, stream) != hipSuccess) {
                 return QWMOE_ERR_HIP;
+            }
+            i += n;
         }
-        return QWMOE_OK;
+        return flush_gather();
     }
 
     int ensure_stage() {
@@ -397,6 +434,27 @@ struct qwmoe_expert_cache {
 
 namespace {
 
+// The device-visible address of host range [p, p + n) when all of it is
+// pinned host memory of one allocation, else null (pageable memory is copied by
+// the copy engine only).
+const uint8_t* device_mapped(const void* p, size_t n) {
+    hipPointerAttribute_t a0, a1;
+    if (hipPointerGetAttributes(&a0, p) != hipSuccess) {
+        (void) hipGetLastError();
+        return nullptr;
+    }
+    const uint8_t* last = (const uint8_t*) p + (n - 1);
+    if (hipPointerGetAttributes(&a1, last) != hipSuccess) {
+        (void) hipGetLastError();
+        return nullptr;
+    }
+    if (a0.type != hipMemoryTypeHost || a1.type != hipMemoryTypeHost || !a0.devicePointer || !a1.devicePointer)
+        return nullptr;
+    if ((const uint8_t*) a1.devicePointer != (const uint8_t*) a0.devicePointer + (n - 1)) return nullptr;
+    if ((uintptr_t) a0.devicePointer % 16 != 0) return nullptr;
+    return (const uint8_t*) a0.devicePointer;
+}
+
 bool valid_role_layer(const qwmoe_expert_cache* c, int role, int layer) {
     return c && role >= 0 && role < N_ROLE && layer >= 0 && layer < c->n_layer;
 }
@@ -409,6 +467,7 @@ int build(qwmoe_expert_cache* c, void* stream, int n_layer, int n_expert, const 
     c->dry = (cfg->flags & QWMOE_CACHE_DRY_RUN) != 0;
     c->stream = c->dry ? nullptr : (hipStream_t) stream;
     c->io_threads = cfg->io_threads > 0 ? std::min(cfg->io_threads, 64) : DEFAULT_IO_THREADS;
+    c->copy_engine_only = (cfg->flags & QWMOE_CACHE_COPY_ENGINE) != 0;
 
     // (role, type, shape) signatures and the routing of every (role, layer)
     struct Sig {
@@ -429,6 +488,7 @@ int build(qwmoe_expert_cache* c, void* stream, int n_layer, int n_expert, const 
             const size_t slab = (size_t) rb * (size_t) s.ne1;
             if (s.host) {
                 c->src[r][il].host = (const uint8_t*) s.host;
+                if (!c->dry) c->src[r][il].mapped = device_mapped(s.host, slab * (size_t) n_expert);
             } else if (s.path) {
                 any_file = true;
                 int fi = -1;
@@ -733,6 +793,26 @@ int qwmoe_expert_cache_touch(qwmoe_expert_cache* c, int role, int layer, int exp
     p.clk[it->second] = ++c->clock;
     c->stats.hits++;
     return QWMOE_OK;
+}
+
+int qwmoe_expert_cache_verify(qwmoe_expert_cache* c, const int32_t* ids, int n_layer, int k, int touch) {
+    if (!c || !ids || n_layer < 0 || n_layer > c->n_layer || k < 0) return QWMOE_ERR_INVALID_ARG;
+    int missing = 0;
+    for (int l = 0; l < n_layer; ++l)
+        for (int i = 0; i < k; ++i) {
+            const int e = ids[(size_t) l * k + i];
+            if (e < 0 || e >= c->n_expert) return QWMOE_ERR_INVALID_ARG;
+            for (int r = 0; r < N_ROLE; ++r)
+                if (!c->pool_of(r, l).key2slot.count(l * c->n_expert + e)) {
+                    ++missing;
+                    break;
+                }
+        }
+    if (missing == 0 && touch)
+        for (int l = 0; l < n_layer; ++l)
+            for (int i = 0; i < k; ++i)
+                for (int r = 0; r < N_ROLE; ++r) qwmoe_expert_cache_touch(c, r, l, ids[(size_t) l * k + i]);
+    return missing;
 }
 
 int qwmoe_expert_cache_resident(const qwmoe_expert_cache* c, int role, int layer, int expert) {

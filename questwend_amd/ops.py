@@ -8,7 +8,7 @@ from __future__ import annotations
 
 import ctypes as C
 
-from . import (BLOCK, CACHE_DRY_RUN, Q8_0, Q8_K, ExpertCacheConfig, ExpertCacheStats, ExpertSrc, GgufTensorInfo, Layer,
+from . import (BLOCK, CACHE_COPY_ENGINE, CACHE_DRY_RUN, Q8_0, Q8_K, ExpertCacheConfig, ExpertCacheStats, ExpertSrc, GgufTensorInfo, Layer,
                MoeHparams, check, lib, row_size, vec_dot_type)
 
 
@@ -355,7 +355,7 @@ class ExpertCache:
     ROLES = ("gate", "up", "down")
 
     def __init__(self, n_layer: int, n_expert: int, sources, vram_budget: int, n_used: int, io_threads: int = 0,
-                 dry_run: bool = False, stream_handle=None, _handle=None):
+                 dry_run: bool = False, stream_handle=None, copy_engine: bool = False, _handle=None):
         self.n_layer, self.n_expert = n_layer, n_expert
         self._keep = []
         if _handle is not None:
@@ -373,7 +373,8 @@ class ExpertCache:
                     self._keep.append(b)
                     e.path = b
                     e.file_offset = s.get("file_offset", 0)
-        cfg = ExpertCacheConfig(vram_budget, n_used, io_threads, CACHE_DRY_RUN if dry_run else 0)
+        flags = (CACHE_DRY_RUN if dry_run else 0) | (CACHE_COPY_ENGINE if copy_engine else 0)
+        cfg = ExpertCacheConfig(vram_budget, n_used, io_threads, flags)
         h = C.c_void_p()
         st = None if dry_run else (stream_handle if stream_handle is not None else stream())
         check(lib().qwmoe_expert_cache_create(st, n_layer, n_expert, arr, C.byref(cfg), C.byref(h)),
@@ -442,6 +443,14 @@ class ExpertCache:
         r = lib().qwmoe_expert_cache_resident(self.h, role, layer, expert)
         check(min(r, 0), "expert_cache_resident")
         return r == 1
+
+    def verify(self, ids, touch: bool = True) -> int:
+        """ids: int32 [n_layer, k] (host array or tensor) -> entries missing in any role."""
+        import numpy as np
+        a = np.ascontiguousarray(ids.cpu().numpy() if hasattr(ids, "cpu") else ids, dtype=np.int32)
+        r = lib().qwmoe_expert_cache_verify(self.h, a.ctypes.data, a.shape[0], a.shape[1], int(touch))
+        check(min(r, 0), "expert_cache_verify")
+        return r
 
     def slot_of_row(self, role: int, layer: int) -> list[int]:
         p = lib().qwmoe_expert_cache_slot_of_row(self.h, role, layer)

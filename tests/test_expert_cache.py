@@ -188,11 +188,29 @@ def random_ops(rng, p: ExpertCachePolicy, n_ops: int):
             if rng.random() < 0.2:
                 ids = ids + [rng.choice(ids)]                     # a repeat within one call hits
             ops.append(("ensure", l, ids))
-        elif u < 0.85:
+        elif u < 0.8:
             ops.append(("touch", rng.randrange(3), l, rng.randrange(p.n_expert)))
-        else:
+        elif u < 0.9:
             ops.append(("ensure_resident", l, rng.randrange(p.n_expert)))
+        else:
+            k = min(p.n_expert, 4)
+            ids = [zipf_ids(rng, p.n_expert, k) for _ in range(rng.randint(1, p.n_layer))]
+            ops.append(("verify", ids))
     return ops
+
+
+def apply_both(c, p, op):
+    if op[0] == "ensure":
+        assert c.ensure(op[1], op[2]) == p.ensure(op[1], op[2])
+    elif op[0] == "touch":
+        c.touch(*op[1:])
+        p.touch(*op[1:])
+    elif op[0] == "verify":
+        import numpy as np
+        assert c.verify(np.array(op[1], np.int32)) == p.verify(op[1])
+    else:
+        c.ensure_resident(*op[1:])
+        p.ensure_resident(*op[1:])
 
 
 @pytest.mark.parametrize("seed", range(40))
@@ -209,6 +227,15 @@ def test_oracle_matches_ordered_lru(seed):
         elif op[0] == "touch":
             p.touch(*op[1:])
             q.touch(*op[1:])
+        elif op[0] == "verify":
+            miss = sum(1 for l, row in enumerate(op[1]) for e in row
+                       if any(l * q.E + e not in q.pools[q.layer_pool[r][l]]["lru"] for r in range(3)))
+            assert p.verify(op[1]) == miss
+            if miss == 0:
+                for l, row in enumerate(op[1]):
+                    for e in row:
+                        for r in range(3):
+                            q.touch(r, l, e)
         else:
             p.ensure_resident(*op[1:])
             q.ensure_resident(*op[1:])
@@ -269,14 +296,7 @@ def test_library_matches_oracle(seed, tmp_path):
         for r in range(3):
             assert c.pool_of(r, l) == p.layer_pool[r][l]
     for op in random_ops(rng, p, 250):
-        if op[0] == "ensure":
-            assert c.ensure(op[1], op[2]) == p.ensure(op[1], op[2])
-        elif op[0] == "touch":
-            c.touch(*op[1:])
-            p.touch(*op[1:])
-        else:
-            c.ensure_resident(*op[1:])
-            p.ensure_resident(*op[1:])
+        apply_both(c, p, op)
     assert_same(c, p)
     # profile file: byte for byte
     prof = tmp_path / "hot.txt"
@@ -288,14 +308,7 @@ def test_library_matches_oracle(seed, tmp_path):
     assert c2.load_prefetch(prof) == p2.load_prefetch(prof.read_text())
     assert_same(c2, p2)
     for op in random_ops(rng, p2, 100):
-        if op[0] == "ensure":
-            assert c2.ensure(op[1], op[2]) == p2.ensure(op[1], op[2])
-        elif op[0] == "touch":
-            c2.touch(*op[1:])
-            p2.touch(*op[1:])
-        else:
-            c2.ensure_resident(*op[1:])
-            p2.ensure_resident(*op[1:])
+        apply_both(c2, p2, op)
     assert_same(c2, p2)
 
 

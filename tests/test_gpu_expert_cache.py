@@ -95,10 +95,12 @@ def random_trace(rng, p, n):
         if u < 0.75:
             k = rng.randint(1, min(p.capacity(l), p.n_expert))
             ops_.append(("ensure", l, rng.sample(range(p.n_expert), k)))
-        elif u < 0.9:
+        elif u < 0.85:
             ops_.append(("touch", rng.randrange(3), l, rng.randrange(p.n_expert)))
-        else:
+        elif u < 0.95:
             ops_.append(("ensure_resident", l, rng.randrange(p.n_expert)))
+        else:
+            ops_.append(("verify", [rng.sample(range(p.n_expert), min(2, p.n_expert)) for _ in range(p.n_layer)]))
     return ops_
 
 
@@ -108,14 +110,20 @@ def apply(cache, p, op):
     elif op[0] == "touch":
         cache.touch(*op[1:])
         p.touch(*op[1:])
+    elif op[0] == "verify":
+        assert cache.verify(np.array(op[1], np.int32)) == p.verify(op[1])
     else:
         cache.ensure_resident(*op[1:])
         p.ensure_resident(*op[1:])
 
 
-def test_host_tier_pool_bytes(tmp_path):
-    """Three layers (two signatures), 16 experts, pinned random slabs, 30% resident."""
-    note("host tier: 3 layers, 16 experts, 30% resident, 120 calls + profile prefetch")
+@pytest.mark.parametrize("source", ["pinned", "pinned-copy-engine", "pageable"])
+def test_host_tier_pool_bytes(tmp_path, source):
+    """Three layers (two signatures), 16 experts, random slabs, 30% resident.
+    Pinned sources send scattered misses through the slab gather kernel (or,
+    with QWMOE_CACHE_COPY_ENGINE, the copy engine); pageable ones always use
+    the copy engine."""
+    note(f"host tier ({source}): 3 layers, 16 experts, 30% resident, 120 calls + profile prefetch")
     H, F, E, n_used = 256, 512, 16, 2
     types = [(Q4_K, Q4_K, Q6_K), (Q8_0, Q8_0, Q4_K), (Q4_K, Q4_K, Q6_K)]
     shapes = ((H, F), (H, F), (F, H))
@@ -125,14 +133,17 @@ def test_host_tier_pool_bytes(tmp_path):
         for l in range(3):
             t, (ne0, ne1) = types[l][r], shapes[r]
             slab = row_size(t, ne0) * ne1
-            host = torch.randint(0, 256, (E * slab,), dtype=torch.uint8, generator=g).pin_memory()
+            host = torch.randint(0, 256, (E * slab,), dtype=torch.uint8, generator=g)
+            if source != "pageable":
+                host = host.pin_memory()
             src[r][l] = host
             sigs[r][l] = (t, ne0, ne1, slab)
     total = sum(sigs[r][l][3] for r in range(3) for l in range(3)) * E
     budget = int(total * 0.3)
     srcs = [[{"type": sigs[r][l][0], "ne0": sigs[r][l][1], "ne1": sigs[r][l][2], "host": src[r][l].data_ptr()}
              for l in range(3)] for r in range(3)]
-    cache = ops.ExpertCache(3, E, srcs, budget, n_used)
+    ce = source == "pinned-copy-engine"
+    cache = ops.ExpertCache(3, E, srcs, budget, n_used, copy_engine=ce)
     p = ExpertCachePolicy(3, E, n_used, sigs, budget)
 
     def slab_bytes(r, l, e):
@@ -140,6 +151,10 @@ def test_host_tier_pool_bytes(tmp_path):
         return src[r][l][e * n:(e + 1) * n].numpy().tobytes()
 
     check_pools(cache, p, slab_bytes)                      # empty pools, rows all 0
+    # consecutive experts into consecutive empty slots: merged into one copy per pool
+    apply(cache, p, ("ensure", 0, [0, 1, 2, 3]))
+    apply(cache, p, ("ensure", 2, [5, 6, 9]))
+    check_pools(cache, p, slab_bytes)
     rng = random.Random(3)
     for i, op in enumerate(random_trace(rng, p, 120)):
         apply(cache, p, op)
@@ -149,7 +164,7 @@ def test_host_tier_pool_bytes(tmp_path):
     prof = tmp_path / "hot.txt"
     cache.save_profile(prof)
     assert prof.read_text() == p.profile_text()
-    c2 = ops.ExpertCache(3, E, srcs, budget, n_used)
+    c2 = ops.ExpertCache(3, E, srcs, budget, n_used, copy_engine=ce)
     p2 = ExpertCachePolicy(3, E, n_used, sigs, budget)
     assert c2.load_prefetch(prof) == p2.load_prefetch(prof.read_text())
     check_pools(c2, p2, slab_bytes)
@@ -278,16 +293,17 @@ def test_decode_stack_through_cache():
         out, xo, ids, _ = spec_stack(x)
         torch.cuda.synchronize()
         ids_h = ids.cpu().numpy()
-        if all(cl.resident_all(l, ids_h[l]) for l in range(n_layer)):
-            # accepted: the speculative run used resident experts only
+        all_res = all(cl.resident_all(l, ids_h[l]) for l in range(n_layer))
+        hits0 = cl.cache.stats()["hits"]
+        assert (cl.cache.verify(ids_h) == 0) == all_res
+        if all_res:
+            # accepted: the speculative run used resident experts only (verify touched them)
+            assert cl.cache.stats()["hits"] == hits0 + 3 * n_layer * k
             assert np.array_equal(bits(out), bits(ref_out)), f"token {t}: accepted speculative output"
             assert torch.equal(ids, ref_ids)
-            for l in range(n_layer):
-                for e in ids_h[l]:
-                    for r in range(3):
-                        cl.cache.touch(r, l, int(e))
             n_spec_ok += 1
             continue
+        assert cl.cache.stats()["hits"] == hits0
         # miss: per-layer path -- router, ensure, experts (decode_cached)
         n_fallback += 1
         xl = x.view(1, H)
