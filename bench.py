@@ -368,6 +368,79 @@ def expert_cache_bench(args) -> int:
     return 0
 
 
+def verify_bench(args) -> int:
+    """The configs[1] stack (48 Q4_K layers of the 30B-A3B shape) on the verify
+    batch of speculative decoding: T = 1..--tokens tokens (n_draft + 1) per step
+    through every layer (qwmoe_layer_stack: qwmoe_ffn_layer per layer, the chain
+    for each T replayed from one captured HIP graph), beside the same T tokens
+    decoded one launch each by the persistent decode stack."""
+    import numpy as np
+    import torch
+    from questwend_amd import Q4_K, ops, row_size
+
+    ops.init(0, 256 << 20)
+    layers = make_weights(torch, ops, Q4_K, args.seed)
+    Ls = [ops.make_layer(H, E, K_USED, F, r, g, u, d, (Q4_K,) * 3) for (r, g, u, d) in layers]
+    Tmax = max(1, args.tokens)
+    stack = ops.LayerStack(Ls, RMS_EPS, max_tokens=Tmax, keepalive=layers)
+    eager = ops.LayerStack(Ls, RMS_EPS, max_tokens=Tmax, graphs=False, keepalive=layers)
+    dstack = ops.DecodeStack(Ls, RMS_EPS, keepalive=layers)
+    xs = torch.empty((args.steps + args.warmup, Tmax, H), dtype=torch.float32, device="cuda:0")
+    ops.randn_(xs, args.seed + 999, 0.0, 1.0)
+    expert = 2 * F * row_size(Q4_K, H) + H * row_size(Q4_K, F)
+
+    def timed(fn, T):
+        for i in range(args.warmup):
+            fn(xs[i, :T])
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            fn(xs[args.warmup + i, :T])
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / args.steps
+
+    def dec(x):
+        for t in range(x.shape[0]):
+            dstack(x[t], want_ids=False)
+
+    rows, same = [], True
+    for T in range(1, Tmax + 1):
+        g_s = timed(lambda x: stack(x, want_ids=False), T)
+        e_s = timed(lambda x: eager(x, want_ids=False), T)
+        d_s = timed(dec, T)
+        o, _, ids, _ = stack(xs[0, :T])
+        o2, _, _, _ = eager(xs[0, :T])
+        torch.cuda.synchronize()
+        same &= bool(torch.equal(o.view(torch.int32), o2.view(torch.int32)))
+        uniq = sum(len(np.unique(ids[l].cpu().numpy())) for l in range(N_LAYER))
+        wbytes = uniq * expert + N_LAYER * E * H * 4
+        rows.append({"T": T, "graph_ms": round(g_s * 1e3, 3), "eager_ms": round(e_s * 1e3, 3),
+                     "decode_stack_x_T_ms": round(d_s * 1e3, 3), "verify_tok_s": round(T / g_s, 1),
+                     "unique_experts_per_layer": round(uniq / N_LAYER, 2),
+                     "weight_gbps": round(wbytes / g_s / 1e9, 1)})
+    last = rows[-1]
+    line = {
+        "metric": "verify-batch tok/s, 30B-A3B Q4_K MoE FFN stack (speculative-decoding verify forward, FFN half)",
+        "value": last["verify_tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": last["graph_ms"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q4_K x q8_K -> f32", "data": "synthetic (seeded)",
+        "config": {"workload": "configs[1] stack, T tokens per step through qwmoe_layer_stack", "n_layer": N_LAYER,
+                   "n_embd": H, "n_expert": E, "n_expert_used": K_USED, "n_ff_exp": F, "weights": "Q4_K",
+                   "tokens": Tmax},
+        "per_T": rows,
+        "graph_equals_eager_bitwise": same,
+        "roofline": {"bound": "hbm", "achieved": last["weight_gbps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(last["weight_gbps"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "note": "unique experts' weights + routers per step / step time"},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+    stack.close()
+    eager.close()
+    dstack.close()
+    return 0
+
+
 def copy_probe(mib: int = 1024, reps: int = 4) -> int:
     """A plain device copy of known size (torch's copy kernel): run under
     ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE`` it gives the factor between
@@ -395,26 +468,31 @@ def main() -> int:
                     help="text file whose 'hbm_bytes_per_launch = N' line is the HBM traffic of one decode "
                          "launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (copy-calibrated)")
     ap.add_argument("--copy-probe", action="store_true", help="run only the copy-kernel calibration probe")
-    ap.add_argument("--workload", choices=["decode", "prefill", "expert_cache"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "prefill", "expert_cache", "verify"], default="decode",
                     help="decode: configs[1] (the headline line); prefill: configs[2]; expert_cache: configs[1] "
-                         "decode with the experts offloaded to pinned host memory")
+                         "decode with the experts offloaded to pinned host memory; verify: configs[1] stack on "
+                         "T = 1..--tokens verify batches")
     ap.add_argument("--resident", type=float, default=0.5, help="expert_cache: fraction of experts in HBM")
     ap.add_argument("--zipf", type=float, default=1.1, help="expert_cache: router skew (0: none)")
     ap.add_argument("--copy-engine", action="store_true",
                     help="expert_cache: every fetch by hipMemcpyAsync (no slab gather kernel)")
-    ap.add_argument("--tokens", type=int, default=512, help="prefill batch size")
+    ap.add_argument("--tokens", type=int, default=None, help="prefill batch size (512); verify: largest T (4)")
     ap.add_argument("--mfma-min-rows", type=int, default=1, help="prefill: experts with this many rows use MFMA")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the sharding plan is "
               "documented, not built)", file=sys.stderr)
         return 2
+    if args.tokens is None:
+        args.tokens = 4 if args.workload == "verify" else 512
     if args.copy_probe:
         return copy_probe()
     if args.workload == "prefill":
         return prefill(args)
     if args.workload == "expert_cache":
         return expert_cache_bench(args)
+    if args.workload == "verify":
+        return verify_bench(args)
 
     import numpy as np
     import torch

@@ -217,6 +217,30 @@ int qwmoe_decode_stack_run(void * stream, qwmoe_decode_stack * s, const float * 
 int qwmoe_decode_stack_status(void * stream, qwmoe_decode_stack * s, int32_t * status_out, int clear);
 void qwmoe_decode_stack_free(qwmoe_decode_stack * s);
 
+/* ---- T-token batches through a layer stack (speculative-decoding verify) ------ */
+
+/* The FFN half of the verify forward: Runtime::decode_verify runs the model on
+ * the T = n_draft + 1 tokens of an MTP draft at once (core/runtime.cpp:1495-1562,
+ * driven by generate_mtp, 1628-1762), so every MoE layer sees a T-token batch
+ * with build_moe's T > 1 semantics (core/runtime.cpp:861-974).  Each layer is
+ * qwmoe_ffn_layer on the batch, RMSNorm between layers as in the decode stack.
+ * The chain for one T is captured into a HIP graph at its first run and
+ * replayed after that, as the reference keeps a persistent verify graph
+ * (1503-1525); mul_mat_id settings (qwmoe_set_mfma_min_rows) are those at
+ * capture.  Layers must share n_embd and n_expert_used.  Creation allocates the
+ * stack's buffers; the first run at each T captures and instantiates a graph;
+ * later runs allocate nothing. */
+#define QWMOE_STACK_NO_GRAPH 1     /* run the chain eagerly every time */
+typedef struct qwmoe_layer_stack qwmoe_layer_stack;
+int qwmoe_layer_stack_create(const qwmoe_layer * layers, int n_layer, float rms_eps, int max_tokens, int flags,
+                             qwmoe_layer_stack ** out);
+/* x [T][H] -> out [T][H] (MoE output of the last layer), x_out [T][H] (its
+ * RMSNorm, may be NULL), ids_out / weights_out [n_layer][T][k] (both or none).
+ * 1 <= T <= max_tokens. */
+int qwmoe_layer_stack_run(void * stream, qwmoe_layer_stack * s, const float * x, int64_t T, float * out,
+                          float * x_out, int32_t * ids_out, float * weights_out);
+void qwmoe_layer_stack_free(qwmoe_layer_stack * s);
+
 /* ---- expert slot table (host) ------------------------------------------------ */
 
 /* Resident-only counterpart of ExpertCache's slot bookkeeping

@@ -68,6 +68,9 @@ SIGNATURES = {
     "qwmoe_decode_stack_run": (I, [P, P, P, P, P, P, P]),
     "qwmoe_decode_stack_status": (I, [P, P, P, I]),
     "qwmoe_decode_stack_free": (None, [P]),
+    "qwmoe_layer_stack_create": (I, [P, I, F, I, I, P]),
+    "qwmoe_layer_stack_run": (I, [P, P, P, I64, P, P, P, P]),
+    "qwmoe_layer_stack_free": (None, [P]),
     "qwmoe_slot_table_create": (P, [I, I]),
     "qwmoe_slot_table_free": (None, [P]),
     "qwmoe_slot_table_fill": (I, [P, U64]),
@@ -152,6 +155,7 @@ class ExpertCacheStats(C.Structure):
 
 
 CACHE_DRY_RUN, CACHE_COPY_ENGINE = 1, 2
+STACK_NO_GRAPH = 1
 
 _lib = None
 

@@ -180,7 +180,6 @@ __device__ void quant_q8K_lds16(uint32_t* lds, const float* src, int nblocks, ui
 
 // 16-byte global loads through the global address space (a generic pointer
 // would become a flat load, which also occupies the LDS counter).
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(1))) const u32x4 g_u32x4;
 __device__ __forceinline__ u32x4 ldg16(const void* p) { return *(g_u32x4*) p; }
 // After a gather the polls were this thread's newest loads and have returned,

@@ -1,0 +1,148 @@
+// layer_stack.cpp -- a batch of T tokens through a stack of MoE FFN layers:
+// the FFN half of the verify forward of speculative decoding, where
+// Runtime::decode_verify runs the main model on the T = n_draft + 1 tokens of a
+// draft at once (core/runtime.cpp:1495-1562, driven by generate_mtp,
+// 1628-1762), and every layer's build_moe sees a T-token batch
+// (core/runtime.cpp:861-974: T > 1 takes the mul + add-chain weighted sum).
+//
+// Each layer is qwmoe_ffn_layer on the batch (router, grouping, gate/up/down
+// mul_mat_id, SwiGLU, weighted sum, RMSNorm into the next layer's input).  The
+// per-layer kernels are latency-bound at these T, so the whole chain for one T
+// is captured once into a HIP graph (on a private stream: capturing launches
+// nothing) and replayed on the caller's stream, as the reference keeps a
+// persistent verify graph (1503-1525).  The graph reads and writes only buffers
+// the stack owns; the caller's input and outputs are copied in and out around it.
+#include <hip/hip_runtime.h>
+
+#include <new>
+#include <vector>
+
+#include "../../include/qwmoe.h"
+
+struct qwmoe_layer_stack {
+    std::vector<qwmoe_layer> layers;
+    float rms_eps = 1e-6f;
+    int max_T = 0;
+    int64_t H = 0, k = 0;
+    bool graphs = true;
+    uint8_t* blk = nullptr;
+    float* xb[2] = {nullptr, nullptr};   // [max_T][H] ping-pong layer inputs
+    float* ob = nullptr;                 // [max_T][H] layer outputs
+    int32_t* ids = nullptr;              // [n_layer][max_T][k]
+    float* w = nullptr;                  // [n_layer][max_T][k]
+    hipStream_t cap = nullptr;           // capture stream
+    std::vector<hipGraphExec_t> exec;    // [T]: the captured chain, or null
+
+    ~qwmoe_layer_stack() {
+        for (hipGraphExec_t e : exec)
+            if (e) (void) hipGraphExecDestroy(e);
+        if (cap) (void) hipStreamDestroy(cap);
+        if (blk) (void) hipFree(blk);
+    }
+
+    // The chain for T tokens on stream st (eager, or recorded while capturing).
+    int enqueue(hipStream_t st, int64_t T) {
+        const int n = (int) layers.size();
+        for (int l = 0; l < n; ++l) {
+            const int rc = qwmoe_ffn_layer(st, &layers[(size_t) l], xb[l & 1], T, ob, rms_eps, xb[(l + 1) & 1],
+                                           ids + (size_t) l * max_T * k, w + (size_t) l * max_T * k);
+            if (rc != QWMOE_OK) return rc;
+        }
+        return QWMOE_OK;
+    }
+
+    int capture(int64_t T) {
+        if (!cap && hipStreamCreateWithFlags(&cap, hipStreamNonBlocking) != hipSuccess) return QWMOE_ERR_HIP;
+        if (hipStreamBeginCapture(cap, hipStreamCaptureModeThreadLocal) != hipSuccess) return QWMOE_ERR_HIP;
+        const int rc = enqueue(cap, T);
+        hipGraph_t g = nullptr;
+        const hipError_t ec = hipStreamEndCapture(cap, &g);
+        if (rc != QWMOE_OK || ec != hipSuccess || !g) {
+            if (g) (void) hipGraphDestroy(g);
+            (void) hipGetLastError();
+            return rc != QWMOE_OK ? rc : QWMOE_ERR_HIP;
+        }
+        hipGraphExec_t e = nullptr;
+        const hipError_t ei = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
+        (void) hipGraphDestroy(g);
+        if (ei != hipSuccess) return QWMOE_ERR_HIP;
+        exec[(size_t) T] = e;
+        return QWMOE_OK;
+    }
+};
+
+extern "C" {
+
+int qwmoe_layer_stack_create(const qwmoe_layer* layers, int n_layer, float rms_eps, int max_tokens, int flags,
+                             qwmoe_layer_stack** out) {
+    if (!out) return QWMOE_ERR_INVALID_ARG;
+    *out = nullptr;
+    if (!layers || n_layer <= 0 || max_tokens <= 0 || max_tokens > 64 || !(rms_eps >= 0.0f))
+        return QWMOE_ERR_INVALID_ARG;
+    const qwmoe_layer& L0 = layers[0];
+    for (int l = 1; l < n_layer; ++l)
+        if (layers[l].n_embd != L0.n_embd || layers[l].n_expert_used != L0.n_expert_used)
+            return QWMOE_ERR_INVALID_ARG;
+    if (L0.n_embd <= 0 || L0.n_expert_used <= 0) return QWMOE_ERR_INVALID_ARG;
+    auto* s = new (std::nothrow) qwmoe_layer_stack();
+    if (!s) return QWMOE_ERR_WORKSPACE;
+    s->layers.assign(layers, layers + n_layer);
+    s->rms_eps = rms_eps;
+    s->max_T = max_tokens;
+    s->H = L0.n_embd;
+    s->k = L0.n_expert_used;
+    s->graphs = (flags & QWMOE_STACK_NO_GRAPH) == 0;
+    s->exec.assign((size_t) max_tokens + 1, nullptr);
+    auto a256 = [](size_t n) { return (n + 255) & ~(size_t) 255; };
+    const size_t xs = a256((size_t) max_tokens * (size_t) s->H * 4);
+    const size_t is = a256((size_t) n_layer * (size_t) max_tokens * (size_t) s->k * 4);
+    if (hipMalloc(&s->blk, 3 * xs + 2 * is) != hipSuccess) {
+        s->blk = nullptr;
+        (void) hipGetLastError();
+        delete s;
+        return QWMOE_ERR_HIP;
+    }
+    s->xb[0] = (float*) s->blk;
+    s->xb[1] = (float*) (s->blk + xs);
+    s->ob = (float*) (s->blk + 2 * xs);
+    s->ids = (int32_t*) (s->blk + 3 * xs);
+    s->w = (float*) (s->blk + 3 * xs + is);
+    *out = s;
+    return QWMOE_OK;
+}
+
+int qwmoe_layer_stack_run(void* stream, qwmoe_layer_stack* s, const float* x, int64_t T, float* out, float* x_out,
+                          int32_t* ids_out, float* weights_out) {
+    if (!s || !x || !out || T <= 0 || T > s->max_T) return QWMOE_ERR_INVALID_ARG;
+    if ((ids_out == nullptr) != (weights_out == nullptr)) return QWMOE_ERR_INVALID_ARG;
+    hipStream_t st = (hipStream_t) stream;
+    const size_t xbytes = (size_t) T * (size_t) s->H * 4;
+    const int n = (int) s->layers.size();
+    if (hipMemcpyAsync(s->xb[0], x, xbytes, hipMemcpyDeviceToDevice, st) != hipSuccess) return QWMOE_ERR_HIP;
+    int rc;
+    if (s->graphs) {
+        if (!s->exec[(size_t) T] && (rc = s->capture(T)) != QWMOE_OK) return rc;
+        if (hipGraphLaunch(s->exec[(size_t) T], st) != hipSuccess) return QWMOE_ERR_HIP;
+    } else if ((rc = s->enqueue(st, T)) != QWMOE_OK) {
+        return rc;
+    }
+    if (hipMemcpyAsync(out, s->ob, xbytes, hipMemcpyDeviceToDevice, st) != hipSuccess) return QWMOE_ERR_HIP;
+    if (x_out && hipMemcpyAsync(x_out, s->xb[n & 1], xbytes, hipMemcpyDeviceToDevice, st) != hipSuccess)
+        return QWMOE_ERR_HIP;
+    if (ids_out) {
+        // [n_layer][T][k] from the stack's [n_layer][max_T][k]
+        const size_t row = (size_t) T * (size_t) s->k * 4, pitch = (size_t) s->max_T * (size_t) s->k * 4;
+        if (hipMemcpy2DAsync(ids_out, row, s->ids, pitch, row, (size_t) n, hipMemcpyDeviceToDevice, st) != hipSuccess ||
+            hipMemcpy2DAsync(weights_out, row, s->w, pitch, row, (size_t) n, hipMemcpyDeviceToDevice, st) != hipSuccess)
+            return QWMOE_ERR_HIP;
+    }
+    return QWMOE_OK;
+}
+
+void qwmoe_layer_stack_free(qwmoe_layer_stack* s) {
+    if (!s) return;
+    (void) hipDeviceSynchronize();
+    delete s;
+}
+
+}  // extern "C"

@@ -9,6 +9,8 @@
 //     AVX2 vec_dot bit for bit (arch/x86/quants.c:1308-1370, 2038-2115, 2426-2508):
 //     the same 8 integer lanes per super-block, the same fma chain over blocks and
 //     the same horizontal-sum tree.
+#include <type_traits>
+
 #include "qw_kernels.hpp"
 #include "qw_rowdot.hpp"
 
@@ -207,6 +209,14 @@ int launch_group(const GroupArgs& g, hipStream_t stream) {
 constexpr int MMID_ROWS = 32;   // rows per workgroup (8 per wave)
 constexpr int MMID_CT = 16;     // activation rows staged per pass
 constexpr int MMID_NT = 4;      // activation rows per row-dot call
+constexpr int MMID_LD = 8;      // staging loads per thread in flight together
+
+// Activation rows staged per pass: MMID_CT, or fewer when no bin can hold more
+// rows (max_rows bounds the rows of one bin), so small batches take less LDS and
+// more workgroups fit on a CU.  More rows than this only mean more passes.
+__host__ __device__ inline int mmid_stage_rows(int64_t max_rows) {
+    return max_rows < 1 ? 1 : max_rows < MMID_CT ? (int) max_rows : MMID_CT;
+}
 
 __host__ __device__ inline uint32_t mmid_slot_bytes(size_t row_bytes) {
     return (uint32_t) (((row_bytes + 15 + 15) / 16) * 16 + 16);
@@ -232,17 +242,43 @@ __global__ void __launch_bounds__(256) k_mmid_gemv(MmidArgs m) {
     const size_t row_bytes = (size_t) (m.K / block_elems(TYPE)) * block_bytes(TYPE);
     const uint32_t RS = mmid_slot_bytes(row_bytes);
     const uint8_t* wmat = m.w + (size_t) mat * m.nb2;
-    // stage the weight rows: each row as its 16-byte aligned superset
+    // stage the weight rows: each row as its 16-byte aligned superset, in rounds
+    // of MMID_LD loads per thread issued together (one memory latency per round)
     const int nchmax = (int) ((row_bytes + 15) / 16) + 1;
-    for (int idx = threadIdx.x; idx < nrows * nchmax; idx += 256) {
-        const int r = idx / nchmax, c = idx % nchmax;
-        const uint8_t* src = wmat + (size_t) (r0 + r) * m.nb1;
-        const uintptr_t s0 = (uintptr_t) src & ~(uintptr_t) 15;
-        const uintptr_t s1 = ((uintptr_t) src + row_bytes + 15) & ~(uintptr_t) 15;
-        if (c < (int) ((s1 - s0) / 16)) ((uint4*) (lds + (r * RS) / 4))[c] = ((const uint4*) s0)[c];
+    for (int base = 0; base < nrows * nchmax; base += MMID_LD * 256) {
+        u32x4 v[MMID_LD];
+        bool ok[MMID_LD];
+#pragma unroll
+        for (int j = 0; j < MMID_LD; ++j) {
+            const int idx = base + threadIdx.x + j * 256;
+            const int r = idx / nchmax, c = idx % nchmax;
+            const uint8_t* src = wmat + (size_t) (r0 + (r < nrows ? r : 0)) * m.nb1;
+            const uintptr_t s0 = (uintptr_t) src & ~(uintptr_t) 15;
+            const uintptr_t s1 = ((uintptr_t) src + row_bytes + 15) & ~(uintptr_t) 15;
+            ok[j] = idx < nrows * nchmax && c < (int) ((s1 - s0) / 16);
+            v[j] = ((const u32x4*) s0)[ok[j] ? c : 0];   // (a row's first chunk when unused)
+        }
+#pragma unroll
+        for (int j = 0; j < MMID_LD; ++j) {
+            const int idx = base + threadIdx.x + j * 256;
+            if (ok[j]) ((u32x4*) (lds + ((idx / nchmax) * RS) / 4))[idx % nchmax] = v[j];
+        }
     }
     const uint32_t ABASE = RS * MMID_ROWS;  // activation staging follows the weights
     const uint32_t ARS = (uint32_t) (((m.act_row_bytes + 3) / 4) * 4 + 16);
+    // Q4_K: the scales of every staged block, unpacked once (table after the
+    // activation staging, 16 bytes per (row, block))
+    const uint32_t STAB = (ABASE + (uint32_t) mmid_stage_rows(m.max_rows) * ARS + 15u) & ~15u;
+    if constexpr (TYPE == T_Q4_K) {
+        const int nbk = (int) (m.K / QK_K);
+        __syncthreads();   // rows staged
+        for (int idx = threadIdx.x; idx < nrows * nbk; idx += 256) {
+            const int r = idx / nbk, b = idx - r * nbk;
+            const uint32_t blk = (uint32_t) r * RS + (uint32_t) ((uintptr_t) (wmat + (size_t) (r0 + r) * m.nb1) & 15) +
+                                 144u * (uint32_t) b;
+            *(u32x4*) (lds + ((STAB + 16u * (uint32_t) idx) >> 2)) = q4k_scale_words(lds, blk);
+        }
+    }
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int rl = wave * 8 + (lane >> 3);  // row within the tile
     const int n = lane & 7;
@@ -250,10 +286,13 @@ __global__ void __launch_bounds__(256) k_mmid_gemv(MmidArgs m) {
     const int rrow = rvalid ? rl : 0;
     const uint32_t wbase = rrow * RS + (uint32_t) ((uintptr_t) (wmat + (size_t) (r0 + rrow) * m.nb1) & 15);
     const int nb = (int) (m.K / block_elems(TYPE));
+    // every staged row 4-byte aligned in LDS (uniform per workgroup)
+    const bool w_al = (((uintptr_t) wmat | (uintptr_t) m.nb1) & 3) == 0;
     const int p0 = m.active_off[g], p1 = m.active_off[g + 1];
     const int nw = (int) ((m.act_row_bytes + 3) / 4);
-    for (int pc = p0; pc < p1; pc += MMID_CT) {
-        const int cnt = (p1 - pc) < MMID_CT ? (p1 - pc) : MMID_CT;
+    const int CT = mmid_stage_rows(m.max_rows);
+    for (int pc = p0; pc < p1; pc += CT) {
+        const int cnt = (p1 - pc) < CT ? (p1 - pc) : CT;
         __syncthreads();  // weights staged / previous chunk consumed
         if (threadIdx.x < cnt) {
             const int e = m.rows[2 * (pc + threadIdx.x)], t = m.rows[2 * (pc + threadIdx.x) + 1];
@@ -262,30 +301,63 @@ __global__ void __launch_bounds__(256) k_mmid_gemv(MmidArgs m) {
             s_chunk[threadIdx.x][2] = (int) ((int64_t) (e % m.b_ne1) + (int64_t) t * m.b_ne1);
         }
         __syncthreads();
-        // all activation rows of the chunk in one cooperative pass
-        for (int idx = threadIdx.x; idx < cnt * nw; idx += 256) {
-            const int tk = idx / nw, c = idx - tk * nw;
-            const uint32_t* src = (const uint32_t*) (m.act_q + (size_t) s_chunk[tk][2] * m.act_row_bytes);
-            lds[(ABASE + tk * ARS) / 4 + c] = src[c];
+        // all activation rows of the chunk in one cooperative pass, MMID_LD loads
+        // per thread in flight at a time
+        for (int base = 0; base < cnt * nw; base += MMID_LD * 256) {
+            uint32_t v[MMID_LD];
+#pragma unroll
+            for (int j = 0; j < MMID_LD; ++j) {
+                const int idx = min(base + (int) threadIdx.x + j * 256, cnt * nw - 1);
+                const int tk = idx / nw, c = idx - tk * nw;
+                v[j] = ((const uint32_t*) (m.act_q + (size_t) s_chunk[tk][2] * m.act_row_bytes))[c];
+            }
+#pragma unroll
+            for (int j = 0; j < MMID_LD; ++j) {
+                const int idx = base + (int) threadIdx.x + j * 256;
+                if (idx < cnt * nw) {
+                    const int tk = idx / nw, c = idx - tk * nw;
+                    lds[(ABASE + tk * ARS) / 4 + c] = v[j];
+                }
+            }
         }
         __syncthreads();
-        // MMID_NT activation rows per row-dot call: the weight bits are unpacked
-        // once per block (rows past cnt repeat the last one and are not stored)
-        for (int tk0 = 0; tk0 < cnt; tk0 += MMID_NT) {
-            uint32_t ab[MMID_NT];
+        // up to MMID_NT activation rows per row-dot call (4, 2 or 1, as many as are
+        // left): the weight bits are unpacked once per block for all of them
+        auto rows_dot = [&](auto nt_tag, int tk0) {
+            constexpr int NT = decltype(nt_tag)::value;
+            uint32_t ab[NT];
 #pragma unroll
-            for (int u = 0; u < MMID_NT; ++u) ab[u] = ABASE + (uint32_t) min(tk0 + u, cnt - 1) * ARS;
-            float v[MMID_NT];
-            row_dot_lds_mt<TYPE, MMID_NT>(lds, wbase, ab, nb, n, v);
+            for (int u = 0; u < NT; ++u) ab[u] = ABASE + (uint32_t) (tk0 + u) * ARS;
+            float v[NT];
+            if constexpr (TYPE == T_Q4_K) {
+                const uint32_t tab = STAB + 16u * (uint32_t) (rrow * nb);
+                if (w_al) row_dot_q4k_mt_tab<true, NT>(lds, wbase, tab, ab, nb, n, v);
+                else row_dot_q4k_mt_tab<false, NT>(lds, wbase, tab, ab, nb, n, v);
+            } else if constexpr (TYPE == T_Q6_K) {
+                row_dot_q6k_mt<NT>(lds, wbase, ab, nb, n, v);
+            } else {
+                row_dot_q80_mt<NT>(lds, wbase, ab, nb, n, v);
+            }
             if (rvalid && n == 0) {
 #pragma unroll
-                for (int u = 0; u < MMID_NT; ++u) {
-                    if (tk0 + u < cnt) {
-                        const int e = s_chunk[tk0 + u][0], t = s_chunk[tk0 + u][1];
-                        float* d = (float*) ((char*) m.dst + (size_t) e * m.dst_nb1 + (size_t) t * m.dst_nb2);
-                        d[r0 + rl] = v[u];
-                    }
+                for (int u = 0; u < NT; ++u) {
+                    const int e = s_chunk[tk0 + u][0], t = s_chunk[tk0 + u][1];
+                    float* d = (float*) ((char*) m.dst + (size_t) e * m.dst_nb1 + (size_t) t * m.dst_nb2);
+                    d[r0 + rl] = v[u];
                 }
+            }
+        };
+        for (int tk0 = 0; tk0 < cnt;) {
+            const int rem = cnt - tk0;
+            if (rem >= 4) {
+                rows_dot(std::integral_constant<int, 4>{}, tk0);
+                tk0 += 4;
+            } else if (rem >= 2) {
+                rows_dot(std::integral_constant<int, 2>{}, tk0);
+                tk0 += 2;
+            } else {
+                rows_dot(std::integral_constant<int, 1>{}, tk0);
+                tk0 += 1;
             }
         }
     }
@@ -293,8 +365,9 @@ __global__ void __launch_bounds__(256) k_mmid_gemv(MmidArgs m) {
 
 int launch_mmid_gemv(const MmidArgs& m, hipStream_t stream) {
     const size_t row_bytes = (size_t) (m.K / block_elems(m.type)) * block_bytes(m.type);
-    const size_t lds_bytes = (size_t) mmid_slot_bytes(row_bytes) * MMID_ROWS +
-                             (size_t) MMID_CT * (((m.act_row_bytes + 3) / 4) * 4 + 16);
+    size_t lds_bytes = (size_t) mmid_slot_bytes(row_bytes) * MMID_ROWS +
+                       (size_t) mmid_stage_rows(m.max_rows) * (((m.act_row_bytes + 3) / 4) * 4 + 16);
+    if (m.type == T_Q4_K) lds_bytes = ((lds_bytes + 15) & ~(size_t) 15) + (size_t) MMID_ROWS * (m.K / QK_K) * 16;
     if (lds_bytes > 160 * 1024) return -2;
     dim3 grid((unsigned) ((m.N + MMID_ROWS - 1) / MMID_ROWS), (unsigned) m.max_active);
     if (grid.y == 0) return 0;

@@ -12,6 +12,9 @@
 
 namespace qw {
 
+// Native 4 x u32 vector (arrays of it stay in registers, unlike arrays of uint4).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
 constexpr int QK_K = 256;
 constexpr int QK8_0 = 32;
 constexpr int WAVE = 64;

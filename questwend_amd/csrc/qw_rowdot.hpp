@@ -196,17 +196,20 @@ __device__ __forceinline__ void reduce8_mt(const float* acc, float* out) {
     }
 }
 
-template <>
-__device__ __forceinline__ void row_dot_lds_mt<T_Q4_K, 4>(const uint32_t* lds, uint32_t wbase, const uint32_t* abase,
-                                                          int nb, int n, float* out) {
-    constexpr int NT = 4;
+// AL: the weight row starts 4-byte aligned in LDS (every 144-byte block then
+// does too) and is read one word per load; the activation rows (Q8_K, 292-byte
+// blocks, 4-byte aligned staging) always are.
+template <bool AL, int NT>
+__device__ __forceinline__ void row_dot_q4k_mt(const uint32_t* lds, uint32_t wbase, const uint32_t* abase, int nb,
+                                               int n, float* out) {
+    auto rw = [&](uint32_t off) { return AL ? lds_u32a(lds, off) : lds_u32(lds, off); };
     float acc[NT], accm[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = accm[t] = 0.0f;
     for (int b = 0; b < nb; ++b) {
         const uint32_t blk = wbase + 144u * b;
-        const uint32_t h0 = lds_u32(lds, blk);
-        const uint32_t s0 = lds_u32(lds, blk + 4), s1 = lds_u32(lds, blk + 8), s2 = lds_u32(lds, blk + 12);
+        const uint32_t h0 = rw(blk);
+        const uint32_t s0 = rw(blk + 4), s1 = rw(blk + 8), s2 = rw(blk + 12);
         const uint8_t q[12] = {(uint8_t) s0, (uint8_t) (s0 >> 8), (uint8_t) (s0 >> 16), (uint8_t) (s0 >> 24),
                                (uint8_t) s1, (uint8_t) (s1 >> 8), (uint8_t) (s1 >> 16), (uint8_t) (s1 >> 24),
                                (uint8_t) s2, (uint8_t) (s2 >> 8), (uint8_t) (s2 >> 16), (uint8_t) (s2 >> 24)};
@@ -215,7 +218,7 @@ __device__ __forceinline__ void row_dot_lds_mt<T_Q4_K, 4>(const uint32_t* lds, u
         int lo[4], hi[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const uint32_t wq = lds_u32(lds, blk + 16 + 32 * j + 4 * n);
+            const uint32_t wq = rw(blk + 16 + 32 * j + 4 * n);
             lo[j] = (int) (wq & 0x0F0F0F0Fu);
             hi[j] = (int) ((wq >> 4) & 0x0F0F0F0Fu);
         }
@@ -226,14 +229,14 @@ __device__ __forceinline__ void row_dot_lds_mt<T_Q4_K, 4>(const uint32_t* lds, u
             int sumi = 0;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int alo = (int) lds_u32(lds, yb + 4 + 64 * j + 4 * n);
-                const int ahi = (int) lds_u32(lds, yb + 4 + 64 * j + 32 + 4 * n);
+                const int alo = (int) lds_u32a(lds, yb + 4 + 64 * j + 4 * n);
+                const int ahi = (int) lds_u32a(lds, yb + 4 + 64 * j + 32 + 4 * n);
                 sumi += mul24(sc[2 * j], sdot4(lo[j], alo, 0)) + mul24(sc[2 * j + 1], sdot4(hi[j], ahi, 0));
             }
-            const float yd = lds_f32(lds, yb);
+            const float yd = bitsf(lds_u32a(lds, yb));
             acc[t] = __builtin_fmaf(yd * wd, (float) sumi, acc[t]);
             const int nn = n & 3;
-            const uint32_t bs01 = lds_u32(lds, yb + 260 + 8 * nn), bs23 = lds_u32(lds, yb + 260 + 8 * nn + 4);
+            const uint32_t bs01 = lds_u32a(lds, yb + 260 + 8 * nn), bs23 = lds_u32a(lds, yb + 260 + 8 * nn + 4);
             const int q8s0 = (int) (int16_t) (bs01 & 0xffff) + (int) (int16_t) (bs01 >> 16);
             const int q8s1 = (int) (int16_t) (bs23 & 0xffff) + (int) (int16_t) (bs23 >> 16);
             const int prod = mul24(mn[2 * nn], q8s0) + mul24(mn[2 * nn + 1], q8s1);
@@ -254,9 +257,91 @@ __device__ __forceinline__ void row_dot_lds_mt<T_Q4_K, 4>(const uint32_t* lds, u
 }
 
 template <>
-__device__ __forceinline__ void row_dot_lds_mt<T_Q6_K, 4>(const uint32_t* lds, uint32_t wbase, const uint32_t* abase,
+__device__ __forceinline__ void row_dot_lds_mt<T_Q4_K, 4>(const uint32_t* lds, uint32_t wbase, const uint32_t* abase,
                                                           int nb, int n, float* out) {
-    constexpr int NT = 4;
+    row_dot_q4k_mt<false, 4>(lds, wbase, abase, nb, n, out);
+}
+
+// The six-bit scales and mins of one Q4_K block, unpacked once (get_scale_min_k4)
+// into four words: sc[0..3], sc[4..7], mn[0..3], mn[4..7], one per byte.
+__device__ __forceinline__ u32x4 q4k_scale_words(const uint32_t* lds, uint32_t blk) {
+    const uint32_t s0 = lds_u32(lds, blk + 4), s1 = lds_u32(lds, blk + 8), s2 = lds_u32(lds, blk + 12);
+    const uint8_t q[12] = {(uint8_t) s0, (uint8_t) (s0 >> 8), (uint8_t) (s0 >> 16), (uint8_t) (s0 >> 24),
+                           (uint8_t) s1, (uint8_t) (s1 >> 8), (uint8_t) (s1 >> 16), (uint8_t) (s1 >> 24),
+                           (uint8_t) s2, (uint8_t) (s2 >> 8), (uint8_t) (s2 >> 16), (uint8_t) (s2 >> 24)};
+    u32x4 w = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        int d, m;
+        scale_min_k4(j, q, d, m);
+        w[j >> 2] |= (uint32_t) d << (8 * (j & 3));
+        w[2 + (j >> 2)] |= (uint32_t) m << (8 * (j & 3));
+    }
+    return w;
+}
+
+// row_dot_q4k_mt with the block scales read from a table of q4k_scale_words
+// (tab: the row's first block entry, 16 bytes per block).  Same integers and
+// float order.
+template <bool AL, int NT>
+__device__ __forceinline__ void row_dot_q4k_mt_tab(const uint32_t* lds, uint32_t wbase, uint32_t tab,
+                                                   const uint32_t* abase, int nb, int n, float* out) {
+    auto rw = [&](uint32_t off) { return AL ? lds_u32a(lds, off) : lds_u32(lds, off); };
+    float acc[NT], accm[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = accm[t] = 0.0f;
+    const int nn = n & 3;
+    for (int b = 0; b < nb; ++b) {
+        const uint32_t blk = wbase + 144u * b;
+        const uint32_t h0 = rw(blk);
+        const u32x4 sw = *(const u32x4*) (lds + ((tab + 16u * b) >> 2));
+        int sc[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sc[j] = (int) ((sw[j >> 2] >> (8 * (j & 3))) & 0xffu);
+        const uint32_t mw = nn < 2 ? sw[2] : sw[3];
+        const int mn0 = (int) ((mw >> (16 * (nn & 1))) & 0xffu), mn1 = (int) ((mw >> (16 * (nn & 1) + 8)) & 0xffu);
+        int lo[4], hi[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t wq = rw(blk + 16 + 32 * j + 4 * n);
+            lo[j] = (int) (wq & 0x0F0F0F0Fu);
+            hi[j] = (int) ((wq >> 4) & 0x0F0F0F0Fu);
+        }
+        const float wd = h2f((uint16_t) (h0 & 0xffff)), wdm = h2f((uint16_t) (h0 >> 16));
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const uint32_t yb = abase[t] + 292u * b;
+            int sumi = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int alo = (int) lds_u32a(lds, yb + 4 + 64 * j + 4 * n);
+                const int ahi = (int) lds_u32a(lds, yb + 4 + 64 * j + 32 + 4 * n);
+                sumi += mul24(sc[2 * j], sdot4(lo[j], alo, 0)) + mul24(sc[2 * j + 1], sdot4(hi[j], ahi, 0));
+            }
+            const float yd = bitsf(lds_u32a(lds, yb));
+            acc[t] = __builtin_fmaf(yd * wd, (float) sumi, acc[t]);
+            const uint32_t bs01 = lds_u32a(lds, yb + 260 + 8 * nn), bs23 = lds_u32a(lds, yb + 260 + 8 * nn + 4);
+            const int q8s0 = (int) (int16_t) (bs01 & 0xffff) + (int) (int16_t) (bs01 >> 16);
+            const int q8s1 = (int) (int16_t) (bs23 & 0xffff) + (int) (int16_t) (bs23 >> 16);
+            const int prod = mul24(mn0, q8s0) + mul24(mn1, q8s1);
+            const float pm = __builtin_fmaf(-yd * wdm, (float) prod, accm[t]);
+            accm[t] = n < 4 ? pm : accm[t];
+        }
+    }
+    float a[NT];
+    reduce8_mt<NT>(acc, a);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        float mm = accm[t];
+        mm = mm + __shfl_down(mm, 2, 8);
+        mm = mm + __shfl_down(mm, 1, 8);
+        out[t] = a[t] + mm;
+    }
+}
+
+template <int NT>
+__device__ __forceinline__ void row_dot_q6k_mt(const uint32_t* lds, uint32_t wbase, const uint32_t* abase, int nb,
+                                               int n, float* out) {
     float acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
@@ -290,24 +375,23 @@ __device__ __forceinline__ void row_dot_lds_mt<T_Q6_K, 4>(const uint32_t* lds, u
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 const uint32_t y = yb + 4 + 128 * j + 4 * n;
-                sumi += mul24(sc[8 * j + 0 + g], sdot4(q6[j][0], (int) lds_u32(lds, y), 0));
-                sumi += mul24(sc[8 * j + 2 + g], sdot4(q6[j][1], (int) lds_u32(lds, y + 32), 0));
-                sumi += mul24(sc[8 * j + 4 + g], sdot4(q6[j][2], (int) lds_u32(lds, y + 64), 0));
-                sumi += mul24(sc[8 * j + 6 + g], sdot4(q6[j][3], (int) lds_u32(lds, y + 96), 0));
+                sumi += mul24(sc[8 * j + 0 + g], sdot4(q6[j][0], (int) lds_u32a(lds, y), 0));
+                sumi += mul24(sc[8 * j + 2 + g], sdot4(q6[j][1], (int) lds_u32a(lds, y + 32), 0));
+                sumi += mul24(sc[8 * j + 4 + g], sdot4(q6[j][2], (int) lds_u32a(lds, y + 64), 0));
+                sumi += mul24(sc[8 * j + 6 + g], sdot4(q6[j][3], (int) lds_u32a(lds, y + 96), 0));
             }
-            const uint32_t bs = lds_u32(lds, yb + 260 + 4 * n);
+            const uint32_t bs = lds_u32a(lds, yb + 260 + 4 * n);
             sumi -= 32 * (mul24((int) (int16_t) (bs & 0xffff), sc[2 * n]) + mul24((int) (int16_t) (bs >> 16), sc[2 * n + 1]));
-            const float d = lds_f32(lds, yb) * wd;
+            const float d = bitsf(lds_u32a(lds, yb)) * wd;
             acc[t] = __builtin_fmaf(d, (float) sumi, acc[t]);
         }
     }
     reduce8_mt<NT>(acc, out);
 }
 
-template <>
-__device__ __forceinline__ void row_dot_lds_mt<T_Q8_0, 4>(const uint32_t* lds, uint32_t wbase, const uint32_t* abase,
-                                                          int nb, int n, float* out) {
-    constexpr int NT = 4;
+template <int NT>
+__device__ __forceinline__ void row_dot_q80_mt(const uint32_t* lds, uint32_t wbase, const uint32_t* abase, int nb,
+                                               int n, float* out) {
     float acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
@@ -324,6 +408,18 @@ __device__ __forceinline__ void row_dot_lds_mt<T_Q8_0, 4>(const uint32_t* lds, u
         }
     }
     reduce8_mt<NT>(acc, out);
+}
+
+template <>
+__device__ __forceinline__ void row_dot_lds_mt<T_Q6_K, 4>(const uint32_t* lds, uint32_t wbase, const uint32_t* abase,
+                                                          int nb, int n, float* out) {
+    row_dot_q6k_mt<4>(lds, wbase, abase, nb, n, out);
+}
+
+template <>
+__device__ __forceinline__ void row_dot_lds_mt<T_Q8_0, 4>(const uint32_t* lds, uint32_t wbase, const uint32_t* abase,
+                                                          int nb, int n, float* out) {
+    row_dot_q80_mt<4>(lds, wbase, abase, nb, n, out);
 }
 
 }  // namespace qw

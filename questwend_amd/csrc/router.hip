@@ -11,53 +11,78 @@
 
 namespace qw {
 
-constexpr int ROUTER_TT = 4;  // tokens per wave in the logits kernel
+constexpr int ROUTER_STEPS = 16; // 32-element steps whose loads are in flight together
 
-// logits[t][e] = vec_dot_f32(H, W[e], x[t]).  One wave = 8 experts x ROUTER_TT
-// tokens; lane (g, m) owns the four fma chains c = 4m..4m+3 of expert g, i.e.
-// elements i == c (mod 32), exactly the 32 chains of the AVX reduction.
-__global__ void __launch_bounds__(64) k_router_logits(const float* __restrict__ W, const float* __restrict__ x,
-                                                      int64_t x_stride, int64_t H, int64_t E, int64_t T,
-                                                      float* __restrict__ logits) {
-    const int lane = threadIdx.x;
-    const int g = lane >> 3, m = lane & 7;
-    const int64_t e = (int64_t) blockIdx.x * 8 + g;
+// logits[t][e] = vec_dot_f32(H, W[e], x[t]).  A group of 32 lanes owns one
+// expert: lane c is the fma chain c of the AVX reduction (elements i == c mod
+// 32, in order), for ROUTER_TT tokens at once; a workgroup holds EPW experts.
+// The loads of ROUTER_STEPS steps are issued together and the next batch is in
+// flight while the current one is accumulated, so a chain waits for memory once
+// per batch, not once per step.  Small batches take one token per group and two
+// experts per workgroup, for more workgroups.
+template <int ROUTER_TT, int EPW>
+__global__ void __launch_bounds__(32 * EPW) k_router_logits(const float* __restrict__ W, const float* __restrict__ x,
+                                                            int64_t x_stride, int64_t H, int64_t E, int64_t T,
+                                                            float* __restrict__ logits) {
+    const int c = threadIdx.x & 31;
+    const int64_t e = (int64_t) blockIdx.x * EPW + (threadIdx.x >> 5);
     const int64_t t0 = (int64_t) blockIdx.y * ROUTER_TT;
     const int64_t np = H & ~(int64_t) 31;
+    const int64_t ns = np / 32;                       // steps
     const bool ev = e < E;
-    const float* w = W + (ev ? e : 0) * H;
-    float acc[ROUTER_TT][4];
-    for (int tt = 0; tt < ROUTER_TT; ++tt)
-        for (int r = 0; r < 4; ++r) acc[tt][r] = 0.0f;
-    for (int64_t s = 0; s < np; s += 32) {
-        const float4 wv = *(const float4*) (w + s + 4 * m);
-        for (int tt = 0; tt < ROUTER_TT; ++tt) {
-            const int64_t t = t0 + tt < T ? t0 + tt : T - 1;
-            const float4 xv = *(const float4*) (x + t * x_stride + s + 4 * m);
-            acc[tt][0] = __builtin_fmaf(wv.x, xv.x, acc[tt][0]);
-            acc[tt][1] = __builtin_fmaf(wv.y, xv.y, acc[tt][1]);
-            acc[tt][2] = __builtin_fmaf(wv.z, xv.z, acc[tt][2]);
-            acc[tt][3] = __builtin_fmaf(wv.w, xv.w, acc[tt][3]);
+    const float* w = W + (ev ? e : 0) * H + c;
+    const float* xt[ROUTER_TT];
+#pragma unroll
+    for (int tt = 0; tt < ROUTER_TT; ++tt) xt[tt] = x + (t0 + tt < T ? t0 + tt : T - 1) * x_stride + c;
+    float acc[ROUTER_TT];
+#pragma unroll
+    for (int tt = 0; tt < ROUTER_TT; ++tt) acc[tt] = 0.0f;
+    float wv[ROUTER_STEPS], xv[ROUTER_TT][ROUTER_STEPS];
+    auto load = [&](int64_t s0, float* wd, float (*xd)[ROUTER_STEPS]) {
+#pragma unroll
+        for (int u = 0; u < ROUTER_STEPS; ++u) {
+            const int64_t s = (s0 + u < ns ? s0 + u : ns - 1) * 32;   // (past the end: never accumulated)
+            wd[u] = w[s];
+#pragma unroll
+            for (int tt = 0; tt < ROUTER_TT; ++tt) xd[tt][u] = xt[tt][s];
+        }
+    };
+    if (ns > 0) load(0, wv, xv);
+    for (int64_t s0 = 0; s0 < ns; s0 += ROUTER_STEPS) {
+        float wn[ROUTER_STEPS], xn[ROUTER_TT][ROUTER_STEPS];
+        const bool more = s0 + ROUTER_STEPS < ns;
+        if (more) load(s0 + ROUTER_STEPS, wn, xn);
+#pragma unroll
+        for (int u = 0; u < ROUTER_STEPS; ++u)
+#pragma unroll
+            for (int tt = 0; tt < ROUTER_TT; ++tt)
+                if (s0 + u < ns) acc[tt] = __builtin_fmaf(wv[u], xv[tt][u], acc[tt]);
+        if (more) {
+#pragma unroll
+            for (int u = 0; u < ROUTER_STEPS; ++u) {
+                wv[u] = wn[u];
+#pragma unroll
+                for (int tt = 0; tt < ROUTER_TT; ++tt) xv[tt][u] = xn[tt][u];
+            }
         }
     }
-    // Chain c_l (l < 8) lives in lanes m = 0,1; c_{8+l} in 2,3; c_{16+l} in 4,5; c_{24+l} in 6,7.
+    const float* wr = W + (ev ? e : 0) * H;
+#pragma unroll
     for (int tt = 0; tt < ROUTER_TT; ++tt) {
-        float v[4];
-        for (int r = 0; r < 4; ++r) {
-            float a = acc[tt][r];
-            a = a + __shfl_down(a, 4, 8);   // (c_l + c_{16+l})            lanes 0..3
-            a = a + __shfl_down(a, 2, 8);   // + (c_{8+l} + c_{24+l}) = s_l  lanes 0,1
-            a = a + __shfl_down(a, 1, 8);   // s_l + s_{l+4} = t0_r          lane 0
-            v[r] = a;
-        }
+        // GGML_F32x8_REDUCE of the four 8-lane accumulators: s_l = (c_l + c_{16+l}) +
+        // (c_{8+l} + c_{24+l}), t0_l = s_l + s_{l+4}, then two _mm_hadd_ps
+        float v = acc[tt] + __shfl_down(acc[tt], 16, 32);
+        v = v + __shfl_down(v, 8, 32);
+        v = v + __shfl_down(v, 4, 32);
+        const float u = v + __shfl_down(v, 1, 32);
+        float sumf = u + __shfl_down(u, 2, 32);
         const int64_t t = t0 + tt;
-        if (m == 0 && ev && t < T) {
-            float sumf = (v[0] + v[1]) + (v[2] + v[3]);   // two _mm_hadd_ps
+        if (c == 0 && ev && t < T) {
             // scalar tail (n % 32): 4-wide multiply + in-order add per full group of 4, fma for the rest
-            const float* xt = x + t * x_stride;
+            const float* xr = x + t * x_stride;
             const int64_t nv = np + ((H - np) & ~(int64_t) 3);
             for (int64_t i = np; i < H; ++i)
-                sumf = (i < nv) ? sumf + w[i] * xt[i] : __builtin_fmaf(w[i], xt[i], sumf);
+                sumf = (i < nv) ? sumf + wr[i] * xr[i] : __builtin_fmaf(wr[i], xr[i], sumf);
             logits[t * E + e] = sumf;
         }
     }
@@ -139,8 +164,15 @@ int launch_router(const RouterArgs& a, float* logits_ws, hipStream_t stream) {
     if (a.E % 8 != 0 || a.E > 64 * ROUTER_EPL || a.k < 1 || a.k > a.E || a.H < 1) return -2;
     if (a.T == 0) return 0;
     float* logits = a.logits ? a.logits : logits_ws;
-    dim3 g1((unsigned) ((a.E + 7) / 8), (unsigned) ((a.T + ROUTER_TT - 1) / ROUTER_TT));
-    hipLaunchKernelGGL(k_router_logits, g1, dim3(64), 0, stream, a.W, a.x, a.x_stride, a.H, a.E, a.T, logits);
+    if (a.T <= 16) {
+        dim3 g1((unsigned) ((a.E + 1) / 2), (unsigned) a.T);
+        hipLaunchKernelGGL((k_router_logits<1, 2>), g1, dim3(64), 0, stream, a.W, a.x, a.x_stride, a.H, a.E, a.T,
+                           logits);
+    } else {
+        dim3 g1((unsigned) ((a.E + 7) / 8), (unsigned) ((a.T + 3) / 4));
+        hipLaunchKernelGGL((k_router_logits<4, 8>), g1, dim3(256), 0, stream, a.W, a.x, a.x_stride, a.H, a.E, a.T,
+                           logits);
+    }
     hipLaunchKernelGGL(k_router_topk, dim3((unsigned) a.T), dim3(64), 0, stream, logits, a.E, a.k, a.T, a.clamp_min,
                        a.scale, a.ids, a.weights, a.probs, a.status);
     return hipGetLastError() == hipSuccess ? 0 : -3;

@@ -218,6 +218,37 @@ class DecodeStack:
             pass
 
 
+class LayerStack:
+    """T-token batches through a stack of MoE FFN layers (qwmoe_layer_stack_*):
+    the verify forward's FFN half, one captured HIP graph per T."""
+
+    def __init__(self, layers: list[Layer], rms_eps: float = 1e-6, max_tokens: int = 8, graphs: bool = True,
+                 keepalive=None):
+        arr = (Layer * len(layers))(*layers)
+        h = C.c_void_p()
+        check(lib().qwmoe_layer_stack_create(C.cast(arr, C.c_void_p), len(layers), rms_eps, max_tokens,
+                                             0 if graphs else 1, C.byref(h)), "layer_stack_create")
+        self.h, self.n_layer, self._keep = h, len(layers), (arr, keepalive)
+        self.H, self.k = layers[0].n_embd, layers[0].n_expert_used
+
+    def __call__(self, x, want_ids: bool = True):
+        """x: f32 [T, H] -> (out [T, H], x_out [T, H], ids [n_layer, T, k], weights)."""
+        torch = _torch()
+        T = x.shape[0]
+        out = torch.empty((T, self.H), dtype=torch.float32, device=x.device)
+        xo = torch.empty_like(out)
+        ids = torch.empty((self.n_layer, T, self.k), dtype=torch.int32, device=x.device) if want_ids else None
+        w = torch.empty((self.n_layer, T, self.k), dtype=torch.float32, device=x.device) if want_ids else None
+        check(lib().qwmoe_layer_stack_run(stream(), self.h, _ptr(x), T, _ptr(out), _ptr(xo), _ptr(ids), _ptr(w)),
+              "layer_stack_run")
+        return out, xo, ids, w
+
+    def close(self) -> None:
+        if self.h:
+            lib().qwmoe_layer_stack_free(self.h)
+            self.h = None
+
+
 def ffn_layer(layer: Layer, x, rms_eps: float = -1.0):
     """One MoE FFN layer.  x: f32 [T, H] -> (out, x_next or None, ids, weights)."""
     torch = _torch()

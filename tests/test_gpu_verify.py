@@ -1,0 +1,114 @@
+"""GPU parity of T-token batches through a layer stack (qwmoe_layer_stack_*),
+the FFN half of speculative decoding's verify forward (core/runtime.cpp:1495-1562).
+
+* T = 1..4 tokens through three layers, free-running (RMSNorm between layers):
+  every layer's ids and weights, the last layer's output and its RMSNorm equal
+  the CPU oracle's T-token layers bit for bit (T > 1 takes build_moe's
+  mul + add-chain weighted sum).
+* The captured graph, replayed many times with changing inputs and T, eager
+  library work and synchronisations in between, equals the eager chain on
+  every replay.
+* At T = 1 the stack equals the persistent decode stack bit for bit.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+from questwend_amd import ops  # noqa: E402
+from oracle_lib import Q4_K, Q6_K, Oracle  # noqa: E402
+from test_gpu_decode import GpuLayer, bits  # noqa: E402
+
+DEV = "cuda:0"
+
+
+def note(msg: str) -> None:
+    print(f"[gpu-verify] {msg}", flush=True)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def lib_init():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    ops.init(0, 512 << 20)
+    yield
+    torch.cuda.synchronize()
+
+
+@pytest.fixture(scope="module")
+def orc():
+    return Oracle()
+
+
+@pytest.fixture(scope="module")
+def layers3():
+    return [GpuLayer(1024, 16, 4, 512, (Q4_K, Q4_K, Q6_K), seed=700 + i) for i in range(3)]
+
+
+@pytest.mark.parametrize("graphs", [True, False])
+def test_layer_stack_matches_oracle(orc, layers3, graphs):
+    note(f"layer stack (graphs={graphs}): 3 layers H=1024 E=16 k=4 F=512, T = 1..4")
+    stack = ops.LayerStack([g.layer for g in layers3], 1e-6, max_tokens=4, graphs=graphs, keepalive=layers3)
+    rng = np.random.default_rng(5)
+    for T in (1, 2, 3, 4, 2):
+        x = rng.standard_normal((T, 1024)).astype(np.float32)
+        out, xo, ids, w = stack(torch.from_numpy(x).to(DEV))
+        torch.cuda.synchronize()
+        xr = x
+        for l, g in enumerate(layers3):
+            r = orc.moe_layer(g.host, xr, rms_eps=1e-6)
+            assert np.array_equal(ids[l].cpu().numpy(), r["ids"]), f"T={T} layer {l} ids"
+            assert np.array_equal(bits(w[l].cpu().numpy()), bits(r["weights"])), f"T={T} layer {l} weights"
+            xr = r["xnext"]
+        assert np.array_equal(bits(out.cpu().numpy()), bits(r["out"])), f"T={T} out"
+        assert np.array_equal(bits(xo.cpu().numpy()), bits(r["xnext"])), f"T={T} x_out"
+    stack.close()
+
+
+def test_layer_stack_graph_replays_equal_eager(layers3):
+    note("layer stack: 24 graph replays (T varies) against the eager chain, eager work in between")
+    Ls = [g.layer for g in layers3]
+    gstack = ops.LayerStack(Ls, 1e-6, max_tokens=4, graphs=True, keepalive=layers3)
+    estack = ops.LayerStack(Ls, 1e-6, max_tokens=4, graphs=False, keepalive=layers3)
+    rng = np.random.default_rng(9)
+    for i in range(24):
+        T = (1, 3, 4, 2)[i % 4]
+        x = torch.from_numpy(rng.standard_normal((T, 1024)).astype(np.float32)).to(DEV)
+        go, gxo, gids, gw = gstack(x)
+        if i % 3 == 0:
+            torch.cuda.synchronize()
+        # unrelated eager library work on the same stream and workspace
+        ops.ffn_layer(Ls[i % 3], torch.from_numpy(rng.standard_normal((5, 1024)).astype(np.float32)).to(DEV),
+                      rms_eps=1e-6)
+        eo, exo, eids, ew = estack(x)
+        torch.cuda.synchronize()
+        assert torch.equal(gids, eids), f"replay {i} (T={T}) ids"
+        assert torch.equal(go.view(torch.int32), eo.view(torch.int32)), f"replay {i} (T={T}) out"
+        assert torch.equal(gxo.view(torch.int32), exo.view(torch.int32)), f"replay {i} (T={T}) x_out"
+        assert torch.equal(gw.view(torch.int32), ew.view(torch.int32)), f"replay {i} (T={T}) weights"
+    gstack.close()
+    estack.close()
+
+
+def test_layer_stack_t1_equals_decode_stack():
+    note("layer stack T=1 vs decode stack: 2 layers of the 30B shape (H=2048 E=128 k=8 F=768 Q4_K)")
+    layers = [GpuLayer(2048, 128, 8, 768, (Q4_K,) * 3, seed=800 + i) for i in range(2)]
+    Ls = [g.layer for g in layers]
+    stack = ops.LayerStack(Ls, 1e-6, max_tokens=1, keepalive=layers)
+    dstack = ops.DecodeStack(Ls, 1e-6, keepalive=layers)
+    rng = np.random.default_rng(3)
+    for t in range(4):
+        x = torch.from_numpy(rng.standard_normal(2048).astype(np.float32)).to(DEV)
+        out, xo, ids, w = stack(x.view(1, -1))
+        dout, dxo, dids, dw = dstack(x)
+        torch.cuda.synchronize()
+        assert torch.equal(ids[:, 0], dids), f"token {t} ids"
+        assert torch.equal(out[0].view(torch.int32), dout.view(torch.int32)), f"token {t} out"
+        assert torch.equal(xo[0].view(torch.int32), dxo.view(torch.int32)), f"token {t} x_out"
+        assert torch.equal(w[:, 0].view(torch.int32), dw.view(torch.int32)), f"token {t} weights"
+    assert dstack.status() & ~1 == 0
+    stack.close()
+    dstack.close()
