@@ -342,8 +342,9 @@ int qwmoe_ffn_layer(void* stream, const qwmoe_layer* L, const float* x, int64_t 
     if (T == 0) return QWMOE_OK;
     hipStream_t st = S(stream);
     Arena ar(kReserved);
-    int32_t* ids = ar.take<int32_t>((size_t) (k * T));
-    float* w = ar.take<float>((size_t) (k * T));
+    // the router writes ids and weights straight into the caller's buffers when it gave them
+    int32_t* ids = ids_out ? ids_out : ar.take<int32_t>((size_t) (k * T));
+    float* w = weights_out ? weights_out : ar.take<float>((size_t) (k * T));
     float* logits = ar.take<float>((size_t) (E * T));
     float* upo = ar.take<float>((size_t) (F * k * T));
     float* gateo = ar.take<float>((size_t) (F * k * T));
@@ -386,24 +387,28 @@ int qwmoe_ffn_layer(void* stream, const qwmoe_layer* L, const float* x, int64_t 
                            G.rows, G.active, G.active_off, G.n_active, G.max_active, L->slot_gate,
                            L->slot_gate ? E : 0, gateo, dnb1, dnb2, T)))
         return rc;
-    if ((rc = qw::launch_swiglu(gateo, upo, act, k * T, F, (size_t) F * 4, (size_t) F * 4, (size_t) F * 4, st)))
-        return rc;
     const int vd = qw::vec_dot_type(L->type_down);
     const size_t qd = qwmoe_row_size(vd, F);
     uint8_t* aq = ar.take<uint8_t>(qd * (size_t) (k * T) + 64);
     if (!aq) return QWMOE_ERR_WORKSPACE;
-    if ((rc = qw::launch_quantize_act(vd, act, F, k, k * T, (size_t) F * 4, (size_t) F * 4 * (size_t) k, aq, st)))
-        return rc;
+    if (vd == qw::T_Q8_K) {   // SwiGLU straight into Q8_K
+        if ((rc = qw::launch_swiglu_q8K(gateo, upo, F, k * T, aq, st))) return rc;
+    } else {
+        if ((rc = qw::launch_swiglu(gateo, upo, act, k * T, F, (size_t) F * 4, (size_t) F * 4, (size_t) F * 4, st)))
+            return rc;
+        if ((rc = qw::launch_quantize_act(vd, act, F, k, k * T, (size_t) F * 4, (size_t) F * 4 * (size_t) k, aq, st)))
+            return rc;
+    }
     if ((rc = mmid_grouped(st, L->type_down, L->down, F, H, L->n_slots_down, L->down_nb1, L->down_nb2, aq, k, qd,
                            G.rows, G.active, G.active_off, G.n_active, G.max_active, L->slot_down,
                            L->slot_down ? E : 0, ex, (size_t) H * 4, (size_t) H * 4 * (size_t) k, T)))
         return rc;
-    if ((rc = qw::launch_weighted_sum(ex, w, out, H, k, T, st))) return rc;
-    if (rms_eps >= 0.0f && (rc = qw::launch_rms_norm(out, x_next, H, T, rms_eps, st))) return rc;
-    if (ids_out && hipMemcpyAsync(ids_out, ids, sizeof(int32_t) * k * T, hipMemcpyDeviceToDevice, st) != hipSuccess)
-        return QWMOE_ERR_HIP;
-    if (weights_out && hipMemcpyAsync(weights_out, w, sizeof(float) * k * T, hipMemcpyDeviceToDevice, st) != hipSuccess)
-        return QWMOE_ERR_HIP;
+    if (rms_eps >= 0.0f && H <= 16384) {
+        if ((rc = qw::launch_weighted_sum_rms(ex, w, out, x_next, H, k, T, rms_eps, st))) return rc;
+    } else {
+        if ((rc = qw::launch_weighted_sum(ex, w, out, H, k, T, st))) return rc;
+        if (rms_eps >= 0.0f && (rc = qw::launch_rms_norm(out, x_next, H, T, rms_eps, st))) return rc;
+    }
     return QWMOE_OK;
 }
 

@@ -108,4 +108,54 @@ int launch_rms_norm(const float* x, float* y, int64_t n, int64_t rows, float eps
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
+// The weighted expert sum of one token (as k_weighted_sum) and its RMSNorm (as
+// k_rms_norm), one 1024-thread block per token: the sums go to LDS in
+// parallel, then the first 256 threads form the double sum of squares in
+// k_rms_norm's per-thread order and reduce it as it does.
+__global__ void __launch_bounds__(1024) k_weighted_sum_rms(const float* __restrict__ ex, const float* __restrict__ w,
+                                                           float* __restrict__ out, float* __restrict__ xn, int64_t H,
+                                                           int64_t k, int64_t T, float eps) {
+    extern __shared__ float ys[];
+    __shared__ double part[4];
+    const int64_t t = blockIdx.x;
+    const float* e0 = ex + t * k * H;
+    const float* wt = w + t * k;
+    for (int64_t h = threadIdx.x; h < H; h += 1024) {
+        const float* e = e0 + h;
+        float v;
+        if (T == 1) {
+            v = vec_dot_f32_avx(k, e, H, wt);
+        } else {
+            v = e[0] * wt[0];
+            for (int64_t j = 1; j < k; ++j) v = v + e[j * H] * wt[j];
+        }
+        out[t * H + h] = v;
+        ys[h] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x < 256) {
+        double s = 0.0;
+        for (int64_t h = threadIdx.x; h < H; h += 256) {
+            const float v = ys[h];
+            s += (double) (v * v);
+        }
+        for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+        if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    }
+    __syncthreads();
+    const double tot = (part[0] + part[1]) + (part[2] + part[3]);
+    const float mean = (float) (tot / (double) H);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    for (int64_t h = threadIdx.x; h < H; h += 1024) xn[t * H + h] = ys[h] * scale;
+}
+
+int launch_weighted_sum_rms(const float* experts, const float* weights, float* out, float* x_next, int64_t H,
+                            int64_t k, int64_t T, float eps, hipStream_t stream) {
+    if (T == 0) return 0;
+    if ((size_t) H * 4 > 64 * 1024) return -2;
+    hipLaunchKernelGGL(k_weighted_sum_rms, dim3((unsigned) T), dim3(1024), (size_t) H * 4, stream, experts, weights,
+                       out, x_next, H, k, T, eps);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
 }  // namespace qw

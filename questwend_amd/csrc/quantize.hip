@@ -16,19 +16,9 @@ namespace qw {
 // ---------------------------------------------------------------------------
 // Activation Q8_K: one wave per 256-value block, 4 values per lane.
 // src rows may be strided (ggml nb1/nb2 in bytes); dst rows are dense.
-__global__ void __launch_bounds__(256) k_quant_q8K(const float* __restrict__ src, int64_t K, int64_t ne1,
-                                                   int64_t nrows, size_t nb1, size_t nb2,
-                                                   BlockQ8_K* __restrict__ dst) {
-    const int lane = threadIdx.x & 63;
-    const int64_t nb = K / QK_K;
-    const int64_t blk = (int64_t) blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
-    if (blk >= nb * nrows) return;
-    const int64_t row = blk / nb, ib = blk % nb;
-    const int64_t i1 = row % ne1, i2 = row / ne1;
-    const float* x = (const float*) ((const char*) src + i1 * nb1 + i2 * nb2) + ib * QK_K;
-    float v[4];
-    const float4 q = *(const float4*) (x + 4 * lane);
-    v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+// quantize_row_q8_K_ref of one block held by a wave, 4 values per lane
+// (values 4*lane .. 4*lane+3).
+__device__ __forceinline__ void quant_q8K_wave(const float* v, int lane, BlockQ8_K* y) {
     // first index of the largest |x|: reduce (|x|, -index) lexicographically
     float am = 0.0f;
     int ai = 0x7fffffff;
@@ -41,14 +31,16 @@ __global__ void __launch_bounds__(256) k_quant_q8K(const float* __restrict__ src
         const int oi = __shfl_xor(ai, off);
         if (om > am || (om == am && oi < ai)) { am = om; ai = oi; }
     }
-    BlockQ8_K* y = dst + blk;
     if (!(am > 0.0f)) {  // amax == 0: d = 0, qs = 0 (bsums written as 0)
         *(int*) &y->qs[4 * lane] = 0;
         if (lane < 16) y->bsums[lane] = 0;
         if (lane == 0) y->d = 0.0f;
         return;
     }
-    const float maxv = __shfl(ai < 256 ? x[ai] : 0.0f, 0);  // same value in every lane
+    // the signed value at that index, from the lane that holds it
+    const int sel = ai & 3;
+    const float mine = sel == 0 ? v[0] : sel == 1 ? v[1] : sel == 2 ? v[2] : v[3];
+    const float maxv = __shfl(mine, ai >> 2);   // same value in every lane
     const float iscale = -127.f / maxv;
     int qv[4];
     int s = 0;
@@ -64,6 +56,47 @@ __global__ void __launch_bounds__(256) k_quant_q8K(const float* __restrict__ src
     s += __shfl_xor(s, 2);
     if ((lane & 3) == 0) y->bsums[lane >> 2] = (int16_t) s;
     if (lane == 0) y->d = 1.0f / iscale;
+}
+
+__global__ void __launch_bounds__(256) k_quant_q8K(const float* __restrict__ src, int64_t K, int64_t ne1,
+                                                   int64_t nrows, size_t nb1, size_t nb2,
+                                                   BlockQ8_K* __restrict__ dst) {
+    const int lane = threadIdx.x & 63;
+    const int64_t nb = K / QK_K;
+    const int64_t blk = (int64_t) blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
+    if (blk >= nb * nrows) return;
+    const int64_t row = blk / nb, ib = blk % nb;
+    const int64_t i1 = row % ne1, i2 = row / ne1;
+    const float* x = (const float*) ((const char*) src + i1 * nb1 + i2 * nb2) + ib * QK_K;
+    const float4 q = *(const float4*) (x + 4 * lane);
+    const float v[4] = {q.x, q.y, q.z, q.w};
+    quant_q8K_wave(v, lane, dst + blk);
+}
+
+// SwiGLU (ggml_swiglu_split: silu(gate) * up, ops.cpp:3182-3238) of n_rows dense
+// rows of F values, quantized straight to Q8_K as the down projection reads it:
+// one wave per 256-value block, the same values and quantizer as k_swiglu then
+// k_quant_q8K, without the fp32 round trip.
+__global__ void __launch_bounds__(256) k_swiglu_q8K(const float* __restrict__ gate, const float* __restrict__ up,
+                                                    int64_t F, int64_t n_rows, BlockQ8_K* __restrict__ dst) {
+    const int lane = threadIdx.x & 63;
+    const int64_t nb = F / QK_K;
+    const int64_t blk = (int64_t) blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
+    if (blk >= nb * n_rows) return;
+    const int64_t off = (blk / nb) * F + (blk % nb) * QK_K + 4 * lane;
+    const float4 g = *(const float4*) (gate + off);
+    const float4 u = *(const float4*) (up + off);
+    const float v[4] = {v_silu(g.x) * u.x, v_silu(g.y) * u.y, v_silu(g.z) * u.z, v_silu(g.w) * u.w};
+    quant_q8K_wave(v, lane, dst + blk);
+}
+
+int launch_swiglu_q8K(const float* gate, const float* up, int64_t F, int64_t n_rows, void* dst, hipStream_t stream) {
+    if (F % QK_K) return -2;
+    const int64_t nblk = (F / QK_K) * n_rows;
+    if (nblk == 0) return 0;
+    hipLaunchKernelGGL(k_swiglu_q8K, dim3((unsigned) ((nblk + 3) / 4)), dim3(256), 0, stream, gate, up, F, n_rows,
+                       (BlockQ8_K*) dst);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
 // Activation Q8_0 (x86 AVX2 branch): one 32-value block per 8 lanes, 4 per lane.

@@ -79,5 +79,10 @@ int launch_swiglu(const float* gate, const float* up, float* out, int64_t n_rows
 int launch_weighted_sum(const float* experts, const float* weights, float* out, int64_t H, int64_t k, int64_t T,
                         hipStream_t stream);
 int launch_rms_norm(const float* x, float* y, int64_t n, int64_t rows, float eps, hipStream_t stream);
+// k_weighted_sum then k_rms_norm of its output, in one launch (H <= 16384)
+int launch_weighted_sum_rms(const float* experts, const float* weights, float* out, float* x_next, int64_t H,
+                            int64_t k, int64_t T, float eps, hipStream_t stream);
+// k_swiglu then k_quant_q8K of its output, in one launch (F % 256 == 0; rows dense)
+int launch_swiglu_q8K(const float* gate, const float* up, int64_t F, int64_t n_rows, void* dst, hipStream_t stream);
 
 }  // namespace qw
