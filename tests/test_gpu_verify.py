@@ -9,6 +9,9 @@ the FFN half of speculative decoding's verify forward (core/runtime.cpp:1495-156
   library work and synchronisations in between, equals the eager chain on
   every replay.
 * At T = 1 the stack equals the persistent decode stack bit for bit.
+* configs[3] (5 correlated verify tokens through a 30B-A3B Q4_K layer at E = 128,
+  40 seeded steps) and configs[0] (a Q8_0 layer at E = 128, decode) at their
+  full shapes, against the oracle.
 """
 from __future__ import annotations
 
@@ -112,3 +115,55 @@ def test_layer_stack_t1_equals_decode_stack():
     assert dstack.status() & ~1 == 0
     stack.close()
     dstack.close()
+
+
+def correlated_tokens(rng, T, H, rho):
+    """T rows of N(0, 1) with pairwise correlation rho (a shared component)."""
+    c = rng.standard_normal(H)
+    return (np.sqrt(rho) * c + np.sqrt(1.0 - rho) * rng.standard_normal((T, H))).astype(np.float32)
+
+
+def test_config4_verify_batches_e128(orc):
+    """5 tokens (1 accepted + 4 draft), activations correlated at
+    rho = 0.8, through a Qwen3-30B-A3B-shaped Q4_K layer (E = 128): ids,
+    weights, output and its RMSNorm equal the oracle on 40 seeded steps, through
+    qwmoe_ffn_layer and through a one-layer stack's captured graph."""
+    note("configs[3]: T=5 correlated verify batches, 30B-A3B Q4_K layer at E=128, 40 steps")
+    g = GpuLayer(2048, 128, 8, 768, (Q4_K,) * 3, seed=900)
+    stack = ops.LayerStack([g.layer], 1e-6, max_tokens=5, keepalive=g)
+    rng = np.random.default_rng(4)
+    overlap = []
+    for step in range(40):
+        x = correlated_tokens(rng, 5, 2048, 0.8)
+        r = orc.moe_layer(g.host, x, rms_eps=1e-6)
+        out, xn, ids, w = ops.ffn_layer(g.layer, torch.from_numpy(x).to(DEV), rms_eps=1e-6)
+        so, sxo, sids, sw = stack(torch.from_numpy(x).to(DEV))
+        torch.cuda.synchronize()
+        assert np.array_equal(ids.cpu().numpy(), r["ids"]), f"step {step} ids"
+        assert np.array_equal(bits(w.cpu().numpy()), bits(r["weights"])), f"step {step} weights"
+        assert np.array_equal(bits(out.cpu().numpy()), bits(r["out"])), f"step {step} out"
+        assert np.array_equal(bits(xn.cpu().numpy()), bits(r["xnext"])), f"step {step} x_next"
+        assert torch.equal(sids[0], ids) and torch.equal(so.view(torch.int32), out.view(torch.int32))
+        assert torch.equal(sxo.view(torch.int32), xn.view(torch.int32))
+        overlap.append(len(np.unique(r["ids"])))
+    note(f"distinct experts per 5-token batch: mean {np.mean(overlap):.1f} of 40 selections")
+    assert np.mean(overlap) < 40          # correlated tokens share experts
+    stack.close()
+
+
+def test_config0_q8_0_decode_e128(orc):
+    """one Qwen3-MoE FFN layer, 1-token decode, Q8_0 experts at the
+    full shape (H=2048, E=128, k=8, F=768): equal to the oracle on 8 tokens."""
+    note("configs[0]: Q8_0 layer at E=128, T=1, 8 tokens")
+    from oracle_lib import Q8_0
+    g = GpuLayer(2048, 128, 8, 768, (Q8_0,) * 3, seed=910)
+    rng = np.random.default_rng(8)
+    for t in range(8):
+        x = rng.standard_normal((1, 2048)).astype(np.float32)
+        r = orc.moe_layer(g.host, x, rms_eps=1e-6)
+        out, xn, ids, w = ops.ffn_layer(g.layer, torch.from_numpy(x).to(DEV), rms_eps=1e-6)
+        torch.cuda.synchronize()
+        assert np.array_equal(ids.cpu().numpy(), r["ids"]), f"token {t} ids"
+        assert np.array_equal(bits(w.cpu().numpy()), bits(r["weights"])), f"token {t} weights"
+        assert np.array_equal(bits(out.cpu().numpy()), bits(r["out"])), f"token {t} out"
+        assert np.array_equal(bits(xn.cpu().numpy()), bits(r["xnext"])), f"token {t} x_next"
