@@ -61,11 +61,12 @@ int check_k(int type, int64_t K) {
     return QWMOE_OK;
 }
 
-// Shared implementation of mul_mat_id once b is quantized and ids are grouped.
-int mmid_grouped(hipStream_t st, int type, const void* as, int64_t K, int64_t N, int64_t n_as, size_t nb01,
-                 size_t nb02, const uint8_t* bq, int64_t ne11, size_t bq_row, const int32_t* rows,
-                 const int32_t* active, const int32_t* active_off, const int32_t* n_active, int64_t max_active,
-                 const int32_t* slot_of, int64_t n_slot_of, float* dst, size_t nb1, size_t nb2, int64_t max_rows) {
+// The kernel arguments of mul_mat_id once b is quantized and ids are grouped.
+qw::MmidArgs mmid_args(int type, const void* as, int64_t K, int64_t N, int64_t n_as, size_t nb01, size_t nb02,
+                       const uint8_t* bq, int64_t ne11, size_t bq_row, const int32_t* rows, const int32_t* active,
+                       const int32_t* active_off, const int32_t* n_active, int64_t max_active,
+                       const int32_t* slot_of, int64_t n_slot_of, float* dst, size_t nb1, size_t nb2,
+                       int64_t max_rows) {
     qw::MmidArgs m{};
     m.type = type;
     m.w = (const uint8_t*) as;
@@ -95,9 +96,23 @@ int mmid_grouped(hipStream_t st, int type, const void* as, int64_t K, int64_t N,
     m.max_rows = max_rows;
     const bool mfma = g_lib.mfma_min_rows > 0 && max_rows >= g_lib.mfma_min_rows && qw::mmid_mfma_supported(m);
     if (mfma) m.mfma_min_rows = g_lib.mfma_min_rows;
+    return m;
+}
+
+int mmid_launch(const qw::MmidArgs& m, hipStream_t st) {
     int rc = qw::launch_mmid_gemv(m, st);
-    if (rc == 0 && mfma) rc = qw::launch_mmid_mfma(m, st);
+    if (rc == 0 && m.mfma_min_rows > 0) rc = qw::launch_mmid_mfma(m, st);
     return rc;
+}
+
+// Shared implementation of mul_mat_id once b is quantized and ids are grouped.
+int mmid_grouped(hipStream_t st, int type, const void* as, int64_t K, int64_t N, int64_t n_as, size_t nb01,
+                 size_t nb02, const uint8_t* bq, int64_t ne11, size_t bq_row, const int32_t* rows,
+                 const int32_t* active, const int32_t* active_off, const int32_t* n_active, int64_t max_active,
+                 const int32_t* slot_of, int64_t n_slot_of, float* dst, size_t nb1, size_t nb2, int64_t max_rows) {
+    return mmid_launch(mmid_args(type, as, K, N, n_as, nb01, nb02, bq, ne11, bq_row, rows, active, active_off, n_active,
+                                 max_active, slot_of, n_slot_of, dst, nb1, nb2, max_rows),
+                       st);
 }
 
 struct Grouping {
@@ -379,14 +394,19 @@ int qwmoe_ffn_layer(void* stream, const qwmoe_layer* L, const float* x, int64_t 
     if ((rc = qw::launch_quantize_act(vg, x, H, 1, T, (size_t) H * 4, (size_t) H * 4, xg, st))) return rc;
     if (xu != xg && (rc = qw::launch_quantize_act(vu, x, H, 1, T, (size_t) H * 4, (size_t) H * 4, xu, st))) return rc;
     const size_t dnb1 = (size_t) F * 4, dnb2 = (size_t) F * 4 * (size_t) k;
-    if ((rc = mmid_grouped(st, L->type_up, L->up, H, F, L->n_slots_up, L->up_nb1, L->up_nb2, xu, 1, qu, G.rows,
-                           G.active, G.active_off, G.n_active, G.max_active, L->slot_up, L->slot_up ? E : 0, upo,
-                           dnb1, dnb2, T)))
-        return rc;
-    if ((rc = mmid_grouped(st, L->type_gate, L->gate, H, F, L->n_slots_gate, L->gate_nb1, L->gate_nb2, xg, 1, qg,
-                           G.rows, G.active, G.active_off, G.n_active, G.max_active, L->slot_gate,
-                           L->slot_gate ? E : 0, gateo, dnb1, dnb2, T)))
-        return rc;
+    const qw::MmidArgs mu = mmid_args(L->type_up, L->up, H, F, L->n_slots_up, L->up_nb1, L->up_nb2, xu, 1, qu, G.rows,
+                                      G.active, G.active_off, G.n_active, G.max_active, L->slot_up,
+                                      L->slot_up ? E : 0, upo, dnb1, dnb2, T);
+    const qw::MmidArgs mg = mmid_args(L->type_gate, L->gate, H, F, L->n_slots_gate, L->gate_nb1, L->gate_nb2, xg, 1, qg,
+                                      G.rows, G.active, G.active_off, G.n_active, G.max_active, L->slot_gate,
+                                      L->slot_gate ? E : 0, gateo, dnb1, dnb2, T);
+    if (mu.mfma_min_rows == 0 && mg.mfma_min_rows == 0 && mu.type == mg.type) {
+        // gate and up in one launch
+        if ((rc = qw::launch_mmid_gemv2(mu, mg, st))) return rc;
+    } else {
+        if ((rc = mmid_launch(mu, st))) return rc;
+        if ((rc = mmid_launch(mg, st))) return rc;
+    }
     const int vd = qw::vec_dot_type(L->type_down);
     const size_t qd = qwmoe_row_size(vd, F);
     uint8_t* aq = ar.take<uint8_t>(qd * (size_t) (k * T) + 64);

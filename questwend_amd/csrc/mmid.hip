@@ -222,8 +222,15 @@ __host__ __device__ inline uint32_t mmid_slot_bytes(size_t row_bytes) {
     return (uint32_t) (((row_bytes + 15 + 15) / 16) * 16 + 16);
 }
 
+// One launch computes up to two mul_mat_ids of the same weight type and shape
+// over the same grouping (gate and up of an FFN): blockIdx.z picks the matrix.
+struct MmidPair {
+    MmidArgs m[2];
+};
+
 template <int TYPE>
-__global__ void __launch_bounds__(256) k_mmid_gemv(MmidArgs m) {
+__global__ void __launch_bounds__(256) k_mmid_gemv(MmidPair pr) {
+    const MmidArgs m = pr.m[blockIdx.z];
     extern __shared__ uint32_t lds[];
     __shared__ int s_chunk[MMID_CT][3];   // (e, t, activation row) of the staged chunk
     const int g = blockIdx.y;
@@ -363,21 +370,39 @@ __global__ void __launch_bounds__(256) k_mmid_gemv(MmidArgs m) {
     }
 }
 
-int launch_mmid_gemv(const MmidArgs& m, hipStream_t stream) {
+static int launch_gemv(const MmidPair& pr, int nz, hipStream_t stream) {
+    const MmidArgs& m = pr.m[0];
     const size_t row_bytes = (size_t) (m.K / block_elems(m.type)) * block_bytes(m.type);
     size_t lds_bytes = (size_t) mmid_slot_bytes(row_bytes) * MMID_ROWS +
                        (size_t) mmid_stage_rows(m.max_rows) * (((m.act_row_bytes + 3) / 4) * 4 + 16);
     if (m.type == T_Q4_K) lds_bytes = ((lds_bytes + 15) & ~(size_t) 15) + (size_t) MMID_ROWS * (m.K / QK_K) * 16;
     if (lds_bytes > 160 * 1024) return -2;
-    dim3 grid((unsigned) ((m.N + MMID_ROWS - 1) / MMID_ROWS), (unsigned) m.max_active);
+    dim3 grid((unsigned) ((m.N + MMID_ROWS - 1) / MMID_ROWS), (unsigned) m.max_active, (unsigned) nz);
     if (grid.y == 0) return 0;
     switch (m.type) {
-        case T_Q4_K: hipLaunchKernelGGL(k_mmid_gemv<T_Q4_K>, grid, dim3(256), lds_bytes, stream, m); break;
-        case T_Q6_K: hipLaunchKernelGGL(k_mmid_gemv<T_Q6_K>, grid, dim3(256), lds_bytes, stream, m); break;
-        case T_Q8_0: hipLaunchKernelGGL(k_mmid_gemv<T_Q8_0>, grid, dim3(256), lds_bytes, stream, m); break;
+        case T_Q4_K: hipLaunchKernelGGL(k_mmid_gemv<T_Q4_K>, grid, dim3(256), lds_bytes, stream, pr); break;
+        case T_Q6_K: hipLaunchKernelGGL(k_mmid_gemv<T_Q6_K>, grid, dim3(256), lds_bytes, stream, pr); break;
+        case T_Q8_0: hipLaunchKernelGGL(k_mmid_gemv<T_Q8_0>, grid, dim3(256), lds_bytes, stream, pr); break;
         default: return -2;
     }
     return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+int launch_mmid_gemv(const MmidArgs& m, hipStream_t stream) {
+    MmidPair pr;
+    pr.m[0] = m;
+    pr.m[1] = m;
+    return launch_gemv(pr, 1, stream);
+}
+
+int launch_mmid_gemv2(const MmidArgs& a, const MmidArgs& b, hipStream_t stream) {
+    if (a.type != b.type || a.K != b.K || a.N != b.N || a.max_active != b.max_active || a.max_rows != b.max_rows ||
+        a.act_row_bytes != b.act_row_bytes)
+        return -2;
+    MmidPair pr;
+    pr.m[0] = a;
+    pr.m[1] = b;
+    return launch_gemv(pr, 2, stream);
 }
 
 }  // namespace qw

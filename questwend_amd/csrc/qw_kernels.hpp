@@ -69,6 +69,8 @@ struct MmidArgs {
     int64_t max_rows;         // bound on the rows of one bin
 };
 int launch_mmid_gemv(const MmidArgs& m, hipStream_t stream);
+// two GEMVs of the same type, shape and grouping in one launch (mfma_min_rows must be 0 in both)
+int launch_mmid_gemv2(const MmidArgs& a, const MmidArgs& b, hipStream_t stream);
 // mmid_mfma.hip
 bool mmid_mfma_supported(const MmidArgs& m);
 int launch_mmid_mfma(const MmidArgs& m, hipStream_t stream);
