@@ -381,17 +381,20 @@ int qwmoe_ffn_layer(void* stream, const qwmoe_layer* L, const float* x, int64_t 
     ra.weights = w;
     ra.status = g_lib.status;
     if (E % 8 || E > 512 || H % 4) return QWMOE_ERR_UNSUPPORTED;
-    if ((rc = qw::launch_router(ra, logits, st))) return rc;
-    // grouping by logical expert (slot rows are injective for resident layers)
-    Grouping G{};
-    if ((rc = group(st, ar, ids, k, T, (size_t) k * 4, E, nullptr, nullptr, nullptr, G))) return rc;
-    // x quantized once per distinct activation type of gate / up
+    // x quantized once per distinct activation type of gate / up; a small batch's
+    // Q8_K copy is made by the router launch
     const int vg = qw::vec_dot_type(L->type_gate), vu = qw::vec_dot_type(L->type_up);
     const size_t qg = qwmoe_row_size(vg, H), qu = qwmoe_row_size(vu, H);
     uint8_t* xg = ar.take<uint8_t>(qg * (size_t) T + 64);
     uint8_t* xu = (vu == vg) ? xg : ar.take<uint8_t>(qu * (size_t) T + 64);
     if (!xg || !xu) return QWMOE_ERR_WORKSPACE;
-    if ((rc = qw::launch_quantize_act(vg, x, H, 1, T, (size_t) H * 4, (size_t) H * 4, xg, st))) return rc;
+    const bool xq_fused = T <= 16 && vg == qw::T_Q8_K && H % 256 == 0;
+    ra.xq = xq_fused ? xg : nullptr;
+    if ((rc = qw::launch_router(ra, logits, st))) return rc;
+    // grouping by logical expert (slot rows are injective for resident layers)
+    Grouping G{};
+    if ((rc = group(st, ar, ids, k, T, (size_t) k * 4, E, nullptr, nullptr, nullptr, G))) return rc;
+    if (!xq_fused && (rc = qw::launch_quantize_act(vg, x, H, 1, T, (size_t) H * 4, (size_t) H * 4, xg, st))) return rc;
     if (xu != xg && (rc = qw::launch_quantize_act(vu, x, H, 1, T, (size_t) H * 4, (size_t) H * 4, xu, st))) return rc;
     const size_t dnb1 = (size_t) F * 4, dnb2 = (size_t) F * 4 * (size_t) k;
     const qw::MmidArgs mu = mmid_args(L->type_up, L->up, H, F, L->n_slots_up, L->up_nb1, L->up_nb2, xu, 1, qu, G.rows,

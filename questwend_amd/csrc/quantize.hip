@@ -16,48 +16,6 @@ namespace qw {
 // ---------------------------------------------------------------------------
 // Activation Q8_K: one wave per 256-value block, 4 values per lane.
 // src rows may be strided (ggml nb1/nb2 in bytes); dst rows are dense.
-// quantize_row_q8_K_ref of one block held by a wave, 4 values per lane
-// (values 4*lane .. 4*lane+3).
-__device__ __forceinline__ void quant_q8K_wave(const float* v, int lane, BlockQ8_K* y) {
-    // first index of the largest |x|: reduce (|x|, -index) lexicographically
-    float am = 0.0f;
-    int ai = 0x7fffffff;
-    for (int i = 0; i < 4; ++i) {
-        const float a = __builtin_fabsf(v[i]);
-        if (a > am) { am = a; ai = 4 * lane + i; }
-    }
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float om = __shfl_xor(am, off);
-        const int oi = __shfl_xor(ai, off);
-        if (om > am || (om == am && oi < ai)) { am = om; ai = oi; }
-    }
-    if (!(am > 0.0f)) {  // amax == 0: d = 0, qs = 0 (bsums written as 0)
-        *(int*) &y->qs[4 * lane] = 0;
-        if (lane < 16) y->bsums[lane] = 0;
-        if (lane == 0) y->d = 0.0f;
-        return;
-    }
-    // the signed value at that index, from the lane that holds it
-    const int sel = ai & 3;
-    const float mine = sel == 0 ? v[0] : sel == 1 ? v[1] : sel == 2 ? v[2] : v[3];
-    const float maxv = __shfl(mine, ai >> 2);   // same value in every lane
-    const float iscale = -127.f / maxv;
-    int qv[4];
-    int s = 0;
-    for (int i = 0; i < 4; ++i) {
-        const int t = nearest_int(iscale * v[i]);
-        qv[i] = t < 127 ? t : 127;
-        s += qv[i];
-    }
-    *(uint32_t*) &y->qs[4 * lane] =
-        (uint32_t) (qv[0] & 0xff) | ((uint32_t) (qv[1] & 0xff) << 8) | ((uint32_t) (qv[2] & 0xff) << 16) |
-        ((uint32_t) (qv[3] & 0xff) << 24);
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
-    if ((lane & 3) == 0) y->bsums[lane >> 2] = (int16_t) s;
-    if (lane == 0) y->d = 1.0f / iscale;
-}
-
 __global__ void __launch_bounds__(256) k_quant_q8K(const float* __restrict__ src, int64_t K, int64_t ne1,
                                                    int64_t nrows, size_t nb1, size_t nb2,
                                                    BlockQ8_K* __restrict__ dst) {

@@ -27,6 +27,7 @@ struct RouterArgs {
     float* logits;        // optional [T][E]
     float* probs;         // optional [T][E]
     int32_t* status;      // optional device word: bit 0 set when a top-k tie needed the exact sort
+    void* xq;             // optional [T][H/256] Q8_K of x, made in the same launch (T <= 16, dense x rows)
 };
 int launch_router(const RouterArgs& a, float* logits_ws, hipStream_t stream);
 

@@ -20,10 +20,21 @@ constexpr int ROUTER_STEPS = 16; // 32-element steps whose loads are in flight t
 // flight while the current one is accumulated, so a chain waits for memory once
 // per batch, not once per step.  Small batches take one token per group and two
 // experts per workgroup, for more workgroups.
+// xq (small batches, EPW == 2): workgroups past the router's also quantize x to
+// Q8_K, one wave per 256-value block (the k_quant_q8K quantizer), so the
+// projections' activation costs no launch of its own.
 template <int ROUTER_TT, int EPW>
 __global__ void __launch_bounds__(32 * EPW) k_router_logits(const float* __restrict__ W, const float* __restrict__ x,
                                                             int64_t x_stride, int64_t H, int64_t E, int64_t T,
-                                                            float* __restrict__ logits) {
+                                                            float* __restrict__ logits, BlockQ8_K* __restrict__ xq) {
+    if (EPW == 2 && blockIdx.x >= (E + 1) / 2) {
+        const int64_t ib = blockIdx.x - (E + 1) / 2, t = blockIdx.y;
+        if (ib >= H / QK_K) return;
+        const float4 q = *(const float4*) (x + t * x_stride + ib * QK_K + 4 * threadIdx.x);
+        const float v[4] = {q.x, q.y, q.z, q.w};
+        quant_q8K_wave(v, threadIdx.x, xq + t * (H / QK_K) + ib);
+        return;
+    }
     const int c = threadIdx.x & 31;
     const int64_t e = (int64_t) blockIdx.x * EPW + (threadIdx.x >> 5);
     const int64_t t0 = (int64_t) blockIdx.y * ROUTER_TT;
@@ -164,14 +175,16 @@ int launch_router(const RouterArgs& a, float* logits_ws, hipStream_t stream) {
     if (a.E % 8 != 0 || a.E > 64 * ROUTER_EPL || a.k < 1 || a.k > a.E || a.H < 1) return -2;
     if (a.T == 0) return 0;
     float* logits = a.logits ? a.logits : logits_ws;
+    if (a.xq && (a.T > 16 || a.H % QK_K)) return -2;
     if (a.T <= 16) {
-        dim3 g1((unsigned) ((a.E + 1) / 2), (unsigned) a.T);
+        const int64_t nq = a.xq ? a.H / QK_K : 0;
+        dim3 g1((unsigned) ((a.E + 1) / 2 + nq), (unsigned) a.T);
         hipLaunchKernelGGL((k_router_logits<1, 2>), g1, dim3(64), 0, stream, a.W, a.x, a.x_stride, a.H, a.E, a.T,
-                           logits);
+                           logits, (BlockQ8_K*) a.xq);
     } else {
         dim3 g1((unsigned) ((a.E + 7) / 8), (unsigned) ((a.T + 3) / 4));
         hipLaunchKernelGGL((k_router_logits<4, 8>), g1, dim3(256), 0, stream, a.W, a.x, a.x_stride, a.H, a.E, a.T,
-                           logits);
+                           logits, (BlockQ8_K*) nullptr);
     }
     hipLaunchKernelGGL(k_router_topk, dim3((unsigned) a.T), dim3(64), 0, stream, logits, a.E, a.k, a.T, a.clamp_min,
                        a.scale, a.ids, a.weights, a.probs, a.status);
