@@ -304,8 +304,6 @@ def expert_cache_bench(args) -> int:
     xs = torch.empty((n_steps, H), dtype=torch.float32, device=dev)
     ops.randn_(xs, args.seed + 777, 0.0, 1.0)
     outs = torch.empty((n_steps, H), dtype=torch.float32, device=dev)
-    routers = [lay[0] for lay in layers]
-
     def step(i):
         x = xs[i]
         out, _, ids, _ = spec(x)
@@ -313,10 +311,8 @@ def expert_cache_bench(args) -> int:
             outs[i].copy_(out)
             return True
         xl = x.view(1, H)
-        for l in range(N_LAYER):                    # decode_cached: router, ensure, layer
-            lid, _ = ops.router_topk(routers[l], xl, K_USED)
-            cache.ensure(l, lid.cpu().numpy().reshape(-1).tolist())
-            o, xl, _, _ = ops.ffn_layer(cached[l], xl, rms_eps=RMS_EPS)
+        for l in range(N_LAYER):                    # decode_cached: router, ids back, ensure, layer
+            o, xl, _, _ = cache.run_layer(l, cached[l], xl, rms_eps=RMS_EPS)
         outs[i].copy_(o.view(-1))
         return False
 

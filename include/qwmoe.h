@@ -440,6 +440,14 @@ int qwmoe_expert_cache_save_profile(const qwmoe_expert_cache * c, const char * p
 int qwmoe_expert_cache_load_prefetch(qwmoe_expert_cache * c, const char * path, uint64_t * n_prefetched);
 /* Waits for every copy the cache issued. */
 int qwmoe_expert_cache_sync(qwmoe_expert_cache * c);
+/* One layer of decode_cached (core/runtime.cpp:2458-2662, ensure_layer 2593-2600)
+ * on the cache's stream: the router's ids for x [T][H] are read back (pinned
+ * host buffer, one synchronisation), ensure() makes them resident, then
+ * qwmoe_ffn_layer runs on the pools.  L gives shapes, router and scale (its
+ * expert fields are taken from the cache).  At most 64 * n_expert_used ids per
+ * call; outputs as qwmoe_ffn_layer's.  The first call allocates a small id buffer. */
+int qwmoe_expert_cache_run_layer(qwmoe_expert_cache * c, int layer, const qwmoe_layer * L, const float * x, int64_t T,
+                                 float * out, float rms_eps, float * x_next, int32_t * ids_out, float * weights_out);
 
 /* ---- host-side checks (no GPU needed) ---------------------------------------- */
 

@@ -116,6 +116,7 @@ SIGNATURES = {
     "qwmoe_expert_cache_save_profile": (I, [P, C.c_char_p]),
     "qwmoe_expert_cache_load_prefetch": (I, [P, C.c_char_p, P]),
     "qwmoe_expert_cache_sync": (I, [P]),
+    "qwmoe_expert_cache_run_layer": (I, [P, I, P, P, I64, P, F, P, P, P]),
 }
 
 

@@ -196,6 +196,10 @@ struct qwmoe_expert_cache {
     int row_next = 0;
     int io_threads = DEFAULT_IO_THREADS;
     bool copy_engine_only = false;            // QWMOE_CACHE_COPY_ENGINE: no slab gather kernel
+    int32_t* run_ids_dev = nullptr;           // run_layer: router ids / weights (device) and their read-back
+    float* run_w_dev = nullptr;
+    int32_t* run_ids_host = nullptr;
+    size_t run_cap = 0;
     Workers* workers = nullptr;
 
     ~qwmoe_expert_cache() {
@@ -208,6 +212,8 @@ struct qwmoe_expert_cache {
             if (row_stage[b]) (void) hipHostFree(row_stage[b]);
         }
         for (void* p : owned_host) (void) hipHostFree(p);
+        if (run_ids_dev) (void) hipFree(run_ids_dev);
+        if (run_ids_host) (void) hipHostFree(run_ids_host);
         for (int fd : fds)
             if (fd >= 0) close(fd);
         if (dev_block) (void) hipFree(dev_block);
@@ -910,6 +916,43 @@ int qwmoe_expert_cache_load_prefetch(qwmoe_expert_cache* c, const char* path, ui
     const int rc = c->flush();
     if (n_prefetched) *n_prefetched = n;
     return rc;
+}
+
+int qwmoe_expert_cache_run_layer(qwmoe_expert_cache* c, int layer, const qwmoe_layer* L, const float* x, int64_t T,
+                                 float* out, float rms_eps, float* x_next, int32_t* ids_out, float* weights_out) {
+    if (!valid_role_layer(c, 0, layer) || !L || !x || !out || T < 0) return QWMOE_ERR_INVALID_ARG;
+    if (c->dry) return QWMOE_ERR_UNSUPPORTED;
+    if (L->n_expert != c->n_expert || L->n_expert_used <= 0 || T > 64) return QWMOE_ERR_INVALID_ARG;
+    if (T == 0) return QWMOE_OK;
+    const size_t n = (size_t) T * (size_t) L->n_expert_used;
+    if (n > c->run_cap) {
+        if (c->run_ids_dev) (void) hipFree(c->run_ids_dev);
+        if (c->run_ids_host) (void) hipHostFree(c->run_ids_host);
+        c->run_ids_dev = nullptr;
+        c->run_ids_host = nullptr;
+        c->run_cap = 0;
+        const size_t cap = (size_t) 64 * (size_t) L->n_expert_used;
+        if (hipMalloc(&c->run_ids_dev, cap * 8) != hipSuccess ||
+            hipHostMalloc(&c->run_ids_host, cap * 4, hipHostMallocDefault) != hipSuccess) {
+            (void) hipGetLastError();
+            return QWMOE_ERR_HIP;
+        }
+        c->run_w_dev = (float*) (c->run_ids_dev + cap);
+        c->run_cap = cap;
+    }
+    // the router's selection, read back (the reference's ensure_layer)
+    int rc = qwmoe_router_topk(c->stream, L->router, x, L->n_embd, L->n_expert, L->n_expert_used, T,
+                               (size_t) L->n_embd * 4, 6.103515625e-5f, L->expert_weights_scale, c->run_ids_dev,
+                               c->run_w_dev, nullptr);
+    if (rc != QWMOE_OK) return rc;
+    if (hipMemcpyAsync(c->run_ids_host, c->run_ids_dev, n * 4, hipMemcpyDeviceToHost, c->stream) != hipSuccess ||
+        hipStreamSynchronize(c->stream) != hipSuccess)
+        return QWMOE_ERR_HIP;
+    if ((rc = qwmoe_expert_cache_ensure(c, layer, c->run_ids_host, (int) n, nullptr, nullptr, nullptr)) != QWMOE_OK)
+        return rc;
+    qwmoe_layer Lc = *L;
+    if ((rc = qwmoe_expert_cache_layer(c, layer, &Lc)) != QWMOE_OK) return rc;
+    return qwmoe_ffn_layer(c->stream, &Lc, x, T, out, rms_eps, x_next, ids_out, weights_out);
 }
 
 int qwmoe_expert_cache_sync(qwmoe_expert_cache* c) {

@@ -513,3 +513,17 @@ class ExpertCache:
 
     def sync(self) -> None:
         check(lib().qwmoe_expert_cache_sync(self.h), "expert_cache_sync")
+
+    def run_layer(self, layer: int, L: Layer, x, rms_eps: float = -1.0):
+        """decode_cached for one layer: router ids read back, ensure(), the layer on
+        the pools.  x: f32 [T, H] -> (out, x_next or None, ids, weights)."""
+        torch = _torch()
+        T, H = x.shape
+        k = L.n_expert_used
+        out = torch.empty((T, H), dtype=torch.float32, device=x.device)
+        xn = torch.empty((T, H), dtype=torch.float32, device=x.device) if rms_eps >= 0 else None
+        ids = torch.empty((T, k), dtype=torch.int32, device=x.device)
+        w = torch.empty((T, k), dtype=torch.float32, device=x.device)
+        check(lib().qwmoe_expert_cache_run_layer(self.h, layer, C.byref(L), _ptr(x), T, _ptr(out), rms_eps, _ptr(xn),
+                                                 _ptr(ids), _ptr(w)), "expert_cache_run_layer")
+        return out, xn, ids, w

@@ -304,14 +304,18 @@ def test_decode_stack_through_cache():
             n_spec_ok += 1
             continue
         assert cl.cache.stats()["hits"] == hits0
-        # miss: per-layer path -- router, ensure, experts (decode_cached)
+        # miss: per-layer path -- router, ensure, experts (decode_cached), through
+        # qwmoe_expert_cache_run_layer on odd tokens and host calls on even ones
         n_fallback += 1
         xl = x.view(1, H)
         for l in range(n_layer):
-            _, _, lid, _ = ops.ffn_layer(cl.cached[l], xl, rms_eps=eps)
-            cl.cache.ensure(l, lid.cpu().numpy().reshape(-1).tolist())
-            lout, xn, lid2, _ = ops.ffn_layer(cl.cached[l], xl, rms_eps=eps)
-            assert torch.equal(lid2, lid)
+            if t % 2:
+                lout, xn, lid2, _ = cl.cache.run_layer(l, cl.cached[l], xl, rms_eps=eps)
+            else:
+                _, _, lid, _ = ops.ffn_layer(cl.cached[l], xl, rms_eps=eps)
+                cl.cache.ensure(l, lid.cpu().numpy().reshape(-1).tolist())
+                lout, xn, lid2, _ = ops.ffn_layer(cl.cached[l], xl, rms_eps=eps)
+                assert torch.equal(lid2, lid)
             assert torch.equal(lid2.view(-1), ref_ids[l]), f"token {t} layer {l} ids"
             xl = xn
         torch.cuda.synchronize()
