@@ -408,3 +408,17 @@ def test_gguf_pools_dry(tmp_path):
         c = ops.ExpertCache.from_gguf(g, 1, 0, dry_run=True)
         assert [(x["role"], x["type"], x["ne0"], x["ne1"]) for x in c.pools()] == \
             [(0, Q4_K, FX.H, FX.F_EXP), (1, Q4_K, FX.H, FX.F_EXP), (2, Q4_K, FX.F_EXP, FX.H)]
+
+
+def test_run_layer_needs_device_pools():
+    ops = lib_or_skip()
+    from questwend_amd import Layer, QwmoeError
+    sigs = uniform_sigs(1)
+    c = make_lib(ops, 1, 16, 2, sigs, 0)
+    import ctypes as C
+    L = Layer()
+    L.n_embd, L.n_expert, L.n_expert_used, L.n_ff = 256, 16, 2, 256
+    rc = ops.lib().qwmoe_expert_cache_run_layer(c.h, 0, C.byref(L), 1, 1, 1, -1.0, None, None, None)
+    assert rc != 0
+    with pytest.raises(QwmoeError):
+        ops.check(rc, "run_layer")

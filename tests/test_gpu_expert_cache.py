@@ -332,3 +332,37 @@ def test_decode_stack_through_cache():
     spec_stack.close()
     ref_stack.close()
     cl.cache.close()
+
+
+def test_file_tier_read_failure_leaves_slots_empty(tmp_path):
+    """A file-tier fetch whose read fails (the file truncated under the cache,
+    forced from the host) returns QWMOE_ERR_IO, leaves the unread slots absent,
+    counts no fetched bytes for them, and the same call succeeds once the file
+    is back."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import gguf_fixtures as FX
+    FX.write_all(tmp_path, Oracle())
+    path = tmp_path / "moe_tiny.gguf"
+    good = path.read_bytes()
+    note("file tier: read failure on a truncated file, then recovery")
+    with ops.Gguf(path) as g:
+        cache = ops.ExpertCache.from_gguf(g, 1, 10 ** 9, io_threads=2)
+        cache.ensure(0, [0, 1])
+        before = cache.stats()
+        path.write_bytes(good[:4096])            # the data section is gone
+        with pytest.raises(qa.QwmoeError) as ei:
+            cache.ensure(1, [2, 3])
+        assert ei.value.status == -7             # QWMOE_ERR_IO
+        for r in range(3):
+            for e in (2, 3):
+                assert not cache.resident(r, 1, e)
+            for e in (0, 1):
+                assert cache.resident(r, 0, e)
+        after = cache.stats()
+        assert after["fetch_bytes"] == before["fetch_bytes"]
+        assert after["misses"] == before["misses"] + 6
+        path.write_bytes(good)
+        cache.ensure(1, [2, 3])
+        cache.sync()
+        assert all(cache.resident(r, 1, e) for r in range(3) for e in (2, 3))
+        cache.close()
