@@ -120,8 +120,8 @@ struct Grouping {
     int64_t max_active;
 };
 
-int group(hipStream_t st, Arena& ar, const int32_t* ids, int64_t n_ids, int64_t T, size_t ids_nb1, int64_t n_bins,
-          int32_t* counts, int32_t* offsets, int32_t* rows_out, Grouping& G) {
+int group_args(Arena& ar, const int32_t* ids, int64_t n_ids, int64_t T, size_t ids_nb1, int64_t n_bins,
+               int32_t* counts, int32_t* offsets, int32_t* rows_out, Grouping& G, qw::GroupArgs& g) {
     const int64_t P = n_ids * T;
     G.max_active = std::min<int64_t>(n_bins, P);
     G.rows = rows_out ? rows_out : ar.take<int32_t>((size_t) (2 * P + 2));
@@ -132,7 +132,7 @@ int group(hipStream_t st, Arena& ar, const int32_t* ids, int64_t n_ids, int64_t 
     if (!G.rows || !G.active || !G.active_off || !G.n_active || !hist) return QWMOE_ERR_WORKSPACE;
     G.counts = counts;
     G.offsets = offsets;
-    qw::GroupArgs g{};
+    g = qw::GroupArgs{};
     g.ids = ids;
     g.n_ids = n_ids;
     g.T = T;
@@ -146,7 +146,14 @@ int group(hipStream_t st, Arena& ar, const int32_t* ids, int64_t n_ids, int64_t 
     g.n_active = G.n_active;
     g.status = g_lib.status;
     g.hist_ws = hist;
-    return qw::launch_group(g, st);
+    return QWMOE_OK;
+}
+
+int group(hipStream_t st, Arena& ar, const int32_t* ids, int64_t n_ids, int64_t T, size_t ids_nb1, int64_t n_bins,
+          int32_t* counts, int32_t* offsets, int32_t* rows_out, Grouping& G) {
+    qw::GroupArgs g;
+    const int rc = group_args(ar, ids, n_ids, T, ids_nb1, n_bins, counts, offsets, rows_out, G, g);
+    return rc != QWMOE_OK ? rc : qw::launch_group(g, st);
 }
 
 }  // namespace
@@ -390,10 +397,20 @@ int qwmoe_ffn_layer(void* stream, const qwmoe_layer* L, const float* x, int64_t 
     if (!xg || !xu) return QWMOE_ERR_WORKSPACE;
     const bool xq_fused = T <= 16 && vg == qw::T_Q8_K && H % 256 == 0;
     ra.xq = xq_fused ? xg : nullptr;
-    if ((rc = qw::launch_router(ra, logits, st))) return rc;
     // grouping by logical expert (slot rows are injective for resident layers)
     Grouping G{};
-    if ((rc = group(st, ar, ids, k, T, (size_t) k * 4, E, nullptr, nullptr, nullptr, G))) return rc;
+    if (T <= qw::GROUP_WAVES && E <= 128) {
+        // small batch: logits (+ Q8_K of x), then top-k and grouping in one launch
+        qw::GroupArgs g;
+        if ((rc = group_args(ar, ids, k, T, (size_t) k * 4, E, nullptr, nullptr, nullptr, G, g))) return rc;
+        qw::RouterArgs rl = ra;
+        rl.ids = nullptr;
+        if ((rc = qw::launch_router(rl, logits, st))) return rc;
+        if ((rc = qw::launch_topk_group(ra, logits, g, st))) return rc;
+    } else {
+        if ((rc = qw::launch_router(ra, logits, st))) return rc;
+        if ((rc = group(st, ar, ids, k, T, (size_t) k * 4, E, nullptr, nullptr, nullptr, G))) return rc;
+    }
     if (!xq_fused && (rc = qw::launch_quantize_act(vg, x, H, 1, T, (size_t) H * 4, (size_t) H * 4, xg, st))) return rc;
     if (xu != xg && (rc = qw::launch_quantize_act(vu, x, H, 1, T, (size_t) H * 4, (size_t) H * 4, xu, st))) return rc;
     const size_t dnb1 = (size_t) F * 4, dnb2 = (size_t) F * 4 * (size_t) k;

@@ -13,6 +13,7 @@
 
 #include "qw_kernels.hpp"
 #include "qw_rowdot.hpp"
+#include "qw_topk.hpp"
 
 namespace qw {
 
@@ -83,10 +84,10 @@ __device__ __forceinline__ int pair_key(const GroupArgs& g, int f, int f1, int& 
     return key;
 }
 
+// The grouping itself, for a GROUP_WAVES * 64-thread workgroup: s_hist holds
+// GROUP_WAVES * n_bins counters when IN_LDS, s_wsum 2 * GROUP_WAVES words.
 template <bool IN_LDS>
-__global__ void __launch_bounds__(GROUP_WAVES * 64) k_group(GroupArgs g) {
-    __shared__ int32_t s_hist[IN_LDS ? GROUP_WAVES * GROUP_LDS_BINS : 1];
-    __shared__ int32_t s_wsum[2][GROUP_WAVES];
+__device__ __forceinline__ void group_body(const GroupArgs& g, int32_t* s_hist, int32_t (*s_wsum)[GROUP_WAVES]) {
     const int lane = threadIdx.x & 63;
     const int w = threadIdx.x >> 6;
     const int P = (int) (g.T * g.n_ids);
@@ -191,6 +192,49 @@ __global__ void __launch_bounds__(GROUP_WAVES * 64) k_group(GroupArgs g) {
             }
         }
     }
+}
+
+template <bool IN_LDS>
+__global__ void __launch_bounds__(GROUP_WAVES * 64) k_group(GroupArgs g) {
+    __shared__ int32_t s_hist[IN_LDS ? GROUP_WAVES * GROUP_LDS_BINS : 1];
+    __shared__ int32_t s_wsum[2][GROUP_WAVES];
+    group_body<IN_LDS>(g, s_hist, s_wsum);
+}
+
+// Small batches (T <= GROUP_WAVES tokens, E <= 128): the router's softmax /
+// top-k / weights for token t on wave t (the k_router_topk steps, with wave
+// barriers), then the grouping of all tokens' ids by the whole workgroup, in one
+// launch.  Dynamic LDS: per wave p[E], order[E], gsum[E / 8], the sort stack and
+// a flag; then the GROUP_WAVES * E counters.
+__global__ void __launch_bounds__(GROUP_WAVES * 64) k_topk_group(RouterArgs ra, const float* __restrict__ logits,
+                                                                 GroupArgs g) {
+    extern __shared__ uint32_t dyn[];
+    __shared__ int32_t s_wsum[2][GROUP_WAVES];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int E = (int) ra.E;
+    const uint32_t per_wave = (uint32_t) (2 * E + E / 8 + 1) * 4u + (uint32_t) sizeof(SortRange) * SORT_STACK;
+    uint8_t* mine = (uint8_t*) dyn + (size_t) w * ((per_wave + 15u) & ~15u);
+    float* p = (float*) mine;
+    int32_t* order = (int32_t*) (p + E);
+    float* gsum = (float*) (order + E);
+    int* need_sort = (int*) (gsum + E / 8);
+    SortRange* stack = (SortRange*) (need_sort + 1);
+    if (w < ra.T)
+        topk_token<true>(logits, ra.E, ra.k, w, ra.clamp_min, ra.scale, ra.ids, ra.weights, ra.probs, ra.status, p, gsum,
+                         order, stack, need_sort, lane);
+    __syncthreads();   // every token's ids are written
+    int32_t* hist = (int32_t*) ((uint8_t*) dyn + (size_t) GROUP_WAVES * ((per_wave + 15u) & ~15u));
+    group_body<true>(g, hist, s_wsum);
+}
+
+int launch_topk_group(const RouterArgs& ra, const float* logits, const GroupArgs& g, hipStream_t stream) {
+    if (ra.T < 1 || ra.T > GROUP_WAVES || ra.E % 8 || ra.E > 128 || ra.k < 1 || ra.k > ra.E || !ra.ids || !ra.weights)
+        return -2;
+    if (g.n_bins != ra.E || g.ids != ra.ids || g.n_ids != ra.k || g.T != ra.T || g.ids_stride != ra.k) return -2;
+    const uint32_t per_wave = (uint32_t) (2 * ra.E + ra.E / 8 + 1) * 4u + (uint32_t) sizeof(SortRange) * SORT_STACK;
+    const size_t lds = (size_t) GROUP_WAVES * ((per_wave + 15u) & ~15u) + (size_t) GROUP_WAVES * ra.E * 4;
+    hipLaunchKernelGGL(k_topk_group, dim3(1), dim3(GROUP_WAVES * 64), lds, stream, ra, logits, g);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
 int launch_group(const GroupArgs& g, hipStream_t stream) {

@@ -47,6 +47,8 @@ struct GroupArgs {
 };
 constexpr int GROUP_WAVES = 16;
 int launch_group(const GroupArgs& g, hipStream_t stream);
+// small batches: top-k (from ready logits) and grouping in one launch; ra.ids must be g.ids
+int launch_topk_group(const RouterArgs& ra, const float* logits, const GroupArgs& g, hipStream_t stream);
 
 struct MmidArgs {
     int type;                 // weight type

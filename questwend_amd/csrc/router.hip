@@ -8,6 +8,7 @@
 //   w      = get_rows / sum_rows / clamp(6.103515625e-5, inf) / div (/ scale)
 #include "qw_kernels.hpp"
 #include "qw_sort.hpp"
+#include "qw_topk.hpp"
 
 namespace qw {
 
@@ -99,76 +100,20 @@ __global__ void __launch_bounds__(32 * EPW) k_router_logits(const float* __restr
     }
 }
 
-// Softmax, exact top-k and weight normalisation for one token per wave.
-// Supports E % 8 == 0 and E <= 64 * ROUTER_EPL.
+// Softmax, exact top-k and weight normalisation for one token per 64-thread
+// workgroup.  Supports E % 8 == 0 and E <= 64 * ROUTER_EPL.
 constexpr int ROUTER_EPL = 8;
 __global__ void __launch_bounds__(64) k_router_topk(const float* __restrict__ logits, int64_t E, int64_t k,
                                                     int64_t T, float clamp_min, float scale, int32_t* __restrict__ ids,
                                                     float* __restrict__ weights, float* __restrict__ probs_out,
                                                     int32_t* __restrict__ status) {
-    __shared__ float p[64 * ROUTER_EPL];
+    __shared__ __align__(16) float p[64 * ROUTER_EPL];
     __shared__ float gsum[64 * ROUTER_EPL / 8];
     __shared__ int32_t order[64 * ROUTER_EPL];
     __shared__ SortRange sort_stack[SORT_STACK];
     __shared__ int need_sort;
-    const int lane = threadIdx.x;
-    const int64_t t = blockIdx.x;
-    const float* l = logits + t * E;
-    float mx = -INFINITY;
-    for (int64_t i = lane; i < E; i += 64) mx = fmaxf(mx, l[i]);
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-    for (int64_t i = lane; i < E; i += 64) p[i] = v_expf(l[i] - mx);
-    if (lane == 0) need_sort = 0;
-    __syncthreads();
-    const int64_t ng = E / 8;
-    for (int64_t gi = lane; gi < ng; gi += 64) gsum[gi] = hsum8(&p[8 * gi]);
-    __syncthreads();
-    double sum = 0.0;
-    if (lane == 0)
-        for (int64_t gi = 0; gi < ng; ++gi) sum += (double) gsum[gi];
-    sum = __shfl(sum, 0);
-    const float inv = (float) (1.0 / sum);
-    for (int64_t i = lane; i < E; i += 64) p[i] = p[i] * inv;
-    __syncthreads();
-    if (probs_out)
-        for (int64_t i = lane; i < E; i += 64) probs_out[t * E + i] = p[i];
-    // rank of every element; a tie group that reaches into the first k places
-    // leaves the order to std::sort's algorithm, which is then replayed exactly.
-    // A NaN (eq == 0) goes to the replay too: softmax makes every probability NaN
-    // then, which std::sort treats as all equivalent.
-    for (int64_t i = lane; i < E; i += 64) {
-        const float pi = p[i];
-        int gt = 0, eq = 0;
-        for (int64_t j = 0; j < E; ++j) {
-            gt += p[j] > pi;
-            eq += p[j] == pi;
-        }
-        if (gt < k) {
-            if (eq != 1) need_sort = 1;
-            else order[gt] = (int32_t) i;
-        }
-    }
-    __syncthreads();
-    if (need_sort) {
-        if (lane == 0) {
-            for (int64_t i = 0; i < E; ++i) order[i] = (int32_t) i;
-            libstdcxx_sort_desc(order, (int) E, p, sort_stack);
-            if (status) atomicOr(status, 1);
-        }
-        __syncthreads();
-    }
-    if (lane == 0) {
-        double s = 0.0;
-        for (int64_t i = 0; i < k; ++i) s += (double) p[order[i]];
-        float wsum = (float) s;
-        wsum = fmaxf(fminf(wsum, INFINITY), clamp_min);
-        for (int64_t i = 0; i < k; ++i) {
-            float wi = p[order[i]] / wsum;
-            if (scale != 0.0f && scale != 1.0f) wi = wi * scale;
-            ids[t * k + i] = order[i];
-            weights[t * k + i] = wi;
-        }
-    }
+    topk_token<false>(logits, E, k, blockIdx.x, clamp_min, scale, ids, weights, probs_out, status, p, gsum, order,
+                      sort_stack, &need_sort, threadIdx.x);
 }
 
 int launch_router(const RouterArgs& a, float* logits_ws, hipStream_t stream) {
@@ -186,6 +131,7 @@ int launch_router(const RouterArgs& a, float* logits_ws, hipStream_t stream) {
         hipLaunchKernelGGL((k_router_logits<4, 8>), g1, dim3(256), 0, stream, a.W, a.x, a.x_stride, a.H, a.E, a.T,
                            logits, (BlockQ8_K*) nullptr);
     }
+    if (!a.ids) return hipGetLastError() == hipSuccess ? 0 : -3;   // logits only (top-k fused elsewhere)
     hipLaunchKernelGGL(k_router_topk, dim3((unsigned) a.T), dim3(64), 0, stream, logits, a.E, a.k, a.T, a.clamp_min,
                        a.scale, a.ids, a.weights, a.probs, a.status);
     return hipGetLastError() == hipSuccess ? 0 : -3;

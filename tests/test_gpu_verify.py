@@ -167,3 +167,22 @@ def test_config0_q8_0_decode_e128(orc):
         assert np.array_equal(bits(w.cpu().numpy()), bits(r["weights"])), f"token {t} weights"
         assert np.array_equal(bits(out.cpu().numpy()), bits(r["out"])), f"token {t} out"
         assert np.array_equal(bits(xn.cpu().numpy()), bits(r["xnext"])), f"token {t} x_next"
+
+
+@pytest.mark.parametrize("T", [1, 3, 16])
+def test_small_batch_router_ties(orc, T):
+    """Small batches take the router's top-k and the grouping in one launch (a
+    wave per token); with router rows duplicated in pairs every top-k has ties,
+    which the std::sort replay inside that launch must order as ggml does."""
+    note(f"small-batch router ties: T={T}, H=1024 E=16 k=4 F=512")
+    g = GpuLayer(1024, 16, 4, 512, (Q4_K,) * 3, seed=950 + T, dup_router=True)
+    x = np.random.default_rng(T).standard_normal((T, 1024)).astype(np.float32)
+    ops.device_status(clear=True)
+    out, xn, ids, w = ops.ffn_layer(g.layer, torch.from_numpy(x).to(DEV), rms_eps=1e-6)
+    torch.cuda.synchronize()
+    r = orc.moe_layer(g.host, x, rms_eps=1e-6)
+    assert np.array_equal(ids.cpu().numpy(), r["ids"])
+    assert np.array_equal(bits(w.cpu().numpy()), bits(r["weights"]))
+    assert np.array_equal(bits(out.cpu().numpy()), bits(r["out"]))
+    assert np.array_equal(bits(xn.cpu().numpy()), bits(r["xnext"]))
+    assert ops.device_status(clear=True) & 1      # the replay ran
