@@ -229,7 +229,8 @@ void qwmoe_decode_stack_free(qwmoe_decode_stack * s);
  * (1503-1525); mul_mat_id settings (qwmoe_set_mfma_min_rows) are those at
  * capture.  Layers must share n_embd and n_expert_used.  Creation allocates the
  * stack's buffers; the first run at each T captures and instantiates a graph;
- * later runs allocate nothing. */
+ * later runs allocate nothing (a run after qwmoe_init reallocated the workspace
+ * captures again). */
 #define QWMOE_STACK_NO_GRAPH 1     /* run the chain eagerly every time */
 typedef struct qwmoe_layer_stack qwmoe_layer_stack;
 int qwmoe_layer_stack_create(const qwmoe_layer * layers, int n_layer, float rms_eps, int max_tokens, int flags,

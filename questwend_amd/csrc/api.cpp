@@ -5,6 +5,7 @@
 #include <algorithm>
 #include <cstdint>
 #include <cstring>
+#include <atomic>
 #include <mutex>
 #include <new>
 #include <random>
@@ -29,6 +30,7 @@ struct Library {
 
 Library g_lib;
 std::mutex g_mu;
+std::atomic<uint64_t> g_ws_generation{1};   // changes whenever the workspace is (re)allocated or freed
 
 // Bump allocator over the workspace for one call.
 struct Arena {
@@ -158,6 +160,10 @@ int group(hipStream_t st, Arena& ar, const int32_t* ids, int64_t n_ids, int64_t 
 
 }  // namespace
 
+namespace qw {
+uint64_t workspace_generation() { return g_ws_generation.load(); }
+}  // namespace qw
+
 extern "C" {
 
 int qwmoe_init(int device, size_t workspace_bytes) {
@@ -178,6 +184,7 @@ int qwmoe_init(int device, size_t workspace_bytes) {
     g_lib.status = (int32_t*) p;
     g_lib.device = device;
     g_lib.ready = true;
+    g_ws_generation.fetch_add(1);
     return QWMOE_OK;
 }
 
@@ -187,6 +194,7 @@ int qwmoe_shutdown(void) {
     (void) hipDeviceSynchronize();
     (void) hipFree(g_lib.ws);
     g_lib = Library{};
+    g_ws_generation.fetch_add(1);
     return QWMOE_OK;
 }
 

@@ -18,6 +18,7 @@
 #include <vector>
 
 #include "../../include/qwmoe.h"
+#include "qw_kernels.hpp"
 
 struct qwmoe_layer_stack {
     std::vector<qwmoe_layer> layers;
@@ -32,6 +33,7 @@ struct qwmoe_layer_stack {
     float* w = nullptr;                  // [n_layer][max_T][k]
     hipStream_t cap = nullptr;           // capture stream
     std::vector<hipGraphExec_t> exec;    // [T]: the captured chain, or null
+    std::vector<uint64_t> exec_gen;      // [T]: the library workspace generation it was captured with
 
     ~qwmoe_layer_stack() {
         for (hipGraphExec_t e : exec)
@@ -52,6 +54,7 @@ struct qwmoe_layer_stack {
     }
 
     int capture(int64_t T) {
+        const uint64_t gen = qw::workspace_generation();
         if (!cap && hipStreamCreateWithFlags(&cap, hipStreamNonBlocking) != hipSuccess) return QWMOE_ERR_HIP;
         if (hipStreamBeginCapture(cap, hipStreamCaptureModeThreadLocal) != hipSuccess) return QWMOE_ERR_HIP;
         const int rc = enqueue(cap, T);
@@ -67,6 +70,7 @@ struct qwmoe_layer_stack {
         (void) hipGraphDestroy(g);
         if (ei != hipSuccess) return QWMOE_ERR_HIP;
         exec[(size_t) T] = e;
+        exec_gen[(size_t) T] = gen;
         return QWMOE_OK;
     }
 };
@@ -93,6 +97,7 @@ int qwmoe_layer_stack_create(const qwmoe_layer* layers, int n_layer, float rms_e
     s->k = L0.n_expert_used;
     s->graphs = (flags & QWMOE_STACK_NO_GRAPH) == 0;
     s->exec.assign((size_t) max_tokens + 1, nullptr);
+    s->exec_gen.assign((size_t) max_tokens + 1, 0);
     auto a256 = [](size_t n) { return (n + 255) & ~(size_t) 255; };
     const size_t xs = a256((size_t) max_tokens * (size_t) s->H * 4);
     const size_t is = a256((size_t) n_layer * (size_t) max_tokens * (size_t) s->k * 4);
@@ -121,6 +126,12 @@ int qwmoe_layer_stack_run(void* stream, qwmoe_layer_stack* s, const float* x, in
     if (hipMemcpyAsync(s->xb[0], x, xbytes, hipMemcpyDeviceToDevice, st) != hipSuccess) return QWMOE_ERR_HIP;
     int rc;
     if (s->graphs) {
+        // a graph holds the workspace addresses of its capture: re-capture after qwmoe_init reallocated it
+        if (s->exec[(size_t) T] && s->exec_gen[(size_t) T] != qw::workspace_generation()) {
+            if (hipStreamSynchronize(st) != hipSuccess) return QWMOE_ERR_HIP;   // its last replay has finished
+            (void) hipGraphExecDestroy(s->exec[(size_t) T]);
+            s->exec[(size_t) T] = nullptr;
+        }
         if (!s->exec[(size_t) T] && (rc = s->capture(T)) != QWMOE_OK) return rc;
         if (hipGraphLaunch(s->exec[(size_t) T], st) != hipSuccess) return QWMOE_ERR_HIP;
     } else if ((rc = s->enqueue(st, T)) != QWMOE_OK) {

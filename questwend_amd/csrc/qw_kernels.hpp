@@ -47,6 +47,9 @@ struct GroupArgs {
 };
 constexpr int GROUP_WAVES = 16;
 int launch_group(const GroupArgs& g, hipStream_t stream);
+// api.cpp: changes whenever the library workspace is (re)allocated or freed (captured graphs
+// that baked in workspace addresses are stale then)
+uint64_t workspace_generation();
 // small batches: top-k (from ready logits) and grouping in one launch; ra.ids must be g.ids
 int launch_topk_group(const RouterArgs& ra, const float* logits, const GroupArgs& g, hipStream_t stream);
 

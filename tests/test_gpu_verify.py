@@ -186,3 +186,21 @@ def test_small_batch_router_ties(orc, T):
     assert np.array_equal(bits(out.cpu().numpy()), bits(r["out"]))
     assert np.array_equal(bits(xn.cpu().numpy()), bits(r["xnext"]))
     assert ops.device_status(clear=True) & 1      # the replay ran
+
+
+def test_layer_stack_recaptures_after_workspace_realloc(layers3):
+    """A captured graph holds the library workspace's addresses; after qwmoe_init
+    reallocates the workspace the next run captures again and gives the same
+    result."""
+    note("layer stack: graph re-captured after the workspace is reallocated")
+    stack = ops.LayerStack([g.layer for g in layers3], 1e-6, max_tokens=4, keepalive=layers3)
+    x = torch.from_numpy(np.random.default_rng(21).standard_normal((3, 1024)).astype(np.float32)).to(DEV)
+    o1, xo1, ids1, _ = stack(x)
+    torch.cuda.synchronize()
+    ops.init(0, 640 << 20)              # a larger workspace: freed and allocated again
+    o2, xo2, ids2, _ = stack(x)
+    torch.cuda.synchronize()
+    assert torch.equal(ids1, ids2)
+    assert torch.equal(o1.view(torch.int32), o2.view(torch.int32))
+    assert torch.equal(xo1.view(torch.int32), xo2.view(torch.int32))
+    stack.close()
