@@ -346,7 +346,8 @@ int qwmoe_gguf_load_moe_layer(void * stream, qwmoe_gguf * g, int il, void * dev,
  * pinned staging, then copied asynchronously: the SSD tier of cpp:297-352 and
  * 412-687, without the opt-in coalescing).  Every copy and row upload is
  * issued on the cache's stream, so work the caller issues on that stream
- * afterwards sees the slabs; calls on one cache must not overlap. */
+ * afterwards sees the slabs; calls on one cache must not overlap, and the
+ * stream must outlive the cache (freeing it waits for that stream). */
 typedef struct qwmoe_expert_cache qwmoe_expert_cache;
 
 typedef struct qwmoe_expert_src {
