@@ -194,6 +194,70 @@ __device__ __forceinline__ void group_body(const GroupArgs& g, int32_t* s_hist, 
     }
 }
 
+// The same grouping by one wave when there are at most 64 pairs and 128 bins:
+// lane p holds pair p; in-bin ranks from the ballots of chunk_rank; the bins'
+// counts (two bins per lane) are scanned across the wave for the offsets and the
+// active list.  cnt: 128 LDS words.
+__device__ __forceinline__ void group_wave(const GroupArgs& g, int32_t* cnt) {
+    const int lane = threadIdx.x & 63;
+    const int P = (int) (g.T * g.n_ids);
+    const int nb = (int) g.n_bins;
+    int t, e;
+    const int key = pair_key(g, lane, P, t, e, true);
+    const int nbits = nb > 1 ? 32 - __clz(nb - 1) : 0;
+    const ChunkRank r = chunk_rank(key, nbits);
+    cnt[lane] = 0;
+    cnt[lane + 64] = 0;
+    wave_sync();
+    if (key >= 0 && r.rank == 0) cnt[key] = r.cnt;
+    wave_sync();
+    const int b0 = 2 * lane, b1 = 2 * lane + 1;
+    const int c0 = b0 < nb ? cnt[b0] : 0, c1 = b1 < nb ? cnt[b1] : 0;
+    int ic = c0 + c1, ia = (c0 > 0) + (c1 > 0);
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int uc = __shfl_up(ic, d), ua = __shfl_up(ia, d);
+        if (lane >= d) {
+            ic += uc;
+            ia += ua;
+        }
+    }
+    const int tc = __shfl(ic, 63), ta = __shfl(ia, 63);
+    const int off0 = ic - (c0 + c1), off1 = off0 + c0;
+    int aidx = ia - ((c0 > 0) + (c1 > 0));
+    if (b0 < nb) {
+        if (g.counts) g.counts[b0] = c0;
+        if (g.offsets) g.offsets[b0] = off0;
+        if (c0 > 0) {
+            g.active[aidx] = b0;
+            g.active_off[aidx] = off0;
+            ++aidx;
+        }
+    }
+    if (b1 < nb) {
+        if (g.counts) g.counts[b1] = c1;
+        if (g.offsets) g.offsets[b1] = off1;
+        if (c1 > 0) {
+            g.active[aidx] = b1;
+            g.active_off[aidx] = off1;
+        }
+    }
+    if (lane == 0) {
+        if (g.n_active) *g.n_active = ta;
+        if (g.offsets) g.offsets[nb] = tc;
+        g.active_off[ta] = tc;
+    }
+    wave_sync();
+    cnt[b0] = off0;   // (bins past nb are never a key)
+    cnt[b1] = off1;
+    wave_sync();
+    if (key >= 0) {
+        const int pos = cnt[key] + r.rank;
+        g.rows[2 * pos] = e;
+        g.rows[2 * pos + 1] = t;
+    }
+}
+
 template <bool IN_LDS>
 __global__ void __launch_bounds__(GROUP_WAVES * 64) k_group(GroupArgs g) {
     __shared__ int32_t s_hist[IN_LDS ? GROUP_WAVES * GROUP_LDS_BINS : 1];
@@ -224,7 +288,11 @@ __global__ void __launch_bounds__(GROUP_WAVES * 64) k_topk_group(RouterArgs ra, 
                          order, stack, need_sort, lane);
     __syncthreads();   // every token's ids are written
     int32_t* hist = (int32_t*) ((uint8_t*) dyn + (size_t) GROUP_WAVES * ((per_wave + 15u) & ~15u));
-    group_body<true>(g, hist, s_wsum);
+    if (ra.T * ra.k <= 64) {
+        if (w == 0) group_wave(g, hist);
+    } else {
+        group_body<true>(g, hist, s_wsum);
+    }
 }
 
 int launch_topk_group(const RouterArgs& ra, const float* logits, const GroupArgs& g, hipStream_t stream) {
