@@ -437,6 +437,103 @@ def verify_bench(args) -> int:
     return 0
 
 
+def config5_bench(args) -> int:
+    """the large-expert regime, 94 MoE layers (H=4096, E=128, top-8,
+    F=1536), Q4_K gate/up and Q6_K down, every layer's experts stored at a seeded
+    random slot permutation read through the slot rows.  Decode at batch 1
+    through all 94 layers (qwmoe_layer_stack at T = 1, its captured graph; the
+    persistent decode kernel's LDS plan does not cover this shape) and prefill of
+    1024 tokens through one layer (qwmoe_ffn_layer, Zipf(1.1)-skewed router)."""
+    import numpy as np
+    import torch
+    from questwend_amd import Q4_K, Q6_K, ops, row_size
+
+    H5, E5, K5, F5, NL5 = 4096, 128, 8, 1536, 94
+    types = (Q4_K, Q4_K, Q6_K)
+    ops.init(0, 1 << 30)
+    dev = "cuda:0"
+    chunk = 8
+    tmp = torch.empty(chunk * F5 * H5, dtype=torch.float32, device=dev)
+    layers, keep = [], []
+    t_gen = time.perf_counter()
+    g = torch.Generator().manual_seed(args.seed)
+    for l in range(NL5):
+        router = torch.empty((E5, H5), dtype=torch.float32, device=dev)
+        ops.randn_(router, args.seed * 1000 + l * 10, 0.0, 0.02)
+        mats, slots = [], []
+        for role, (rows, cols) in enumerate(((F5, H5), (F5, H5), (H5, F5))):
+            q = torch.empty((E5 * rows, row_size(types[role], cols)), dtype=torch.uint8, device=dev)
+            perm = torch.randperm(E5, generator=g).to(torch.int32)
+            for e0 in range(0, E5, chunk):
+                n = chunk * rows * cols
+                ops.randn_(tmp[:n], args.seed * 1000 + l * 10 + 1 + role * 100000 + e0, 0.0, 0.02)
+                # logical experts e0..e0+chunk go to their slots perm[e]
+                qc = ops.quantize_chunk(types[role], tmp[:n].view(chunk * rows, cols)).view(chunk, rows, -1)
+                q.view(E5, rows, -1)[perm[e0:e0 + chunk].long().to(dev)] = qc
+            mats.append(q)
+            slots.append(perm.to(dev))
+        L = ops.make_layer(H5, E5, K5, F5, router, *mats, types, n_slots=(E5, E5, E5), slots=tuple(slots))
+        layers.append(L)
+        keep.append((router, mats, slots))
+    torch.cuda.synchronize()
+    del tmp
+    t_gen = time.perf_counter() - t_gen
+
+    # decode: one token through all 94 layers per step
+    stack = ops.LayerStack(layers, RMS_EPS, max_tokens=1, keepalive=keep)
+    xs = torch.empty((args.steps + args.warmup, 1, H5), dtype=torch.float32, device=dev)
+    ops.randn_(xs, args.seed + 4242, 0.0, 1.0)
+    for i in range(args.warmup):
+        stack(xs[i], want_ids=False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        stack(xs[args.warmup + i], want_ids=False)
+    torch.cuda.synchronize()
+    dec_s = (time.perf_counter() - t0) / args.steps
+    expert5 = 2 * F5 * row_size(Q4_K, H5) + H5 * row_size(Q6_K, F5)
+    dec_bytes = NL5 * (K5 * expert5 + E5 * H5 * 4)
+
+    # prefill: 1024 tokens through layer 0, router rows Zipf(1.1)-skewed
+    L0 = layers[0]
+    keep[0][0].mul_(torch.from_numpy(zipf_row_scales(E5, 1.1)).to(dev)[:, None])
+    T5 = 1024
+    x = torch.empty((T5, H5), dtype=torch.float32, device=dev)
+    ops.randn_(x, args.seed + 99, 0.0, 1.0)
+    for _ in range(2):
+        ops.ffn_layer(L0, x, rms_eps=RMS_EPS)
+    torch.cuda.synchronize()
+    reps = max(3, args.steps // 4)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        out, _, ids, _ = ops.ffn_layer(L0, x, rms_eps=RMS_EPS)
+    torch.cuda.synchronize()
+    pre_s = (time.perf_counter() - t0) / reps
+    used = int((np.bincount(ids.cpu().numpy().reshape(-1), minlength=E5) > 0).sum())
+    pre_bytes = used * expert5 + E5 * H5 * 4
+    line = {
+        "metric": "configs[4] decode tok/s (94-layer stack, batch 1) and prefill tok/s (T=1024, one layer)",
+        "value": round(1.0 / dec_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(dec_s * 1e3, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q4_K/q6_K x q8_K -> f32", "data": "synthetic (seeded; slot permutation seeded; prefill router Zipf(1.1))",
+        "config": {"workload": "configs[4]: 94 layers H=4096 E=128 k=8 F=1536, Q4_K gate/up, Q6_K down, permuted slots",
+                   "decode_path": "qwmoe_layer_stack T=1 (captured graph)", "prefill_path": "qwmoe_ffn_layer T=1024"},
+        "decode": {"tok_s": round(1.0 / dec_s, 2), "ms_per_token": round(dec_s * 1e3, 3),
+                   "weight_bytes_per_token": dec_bytes, "gbps": round(dec_bytes / dec_s / 1e9, 1),
+                   "frac_of_8tbs": round(dec_bytes / dec_s / 1e9 / HBM_PEAK_GBS, 4)},
+        "prefill": {"tokens": T5, "ms_per_layer": round(pre_s * 1e3, 3), "tok_s": round(T5 / pre_s, 1),
+                    "used_experts": used, "weight_gbps": round(pre_bytes / pre_s / 1e9, 1)},
+        "roofline": {"bound": "hbm", "achieved": round(dec_bytes / dec_s / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dec_bytes / dec_s / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+                     "note": "decode: selected experts' weights + routers per token / token time"},
+        "weight_gen_s": round(t_gen, 1),
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+    stack.close()
+    return 0
+
+
 def copy_probe(mib: int = 1024, reps: int = 4) -> int:
     """A plain device copy of known size (torch's copy kernel): run under
     ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE`` it gives the factor between
@@ -464,10 +561,10 @@ def main() -> int:
                     help="text file whose 'hbm_bytes_per_launch = N' line is the HBM traffic of one decode "
                          "launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (copy-calibrated)")
     ap.add_argument("--copy-probe", action="store_true", help="run only the copy-kernel calibration probe")
-    ap.add_argument("--workload", choices=["decode", "prefill", "expert_cache", "verify"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "prefill", "expert_cache", "verify", "config5"], default="decode",
                     help="decode: configs[1] (the headline line); prefill: configs[2]; expert_cache: configs[1] "
                          "decode with the experts offloaded to pinned host memory; verify: configs[1] stack on "
-                         "T = 1..--tokens verify batches")
+                         "T = 1..--tokens verify batches; config5: configs[4] decode and prefill")
     ap.add_argument("--resident", type=float, default=0.5, help="expert_cache: fraction of experts in HBM")
     ap.add_argument("--zipf", type=float, default=1.1, help="expert_cache: router skew (0: none)")
     ap.add_argument("--copy-engine", action="store_true",
@@ -489,6 +586,8 @@ def main() -> int:
         return expert_cache_bench(args)
     if args.workload == "verify":
         return verify_bench(args)
+    if args.workload == "config5":
+        return config5_bench(args)
 
     import numpy as np
     import torch

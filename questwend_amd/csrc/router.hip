@@ -12,19 +12,18 @@
 
 namespace qw {
 
-constexpr int ROUTER_STEPS = 16; // 32-element steps whose loads are in flight together
 
 // logits[t][e] = vec_dot_f32(H, W[e], x[t]).  A group of 32 lanes owns one
 // expert: lane c is the fma chain c of the AVX reduction (elements i == c mod
 // 32, in order), for ROUTER_TT tokens at once; a workgroup holds EPW experts.
-// The loads of ROUTER_STEPS steps are issued together and the next batch is in
-// flight while the current one is accumulated, so a chain waits for memory once
-// per batch, not once per step.  Small batches take one token per group and two
-// experts per workgroup, for more workgroups.
+// The loads of ROUTER_STEPS 32-element steps are issued together and the next
+// batch is in flight while the current one is accumulated, so a chain waits for
+// memory once per batch, not once per step.  Small batches take one token per
+// group, two experts per workgroup (for more workgroups) and 32-step batches.
 // xq (small batches, EPW == 2): workgroups past the router's also quantize x to
 // Q8_K, one wave per 256-value block (the k_quant_q8K quantizer), so the
 // projections' activation costs no launch of its own.
-template <int ROUTER_TT, int EPW>
+template <int ROUTER_TT, int EPW, int ROUTER_STEPS>
 __global__ void __launch_bounds__(32 * EPW) k_router_logits(const float* __restrict__ W, const float* __restrict__ x,
                                                             int64_t x_stride, int64_t H, int64_t E, int64_t T,
                                                             float* __restrict__ logits, BlockQ8_K* __restrict__ xq) {
@@ -124,11 +123,11 @@ int launch_router(const RouterArgs& a, float* logits_ws, hipStream_t stream) {
     if (a.T <= 16) {
         const int64_t nq = a.xq ? a.H / QK_K : 0;
         dim3 g1((unsigned) ((a.E + 1) / 2 + nq), (unsigned) a.T);
-        hipLaunchKernelGGL((k_router_logits<1, 2>), g1, dim3(64), 0, stream, a.W, a.x, a.x_stride, a.H, a.E, a.T,
+        hipLaunchKernelGGL((k_router_logits<1, 2, 32>), g1, dim3(64), 0, stream, a.W, a.x, a.x_stride, a.H, a.E, a.T,
                            logits, (BlockQ8_K*) a.xq);
     } else {
         dim3 g1((unsigned) ((a.E + 7) / 8), (unsigned) ((a.T + 3) / 4));
-        hipLaunchKernelGGL((k_router_logits<4, 8>), g1, dim3(256), 0, stream, a.W, a.x, a.x_stride, a.H, a.E, a.T,
+        hipLaunchKernelGGL((k_router_logits<4, 8, 16>), g1, dim3(256), 0, stream, a.W, a.x, a.x_stride, a.H, a.E, a.T,
                            logits, (BlockQ8_K*) nullptr);
     }
     if (!a.ids) return hipGetLastError() == hipSuccess ? 0 : -3;   // logits only (top-k fused elsewhere)
