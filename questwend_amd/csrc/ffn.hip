@@ -120,17 +120,49 @@ __global__ void __launch_bounds__(1024) k_weighted_sum_rms(const float* __restri
     const int64_t t = blockIdx.x;
     const float* e0 = ex + t * k * H;
     const float* wt = w + t * k;
-    for (int64_t h = threadIdx.x; h < H; h += 1024) {
-        const float* e = e0 + h;
-        float v;
-        if (T == 1) {
-            v = vec_dot_f32_avx(k, e, H, wt);
-        } else {
-            v = e[0] * wt[0];
-            for (int64_t j = 1; j < k; ++j) v = v + e[j * H] * wt[j];
+    if (T == 1 && k >= 32) {
+        for (int64_t h = threadIdx.x; h < H; h += 1024) {
+            const float v = vec_dot_f32_avx(k, e0 + h, H, wt);
+            out[t * H + h] = v;
+            ys[h] = v;
         }
-        out[t * H + h] = v;
-        ys[h] = v;
+    } else {
+        // four outputs per thread, eight experts' values loaded together; each
+        // output's sequence is the one above: T == 1 -> vec_dot_f32's scalar tail
+        // (groups of four as mul + add, the rest fused), T > 1 -> mul, then adds
+        const int64_t nv = k & ~(int64_t) 3;
+        for (int64_t h0 = threadIdx.x; h0 < H; h0 += 4 * 1024) {
+            float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (int64_t j0 = 0; j0 < k; j0 += 8) {
+                float ev[8][4];
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj)
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const int64_t h = h0 + 1024 * u, j = j0 + jj;
+                        ev[jj][u] = e0[(j < k ? j : k - 1) * H + (h < H ? h : H - 1)];
+                    }
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) {
+                    const int64_t j = j0 + jj;
+                    if (j >= k) break;
+                    const float wj = wt[j];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        if (T == 1) acc[u] = (j < nv) ? acc[u] + ev[jj][u] * wj : __builtin_fmaf(ev[jj][u], wj, acc[u]);
+                        else acc[u] = j == 0 ? ev[jj][u] * wj : acc[u] + ev[jj][u] * wj;
+                    }
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int64_t h = h0 + 1024 * u;
+                if (h < H) {
+                    out[t * H + h] = acc[u];
+                    ys[h] = acc[u];
+                }
+            }
+        }
     }
     __syncthreads();
     if (threadIdx.x < 256) {
