@@ -482,8 +482,342 @@ __global__ void __launch_bounds__(256) k_mmid_gemv(MmidPair pr) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Block-parallel GEMV for bins of a few rows (decode, verify batches).  Lane =
+// (row, super-block): each lane forms every integer of its block for all eight
+// AVX lanes at once (the sums that dominate the work, independent per block),
+// then lanes (row, chain) run the float fma chains over the blocks in order
+// from those integers, and one lane per row forms the horizontal-sum tree.
+// Integers, chain order and tree are those of row_dot_lds.  Each wave stages
+// its own rows (16-byte loads over the rows' contiguous bytes) and needs no
+// workgroup barrier after that; the workgroup shares the staged activations.
+
+constexpr int BP_LD = 12;        // staging loads per lane in flight together
+constexpr int BP_MAX_ROWS = 8;   // bins of at most this many rows take this kernel
+
+template <int TYPE>
+struct BpType {
+    static constexpr int NPW = TYPE == T_Q4_K ? 14 : 9;   // words per (row, block): S[8] (P[4]) fd (fm)
+    static constexpr int NCH = TYPE == T_Q4_K ? 12 : 8;   // float chains per row
+};
+
+// Activation blocks staged at 304-byte strides, each starting 12 bytes into its
+// slot, so its quants and bsums lie 16-byte aligned.
+constexpr uint32_t BP_ABLK = 304;
+
+__device__ __forceinline__ u32x4 lds_x4(const uint32_t* lds, uint32_t byte_off) {
+    return *(const u32x4*) (lds + (byte_off >> 2));
+}
+
+__host__ __device__ inline int bp_bpr(int64_t nb) { return nb <= 4 ? 4 : nb <= 8 ? 8 : 16; }
+
+template <int TYPE>
+__host__ __device__ inline uint32_t bp_wave_bytes(int bpr, uint32_t RS) {
+    return (uint32_t) (64 / bpr) * RS + 64u * BpType<TYPE>::NPW * 4u + (uint32_t) (64 / bpr) * BpType<TYPE>::NCH * 4u;
+}
+
+// The integers of one Q4_K block times one Q8_K block for all eight AVX lanes,
+// and the two block scales (row_dot_lds<T_Q4_K>'s sumi, prod, d, dmin).
+// rw(o): the weight block's 32-bit word at byte offset o.
+template <class RW>
+__device__ __forceinline__ void bp_q4k_block(RW rw, const uint32_t* lds, uint32_t yb, uint32_t* part) {
+    const uint32_t h0 = rw(0), s0 = rw(4), s1 = rw(8), s2 = rw(12);
+    const uint8_t q[12] = {(uint8_t) s0, (uint8_t) (s0 >> 8), (uint8_t) (s0 >> 16), (uint8_t) (s0 >> 24),
+                           (uint8_t) s1, (uint8_t) (s1 >> 8), (uint8_t) (s1 >> 16), (uint8_t) (s1 >> 24),
+                           (uint8_t) s2, (uint8_t) (s2 >> 8), (uint8_t) (s2 >> 16), (uint8_t) (s2 >> 24)};
+    int sc[8], mn[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) scale_min_k4(j, q, sc[j], mn[j]);
+    int sumi[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const u32x4 l0 = lds_x4(lds, yb + 4 + 64 * j), l1 = lds_x4(lds, yb + 20 + 64 * j);
+        const u32x4 h0v = lds_x4(lds, yb + 36 + 64 * j), h1v = lds_x4(lds, yb + 52 + 64 * j);
+        const uint32_t alo[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+        const uint32_t ahi[8] = {h0v.x, h0v.y, h0v.z, h0v.w, h1v.x, h1v.y, h1v.z, h1v.w};
+#pragma unroll
+        for (int n = 0; n < 8; ++n) {
+            const uint32_t wq = rw(16 + 32 * j + 4 * n);
+            const int lo = (int) (wq & 0x0F0F0F0Fu), hi = (int) ((wq >> 4) & 0x0F0F0F0Fu);
+            sumi[n] += mul24(sc[2 * j], sdot4(lo, (int) alo[n], 0)) + mul24(sc[2 * j + 1], sdot4(hi, (int) ahi[n], 0));
+        }
+    }
+#pragma unroll
+    for (int n = 0; n < 8; ++n) part[n] = (uint32_t) sumi[n];
+    const u32x4 b0 = lds_x4(lds, yb + 260), b1 = lds_x4(lds, yb + 276);
+    const uint32_t bsw[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+        const uint32_t bs01 = bsw[2 * n], bs23 = bsw[2 * n + 1];
+        const int q8s0 = (int) (int16_t) (bs01 & 0xffff) + (int) (int16_t) (bs01 >> 16);
+        const int q8s1 = (int) (int16_t) (bs23 & 0xffff) + (int) (int16_t) (bs23 >> 16);
+        part[8 + n] = (uint32_t) (mul24(mn[2 * n], q8s0) + mul24(mn[2 * n + 1], q8s1));
+    }
+    const float yd = bitsf(lds_u32a(lds, yb));
+    part[12] = __float_as_uint(yd * h2f((uint16_t) (h0 & 0xffff)));
+    part[13] = __float_as_uint(-yd * h2f((uint16_t) (h0 >> 16)));
+}
+
+// The same for one Q6_K block (row_dot_lds<T_Q6_K>'s sumi and d); d16: the
+// block's f16 scale.
+template <class RW>
+__device__ __forceinline__ void bp_q6k_block(RW rw, uint16_t d16, const uint32_t* lds, uint32_t yb, uint32_t* part) {
+    int sc[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t s = rw(192 + 4 * i);
+        sc[4 * i + 0] = (int) (int8_t) (s & 0xff);
+        sc[4 * i + 1] = (int) (int8_t) ((s >> 8) & 0xff);
+        sc[4 * i + 2] = (int) (int8_t) ((s >> 16) & 0xff);
+        sc[4 * i + 3] = (int) (int8_t) (s >> 24);
+    }
+    const u32x4 b0 = lds_x4(lds, yb + 260), b1 = lds_x4(lds, yb + 276);
+    const uint32_t bsw[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+        const int g = n >= 4 ? 1 : 0;
+        int sumi = 0;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t qa = rw(64 * j + 4 * n);
+            const uint32_t qb = rw(64 * j + 32 + 4 * n);
+            const uint32_t qh = rw(128 + 32 * j + 4 * n);
+            const int q0 = (int) ((qa & 0x0F0F0F0Fu) | ((qh & 0x03030303u) << 4));
+            const int q1 = (int) ((qb & 0x0F0F0F0Fu) | ((qh & 0x0C0C0C0Cu) << 2));
+            const int q2 = (int) (((qa >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u));
+            const int q3 = (int) (((qb >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u));
+            const uint32_t y = yb + 4 + 128 * j + 4 * n;
+            sumi += mul24(sc[8 * j + 0 + g], sdot4(q0, (int) lds_u32a(lds, y), 0));
+            sumi += mul24(sc[8 * j + 2 + g], sdot4(q1, (int) lds_u32a(lds, y + 32), 0));
+            sumi += mul24(sc[8 * j + 4 + g], sdot4(q2, (int) lds_u32a(lds, y + 64), 0));
+            sumi += mul24(sc[8 * j + 6 + g], sdot4(q3, (int) lds_u32a(lds, y + 96), 0));
+        }
+        const uint32_t bs = bsw[n];
+        sumi -= 32 * (mul24((int) (int16_t) (bs & 0xffff), sc[2 * n]) + mul24((int) (int16_t) (bs >> 16), sc[2 * n + 1]));
+        part[n] = (uint32_t) sumi;
+    }
+    part[8] = __float_as_uint(bitsf(lds_u32a(lds, yb)) * h2f(d16));
+}
+
+// DIRECT: every lane loads its own block into registers (rows 16-byte aligned
+// for Q4_K, 4-byte aligned for Q6_K), no weight staging in LDS.
+template <int TYPE, int BPR, bool DIRECT>
+__global__ void __launch_bounds__(256) k_mmid_gemv_bp(MmidPair pr) {
+    constexpr int RPW = 64 / BPR;                 // rows per wave
+    constexpr int NPW = BpType<TYPE>::NPW, NCH = BpType<TYPE>::NCH;
+    const MmidArgs m = pr.m[blockIdx.z];
+    extern __shared__ uint32_t lds[];
+    __shared__ int s_chunk[MMID_CT][3];
+    const int g = blockIdx.y;
+    const int64_t r0 = (int64_t) blockIdx.x * (4 * RPW);
+    if (r0 >= m.N) return;
+    // the bin's count, offsets and id in one round (g < max_active keeps every
+    // address inside the grouping's arrays; the values count only when g < n_active)
+    const int n_act = *m.n_active;
+    const int p0 = m.active_off[g], p1 = m.active_off[g + 1];
+    const int bin = m.active[g];
+    if (g >= n_act) return;
+    if (m.mfma_min_rows > 0 && p1 - p0 >= m.mfma_min_rows) return;
+    const int CT = mmid_stage_rows(m.max_rows);
+    // the slot and the first chunk's pairs in the next round
+    int64_t mat = bin;
+    if (m.slot_of) mat = (bin < m.n_slot_of) ? m.slot_of[bin] : -1;
+    int pe = 0, pt = 0;
+    if ((int) threadIdx.x < min(p1 - p0, CT)) {
+        pe = m.rows[2 * (p0 + threadIdx.x)];
+        pt = m.rows[2 * (p0 + threadIdx.x) + 1];
+    }
+    if (mat < 0 || mat >= m.n_as) {
+        if (threadIdx.x == 0 && m.status) atomicOr(m.status, 4);
+        return;
+    }
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nb = (int) (m.K / QK_K);
+    const size_t row_bytes = (size_t) nb * block_bytes(TYPE);
+    const uint32_t RS = mmid_slot_bytes(row_bytes);
+    const uint32_t ARS = (uint32_t) nb * BP_ABLK;   // one staged activation row
+    const uint32_t WB = (uint32_t) CT * ARS;                         // this wave's region
+    const uint32_t WBASE = WB + (uint32_t) wave * bp_wave_bytes<TYPE>(BPR, DIRECT ? 0u : RS);
+    const uint32_t PBASE = WBASE + (DIRECT ? 0u : (uint32_t) RPW * RS);   // partials [64][NPW]
+    const uint32_t CBASE = PBASE + 64u * NPW * 4u;                  // chain values [RPW][NCH]
+    const int64_t wr0 = r0 + (int64_t) wave * RPW;
+    const int wrows = (int) (m.N - wr0 < 0 ? 0 : m.N - wr0 < RPW ? m.N - wr0 : RPW);
+    const uint8_t* wmat = m.w + (size_t) mat * m.nb2;
+    const int rl = lane / BPR, b = lane % BPR;
+    const bool bvalid = rl < wrows && b < nb;
+    const int rrow = rl < wrows ? rl : 0;
+    // DIRECT: the lane's block (Q4_K 36 words from a 16-byte aligned address;
+    // Q6_K the 53 aligned words holding its 210 bytes, sh = its byte offset in
+    // the first, 0 or 2)
+    constexpr int NWD = DIRECT ? (TYPE == T_Q4_K ? 36 : 53) : 1;
+    uint32_t wd[NWD];
+    uint32_t sh = 0;
+    if constexpr (DIRECT) {
+        const uint8_t* bp = wmat + (size_t) (wr0 + rrow) * m.nb1 + block_bytes(TYPE) * (size_t) (b < nb ? b : 0);
+        if constexpr (TYPE == T_Q4_K) {
+#pragma unroll
+            for (int i = 0; i < 9; ++i) {
+                const u32x4 v = ((const u32x4*) bp)[i];
+                wd[4 * i] = v.x; wd[4 * i + 1] = v.y; wd[4 * i + 2] = v.z; wd[4 * i + 3] = v.w;
+            }
+        } else {
+            sh = (uint32_t) ((uintptr_t) bp & 3);
+            const uint32_t* a = (const uint32_t*) ((uintptr_t) bp & ~(uintptr_t) 3);
+#pragma unroll
+            for (int i = 0; i < 53; ++i) wd[i] = a[i];
+        }
+    }
+    // this wave's rows, each as its 16-byte aligned superset
+    const int nchmax = (int) ((row_bytes + 15) / 16) + 1;
+    for (int base = 0; base < (DIRECT ? 0 : wrows * nchmax); base += BP_LD * 64) {
+        u32x4 v[BP_LD];
+        bool ok[BP_LD];
+#pragma unroll
+        for (int j = 0; j < BP_LD; ++j) {
+            const int idx = base + lane + j * 64;
+            const int r = idx / nchmax, c = idx % nchmax;
+            const uint8_t* src = wmat + (size_t) (wr0 + (r < wrows ? r : 0)) * m.nb1;
+            const uintptr_t s0 = (uintptr_t) src & ~(uintptr_t) 15;
+            const uintptr_t s1 = ((uintptr_t) src + row_bytes + 15) & ~(uintptr_t) 15;
+            ok[j] = idx < wrows * nchmax && c < (int) ((s1 - s0) / 16);
+            v[j] = ((const u32x4*) s0)[ok[j] ? c : 0];
+        }
+#pragma unroll
+        for (int j = 0; j < BP_LD; ++j) {
+            const int idx = base + lane + j * 64;
+            if (ok[j]) ((u32x4*) (lds + (WBASE + (uint32_t) (idx / nchmax) * RS) / 4))[idx % nchmax] = v[j];
+        }
+    }
+    const uint32_t blk = WBASE + (uint32_t) rrow * RS +
+                         (uint32_t) ((uintptr_t) (wmat + (size_t) (wr0 + rrow) * m.nb1) & 15) +
+                         (uint32_t) block_bytes(TYPE) * (uint32_t) b;
+    const bool w_al = (((uintptr_t) wmat | (uintptr_t) m.nb1) & 3) == 0;
+    const int nw = (int) ((m.act_row_bytes + 3) / 4);
+    for (int pc = p0; pc < p1; pc += CT) {
+        const int cnt = (p1 - pc) < CT ? (p1 - pc) : CT;
+        __syncthreads();   // previous chunk consumed
+        if (threadIdx.x < cnt) {
+            const int e = pc == p0 ? pe : m.rows[2 * (pc + threadIdx.x)];
+            const int t = pc == p0 ? pt : m.rows[2 * (pc + threadIdx.x) + 1];
+            s_chunk[threadIdx.x][0] = e;
+            s_chunk[threadIdx.x][1] = t;
+            s_chunk[threadIdx.x][2] = (int) ((int64_t) (e % m.b_ne1) + (int64_t) t * m.b_ne1);
+        }
+        __syncthreads();
+        for (int base = 0; base < cnt * nw; base += MMID_LD * 256) {
+            uint32_t v[MMID_LD];
+#pragma unroll
+            for (int j = 0; j < MMID_LD; ++j) {
+                const int idx = min(base + (int) threadIdx.x + j * 256, cnt * nw - 1);
+                const int tk = idx / nw, c = idx - tk * nw;
+                v[j] = ((const uint32_t*) (m.act_q + (size_t) s_chunk[tk][2] * m.act_row_bytes))[c];
+            }
+#pragma unroll
+            for (int j = 0; j < MMID_LD; ++j) {
+                const int idx = base + (int) threadIdx.x + j * 256;
+                if (idx < cnt * nw) {
+                    const int tk = idx / nw, c = idx - tk * nw;
+                    lds[(tk * ARS) / 4 + (uint32_t) (c / 73) * (BP_ABLK / 4) + 3 + (uint32_t) (c % 73)] = v[j];
+                }
+            }
+        }
+        __syncthreads();   // activations (and, on the first pass, every wave's rows) staged
+        for (int tk = 0; tk < cnt; ++tk) {
+            const uint32_t yb = (uint32_t) tk * ARS + BP_ABLK * (uint32_t) b + 12u;
+            if (bvalid) {
+                uint32_t part[NPW];
+                if constexpr (DIRECT && TYPE == T_Q4_K) {
+                    bp_q4k_block([&](uint32_t o) { return wd[o / 4]; }, lds, yb, part);
+                } else if constexpr (DIRECT) {
+                    const uint16_t d16 = (uint16_t) (sh ? wd[52] >> 16 : wd[52] & 0xffff);
+                    bp_q6k_block([&](uint32_t o) { return __builtin_amdgcn_alignbyte(wd[o / 4 + 1], wd[o / 4], sh); },
+                                 d16, lds, yb, part);
+                } else if constexpr (TYPE == T_Q4_K) {
+                    if (w_al) bp_q4k_block([&](uint32_t o) { return lds_u32a(lds, blk + o); }, lds, yb, part);
+                    else bp_q4k_block([&](uint32_t o) { return lds_u32(lds, blk + o); }, lds, yb, part);
+                } else {
+                    bp_q6k_block([&](uint32_t o) { return lds_u32(lds, blk + o); }, lds_u16(lds, blk + 208), lds, yb,
+                                 part);
+                }
+#pragma unroll
+                for (int i = 0; i < NPW; ++i) lds[PBASE / 4 + (uint32_t) lane * NPW + i] = part[i];
+            }
+            wave_sync();
+            // chain (row, c): c < 8 -> AVX lane c of acc over the blocks in order;
+            // Q4_K c >= 8 -> lane c - 8 of the mins' accm
+            for (int q = lane; q < wrows * NCH; q += 64) {
+                const int r = q / NCH, c = q - r * NCH;
+                const int sw = c < 8 ? NPW - (TYPE == T_Q4_K ? 2 : 1) : NPW - 1;
+                float acc = 0.0f;
+#pragma unroll
+                for (int bb = 0; bb < BPR; ++bb) {
+                    if (bb >= nb) break;
+                    const uint32_t pw = PBASE / 4 + (uint32_t) (r * BPR + bb) * NPW;
+                    acc = __builtin_fmaf(bitsf(lds[pw + sw]), (float) (int) lds[pw + c], acc);
+                }
+                lds[CBASE / 4 + (uint32_t) q] = __float_as_uint(acc);
+            }
+            wave_sync();
+            if (lane < wrows) {
+                const uint32_t* A = lds + CBASE / 4 + (uint32_t) lane * NCH;
+                auto f = [&](int i) { return bitsf(A[i]); };
+                float v = ((f(0) + f(4)) + (f(2) + f(6))) + ((f(1) + f(5)) + (f(3) + f(7)));
+                if constexpr (TYPE == T_Q4_K) v = v + ((f(8) + f(10)) + (f(9) + f(11)));
+                const int e = s_chunk[tk][0], t = s_chunk[tk][1];
+                float* d = (float*) ((char*) m.dst + (size_t) e * m.dst_nb1 + (size_t) t * m.dst_nb2);
+                d[wr0 + lane] = v;
+            }
+        }
+    }
+}
+
+// Rows every lane can load directly: Q4_K 16-byte aligned, Q6_K 4-byte aligned.
+static bool gemv_bp_direct(const MmidArgs& m) {
+    const uintptr_t a = (uintptr_t) m.w | (uintptr_t) m.nb1 | (uintptr_t) m.nb2;
+    return (a & (m.type == T_Q4_K ? 15 : 3)) == 0;
+}
+
+// The block-parallel kernel's LDS bytes, or 0 when it does not apply.
+static size_t gemv_bp_lds(const MmidArgs& m) {
+    if ((m.type != T_Q4_K && m.type != T_Q6_K) || m.max_rows > BP_MAX_ROWS || m.K % QK_K != 0) return 0;
+    const int64_t nb = m.K / QK_K;
+    if (nb < 1 || nb > 16 || m.act_row_bytes != (size_t) nb * 292) return 0;
+    const size_t row_bytes = (size_t) nb * block_bytes(m.type);
+    const uint32_t RS = mmid_slot_bytes(row_bytes);
+    const int bpr = bp_bpr(nb);
+    const uint32_t rs = gemv_bp_direct(m) ? 0u : RS;
+    const uint32_t wb = m.type == T_Q4_K ? bp_wave_bytes<T_Q4_K>(bpr, rs) : bp_wave_bytes<T_Q6_K>(bpr, rs);
+    const size_t lds = (size_t) mmid_stage_rows(m.max_rows) * (size_t) nb * BP_ABLK + 4 * (size_t) wb;
+    return lds <= 160 * 1024 ? lds : 0;
+}
+
+static int launch_gemv_bp(const MmidPair& pr, int nz, size_t lds_bytes, hipStream_t stream) {
+    const MmidArgs& m = pr.m[0];
+    const int bpr = bp_bpr(m.K / QK_K);
+    dim3 grid((unsigned) ((m.N + 4 * (64 / bpr) - 1) / (4 * (64 / bpr))), (unsigned) m.max_active, (unsigned) nz);
+    if (grid.y == 0) return 0;
+    const bool direct = gemv_bp_direct(m);
+#define QW_BP(T, B)                                                                                     \
+    do {                                                                                                \
+        if (direct) hipLaunchKernelGGL((k_mmid_gemv_bp<T, B, true>), grid, dim3(256), lds_bytes, stream, pr);  \
+        else hipLaunchKernelGGL((k_mmid_gemv_bp<T, B, false>), grid, dim3(256), lds_bytes, stream, pr);        \
+    } while (0)
+    if (m.type == T_Q4_K) {
+        if (bpr == 4) QW_BP(T_Q4_K, 4);
+        else if (bpr == 8) QW_BP(T_Q4_K, 8);
+        else QW_BP(T_Q4_K, 16);
+    } else {
+        if (bpr == 4) QW_BP(T_Q6_K, 4);
+        else if (bpr == 8) QW_BP(T_Q6_K, 8);
+        else QW_BP(T_Q6_K, 16);
+    }
+#undef QW_BP
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
 static int launch_gemv(const MmidPair& pr, int nz, hipStream_t stream) {
     const MmidArgs& m = pr.m[0];
+    if (const size_t bp = gemv_bp_lds(m)) return launch_gemv_bp(pr, nz, bp, stream);
     const size_t row_bytes = (size_t) (m.K / block_elems(m.type)) * block_bytes(m.type);
     size_t lds_bytes = (size_t) mmid_slot_bytes(row_bytes) * MMID_ROWS +
                        (size_t) mmid_stage_rows(m.max_rows) * (((m.act_row_bytes + 3) / 4) * 4 + 16);

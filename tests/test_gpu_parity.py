@@ -159,6 +159,27 @@ def test_mul_mat_id_ragged_rows(orc):
     assert np.array_equal(bits(got), bits(orc.mul_mat_id(t, K, N, n_as, w, b, ids)))
 
 
+@pytest.mark.parametrize("t,K", [(Q4_K, 4096), (Q4_K, 768), (Q6_K, 1536), (Q6_K, 512)])
+@pytest.mark.parametrize("off", [0, 2, 5])
+def test_mul_mat_id_small_bins_unaligned_ragged(orc, t, K, off):
+    """Bins of at most eight rows (decode and verify batches) with N not a
+    multiple of any row tile and the weights starting off bytes past an aligned
+    address (rows then misaligned for word reads)."""
+    note(f"mul_mat_id small bins type={t} K={K} N=70 weight offset {off}")
+    rng = np.random.default_rng(K + off)
+    N, n_as = 70, 9
+    w = orc.quantize(t, (rng.standard_normal((n_as * N, K)) * 0.02).astype(np.float32))
+    buf = np.zeros(w.size + 16, np.uint8)
+    buf[off:off + w.size] = w
+    wd = dev(buf)[off:off + w.size]
+    for T, n_ids in ((1, 8), (3, 4), (8, 2)):
+        b = rng.standard_normal((T, 1, K)).astype(np.float32)
+        ids = np.stack([rng.choice(n_as, n_ids, replace=False) for _ in range(T)]).astype(np.int32)
+        got = host(ops.mul_mat_id(t, wd, K, N, n_as, dev(b), dev(ids)))
+        assert np.array_equal(bits(got), bits(orc.mul_mat_id(t, K, N, n_as, w, b, ids))), f"T={T}"
+    assert_status_clean()
+
+
 def test_mul_mat_id_bad_id_sets_status(orc):
     note("mul_mat_id with an out-of-range id (host-forced error path)")
     rng = np.random.default_rng(4)
@@ -200,7 +221,7 @@ def test_group_by_expert(orc, T, k, n_as, dup):
 # ---------------------------------------------------------------- router
 
 @pytest.mark.parametrize("H,E,k,T", [(2048, 128, 8, 1), (2048, 128, 8, 5), (4096, 128, 8, 3), (2048, 128, 8, 64),
-                                     (512, 16, 4, 9), (2052, 64, 6, 2)])
+                                     (512, 16, 4, 9), (2052, 64, 6, 2), (8192, 64, 4, 2)])
 def test_router_bit_exact(orc, H, E, k, T):
     note(f"router H={H} E={E} k={k} T={T}")
     rng = np.random.default_rng(H + E + T)
