@@ -439,18 +439,24 @@ int qwmoe_ffn_layer(void* stream, const qwmoe_layer* L, const float* x, int64_t 
     const size_t qd = qwmoe_row_size(vd, F);
     uint8_t* aq = ar.take<uint8_t>(qd * (size_t) (k * T) + 64);
     if (!aq) return QWMOE_ERR_WORKSPACE;
-    if (vd == qw::T_Q8_K) {   // SwiGLU straight into Q8_K
+    qw::MmidArgs md = mmid_args(L->type_down, L->down, F, H, L->n_slots_down, L->down_nb1, L->down_nb2, aq, k, qd,
+                                G.rows, G.active, G.active_off, G.n_active, G.max_active, L->slot_down,
+                                L->slot_down ? E : 0, ex, (size_t) H * 4, (size_t) H * 4 * (size_t) k, T);
+    md.swiglu_gate = gateo;
+    md.swiglu_up = upo;
+    if (vd == qw::T_Q8_K && qw::mmid_gemv_swiglu_ok(md)) {
+        // small bins: the down GEMV forms SwiGLU's Q8_K rows itself
+    } else if (vd == qw::T_Q8_K) {   // SwiGLU straight into Q8_K
+        md.swiglu_gate = md.swiglu_up = nullptr;
         if ((rc = qw::launch_swiglu_q8K(gateo, upo, F, k * T, aq, st))) return rc;
     } else {
+        md.swiglu_gate = md.swiglu_up = nullptr;
         if ((rc = qw::launch_swiglu(gateo, upo, act, k * T, F, (size_t) F * 4, (size_t) F * 4, (size_t) F * 4, st)))
             return rc;
         if ((rc = qw::launch_quantize_act(vd, act, F, k, k * T, (size_t) F * 4, (size_t) F * 4 * (size_t) k, aq, st)))
             return rc;
     }
-    if ((rc = mmid_grouped(st, L->type_down, L->down, F, H, L->n_slots_down, L->down_nb1, L->down_nb2, aq, k, qd,
-                           G.rows, G.active, G.active_off, G.n_active, G.max_active, L->slot_down,
-                           L->slot_down ? E : 0, ex, (size_t) H * 4, (size_t) H * 4 * (size_t) k, T)))
-        return rc;
+    if ((rc = mmid_launch(md, st))) return rc;
     if (rms_eps >= 0.0f && H <= 16384) {
         if ((rc = qw::launch_weighted_sum_rms(ex, w, out, x_next, H, k, T, rms_eps, st))) return rc;
     } else {

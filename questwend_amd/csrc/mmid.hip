@@ -704,20 +704,32 @@ __global__ void __launch_bounds__(256) k_mmid_gemv_bp(MmidPair pr) {
             s_chunk[threadIdx.x][2] = (int) ((int64_t) (e % m.b_ne1) + (int64_t) t * m.b_ne1);
         }
         __syncthreads();
-        for (int base = 0; base < cnt * nw; base += MMID_LD * 256) {
-            uint32_t v[MMID_LD];
-#pragma unroll
-            for (int j = 0; j < MMID_LD; ++j) {
-                const int idx = min(base + (int) threadIdx.x + j * 256, cnt * nw - 1);
-                const int tk = idx / nw, c = idx - tk * nw;
-                v[j] = ((const uint32_t*) (m.act_q + (size_t) s_chunk[tk][2] * m.act_row_bytes))[c];
+        if (m.swiglu_gate) {
+            // SwiGLU straight into Q8_K, one block per wave (k_swiglu_q8K's values and quantizer)
+            for (int q = wave; q < cnt * nb; q += 4) {
+                const int tk = q / nb, ib = q - tk * nb;
+                const size_t off = (size_t) s_chunk[tk][2] * (size_t) m.K + (size_t) ib * QK_K + 4 * (size_t) lane;
+                const float4 gv = *(const float4*) (m.swiglu_gate + off);
+                const float4 uv = *(const float4*) (m.swiglu_up + off);
+                const float v[4] = {v_silu(gv.x) * uv.x, v_silu(gv.y) * uv.y, v_silu(gv.z) * uv.z, v_silu(gv.w) * uv.w};
+                quant_q8K_wave(v, lane, (BlockQ8_K*) ((char*) lds + (uint32_t) tk * ARS + BP_ABLK * (uint32_t) ib + 12u));
             }
+        } else {
+            for (int base = 0; base < cnt * nw; base += MMID_LD * 256) {
+                uint32_t v[MMID_LD];
 #pragma unroll
-            for (int j = 0; j < MMID_LD; ++j) {
-                const int idx = base + (int) threadIdx.x + j * 256;
-                if (idx < cnt * nw) {
+                for (int j = 0; j < MMID_LD; ++j) {
+                    const int idx = min(base + (int) threadIdx.x + j * 256, cnt * nw - 1);
                     const int tk = idx / nw, c = idx - tk * nw;
-                    lds[(tk * ARS) / 4 + (uint32_t) (c / 73) * (BP_ABLK / 4) + 3 + (uint32_t) (c % 73)] = v[j];
+                    v[j] = ((const uint32_t*) (m.act_q + (size_t) s_chunk[tk][2] * m.act_row_bytes))[c];
+                }
+#pragma unroll
+                for (int j = 0; j < MMID_LD; ++j) {
+                    const int idx = base + (int) threadIdx.x + j * 256;
+                    if (idx < cnt * nw) {
+                        const int tk = idx / nw, c = idx - tk * nw;
+                        lds[(tk * ARS) / 4 + (uint32_t) (c / 73) * (BP_ABLK / 4) + 3 + (uint32_t) (c % 73)] = v[j];
+                    }
                 }
             }
         }
@@ -791,6 +803,11 @@ static size_t gemv_bp_lds(const MmidArgs& m) {
     return lds <= 160 * 1024 ? lds : 0;
 }
 
+bool mmid_gemv_swiglu_ok(const MmidArgs& m) {
+    return m.mfma_min_rows == 0 && gemv_bp_lds(m) != 0 &&
+           (((uintptr_t) m.swiglu_gate | (uintptr_t) m.swiglu_up | (uintptr_t) (m.K * 4)) & 15) == 0;
+}
+
 static int launch_gemv_bp(const MmidPair& pr, int nz, size_t lds_bytes, hipStream_t stream) {
     const MmidArgs& m = pr.m[0];
     const int bpr = bp_bpr(m.K / QK_K);
@@ -817,6 +834,9 @@ static int launch_gemv_bp(const MmidPair& pr, int nz, size_t lds_bytes, hipStrea
 
 static int launch_gemv(const MmidPair& pr, int nz, hipStream_t stream) {
     const MmidArgs& m = pr.m[0];
+    if (m.swiglu_gate || pr.m[nz - 1].swiglu_gate) {
+        if (!mmid_gemv_swiglu_ok(m) || (nz == 2 && !mmid_gemv_swiglu_ok(pr.m[1]))) return -2;
+    }
     if (const size_t bp = gemv_bp_lds(m)) return launch_gemv_bp(pr, nz, bp, stream);
     const size_t row_bytes = (size_t) (m.K / block_elems(m.type)) * block_bytes(m.type);
     size_t lds_bytes = (size_t) mmid_slot_bytes(row_bytes) * MMID_ROWS +

@@ -73,8 +73,16 @@ struct MmidArgs {
     int64_t max_active;       // grid bound on active bins
     int mfma_min_rows;        // bins with at least this many rows go to the matrix-core kernel (0: none do)
     int64_t max_rows;         // bound on the rows of one bin
+    // optional (Q8_K activations only): activation row r is the Q8_K of
+    // silu(swiglu_gate[r]) * swiglu_up[r] (f32 rows of K values), formed inside
+    // the GEMV instead of read from act_q; see mmid_gemv_swiglu_ok
+    const float* swiglu_gate;
+    const float* swiglu_up;
 };
 int launch_mmid_gemv(const MmidArgs& m, hipStream_t stream);
+// whether launch_mmid_gemv forms the activations itself for these arguments with
+// swiglu_gate / swiglu_up set (small bins on the block-parallel kernel)
+bool mmid_gemv_swiglu_ok(const MmidArgs& m);
 // two GEMVs of the same type, shape and grouping in one launch (mfma_min_rows must be 0 in both)
 int launch_mmid_gemv2(const MmidArgs& a, const MmidArgs& b, hipStream_t stream);
 // mmid_mfma.hip
