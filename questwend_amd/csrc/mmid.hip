@@ -601,7 +601,8 @@ __device__ __forceinline__ void bp_q6k_block(RW rw, uint16_t d16, const uint32_t
 
 // DIRECT: every lane loads its own block into registers (rows 16-byte aligned
 // for Q4_K, 4-byte aligned for Q6_K), no weight staging in LDS.
-template <int TYPE, int BPR, bool DIRECT>
+// SWIGLU: the activation rows are formed from m.swiglu_gate / m.swiglu_up.
+template <int TYPE, int BPR, bool DIRECT, bool SWIGLU>
 __global__ void __launch_bounds__(256) k_mmid_gemv_bp(MmidPair pr) {
     constexpr int RPW = 64 / BPR;                 // rows per wave
     constexpr int NPW = BpType<TYPE>::NPW, NCH = BpType<TYPE>::NCH;
@@ -704,7 +705,7 @@ __global__ void __launch_bounds__(256) k_mmid_gemv_bp(MmidPair pr) {
             s_chunk[threadIdx.x][2] = (int) ((int64_t) (e % m.b_ne1) + (int64_t) t * m.b_ne1);
         }
         __syncthreads();
-        if (m.swiglu_gate) {
+        if constexpr (SWIGLU) {
             // SwiGLU straight into Q8_K, one block per wave (k_swiglu_q8K's values and quantizer)
             for (int q = wave; q < cnt * nb; q += 4) {
                 const int tk = q / nb, ib = q - tk * nb;
@@ -813,11 +814,16 @@ static int launch_gemv_bp(const MmidPair& pr, int nz, size_t lds_bytes, hipStrea
     const int bpr = bp_bpr(m.K / QK_K);
     dim3 grid((unsigned) ((m.N + 4 * (64 / bpr) - 1) / (4 * (64 / bpr))), (unsigned) m.max_active, (unsigned) nz);
     if (grid.y == 0) return 0;
-    const bool direct = gemv_bp_direct(m);
-#define QW_BP(T, B)                                                                                     \
-    do {                                                                                                \
-        if (direct) hipLaunchKernelGGL((k_mmid_gemv_bp<T, B, true>), grid, dim3(256), lds_bytes, stream, pr);  \
-        else hipLaunchKernelGGL((k_mmid_gemv_bp<T, B, false>), grid, dim3(256), lds_bytes, stream, pr);        \
+    const bool direct = gemv_bp_direct(m), sw = m.swiglu_gate != nullptr;
+#define QW_BP2(T, B, D)                                                                                   \
+    do {                                                                                                  \
+        if (sw) hipLaunchKernelGGL((k_mmid_gemv_bp<T, B, D, true>), grid, dim3(256), lds_bytes, stream, pr);   \
+        else hipLaunchKernelGGL((k_mmid_gemv_bp<T, B, D, false>), grid, dim3(256), lds_bytes, stream, pr);     \
+    } while (0)
+#define QW_BP(T, B)                  \
+    do {                             \
+        if (direct) QW_BP2(T, B, true);  \
+        else QW_BP2(T, B, false);        \
     } while (0)
     if (m.type == T_Q4_K) {
         if (bpr == 4) QW_BP(T_Q4_K, 4);
@@ -829,6 +835,7 @@ static int launch_gemv_bp(const MmidPair& pr, int nz, size_t lds_bytes, hipStrea
         else QW_BP(T_Q6_K, 16);
     }
 #undef QW_BP
+#undef QW_BP2
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
