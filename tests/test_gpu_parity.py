@@ -160,7 +160,7 @@ def test_mul_mat_id_ragged_rows(orc):
 
 
 @pytest.mark.parametrize("t,K", [(Q4_K, 4096), (Q4_K, 768), (Q6_K, 1536), (Q6_K, 512)])
-@pytest.mark.parametrize("off", [0, 2, 5])
+@pytest.mark.parametrize("off", [0, 2, 4, 5])
 def test_mul_mat_id_small_bins_unaligned_ragged(orc, t, K, off):
     """Bins of at most eight rows (decode and verify batches) with N not a
     multiple of any row tile and the weights starting off bytes past an aligned
