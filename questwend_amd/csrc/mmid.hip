@@ -488,9 +488,13 @@ __global__ void __launch_bounds__(256) k_mmid_gemv(MmidPair pr) {
 // AVX lanes at once (the sums that dominate the work, independent per block),
 // then lanes (row, chain) run the float fma chains over the blocks in order
 // from those integers, and one lane per row forms the horizontal-sum tree.
-// Integers, chain order and tree are those of row_dot_lds.  Each wave stages
-// its own rows (16-byte loads over the rows' contiguous bytes) and needs no
-// workgroup barrier after that; the workgroup shares the staged activations.
+// Integers, chain order and tree are those of row_dot_lds.  With aligned rows
+// each lane loads its own block straight into registers; otherwise each wave
+// stages its own rows in LDS (16-byte loads over the rows' bytes).  Either way a
+// wave needs no workgroup barrier for its weights; the workgroup shares the
+// staged activations.  (Measured at K = 4096: staging the Q4_K rows in LDS
+// costs 27.6 us per gate/up launch against 19.6 us for the register loads, the
+// larger LDS footprint halving the workgroups per CU.)
 
 constexpr int BP_LD = 12;        // staging loads per lane in flight together
 constexpr int BP_MAX_ROWS = 8;   // bins of at most this many rows take this kernel
