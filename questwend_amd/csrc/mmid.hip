@@ -283,13 +283,23 @@ __global__ void __launch_bounds__(GROUP_WAVES * 64) k_topk_group(RouterArgs ra, 
     float* gsum = (float*) (order + E);
     int* need_sort = (int*) (gsum + E / 8);
     SortRange* stack = (SortRange*) (need_sort + 1);
+    // up to 64 pairs: the ids go to LDS, the one-wave grouping reads them there
+    // while the next wave copies them out to the caller's buffer
+    __shared__ int32_t s_ids[64];
+    const bool small = ra.T * ra.k <= 64;
     if (w < ra.T)
-        topk_token<true>(logits, ra.E, ra.k, w, ra.clamp_min, ra.scale, ra.ids, ra.weights, ra.probs, ra.status, p, gsum,
-                         order, stack, need_sort, lane);
+        topk_token<true>(logits, ra.E, ra.k, w, ra.clamp_min, ra.scale, small ? s_ids : ra.ids, ra.weights, ra.probs,
+                         ra.status, p, gsum, order, stack, need_sort, lane);
     __syncthreads();   // every token's ids are written
     int32_t* hist = (int32_t*) ((uint8_t*) dyn + (size_t) GROUP_WAVES * ((per_wave + 15u) & ~15u));
-    if (ra.T * ra.k <= 64) {
-        if (w == 0) group_wave(g, hist);
+    if (small) {
+        if (w == 0) {
+            GroupArgs gl = g;
+            gl.ids = s_ids;
+            group_wave(gl, hist);
+        } else if (w == 1 && lane < ra.T * ra.k) {
+            ra.ids[lane] = s_ids[lane];
+        }
     } else {
         group_body<true>(g, hist, s_wsum);
     }
