@@ -493,7 +493,7 @@ __global__ void __launch_bounds__(256) k_mmid_gemv(MmidPair pr) {
 }
 
 // ---------------------------------------------------------------------------
-// Block-parallel GEMV for bins of a few rows (decode, verify batches).  Lane =
+// Block-parallel GEMV (Q4_K / Q6_K rows of at most 16 super-blocks).  Lane =
 // (row, super-block): each lane forms every integer of its block for all eight
 // AVX lanes at once (the sums that dominate the work, independent per block),
 // then lanes (row, chain) run the float fma chains over the blocks in order
@@ -507,7 +507,7 @@ __global__ void __launch_bounds__(256) k_mmid_gemv(MmidPair pr) {
 // larger LDS footprint halving the workgroups per CU.)
 
 constexpr int BP_LD = 12;        // staging loads per lane in flight together
-constexpr int BP_MAX_ROWS = 8;   // bins of at most this many rows take this kernel
+constexpr int BP_SWIGLU_MAX_ROWS = 8;   // bins of at most this many rows form SwiGLU's rows in the kernel
 
 template <int TYPE>
 struct BpType {
@@ -806,7 +806,7 @@ static bool gemv_bp_direct(const MmidArgs& m) {
 
 // The block-parallel kernel's LDS bytes, or 0 when it does not apply.
 static size_t gemv_bp_lds(const MmidArgs& m) {
-    if ((m.type != T_Q4_K && m.type != T_Q6_K) || m.max_rows > BP_MAX_ROWS || m.K % QK_K != 0) return 0;
+    if ((m.type != T_Q4_K && m.type != T_Q6_K) || m.K % QK_K != 0) return 0;
     const int64_t nb = m.K / QK_K;
     if (nb < 1 || nb > 16 || m.act_row_bytes != (size_t) nb * 292) return 0;
     const size_t row_bytes = (size_t) nb * block_bytes(m.type);
@@ -819,7 +819,8 @@ static size_t gemv_bp_lds(const MmidArgs& m) {
 }
 
 bool mmid_gemv_swiglu_ok(const MmidArgs& m) {
-    return m.mfma_min_rows == 0 && gemv_bp_lds(m) != 0 &&
+    // (larger batches: every row tile of a bin would form the same rows again)
+    return m.mfma_min_rows == 0 && m.max_rows <= BP_SWIGLU_MAX_ROWS && gemv_bp_lds(m) != 0 &&
            (((uintptr_t) m.swiglu_gate | (uintptr_t) m.swiglu_up | (uintptr_t) (m.K * 4)) & 15) == 0;
 }
 
