@@ -573,8 +573,9 @@ __device__ __forceinline__ void bp_q4k_block(RW rw, const uint32_t* lds, uint32_
 }
 
 // The same for one Q6_K block (row_dot_lds<T_Q6_K>'s sumi and d); d16: the
-// block's f16 scale.
-template <class RW>
+// block's f16 scale.  VEC: the activations are read a 32-byte quarter at a time
+// (fewer LDS reads, more registers: the form for bins of many rows).
+template <bool VEC, class RW>
 __device__ __forceinline__ void bp_q6k_block(RW rw, uint16_t d16, const uint32_t* lds, uint32_t yb, uint32_t* part) {
     int sc[16];
 #pragma unroll
@@ -587,35 +588,71 @@ __device__ __forceinline__ void bp_q6k_block(RW rw, uint16_t d16, const uint32_t
     }
     const u32x4 b0 = lds_x4(lds, yb + 260), b1 = lds_x4(lds, yb + 276);
     const uint32_t bsw[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+    if constexpr (!VEC) {
 #pragma unroll
-    for (int n = 0; n < 8; ++n) {
-        const int g = n >= 4 ? 1 : 0;
-        int sumi = 0;
+        for (int n = 0; n < 8; ++n) {
+            const int g = n >= 4 ? 1 : 0;
+            int sumi = 0;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+            for (int j = 0; j < 2; ++j) {
+                const uint32_t qa = rw(64 * j + 4 * n);
+                const uint32_t qb = rw(64 * j + 32 + 4 * n);
+                const uint32_t qh = rw(128 + 32 * j + 4 * n);
+                const int q0 = (int) ((qa & 0x0F0F0F0Fu) | ((qh & 0x03030303u) << 4));
+                const int q1 = (int) ((qb & 0x0F0F0F0Fu) | ((qh & 0x0C0C0C0Cu) << 2));
+                const int q2 = (int) (((qa >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u));
+                const int q3 = (int) (((qb >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u));
+                const uint32_t y = yb + 4 + 128 * j + 4 * n;
+                sumi += mul24(sc[8 * j + 0 + g], sdot4(q0, (int) lds_u32a(lds, y), 0));
+                sumi += mul24(sc[8 * j + 2 + g], sdot4(q1, (int) lds_u32a(lds, y + 32), 0));
+                sumi += mul24(sc[8 * j + 4 + g], sdot4(q2, (int) lds_u32a(lds, y + 64), 0));
+                sumi += mul24(sc[8 * j + 6 + g], sdot4(q3, (int) lds_u32a(lds, y + 96), 0));
+            }
+            const uint32_t bs = bsw[n];
+            part[n] = (uint32_t) (sumi - 32 * (mul24((int) (int16_t) (bs & 0xffff), sc[2 * n]) +
+                                               mul24((int) (int16_t) (bs >> 16), sc[2 * n + 1])));
+        }
+        part[8] = __float_as_uint(bitsf(lds_u32a(lds, yb)) * h2f(d16));
+        return;
+    }
+    int sumi[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        // the 6-bit quants of every lane n for the four 32-value quarters of half j
+        int qv[4][8];
+#pragma unroll
+        for (int n = 0; n < 8; ++n) {
             const uint32_t qa = rw(64 * j + 4 * n);
             const uint32_t qb = rw(64 * j + 32 + 4 * n);
             const uint32_t qh = rw(128 + 32 * j + 4 * n);
-            const int q0 = (int) ((qa & 0x0F0F0F0Fu) | ((qh & 0x03030303u) << 4));
-            const int q1 = (int) ((qb & 0x0F0F0F0Fu) | ((qh & 0x0C0C0C0Cu) << 2));
-            const int q2 = (int) (((qa >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u));
-            const int q3 = (int) (((qb >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u));
-            const uint32_t y = yb + 4 + 128 * j + 4 * n;
-            sumi += mul24(sc[8 * j + 0 + g], sdot4(q0, (int) lds_u32a(lds, y), 0));
-            sumi += mul24(sc[8 * j + 2 + g], sdot4(q1, (int) lds_u32a(lds, y + 32), 0));
-            sumi += mul24(sc[8 * j + 4 + g], sdot4(q2, (int) lds_u32a(lds, y + 64), 0));
-            sumi += mul24(sc[8 * j + 6 + g], sdot4(q3, (int) lds_u32a(lds, y + 96), 0));
+            qv[0][n] = (int) ((qa & 0x0F0F0F0Fu) | ((qh & 0x03030303u) << 4));
+            qv[1][n] = (int) ((qb & 0x0F0F0F0Fu) | ((qh & 0x0C0C0C0Cu) << 2));
+            qv[2][n] = (int) (((qa >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u));
+            qv[3][n] = (int) (((qb >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u));
         }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            // the quarter's 32 activation bytes, lane n's four in word n
+            const u32x4 a0 = lds_x4(lds, yb + 4 + 128 * j + 32 * q), a1 = lds_x4(lds, yb + 20 + 128 * j + 32 * q);
+            const uint32_t a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+            for (int n = 0; n < 8; ++n)
+                sumi[n] += mul24(sc[8 * j + 2 * q + (n >= 4 ? 1 : 0)], sdot4(qv[q][n], (int) a[n], 0));
+        }
+    }
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
         const uint32_t bs = bsw[n];
-        sumi -= 32 * (mul24((int) (int16_t) (bs & 0xffff), sc[2 * n]) + mul24((int) (int16_t) (bs >> 16), sc[2 * n + 1]));
-        part[n] = (uint32_t) sumi;
+        part[n] = (uint32_t) (sumi[n] - 32 * (mul24((int) (int16_t) (bs & 0xffff), sc[2 * n]) +
+                                              mul24((int) (int16_t) (bs >> 16), sc[2 * n + 1])));
     }
     part[8] = __float_as_uint(bitsf(lds_u32a(lds, yb)) * h2f(d16));
 }
 
 // DIRECT: every lane loads its own block into registers (rows 16-byte aligned
 // for Q4_K, 4-byte aligned for Q6_K), no weight staging in LDS.
-// SWIGLU: the activation rows are formed from m.swiglu_gate / m.swiglu_up.
+// SWIGLU: the activation rows are formed from m.swiglu_gate / m.swiglu_up
+// (small bins only; the other kernels take Q6_K's many-row form).
 template <int TYPE, int BPR, bool DIRECT, bool SWIGLU>
 __global__ void __launch_bounds__(256) k_mmid_gemv_bp(MmidPair pr) {
     constexpr int RPW = 64 / BPR;                 // rows per wave
@@ -757,14 +794,15 @@ __global__ void __launch_bounds__(256) k_mmid_gemv_bp(MmidPair pr) {
                     bp_q4k_block([&](uint32_t o) { return wd[o / 4]; }, lds, yb, part);
                 } else if constexpr (DIRECT) {
                     const uint16_t d16 = (uint16_t) (sh ? wd[52] >> 16 : wd[52] & 0xffff);
-                    bp_q6k_block([&](uint32_t o) { return __builtin_amdgcn_alignbyte(wd[o / 4 + 1], wd[o / 4], sh); },
-                                 d16, lds, yb, part);
+                    bp_q6k_block<!SWIGLU>(
+                        [&](uint32_t o) { return __builtin_amdgcn_alignbyte(wd[o / 4 + 1], wd[o / 4], sh); }, d16, lds,
+                        yb, part);
                 } else if constexpr (TYPE == T_Q4_K) {
                     if (w_al) bp_q4k_block([&](uint32_t o) { return lds_u32a(lds, blk + o); }, lds, yb, part);
                     else bp_q4k_block([&](uint32_t o) { return lds_u32(lds, blk + o); }, lds, yb, part);
                 } else {
-                    bp_q6k_block([&](uint32_t o) { return lds_u32(lds, blk + o); }, lds_u16(lds, blk + 208), lds, yb,
-                                 part);
+                    bp_q6k_block<!SWIGLU>([&](uint32_t o) { return lds_u32(lds, blk + o); }, lds_u16(lds, blk + 208),
+                                          lds, yb, part);
                 }
 #pragma unroll
                 for (int i = 0; i < NPW; ++i) lds[PBASE / 4 + (uint32_t) lane * NPW + i] = part[i];
