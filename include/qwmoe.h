@@ -216,6 +216,15 @@ int qwmoe_decode_stack_run(void * stream, qwmoe_decode_stack * s, const float * 
  * (launch abandoned), 16 a slot table entry was out of range. */
 int qwmoe_decode_stack_status(void * stream, qwmoe_decode_stack * s, int32_t * status_out, int clear);
 void qwmoe_decode_stack_free(qwmoe_decode_stack * s);
+/* Which kernel a stack runs (no reference counterpart; the kernel choice only):
+ * 1 = one workgroup per CU over every selected expert; 2 = one selected expert
+ * per XCD (256-CU devices, k <= 8, H = 2048, Q4_K down), exchanges inside an XCD
+ * through its L2; 3 = the same with every exchange word stored at device scope
+ * (used when the workgroup -> XCD mapping checked at creation is not b % 8).
+ * Creation picks 2 or 3 where the shape allows, else 1; QWMOE_DECODE_XCD=0 in
+ * the environment at creation forces 1, QWMOE_DECODE_XCD_LOCAL=0 forces 3 over 2.
+ * Results are identical. */
+int qwmoe_decode_stack_kernel(const qwmoe_decode_stack * s);
 
 /* ---- T-token batches through a layer stack (speculative-decoding verify) ------ */
 

@@ -68,6 +68,7 @@ SIGNATURES = {
     "qwmoe_decode_stack_run": (I, [P, P, P, P, P, P, P]),
     "qwmoe_decode_stack_status": (I, [P, P, P, I]),
     "qwmoe_decode_stack_free": (None, [P]),
+    "qwmoe_decode_stack_kernel": (I, [P]),
     "qwmoe_layer_stack_create": (I, [P, I, F, I, I, P]),
     "qwmoe_layer_stack_run": (I, [P, P, P, I64, P, P, P, P]),
     "qwmoe_layer_stack_free": (None, [P]),

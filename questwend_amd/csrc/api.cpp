@@ -4,6 +4,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdlib>
 #include <cstring>
 #include <atomic>
 #include <mutex>
@@ -507,23 +508,49 @@ int qwmoe_decode_stack_create(const qwmoe_layer* layers, int n_layer, float rms_
     d.type_down = L0.type_down;
     d.scale = L0.expert_weights_scale;
     d.rms_eps = rms_eps;
-    int rc = qw::plan_decode_stack(d, cus);
-    if (rc == 0) rc = qw::check_decode_residency(d);
+    // The kernel with one selected expert per XCD where the shape and device
+    // allow it (QWMOE_DECODE_XCD=0 selects the per-CU kernel everywhere).
+    const char* xe = getenv("QWMOE_DECODE_XCD");
+    const bool allow_xcd = !(xe && xe[0] == '0');
+    int rc = 0;
+    if (allow_xcd && qw::check_decode_xcd(d, cus) == 0) {
+        d.use_xcd = 1;
+        d.grid = cus;
+    } else {
+        rc = qw::plan_decode_stack(d, cus);
+        if (rc == 0) rc = qw::check_decode_residency(d);
+    }
     if (rc) {
         delete s;
         return rc;
     }
-    // one device block: layer table | act | y | logits | status, abort
+    // one device block: layer table | act | y | logits | down outputs | status, abort
+    auto r256 = [](size_t n) { return (n + 255) & ~(size_t) 255; };
+    const size_t nx = d.use_xcd ? 8 : 1;   // XCD kernel: one region per XCD
     const size_t n_layers_b = sizeof(qw::DecodeLayer) * (size_t) n_layer;
-    const size_t off_xa = (n_layers_b + 255) & ~(size_t) 255;
-    const size_t off_xy = off_xa + (((size_t) (d.k * d.F) * 8 + 255) & ~(size_t) 255);
-    const size_t off_xl = off_xy + (((size_t) d.H * 8 + 255) & ~(size_t) 255);
-    const size_t off_st = off_xl + (((size_t) d.E * 8 + 255) & ~(size_t) 255);
+    const size_t off_xa = r256(n_layers_b);
+    const size_t off_xy = off_xa + r256((size_t) (d.use_xcd ? d.F : d.k * d.F) * 8 * nx);
+    const size_t off_xl = off_xy + r256((size_t) d.H * 8 * nx);
+    const size_t off_xd = off_xl + r256((size_t) d.E * 8 * nx);
+    const size_t off_st = off_xd + (d.use_xcd ? r256((size_t) d.H * 8 * 16) : 0);
     const size_t total = off_st + 256;
     void* blk = nullptr;
     if (hipMalloc(&blk, total) != hipSuccess) {
         delete s;
         return QWMOE_ERR_HIP;
+    }
+    if (d.use_xcd) {
+        // XCD-local exchange words may be stored with workgroup scope only when
+        // workgroup b of the launch runs on XCD b % 8 (QWMOE_DECODE_XCD_LOCAL=0:
+        // never); the kernel also flags a workgroup found elsewhere (status 64)
+        const char* le = getenv("QWMOE_DECODE_XCD_LOCAL");
+        int ok = 0;
+        if (qw::probe_xcd_mapping((int32_t*) ((uint8_t*) blk + off_xd), d.grid, nullptr, &ok) != 0) {
+            (void) hipFree(blk);
+            delete s;
+            return QWMOE_ERR_HIP;
+        }
+        d.xcd_local = (ok && !(le && le[0] == '0')) ? 1 : 0;
     }
     std::vector<qw::DecodeLayer> host((size_t) n_layer);
     for (int l = 0; l < n_layer; ++l) {
@@ -559,6 +586,7 @@ int qwmoe_decode_stack_create(const qwmoe_layer* layers, int n_layer, float rms_
     d.xa = (uint64_t*) (base + off_xa);
     d.xy = (uint64_t*) (base + off_xy);
     d.xl = (uint64_t*) (base + off_xl);
+    d.xd = d.use_xcd ? (uint64_t*) (base + off_xd) : nullptr;
     d.status = (int32_t*) (base + off_st);
     d.abort_flag = (int32_t*) (base + off_st + 128);
     d.epoch = 1;
@@ -574,7 +602,13 @@ int qwmoe_decode_stack_run(void* stream, qwmoe_decode_stack* s, const float* x, 
     if (d.epoch > 0x7fffffffu - (uint32_t) d.n_layer) return QWMOE_ERR_UNSUPPORTED;  // epoch space exhausted
     const uint32_t e0 = d.epoch;
     d.epoch += (uint32_t) d.n_layer;
+    if (d.use_xcd) return qw::launch_decode_xcd(d, x, out, x_out, ids_out, weights_out, e0, S(stream));
     return qw::launch_decode_stack(d, x, out, x_out, ids_out, weights_out, e0, S(stream));
+}
+
+int qwmoe_decode_stack_kernel(const qwmoe_decode_stack* s) {
+    if (!s) return QWMOE_ERR_INVALID_ARG;
+    return s->d.use_xcd ? (s->d.xcd_local ? 2 : 3) : 1;
 }
 
 int qwmoe_decode_stack_status(void* stream, qwmoe_decode_stack* s, int32_t* status_out, int clear) {

@@ -29,6 +29,9 @@ struct DecodeStackDesc {
     uint64_t* xa = nullptr;       // exchange words
     uint64_t* xy = nullptr;
     uint64_t* xl = nullptr;
+    uint64_t* xd = nullptr;       // XCD kernel: down outputs crossing XCDs
+    int use_xcd = 0;              // 1: k_decode_xcd (one expert per XCD), 0: k_decode_stack
+    int xcd_local = 0;            // XCD kernel: XCD-local words stored with workgroup scope
     int32_t* status = nullptr;
     int32_t* abort_flag = nullptr;
     uint32_t epoch = 1;           // next launch's first layer epoch
@@ -44,6 +47,14 @@ int plan_decode_stack(DecodeStackDesc& d, int grid);
 const void* decode_kernel(const DecodeStackDesc& d);
 // 0 if one WG of the planned kernel fits on a CU (grid = CU count => all resident).
 int check_decode_residency(const DecodeStackDesc& d);
+// decode_xcd.hip: the kernel with one selected expert per XCD (grid = 8 XCDs x 32 CUs)
+const void* decode_xcd_kernel(const DecodeStackDesc& d);
+// 0 if the shape has an XCD kernel and the device has 256 CUs
+int check_decode_xcd(const DecodeStackDesc& d, int cus);
+// writes each workgroup's XCD id to dev_buf[0..n) and sets *ok when workgroup b runs on XCD b % 8
+int probe_xcd_mapping(int32_t* dev_buf, int n, hipStream_t stream, int* ok);
+int launch_decode_xcd(const DecodeStackDesc& d, const float* x_in, float* out, float* x_out, int32_t* ids_out,
+                      float* w_out, uint32_t epoch0, hipStream_t stream);
 int launch_decode_stack(const DecodeStackDesc& d, const float* x_in, float* out, float* x_out, int32_t* ids_out,
                         float* w_out, uint32_t epoch0, hipStream_t stream);
 

@@ -201,6 +201,10 @@ class DecodeStack:
         self.run(x, out, xo, ids, w)
         return out, xo, ids, w
 
+    def kernel(self) -> int:
+        """1: one workgroup per CU; 2: one expert per XCD; 3: the same, device-scope words."""
+        return int(lib().qwmoe_decode_stack_kernel(self.h))
+
     def status(self, clear: bool = True) -> int:
         v = C.c_int32(0)
         check(lib().qwmoe_decode_stack_status(stream(), self.h, C.byref(v), int(clear)), "decode_stack_status")
