@@ -100,6 +100,13 @@ __device__ __forceinline__ void x_abort(const XcdArgs& a, int bit) {
 // completed, and the compiler keeps memory accesses on their side.
 __device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
+// Says, at a point where it costs nothing, that every load of this thread has
+// returned (vmcnt(0)).  The compiler tracks pending loads per register, and a
+// load consumed on one path only (the prefetches of the next layer) stays
+// "pending" across the loop back-edge: the next write to its register would
+// then wait vmcnt(N), i.e. for the weight loads issued after it.
+__device__ __forceinline__ void all_loads_returned() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 // Polls n tagged words (this thread's: i = tid + XT * m, m < MAXJ) until each
 // carries epoch ep, then stores the payloads to dst[i] (LDS).  Only the words
 // not yet seen are polled again.  Returns false if the wait gave up.
@@ -139,13 +146,51 @@ __device__ __forceinline__ bool gather(const XcdArgs& a, const uint64_t* src, in
     return true;
 }
 
-// quantize_row_q8_K_ref (ggml-quants.c:2768-2803) of nblocks x 256 fp32 values
-// in LDS into QB-strided LDS blocks.  Sixteen lanes (one DPP row) per block,
-// sixteen consecutive values per lane: the first-index max |x| is a four-step
-// row reduction, and each lane's values form exactly one bsums group.
-// Threads [0, 16 * nblocks) take part.
-__device__ __forceinline__ void quant_q8K_xb(const float* src, int nblocks, uint8_t* q, int tid) {
-    const int tt = tid;
+// Wave-wide reductions without the LDS crossbar: an all-reduce inside each
+// 16-lane row (DPP xor1, xor2, half-mirror, mirror), then row_bcast:15 and
+// row_bcast:31 fold rows 0..3 into lane 63, which readlane makes uniform.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_rows_f(float old, float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROWS, 0xF, false));
+}
+template <int CTRL, int ROWS>
+__device__ __forceinline__ int dpp_rows_i(int old, int v) {
+    return __builtin_amdgcn_update_dpp(old, v, CTRL, ROWS, 0xF, false);
+}
+__device__ __forceinline__ float wave_max_uniform(float v) {
+    v = fmaxf(v, dpp_f<DPP_XOR1>(v));
+    v = fmaxf(v, dpp_f<DPP_XOR2>(v));
+    v = fmaxf(v, dpp_f<DPP_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_f<DPP_MIRROR>(v));
+    v = fmaxf(v, dpp_rows_f<0x142, 0xA>(v, v));   // rows 1, 3 <- lane 15 of rows 0, 2
+    v = fmaxf(v, dpp_rows_f<0x143, 0xC>(v, v));   // rows 2, 3 <- lane 31
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+// (|x|, index) of the first largest |x| over the wave, uniform.
+__device__ __forceinline__ void wave_argmax_first(float& am, int& ai) {
+#define QW_AMAX_STEP(OM, OI)                                        \
+    {                                                               \
+        const float om = OM;                                        \
+        const int oi = OI;                                          \
+        if (om > am || (om == am && oi < ai)) { am = om; ai = oi; } \
+    }
+    QW_AMAX_STEP(dpp_f<DPP_XOR1>(am), dpp_i<DPP_XOR1>(ai))
+    QW_AMAX_STEP(dpp_f<DPP_XOR2>(am), dpp_i<DPP_XOR2>(ai))
+    QW_AMAX_STEP(dpp_f<DPP_HALF_MIRROR>(am), dpp_i<DPP_HALF_MIRROR>(ai))
+    QW_AMAX_STEP(dpp_f<DPP_MIRROR>(am), dpp_i<DPP_MIRROR>(ai))
+    QW_AMAX_STEP((dpp_rows_f<0x142, 0xA>(am, am)), (dpp_rows_i<0x142, 0xA>(ai, ai)))
+    QW_AMAX_STEP((dpp_rows_f<0x143, 0xC>(am, am)), (dpp_rows_i<0x143, 0xC>(ai, ai)))
+#undef QW_AMAX_STEP
+    am = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(am), 63));
+    ai = __builtin_amdgcn_readlane(ai, 63);
+}
+
+// quantize_row_q8_K_ref of nblocks x 256 values x[i] = src[i] * mul (LDS) into
+// QB-strided LDS blocks.  Sixteen lanes (one DPP row) per block, sixteen
+// consecutive values per lane: the first-index max |x| is a four-step row
+// reduction and each lane's values form exactly one bsums group.  Lanes
+// [0, 16 * nblocks) of the calling wave(s), numbered by tt, take part.
+__device__ __forceinline__ void quant_q8K_r16(const float* src, float mul, int nblocks, uint8_t* q, int tt) {
     if (tt < 0 || tt >= 16 * nblocks) return;
     const int b = tt >> 4, l = tt & 15;
     const float* x = src + b * QK_K + 16 * l;
@@ -153,10 +198,10 @@ __device__ __forceinline__ void quant_q8K_xb(const float* src, int nblocks, uint
 #pragma unroll
     for (int i = 0; i < 16; i += 4) {
         const float4 t4 = *(const float4*) (x + i);
-        v[i] = t4.x;
-        v[i + 1] = t4.y;
-        v[i + 2] = t4.z;
-        v[i + 3] = t4.w;
+        v[i] = t4.x * mul;
+        v[i + 1] = t4.y * mul;
+        v[i + 2] = t4.z * mul;
+        v[i + 3] = t4.w * mul;
     }
     float am = 0.0f;
     int ai = 0x7fffffff;
@@ -183,7 +228,7 @@ __device__ __forceinline__ void quant_q8K_xb(const float* src, int nblocks, uint
         if (l == 0) *(float*) (blk + 256) = 0.0f;
         return;
     }
-    const float iscale = -127.f / src[b * QK_K + ai];
+    const float iscale = -127.f / (src[b * QK_K + ai] * mul);
     int s = 0;
     u32x4 words = {0u, 0u, 0u, 0u};
 #pragma unroll
@@ -198,38 +243,111 @@ __device__ __forceinline__ void quant_q8K_xb(const float* src, int nblocks, uint
     if (l == 0) *(float*) (blk + 256) = 1.0f / iscale;
 }
 
-// Integer partials of one Q4_K super-block for lane t (0..7) of its 8-lane
+// quantize_row_q8_K_ref (ggml-quants.c:2768-2803) of one 256-value block by one
+// wave, four values per lane (v[i] = value 4 * lane + i), into a QB-strided LDS
+// block: the first-index max |x| is a wave reduction of (|x|, index), each
+// four-lane group's values form one bsums group.
+__device__ __forceinline__ void quant_q8K_w64(const float v[4], int lane, uint8_t* blk) {
+    float am = 0.0f;
+    int ai = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float ax = __builtin_fabsf(v[i]);
+        if (ax > am) { am = ax; ai = 4 * lane + i; }
+    }
+    wave_argmax_first(am, ai);
+    if (!(am > 0.0f)) {   // amax == 0: d = 0, qs = 0 (bsums written as 0)
+        *(uint32_t*) (blk + 4 * lane) = 0u;
+        if ((lane & 3) == 0) *(int16_t*) (blk + 260 + 2 * (lane >> 2)) = 0;
+        if (lane == 0) *(float*) (blk + 256) = 0.0f;
+        return;
+    }
+    const int sel = ai & 3;
+    const float mine = sel == 0 ? v[0] : sel == 1 ? v[1] : sel == 2 ? v[2] : v[3];
+    const float maxv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), ai >> 2));   // the signed value
+    const float iscale = -127.f / maxv;
+    int s = 0;
+    uint32_t w = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        int q = nearest_int(iscale * v[i]);
+        q = q < 127 ? q : 127;
+        s += q;
+        w |= (uint32_t) (q & 0xff) << (8 * i);
+    }
+    *(uint32_t*) (blk + 4 * lane) = w;
+    s += dpp_i<DPP_XOR1>(s);
+    s += dpp_i<DPP_XOR2>(s);
+    if ((lane & 3) == 0) *(int16_t*) (blk + 260 + 2 * (lane >> 2)) = (int16_t) s;
+    if (lane == 0) *(float*) (blk + 256) = 1.0f / iscale;
+}
+
+// The scale bytes of a Q4_K block (get_scale_min_k4 / the utmp shuffle of
+// quants.c:2067-2072): sub-blocks 0..3 from s0, 4..7 from s2 and the top bits
+// of s0; mins likewise from s1 / s2.  hi selects the upper four (branch-free).
+__device__ __forceinline__ uint32_t q4k_scale_word(uint32_t s0, uint32_t s2, bool hi) {
+    const uint32_t lo4 = s0 & 0x3f3f3f3fu;
+    const uint32_t hi4 = (s2 & 0x0f0f0f0fu) | (((s0 >> 6) & 0x03030303u) << 4);
+    const uint32_t m = 0u - (uint32_t) hi;
+    return lo4 ^ ((lo4 ^ hi4) & m);
+}
+__device__ __forceinline__ uint32_t q4k_min_word(uint32_t s1, uint32_t s2, bool hi) {
+    const uint32_t lo4 = s1 & 0x3f3f3f3fu;
+    const uint32_t hi4 = ((s2 >> 4) & 0x0f0f0f0fu) | (((s1 >> 6) & 0x03030303u) << 4);
+    const uint32_t m = 0u - (uint32_t) hi;
+    return lo4 ^ ((lo4 ^ hi4) & m);
+}
+
+// The weight side of one Q4_K super-block for lane t (0..7) of its 8-lane
 // group: hdr = bytes 0..15 (d, dmin, scales), qc = quant bytes 16t..16t+15,
-// i.e. 64-element chunk j = t >> 1 and AVX lanes n = 4 (t & 1) + i.  yq: the
-// Q8_K block's qs in LDS.  p[i] = sc_{2j} . sum(q4lo . q8) + sc_{2j+1} . sum(q4hi . q8)
-// over AVX lane n's four bytes (the maddubs + madd of quants.c:2092-2100).
-__device__ __forceinline__ void q4k_partials(const u32x4& hdr, const u32x4& qc, const uint8_t* yq, int t, int p[4]) {
-    const int j = t >> 1, hb = t & 1;
-    const uint32_t s0 = hdr[1], s2 = hdr[3];
-    const uint32_t scw = j < 2 ? (s0 & 0x3f3f3f3fu) : ((s2 & 0x0f0f0f0fu) | (((s0 >> 6) & 0x03030303u) << 4));
+// i.e. 64-element chunk j = t >> 1 and AVX lanes n = 4 (t & 1) + i.
+struct Q4KLane {
+    uint32_t lo[4], hi[4];   // the nibbles of qc as bytes (sub-blocks 2j and 2j + 1)
+    int scl, sch;            // their scales
+    int m0, m1;              // the mins of sub-blocks 2n', 2n' + 1, n' = t & 3 (min lane n')
+    float d, dmin;           // fp16 d and dmin as fp32
+};
+__device__ __forceinline__ Q4KLane q4k_lane(const u32x4& hdr, const u32x4& qc, int t) {
+    Q4KLane w;
+    const int j = t >> 1, n = t & 3;
+    const uint32_t scw = q4k_scale_word(hdr[1], hdr[3], j >= 2);
     const int sh = 16 * (j & 1);
-    const int scl = (int) ((scw >> sh) & 0xffu), sch = (int) ((scw >> (sh + 8)) & 0xffu);
+    w.scl = (int) __builtin_amdgcn_ubfe(scw, sh, 8);
+    w.sch = (int) __builtin_amdgcn_ubfe(scw, sh + 8, 8);
+    const uint32_t mw = q4k_min_word(hdr[2], hdr[3], n >= 2);
+    w.m0 = (int) __builtin_amdgcn_ubfe(mw, 16 * (n & 1), 8);
+    w.m1 = (int) __builtin_amdgcn_ubfe(mw, 16 * (n & 1) + 8, 8);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        w.lo[i] = qc[i] & 0x0F0F0F0Fu;
+        w.hi[i] = (qc[i] >> 4) & 0x0F0F0F0Fu;
+    }
+    w.d = h2f((uint16_t) (hdr[0] & 0xffff));
+    w.dmin = h2f((uint16_t) (hdr[0] >> 16));
+    return w;
+}
+
+// Integer partials of that lane against a Q8_K block (qs at yq in LDS):
+// p[i] = sc_{2j} . sum(q4lo . q8) + sc_{2j+1} . sum(q4hi . q8) over AVX lane n's
+// four bytes (the maddubs + madd of quants.c:2092-2100).
+__device__ __forceinline__ void q4k_dot(const Q4KLane& w, const uint8_t* yq, int t, int p[4]) {
+    const int j = t >> 1, hb = t & 1;
     const u32x4 alo = *(const u32x4*) (yq + 64 * j + 16 * hb);
     const u32x4 ahi = *(const u32x4*) (yq + 64 * j + 32 + 16 * hb);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int lo = (int) (qc[i] & 0x0F0F0F0Fu), hi = (int) ((qc[i] >> 4) & 0x0F0F0F0Fu);
-        p[i] = mul24(scl, sdot4(lo, (int) alo[i], 0)) + mul24(sch, sdot4(hi, (int) ahi[i], 0));
-    }
+    for (int i = 0; i < 4; ++i)
+        p[i] = mul24(w.scl, sdot4((int) w.lo[i], (int) alo[i], 0)) + mul24(w.sch, sdot4((int) w.hi[i], (int) ahi[i], 0));
 }
 
-// Min lane n = t (t < 4) of a Q4_K super-block: mins of sub-blocks 2n, 2n+1
-// times the Q8_K sums of those sub-blocks (_mm_madd_epi16(mins, hadd(bsums)),
-// quants.c:2084-2087).  yb: the Q8_K block in LDS (bsums at 260).
-__device__ __forceinline__ int q4k_min_prod(const u32x4& hdr, const uint8_t* yb, int t) {
-    const uint32_t s1 = hdr[2], s2 = hdr[3];
+// Min lane n = t & 3: mins of sub-blocks 2n, 2n+1 times the Q8_K sums of those
+// sub-blocks (_mm_madd_epi16(mins, hadd(bsums)), quants.c:2084-2087).  yb: the
+// Q8_K block in LDS (bsums at 260).
+__device__ __forceinline__ int q4k_min_dot(const Q4KLane& w, const uint8_t* yb, int t) {
     const int n = t & 3;
-    const uint32_t mw = n < 2 ? (s1 & 0x3f3f3f3fu) : (((s2 >> 4) & 0x0f0f0f0fu) | (((s1 >> 6) & 0x03030303u) << 4));
-    const int m0 = (int) ((mw >> (16 * (n & 1))) & 0xffu), m1 = (int) ((mw >> (16 * (n & 1) + 8)) & 0xffu);
     const uint32_t bs01 = *(const uint32_t*) (yb + 260 + 8 * n), bs23 = *(const uint32_t*) (yb + 264 + 8 * n);
     const int q8s0 = (int) (int16_t) (bs01 & 0xffff) + (int) (int16_t) (bs01 >> 16);
     const int q8s1 = (int) (int16_t) (bs23 & 0xffff) + (int) (int16_t) (bs23 >> 16);
-    return mul24(m0, q8s0) + mul24(m1, q8s1);
+    return mul24(w.m0, q8s0) + mul24(w.m1, q8s1);
 }
 
 // Sum over the four 64-element chunks: lanes t and t ^ 2 (quad_perm), then t
@@ -238,8 +356,37 @@ __device__ __forceinline__ void reduce_chunks(int p[4]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int a = p[i] + dpp_i<DPP_XOR2>(p[i]);
-        p[i] = a + __builtin_amdgcn_update_dpp(0, a, 0x104, 0xF, 0xF, false);   // row_shl:4: lane i <- i + 4
+        p[i] = a + __builtin_amdgcn_update_dpp(0, a, 0x104, 0xF, 0xF, true);   // row_shl:4: lane i <- i + 4 (0 past the row)
     }
+}
+
+// Router logit of x = y * sc (the RMSNorm, formed value by value); lane c < 32
+// of a half-wave is chain c of AVX2 ggml_vec_dot_f32 (GGML_F32_STEP 32) and
+// holds that chain's router weights w[s] = W[e][c + 32 s] in registers; then the
+// reduction tree of that function; lane 0 returns the logit.  x is read from
+// LDS sixteen steps at a time, the next sixteen in flight during the fmas.
+template <int H>
+__device__ __forceinline__ float router_chain(const float (&w)[H / 32], const float* y, float sc, int c) {
+    float acc = 0.0f;
+    float xv[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) xv[u] = y[32 * u + c];
+#pragma unroll
+    for (int s0 = 0; s0 < H / 32; s0 += 16) {
+        float xn[16];
+        const int s1 = s0 + 16 < H / 32 ? s0 + 16 : s0;   // (the last round reloads its own)
+#pragma unroll
+        for (int u = 0; u < 16; ++u) xn[u] = y[32 * (s1 + u) + c];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) acc = __builtin_fmaf(w[s0 + u], xv[u] * sc, acc);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) xv[u] = xn[u];
+    }
+    float t = acc + __shfl_down(acc, 16, 32);   // c_l + c_{16+l}
+    t = t + __shfl_down(t, 8, 32);               // (c_l + c_{16+l}) + (c_{8+l} + c_{24+l})
+    t = t + __shfl_down(t, 4, 32);               // t0_l = s_l + s_{l+4}
+    const float u = t + __shfl_down(t, 1, 32);
+    return u + __shfl_down(u, 2, 32);            // (t0_0 + t0_1) + (t0_2 + t0_3)
 }
 
 // std::sort's order of tied probabilities (qw_sort.hpp), kept out of line: the
@@ -248,28 +395,12 @@ __device__ __attribute__((noinline)) void sort_desc_replay(int32_t* order, int n
     libstdcxx_sort_desc(order, n, p, stack);
 }
 
-// Router logits e = NLOG * j + hw of x (LDS) from the LDS router rows; lanes
-// c < 32 of half-wave hw are the 32 fma chains of AVX2 ggml_vec_dot_f32
-// (GGML_F32_STEP 32), then its reduction tree; lane 0 returns the logit.
-template <int H>
-__device__ __forceinline__ float router_chain(const float* w, const float* x, int c) {
-    float acc = 0.0f;
-#pragma unroll 1
-    for (int s0 = 0; s0 < H; s0 += 16 * 32) {
-        float wv[16], xv[16];
-#pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            wv[u] = w[s0 + 32 * u + c];
-            xv[u] = x[s0 + 32 * u + c];
-        }
-#pragma unroll
-        for (int u = 0; u < 16; ++u) acc = __builtin_fmaf(wv[u], xv[u], acc);
-    }
-    float t = acc + __shfl_down(acc, 16, 32);   // c_l + c_{16+l}
-    t = t + __shfl_down(t, 8, 32);               // (c_l + c_{16+l}) + (c_{8+l} + c_{24+l})
-    t = t + __shfl_down(t, 4, 32);               // t0_l = s_l + s_{l+4}
-    const float u = t + __shfl_down(t, 1, 32);
-    return u + __shfl_down(u, 2, 32);            // (t0_0 + t0_1) + (t0_2 + t0_3)
+// A float held by lane id & 63 of register (id >> 6) of a two-register array,
+// read by every lane (id uniform).
+__device__ __forceinline__ float lane_value(const float v[2], int id) {
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[0]), id & 63));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[1]), id & 63));
+    return id < 64 ? a : b;
 }
 
 }  // namespace
@@ -282,31 +413,30 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
     constexpr int PPW = NP / XW;          // pairs per wave
     constexpr int NH = H / NJ;            // down rows per workgroup
     constexpr int RW = NH / XW;           // down rows per wave (one per 8-lane group)
+    constexpr int RW0 = XW - (NLOG + 1) / 2;   // first router wave (two logits per router wave)
+    constexpr int QXW = 4, QXN = NBH / 4; // waves 4, 5 quantize the next layer's x, 16 lanes per block (they share
+                                          // SIMDs with waves 0, 1, which poll the logits, not with the router waves)
     static_assert(NBH == 8, "gate/up rows: one super-block per 8-lane group");
     static_assert(PPW >= 1 && PPW * XW == NP && 2 * PPW * 8 <= 64, "pairs per wave");
-    static_assert(RW == 8, "down rows: one row per 8-lane group");
-    static_assert(E <= 128, "ranking: four lanes per logit");
+    static_assert(RW == 8 && NH == 64, "down rows: one row per 8-lane group; y: one row per lane of wave 0");
+    static_assert(E <= 128 && E % 32 == 0, "logits: two per lane in the per-wave softmax");
+    static_assert(NBF <= XW, "Q8_K of act: one wave per block");
+    static_assert(QXW + QXN <= RW0 && QXN * 4 == NBH, "x quantizer and router waves");
 
-    __shared__ __align__(16) float s_rw[NLOG * H];              // router rows of this workgroup
-    __shared__ __align__(16) float s_x[H];                      // x of the current layer
-    __shared__ __align__(16) float s_y[H];                      // gathered y
+    __shared__ __align__(16) float s_y[H];                      // y of the last layer (x = y * sc)
     __shared__ __align__(16) uint8_t s_xq[NBH * QB];            // Q8_K(x)
     __shared__ __align__(16) float s_act[F];
     __shared__ __align__(16) uint8_t s_aq[NBF * QB];            // Q8_K(act)
     __shared__ __align__(16) uint32_t s_tr[XW][2 * PPW][NBH][16];   // gate/up block records
-    __shared__ __align__(16) float s_d8[NXCD * NH];
-    __shared__ __align__(16) float s_p[E];
-    __shared__ float s_e[E];
-    __shared__ int32_t s_order[E];
-    __shared__ float s_gsum[E / 8];
+    __shared__ __align__(16) float s_p[E];                      // logits
+    __shared__ __align__(16) float s_pe[E];                     // the exact path's probabilities
+    __shared__ __align__(16) int32_t s_order[E];
     __shared__ int32_t s_slot[2][3][E];
     __shared__ uint64_t s_L[2][XLW];
     __shared__ SortRange s_stack[SORT_STACK];
     __shared__ double s_red[XW];
-    __shared__ int32_t s_spec[8];
-    __shared__ int32_t s_ids[8];
-    __shared__ float s_w[8];
-    __shared__ int s_fail, s_bad, s_need_sort;
+    __shared__ __align__(16) int32_t s_spec[8];
+    __shared__ int s_fail, s_need_sort;
 
     const int b = blockIdx.x, tid0 = threadIdx.x;
     const int xcd = b & (NXCD - 1), j = b >> 3;
@@ -316,30 +446,44 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
 
     if ((int) (__builtin_amdgcn_s_getreg((3 << 11) | 20) & 7) != xcd && tid0 == 0) atomicOr(a.status, 64);
 
+    // The end of a layer (and the prologue): the next layer's router logits from
+    // x = y * sc (router waves) and Q8_K(x) (waves QXW..QXW + QXN - 1).
+    // Router weights of this lane's chain (router waves): W[NLOG j + hw][c + 32 s].
+    float rw[H / 32];
+    auto load_router = [&](const float* router, int tid) {
+        const int wave = tid >> 6, lane = tid & 63;
+        const int hw = 2 * (wave - RW0) + ((lane >> 5) & 1), c = lane & 31;
+        if (wave >= RW0 && hw < NLOG) {
+            const float* src = router + (size_t) (NLOG * j + hw) * H + c;
+#pragma unroll
+            for (int s2 = 0; s2 < H / 32; ++s2) rw[s2] = *(const __attribute__((address_space(1))) float*) (src + 32 * s2);
+        }
+    };
+    auto next_x = [&](int tid, float sc, uint32_t ep_next) {
+        const int wave = tid >> 6, lane = tid & 63;
+        const int hw = 2 * (wave - RW0) + ((lane >> 5) & 1), c = lane & 31;
+        if (wave >= RW0 && hw < NLOG) {
+            const float lg = router_chain<H>(rw, s_y, sc, c);
+            if (c == 0) st_local(a.xl + xcd * E + NLOG * j + hw, tag(lg, ep_next), local);
+        }
+        if (wave >= QXW && wave < QXW + QXN) quant_q8K_r16(s_y, sc, NBH, s_xq, tid - 64 * QXW);
+    };
+
     // ---- prologue: descriptors, x of layer 0, router rows and slot rows of layer 0
     if (tid0 == 0) s_fail = 0;
     if (tid0 < 8) s_spec[tid0] = 0;
     if (tid0 < 2 * XLW && tid0 / XLW < a.n_layer) s_L[tid0 / XLW][tid0 % XLW] = ldg64((const uint64_t*) a.layers + tid0);
-    for (int i = tid0; i < H; i += XT) s_x[i] = a.x_in[i];
+    for (int i = tid0; i < H; i += XT) s_y[i] = a.x_in[i];   // layer 0 takes x_in as it is (sc = 1)
     {
         const DecodeLayer& L0 = a.layers[0];
-        const float* rsrc = L0.router + (size_t) NLOG * j * H;
-        for (int c = tid0; c < NLOG * H / 4; c += XT) *(u32x4*) (s_rw + 4 * c) = ldg16(rsrc + 4 * c);
+        load_router(L0.router, tid0);
         for (int i = tid0; i < 3 * E; i += XT) {
             const int32_t* so = i < E ? L0.slot_gate : i < 2 * E ? L0.slot_up : L0.slot_down;
             s_slot[0][i / E][i % E] = so ? ldg32(so + i % E) : i % E;
         }
     }
     __syncthreads();
-    quant_q8K_xb(s_x, NBH, s_xq, tid0);
-    {
-        const int rw0 = XW - (NLOG + 1) / 2;   // router waves: the last ones
-        const int w = tid0 >> 6, hw = 2 * (w - rw0) + ((tid0 >> 5) & 1), c = tid0 & 31;
-        if (w >= rw0 && hw < NLOG) {
-            const float lg = router_chain<H>(s_rw + hw * H, s_x, c);
-            if (c == 0) st_local(a.xl + xcd * E + NLOG * j + hw, tag(lg, a.epoch0), local);
-        }
-    }
+    next_x(tid0, 1.0f, a.epoch0);
 
     for (int l = 0; l < a.n_layer; ++l) {
         const DecodeLayer& L = *(const DecodeLayer*) s_L[l & 1];
@@ -347,16 +491,13 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
         const int tid = opaque(tid0);
         const int wave = tid >> 6, lane = tid & 63, g = lane >> 3, t = lane & 7;
 
-        // ---- L: the layer's logits (all E, from this XCD) ----------------------
-        if (!gather<1>(a, a.xl + xcd * E, E, ep, s_p, tid)) s_fail = 1;
-        if (tid == 0) {
-            s_bad = 0;
-            s_need_sort = 0;
-        }
+        all_loads_returned();   // (the last were the y polls and the prefetches they follow)
+        // ---- L: the layer's logits (all E, from this XCD's router workgroups) ------
+        if (tid < E && !gather<1>(a, a.xl + xcd * E, E, ep, s_p, tid)) s_fail = 1;
         lds_barrier();
         if (s_fail) return;
         // logit ranks (strictly larger count; four lanes per value); the rank-c
-        // expert is XCD c's speculative expert, its rows are loaded at once
+        // expert is XCD c's speculative expert, its gate/up rows are loaded at once
         {
             const int i = tid >> 2, sub = tid & 3;
             const float li = s_p[i < E ? i : 0];
@@ -366,12 +507,11 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
                 const float4 q = *(const float4*) (s_p + 4 * (c0 + sub));
                 rank += (q.x > li) + (q.y > li) + (q.z > li) + (q.w > li);
             }
-            rank += __shfl_xor(rank, 1);
-            rank += __shfl_xor(rank, 2);
+            rank += dpp_i<DPP_XOR1>(rank);
+            rank += dpp_i<DPP_XOR2>(rank);
             if (i < E && sub == 0) {
                 s_order[i] = rank;
                 if (rank < k) s_spec[rank] = i;
-                if (li != li) s_bad = 1;
             }
         }
         lds_barrier();
@@ -408,95 +548,150 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
                 dq[bb] = ldg16(rd + 144 * bb + 16 + 16 * t);
             }
         };
-        const int spec_e = expert_xcd ? s_spec[xcd] : 0;
+        const int spec_e = __builtin_amdgcn_readfirstlane(s_spec[expert_xcd ? xcd : 0]);
         if (expert_xcd) issue(spec_e);
 
-        // ---- softmax, exact order, weights (every workgroup, same values) -------
+        // ---- softmax, top-k, weights: every wave on its own, in registers ------------
+        // ggml_soft_max (ops.cpp:5455-5566): max, ggml_v_expf, sums of eight
+        // (hsum_float_8) added in double, scale by 1 / sum.  Lane holds logits
+        // lane and lane + 64.
+        float pv[2];
+        int ids[8];
+        float pk[8], wk[8];
+        bool fast;
         {
-            float mx = -INFINITY;
-            for (int i = lane; i < E; i += 64) mx = fmaxf(mx, s_p[i]);
-            mx = fmaxf(mx, dpp_f<DPP_XOR1>(mx));
-            mx = fmaxf(mx, dpp_f<DPP_XOR2>(mx));
-            mx = fmaxf(mx, dpp_f<DPP_HALF_MIRROR>(mx));
-            mx = fmaxf(mx, dpp_f<DPP_MIRROR>(mx));
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            for (int i = tid; i < E; i += XT) s_e[i] = v_expf(s_p[i] - mx);
-            lds_barrier();
-            for (int gi = tid; gi < E / 8; gi += XT) s_gsum[gi] = hsum8(&s_e[8 * gi]);
-            lds_barrier();
+            float lv[2];
+            int rk[2];
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {
+                const int i = lane + 64 * m;
+                lv[m] = i < E ? s_p[i] : -INFINITY;
+                rk[m] = i < E ? s_order[i] : E;
+            }
+            const float mx = wave_max_uniform(fmaxf(lv[0], lv[1]));
+            float ev[2], gs[2];
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {
+                ev[m] = lane + 64 * m < E ? v_expf(lv[m] - mx) : 0.0f;
+                // hsum_float_8 of lanes 8q..8q+7 into lane 8q: (a_i + a_{i+4}),
+                // then (r0 + r2), (r1 + r3), then their sum (quants.c:42-48 pairing)
+                const float r = ev[m] + dpp_f<0x104>(ev[m]);   // row_shl:4
+                const float r2 = r + dpp_f<0x102>(r);          // row_shl:2
+                gs[m] = r2 + dpp_f<0x101>(r2);                  // row_shl:1
+            }
             double sum = 0.0;
-            for (int gi = 0; gi < E / 8; ++gi) sum += (double) s_gsum[gi];
+#pragma unroll
+            for (int gi = 0; gi < E / 8; ++gi)
+                sum += (double) __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gs[gi >> 3]), 8 * (gi & 7)));
             const float inv = (float) (1.0 / sum);
-            for (int i = tid; i < E; i += XT) s_p[i] = s_e[i] * inv;
+            pv[0] = ev[0] * inv;
+            pv[1] = ev[1] * inv;
+            // The speculative order is argsort's first k iff its probabilities
+            // strictly decrease and every other probability is strictly below the
+            // k-th (ties, rank collisions and NaN all fail this).
+            bool ok = true;
+            const int4 sp0 = *(const int4*) s_spec, sp1 = *(const int4*) (s_spec + 4);
+            const int spv[8] = {sp0.x, sp0.y, sp0.z, sp0.w, sp1.x, sp1.y, sp1.z, sp1.w};
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                ids[r] = r < k ? __builtin_amdgcn_readfirstlane(spv[r]) : 0;
+                pk[r] = r < k ? lane_value(pv, ids[r]) : 0.0f;
+                if (r > 0 && r < k) ok = ok && (pk[r - 1] > pk[r]);
+            }
+            float qk = pk[0];
+#pragma unroll
+            for (int r = 1; r < 8; ++r) qk = r == k - 1 ? pk[r] : qk;
+            bool bad_lane = false;
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {
+                const int i = lane + 64 * m;
+                int sp = -1;
+#pragma unroll
+                for (int r = 0; r < 8; ++r) sp = rk[m] == r ? ids[r] : sp;
+                const bool in_spec = rk[m] < k && sp == i;
+                if (i < E && !in_spec && !(pv[m] < qk)) bad_lane = true;
+            }
+            fast = ok && !__any(bad_lane);
+        }
+        if (!fast) {
+            // exact order (every wave reached the same decision): rank the
+            // probabilities; a tie or NaN inside the first k places leaves the
+            // order to std::sort, which is replayed exactly
+            if (wave == 0) {
+                if (lane < E) s_pe[lane] = pv[0];
+                if (lane + 64 < E) s_pe[lane + 64] = pv[1];
+            }
+            if (tid == 0) s_need_sort = 0;
             lds_barrier();
-            // the speculative order is the argsort's first k iff its probabilities
-            // strictly decrease and every other one is strictly below the k-th
-            {
-                const float q = s_p[s_spec[k - 1]];
-                for (int i = tid; i < E; i += XT) {
-                    const int r = s_order[i];
-                    const float pi = s_p[i];
-                    const bool ok = r >= k ? (pi < q) : (s_spec[r] == i && (r == 0 || s_p[s_spec[r - 1]] > pi));
-                    if (!ok) s_bad = 1;
+            for (int i = tid; i < E; i += XT) {
+                const float pi = s_pe[i];
+                int gt = 0, eq = 0;
+                for (int jj = 0; jj < E; jj += 4) {
+                    const float4 q = *(const float4*) (s_pe + jj);
+                    gt += (q.x > pi) + (q.y > pi) + (q.z > pi) + (q.w > pi);
+                    eq += (q.x == pi) + (q.y == pi) + (q.z == pi) + (q.w == pi);
+                }
+                if (gt < k) {
+                    if (eq != 1) s_need_sort = 1;
+                    else s_order[gt] = i;
                 }
             }
             lds_barrier();
-            if (!s_bad) {
-                if (tid < k) s_order[tid] = s_spec[tid];
-            } else {
-                for (int i = tid; i < E; i += XT) {
-                    const float pi = s_p[i];
-                    int gt = 0, eq = 0;
-                    for (int jj = 0; jj < E; jj += 4) {
-                        const float4 q = *(const float4*) (s_p + jj);
-                        gt += (q.x > pi) + (q.y > pi) + (q.z > pi) + (q.w > pi);
-                        eq += (q.x == pi) + (q.y == pi) + (q.z == pi) + (q.w == pi);
-                    }
-                    if (gt < k) {
-                        if (eq != 1) s_need_sort = 1;
-                        else s_order[gt] = i;
-                    }
-                }
+            if (s_need_sort) {
+                for (int i = tid; i < E; i += XT) s_order[i] = i;
                 lds_barrier();
-                if (s_need_sort) {
-                    for (int i = tid; i < E; i += XT) s_order[i] = i;
-                    lds_barrier();
-                    if (tid == 0) {
-                        sort_desc_replay(s_order, E, s_p, s_stack);
-                        if (b == 0) atomicOr(a.status, 1);
-                    }
+                if (tid == 0) {
+                    sort_desc_replay(s_order, E, s_pe, s_stack);
+                    if (b == 0) atomicOr(a.status, 1);
                 }
             }
             lds_barrier();
-            if (tid < k) {
-                const int id = s_order[tid];
-                s_ids[tid] = id;
-                s_e[tid] = s_p[id];
+            const int4 so0 = *(const int4*) s_order, so1 = *(const int4*) (s_order + 4);
+            const int sov[8] = {so0.x, so0.y, so0.z, so0.w, so1.x, so1.y, so1.z, so1.w};
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                ids[r] = r < k ? __builtin_amdgcn_readfirstlane(sov[r]) : 0;
+                pk[r] = r < k ? lane_value(pv, ids[r]) : 0.0f;
             }
-            lds_barrier();
-            if (tid < k) {
-                double s = 0.0;
-                for (int i = 0; i < k; ++i) s += (double) s_e[i];
-                float wsum = (float) s;
-                wsum = fmaxf(fminf(wsum, INFINITY), 6.103515625e-5f);
-                float wi = s_e[tid] / wsum;
+        }
+        // weights: selected probabilities / clamp(sum) (* scale), core/runtime.cpp:887-897
+        {
+            double sp = 0.0;
+#pragma unroll
+            for (int r = 0; r < 8; ++r)
+                if (r < k) sp += (double) pk[r];
+            float wsum = (float) sp;
+            wsum = fmaxf(fminf(wsum, INFINITY), 6.103515625e-5f);
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                float wi = pk[r] / wsum;
                 if (a.scale != 0.0f && a.scale != 1.0f) wi = wi * a.scale;
-                s_w[tid] = wi;
-                if (b == 0 && a.ids_out) {
-                    a.ids_out[l * k + tid] = s_ids[tid];
-                    a.w_out[l * k + tid] = wi;
-                }
+                wk[r] = wi;
             }
         }
-        // slot checks of the selected experts (reported once, by workgroup 0)
-        if (b == 0 && tid < 3 * k) {
-            const int role = tid / k, e = s_ids[tid % k];
-            const int32_t s = s_slot[l & 1][role][e];
-            const int64_t n = role == 0 ? L.n_slots_gate : role == 1 ? L.n_slots_up : L.n_slots_down;
-            if (s < 0 || s >= n) atomicOr(a.status, 16);
+        int my_e = ids[0];
+#pragma unroll
+        for (int r = 1; r < 8; ++r) my_e = r == xcd ? ids[r] : my_e;
+        if (wave == 0 && lane < k) {
+            int id = ids[0];
+            float wi = wk[0];
+#pragma unroll
+            for (int r = 1; r < 8; ++r) {
+                id = lane == r ? ids[r] : id;
+                wi = lane == r ? wk[r] : wi;
+            }
+            if (b == 0 && a.ids_out) {
+                a.ids_out[l * k + lane] = id;
+                a.w_out[l * k + lane] = wi;
+            }
+            // slot checks of the selected experts (reported once, by workgroup 0)
+            if (b == 0) {
+                const int sg = s_slot[l & 1][0][id], su = s_slot[l & 1][1][id], sd = s_slot[l & 1][2][id];
+                if (sg < 0 || sg >= L.n_slots_gate || su < 0 || su >= L.n_slots_up || sd < 0 ||
+                    sd >= L.n_slots_down)
+                    atomicOr(a.status, 16);
+            }
         }
-        const int my_e = expert_xcd ? s_ids[xcd] : 0;
         if (expert_xcd && my_e != spec_e) issue(my_e);   // misspeculated: load the right rows
         if (expert_xcd) issue_down(my_e);
 
@@ -506,16 +701,18 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
             for (int r = 0; r < 2 * PPW; ++r) {
                 int p[4];
                 const uint8_t* yb = s_xq + QB * g;
-                q4k_partials(gh[r], gq[r], yb, t, p);
+                const Q4KLane w = q4k_lane(gh[r], gq[r], t);
+                q4k_dot(w, yb, t, p);
                 reduce_chunks(p);
+                const int pm = q4k_min_dot(w, yb, t);
                 uint32_t* rec = s_tr[wave][r][g];
                 if (t < 2) *(u32x4*) (rec + 4 * t) = u32x4{(uint32_t) p[0], (uint32_t) p[1], (uint32_t) p[2], (uint32_t) p[3]};
-                if (t < 4) rec[8 + t] = (uint32_t) q4k_min_prod(gh[r], yb, t);
-                if (t == 0) rec[12] = gh[r][0];
+                if (t < 4) rec[8 + t] = (uint32_t) pm;
+                if (t == 0) *(uint2*) (rec + 12) = uint2{fbits(w.d), fbits(w.dmin)};
             }
             wave_lds_sync();
             // chain lanes: row r = lane >> 3 (< 2 * PPW), AVX lane n = lane & 7
-            float res = 0.0f;
+            float res;
             {
                 const int r = g < 2 * PPW ? g : 0, n = t;
                 float acc = 0.0f, accm = 0.0f;
@@ -524,10 +721,10 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
                     const uint32_t* rec = s_tr[wave][r][bb];
                     const int S = (int) rec[n];
                     const int pm = (int) rec[8 + (n & 3)];
-                    const uint32_t h0 = rec[12];
+                    const float wd = bitsf(rec[12]), wdm = bitsf(rec[13]);
                     const float yd = *(const float*) (s_xq + QB * bb + 256);
-                    acc = __builtin_fmaf(yd * h2f((uint16_t) (h0 & 0xffff)), (float) S, acc);
-                    const float pmv = __builtin_fmaf(-yd * h2f((uint16_t) (h0 >> 16)), (float) pm, accm);
+                    acc = __builtin_fmaf(yd * wd, (float) S, acc);
+                    const float pmv = __builtin_fmaf(-yd * wdm, (float) pm, accm);
                     accm = n < 4 ? pmv : accm;
                 }
                 float s = acc;
@@ -545,17 +742,10 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
                 st_local(a.xa + xcd * F + f, tag(v_silu(res) * up, ep), local);
             }
         }
-        // next layer's router rows, slot rows and the descriptor of layer l + 2:
-        // issued once the gate/up rows are consumed, stored to LDS once they are needed
+        // next layer's slot rows and the descriptor of layer l + 2: issued once the
+        // gate/up rows are consumed, stored to LDS after the y exchange
         const bool nxt = l + 1 < a.n_layer;
         const DecodeLayer& L1 = *(const DecodeLayer*) s_L[(l + 1) & 1];
-        constexpr int RPT = NLOG * H / 4 / XT;   // router chunks per thread
-        u32x4 rp[RPT];
-        {
-            const float* rsrc = nxt ? L1.router + (size_t) NLOG * j * H : (const float*) a.layers;   // (dummy: 16-aligned)
-#pragma unroll
-            for (int m = 0; m < RPT; ++m) rp[m] = ldg16(rsrc + 4 * (nxt ? tid + m * XT : 0));
-        }
         int32_t sl_next = 0;
         if (tid < 3 * E) {
             const int32_t* so = !nxt ? nullptr : tid < E ? L1.slot_gate : tid < 2 * E ? L1.slot_up : L1.slot_down;
@@ -564,13 +754,20 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
         const bool next2 = l + 2 < a.n_layer && tid < XLW;
         const uint64_t lw = ldg64((const uint64_t*) (a.layers + (next2 ? l + 2 : l)) + (tid % XLW));
 
-        // ---- act of this XCD's expert -> Q8_K ------------------------------------
-        float dres = 0.0f;
+        // ---- act of this XCD's expert -> Q8_K (one wave per block) -----------------
         if (expert_xcd) {
+            // the weight side of the down rows, prepared while the act words are awaited
+            Q4KLane dw[NBF];
+#pragma unroll
+            for (int bb = 0; bb < NBF; ++bb) dw[bb] = q4k_lane(dh[bb], dq[bb], t);
             if (!gather<(F + XT - 1) / XT>(a, a.xa + xcd * F, F, ep, s_act, tid)) s_fail = 1;
             lds_barrier();
             if (s_fail) return;
-            quant_q8K_xb(s_act, NBF, s_aq, tid);
+            if (wave < NBF) {
+                const float4 v4 = *(const float4*) (s_act + QK_K * wave + 4 * lane);
+                const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+                quant_q8K_w64(v, lane, s_aq + QB * wave);
+            }
             lds_barrier();
             // ---- D: down rows 8 * wave + g of this workgroup, in-lane block chain
             float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -579,14 +776,14 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
             for (int bb = 0; bb < NBF; ++bb) {
                 const uint8_t* yb = s_aq + QB * bb;
                 int p[4];
-                q4k_partials(dh[bb], dq[bb], yb, t, p);
+                q4k_dot(dw[bb], yb, t, p);
                 reduce_chunks(p);
                 const float yd = *(const float*) (yb + 256);
-                const float D = yd * h2f((uint16_t) (dh[bb][0] & 0xffff));
+                const float D = yd * dw[bb].d;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(D, (float) p[i], acc[i]);
-                const int pm = q4k_min_prod(dh[bb], yb, t);
-                accm = __builtin_fmaf(-yd * h2f((uint16_t) (dh[bb][0] >> 16)), (float) pm, accm);
+                const int pm = q4k_min_dot(dw[bb], yb, t);
+                accm = __builtin_fmaf(-yd * dw[bb].dmin, (float) pm, accm);
             }
             // hsum_float_8: lane t = 0 holds AVX lanes 0..3, lane t = 1 lanes 4..7
             float r4[4];
@@ -596,32 +793,31 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
             // min lanes 0..3: (m0 + m2) + (m1 + m3)
             const float m2 = accm + dpp_f<DPP_XOR2>(accm);
             const float mm = m2 + dpp_f<DPP_XOR1>(m2);
-            dres = hs + mm;
-            if (t == 0) st_cross(a.xd + (((size_t) (l & 1) * NXCD + xcd) * NJ + j) * NH + RW * wave + g, tag(dres, ep));
+            if (t == 0)
+                st_cross(a.xd + (((size_t) (l & 1) * NXCD + xcd) * NJ + j) * NH + RW * wave + g, tag(hs + mm, ep));
         }
-        // next layer's router rows to LDS (this layer's router ran at the end of the last)
-#pragma unroll
-        for (int m = 0; m < RPT; ++m)
-            if (nxt) *(u32x4*) (s_rw + 4 * (tid + m * XT)) = rp[m];
+        // next layer's router weights, into the router lanes' registers (the gate/up
+        // and down rows are consumed; they arrive while y is exchanged and normed)
+        if (nxt) load_router(L1.router, tid);
 
-        // ---- D -> y[h] for this workgroup's rows, in every XCD -------------------
-        {
-            const uint64_t* src = a.xd + (size_t) (l & 1) * NXCD * NJ * NH;
-            // word (c, h) of workgroup (c, j) -> s_d8[c * NH + h]
-            const int n = k * NH;
-            const int i = tid < n ? tid : n - 1;
-            const int c = i / NH, h = i % NH;
-            uint32_t v = 0;
-            bool ok = tid >= n;
+        // ---- D -> y[h]: wave 0, lane h; the k expert XCDs' down outputs of row h --------
+        if (wave == 0) {
+            const uint64_t* src = a.xd + ((size_t) (l & 1) * NXCD * NJ + j) * NH + lane;
+            float dv[8];
+            uint32_t got = 0;
+            const uint32_t all = (1u << k) - 1u;
             long spins = 0;
-            const uint64_t* wp = src + ((size_t) c * NJ + j) * NH + h;
-            while (!ok) {
-                const uint64_t x = poll64(wp);
-                if ((uint32_t) (x >> 32) == ep) {
-                    v = (uint32_t) x;
-                    ok = true;
-                    break;
-                }
+            while (got != all) {
+                uint64_t v[8];
+#pragma unroll
+                for (int c = 0; c < 8; ++c) v[c] = poll64(src + (size_t) (c < k ? c : 0) * NJ * NH);
+#pragma unroll
+                for (int c = 0; c < 8; ++c)
+                    if (c < k && !(got & (1u << c)) && (uint32_t) (v[c] >> 32) == ep) {
+                        dv[c] = bitsf((uint32_t) v[c]);
+                        got |= 1u << c;
+                    }
+                if (got == all) break;
                 if (++spins > XSPIN) {
                     x_abort(a, 8);
                     break;
@@ -629,8 +825,60 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
                 if ((spins & 255) == 0 && x_aborted(a)) break;
                 __builtin_amdgcn_s_sleep(1);
             }
+            if (got != all) s_fail = 1;
+            else {
+                // ggml_vec_dot_f32(k, experts^T row, w): k < 32 -> scalar tail: groups
+                // of four as mul + add, the remainder fused
+                float sumf = 0.0f;
+                const int nv = k & ~3;
+#pragma unroll
+                for (int c = 0; c < 8; ++c)
+                    if (c < k) sumf = (c < nv) ? sumf + dv[c] * wk[c] : __builtin_fmaf(dv[c], wk[c], sumf);
+                st_local(a.xy + xcd * H + NH * j + lane, tag(sumf, ep), local);
+            }
+        }
+
+        // ---- Y: all y of this XCD, its RMSNorm (sum of squares in double) ------------
+        {
+            float yv[H / XT];
+            bool ok = true;
+            {
+                const uint64_t* src = a.xy + xcd * H;
+                uint32_t got = 0;
+                const uint32_t all = (1u << (H / XT)) - 1u;
+                long spins = 0;
+                while (got != all) {
+                    uint64_t v[H / XT];
+#pragma unroll
+                    for (int m = 0; m < H / XT; ++m) v[m] = poll64(src + tid + m * XT);
+#pragma unroll
+                    for (int m = 0; m < H / XT; ++m)
+                        if (!(got & (1u << m)) && (uint32_t) (v[m] >> 32) == ep) {
+                            yv[m] = bitsf((uint32_t) v[m]);
+                            got |= 1u << m;
+                        }
+                    if (got == all) break;
+                    if (++spins > XSPIN) {
+                        x_abort(a, 8);
+                        ok = false;
+                        break;
+                    }
+                    if ((spins & 255) == 0 && x_aborted(a)) {
+                        ok = false;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+            }
+            double s = 0.0;
+#pragma unroll
+            for (int m = 0; m < H / XT; ++m) {
+                s_y[tid + m * XT] = yv[m];
+                s += (double) (yv[m] * yv[m]);
+            }
+            for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+            if (lane == 0) s_red[wave] = s;
             if (!ok) s_fail = 1;
-            else if (tid < n) s_d8[tid] = bitsf(v);
         }
         lds_barrier();
         if (s_fail) return;
@@ -638,52 +886,19 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
         // descriptor of layer l + 2 takes its place
         if (next2) s_L[l & 1][tid] = lw;
         if (tid < 3 * E) s_slot[(l + 1) & 1][tid / E][tid % E] = sl_next;   // (in place of layer l - 1's)
-        if (tid < NH) {
-            // ggml_vec_dot_f32(k, experts^T row, w): k < 32 -> scalar tail: groups
-            // of four as mul + add, the remainder fused
-            float sumf = 0.0f;
-            const int nv = k & ~3;
-            for (int i = 0; i < k; ++i) {
-                const float d = s_d8[i * NH + tid];
-                sumf = (i < nv) ? sumf + d * s_w[i] : __builtin_fmaf(d, s_w[i], sumf);
-            }
-            st_local(a.xy + xcd * H + NH * j + tid, tag(sumf, ep), local);
-        }
-
-        // ---- Y: all y of this XCD -> RMSNorm -> x of the next layer ----------------
-        if (!gather<H / XT>(a, a.xy + xcd * H, H, ep, s_y, tid)) s_fail = 1;
-        lds_barrier();
-        if (s_fail) return;
-        {
-            double s = 0.0;
-            for (int i = tid; i < H; i += XT) {
-                const float v = s_y[i];
-                s += (double) (v * v);
-            }
-            for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
-            if (lane == 0) s_red[wave] = s;
-            lds_barrier();
-            double tot = 0.0;
-            for (int w = 0; w < XW; ++w) tot += s_red[w];
-            const float mean = (float) (tot / (double) H);
-            const float sc = 1.0f / sqrtf(mean + a.rms_eps);
-            for (int i = tid; i < H; i += XT) s_x[i] = s_y[i] * sc;
-            if (!nxt && b == 0) {
+        double tot = 0.0;
+#pragma unroll
+        for (int w = 0; w < XW; ++w) tot += s_red[w];
+        const float mean = (float) (tot / (double) H);
+        const float sc = 1.0f / sqrtf(mean + a.rms_eps);
+        if (!nxt) {
+            if (b == 0)
                 for (int i = tid; i < H; i += XT) {
                     a.out[i] = s_y[i];
-                    if (a.x_out) a.x_out[i] = s_x[i];
+                    if (a.x_out) a.x_out[i] = s_y[i] * sc;
                 }
-            }
-            lds_barrier();
-        }
-        if (nxt) {
-            quant_q8K_xb(s_x, NBH, s_xq, tid);
-            const int rw0 = XW - (NLOG + 1) / 2;
-            const int hw = 2 * (wave - rw0) + ((lane >> 5) & 1), c = lane & 31;
-            if (wave >= rw0 && hw < NLOG) {
-                const float lg = router_chain<H>(s_rw + hw * H, s_x, c);
-                if (c == 0) st_local(a.xl + xcd * E + NLOG * j + hw, tag(lg, ep + 1), local);
-            }
+        } else {
+            next_x(tid, sc, ep + 1);
         }
     }
 }
