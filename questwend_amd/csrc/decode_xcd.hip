@@ -96,6 +96,12 @@ __device__ __forceinline__ void x_abort(const XcdArgs& a, int bit) {
     __hip_atomic_store(a.abort_flag, (int32_t) a.epoch0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// A wave-uniform value moved to scalar registers.
+__device__ __forceinline__ uint32_t uni32(uint32_t v) { return (uint32_t) __builtin_amdgcn_readfirstlane((int) v); }
+__device__ __forceinline__ uint64_t uni64(uint64_t v) {
+    return ((uint64_t) uni32((uint32_t) (v >> 32)) << 32) | uni32((uint32_t) v);
+}
+
 // Wave-local LDS ordering: every LDS access of this wave issued before has
 // completed, and the compiler keeps memory accesses on their side.
 __device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
@@ -431,11 +437,13 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
     __shared__ __align__(16) float s_p[E];                      // logits
     __shared__ __align__(16) float s_pe[E];                     // the exact path's probabilities
     __shared__ __align__(16) int32_t s_order[E];
-    __shared__ int32_t s_slot[2][3][E];
+    __shared__ __align__(16) int4 s_slotx[2][E];              // {gate, up, down} slot of each expert
+    __shared__ __align__(16) int4 s_specx[8];                 // speculative expert of rank r and its slots
+    __shared__ __align__(16) int4 s_my;                       // this XCD's expert and its slots (wave 0)
+    __shared__ uint32_t s_topk_ep;                            // epoch of the layer whose s_my is posted
     __shared__ uint64_t s_L[2][XLW];
     __shared__ SortRange s_stack[SORT_STACK];
     __shared__ double s_red[XW];
-    __shared__ __align__(16) int32_t s_spec[8];
     __shared__ int s_fail, s_need_sort;
 
     const int b = blockIdx.x, tid0 = threadIdx.x;
@@ -471,7 +479,8 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
 
     // ---- prologue: descriptors, x of layer 0, router rows and slot rows of layer 0
     if (tid0 == 0) s_fail = 0;
-    if (tid0 < 8) s_spec[tid0] = 0;
+    if (tid0 < 8) s_specx[tid0] = int4{0, 0, 0, 0};
+    if (tid0 == 0) s_topk_ep = 0;
     if (tid0 < 2 * XLW && tid0 / XLW < a.n_layer) s_L[tid0 / XLW][tid0 % XLW] = ldg64((const uint64_t*) a.layers + tid0);
     for (int i = tid0; i < H; i += XT) s_y[i] = a.x_in[i];   // layer 0 takes x_in as it is (sc = 1)
     {
@@ -479,7 +488,7 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
         load_router(L0.router, tid0);
         for (int i = tid0; i < 3 * E; i += XT) {
             const int32_t* so = i < E ? L0.slot_gate : i < 2 * E ? L0.slot_up : L0.slot_down;
-            s_slot[0][i / E][i % E] = so ? ldg32(so + i % E) : i % E;
+            ((int32_t*) &s_slotx[0][i % E])[i / E] = so ? ldg32(so + i % E) : i % E;
         }
     }
     __syncthreads();
@@ -492,12 +501,33 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
         const int wave = tid >> 6, lane = tid & 63, g = lane >> 3, t = lane & 7;
 
         all_loads_returned();   // (the last were the y polls and the prefetches they follow)
+        // The layer's tensors (uniform) and this lane's row offsets: read once, while
+        // the logits are awaited.  Rows: gate/up pairs f = NP j + PPW wave + p (block
+        // g of each), down row NH j + RW wave + g.
+        const uint8_t* const Lgate = (const uint8_t*) uni64((uint64_t) L.gate);
+        const uint8_t* const Lup = (const uint8_t*) uni64((uint64_t) L.up);
+        const uint8_t* const Ldown = (const uint8_t*) uni64((uint64_t) L.down);
+        const uint32_t gnb1 = uni32((uint32_t) L.gate_nb1), unb1 = uni32((uint32_t) L.up_nb1);
+        const uint32_t dnb1 = uni32((uint32_t) L.down_nb1);
+        const uint64_t gnb2 = uni64(L.gate_nb2), unb2 = uni64(L.up_nb2), dnb2 = uni64(L.down_nb2);
+        const uint32_t nsg = uni32((uint32_t) min(L.n_slots_gate, (int64_t) INT32_MAX));
+        const uint32_t nsu = uni32((uint32_t) min(L.n_slots_up, (int64_t) INT32_MAX));
+        const uint32_t nsd = uni32((uint32_t) min(L.n_slots_down, (int64_t) INT32_MAX));
+        uint32_t og[PPW], ou[PPW];
+#pragma unroll
+        for (int p = 0; p < PPW; ++p) {
+            const uint32_t f = (uint32_t) (NP * j + PPW * wave + p);
+            og[p] = f * gnb1 + 144u * (uint32_t) g;
+            ou[p] = f * unb1 + 144u * (uint32_t) g;
+        }
+        const uint32_t od = (uint32_t) (NH * j + RW * wave + g) * dnb1;
+
         // ---- L: the layer's logits (all E, from this XCD's router workgroups) ------
         if (tid < E && !gather<1>(a, a.xl + xcd * E, E, ep, s_p, tid)) s_fail = 1;
         lds_barrier();
         if (s_fail) return;
         // logit ranks (strictly larger count; four lanes per value); the rank-c
-        // expert is XCD c's speculative expert, its gate/up rows are loaded at once
+        // expert is XCD c's speculative expert: {id, gate, up, down slots}
         {
             const int i = tid >> 2, sub = tid & 3;
             const float li = s_p[i < E ? i : 0];
@@ -511,7 +541,10 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
             rank += dpp_i<DPP_XOR2>(rank);
             if (i < E && sub == 0) {
                 s_order[i] = rank;
-                if (rank < k) s_spec[rank] = i;
+                if (rank < k) {
+                    const int4 sl = s_slotx[l & 1][i];
+                    s_specx[rank] = int4{i, sl.x, sl.y, sl.z};
+                }
             }
         }
         lds_barrier();
@@ -519,47 +552,41 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
         // ---- weight loads of this XCD's expert ------------------------------------
         u32x4 gh[2 * PPW], gq[2 * PPW];    // gate/up rows: header and chunk t of block g
         u32x4 dh[NBF], dq[NBF];            // down row 8 * wave + g: header and chunk t of each block
-        // gate/up rows: issued for the speculative expert (reissued if it was wrong);
-        // down rows: issued once the expert is certain (they are used after the act exchange)
-        auto issue = [&](int e) {
-            const int e_c = e < 0 || e >= E ? 0 : e;
-            int sg = s_slot[l & 1][0][e_c], su = s_slot[l & 1][1][e_c];
-            sg = (sg < 0 || sg >= L.n_slots_gate) ? 0 : sg;
-            su = (su < 0 || su >= L.n_slots_up) ? 0 : su;
+        // gate/up rows of the speculative expert are issued at once (and again if it
+        // was wrong); down rows once the expert is certain (used after the act exchange)
+        auto issue = [&](uint32_t sg, uint32_t su) {
+            sg = sg < nsg ? sg : 0u;   // (a slot out of range reads slot 0; reported below)
+            su = su < nsu ? su : 0u;
+            const uint8_t* bg = Lgate + (uint64_t) sg * gnb2;
+            const uint8_t* bu = Lup + (uint64_t) su * unb2;
 #pragma unroll
             for (int p = 0; p < PPW; ++p) {
-                const int f = NP * j + PPW * wave + p;
-                const uint8_t* rg = L.gate + (size_t) sg * L.gate_nb2 + (size_t) f * L.gate_nb1 + 144 * g;
-                const uint8_t* ru = L.up + (size_t) su * L.up_nb2 + (size_t) f * L.up_nb1 + 144 * g;
-                gh[2 * p] = ldg16(rg);
-                gq[2 * p] = ldg16(rg + 16 + 16 * t);
-                gh[2 * p + 1] = ldg16(ru);
-                gq[2 * p + 1] = ldg16(ru + 16 + 16 * t);
+                gh[2 * p] = ldg16(bg + og[p]);
+                gq[2 * p] = ldg16(bg + og[p] + 16 + 16 * t);
+                gh[2 * p + 1] = ldg16(bu + ou[p]);
+                gq[2 * p + 1] = ldg16(bu + ou[p] + 16 + 16 * t);
             }
         };
-        auto issue_down = [&](int e) {
-            const int e_c = e < 0 || e >= E ? 0 : e;
-            int sd = s_slot[l & 1][2][e_c];
-            sd = (sd < 0 || sd >= L.n_slots_down) ? 0 : sd;
-            const uint8_t* rd = L.down + (size_t) sd * L.down_nb2 + (size_t) (NH * j + RW * wave + g) * L.down_nb1;
+        auto issue_down = [&](uint32_t sd) {
+            sd = sd < nsd ? sd : 0u;
+            const uint8_t* rd = Ldown + (uint64_t) sd * dnb2 + od;
 #pragma unroll
             for (int bb = 0; bb < NBF; ++bb) {
                 dh[bb] = ldg16(rd + 144 * bb);
                 dq[bb] = ldg16(rd + 144 * bb + 16 + 16 * t);
             }
         };
-        const int spec_e = __builtin_amdgcn_readfirstlane(s_spec[expert_xcd ? xcd : 0]);
-        if (expert_xcd) issue(spec_e);
+        const int4 spec = s_specx[expert_xcd ? xcd : 0];
+        const int spec_e = __builtin_amdgcn_readfirstlane(spec.x);
+        if (expert_xcd) issue((uint32_t) __builtin_amdgcn_readfirstlane(spec.y), (uint32_t) __builtin_amdgcn_readfirstlane(spec.z));
 
-        // ---- softmax, top-k, weights: every wave on its own, in registers ------------
+        // ---- softmax, top-k, weights: wave 0, in registers; posted in LDS ----------
         // ggml_soft_max (ops.cpp:5455-5566): max, ggml_v_expf, sums of eight
         // (hsum_float_8) added in double, scale by 1 / sum.  Lane holds logits
-        // lane and lane + 64.
-        float pv[2];
-        int ids[8];
-        float pk[8], wk[8];
-        bool fast;
-        {
+        // lane and lane + 64.  Lane r < k ends with selected expert r and its weight.
+        int sel_id = 0;
+        float sel_w = 0.0f;
+        if (wave == 0) {
             float lv[2];
             int rk[2];
 #pragma unroll
@@ -569,7 +596,7 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
                 rk[m] = i < E ? s_order[i] : E;
             }
             const float mx = wave_max_uniform(fmaxf(lv[0], lv[1]));
-            float ev[2], gs[2];
+            float ev[2], gs[2], pv[2];
 #pragma unroll
             for (int m = 0; m < 2; ++m) {
                 ev[m] = lane + 64 * m < E ? v_expf(lv[m] - mx) : 0.0f;
@@ -589,158 +616,155 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
             // The speculative order is argsort's first k iff its probabilities
             // strictly decrease and every other probability is strictly below the
             // k-th (ties, rank collisions and NaN all fail this).
-            bool ok = true;
-            const int4 sp0 = *(const int4*) s_spec, sp1 = *(const int4*) (s_spec + 4);
-            const int spv[8] = {sp0.x, sp0.y, sp0.z, sp0.w, sp1.x, sp1.y, sp1.z, sp1.w};
-#pragma unroll
-            for (int r = 0; r < 8; ++r) {
-                ids[r] = r < k ? __builtin_amdgcn_readfirstlane(spv[r]) : 0;
-                pk[r] = r < k ? lane_value(pv, ids[r]) : 0.0f;
-                if (r > 0 && r < k) ok = ok && (pk[r - 1] > pk[r]);
+            sel_id = s_specx[lane & 7].x;
+            float pr;
+            {
+                const float pa = __shfl(pv[0], sel_id & 63), pb = __shfl(pv[1], sel_id & 63);
+                pr = sel_id < 64 ? pa : pb;
             }
-            float qk = pk[0];
-#pragma unroll
-            for (int r = 1; r < 8; ++r) qk = r == k - 1 ? pk[r] : qk;
-            bool bad_lane = false;
+            const float pprev = dpp_f<0x111>(pr);   // row_shr:1: lane r <- r - 1
+            bool bad = lane > 0 && lane < k && !(pprev > pr);
+            const float qk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pr), k - 1));
 #pragma unroll
             for (int m = 0; m < 2; ++m) {
                 const int i = lane + 64 * m;
-                int sp = -1;
-#pragma unroll
-                for (int r = 0; r < 8; ++r) sp = rk[m] == r ? ids[r] : sp;
+                const int sp = __shfl(sel_id, rk[m] < k ? rk[m] : 0);   // speculative expert of rank rk
                 const bool in_spec = rk[m] < k && sp == i;
-                if (i < E && !in_spec && !(pv[m] < qk)) bad_lane = true;
+                if (i < E && !in_spec && !(pv[m] < qk)) bad = true;
             }
-            fast = ok && !__any(bad_lane);
-        }
-        if (!fast) {
-            // exact order (every wave reached the same decision): rank the
-            // probabilities; a tie or NaN inside the first k places leaves the
-            // order to std::sort, which is replayed exactly
-            if (wave == 0) {
+            if (__any(bad)) {
+                // exact order: rank the probabilities; a tie or NaN inside the first
+                // k places leaves the order to std::sort, which is replayed exactly
                 if (lane < E) s_pe[lane] = pv[0];
                 if (lane + 64 < E) s_pe[lane + 64] = pv[1];
-            }
-            if (tid == 0) s_need_sort = 0;
-            lds_barrier();
-            for (int i = tid; i < E; i += XT) {
-                const float pi = s_pe[i];
-                int gt = 0, eq = 0;
-                for (int jj = 0; jj < E; jj += 4) {
-                    const float4 q = *(const float4*) (s_pe + jj);
-                    gt += (q.x > pi) + (q.y > pi) + (q.z > pi) + (q.w > pi);
-                    eq += (q.x == pi) + (q.y == pi) + (q.z == pi) + (q.w == pi);
+                wave_lds_sync();
+                bool tie = false;
+#pragma unroll 1
+                for (int m = 0; m < 2; ++m) {
+                    const int i = lane + 64 * m;
+                    const float pi = i < E ? pv[m] : 0.0f;
+                    int gt = 0, eq = 0;
+#pragma unroll 2
+                    for (int jj = 0; jj < E; jj += 4) {
+                        const float4 q = *(const float4*) (s_pe + jj);
+                        gt += (q.x > pi) + (q.y > pi) + (q.z > pi) + (q.w > pi);
+                        eq += (q.x == pi) + (q.y == pi) + (q.z == pi) + (q.w == pi);
+                    }
+                    if (i < E && gt < k) {
+                        if (eq != 1) tie = true;
+                        else s_order[gt] = i;
+                    }
                 }
-                if (gt < k) {
-                    if (eq != 1) s_need_sort = 1;
-                    else s_order[gt] = i;
+                if (__any(tie)) {
+                    wave_lds_sync();
+                    for (int i = lane; i < E; i += 64) s_order[i] = i;
+                    wave_lds_sync();
+                    if (lane == 0) {
+                        sort_desc_replay(s_order, E, s_pe, s_stack);
+                        if (b == 0) atomicOr(a.status, 1);
+                    }
                 }
+                wave_lds_sync();
+                sel_id = s_order[lane & 7];
+                const float pa = __shfl(pv[0], sel_id & 63), pb = __shfl(pv[1], sel_id & 63);
+                pr = sel_id < 64 ? pa : pb;
             }
-            lds_barrier();
-            if (s_need_sort) {
-                for (int i = tid; i < E; i += XT) s_order[i] = i;
-                lds_barrier();
-                if (tid == 0) {
-                    sort_desc_replay(s_order, E, s_pe, s_stack);
-                    if (b == 0) atomicOr(a.status, 1);
-                }
-            }
-            lds_barrier();
-            const int4 so0 = *(const int4*) s_order, so1 = *(const int4*) (s_order + 4);
-            const int sov[8] = {so0.x, so0.y, so0.z, so0.w, so1.x, so1.y, so1.z, so1.w};
-#pragma unroll
-            for (int r = 0; r < 8; ++r) {
-                ids[r] = r < k ? __builtin_amdgcn_readfirstlane(sov[r]) : 0;
-                pk[r] = r < k ? lane_value(pv, ids[r]) : 0.0f;
-            }
-        }
-        // weights: selected probabilities / clamp(sum) (* scale), core/runtime.cpp:887-897
-        {
+            // weights: selected probabilities / clamp(sum) (* scale), core/runtime.cpp:887-897
             double sp = 0.0;
 #pragma unroll
             for (int r = 0; r < 8; ++r)
-                if (r < k) sp += (double) pk[r];
+                if (r < k) sp += (double) __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pr), r));
             float wsum = (float) sp;
             wsum = fmaxf(fminf(wsum, INFINITY), 6.103515625e-5f);
-#pragma unroll
-            for (int r = 0; r < 8; ++r) {
-                float wi = pk[r] / wsum;
-                if (a.scale != 0.0f && a.scale != 1.0f) wi = wi * a.scale;
-                wk[r] = wi;
+            sel_w = pr / wsum;
+            if (a.scale != 0.0f && a.scale != 1.0f) sel_w = sel_w * a.scale;
+            // this XCD's expert and its slots, for the other waves
+            const int my_e = __builtin_amdgcn_readlane(sel_id, expert_xcd ? xcd : 0);
+            if (lane == 0) {
+                const int4 sl = s_slotx[l & 1][my_e];
+                s_my = int4{my_e, sl.x, sl.y, sl.z};
             }
+            if (lane < k) {
+                if (b == 0 && a.ids_out) {
+                    a.ids_out[l * k + lane] = sel_id;
+                    a.w_out[l * k + lane] = sel_w;
+                }
+                // slot checks of the selected experts (reported once, by workgroup 0)
+                if (b == 0) {
+                    const int4 sl = s_slotx[l & 1][sel_id];
+                    if ((uint32_t) sl.x >= nsg || (uint32_t) sl.y >= nsu || (uint32_t) sl.z >= nsd)
+                        atomicOr(a.status, 16);
+                }
+            }
+            wave_lds_sync();
+            if (lane == 0) __hip_atomic_store(&s_topk_ep, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);   // posted after the values above
         }
-        int my_e = ids[0];
-#pragma unroll
-        for (int r = 1; r < 8; ++r) my_e = r == xcd ? ids[r] : my_e;
-        if (wave == 0 && lane < k) {
-            int id = ids[0];
-            float wi = wk[0];
-#pragma unroll
-            for (int r = 1; r < 8; ++r) {
-                id = lane == r ? ids[r] : id;
-                wi = lane == r ? wk[r] : wi;
-            }
-            if (b == 0 && a.ids_out) {
-                a.ids_out[l * k + lane] = id;
-                a.w_out[l * k + lane] = wi;
-            }
-            // slot checks of the selected experts (reported once, by workgroup 0)
-            if (b == 0) {
-                const int sg = s_slot[l & 1][0][id], su = s_slot[l & 1][1][id], sd = s_slot[l & 1][2][id];
-                if (sg < 0 || sg >= L.n_slots_gate || su < 0 || su >= L.n_slots_up || sd < 0 ||
-                    sd >= L.n_slots_down)
-                    atomicOr(a.status, 16);
-            }
-        }
-        if (expert_xcd && my_e != spec_e) issue(my_e);   // misspeculated: load the right rows
-        if (expert_xcd) issue_down(my_e);
 
         // ---- A: gate/up rows of this workgroup's pairs, SwiGLU -----------------
         if (expert_xcd) {
+            int e_cur = spec_e;
+            int4 my;
+            float res, up;
+            for (;;) {
 #pragma unroll
-            for (int r = 0; r < 2 * PPW; ++r) {
-                int p[4];
-                const uint8_t* yb = s_xq + QB * g;
-                const Q4KLane w = q4k_lane(gh[r], gq[r], t);
-                q4k_dot(w, yb, t, p);
-                reduce_chunks(p);
-                const int pm = q4k_min_dot(w, yb, t);
-                uint32_t* rec = s_tr[wave][r][g];
-                if (t < 2) *(u32x4*) (rec + 4 * t) = u32x4{(uint32_t) p[0], (uint32_t) p[1], (uint32_t) p[2], (uint32_t) p[3]};
-                if (t < 4) rec[8 + t] = (uint32_t) pm;
-                if (t == 0) *(uint2*) (rec + 12) = uint2{fbits(w.d), fbits(w.dmin)};
-            }
-            wave_lds_sync();
-            // chain lanes: row r = lane >> 3 (< 2 * PPW), AVX lane n = lane & 7
-            float res;
-            {
-                const int r = g < 2 * PPW ? g : 0, n = t;
-                float acc = 0.0f, accm = 0.0f;
-#pragma unroll
-                for (int bb = 0; bb < NBH; ++bb) {
-                    const uint32_t* rec = s_tr[wave][r][bb];
-                    const int S = (int) rec[n];
-                    const int pm = (int) rec[8 + (n & 3)];
-                    const float wd = bitsf(rec[12]), wdm = bitsf(rec[13]);
-                    const float yd = *(const float*) (s_xq + QB * bb + 256);
-                    acc = __builtin_fmaf(yd * wd, (float) S, acc);
-                    const float pmv = __builtin_fmaf(-yd * wdm, (float) pm, accm);
-                    accm = n < 4 ? pmv : accm;
+                for (int r = 0; r < 2 * PPW; ++r) {
+                    int p[4];
+                    const uint8_t* yb = s_xq + QB * g;
+                    const Q4KLane w = q4k_lane(gh[r], gq[r], t);
+                    q4k_dot(w, yb, t, p);
+                    reduce_chunks(p);
+                    const int pm = q4k_min_dot(w, yb, t);
+                    uint32_t* rec = s_tr[wave][r][g];
+                    if (t < 2) *(u32x4*) (rec + 4 * t) = u32x4{(uint32_t) p[0], (uint32_t) p[1], (uint32_t) p[2], (uint32_t) p[3]};
+                    if (t < 4) rec[8 + t] = (uint32_t) pm;
+                    if (t == 0) *(uint2*) (rec + 12) = uint2{fbits(w.d), fbits(w.dmin)};
                 }
-                float s = acc;
-                s = s + __shfl_down(s, 4, 8);
-                s = s + __shfl_down(s, 2, 8);
-                s = s + __shfl_down(s, 1, 8);
-                float m = accm;
-                m = m + __shfl_down(m, 2, 8);
-                m = m + __shfl_down(m, 1, 8);
-                res = s + m;
+                wave_lds_sync();
+                // chain lanes: row r = lane >> 3 (< 2 * PPW), AVX lane n = lane & 7
+                {
+                    const int r = g < 2 * PPW ? g : 0, n = t;
+                    float acc = 0.0f, accm = 0.0f;
+#pragma unroll
+                    for (int bb = 0; bb < NBH; ++bb) {
+                        const uint32_t* rec = s_tr[wave][r][bb];
+                        const int S = (int) rec[n];
+                        const int pm = (int) rec[8 + (n & 3)];
+                        const float wd = bitsf(rec[12]), wdm = bitsf(rec[13]);
+                        const float yd = *(const float*) (s_xq + QB * bb + 256);
+                        acc = __builtin_fmaf(yd * wd, (float) S, acc);
+                        const float pmv = __builtin_fmaf(-yd * wdm, (float) pm, accm);
+                        accm = n < 4 ? pmv : accm;
+                    }
+                    float s2 = acc;
+                    s2 = s2 + __shfl_down(s2, 4, 8);
+                    s2 = s2 + __shfl_down(s2, 2, 8);
+                    s2 = s2 + __shfl_down(s2, 1, 8);
+                    float m = accm;
+                    m = m + __shfl_down(m, 2, 8);
+                    m = m + __shfl_down(m, 1, 8);
+                    res = s2 + m;
+                }
+                up = __shfl_down(res, 8);   // lane 16p: gate of pair p; lane 16p + 8: its up
+                // the exact expert of this XCD (posted by wave 0)
+                long spins = 0;
+                while (__hip_atomic_load(&s_topk_ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != ep) {
+                    if (++spins > XSPIN) {
+                        x_abort(a, 8);
+                        return;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+                my = s_my;
+                if (__builtin_amdgcn_readfirstlane(my.x) == e_cur) break;
+                // misspeculated: load the right rows and compute again
+                e_cur = __builtin_amdgcn_readfirstlane(my.x);
+                issue((uint32_t) __builtin_amdgcn_readfirstlane(my.y), (uint32_t) __builtin_amdgcn_readfirstlane(my.z));
             }
-            const float up = __shfl_down(res, 8);   // lane 16p: gate of pair p; lane 16p + 8: its up
             if ((lane & 15) == 0 && (lane >> 4) < PPW) {
                 const int f = NP * j + PPW * wave + (lane >> 4);
                 st_local(a.xa + xcd * F + f, tag(v_silu(res) * up, ep), local);
             }
+            issue_down((uint32_t) __builtin_amdgcn_readfirstlane(my.w));
         }
         // next layer's slot rows and the descriptor of layer l + 2: issued once the
         // gate/up rows are consumed, stored to LDS after the y exchange
@@ -833,7 +857,10 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
                 const int nv = k & ~3;
 #pragma unroll
                 for (int c = 0; c < 8; ++c)
-                    if (c < k) sumf = (c < nv) ? sumf + dv[c] * wk[c] : __builtin_fmaf(dv[c], wk[c], sumf);
+                    if (c < k) {
+                        const float wc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sel_w), c));
+                        sumf = (c < nv) ? sumf + dv[c] * wc : __builtin_fmaf(dv[c], wc, sumf);
+                    }
                 st_local(a.xy + xcd * H + NH * j + lane, tag(sumf, ep), local);
             }
         }
@@ -885,7 +912,7 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
         // every thread is past its last read of layer l's descriptor: the
         // descriptor of layer l + 2 takes its place
         if (next2) s_L[l & 1][tid] = lw;
-        if (tid < 3 * E) s_slot[(l + 1) & 1][tid / E][tid % E] = sl_next;   // (in place of layer l - 1's)
+        if (tid < 3 * E) ((int32_t*) &s_slotx[(l + 1) & 1][tid % E])[tid / E] = sl_next;   // (in place of layer l - 1's)
         double tot = 0.0;
 #pragma unroll
         for (int w = 0; w < XW; ++w) tot += s_red[w];
