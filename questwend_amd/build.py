@@ -26,7 +26,11 @@ SOURCES = ["quantize.hip", "router.hip", "mmid.hip", "mmid_mfma.hip", "ffn.hip",
 
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Wall", "-Wno-unused-function",
           "-Wno-unused-variable", "-Wno-unused-but-set-variable"]
-DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# v_dot4c_i32_i8 (dot6-insts) ties its accumulator to the destination, which
+# costs a v_mov of 0 before every dot product that starts a sum; without it the
+# compiler emits the VOP3P v_dot4_i32_i8 with an inline 0.
+DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          "-Xclang", "-target-feature", "-Xclang", "-dot6-insts"]
 
 
 def hipcc() -> str:

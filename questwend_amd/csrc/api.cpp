@@ -541,8 +541,8 @@ int qwmoe_decode_stack_create(const qwmoe_layer* layers, int n_layer, float rms_
     }
     if (d.use_xcd) {
         // XCD-local exchange words may be stored with workgroup scope only when
-        // workgroup b of the launch runs on XCD b % 8 (QWMOE_DECODE_XCD_LOCAL=0:
-        // never); the kernel also flags a workgroup found elsewhere (status 64)
+        // the launch's workgroups are dealt to the XCDs round robin (each XCD
+        // then holds one workgroup of every role; QWMOE_DECODE_XCD_LOCAL=0: never)
         const char* le = getenv("QWMOE_DECODE_XCD_LOCAL");
         int ok = 0;
         if (qw::probe_xcd_mapping((int32_t*) ((uint8_t*) blk + off_xd), d.grid, nullptr, &ok) != 0) {

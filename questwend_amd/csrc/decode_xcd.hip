@@ -305,8 +305,11 @@ __device__ __forceinline__ uint32_t q4k_min_word(uint32_t s1, uint32_t s2, bool 
 }
 
 // The weight side of one Q4_K super-block for lane t (0..7) of its 8-lane
-// group: hdr = bytes 0..15 (d, dmin, scales), qc = quant bytes 16t..16t+15,
-// i.e. 64-element chunk j = t >> 1 and AVX lanes n = 4 (t & 1) + i.
+// group: hdr = bytes 0..15 (d, dmin, scales), qc = the 16 quant bytes of
+// 64-element chunk j = t & 3, half hb = t >> 2 (AVX lanes n = 4 hb + i), at
+// block offset q4k_chunk(t).  Lanes t, t ^ 1, t ^ 2, t ^ 3 hold the four
+// chunks of one half, so their sum is two quad_perm steps.
+__device__ __forceinline__ uint32_t q4k_chunk(int t) { return 16u + 16u * (uint32_t) (2 * (t & 3) + (t >> 2)); }
 struct Q4KLane {
     uint32_t lo[4], hi[4];   // the nibbles of qc as bytes (sub-blocks 2j and 2j + 1)
     int scl, sch;            // their scales
@@ -315,7 +318,7 @@ struct Q4KLane {
 };
 __device__ __forceinline__ Q4KLane q4k_lane(const u32x4& hdr, const u32x4& qc, int t) {
     Q4KLane w;
-    const int j = t >> 1, n = t & 3;
+    const int j = t & 3, n = t & 3;
     const uint32_t scw = q4k_scale_word(hdr[1], hdr[3], j >= 2);
     const int sh = 16 * (j & 1);
     w.scl = (int) __builtin_amdgcn_ubfe(scw, sh, 8);
@@ -337,7 +340,7 @@ __device__ __forceinline__ Q4KLane q4k_lane(const u32x4& hdr, const u32x4& qc, i
 // p[i] = sc_{2j} . sum(q4lo . q8) + sc_{2j+1} . sum(q4hi . q8) over AVX lane n's
 // four bytes (the maddubs + madd of quants.c:2092-2100).
 __device__ __forceinline__ void q4k_dot(const Q4KLane& w, const uint8_t* yq, int t, int p[4]) {
-    const int j = t >> 1, hb = t & 1;
+    const int j = t & 3, hb = t >> 2;
     const u32x4 alo = *(const u32x4*) (yq + 64 * j + 16 * hb);
     const u32x4 ahi = *(const u32x4*) (yq + 64 * j + 32 + 16 * hb);
 #pragma unroll
@@ -356,13 +359,17 @@ __device__ __forceinline__ int q4k_min_dot(const Q4KLane& w, const uint8_t* yb, 
     return mul24(w.m0, q8s0) + mul24(w.m1, q8s1);
 }
 
-// Sum over the four 64-element chunks: lanes t and t ^ 2 (quad_perm), then t
-// and t + 4 (row_shl:4).  Valid in lanes t = 0 (AVX lanes 0..3) and t = 1 (4..7).
+// Sum over the four 64-element chunks: lanes t ^ 1, then t ^ 2 (quad_perm; the
+// sums are exact integers).  Every lane of a half ends with the sums of its AVX
+// lanes 4 hb .. 4 hb + 3.
 __device__ __forceinline__ void reduce_chunks(int p[4]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int a = p[i] + dpp_i<DPP_XOR2>(p[i]);
-        p[i] = a + __builtin_amdgcn_update_dpp(0, a, 0x104, 0xF, 0xF, true);   // row_shl:4: lane i <- i + 4 (0 past the row)
+        const int a = p[i] + dpp_i<DPP_XOR1>(p[i]);
+        p[i] = a + dpp_i<DPP_XOR2>(a);
+        // materialised here: an add sunk into a lane-conditional store would
+        // keep its DPP operand as a separate v_mov_dpp
+        asm volatile("" : "+v"(p[i]));
     }
 }
 
@@ -439,6 +446,7 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
     __shared__ __align__(16) int32_t s_order[E];
     __shared__ __align__(16) int4 s_slotx[2][E];              // {gate, up, down} slot of each expert
     __shared__ __align__(16) int4 s_specx[8];                 // speculative expert of rank r and its slots
+    __shared__ float s_specl[9];                              // logit of rank r <= k
     __shared__ __align__(16) int4 s_my;                       // this XCD's expert and its slots (wave 0)
     __shared__ uint32_t s_topk_ep;                            // epoch of the layer whose s_my is posted
     __shared__ uint64_t s_L[2][XLW];
@@ -447,12 +455,15 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
     __shared__ int s_fail, s_need_sort;
 
     const int b = blockIdx.x, tid0 = threadIdx.x;
-    const int xcd = b & (NXCD - 1), j = b >> 3;
+    // Roles: the XCD this workgroup runs on (XCC_ID) and j = b / 8.  The
+    // dispatcher deals workgroups to the XCDs round robin, starting where the
+    // previous dispatch left off, so XCD (b + r) % 8 for one rotation r per
+    // launch: every XCD holds exactly one workgroup of each j.
+    const int xcd = (int) (__builtin_amdgcn_s_getreg((3 << 11) | 20) & (NXCD - 1)), j = b >> 3;
     const int k = a.k;
     const bool expert_xcd = xcd < k;
     const int local = a.local_st;
 
-    if ((int) (__builtin_amdgcn_s_getreg((3 << 11) | 20) & 7) != xcd && tid0 == 0) atomicOr(a.status, 64);
 
     // The end of a layer (and the prologue): the next layer's router logits from
     // x = y * sc (router waves) and Q8_K(x) (waves QXW..QXW + QXN - 1).
@@ -541,6 +552,7 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
             rank += dpp_i<DPP_XOR2>(rank);
             if (i < E && sub == 0) {
                 s_order[i] = rank;
+                if (rank <= k) s_specl[rank] = li;   // (rank k: any of equal values)
                 if (rank < k) {
                     const int4 sl = s_slotx[l & 1][i];
                     s_specx[rank] = int4{i, sl.x, sl.y, sl.z};
@@ -562,9 +574,9 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
 #pragma unroll
             for (int p = 0; p < PPW; ++p) {
                 gh[2 * p] = ldg16(bg + og[p]);
-                gq[2 * p] = ldg16(bg + og[p] + 16 + 16 * t);
+                gq[2 * p] = ldg16(bg + og[p] + q4k_chunk(t));
                 gh[2 * p + 1] = ldg16(bu + ou[p]);
-                gq[2 * p + 1] = ldg16(bu + ou[p] + 16 + 16 * t);
+                gq[2 * p + 1] = ldg16(bu + ou[p] + q4k_chunk(t));
             }
         };
         auto issue_down = [&](uint32_t sd) {
@@ -573,30 +585,23 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
 #pragma unroll
             for (int bb = 0; bb < NBF; ++bb) {
                 dh[bb] = ldg16(rd + 144 * bb);
-                dq[bb] = ldg16(rd + 144 * bb + 16 + 16 * t);
+                dq[bb] = ldg16(rd + 144 * bb + q4k_chunk(t));
             }
         };
         const int4 spec = s_specx[expert_xcd ? xcd : 0];
         const int spec_e = __builtin_amdgcn_readfirstlane(spec.x);
         if (expert_xcd) issue((uint32_t) __builtin_amdgcn_readfirstlane(spec.y), (uint32_t) __builtin_amdgcn_readfirstlane(spec.z));
 
-        // ---- softmax, top-k, weights: wave 0, in registers; posted in LDS ----------
+        // ---- top-k: wave 0, posted in LDS; the weights follow later ---------------
         // ggml_soft_max (ops.cpp:5455-5566): max, ggml_v_expf, sums of eight
         // (hsum_float_8) added in double, scale by 1 / sum.  Lane holds logits
-        // lane and lane + 64.  Lane r < k ends with selected expert r and its weight.
-        int sel_id = 0;
-        float sel_w = 0.0f;
-        if (wave == 0) {
+        // lane and lane + 64.
+        auto probs = [&](float (&pv)[2]) {
             float lv[2];
-            int rk[2];
 #pragma unroll
-            for (int m = 0; m < 2; ++m) {
-                const int i = lane + 64 * m;
-                lv[m] = i < E ? s_p[i] : -INFINITY;
-                rk[m] = i < E ? s_order[i] : E;
-            }
+            for (int m = 0; m < 2; ++m) lv[m] = lane + 64 * m < E ? s_p[lane + 64 * m] : -INFINITY;
             const float mx = wave_max_uniform(fmaxf(lv[0], lv[1]));
-            float ev[2], gs[2], pv[2];
+            float ev[2], gs[2];
 #pragma unroll
             for (int m = 0; m < 2; ++m) {
                 ev[m] = lane + 64 * m < E ? v_expf(lv[m] - mx) : 0.0f;
@@ -613,28 +618,39 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
             const float inv = (float) (1.0 / sum);
             pv[0] = ev[0] * inv;
             pv[1] = ev[1] * inv;
-            // The speculative order is argsort's first k iff its probabilities
-            // strictly decrease and every other probability is strictly below the
-            // k-th (ties, rank collisions and NaN all fail this).
-            sel_id = s_specx[lane & 7].x;
-            float pr;
-            {
-                const float pa = __shfl(pv[0], sel_id & 63), pb = __shfl(pv[1], sel_id & 63);
-                pr = sel_id < 64 ? pa : pb;
-            }
-            const float pprev = dpp_f<0x111>(pr);   // row_shr:1: lane r <- r - 1
-            bool bad = lane > 0 && lane < k && !(pprev > pr);
-            const float qk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pr), k - 1));
+        };
+        // Lane r < k ends with selected expert r (and, after the gate/up rows, its weight).
+        int sel_id = 0;
+        float sel_w = 0.0f;
+        if (wave == 0) {
+            // The speculative order (logit ranks) is argsort's first k when
+            //  (1) ranks 0..k-1 are held once each (no equal or NaN logit there), and
+            //  (2) e_r = v_expf(l_r - l_0) of ranks r = 0..k satisfy e_r > e_{r+1} (1 + 2^-20)
+            //      for r < k, and e_{k-1} >= 2^-100.
+            // v_expf is non-decreasing on (-inf, 0] (checked over every float), and so
+            // is rounding e * inv for the softmax's inv in [1/E, 1]: every other
+            // probability is at most p_k, and a ratio above 1 + 2^-21 survives the
+            // rounding of e * inv, so p_0 > ... > p_{k-1} > every other p.
+            int rk[2];
 #pragma unroll
-            for (int m = 0; m < 2; ++m) {
-                const int i = lane + 64 * m;
-                const int sp = __shfl(sel_id, rk[m] < k ? rk[m] : 0);   // speculative expert of rank rk
-                const bool in_spec = rk[m] < k && sp == i;
-                if (i < E && !in_spec && !(pv[m] < qk)) bad = true;
-            }
-            if (__any(bad)) {
+            for (int m = 0; m < 2; ++m) rk[m] = lane + 64 * m < E ? s_order[lane + 64 * m] : E;
+            const float lr = s_specl[lane <= k ? lane : 0];
+            bool ok = __popcll(__ballot(rk[0] < k)) + __popcll(__ballot(rk[1] < k)) == k;
+#pragma unroll
+            for (int r = 0; r < 8; ++r)
+                if (r < k) ok = ok && __ballot(rk[0] == r || rk[1] == r) != 0;
+            const float er = v_expf(lr - __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lr), 0)));
+            const float en = dpp_f<0x101>(er);   // row_shl:1: lane r <- r + 1 (r <= 8)
+            bool bad = lane < k && !(er > en * 0x1.00001p+0f);
+            if (lane == k - 1 && !(er >= 0x1p-100f)) bad = true;
+            ok = ok && !__any(bad);
+            if (ok) {
+                sel_id = s_specx[lane & 7].x;
+            } else {
                 // exact order: rank the probabilities; a tie or NaN inside the first
                 // k places leaves the order to std::sort, which is replayed exactly
+                float pv[2];
+                probs(pv);
                 if (lane < E) s_pe[lane] = pv[0];
                 if (lane + 64 < E) s_pe[lane + 64] = pv[1];
                 wave_lds_sync();
@@ -666,35 +682,12 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
                 }
                 wave_lds_sync();
                 sel_id = s_order[lane & 7];
-                const float pa = __shfl(pv[0], sel_id & 63), pb = __shfl(pv[1], sel_id & 63);
-                pr = sel_id < 64 ? pa : pb;
             }
-            // weights: selected probabilities / clamp(sum) (* scale), core/runtime.cpp:887-897
-            double sp = 0.0;
-#pragma unroll
-            for (int r = 0; r < 8; ++r)
-                if (r < k) sp += (double) __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pr), r));
-            float wsum = (float) sp;
-            wsum = fmaxf(fminf(wsum, INFINITY), 6.103515625e-5f);
-            sel_w = pr / wsum;
-            if (a.scale != 0.0f && a.scale != 1.0f) sel_w = sel_w * a.scale;
             // this XCD's expert and its slots, for the other waves
             const int my_e = __builtin_amdgcn_readlane(sel_id, expert_xcd ? xcd : 0);
             if (lane == 0) {
                 const int4 sl = s_slotx[l & 1][my_e];
                 s_my = int4{my_e, sl.x, sl.y, sl.z};
-            }
-            if (lane < k) {
-                if (b == 0 && a.ids_out) {
-                    a.ids_out[l * k + lane] = sel_id;
-                    a.w_out[l * k + lane] = sel_w;
-                }
-                // slot checks of the selected experts (reported once, by workgroup 0)
-                if (b == 0) {
-                    const int4 sl = s_slotx[l & 1][sel_id];
-                    if ((uint32_t) sl.x >= nsg || (uint32_t) sl.y >= nsu || (uint32_t) sl.z >= nsd)
-                        atomicOr(a.status, 16);
-                }
             }
             wave_lds_sync();
             if (lane == 0) __hip_atomic_store(&s_topk_ep, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);   // posted after the values above
@@ -715,7 +708,7 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
                     reduce_chunks(p);
                     const int pm = q4k_min_dot(w, yb, t);
                     uint32_t* rec = s_tr[wave][r][g];
-                    if (t < 2) *(u32x4*) (rec + 4 * t) = u32x4{(uint32_t) p[0], (uint32_t) p[1], (uint32_t) p[2], (uint32_t) p[3]};
+                    if ((t & 3) == 0) *(u32x4*) (rec + t) = u32x4{(uint32_t) p[0], (uint32_t) p[1], (uint32_t) p[2], (uint32_t) p[3]};
                     if (t < 4) rec[8 + t] = (uint32_t) pm;
                     if (t == 0) *(uint2*) (rec + 12) = uint2{fbits(w.d), fbits(w.dmin)};
                 }
@@ -766,6 +759,31 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
             }
             issue_down((uint32_t) __builtin_amdgcn_readfirstlane(my.w));
         }
+        // ---- weights of the selected experts (wave 0; used by the y sum) -----------
+        // selected probabilities / clamp(sum) (* scale), core/runtime.cpp:887-897
+        if (wave == 0) {
+            float pv[2];
+            probs(pv);
+            const float pa = __shfl(pv[0], sel_id & 63), pb = __shfl(pv[1], sel_id & 63);
+            const float pr = sel_id < 64 ? pa : pb;
+            double sp = 0.0;
+#pragma unroll
+            for (int r = 0; r < 8; ++r)
+                if (r < k) sp += (double) __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pr), r));
+            float wsum = (float) sp;
+            wsum = fmaxf(fminf(wsum, INFINITY), 6.103515625e-5f);
+            sel_w = pr / wsum;
+            if (a.scale != 0.0f && a.scale != 1.0f) sel_w = sel_w * a.scale;
+            if (lane < k && b == 0) {
+                if (a.ids_out) {
+                    a.ids_out[l * k + lane] = sel_id;
+                    a.w_out[l * k + lane] = sel_w;
+                }
+                // slot checks of the selected experts (reported once, by workgroup 0)
+                const int4 sl = s_slotx[l & 1][sel_id];
+                if ((uint32_t) sl.x >= nsg || (uint32_t) sl.y >= nsu || (uint32_t) sl.z >= nsd) atomicOr(a.status, 16);
+            }
+        }
         // next layer's slot rows and the descriptor of layer l + 2: issued once the
         // gate/up rows are consumed, stored to LDS after the y exchange
         const bool nxt = l + 1 < a.n_layer;
@@ -809,10 +827,10 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
                 const int pm = q4k_min_dot(dw[bb], yb, t);
                 accm = __builtin_fmaf(-yd * dw[bb].dmin, (float) pm, accm);
             }
-            // hsum_float_8: lane t = 0 holds AVX lanes 0..3, lane t = 1 lanes 4..7
+            // hsum_float_8: lane t = 0 holds AVX lanes 0..3, lane t = 4 lanes 4..7
             float r4[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) r4[i] = acc[i] + dpp_f<DPP_XOR1>(acc[i]);
+            for (int i = 0; i < 4; ++i) r4[i] = acc[i] + dpp_f<0x12C>(acc[i]);   // row_ror:12: lane i <- (i + 4) mod 16
             const float hs = (r4[0] + r4[2]) + (r4[1] + r4[3]);
             // min lanes 0..3: (m0 + m2) + (m1 + m3)
             const float m2 = accm + dpp_f<DPP_XOR2>(accm);
@@ -978,7 +996,8 @@ int launch_decode_xcd(const DecodeStackDesc& d, const float* x_in, float* out, f
 }
 
 // Records each workgroup's XCD id: used once at create time to check that
-// workgroup b of a 256-workgroup launch runs on XCD b % 8.
+// the workgroups of a 256-workgroup launch are dealt to the XCDs round robin
+// (XCD (b + r) % 8 for one r).
 __global__ void k_xcd_probe(int32_t* out) {
     if (threadIdx.x == 0) out[blockIdx.x] = (int32_t) (__builtin_amdgcn_s_getreg((3 << 11) | 20) & 0xf);
 }
@@ -991,9 +1010,9 @@ int probe_xcd_mapping(int32_t* dev_buf, int n, hipStream_t stream, int* ok) {
     if (hipMemcpyAsync(h.data(), dev_buf, sizeof(int32_t) * (size_t) n, hipMemcpyDeviceToHost, stream) != hipSuccess ||
         hipStreamSynchronize(stream) != hipSuccess)
         return -3;
-    int good = 1;
+    int good = n > 0;
     for (int i = 0; i < n; ++i)
-        if (h[(size_t) i] != i % NXCD) good = 0;
+        if (h[(size_t) i] < 0 || h[(size_t) i] >= NXCD || (h[(size_t) i] - i - h[0]) % NXCD != 0) good = 0;
     *ok = good;
     return 0;
 }

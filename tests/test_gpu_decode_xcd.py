@@ -159,3 +159,26 @@ def test_xcd_kernel_equals_other_kernels():
     for s in (s1, s2, s3):
         assert s.status() & ~1 == 0
         s.close()
+
+
+def test_xcd_kernel_after_odd_sized_launches():
+    """The dispatcher deals workgroups to the XCDs round robin from where the
+    previous dispatch stopped, so one-workgroup launches before the stack shift
+    which XCD workgroup 0 lands on.  Every shift: the same bits as the per-CU
+    kernel and no status bit beyond the tie replay."""
+    note("XCD kernel after 0..7 one-workgroup launches: 2 layers 30B shape vs per-CU kernel")
+    layers = [GpuLayer(H, 128, 8, F, (Q4_K,) * 3, seed=920 + i) for i in range(2)]
+    s2 = make_stack(layers)
+    s1 = make_stack(layers, {"QWMOE_DECODE_XCD": "0"})
+    assert (s2.kernel(), s1.kernel()) == (2, 1)
+    x = torch.empty(H, dtype=torch.float32, device=DEV)
+    ops.randn_(x, 77, 0.0, 1.0)
+    ref = run_tokens(s1, [x])
+    pad = torch.empty(255, dtype=torch.float32, device=DEV)   # one workgroup of k_randn
+    for r in range(8):
+        for i in range(r):
+            ops.randn_(pad, 100 + i, 0.0, 1.0)
+        same_bits(ref, run_tokens(s2, [x]))
+        assert s2.status() & ~1 == 0, f"shift {r}: status {s2.status()}"
+    s1.close()
+    s2.close()
