@@ -778,6 +778,25 @@ float orc_vec_dot_f32(int n, const float * x, const float * y, int tail_mode) {
     return vec_dot_f32(n, x, y, tail_mode);
 }
 float orc_v_expf(float x) { return v_expf(x); }
+// Number of steps down the float line where v_expf increases: x runs over the
+// bit patterns first..last (negative floats, so x decreases as the pattern
+// grows) and a step counts when v_expf(next) > v_expf(previous).  A property
+// of the restatement (bit-identical to ggml_v_expf), used by the tests that
+// support the GPU router's shortcut: a larger logit never gets a smaller exp.
+int64_t orc_v_expf_increases(uint32_t first, uint32_t last) {
+    int64_t bad = 0;
+    float x;
+    std::memcpy(&x, &first, 4);
+    float prev = v_expf(x);
+    for (uint32_t b = first; b != last;) {
+        ++b;
+        std::memcpy(&x, &b, 4);
+        const float y = v_expf(x);
+        if (y > prev) ++bad;
+        prev = y;
+    }
+    return bad;
+}
 void orc_swiglu(int64_t n, const float * gate, const float * up, float * out) { vec_swiglu((int) n, out, gate, up); }
 void orc_soft_max(int64_t ne0, int64_t ne1, const float * x, float * y) {
     for (int64_t r = 0; r < ne1; ++r) soft_max_row((int) ne0, x + r * ne0, y + r * ne0);

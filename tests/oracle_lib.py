@@ -56,6 +56,8 @@ class Oracle:
         L.orc_vec_dot_f32.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int]
         L.orc_v_expf.restype = C.c_float
         L.orc_v_expf.argtypes = [C.c_float]
+        L.orc_v_expf_increases.restype = C.c_int64
+        L.orc_v_expf_increases.argtypes = [C.c_uint32, C.c_uint32]
         L.orc_swiglu.argtypes = [C.c_int64, C.c_void_p, C.c_void_p, C.c_void_p]
         L.orc_soft_max.argtypes = [C.c_int64, C.c_int64, C.c_void_p, C.c_void_p]
         L.orc_argsort_desc.argtypes = [C.c_int64, C.c_int64, C.c_void_p, C.c_void_p]

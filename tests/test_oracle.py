@@ -283,6 +283,20 @@ def test_softmax_and_expf_accuracy(orc):
     assert np.allclose(p.sum(1), 1.0, atol=1e-5)
 
 
+def test_v_expf_never_increases_as_x_decreases(orc):
+    """Every float in [-inf, -0]: a smaller x never gets a larger ggml_v_expf.
+    The GPU router posts its top-k from this (with a margin that rounding of
+    e * (1/sum) cannot undo) before the softmax sums are formed."""
+    from concurrent.futures import ThreadPoolExecutor
+    edges = [0x80000000 + ((0xFF800000 - 0x80000000) * i) // 8 for i in range(9)]   # chunks share end points
+    with ThreadPoolExecutor(8) as ex:                  # ctypes drops the GIL during the call
+        bad = list(ex.map(lambda i: orc.lib.orc_v_expf_increases(edges[i], edges[i + 1]), range(8)))
+    assert bad == [0] * 8
+    assert orc.lib.orc_v_expf(-0.0) == 1.0 and orc.lib.orc_v_expf(float("-inf")) == 0.0
+    # the counter sees increases where they exist: x = 1.0 upward, 256 steps
+    assert orc.lib.orc_v_expf_increases(0x3F800000, 0x3F800100) > 200
+
+
 def test_argsort_brute_force_without_ties(orc):
     rng = np.random.default_rng(2)
     x = rng.permutation(np.arange(128, dtype=np.float32)).reshape(1, 128) / 7
