@@ -45,6 +45,7 @@ extern "C" {
 #define QWMOE_ERR_NOT_INITIALIZED (-5)
 #define QWMOE_ERR_FORMAT (-6)          /* malformed or unsupported GGUF file */
 #define QWMOE_ERR_IO (-7)              /* a file could not be opened or read */
+#define QWMOE_ERR_SCRATCH (-8)         /* the call needs more than the static scratch of qwmoe_mul_mat_id_noalloc */
 
 /* ggml_type values used on the path (ggml/include/ggml.h:390-416). */
 enum qwmoe_type {
@@ -133,6 +134,22 @@ int qwmoe_mul_mat_id(void * stream, int type, const void * as, int64_t ne00, int
                      size_t nb01, size_t nb02, const float * b, int64_t ne11, int64_t ne12, size_t nb11,
                      size_t nb12, const int32_t * ids, int64_t n_ids, size_t ids_nb1, const int32_t * slot_of,
                      int64_t n_slot_of, float * dst, size_t nb1, size_t nb2);
+
+/* qwmoe_mul_mat_id that allocates nothing and uses no library workspace.  No
+ * counterpart in the reference: for callers that cannot allocate device
+ * memory during the call (HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Same arguments, results bit-identical to
+ * qwmoe_mul_mat_id.  The quantized activations and the grouping arrays live in
+ * a static device array of 8 MiB per GPU (held until the process ends), whose
+ * address qwmoe_init looks up once; the call runs on the library's device.
+ * A call needing more (about ne11 * ne12 * row_size(vec_dot_type, ne00) +
+ * 8 * n_ids * ne12 + 72 * n_bins bytes, n_bins = n_slot_of or ne02) returns
+ * QWMOE_ERR_SCRATCH before anything is enqueued.  Every call on a GPU shares
+ * that array: calls that overlap on one GPU (two streams, two threads) race. */
+int qwmoe_mul_mat_id_noalloc(void * stream, int type, const void * as, int64_t ne00, int64_t ne01, int64_t ne02,
+                             size_t nb01, size_t nb02, const float * b, int64_t ne11, int64_t ne12, size_t nb11,
+                             size_t nb12, const int32_t * ids, int64_t n_ids, size_t ids_nb1,
+                             const int32_t * slot_of, int64_t n_slot_of, float * dst, size_t nb1, size_t nb2);
 
 /* Per-expert grouping of the (slot e, token t) pairs, in the order of
  * ggml-cpu.c:1622-1637 (token outer, slot inner): counts[n_as],

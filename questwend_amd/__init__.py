@@ -58,6 +58,7 @@ SIGNATURES = {
     "qwmoe_dequantize": (I, [P, I, P, P, I64]),
     "qwmoe_fill_randn": (I, [P, P, I64, U64, F, F]),
     "qwmoe_mul_mat_id": (I, [P, I, P, I64, I64, I64, SZ, SZ, P, I64, I64, SZ, SZ, P, I64, SZ, P, I64, P, SZ, SZ]),
+    "qwmoe_mul_mat_id_noalloc": (I, [P, I, P, I64, I64, I64, SZ, SZ, P, I64, I64, SZ, SZ, P, I64, SZ, P, I64, P, SZ, SZ]),
     "qwmoe_group_by_expert": (I, [P, P, I64, I64, SZ, I64, P, P, P]),
     "qwmoe_router_topk": (I, [P, P, P, I64, I64, I64, I64, SZ, F, F, P, P, P]),
     "qwmoe_swiglu": (I, [P, P, P, P, I64, I64]),

@@ -37,7 +37,9 @@ std::atomic<uint64_t> g_ws_generation{1};   // changes whenever the workspace is
 struct Arena {
     uint8_t* base;
     size_t cap, off;
+    bool track = true;   // record the high-water mark of the library workspace
     explicit Arena(size_t reserved) : base(g_lib.ws), cap(g_lib.ws_bytes), off(reserved) {}
+    Arena(void* buf, size_t bytes) : base((uint8_t*) buf), cap(bytes), off(0), track(false) {}
     template <typename T>
     T* take(size_t count) {
         off = (off + 255) & ~(size_t) 255;
@@ -47,7 +49,7 @@ struct Arena {
         return p;
     }
     ~Arena() {
-        if (off > g_lib.high_water) g_lib.high_water = off;
+        if (track && off > g_lib.high_water) g_lib.high_water = off;
     }
 };
 
@@ -178,8 +180,11 @@ int qwmoe_init(int device, size_t workspace_bytes) {
     const size_t bytes = workspace_bytes ? workspace_bytes : ((size_t) 256 << 20);
     void* p = nullptr;
     if (hipMalloc(&p, bytes) != hipSuccess) return QWMOE_ERR_HIP;
-    if (hipMemset(p, 0, kReserved) != hipSuccess) return QWMOE_ERR_HIP;
-    if (hipDeviceSynchronize() != hipSuccess) return QWMOE_ERR_HIP;
+    if (hipMemset(p, 0, kReserved) != hipSuccess || hipDeviceSynchronize() != hipSuccess ||
+        qw::scratch_setup(device) != 0) {
+        (void) hipFree(p);
+        return QWMOE_ERR_HIP;
+    }
     g_lib.ws = (uint8_t*) p;
     g_lib.ws_bytes = bytes;
     g_lib.status = (int32_t*) p;
@@ -209,6 +214,8 @@ const char* qwmoe_strerror(int status) {
         case QWMOE_ERR_NOT_INITIALIZED: return "qwmoe_init has not been called";
         case QWMOE_ERR_FORMAT: return "malformed or unsupported GGUF file";
         case QWMOE_ERR_IO: return "file could not be opened or read";
+        case QWMOE_ERR_SCRATCH:
+            return "the call needs more than the 8 MiB static scratch of the allocation-free entry point";
     }
     return "unknown status";
 }
@@ -280,11 +287,17 @@ int qwmoe_group_by_expert(void* stream, const int32_t* ids, int64_t n_ids, int64
     return group(S(stream), ar, ids, n_ids, T, ids_nb1, n_as, counts, offsets, rows, G);
 }
 
-int qwmoe_mul_mat_id(void* stream, int type, const void* as, int64_t ne00, int64_t ne01, int64_t ne02, size_t nb01,
-                     size_t nb02, const float* b, int64_t ne11, int64_t ne12, size_t nb11, size_t nb12,
-                     const int32_t* ids, int64_t n_ids, size_t ids_nb1, const int32_t* slot_of, int64_t n_slot_of,
-                     float* dst, size_t nb1, size_t nb2) {
-    if (!g_lib.ready) return QWMOE_ERR_NOT_INITIALIZED;
+}  // extern "C"
+
+namespace {
+
+// qwmoe_mul_mat_id with its quantized activations and grouping arrays taken
+// from `ar` (the library workspace, or the static scratch of the
+// allocation-free variant); err_space: the status when `ar` is too small.
+int mul_mat_id_in(Arena& ar, int err_space, void* stream, int type, const void* as, int64_t ne00, int64_t ne01,
+                  int64_t ne02, size_t nb01, size_t nb02, const float* b, int64_t ne11, int64_t ne12, size_t nb11,
+                  size_t nb12, const int32_t* ids, int64_t n_ids, size_t ids_nb1, const int32_t* slot_of,
+                  int64_t n_slot_of, float* dst, size_t nb1, size_t nb2) {
     if (!as || !b || !ids || !dst || ne01 <= 0 || ne02 <= 0 || ne11 <= 0 || ne12 < 0 || n_ids <= 0)
         return QWMOE_ERR_INVALID_ARG;
     if (!weight_type_ok(type)) return QWMOE_ERR_UNSUPPORTED;
@@ -301,17 +314,47 @@ int qwmoe_mul_mat_id(void* stream, int type, const void* as, int64_t ne00, int64
     const size_t qrow = qwmoe_row_size(vdt, ne00);
     if (qrow % 4) return QWMOE_ERR_UNSUPPORTED;
     hipStream_t st = S(stream);
-    Arena ar(kReserved);
     uint8_t* bq = ar.take<uint8_t>(qrow * (size_t) (ne11 * ne12) + 64);
-    if (!bq) return QWMOE_ERR_WORKSPACE;
+    if (!bq) return err_space;
+    const int64_t n_bins = slot_of ? n_slot_of : ne02;
+    Grouping G{};
+    qw::GroupArgs ga;
+    rc = group_args(ar, ids, n_ids, ne12, ids_nb1, n_bins, nullptr, nullptr, nullptr, G, ga);
+    if (rc) return rc == QWMOE_ERR_WORKSPACE ? err_space : rc;
     rc = qwmoe_quantize_act(stream, vdt, b, ne00, ne11, ne12, nb11, nb12, bq);
     if (rc) return rc;
-    Grouping G{};
-    const int64_t n_bins = slot_of ? n_slot_of : ne02;
-    rc = group(st, ar, ids, n_ids, ne12, ids_nb1, n_bins, nullptr, nullptr, nullptr, G);
-    if (rc) return rc;
+    if (qw::launch_group(ga, st) != 0) return QWMOE_ERR_HIP;
     return mmid_grouped(st, type, as, ne00, ne01, ne02, nb01, nb02, bq, ne11, qrow, G.rows, G.active, G.active_off,
                         G.n_active, G.max_active, slot_of, n_slot_of, dst, nb1, nb2, n_ids * ne12);
+}
+
+}  // namespace
+
+extern "C" {
+
+int qwmoe_mul_mat_id(void* stream, int type, const void* as, int64_t ne00, int64_t ne01, int64_t ne02, size_t nb01,
+                     size_t nb02, const float* b, int64_t ne11, int64_t ne12, size_t nb11, size_t nb12,
+                     const int32_t* ids, int64_t n_ids, size_t ids_nb1, const int32_t* slot_of, int64_t n_slot_of,
+                     float* dst, size_t nb1, size_t nb2) {
+    if (!g_lib.ready) return QWMOE_ERR_NOT_INITIALIZED;
+    Arena ar(kReserved);
+    return mul_mat_id_in(ar, QWMOE_ERR_WORKSPACE, stream, type, as, ne00, ne01, ne02, nb01, nb02, b, ne11, ne12, nb11,
+                         nb12, ids, n_ids, ids_nb1, slot_of, n_slot_of, dst, nb1, nb2);
+}
+
+int qwmoe_mul_mat_id_noalloc(void* stream, int type, const void* as, int64_t ne00, int64_t ne01, int64_t ne02,
+                             size_t nb01, size_t nb02, const float* b, int64_t ne11, int64_t ne12, size_t nb11,
+                             size_t nb12, const int32_t* ids, int64_t n_ids, size_t ids_nb1, const int32_t* slot_of,
+                             int64_t n_slot_of, float* dst, size_t nb1, size_t nb2) {
+    if (!g_lib.ready) return QWMOE_ERR_NOT_INITIALIZED;
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess) return QWMOE_ERR_HIP;
+    if (cur != g_lib.device) return QWMOE_ERR_INVALID_ARG;   // the status word lives on the library's device
+    void* ptr = qw::scratch_ptr(cur);   // looked up by qwmoe_init
+    if (!ptr) return QWMOE_ERR_NOT_INITIALIZED;
+    Arena ar(ptr, qw::kScratchBytes);
+    return mul_mat_id_in(ar, QWMOE_ERR_SCRATCH, stream, type, as, ne00, ne01, ne02, nb01, nb02, b, ne11, ne12, nb11,
+                         nb12, ids, n_ids, ids_nb1, slot_of, n_slot_of, dst, nb1, nb2);
 }
 
 int qwmoe_router_topk(void* stream, const float* W, const float* x, int64_t H, int64_t E, int64_t k, int64_t T,

@@ -101,4 +101,11 @@ int launch_weighted_sum_rms(const float* experts, const float* weights, float* o
 // k_swiglu then k_quant_q8K of its output, in one launch (F % 256 == 0; rows dense)
 int launch_swiglu_q8K(const float* gate, const float* up, int64_t F, int64_t n_rows, void* dst, hipStream_t stream);
 
+// Static device scratch of the allocation-free entry point (scratch.hip):
+// kScratchBytes per GPU.  scratch_setup(device), with that device current,
+// looks up this GPU's copy once; scratch_ptr(device) returns it (null before).
+constexpr size_t kScratchBytes = (size_t) 8 << 20;
+int scratch_setup(int device);
+void* scratch_ptr(int device);
+
 }  // namespace qw

@@ -86,10 +86,11 @@ def randn_(t, seed: int, mean: float = 0.0, std: float = 1.0):
     return t
 
 
-def mul_mat_id(qtype: int, w, K: int, N: int, n_as: int, b, ids, slot_of=None, out=None):
+def mul_mat_id(qtype: int, w, K: int, N: int, n_as: int, b, ids, slot_of=None, out=None, noalloc=False):
     """ggml_mul_mat_id.  w: uint8 with n_as matrices of N rows (dense);
     b: f32 [T, ne11, K]; ids: i32 [T, n_ids] (row stride may exceed n_ids);
-    returns f32 [T, n_ids, N]."""
+    returns f32 [T, n_ids, N].  noalloc: through qwmoe_mul_mat_id_noalloc
+    (static scratch, no library workspace)."""
     torch = _torch()
     T, ne11, _ = b.shape
     n_ids = ids.shape[1]
@@ -97,10 +98,11 @@ def mul_mat_id(qtype: int, w, K: int, N: int, n_as: int, b, ids, slot_of=None, o
     if out is None:
         out = torch.empty((T, n_ids, N), dtype=torch.float32, device=b.device)
     n_slot_of = 0 if slot_of is None else slot_of.numel()
-    check(lib().qwmoe_mul_mat_id(stream(), qtype, _ptr(w), K, N, n_as, rs, rs * N, _ptr(b), ne11, T,
-                                 b.stride(1) * 4, b.stride(0) * 4, _ptr(ids), n_ids, ids.stride(0) * 4,
-                                 _ptr(slot_of), n_slot_of, _ptr(out), out.stride(1) * 4, out.stride(0) * 4),
-          "mul_mat_id")
+    fn = lib().qwmoe_mul_mat_id_noalloc if noalloc else lib().qwmoe_mul_mat_id
+    check(fn(stream(), qtype, _ptr(w), K, N, n_as, rs, rs * N, _ptr(b), ne11, T, b.stride(1) * 4, b.stride(0) * 4,
+             _ptr(ids), n_ids, ids.stride(0) * 4, _ptr(slot_of), n_slot_of, _ptr(out), out.stride(1) * 4,
+             out.stride(0) * 4),
+          "mul_mat_id_noalloc" if noalloc else "mul_mat_id")
     return out
 
 
