@@ -20,6 +20,8 @@
 #include "ggml.h"
 #include "ggml-cpu.h"
 
+#include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -214,6 +216,69 @@ int qwref_layer_eval(qwref_layer * L, const float * x, float * out, float * xnex
     if (up)      copy_2d(L->up, up, 4);
     if (act)     copy_2d(L->act, act, 4);
     if (experts) copy_2d(L->experts, experts, 4);
+    return 0;
+}
+
+// A stack of T = 1 layers (each created with rms_eps >= 0) on n_warmup +
+// n_steps independent tokens xs[s] (the decode benchmark's inputs): each step
+// runs x = xs[s] through every layer in order, x <- xnext.  Per timed step:
+// the seconds it took (steady_clock around the whole stack), the last layer's
+// output out[s] [H], every layer's ids[s][l] [k], and the top-k margin of every
+// layer: the k-th largest probability minus the (k+1)-th, margin[s][l].
+int qwref_stack_run(qwref_layer ** Ls, int n_layer, const float * xs, int n_warmup, int n_steps,
+                    float * out, int32_t * ids, float * margin, double * step_s, int n_threads) {
+    if (n_layer <= 0 || !Ls || !xs) return -2;
+    const int64_t H = Ls[0]->H;
+    std::vector<float> x((size_t) H), xn((size_t) H);
+    for (int s = 0; s < n_warmup + n_steps; ++s) {
+        const int ts = s - n_warmup;   // < 0: warm-up
+        memcpy(x.data(), xs + (size_t) s * H, sizeof(float) * H);
+        const auto t0 = std::chrono::steady_clock::now();
+        for (int l = 0; l < n_layer; ++l) {
+            qwref_layer * L = Ls[l];
+            const bool last = l + 1 == n_layer;
+            if (qwref_layer_eval(L, x.data(), last && ts >= 0 && out ? out + (size_t) ts * H : nullptr, xn.data(),
+                                 nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                 n_threads) != 0)
+                return -1;
+            x.swap(xn);
+        }
+        const auto t1 = std::chrono::steady_clock::now();
+        if (ts >= 0 && step_s) step_s[ts] = std::chrono::duration<double>(t1 - t0).count();
+    }
+    // ids and margins: a second, untimed pass (a layer graph keeps only its
+    // last evaluation, and reading them inside the timed steps would add copies)
+    if (ids || margin) {
+        const int64_t E = Ls[0]->E, k = Ls[0]->K;
+        std::vector<float> probs((size_t) E);
+        for (int ts = 0; ts < n_steps; ++ts) {
+            memcpy(x.data(), xs + (size_t) (n_warmup + ts) * H, sizeof(float) * H);
+            for (int l = 0; l < n_layer; ++l) {
+                qwref_layer * L = Ls[l];
+                int32_t * id = ids ? ids + ((size_t) ts * n_layer + l) * k : nullptr;
+                if (qwref_layer_eval(L, x.data(), nullptr, xn.data(), id, nullptr, nullptr, probs.data(), nullptr,
+                                     nullptr, nullptr, nullptr, n_threads) != 0)
+                    return -1;
+                if (margin) {
+                    std::vector<float> p(probs);
+                    std::nth_element(p.begin(), p.begin() + k, p.end(), [](float a, float b) { return a > b; });
+                    const float pk1 = p[(size_t) k];
+                    const float pk = *std::min_element(p.begin(), p.begin() + k);
+                    margin[(size_t) ts * n_layer + l] = pk - pk1;
+                }
+                x.swap(xn);
+            }
+        }
+    }
+    return 0;
+}
+
+// The ISA branch this build of the ggml CPU backend takes (compile-time
+// flags): 512 for AVX-512, 256 for AVX2, 0 otherwise.
+int qwref_isa(void) {
+    ensure_init();
+    if (ggml_cpu_has_avx512()) return 512;
+    if (ggml_cpu_has_avx2()) return 256;
     return 0;
 }
 

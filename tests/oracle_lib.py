@@ -19,6 +19,7 @@ import numpy as np
 ROOT = Path(__file__).resolve().parents[1]
 ORACLE_SO = ROOT / "oracle" / "liboracle.so"
 REF_SO = ROOT / "oracle" / "_ref" / "libqwref.so"
+REF_SO_AVX512 = ROOT / "oracle" / "_ref" / "libqwref_avx512.so"   # ggml's AVX-512 branch (timed baseline)
 
 F32, Q8_0, Q4_K, Q6_K, Q8_K, I32 = 0, 8, 12, 14, 15, 26
 BLOCK = {Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210), Q8_K: (256, 292), F32: (1, 4)}
@@ -266,6 +267,30 @@ class RefGGML:
                                        C.c_int64, C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p, C.c_int]
         L.qwref_unary.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_float,
                                   C.c_void_p, C.c_int]
+        L.qwref_stack_run.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p,
+                                      C.c_void_p, C.c_void_p, C.c_int]
+        L.qwref_isa.restype = C.c_int
+
+    def isa(self) -> int:
+        """512: this build takes ggml's AVX-512 branch; 256: AVX2."""
+        return self.lib.qwref_isa()
+
+    def stack_run(self, layers, xs, n_warmup: int, n_threads: int, want_ids=True):
+        """Layers (RefLayer, T = 1, each with an RMSNorm) chained on the tokens
+        xs [n_warmup + n_steps, H]: per timed step the seconds (steady_clock),
+        the last layer's output, every layer's ids and top-k margins."""
+        xs = np.ascontiguousarray(xs, np.float32)
+        n_steps = xs.shape[0] - n_warmup
+        H, k, nl = layers[0].lw.H, layers[0].lw.k, len(layers)
+        hs = (C.c_void_p * nl)(*[r.h for r in layers])
+        out = np.zeros((n_steps, H), np.float32)
+        ids = np.zeros((n_steps, nl, k), np.int32) if want_ids else None
+        margin = np.zeros((n_steps, nl), np.float32) if want_ids else None
+        step_s = np.zeros(n_steps, np.float64)
+        rc = self.lib.qwref_stack_run(hs, nl, _p(xs), n_warmup, n_steps, _p(out), _p(ids), _p(margin), _p(step_s),
+                                      n_threads)
+        assert rc == 0
+        return dict(out=out, ids=ids, margin=margin, step_s=step_s)
 
     def quantize(self, t, x):
         x = np.ascontiguousarray(x, np.float32)

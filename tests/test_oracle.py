@@ -133,6 +133,53 @@ def test_layer_matches_ggml_all_intermediates(orc, T):
         assert np.array_equal(bits(a[key]), bits(b[key])), key
 
 
+def _host_has_avx512_branch() -> bool:
+    try:
+        flags = open("/proc/cpuinfo").read()
+    except OSError:
+        return False
+    need = ("avx512f", "avx512cd", "avx512vl", "avx512dq", "avx512bw", "avx512vbmi", "avx512_vnni", "avx512_bf16",
+            "avx_vnni")
+    return all(f" {f}" in flags for f in need)
+
+
+@needs_ref
+def test_stack_run_avx2_bit_exact_and_avx512_within_tolerance(orc):
+    """The chained-stack driver the benchmark times: the AVX2 build equals the
+    restatement bit for bit through a 4-layer stack (ids, output); the AVX-512
+    build (the timed CPU baseline) takes the AVX-512 branch, and teacher-forced
+    per layer its ids agree and its output stays far inside 1e-3."""
+    from oracle_lib import REF_SO_AVX512
+    lws = [LayerWeights(1024, 32, 8, 512, Q4_K, Q4_K, Q4_K, seed=70 + l, oracle=orc) for l in range(4)]
+    xs = np.random.default_rng(8).standard_normal((5, 1024)).astype(np.float32)
+    ref = RefGGML()
+    assert ref.isa() == 256
+    L2 = [ref.layer(lw, 1, rms_eps=1e-6, n_threads=2) for lw in lws]
+    r = ref.stack_run(L2, xs, 2, 2)
+    assert r["step_s"].shape == (3,) and (r["step_s"] > 0).all()
+    for s in range(3):
+        x = xs[2 + s:3 + s]
+        for l, lw in enumerate(lws):
+            o = orc.moe_layer(lw, x, rms_eps=1e-6)
+            assert np.array_equal(r["ids"][s, l], o["ids"][0])
+            p = np.sort(L2[l](x)["probs"][0])[::-1]
+            assert r["margin"][s, l] == p[7] - p[8]
+            x = o["xnext"]
+        assert np.array_equal(r["out"][s].view(np.int32), o["out"][0].view(np.int32))
+    if not (REF_SO_AVX512.exists() and _host_has_avx512_branch()):
+        pytest.skip("AVX-512 reference build or host ISA absent")
+    r5 = RefGGML(REF_SO_AVX512)
+    assert r5.isa() == 512
+    L5 = [r5.layer(lw, 1, rms_eps=1e-6, n_threads=2) for lw in lws]
+    for s in range(3):
+        x = xs[2 + s:3 + s]
+        for l, lw in enumerate(lws):
+            o, c = orc.moe_layer(lw, x, rms_eps=1e-6), L5[l](x)
+            assert np.array_equal(c["ids"][0], o["ids"][0])
+            assert np.abs(c["out"] - o["out"]).max() <= 1e-5 * np.abs(o["out"]).max()
+            x = o["xnext"]
+
+
 @needs_ref
 def test_mul_mat_id_matches_ggml(orc):
     ref = RefGGML()
