@@ -230,7 +230,9 @@ int qwmoe_decode_stack_create(const qwmoe_layer * layers, int n_layer, float rms
 int qwmoe_decode_stack_run(void * stream, qwmoe_decode_stack * s, const float * x, float * out, float * x_out,
                            int32_t * ids_out, float * weights_out);
 /* Synchronises `stream`; status bits: 1 top-k tie replayed, 8 a wait timed out
- * (launch abandoned), 16 a slot table entry was out of range. */
+ * (launch abandoned), 16 a slot table entry was out of range.  With 8, the
+ * XCD kernel (qwmoe_decode_stack_kernel 2 or 3) names the exchange it waited
+ * for: 256 router logits, 512 act, 1024 down outputs, 2048 y, 4096 top-k. */
 int qwmoe_decode_stack_status(void * stream, qwmoe_decode_stack * s, int32_t * status_out, int clear);
 void qwmoe_decode_stack_free(qwmoe_decode_stack * s);
 /* Which kernel a stack runs (no reference counterpart; the kernel choice only):

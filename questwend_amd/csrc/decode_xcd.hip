@@ -46,6 +46,8 @@ constexpr int XW = XT / 64;             // waves
 constexpr int NXCD = 8;
 constexpr int NJ = 32;                  // workgroups per XCD
 constexpr long XSPIN = 1L << 22;        // polls before a wait gives up (~seconds)
+// Status bits of a wait that gave up (with 8): which exchange it waited for.
+constexpr int XW_LOGITS = 256, XW_ACT = 512, XW_DOWN = 1024, XW_Y = 2048, XW_TOPK = 4096;
 constexpr int QB = 304;                 // LDS Q8_K block: qs[256] | d | bsums[16] | pad (16-aligned qs)
 constexpr int XLW = sizeof(DecodeLayer) / 8;
 
@@ -114,11 +116,12 @@ __device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcn
 __device__ __forceinline__ void all_loads_returned() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // Polls n tagged words (this thread's: i = tid + XT * m, m < MAXJ) until each
-// carries epoch ep, then stores the payloads to dst[i] (LDS).  Only the words
-// not yet seen are polled again.  Returns false if the wait gave up.
+// carries epoch ep, then stores the payloads to dst[i] (LDS).  A sweep reloads
+// every word of the thread and keeps the first payload seen with the epoch.
+// Returns false if the wait gave up.
 template <int MAXJ>
 __device__ __forceinline__ bool gather(const XcdArgs& a, const uint64_t* src, int n, uint32_t ep, float* dst,
-                                       int tid) {
+                                       int tid, int where) {
     uint32_t got = 0;
     uint32_t val[MAXJ];
 #pragma unroll
@@ -140,7 +143,7 @@ __device__ __forceinline__ bool gather(const XcdArgs& a, const uint64_t* src, in
             }
         if (got == all) break;
         if (++spins > XSPIN) {
-            x_abort(a, 8);
+            x_abort(a, 8 | where);
             return false;
         }
         if ((spins & 255) == 0 && x_aborted(a)) return false;
@@ -534,7 +537,7 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
         const uint32_t od = (uint32_t) (NH * j + RW * wave + g) * dnb1;
 
         // ---- L: the layer's logits (all E, from this XCD's router workgroups) ------
-        if (tid < E && !gather<1>(a, a.xl + xcd * E, E, ep, s_p, tid)) s_fail = 1;
+        if (tid < E && !gather<1>(a, a.xl + xcd * E, E, ep, s_p, tid, XW_LOGITS)) s_fail = 1;
         lds_barrier();
         if (s_fail) return;
         // logit ranks (strictly larger count; four lanes per value); the rank-c
@@ -742,7 +745,7 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
                 long spins = 0;
                 while (__hip_atomic_load(&s_topk_ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != ep) {
                     if (++spins > XSPIN) {
-                        x_abort(a, 8);
+                        x_abort(a, 8 | XW_TOPK);
                         return;
                     }
                     __builtin_amdgcn_s_sleep(1);
@@ -802,7 +805,7 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
             Q4KLane dw[NBF];
 #pragma unroll
             for (int bb = 0; bb < NBF; ++bb) dw[bb] = q4k_lane(dh[bb], dq[bb], t);
-            if (!gather<(F + XT - 1) / XT>(a, a.xa + xcd * F, F, ep, s_act, tid)) s_fail = 1;
+            if (!gather<(F + XT - 1) / XT>(a, a.xa + xcd * F, F, ep, s_act, tid, XW_ACT)) s_fail = 1;
             lds_barrier();
             if (s_fail) return;
             if (wave < NBF) {
@@ -861,7 +864,7 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
                     }
                 if (got == all) break;
                 if (++spins > XSPIN) {
-                    x_abort(a, 8);
+                    x_abort(a, 8 | XW_DOWN);
                     break;
                 }
                 if ((spins & 255) == 0 && x_aborted(a)) break;
@@ -904,7 +907,7 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
                         }
                     if (got == all) break;
                     if (++spins > XSPIN) {
-                        x_abort(a, 8);
+                        x_abort(a, 8 | XW_Y);
                         ok = false;
                         break;
                     }
