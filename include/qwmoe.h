@@ -208,7 +208,11 @@ typedef struct qwmoe_layer {
 
 /* The whole layer for T tokens: router -> 3x mul_mat_id + swiglu -> weighted
  * sum, then (rms_eps >= 0) x_next = rms_norm(out, rms_eps).
- * x, out, x_next: f32 [H, T] dense.  ids_out / weights_out: optional [k, T]. */
+ * x, out, x_next: f32 [H, T] dense.  ids_out / weights_out: optional [k, T].
+ * Requirements (else QWMOE_ERR_INVALID_ARG / QWMOE_ERR_UNSUPPORTED): each
+ * expert stride covers its rows (nb1 >= row size, nb2 >= nb1 * rows), every
+ * n_slots_* > 0, E a multiple of 8 up to 512, H a multiple of 4, x and the
+ * router 16-byte aligned, F a multiple of 8. */
 int qwmoe_ffn_layer(void * stream, const qwmoe_layer * layer, const float * x, int64_t T, float * out,
                     float rms_eps, float * x_next, int32_t * ids_out, float * weights_out);
 
@@ -239,7 +243,7 @@ void qwmoe_decode_stack_free(qwmoe_decode_stack * s);
  * 1 = one workgroup per CU over every selected expert; 2 = one selected expert
  * per XCD (256-CU devices, k <= 8, H = 2048, Q4_K down), exchanges inside an XCD
  * through its L2; 3 = the same with every exchange word stored at device scope
- * (used when the workgroup -> XCD mapping checked at creation is not b % 8).
+ * (used when creation finds the workgroups not dealt to the XCDs round robin).
  * Creation picks 2 or 3 where the shape allows, else 1; QWMOE_DECODE_XCD=0 in
  * the environment at creation forces 1, QWMOE_DECODE_XCD_LOCAL=0 forces 3 over 2.
  * Results are identical. */
@@ -269,6 +273,10 @@ int qwmoe_layer_stack_create(const qwmoe_layer * layers, int n_layer, float rms_
 int qwmoe_layer_stack_run(void * stream, qwmoe_layer_stack * s, const float * x, int64_t T, float * out,
                           float * x_out, int32_t * ids_out, float * weights_out);
 void qwmoe_layer_stack_free(qwmoe_layer_stack * s);
+/* Graphs the stack has captured so far (no reference counterpart; a
+ * diagnostic): a run captures again after qwmoe_init reallocated the workspace
+ * or qwmoe_set_mfma_min_rows changed the threshold. */
+int64_t qwmoe_layer_stack_captures(const qwmoe_layer_stack * s);
 
 /* ---- expert slot table (host) ------------------------------------------------ */
 

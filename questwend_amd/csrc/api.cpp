@@ -31,7 +31,9 @@ struct Library {
 
 Library g_lib;
 std::mutex g_mu;
-std::atomic<uint64_t> g_ws_generation{1};   // changes whenever the workspace is (re)allocated or freed
+// Changes whenever something a captured layer-stack graph baked in changes: the
+// workspace is (re)allocated or freed, or the matrix-core row threshold is set.
+std::atomic<uint64_t> g_ws_generation{1};
 
 // Bump allocator over the workspace for one call.
 struct Arena {
@@ -171,10 +173,12 @@ extern "C" {
 
 int qwmoe_init(int device, size_t workspace_bytes) {
     std::lock_guard<std::mutex> lk(g_mu);
+    const int mfma_min_rows = g_lib.mfma_min_rows;   // a setting, kept across re-initialisation
     if (g_lib.ready) {
         if (g_lib.device == device && (workspace_bytes == 0 || workspace_bytes <= g_lib.ws_bytes)) return QWMOE_OK;
         (void) hipFree(g_lib.ws);
         g_lib = Library{};
+        g_lib.mfma_min_rows = mfma_min_rows;
     }
     if (hipSetDevice(device) != hipSuccess) return QWMOE_ERR_HIP;
     const size_t bytes = workspace_bytes ? workspace_bytes : ((size_t) 256 << 20);
@@ -199,7 +203,9 @@ int qwmoe_shutdown(void) {
     if (!g_lib.ready) return QWMOE_OK;
     (void) hipDeviceSynchronize();
     (void) hipFree(g_lib.ws);
+    const int mfma_min_rows = g_lib.mfma_min_rows;
     g_lib = Library{};
+    g_lib.mfma_min_rows = mfma_min_rows;
     g_ws_generation.fetch_add(1);
     return QWMOE_OK;
 }
@@ -223,7 +229,10 @@ const char* qwmoe_strerror(int status) {
 int qwmoe_set_mfma_min_rows(int rows) {
     if (rows < 0) return QWMOE_ERR_INVALID_ARG;
     std::lock_guard<std::mutex> lk(g_mu);
-    g_lib.mfma_min_rows = rows;
+    if (g_lib.mfma_min_rows != rows) {
+        g_lib.mfma_min_rows = rows;
+        g_ws_generation.fetch_add(1);   // captured graphs chose kernels with the old threshold
+    }
     return QWMOE_OK;
 }
 
@@ -413,6 +422,15 @@ int qwmoe_ffn_layer(void* stream, const qwmoe_layer* L, const float* x, int64_t 
     if ((rc = check_k(L->type_gate, H)) || (rc = check_k(L->type_up, H)) || (rc = check_k(L->type_down, F))) return rc;
     if (F % 8) return QWMOE_ERR_UNSUPPORTED;
     if (rms_eps >= 0.0f && !x_next) return QWMOE_ERR_INVALID_ARG;
+    // the checks of the calls it fuses: expert strides (qwmoe_mul_mat_id) and
+    // the router's shape and 16-byte alignment (qwmoe_router_topk)
+    const size_t rsg = qwmoe_row_size(L->type_gate, H), rsu = qwmoe_row_size(L->type_up, H);
+    const size_t rsd = qwmoe_row_size(L->type_down, F);
+    if (L->gate_nb1 < rsg || L->gate_nb2 < L->gate_nb1 * (size_t) F || L->up_nb1 < rsu ||
+        L->up_nb2 < L->up_nb1 * (size_t) F || L->down_nb1 < rsd || L->down_nb2 < L->down_nb1 * (size_t) H ||
+        L->n_slots_gate <= 0 || L->n_slots_up <= 0 || L->n_slots_down <= 0)
+        return QWMOE_ERR_INVALID_ARG;
+    if (E % 8 || E > 512 || H % 4 || ((uintptr_t) x & 15) || ((uintptr_t) L->router & 15)) return QWMOE_ERR_UNSUPPORTED;
     if (T == 0) return QWMOE_OK;
     hipStream_t st = S(stream);
     Arena ar(kReserved);

@@ -33,7 +33,8 @@ struct qwmoe_layer_stack {
     float* w = nullptr;                  // [n_layer][max_T][k]
     hipStream_t cap = nullptr;           // capture stream
     std::vector<hipGraphExec_t> exec;    // [T]: the captured chain, or null
-    std::vector<uint64_t> exec_gen;      // [T]: the library workspace generation it was captured with
+    std::vector<uint64_t> exec_gen;      // [T]: the library generation it was captured with
+    int64_t captures = 0;                // graphs captured so far (a diagnostic)
 
     ~qwmoe_layer_stack() {
         for (hipGraphExec_t e : exec)
@@ -71,6 +72,7 @@ struct qwmoe_layer_stack {
         if (ei != hipSuccess) return QWMOE_ERR_HIP;
         exec[(size_t) T] = e;
         exec_gen[(size_t) T] = gen;
+        ++captures;
         return QWMOE_OK;
     }
 };
@@ -126,7 +128,8 @@ int qwmoe_layer_stack_run(void* stream, qwmoe_layer_stack* s, const float* x, in
     if (hipMemcpyAsync(s->xb[0], x, xbytes, hipMemcpyDeviceToDevice, st) != hipSuccess) return QWMOE_ERR_HIP;
     int rc;
     if (s->graphs) {
-        // a graph holds the workspace addresses of its capture: re-capture after qwmoe_init reallocated it
+        // a graph holds the workspace addresses and the kernel choices of its capture: capture again
+        // after qwmoe_init reallocated the workspace or qwmoe_set_mfma_min_rows changed the threshold
         if (s->exec[(size_t) T] && s->exec_gen[(size_t) T] != qw::workspace_generation()) {
             if (hipStreamSynchronize(st) != hipSuccess) return QWMOE_ERR_HIP;   // its last replay has finished
             (void) hipGraphExecDestroy(s->exec[(size_t) T]);
@@ -149,6 +152,8 @@ int qwmoe_layer_stack_run(void* stream, qwmoe_layer_stack* s, const float* x, in
     }
     return QWMOE_OK;
 }
+
+int64_t qwmoe_layer_stack_captures(const qwmoe_layer_stack* s) { return s ? s->captures : -1; }
 
 void qwmoe_layer_stack_free(qwmoe_layer_stack* s) {
     if (!s) return;

@@ -12,6 +12,7 @@
 #include <type_traits>
 
 #include "qw_kernels.hpp"
+#include "qw_bp_rows.hpp"
 #include "qw_rowdot.hpp"
 #include "qw_topk.hpp"
 
@@ -658,13 +659,13 @@ __device__ __forceinline__ void bp_q6k_block(RW rw, uint16_t d16, const uint32_t
 // (small bins only; the other kernels take Q6_K's many-row form).
 template <int TYPE, int BPR, bool DIRECT, bool SWIGLU>
 __global__ void __launch_bounds__(256) k_mmid_gemv_bp(MmidPair pr) {
-    constexpr int RPW = 64 / BPR;                 // rows per wave
+    constexpr int RPW = bp_rows_per_wave(BPR);    // rows per wave
     constexpr int NPW = BpType<TYPE>::NPW, NCH = BpType<TYPE>::NCH;
     const MmidArgs m = pr.m[blockIdx.z];
     extern __shared__ uint32_t lds[];
     __shared__ int s_chunk[MMID_CT][3];
     const int g = blockIdx.y;
-    const int64_t r0 = (int64_t) blockIdx.x * (4 * RPW);
+    const int64_t r0 = bp_wg_row0(blockIdx.x, BPR);
     if (r0 >= m.N) return;
     // the bin's count, offsets and id in one round (g < max_active keeps every
     // address inside the grouping's arrays; the values count only when g < n_active)
@@ -695,8 +696,8 @@ __global__ void __launch_bounds__(256) k_mmid_gemv_bp(MmidPair pr) {
     const uint32_t WBASE = WB + (uint32_t) wave * bp_wave_bytes<TYPE>(BPR, DIRECT ? 0u : RS);
     const uint32_t PBASE = WBASE + (DIRECT ? 0u : (uint32_t) RPW * RS);   // partials [64][NPW]
     const uint32_t CBASE = PBASE + 64u * NPW * 4u;                  // chain values [RPW][NCH]
-    const int64_t wr0 = r0 + (int64_t) wave * RPW;
-    const int wrows = (int) (m.N - wr0 < 0 ? 0 : m.N - wr0 < RPW ? m.N - wr0 : RPW);
+    const int64_t wr0 = bp_wave_row0(blockIdx.x, wave, BPR);
+    const int wrows = bp_wave_rows(m.N, wr0, BPR);
     const uint8_t* wmat = m.w + (size_t) mat * m.nb2;
     const int rl = lane / BPR, b = lane % BPR;
     const bool bvalid = rl < wrows && b < nb;
@@ -710,7 +711,7 @@ __global__ void __launch_bounds__(256) k_mmid_gemv_bp(MmidPair pr) {
     if constexpr (DIRECT) {
         // a wave past the matrix end (wrows == 0) loads the workgroup's first row,
         // which exists (r0 < N), and uses nothing it loaded
-        const int64_t lrow = wrows > 0 ? wr0 + rrow : r0;
+        const int64_t lrow = bp_direct_row(r0, wr0, wrows, rl);
         const uint8_t* bp = wmat + (size_t) lrow * m.nb1 + block_bytes(TYPE) * (size_t) (b < nb ? b : 0);
         if constexpr (TYPE == T_Q4_K) {
 #pragma unroll
@@ -734,7 +735,7 @@ __global__ void __launch_bounds__(256) k_mmid_gemv_bp(MmidPair pr) {
         for (int j = 0; j < BP_LD; ++j) {
             const int idx = base + lane + j * 64;
             const int r = idx / nchmax, c = idx % nchmax;
-            const uint8_t* src = wmat + (size_t) (wr0 + (r < wrows ? r : 0)) * m.nb1;
+            const uint8_t* src = wmat + (size_t) bp_staged_row(wr0, wrows, r) * m.nb1;
             const uintptr_t s0 = (uintptr_t) src & ~(uintptr_t) 15;
             const uintptr_t s1 = ((uintptr_t) src + row_bytes + 15) & ~(uintptr_t) 15;
             ok[j] = idx < wrows * nchmax && c < (int) ((s1 - s0) / 16);
@@ -848,15 +849,21 @@ static bool gemv_bp_direct(const MmidArgs& m) {
     return (a & (m.type == T_Q4_K ? 15 : 3)) == 0;
 }
 
+// Direct loads for a launch of nz matrices: every matrix's rows must allow them
+// (gate and up of one launch may sit at different alignments).
+static bool gemv_bp_direct(const MmidPair& pr, int nz) {
+    return gemv_bp_direct(pr.m[0]) && (nz < 2 || gemv_bp_direct(pr.m[1]));
+}
+
 // The block-parallel kernel's LDS bytes, or 0 when it does not apply.
-static size_t gemv_bp_lds(const MmidArgs& m) {
+static size_t gemv_bp_lds(const MmidArgs& m, bool direct) {
     if ((m.type != T_Q4_K && m.type != T_Q6_K) || m.K % QK_K != 0) return 0;
     const int64_t nb = m.K / QK_K;
     if (nb < 1 || nb > 16 || m.act_row_bytes != (size_t) nb * 292) return 0;
     const size_t row_bytes = (size_t) nb * block_bytes(m.type);
     const uint32_t RS = mmid_slot_bytes(row_bytes);
     const int bpr = bp_bpr(nb);
-    const uint32_t rs = gemv_bp_direct(m) ? 0u : RS;
+    const uint32_t rs = direct ? 0u : RS;
     const uint32_t wb = m.type == T_Q4_K ? bp_wave_bytes<T_Q4_K>(bpr, rs) : bp_wave_bytes<T_Q6_K>(bpr, rs);
     const size_t lds = (size_t) mmid_stage_rows(m.max_rows) * (size_t) nb * BP_ABLK + 4 * (size_t) wb;
     return lds <= 160 * 1024 ? lds : 0;
@@ -864,7 +871,7 @@ static size_t gemv_bp_lds(const MmidArgs& m) {
 
 bool mmid_gemv_swiglu_ok(const MmidArgs& m) {
     // (larger batches: every row tile of a bin would form the same rows again)
-    return m.mfma_min_rows == 0 && m.max_rows <= BP_SWIGLU_MAX_ROWS && gemv_bp_lds(m) != 0 &&
+    return m.mfma_min_rows == 0 && m.max_rows <= BP_SWIGLU_MAX_ROWS && gemv_bp_lds(m, gemv_bp_direct(m)) != 0 &&
            (((uintptr_t) m.swiglu_gate | (uintptr_t) m.swiglu_up | (uintptr_t) (m.K * 4)) & 15) == 0;
 }
 
@@ -873,7 +880,7 @@ static int launch_gemv_bp(const MmidPair& pr, int nz, size_t lds_bytes, hipStrea
     const int bpr = bp_bpr(m.K / QK_K);
     dim3 grid((unsigned) ((m.N + 4 * (64 / bpr) - 1) / (4 * (64 / bpr))), (unsigned) m.max_active, (unsigned) nz);
     if (grid.y == 0) return 0;
-    const bool direct = gemv_bp_direct(m), sw = m.swiglu_gate != nullptr;
+    const bool direct = gemv_bp_direct(pr, nz), sw = m.swiglu_gate != nullptr;
 #define QW_BP2(T, B, D)                                                                                   \
     do {                                                                                                  \
         if (sw) hipLaunchKernelGGL((k_mmid_gemv_bp<T, B, D, true>), grid, dim3(256), lds_bytes, stream, pr);   \
@@ -903,7 +910,7 @@ static int launch_gemv(const MmidPair& pr, int nz, hipStream_t stream) {
     if (m.swiglu_gate || pr.m[nz - 1].swiglu_gate) {
         if (!mmid_gemv_swiglu_ok(m) || (nz == 2 && !mmid_gemv_swiglu_ok(pr.m[1]))) return -2;
     }
-    if (const size_t bp = gemv_bp_lds(m)) return launch_gemv_bp(pr, nz, bp, stream);
+    if (const size_t bp = gemv_bp_lds(m, gemv_bp_direct(pr, nz))) return launch_gemv_bp(pr, nz, bp, stream);
     const size_t row_bytes = (size_t) (m.K / block_elems(m.type)) * block_bytes(m.type);
     size_t lds_bytes = (size_t) mmid_slot_bytes(row_bytes) * MMID_ROWS +
                        (size_t) mmid_stage_rows(m.max_rows) * (((m.act_row_bytes + 3) / 4) * 4 + 16);

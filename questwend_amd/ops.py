@@ -249,6 +249,9 @@ class LayerStack:
               "layer_stack_run")
         return out, xo, ids, w
 
+    def captures(self) -> int:
+        return lib().qwmoe_layer_stack_captures(self.h)
+
     def close(self) -> None:
         if self.h:
             lib().qwmoe_layer_stack_free(self.h)

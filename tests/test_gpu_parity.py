@@ -369,6 +369,33 @@ def test_layer_30b_shape(orc, types, T, permute):
     assert_status_clean()
 
 
+@pytest.mark.parametrize("t", [Q4_K, Q6_K])
+@pytest.mark.parametrize("off", [1, 2, 4])
+@pytest.mark.parametrize("moved", ["gate", "up"])
+def test_layer_gate_up_different_alignment(orc, t, off, moved):
+    """ffn_layer launches gate and up as one pair: with one of them off bytes
+    past an aligned address and the other aligned, the pair must take the loads
+    that suit both (Q4_K direct loads need 16-byte rows, Q6_K 4-byte)."""
+    note(f"ffn_layer type={t}: {moved} at byte offset {off}, the other aligned")
+    lw = LayerWeights(2048, 16, 8, 768, t, t, Q4_K, seed=300 + off + t, oracle=orc)
+    src = lw.gate if moved == "gate" else lw.up
+    buf = torch.zeros(src.size + 64, dtype=torch.uint8, device=DEV)
+    mv = buf[off:off + src.size]
+    mv.copy_(dev(src))
+    gate = mv if moved == "gate" else dev(lw.gate)
+    up = mv if moved == "up" else dev(lw.up)
+    keep = [dev(lw.router), gate, up, dev(lw.down), buf]
+    L = ops.make_layer(lw.H, lw.E, lw.k, lw.F, keep[0], keep[1], keep[2], keep[3], (t, t, Q4_K),
+                       n_slots=(lw.n_slots,) * 3)
+    for T in (1, 3):
+        x = np.random.default_rng(T + off).standard_normal((T, 2048)).astype(np.float32)
+        out, xn, ids, w = ops.ffn_layer(L, dev(x), rms_eps=1e-6)
+        r = orc.moe_layer(lw, x, rms_eps=1e-6)
+        assert np.array_equal(host(ids), r["ids"]), f"T={T}"
+        assert np.array_equal(bits(host(out)), bits(r["out"])), f"T={T}"
+    assert_status_clean()
+
+
 def test_stack_free_running(orc):
     """4 layers deep with RMSNorm between them, no teacher forcing: every
     layer's ids and the final output stay bit-identical."""

@@ -204,3 +204,35 @@ def test_layer_stack_recaptures_after_workspace_realloc(layers3):
     assert torch.equal(o1.view(torch.int32), o2.view(torch.int32))
     assert torch.equal(xo1.view(torch.int32), xo2.view(torch.int32))
     stack.close()
+
+
+def test_layer_stack_recaptures_after_threshold_change(layers3):
+    """A captured graph holds the kernel choice the matrix-core threshold made:
+    setting another threshold makes the next run capture again (same bits);
+    setting the same one does not.  The threshold outlives re-initialisation."""
+    note("layer stack: graph re-captured after qwmoe_set_mfma_min_rows changes the threshold")
+    stack = ops.LayerStack([g.layer for g in layers3], 1e-6, max_tokens=4, keepalive=layers3)
+    x = torch.from_numpy(np.random.default_rng(22).standard_normal((3, 1024)).astype(np.float32)).to(DEV)
+    prev = ops.set_mfma_min_rows(2)
+    try:
+        o1, _, ids1, _ = stack(x)
+        o1b, _, _, _ = stack(x)
+        torch.cuda.synchronize()
+        assert stack.captures() == 1
+        ops.set_mfma_min_rows(2)                       # unchanged: the graph stays
+        stack(x)
+        assert stack.captures() == 1
+        ops.set_mfma_min_rows(0)                       # every expert on the GEMV now
+        o2, _, ids2, _ = stack(x)
+        torch.cuda.synchronize()
+        assert stack.captures() == 2
+        assert torch.equal(ids1, ids2)
+        assert torch.equal(o1.view(torch.int32), o2.view(torch.int32))
+        assert torch.equal(o1.view(torch.int32), o1b.view(torch.int32))
+        ops.set_mfma_min_rows(5)
+        ops.init(0, 768 << 20)                         # reallocates the workspace
+        assert ops.set_mfma_min_rows(5) == 5           # (returns the previous value)
+    finally:
+        ops.set_mfma_min_rows(prev)
+    stack.close()
+
