@@ -6,7 +6,10 @@ goes through the C ABI; there is no CPU path.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes as C
+import sys
+import weakref
 
 from . import (BLOCK, CACHE_COPY_ENGINE, CACHE_DRY_RUN, Q8_0, Q8_K, ExpertCacheConfig, ExpertCacheStats, ExpertSrc, GgufTensorInfo, Layer,
                MoeHparams, check, lib, row_size, vec_dot_type)
@@ -176,7 +179,47 @@ def make_layer(H, E, k, F, router, gate, up, down, types, n_slots=None, slots=No
     return L
 
 
-class DecodeStack:
+# Handles (decode / layer stacks, expert caches, GGUF files) still open when
+# the program ends are freed by an atexit hook: Python runs it before the
+# interpreter shuts down and before the shared libraries' static destructors
+# (the HIP runtime's among them), so hipFree / hipHostFree, stream
+# synchronisation and worker-thread joins run against a runtime that is whole.
+# A finaliser that runs during interpreter shutdown does nothing: the process
+# is ending and its memory goes with it.
+_open_handles: "weakref.WeakSet" = weakref.WeakSet()
+
+
+@atexit.register
+def _close_open_handles() -> None:
+    for obj in list(_open_handles):
+        try:
+            obj.close()
+        except Exception:  # noqa: BLE001  (best effort at exit)
+            pass
+
+
+class _Handle:
+    h = None
+
+    def _opened(self) -> None:
+        _open_handles.add(self)
+
+    def close(self) -> None:   # each handle class frees its object in _free()
+        if self.h:
+            self._free()
+            self.h = None
+        _open_handles.discard(self)
+
+    def __del__(self):
+        if sys.is_finalizing():
+            return
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001
+            pass
+
+
+class DecodeStack(_Handle):
     """A persistent-kernel decode stack over ``layers`` (qwmoe_decode_stack_*).
 
     Keeps references to the layer tensors it points at; ``run`` pushes one
@@ -189,6 +232,7 @@ class DecodeStack:
               "decode_stack_create")
         self.h, self.n_layer, self._keep = h, len(layers), (arr, keepalive)
         self.H, self.k = layers[0].n_embd, layers[0].n_expert_used
+        self._opened()
 
     def run(self, x, out, x_out=None, ids=None, weights=None) -> None:
         check(lib().qwmoe_decode_stack_run(stream(), self.h, _ptr(x), _ptr(out), _ptr(x_out), _ptr(ids),
@@ -212,19 +256,11 @@ class DecodeStack:
         check(lib().qwmoe_decode_stack_status(stream(), self.h, C.byref(v), int(clear)), "decode_stack_status")
         return v.value
 
-    def close(self) -> None:
-        if self.h:
-            lib().qwmoe_decode_stack_free(self.h)
-            self.h = None
-
-    def __del__(self):
-        try:
-            self.close()
-        except Exception:
-            pass
+    def _free(self) -> None:
+        lib().qwmoe_decode_stack_free(self.h)
 
 
-class LayerStack:
+class LayerStack(_Handle):
     """T-token batches through a stack of MoE FFN layers (qwmoe_layer_stack_*):
     the verify forward's FFN half, one captured HIP graph per T."""
 
@@ -236,6 +272,7 @@ class LayerStack:
                                              0 if graphs else 1, C.byref(h)), "layer_stack_create")
         self.h, self.n_layer, self._keep = h, len(layers), (arr, keepalive)
         self.H, self.k = layers[0].n_embd, layers[0].n_expert_used
+        self._opened()
 
     def __call__(self, x, want_ids: bool = True):
         """x: f32 [T, H] -> (out [T, H], x_out [T, H], ids [n_layer, T, k], weights)."""
@@ -252,10 +289,8 @@ class LayerStack:
     def captures(self) -> int:
         return lib().qwmoe_layer_stack_captures(self.h)
 
-    def close(self) -> None:
-        if self.h:
-            lib().qwmoe_layer_stack_free(self.h)
-            self.h = None
+    def _free(self) -> None:
+        lib().qwmoe_layer_stack_free(self.h)
 
 
 def ffn_layer(layer: Layer, x, rms_eps: float = -1.0):
@@ -272,7 +307,7 @@ def ffn_layer(layer: Layer, x, rms_eps: float = -1.0):
     return out, xn, ids, w
 
 
-class Gguf:
+class Gguf(_Handle):
     """A GGUF model file (or shard set) opened through qwmoe_gguf_*: metadata on
     the host, MoE layers loaded into device memory on request."""
 
@@ -282,11 +317,10 @@ class Gguf:
         h = C.c_void_p()
         check(lib().qwmoe_gguf_open(str(path).encode(), C.byref(h)), "gguf_open")
         self.h = h
+        self._opened()
 
-    def close(self) -> None:
-        if self.h:
-            lib().qwmoe_gguf_close(self.h)
-            self.h = None
+    def _free(self) -> None:
+        lib().qwmoe_gguf_close(self.h)
 
     def __enter__(self):
         return self
@@ -383,7 +417,7 @@ class Gguf:
         return L, buf
 
 
-class ExpertCache:
+class ExpertCache(_Handle):
     """Expert slot pools in device memory fed from host memory or a file,
     through qwmoe_expert_cache_* (ExpertCache, core/expert_cache.h:39-166).
 
@@ -400,6 +434,7 @@ class ExpertCache:
         self._keep = []
         if _handle is not None:
             self.h = _handle
+            self._opened()
             return
         arr = (ExpertSrc * (3 * n_layer))()
         for r in range(3):
@@ -420,6 +455,7 @@ class ExpertCache:
         check(lib().qwmoe_expert_cache_create(st, n_layer, n_expert, arr, C.byref(cfg), C.byref(h)),
               "expert_cache_create")
         self.h = h
+        self._opened()
 
     @classmethod
     def from_gguf(cls, g: "Gguf", tier: int, vram_budget: int, n_used: int = 0, io_threads: int = 0,
@@ -431,16 +467,8 @@ class ExpertCache:
         hp = g.hparams()
         return cls(hp["n_layer"], hp["n_expert"], None, 0, 0, _handle=h)
 
-    def close(self) -> None:
-        if self.h:
-            lib().qwmoe_expert_cache_free(self.h)
-            self.h = None
-
-    def __del__(self):
-        try:
-            self.close()
-        except Exception:  # noqa: BLE001  (interpreter shutdown)
-            pass
+    def _free(self) -> None:
+        lib().qwmoe_expert_cache_free(self.h)
 
     def pools(self) -> list[dict]:
         out = []

@@ -144,3 +144,25 @@ def test_missing_file_and_truncated_data(files, tmp_path):
     with pytest.raises(qa.QwmoeError) as e:   # a shard of the set is missing
         ops.Gguf(tmp_path / "x-00001-of-00002.gguf")
     assert e.value.status == QWMOE_ERR_IO
+
+
+def test_open_handles_closed_at_exit(files):
+    """A handle left open is freed by the library's exit hook (which Python
+    runs before interpreter shutdown and the libraries' static destructors);
+    a closed handle leaves the registry; a process that leaves one open exits
+    cleanly."""
+    import subprocess
+    import sys
+    d, _ = files
+    g = ops.Gguf(d / "moe_tiny.gguf")
+    assert g in ops._open_handles
+    g2 = ops.Gguf(d / "moe_tiny.gguf")
+    g2.close()
+    assert g2 not in ops._open_handles and g2.h is None
+    ops._close_open_handles()
+    assert g.h is None and g not in ops._open_handles
+    code = ("import sys; sys.path.insert(0, %r); from questwend_amd import ops; "
+            "g = ops.Gguf(%r); print('open', bool(g.h))") % (str(qa.__file__.rsplit('/', 2)[0]), str(d / "moe_tiny.gguf"))
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert r.stdout.strip() == "open True"
