@@ -7,10 +7,10 @@
 //   * every pool gets the same residency fraction f = budget / total expert
 //     bytes (capped at 1), n_slots = (int) (f * n_layers_of_pool * n_expert)
 //     clamped to [n_used, n_layers_of_pool * n_expert] (cpp:155-186);
-//   * key = layer * n_expert + expert; an access bumps the key's count and, on a
-//     hit, stamps the slot with ++clock; a miss installs into the first slot with
-//     the smallest stamp (empty slots have stamp 0), evicting its key
-//     (cpp:374-410, 709-721);
+//   * key = layer * n_expert + expert; an access counts as a use of the key and,
+//     on a hit, stamps the slot with the next tick; a miss installs into the
+//     slot with the oldest stamp, the lowest such slot (empty slots have stamp
+//     0), evicting its key (cpp:374-410, 709-721);
 //   * slot_of rows hold 0 for absent experts (cpp:694-697).
 //
 // Mechanics, MI355X-first:
@@ -43,7 +43,7 @@
 #include <new>
 #include <string>
 #include <thread>
-#include <unordered_map>
+#include <tuple>
 #include <vector>
 
 #include "../../include/qwmoe.h"
@@ -67,6 +67,9 @@ int64_t row_bytes(int type, int64_t ne0) {
     }
 }
 
+// One slot pool: the experts of every layer whose tensors of one role share a
+// type and shape.  Keys are layer * n_expert + expert.  Residency is two
+// tables kept in step: what each slot holds, and where each key is.
 struct Pool {
     int role = 0, type = 0;
     int64_t ne0 = 0, ne1 = 0;
@@ -74,10 +77,16 @@ struct Pool {
     int n_layers = 0;
     int n_slots = 0;
     uint8_t* dev = nullptr;                   // [n_slots][slab]
-    std::unordered_map<int, int> key2slot;
-    std::vector<int> slot2key;                // -1: empty
-    std::vector<uint64_t> clk;                // LRU stamps
-    std::map<int, uint64_t> count;            // accesses per key (ordered: profile files list keys ascending)
+    std::vector<int32_t> holder;              // [n_slots]: the key a slot holds, -1 when empty
+    std::vector<uint64_t> stamp;              // [n_slots]: tick of its last install or hit, 0 never
+    std::vector<int32_t> home;                // [n_layer * n_expert]: the slot holding a key, -1 absent
+    int n_held = 0;                           // keys resident
+    std::map<int, uint64_t> uses;             // accesses per key (ascending keys: the profile file's order)
+
+    bool holds(int key) const { return home[(size_t) key] >= 0; }
+    // The slot a newly admitted key takes: the one used longest ago (never-used
+    // slots first), the lowest index among equal stamps.
+    int oldest() const { return (int) (std::min_element(stamp.begin(), stamp.end()) - stamp.begin()); }
 };
 
 struct Source {
@@ -180,7 +189,7 @@ struct qwmoe_expert_cache {
     std::vector<int> fds;
     std::vector<int32_t> rows;                // [3][n_layer][n_expert], 0 = absent
     size_t dirty_lo = SIZE_MAX, dirty_hi = 0; // changed span of rows
-    uint64_t clock = 0;
+    uint64_t tick = 0;                        // use counter behind the slots' stamps
     qwmoe_expert_cache_stats stats{};
     std::vector<Job> jobs;                    // installs whose slab is not fetched yet
     uint8_t* dev_block = nullptr;
@@ -229,59 +238,77 @@ struct qwmoe_expert_cache {
         dirty_hi = std::max(dirty_hi, i + 1);
     }
 
-    // Claims the LRU slot of `pool` for `key`, evicting its occupant
-    // (install / reserve_victim, cpp:374-410); the slab is fetched later.
-    int claim(int pi, int key) {
+    // Puts `key` in the oldest slot of pool pi; the key held there before (if
+    // any) is evicted and its slot-table row cleared.  The policy of the
+    // reference's install / reserve_victim (core/expert_cache.cpp:374-410); the
+    // slab itself is fetched later, with the other jobs of the call.
+    int admit(int pi, int key) {
         Pool& p = pools[pi];
-        int victim = 0;
-        uint64_t best = p.clk[0];
-        for (int s = 1; s < p.n_slots; ++s)
-            if (p.clk[s] < best) {
-                best = p.clk[s];
-                victim = s;
-            }
-        const int old = p.slot2key[victim];
-        if (old >= 0) {
-            set_row(p.role, old, 0);
-            p.key2slot.erase(old);
+        const int s = p.oldest();
+        if (const int prev = p.holder[(size_t) s]; prev >= 0) {
+            p.home[(size_t) prev] = -1;
+            --p.n_held;
+            set_row(p.role, prev, 0);
             stats.evictions++;
         }
-        p.slot2key[victim] = key;
-        p.clk[victim] = ++clock;
-        p.key2slot[key] = victim;
-        set_row(p.role, key, victim);
-        return victim;
+        p.holder[(size_t) s] = key;
+        p.home[(size_t) key] = s;
+        ++p.n_held;
+        p.stamp[(size_t) s] = ++tick;
+        set_row(p.role, key, s);
+        return s;
     }
 
     int install(int role, int layer, int expert) {
         const int pi = layer_pool[role][layer];
-        const int slot = claim(pi, layer * n_expert + expert);
+        const int slot = admit(pi, layer * n_expert + expert);
         jobs.push_back({pi, role, layer, expert, slot});
         return slot;
     }
 
-    // slot_for (cpp:709-721)
+    // The slot of (role, layer, expert), admitting it on a miss; every lookup
+    // counts as a use, a hit renews the slot's stamp (slot_for,
+    // core/expert_cache.cpp:709-721).
     int slot_for(int role, int layer, int expert) {
-        Pool& p = pool_of(role, layer);
         const int key = layer * n_expert + expert;
-        p.count[key]++;
-        auto it = p.key2slot.find(key);
-        if (it != p.key2slot.end()) {
-            stats.hits++;
-            p.clk[it->second] = ++clock;
-            return it->second;
+        Pool& p = pool_of(role, layer);
+        ++p.uses[key];
+        const int s = p.home[(size_t) key];
+        if (s < 0) {
+            stats.misses++;
+            return install(role, layer, expert);
         }
-        stats.misses++;
-        return install(role, layer, expert);
+        stats.hits++;
+        p.stamp[(size_t) s] = ++tick;
+        return s;
+    }
+
+    // Slot counts: every pool keeps the same share of its experts, the budget
+    // over the bytes of all experts of all pools (at most all of them), and at
+    // least n_used slots but never more than it has experts
+    // (core/expert_cache.cpp:155-186).  Slots start empty.
+    void size_pools(size_t budget, int n_used) {
+        size_t all_bytes = 0;
+        for (const Pool& p : pools) all_bytes += p.slab * (size_t) p.n_layers * (size_t) n_expert;
+        const double share = all_bytes == 0 ? 1.0 : std::min(1.0, (double) budget / (double) all_bytes);
+        for (Pool& p : pools) {
+            const int experts = p.n_layers * n_expert;
+            p.n_slots = std::min(experts, std::max(n_used, (int) (share * experts)));
+            p.holder.assign((size_t) p.n_slots, -1);
+            p.stamp.assign((size_t) p.n_slots, 0);
+            p.home.assign((size_t) n_layer * (size_t) n_expert, -1);
+            p.n_held = 0;
+        }
     }
 
     // Forgets installs whose fetch failed: their slots are empty again.
     void drop(const Job& j) {
         Pool& p = pools[j.pool];
         const int key = j.layer * n_expert + j.expert;
-        p.key2slot.erase(key);
-        p.slot2key[j.slot] = -1;
-        p.clk[j.slot] = 0;
+        if (p.home[(size_t) key] >= 0) --p.n_held;
+        p.home[(size_t) key] = -1;
+        p.holder[(size_t) j.slot] = -1;
+        p.stamp[(size_t) j.slot] = 0;
         set_row(p.role, key, 0);
     }
 
@@ -475,14 +502,10 @@ int build(qwmoe_expert_cache* c, void* stream, int n_layer, int n_expert, const 
     c->io_threads = cfg->io_threads > 0 ? std::min(cfg->io_threads, 64) : DEFAULT_IO_THREADS;
     c->copy_engine_only = (cfg->flags & QWMOE_CACHE_COPY_ENGINE) != 0;
 
-    // (role, type, shape) signatures and the routing of every (role, layer)
-    struct Sig {
-        int role, type;
-        int64_t ne0, ne1;
-        size_t slab;
-        int n_layers;
-    };
-    std::vector<Sig> sigs;
+    // Pools, numbered in order of first appearance (roles outer, layers inner):
+    // one per (role, type, ne0, ne1); layer_pool[r][l] names the pool of layer
+    // l's tensor of role r.
+    std::map<std::tuple<int, int, int64_t, int64_t>, int> pool_by_shape;
     bool any_file = false;
     for (int r = 0; r < N_ROLE; ++r) {
         c->layer_pool[r].assign(n_layer, -1);
@@ -510,46 +533,26 @@ int build(qwmoe_expert_cache* c, void* stream, int n_layer, int n_expert, const 
             } else {
                 return QWMOE_ERR_INVALID_ARG;
             }
-            int idx = -1;
-            for (size_t k = 0; k < sigs.size(); ++k)
-                if (sigs[k].role == r && sigs[k].type == s.type && sigs[k].ne0 == s.ne0 && sigs[k].ne1 == s.ne1) {
-                    idx = (int) k;
-                    break;
-                }
-            if (idx < 0) {
-                idx = (int) sigs.size();
-                sigs.push_back({r, s.type, s.ne0, s.ne1, slab, 0});
+            const auto [at, fresh] = pool_by_shape.try_emplace({r, s.type, s.ne0, s.ne1}, (int) c->pools.size());
+            if (fresh) {
+                Pool np;
+                np.role = r;
+                np.type = s.type;
+                np.ne0 = s.ne0;
+                np.ne1 = s.ne1;
+                np.slab = slab;
+                c->pools.push_back(std::move(np));
             }
-            sigs[idx].n_layers++;
-            c->layer_pool[r][il] = idx;
+            c->pools[(size_t) at->second].n_layers++;
+            c->layer_pool[r][il] = at->second;
         }
     }
-
-    // uniform residency fraction (cpp:155-186)
-    size_t total = 0;
-    for (const Sig& s : sigs) total += s.slab * (size_t) s.n_layers * (size_t) n_expert;
-    double frac = total ? (double) cfg->vram_budget / (double) total : 1.0;
-    if (frac > 1.0) frac = 1.0;
-    c->pools.resize(sigs.size());
+    c->size_pools(cfg->vram_budget, cfg->n_used);
     size_t dev_bytes = 0;
-    std::vector<size_t> pool_off(sigs.size());
-    for (size_t k = 0; k < sigs.size(); ++k) {
-        const int cap = sigs[k].n_layers * n_expert;
-        int n_slots = (int) (frac * cap);
-        if (n_slots < cfg->n_used) n_slots = cfg->n_used;
-        if (n_slots > cap) n_slots = cap;
-        Pool& p = c->pools[k];
-        p.role = sigs[k].role;
-        p.type = sigs[k].type;
-        p.ne0 = sigs[k].ne0;
-        p.ne1 = sigs[k].ne1;
-        p.slab = sigs[k].slab;
-        p.n_layers = sigs[k].n_layers;
-        p.n_slots = n_slots;
-        p.slot2key.assign(n_slots, -1);
-        p.clk.assign(n_slots, 0);
+    std::vector<size_t> pool_off(c->pools.size());
+    for (size_t k = 0; k < c->pools.size(); ++k) {
         pool_off[k] = dev_bytes;
-        dev_bytes += align256(p.slab * (size_t) n_slots);
+        dev_bytes += align256(c->pools[k].slab * (size_t) c->pools[k].n_slots);
     }
     c->rows.assign((size_t) N_ROLE * n_layer * n_expert, 0);
     if (c->dry) return QWMOE_OK;
@@ -561,7 +564,7 @@ int build(qwmoe_expert_cache* c, void* stream, int n_layer, int n_expert, const 
         (void) hipGetLastError();
         return QWMOE_ERR_HIP;
     }
-    for (size_t k = 0; k < sigs.size(); ++k) c->pools[k].dev = c->dev_block + pool_off[k];
+    for (size_t k = 0; k < c->pools.size(); ++k) c->pools[k].dev = c->dev_block + pool_off[k];
     c->dev_rows = (int32_t*) (c->dev_block + rows_off);
     for (int b = 0; b < 2; ++b)
         if (hipHostMalloc(&c->row_stage[b], c->rows.size() * sizeof(int32_t), hipHostMallocDefault) != hipSuccess ||
@@ -780,8 +783,7 @@ int qwmoe_expert_cache_ensure_resident(qwmoe_expert_cache* c, int layer, int exp
     if (!valid_role_layer(c, 0, layer) || expert < 0 || expert >= c->n_expert) return QWMOE_ERR_INVALID_ARG;
     const int key = layer * c->n_expert + expert;
     for (int r = 0; r < N_ROLE; ++r) {
-        Pool& p = c->pool_of(r, layer);
-        if (p.key2slot.find(key) == p.key2slot.end()) {
+        if (!c->pool_of(r, layer).holds(key)) {
             c->stats.misses++;
             c->install(r, layer, expert);
         }
@@ -793,10 +795,10 @@ int qwmoe_expert_cache_touch(qwmoe_expert_cache* c, int role, int layer, int exp
     if (!valid_role_layer(c, role, layer) || expert < 0 || expert >= c->n_expert) return QWMOE_ERR_INVALID_ARG;
     Pool& p = c->pool_of(role, layer);
     const int key = layer * c->n_expert + expert;
-    auto it = p.key2slot.find(key);
-    if (it == p.key2slot.end()) return QWMOE_OK;
-    p.count[key]++;
-    p.clk[it->second] = ++c->clock;
+    const int s = p.home[(size_t) key];
+    if (s < 0) return QWMOE_OK;
+    ++p.uses[key];
+    p.stamp[(size_t) s] = ++c->tick;
     c->stats.hits++;
     return QWMOE_OK;
 }
@@ -809,7 +811,7 @@ int qwmoe_expert_cache_verify(qwmoe_expert_cache* c, const int32_t* ids, int n_l
             const int e = ids[(size_t) l * k + i];
             if (e < 0 || e >= c->n_expert) return QWMOE_ERR_INVALID_ARG;
             for (int r = 0; r < N_ROLE; ++r)
-                if (!c->pool_of(r, l).key2slot.count(l * c->n_expert + e)) {
+                if (!c->pool_of(r, l).holds(l * c->n_expert + e)) {
                     ++missing;
                     break;
                 }
@@ -824,7 +826,7 @@ int qwmoe_expert_cache_verify(qwmoe_expert_cache* c, const int32_t* ids, int n_l
 int qwmoe_expert_cache_resident(const qwmoe_expert_cache* c, int role, int layer, int expert) {
     if (!valid_role_layer(c, role, layer) || expert < 0 || expert >= c->n_expert) return QWMOE_ERR_INVALID_ARG;
     const Pool& p = c->pools[c->layer_pool[role][layer]];
-    return p.key2slot.count(layer * c->n_expert + expert) ? 1 : 0;
+    return p.holds(layer * c->n_expert + expert) ? 1 : 0;
 }
 
 const int32_t* qwmoe_expert_cache_slot_of_row(const qwmoe_expert_cache* c, int role, int layer) {
@@ -875,7 +877,7 @@ int qwmoe_expert_cache_save_profile(const qwmoe_expert_cache* c, const char* pat
     if (!f) return QWMOE_ERR_IO;
     fprintf(f, "QWENEXPCACHE 1\n%d %d\n", c->n_layer, c->n_expert);
     for (const Pool& p : c->pools)
-        for (const auto& kv : p.count)
+        for (const auto& kv : p.uses)
             fprintf(f, "%d %d %d %llu\n", p.role, kv.first / c->n_expert, kv.first % c->n_expert,
                     (unsigned long long) kv.second);
     const bool ok = fclose(f) == 0;
@@ -907,9 +909,9 @@ int qwmoe_expert_cache_load_prefetch(qwmoe_expert_cache* c, const char* path, ui
     uint64_t n = 0;
     for (const Ent& en : ents) {
         Pool& p = c->pool_of(en.role, en.layer);
-        if ((int) p.key2slot.size() >= p.n_slots) continue;
+        if (p.n_held >= p.n_slots) continue;
         const int key = en.layer * c->n_expert + en.expert;
-        if (p.key2slot.count(key)) continue;
+        if (p.holds(key)) continue;
         c->install(en.role, en.layer, en.expert);
         n++;
     }
