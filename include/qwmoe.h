@@ -181,6 +181,38 @@ int qwmoe_weighted_sum(void * stream, const float * experts, const float * weigh
 /* ggml_rms_norm (ggml/src/ggml-cpu/ops.cpp:3795-3860) over `rows` rows of n. */
 int qwmoe_rms_norm(void * stream, const float * x, float * y, int64_t n, int64_t rows, float eps);
 
+/* ---- the step either side of the expert FFN (one decoder layer's FFN half) ---- */
+
+/* The router input of a decoder layer: y = ggml_mul(ggml_rms_norm(x, eps), w),
+ * w [n] the layer's ffn_norm (or post_attention_norm) weight, as Seg A builds
+ * it (core/runtime.cpp:2028-2030); every row rounded as those two ops round. */
+int qwmoe_rms_norm_mul(void * stream, const float * x, const float * w, float * y, int64_t n, int64_t rows,
+                       float eps);
+
+/* The shared expert of a layer (blk.N.ffn_{gate,up,down}_shexp and
+ * ffn_gate_inp_shexp). */
+typedef struct qwmoe_shared_expert {
+    int64_t n_ff;              /* rows of gate / up, columns of down */
+    int type_gate, type_up, type_down;   /* Q4_K, Q6_K or Q8_0 */
+    const void * gate;         /* [H, n_ff], row stride gate_nb1 */
+    const void * up;           /* [H, n_ff], row stride up_nb1 */
+    const void * down;         /* [n_ff, H], row stride down_nb1 */
+    size_t gate_nb1, up_nb1, down_nb1;
+    const float * gate_inp;    /* f32 [H] (the [H, 1] gate matrix) */
+} qwmoe_shared_expert;
+
+/* The shared-expert branch of build_moe (core/runtime.cpp:963-972) for T
+ * tokens: out = moe_out + down(silu(gate x) * up x) * sigmoid(gate_inp . x),
+ * plus resid when it is non-NULL (the layer's residual add).  x, moe_out, resid,
+ * out: f32 [H, T] dense; out may be moe_out.  The projections are ggml_mul_mat
+ * of the quantized weights (the mul_mat_id row dots, x quantized to the
+ * weight's vec_dot type); silu then mul rounds as swiglu does; the gate's dot
+ * follows ggml_vec_dot_f32's AVX2 order and its expf is correctly rounded.
+ * Requirements: H a multiple of 32 (and of 256 for K-quant gate/up), n_ff a
+ * multiple of 8 (and of 256 for a K-quant down). */
+int qwmoe_shared_expert_add(void * stream, const qwmoe_shared_expert * se, int64_t H, const float * x, int64_t T,
+                            const float * moe_out, const float * resid, float * out);
+
 /* ---- fused layer ------------------------------------------------------------ */
 
 /* One MoE FFN layer's tensors: the ggml graph inputs of build_moe

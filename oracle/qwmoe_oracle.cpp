@@ -808,6 +808,55 @@ void orc_rms_norm(int64_t ne0, int64_t ne1, const float * x, float * y, float ep
     for (int64_t r = 0; r < ne1; ++r) rms_norm_row((int) ne0, x + r * ne0, y + r * ne0, eps);
 }
 
+// The router input of a decoder layer: ggml_mul(ggml_rms_norm(x, eps), w)
+// (core/runtime.cpp:2028-2030; ops.cpp:3795-3860, then the element-wise
+// binary op, one rounding per op).
+void orc_rms_norm_mul(int64_t ne0, int64_t ne1, const float * x, const float * w, float * y, float eps) {
+    for (int64_t r = 0; r < ne1; ++r) {
+        rms_norm_row((int) ne0, x + r * ne0, y + r * ne0, eps);
+        for (int64_t i = 0; i < ne0; ++i) y[r * ne0 + i] = y[r * ne0 + i] * w[i];
+    }
+}
+
+// The shared-expert branch of build_moe (core/runtime.cpp:963-972), token by
+// token: g = mul_mat(gate, x), u = mul_mat(up, x) (ggml_mul_mat of a quantized
+// weight: x to the weight's vec_dot type, then one vec_dot per row),
+// a = mul(silu(g), u) (ggml_vec_silu_f32 takes ggml_v_silu for every block of 8,
+// then one multiply: vec_swiglu's rounding), sh = mul_mat(down, a),
+// sg = sigmoid(mul_mat(gate_inp, x)) with the f32 dot in vec_dot_f32's order and
+// op_sigmoid's 1 / (1 + expf(-v)) (unary-ops.cpp:31-33, libm expf), then
+// out = (moe_out + sh * sg) (+ resid): ggml_mul, ggml_add, the residual add.
+// Weights dense: gate / up [F][row(H)], down [H][row(F)]; x, moe_out, resid,
+// out [T][H].  Needs F % 8 == 0.
+int orc_shared_expert_add(int64_t H, int64_t F, int type_gate, int type_up, int type_down, const void * gate,
+                          const void * up, const void * down, const float * gate_inp, const float * x, int64_t T,
+                          const float * moe_out, const float * resid, float * out) {
+    if (F % 8) return -1;
+    const size_t rg = row_size(type_gate, H), ru = row_size(type_up, H), rd = row_size(type_down, F);
+    const int vg = vec_dot_type(type_gate), vu = vec_dot_type(type_up), vd = vec_dot_type(type_down);
+    std::vector<uint8_t> xg(row_size(vg, H)), xu(row_size(vu, H)), aq(row_size(vd, F));
+    std::vector<float> g((size_t) F), u((size_t) F), a((size_t) F);
+    for (int64_t t = 0; t < T; ++t) {
+        const float * xt = x + t * H;
+        from_float(vg, xt, xg.data(), H);
+        from_float(vu, xt, xu.data(), H);
+        for (int64_t f = 0; f < F; ++f) {
+            g[(size_t) f] = vec_dot(type_gate, (int) H, (const uint8_t *) gate + (size_t) f * rg, xg.data());
+            u[(size_t) f] = vec_dot(type_up, (int) H, (const uint8_t *) up + (size_t) f * ru, xu.data());
+        }
+        vec_swiglu((int) F, a.data(), g.data(), u.data());
+        from_float(vd, a.data(), aq.data(), F);
+        const float v = vec_dot_f32((int) H, gate_inp, xt, 2);
+        const float sg = 1.f / (1.f + expf(-v));
+        for (int64_t h = 0; h < H; ++h) {
+            const float sh = vec_dot(type_down, (int) F, (const uint8_t *) down + (size_t) h * rd, aq.data());
+            const float o = moe_out[t * H + h] + sh * sg;
+            out[t * H + h] = resid ? o + resid[t * H + h] : o;
+        }
+    }
+    return 0;
+}
+
 // Per-expert row grouping of ggml_compute_forward_mul_mat_id
 // (ggml-cpu.c:1622-1637): t outer, slot e inner.  counts[n_as]; rows holds,
 // for each expert a in 0..n_as-1 in order, its (e, t) pairs as 2 x int32,

@@ -273,6 +273,54 @@ int qwref_stack_run(qwref_layer ** Ls, int n_layer, const float * xs, int n_warm
     return 0;
 }
 
+// The shared-expert branch of build_moe (core/runtime.cpp:963-972) on the CPU
+// backend, for T tokens, as the reference builds it: g = mul_mat(gate, x),
+// u = mul_mat(up, x), sh = mul_mat(down, mul(silu(g), u)),
+// sg = sigmoid(mul_mat(gate_inp, x)), out = add(moe_out, mul(sh, sg)), then
+// add(out, resid) when resid is given.  Weights: gate / up [H, F], down [F, H]
+// of their types, gate_inp f32 [H, 1]; x, moe_out, resid, out [H, T] dense.
+int qwref_shared_expert_add(int64_t H, int64_t F, int64_t T, int type_gate, int type_up, int type_down,
+                            const void * gate, const void * up, const void * down, const float * gate_inp,
+                            const float * x, const float * moe_out, const float * resid, float * out,
+                            int n_threads) {
+    ensure_init();
+    ggml_init_params wp = { ggml_tensor_overhead() * 8, nullptr, true };
+    ggml_context * wctx = ggml_init(wp);
+    ggml_tensor * Wg = ggml_new_tensor_2d(wctx, (ggml_type) type_gate, H, F);
+    ggml_tensor * Wu = ggml_new_tensor_2d(wctx, (ggml_type) type_up, H, F);
+    ggml_tensor * Wd = ggml_new_tensor_2d(wctx, (ggml_type) type_down, F, H);
+    ggml_tensor * Wi = ggml_new_tensor_2d(wctx, GGML_TYPE_F32, H, 1);
+    Wg->data = (void *) gate; Wu->data = (void *) up; Wd->data = (void *) down; Wi->data = (void *) gate_inp;
+    const size_t bytes = sizeof(float) * (size_t) T * (size_t) (H * 8 + F * 6 + 8);
+    ggml_init_params ip = { bytes + ggml_tensor_overhead() * 32 + ggml_graph_overhead() + (1 << 20), nullptr, false };
+    ggml_context * ctx = ggml_init(ip);
+    ggml_tensor * X = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, H, T);
+    ggml_tensor * M = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, H, T);
+    memcpy(X->data, x, sizeof(float) * H * T);
+    memcpy(M->data, moe_out, sizeof(float) * H * T);
+    ggml_tensor * g = ggml_mul_mat(ctx, Wg, X);
+    ggml_tensor * u = ggml_mul_mat(ctx, Wu, X);
+    ggml_tensor * sh = ggml_mul_mat(ctx, Wd, ggml_mul(ctx, ggml_silu(ctx, g), u));
+    ggml_tensor * sg = ggml_sigmoid(ctx, ggml_mul_mat(ctx, Wi, X));
+    sh = ggml_mul(ctx, sh, sg);
+    ggml_tensor * O = ggml_add(ctx, M, sh);
+    if (resid) {
+        ggml_tensor * R = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, H, T);
+        memcpy(R->data, resid, sizeof(float) * H * T);
+        O = ggml_add(ctx, O, R);
+    }
+    ggml_cgraph * gf = ggml_new_graph(ctx);
+    ggml_build_forward_expand(gf, O);
+    ggml_cplan plan = ggml_graph_plan(gf, n_threads, nullptr);
+    std::vector<uint8_t> work(plan.work_size + 64);
+    plan.work_data = work.data();
+    const int rc = ggml_graph_compute(gf, &plan) == GGML_STATUS_SUCCESS ? 0 : -1;
+    if (rc == 0) memcpy(out, O->data, sizeof(float) * H * T);
+    ggml_free(ctx);
+    ggml_free(wctx);
+    return rc;
+}
+
 // The ISA branch this build of the ggml CPU backend takes (compile-time
 // flags): 512 for AVX-512, 256 for AVX2, 0 otherwise.
 int qwref_isa(void) {
@@ -316,7 +364,7 @@ int qwref_mul_mat_id(int type, int64_t K, int64_t N, int64_t n_as, const void * 
 // Single-op helpers on the CPU backend, used to pin the oracle op by op.
 // op: 0 soft_max rows [E, T]; 1 argsort DESC rows (i32 out); 2 rms_norm rows
 // (param = eps); 3 swiglu_split(a = gate, b = up); 4 vec_dot_f32 via mul_mat
-// of a [n, rows] by b [n, 1].
+// of a [n, rows] by b [n, 1]; 5 mul(rms_norm(a, param), b [n]).
 int qwref_unary(int op, const float * a, const float * b, int64_t ne0, int64_t ne1, float param,
                 void * dst, int n_threads) {
     ensure_init();
@@ -340,6 +388,12 @@ int qwref_unary(int op, const float * a, const float * b, int64_t ne0, int64_t n
             ggml_tensor * B = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, ne0, 1);
             memcpy(B->data, b, sizeof(float) * ne0);
             R = ggml_mul_mat(ctx, A, B);   // [ne1, 1]
+            break;
+        }
+        case 5: {   // the router input: mul(rms_norm(a, param), b) with b [ne0] broadcast over rows
+            ggml_tensor * B = ggml_new_tensor_1d(ctx, GGML_TYPE_F32, ne0);
+            memcpy(B->data, b, sizeof(float) * ne0);
+            R = ggml_mul(ctx, ggml_rms_norm(ctx, A, param), B);
             break;
         }
         default: ggml_free(ctx); return -2;

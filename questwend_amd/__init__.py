@@ -41,6 +41,17 @@ class Layer(C.Structure):
     ]
 
 
+class SharedExpert(C.Structure):
+    """Mirror of ``qwmoe_shared_expert`` (include/qwmoe.h)."""
+
+    _fields_ = [
+        ("n_ff", C.c_int64), ("type_gate", C.c_int), ("type_up", C.c_int), ("type_down", C.c_int),
+        ("gate", C.c_void_p), ("up", C.c_void_p), ("down", C.c_void_p),
+        ("gate_nb1", C.c_size_t), ("up_nb1", C.c_size_t), ("down_nb1", C.c_size_t),
+        ("gate_inp", C.c_void_p),
+    ]
+
+
 # name -> (restype, argtypes); every exported symbol of include/qwmoe.h
 P, I64, SZ, I, F, U64 = C.c_void_p, C.c_int64, C.c_size_t, C.c_int, C.c_float, C.c_uint64
 SIGNATURES = {
@@ -64,6 +75,8 @@ SIGNATURES = {
     "qwmoe_swiglu": (I, [P, P, P, P, I64, I64]),
     "qwmoe_weighted_sum": (I, [P, P, P, P, I64, I64, I64]),
     "qwmoe_rms_norm": (I, [P, P, P, I64, I64, F]),
+    "qwmoe_rms_norm_mul": (I, [P, P, P, P, I64, I64, F]),
+    "qwmoe_shared_expert_add": (I, [P, P, I64, P, I64, P, P, P]),
     "qwmoe_ffn_layer": (I, [P, P, P, I64, P, F, P, P, P]),
     "qwmoe_decode_stack_create": (I, [P, I, F, P]),
     "qwmoe_decode_stack_run": (I, [P, P, P, P, P, P, P]),

@@ -409,6 +409,80 @@ int qwmoe_rms_norm(void* stream, const float* x, float* y, int64_t n, int64_t ro
     return qw::launch_rms_norm(x, y, n, rows, eps, S(stream));
 }
 
+int qwmoe_rms_norm_mul(void* stream, const float* x, const float* w, float* y, int64_t n, int64_t rows, float eps) {
+    if (!x || !w || !y || n <= 0 || rows < 0 || !(eps >= 0.0f)) return QWMOE_ERR_INVALID_ARG;
+    return qw::launch_rms_norm(x, y, n, rows, eps, S(stream), w);
+}
+
+int qwmoe_shared_expert_add(void* stream, const qwmoe_shared_expert* se, int64_t H, const float* x, int64_t T,
+                            const float* moe_out, const float* resid, float* out) {
+    if (!g_lib.ready) return QWMOE_ERR_NOT_INITIALIZED;
+    if (!se || !x || !moe_out || !out || H <= 0 || T < 0) return QWMOE_ERR_INVALID_ARG;
+    const int64_t F = se->n_ff;
+    if (F <= 0 || !se->gate || !se->up || !se->down || !se->gate_inp) return QWMOE_ERR_INVALID_ARG;
+    if (!weight_type_ok(se->type_gate) || !weight_type_ok(se->type_up) || !weight_type_ok(se->type_down))
+        return QWMOE_ERR_UNSUPPORTED;
+    int rc;
+    if ((rc = check_k(se->type_gate, H)) || (rc = check_k(se->type_up, H)) || (rc = check_k(se->type_down, F)))
+        return rc;
+    if (F % 8 || H % 32) return QWMOE_ERR_UNSUPPORTED;   // SwiGLU in blocks of 8; the gate's 32 chains
+    if (se->gate_nb1 < qwmoe_row_size(se->type_gate, H) || se->up_nb1 < qwmoe_row_size(se->type_up, H) ||
+        se->down_nb1 < qwmoe_row_size(se->type_down, F))
+        return QWMOE_ERR_INVALID_ARG;
+    if (T == 0) return QWMOE_OK;
+    hipStream_t st = S(stream);
+    Arena ar(kReserved);
+    // every token uses "expert" 0 once: the mul_mat_id kernels then compute the
+    // dense mul_mat (same row dots as ggml_mul_mat of a quantized weight)
+    int32_t* rows = ar.take<int32_t>((size_t) (2 * T + 2));
+    int32_t* active = ar.take<int32_t>(2);
+    int32_t* active_off = ar.take<int32_t>(3);
+    int32_t* n_active = ar.take<int32_t>(1);
+    float* upo = ar.take<float>((size_t) (F * T));
+    float* gateo = ar.take<float>((size_t) (F * T));
+    float* act = ar.take<float>((size_t) (F * T));
+    float* sh = ar.take<float>((size_t) (H * T));
+    const int vg = qw::vec_dot_type(se->type_gate), vu = qw::vec_dot_type(se->type_up);
+    const int vd = qw::vec_dot_type(se->type_down);
+    const size_t qg = qwmoe_row_size(vg, H), qu = qwmoe_row_size(vu, H), qd = qwmoe_row_size(vd, F);
+    uint8_t* xg = ar.take<uint8_t>(qg * (size_t) T + 64);
+    uint8_t* xu = (vu == vg) ? xg : ar.take<uint8_t>(qu * (size_t) T + 64);
+    uint8_t* aq = ar.take<uint8_t>(qd * (size_t) T + 64);
+    if (!rows || !active || !active_off || !n_active || !upo || !gateo || !act || !sh || !xg || !xu || !aq)
+        return QWMOE_ERR_WORKSPACE;
+    if ((rc = qw::launch_group_dense(rows, active, active_off, n_active, T, st))) return rc;
+    if ((rc = qw::launch_quantize_act(vg, x, H, 1, T, (size_t) H * 4, (size_t) H * 4, xg, st))) return rc;
+    if (xu != xg && (rc = qw::launch_quantize_act(vu, x, H, 1, T, (size_t) H * 4, (size_t) H * 4, xu, st))) return rc;
+    const size_t fb = (size_t) F * 4;
+    const qw::MmidArgs mu = mmid_args(se->type_up, se->up, H, F, 1, se->up_nb1, se->up_nb1 * (size_t) F, xu, 1, qu,
+                                      rows, active, active_off, n_active, 1, nullptr, 0, upo, fb, fb, T);
+    const qw::MmidArgs mg = mmid_args(se->type_gate, se->gate, H, F, 1, se->gate_nb1, se->gate_nb1 * (size_t) F, xg, 1,
+                                      qg, rows, active, active_off, n_active, 1, nullptr, 0, gateo, fb, fb, T);
+    if (mu.mfma_min_rows == 0 && mg.mfma_min_rows == 0 && mu.type == mg.type) {
+        if ((rc = qw::launch_mmid_gemv2(mu, mg, st))) return rc;
+    } else {
+        if ((rc = mmid_launch(mu, st))) return rc;
+        if ((rc = mmid_launch(mg, st))) return rc;
+    }
+    // ggml_mul(ggml_silu(g), u) rounds as swiglu_split does: silu, then one multiply
+    qw::MmidArgs md = mmid_args(se->type_down, se->down, F, H, 1, se->down_nb1, se->down_nb1 * (size_t) H, aq, 1, qd,
+                                rows, active, active_off, n_active, 1, nullptr, 0, sh, (size_t) H * 4, (size_t) H * 4, T);
+    md.swiglu_gate = gateo;
+    md.swiglu_up = upo;
+    if (vd == qw::T_Q8_K && qw::mmid_gemv_swiglu_ok(md)) {
+        // the down GEMV forms SwiGLU's Q8_K rows itself
+    } else if (vd == qw::T_Q8_K) {
+        md.swiglu_gate = md.swiglu_up = nullptr;
+        if ((rc = qw::launch_swiglu_q8K(gateo, upo, F, T, aq, st))) return rc;
+    } else {
+        md.swiglu_gate = md.swiglu_up = nullptr;
+        if ((rc = qw::launch_swiglu(gateo, upo, act, T, F, fb, fb, fb, st))) return rc;
+        if ((rc = qw::launch_quantize_act(vd, act, F, 1, T, fb, fb, aq, st))) return rc;
+    }
+    if ((rc = mmid_launch(md, st))) return rc;
+    return qw::launch_shared_gate_add(x, (size_t) H, se->gate_inp, sh, moe_out, resid, out, (size_t) H, H, T, st);
+}
+
 int qwmoe_ffn_layer(void* stream, const qwmoe_layer* L, const float* x, int64_t T, float* out, float rms_eps,
                     float* x_next, int32_t* ids_out, float* weights_out) {
     if (!g_lib.ready) return QWMOE_ERR_NOT_INITIALIZED;

@@ -5,7 +5,11 @@
 //                            transposed experts by the weights (ggml_vec_dot_f32 of
 //                            length k); T > 1 -> mul by the weights, then an add
 //                            chain in slot order
-//   rms_norm                 ggml/src/ggml-cpu/ops.cpp:3795-3860
+//   rms_norm                 ggml/src/ggml-cpu/ops.cpp:3795-3860, then optionally
+//                            ggml_mul by a norm weight (the router input of a
+//                            decoder layer, core/runtime.cpp:2028-2030)
+//   shared-expert gate       core/runtime.cpp:963-972: sigmoid(mul_mat(gate_inp, x))
+//                            times the shared expert's output, added to the MoE output
 #include "qw_kernels.hpp"
 
 namespace qw {
@@ -83,8 +87,10 @@ int launch_weighted_sum(const float* experts, const float* weights, float* out, 
 // One row per 256-thread block.  The reference sums x*x in double, in order;
 // the tree order used here can only differ after the final rounding to float
 // when the sum lies within ~1e-13 (relative) of a float rounding boundary.
+// w (optional, [n]): ggml_mul of the normed row by the norm weight, rounded
+// after the scale as the two ops round.
 __global__ void __launch_bounds__(256) k_rms_norm(const float* __restrict__ x, float* __restrict__ y, int64_t n,
-                                                  float eps) {
+                                                  float eps, const float* __restrict__ w) {
     __shared__ double part[4];
     const float* xr = x + (int64_t) blockIdx.x * n;
     float* yr = y + (int64_t) blockIdx.x * n;
@@ -99,12 +105,78 @@ __global__ void __launch_bounds__(256) k_rms_norm(const float* __restrict__ x, f
     const double tot = (part[0] + part[1]) + (part[2] + part[3]);
     const float mean = (float) (tot / (double) n);
     const float scale = 1.0f / sqrtf(mean + eps);
-    for (int64_t i = threadIdx.x; i < n; i += 256) yr[i] = xr[i] * scale;
+    if (w)
+        for (int64_t i = threadIdx.x; i < n; i += 256) yr[i] = (xr[i] * scale) * w[i];
+    else
+        for (int64_t i = threadIdx.x; i < n; i += 256) yr[i] = xr[i] * scale;
 }
 
-int launch_rms_norm(const float* x, float* y, int64_t n, int64_t rows, float eps, hipStream_t stream) {
+int launch_rms_norm(const float* x, float* y, int64_t n, int64_t rows, float eps, hipStream_t stream,
+                    const float* weight) {
     if (rows == 0) return 0;
-    hipLaunchKernelGGL(k_rms_norm, dim3((unsigned) rows), dim3(256), 0, stream, x, y, n, eps);
+    hipLaunchKernelGGL(k_rms_norm, dim3((unsigned) rows), dim3(256), 0, stream, x, y, n, eps, weight);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+// ggml_vec_dot_f32 of H values (H % 32 == 0) in its AVX2 order: lane c < 32 of
+// the calling wave runs chain c (c, c + 32, ... fused), lane 0 returns the sum
+// tree (vec.cpp:11-140 with GGML_F32_STEP 32, GGML_F32_EPR 8).
+__device__ __forceinline__ float vec_dot_f32_wave(int64_t H, const float* x, const float* y, int lane) {
+    float c = 0.0f;
+    if (lane < 32)
+        for (int64_t s = lane; s < H; s += 32) c = __builtin_fmaf(x[s], y[s], c);
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) v[i] = __shfl(c, i);
+    float s8[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) s8[l] = (v[l] + v[16 + l]) + (v[8 + l] + v[24 + l]);
+    float t0[4];
+#pragma unroll
+    for (int l = 0; l < 4; ++l) t0[l] = s8[l] + s8[l + 4];
+    return (t0[0] + t0[1]) + (t0[2] + t0[3]);
+}
+
+// The shared expert's gate and its share of the layer output, one token per
+// 256-thread block: g = ggml_sigmoid(gate_inp . x) = 1 / (1 + expf(-dot)),
+// then out = moe_out + sh * g (and + resid when given), each op rounded as
+// ggml's mul and add round.  expf is taken in double and rounded once, which
+// gives the correctly rounded float the reference's libm expf returns (that
+// one is correctly rounded except in rare cases within 1 ulp).
+__global__ void __launch_bounds__(256) k_shared_gate_add(const float* __restrict__ x, size_t x_stride,
+                                                         const float* __restrict__ gate_inp,
+                                                         const float* __restrict__ sh, const float* moe_out,
+                                                         const float* __restrict__ resid, float* out,
+                                                         size_t o_stride, int64_t H) {
+    __shared__ float s_g;
+    const int64_t t = blockIdx.x;
+    const float* xt = x + (size_t) t * x_stride;
+    if (threadIdx.x < 64) {
+        const float d = vec_dot_f32_wave(H, gate_inp, xt, (int) threadIdx.x);
+        if (threadIdx.x == 0) {
+            const float e = (float) exp((double) (-d));
+            s_g = 1.0f / (1.0f + e);
+        }
+    }
+    __syncthreads();
+    const float g = s_g;
+    const float* mo = moe_out + (size_t) t * o_stride;
+    float* o = out + (size_t) t * o_stride;
+    const float* sht = sh + (size_t) t * H;
+    const float* rt = resid ? resid + (size_t) t * o_stride : nullptr;
+    for (int64_t h = threadIdx.x; h < H; h += 256) {
+        const float v = mo[h] + sht[h] * g;
+        o[h] = rt ? v + rt[h] : v;
+    }
+}
+
+int launch_shared_gate_add(const float* x, size_t x_stride, const float* gate_inp, const float* sh,
+                           const float* moe_out, const float* resid, float* out, size_t o_stride, int64_t H, int64_t T,
+                           hipStream_t stream) {
+    if (H % 32 != 0) return -2;
+    if (T == 0) return 0;
+    hipLaunchKernelGGL(k_shared_gate_add, dim3((unsigned) T), dim3(256), 0, stream, x, x_stride, gate_inp, sh, moe_out,
+                       resid, out, o_stride, H);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 

@@ -316,6 +316,28 @@ int launch_topk_group(const RouterArgs& ra, const float* logits, const GroupArgs
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
+__global__ void k_group_dense(int32_t* rows, int32_t* active, int32_t* active_off, int32_t* n_active, int64_t T) {
+    const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (t < T) {
+        rows[2 * t] = 0;
+        rows[2 * t + 1] = (int32_t) t;
+    }
+    if (t == 0) {
+        active[0] = 0;
+        active_off[0] = 0;
+        active_off[1] = (int32_t) T;
+        *n_active = 1;
+    }
+}
+
+int launch_group_dense(int32_t* rows, int32_t* active, int32_t* active_off, int32_t* n_active, int64_t T,
+                       hipStream_t stream) {
+    if (T <= 0 || T >= (int64_t(1) << 31)) return -2;
+    hipLaunchKernelGGL(k_group_dense, dim3((unsigned) ((T + 255) / 256)), dim3(256), 0, stream, rows, active, active_off,
+                       n_active, T);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
 int launch_group(const GroupArgs& g, hipStream_t stream) {
     if (g.n_bins <= 0 || g.n_bins >= (int64_t(1) << 30) || g.n_ids <= 0 || g.T < 0 || g.T * g.n_ids >= (int64_t(1) << 31))
         return -2;

@@ -47,6 +47,10 @@ struct GroupArgs {
 };
 constexpr int GROUP_WAVES = 16;
 int launch_group(const GroupArgs& g, hipStream_t stream);
+// The grouping of T tokens that all use matrix 0 once (a dense mul_mat through
+// the mul_mat_id kernels): rows (0, t), one active bin.
+int launch_group_dense(int32_t* rows, int32_t* active, int32_t* active_off, int32_t* n_active, int64_t T,
+                       hipStream_t stream);
 // api.cpp: changes whenever the library workspace is (re)allocated or freed (captured graphs
 // that baked in workspace addresses are stale then)
 uint64_t workspace_generation();
@@ -94,7 +98,13 @@ int launch_swiglu(const float* gate, const float* up, float* out, int64_t n_rows
                   size_t u_stride, size_t o_stride, hipStream_t stream);
 int launch_weighted_sum(const float* experts, const float* weights, float* out, int64_t H, int64_t k, int64_t T,
                         hipStream_t stream);
-int launch_rms_norm(const float* x, float* y, int64_t n, int64_t rows, float eps, hipStream_t stream);
+int launch_rms_norm(const float* x, float* y, int64_t n, int64_t rows, float eps, hipStream_t stream,
+                    const float* weight = nullptr);
+// out[t] = moe_out[t] + sh[t] * sigmoid(gate_inp . x[t]) (+ resid[t]); rows of
+// x / moe_out / resid / out at the given float strides, sh dense [T][H].
+int launch_shared_gate_add(const float* x, size_t x_stride, const float* gate_inp, const float* sh,
+                           const float* moe_out, const float* resid, float* out, size_t o_stride, int64_t H, int64_t T,
+                           hipStream_t stream);
 // k_weighted_sum then k_rms_norm of its output, in one launch (H <= 16384)
 int launch_weighted_sum_rms(const float* experts, const float* weights, float* out, float* x_next, int64_t H,
                             int64_t k, int64_t T, float eps, hipStream_t stream);

@@ -11,7 +11,7 @@ import ctypes as C
 import sys
 import weakref
 
-from . import (BLOCK, CACHE_COPY_ENGINE, CACHE_DRY_RUN, Q8_0, Q8_K, ExpertCacheConfig, ExpertCacheStats, ExpertSrc, GgufTensorInfo, Layer,
+from . import (BLOCK, CACHE_COPY_ENGINE, CACHE_DRY_RUN, Q8_0, Q8_K, ExpertCacheConfig, ExpertCacheStats, ExpertSrc, GgufTensorInfo, Layer, SharedExpert,
                MoeHparams, check, lib, row_size, vec_dot_type)
 
 
@@ -151,11 +151,34 @@ def weighted_sum(experts, weights):
     return out
 
 
-def rms_norm(x, eps: float):
+def rms_norm(x, eps: float, weight=None):
+    """ggml_rms_norm of each row of x; with ``weight`` [n], then ggml_mul by it
+    (the router input of a decoder layer)."""
     torch = _torch()
     n = x.shape[-1]
     out = torch.empty_like(x)
-    check(lib().qwmoe_rms_norm(stream(), _ptr(x), _ptr(out), n, x.numel() // n, eps), "rms_norm")
+    if weight is None:
+        check(lib().qwmoe_rms_norm(stream(), _ptr(x), _ptr(out), n, x.numel() // n, eps), "rms_norm")
+    else:
+        check(lib().qwmoe_rms_norm_mul(stream(), _ptr(x), _ptr(weight), _ptr(out), n, x.numel() // n, eps),
+              "rms_norm_mul")
+    return out
+
+
+def make_shared_expert(F: int, gate, up, down, gate_inp, types) -> SharedExpert:
+    """A qwmoe_shared_expert over dense device tensors: gate / up [F, row(H)],
+    down [H, row(F)] (uint8 rows), gate_inp f32 [H]."""
+    return SharedExpert(F, types[0], types[1], types[2], _ptr(gate), _ptr(up), _ptr(down), gate.stride(0),
+                        up.stride(0), down.stride(0), _ptr(gate_inp))
+
+
+def shared_expert_add(se: SharedExpert, x, moe_out, resid=None, out=None):
+    """moe_out + shared expert(x) (+ resid) for x, moe_out, resid f32 [T, H]."""
+    T, H = x.shape
+    if out is None:
+        out = _torch().empty_like(moe_out)
+    check(lib().qwmoe_shared_expert_add(stream(), C.byref(se), H, _ptr(x), T, _ptr(moe_out), _ptr(resid), _ptr(out)),
+          "shared_expert_add")
     return out
 
 

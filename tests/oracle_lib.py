@@ -57,6 +57,9 @@ class Oracle:
         L.orc_vec_dot_f32.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int]
         L.orc_v_expf.restype = C.c_float
         L.orc_v_expf.argtypes = [C.c_float]
+        L.orc_rms_norm_mul.argtypes = [C.c_int64, C.c_int64, C.c_void_p, C.c_void_p, C.c_void_p, C.c_float]
+        L.orc_shared_expert_add.argtypes = ([C.c_int64, C.c_int64] + [C.c_int] * 3 + [C.c_void_p] * 5 + [C.c_int64]
+                                            + [C.c_void_p] * 3)
         L.orc_v_expf_increases.restype = C.c_int64
         L.orc_v_expf_increases.argtypes = [C.c_uint32, C.c_uint32]
         L.orc_swiglu.argtypes = [C.c_int64, C.c_void_p, C.c_void_p, C.c_void_p]
@@ -128,6 +131,24 @@ class Oracle:
         y = np.zeros_like(x)
         self.lib.orc_rms_norm(x.shape[-1], x.size // x.shape[-1], _p(x), _p(y), eps)
         return y
+
+    def rms_norm_mul(self, x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        w = np.ascontiguousarray(w, np.float32)
+        y = np.zeros_like(x)
+        self.lib.orc_rms_norm_mul(x.shape[-1], x.size // x.shape[-1], _p(x), _p(w), _p(y), eps)
+        return y
+
+    def shared_expert_add(self, se: "SharedWeights", x, moe_out, resid=None) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        T, H = x.shape
+        mo = np.ascontiguousarray(moe_out, np.float32)
+        rs = None if resid is None else np.ascontiguousarray(resid, np.float32)
+        out = np.zeros((T, H), np.float32)
+        assert self.lib.orc_shared_expert_add(H, se.F, se.type_gate, se.type_up, se.type_down, _p(se.gate),
+                                              _p(se.up), _p(se.down), _p(se.gate_inp), _p(x), T, _p(mo), _p(rs),
+                                              _p(out)) == 0
+        return out
 
     def swiglu(self, gate: np.ndarray, up: np.ndarray) -> np.ndarray:
         g = np.ascontiguousarray(gate, np.float32)
@@ -248,6 +269,20 @@ def zipf_row_scales(E: int, s: float) -> np.ndarray:
     return (1.0 + 1.5 * w / w.max()).astype(np.float32)
 
 
+class SharedWeights:
+    """A shared expert's weights, seeded: gate / up [F, H] and down [H, F]
+    quantized from N(0, 0.02) fp32, gate_inp f32 [H] N(0, 0.02) (blk.N.ffn_*_shexp)."""
+
+    def __init__(self, H, F, type_gate, type_up, type_down, seed, oracle: Oracle):
+        rng = np.random.default_rng(seed)
+        self.H, self.F = H, F
+        self.type_gate, self.type_up, self.type_down = type_gate, type_up, type_down
+        self.gate = oracle.quantize(type_gate, (rng.standard_normal((F, H)) * 0.02).astype(np.float32))
+        self.up = oracle.quantize(type_up, (rng.standard_normal((F, H)) * 0.02).astype(np.float32))
+        self.down = oracle.quantize(type_down, (rng.standard_normal((H, F)) * 0.02).astype(np.float32))
+        self.gate_inp = (rng.standard_normal(H) * 0.02).astype(np.float32)
+
+
 class RefGGML:
     def __init__(self, path: Path = REF_SO):
         if not path.exists():
@@ -270,6 +305,19 @@ class RefGGML:
         L.qwref_stack_run.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p,
                                       C.c_void_p, C.c_void_p, C.c_int]
         L.qwref_isa.restype = C.c_int
+        L.qwref_shared_expert_add.argtypes = ([C.c_int64, C.c_int64, C.c_int64] + [C.c_int] * 3 + [C.c_void_p] * 8
+                                              + [C.c_int])
+
+    def shared_expert_add(self, se: SharedWeights, x, moe_out, resid=None, n_threads=4):
+        x = np.ascontiguousarray(x, np.float32)
+        T, H = x.shape
+        mo = np.ascontiguousarray(moe_out, np.float32)
+        rs = None if resid is None else np.ascontiguousarray(resid, np.float32)
+        out = np.zeros((T, H), np.float32)
+        assert self.lib.qwref_shared_expert_add(H, se.F, T, se.type_gate, se.type_up, se.type_down, _p(se.gate),
+                                                _p(se.up), _p(se.down), _p(se.gate_inp), _p(x), _p(mo), _p(rs),
+                                                _p(out), n_threads) == 0
+        return out
 
     def isa(self) -> int:
         """512: this build takes ggml's AVX-512 branch; 256: AVX2."""

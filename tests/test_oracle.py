@@ -181,6 +181,41 @@ def test_stack_run_avx2_bit_exact_and_avx512_within_tolerance(orc):
 
 
 @needs_ref
+def test_rms_norm_mul_matches_ggml(orc):
+    """The router input of a decoder layer: mul(rms_norm(x), w) bit for bit."""
+    ref = RefGGML()
+    rng = np.random.default_rng(41)
+    for n, rows in ((2048, 3), (4096, 1), (512, 7)):
+        x = (rng.standard_normal((rows, n)) * 3).astype(np.float32)
+        w = (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+        got = orc.rms_norm_mul(x, w, 1e-6)
+        want = ref.unary(5, x, w, param=1e-6)
+        assert np.array_equal(got.view(np.int32), want.view(np.int32)), (n, rows)
+        assert not np.array_equal(got, orc.rms_norm(x, 1e-6))      # the weight is applied
+
+
+@needs_ref
+@pytest.mark.parametrize("types", [(Q4_K, Q4_K, Q4_K), (Q4_K, Q4_K, Q6_K), (Q8_0, Q8_0, Q8_0)])
+@pytest.mark.parametrize("T", [1, 3])
+def test_shared_expert_matches_ggml(orc, types, T):
+    """The shared-expert branch (silu, mul, sigmoid gate, adds) bit for bit
+    against the reference graph, with and without the residual add."""
+    from oracle_lib import SharedWeights
+    se = SharedWeights(1024, 512, *types, seed=60 + T, oracle=orc)
+    rng = np.random.default_rng(T)
+    x = rng.standard_normal((T, 1024)).astype(np.float32)
+    mo = rng.standard_normal((T, 1024)).astype(np.float32)
+    res = rng.standard_normal((T, 1024)).astype(np.float32)
+    ref = RefGGML()
+    for resid in (None, res):
+        got = orc.shared_expert_add(se, x, mo, resid)
+        want = ref.shared_expert_add(se, x, mo, resid)
+        assert np.array_equal(got.view(np.int32), want.view(np.int32))
+    # the branch is not a no-op: its share moves the output
+    assert np.abs(orc.shared_expert_add(se, x, mo) - mo).max() > 1e-3
+
+
+@needs_ref
 def test_mul_mat_id_matches_ggml(orc):
     ref = RefGGML()
     rng = np.random.default_rng(3)
