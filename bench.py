@@ -206,13 +206,51 @@ def cpu_reference_stack(layers, xs, n_warmup: int, gpu_out, gpu_ids, gpu_layer=N
     return base, par
 
 
-def zipf_row_scales(E: int, s: float):
-    """Router row scales following a Zipf(s) rank profile (mean about 1): experts
-    with larger logit variance win the top-k more often, which skews the
-    per-expert row counts of a prefill batch towards low ids."""
+def zipf_router_scales(E: int = 128, k: int = 8, s: float = 1.1, T: int = 512, cap_frac: float = 0.55,
+                       iters: int = 120, n: int = 20000, seed: int = 1234):
+    """configs[2]'s skewed gate: per-expert router row scales under which the
+    chance that expert i is among a token's top k follows a Zipf(s) rank profile,
+    p_i = min(cap, C i^-s) with C such that the k picks per token add up.  With
+    a scale-only skew an expert saturates near half of the tokens, so the profile
+    is capped at cap_frac of them; far down the tail the fit runs out of
+    probability and those experts get almost nothing (a batch of T tokens then
+    has row counts from 0 to about 250, the configured "0 to about 300").
+
+    The router rows are random, so a token's logits are independent normals
+    scaled row by row; the scales are fitted on n such draws by a fixed-point
+    iteration (deterministic, ~1 s).  Top-k ignores a common factor, so the
+    scales are returned with the largest at 1: every row stays within the
+    configured N(0, 0.02) size and the logits within a few units (no softmax
+    underflow to exact ties).  float32 [E]."""
     import numpy as np
-    w = np.arange(1, E + 1, dtype=np.float64) ** (-s)
-    return (1.0 + 1.5 * w / w.max()).astype(np.float32)
+    p = np.arange(1, E + 1, dtype=np.float64) ** (-s)
+    cap = cap_frac * T
+    lo, hi = 0.0, 1e9
+    for _ in range(200):                      # C: the capped profile sums to k picks per token
+        C = 0.5 * (lo + hi)
+        lo, hi = (C, hi) if np.minimum(cap, C * p).sum() < k * T else (lo, C)
+    target = np.minimum(cap, C * p) / T
+    z = np.random.default_rng(seed).standard_normal((n, E)).astype(np.float32)
+    sc = np.ones(E)
+    for _ in range(iters):
+        top = np.argpartition(-(z * sc.astype(np.float32)), k - 1, axis=1)[:, :k]
+        freq = np.bincount(top.ravel(), minlength=E) / n
+        sc *= np.clip((target / np.maximum(freq, 1e-6)) ** 0.5, 0.5, 2.0)
+        sc /= np.exp(np.log(sc).mean())
+    return (sc / sc.max()).astype(np.float32)
+
+
+def row_count_profile(counts) -> dict:
+    """Shape of a batch's per-expert row counts: largest, experts with none, and
+    the log-log slope of the sorted counts over ranks 5..100 (a Zipf(s) profile
+    gives -s)."""
+    import numpy as np
+    c = np.sort(np.asarray(counts))[::-1].astype(np.float64)
+    r = np.arange(1, c.size + 1)
+    m = (r >= 5) & (r <= min(100, c.size)) & (c > 0)
+    slope = float(np.polyfit(np.log(r[m]), np.log(c[m]), 1)[0]) if m.sum() > 2 else None
+    return {"max_rows": int(c[0]), "experts_with_no_rows": int((c == 0).sum()),
+            "loglog_slope_rank5_100": None if slope is None else round(slope, 3)}
 
 
 def prefill(args) -> int:
@@ -229,7 +267,7 @@ def prefill(args) -> int:
     dev = "cuda:0"
     router = torch.empty((E, H), dtype=torch.float32, device=dev)
     ops.randn_(router, args.seed * 1000 + 1, 0.0, 0.02)
-    router *= torch.from_numpy(zipf_row_scales(E, 1.1)).to(dev)[:, None]
+    router *= torch.from_numpy(zipf_router_scales(E, K_USED, 1.1, T)).to(dev)[:, None]
     mats = []
     tmp = torch.empty(16 * F * H, dtype=torch.float32, device=dev)
     for role, (rows, cols) in enumerate(((F, H), (F, H), (H, F))):
@@ -281,7 +319,7 @@ def prefill(args) -> int:
         "config": {"workload": "Qwen3-30B-A3B MoE FFN layer, prefill T=512 (configs[2])", "n_embd": H,
                    "n_expert": E, "n_expert_used": K_USED, "n_ff_exp": F, "tokens": T, "weights": "Q4_K",
                    "path": f"qwmoe_ffn_layer (mfma_min_rows {args.mfma_min_rows})"},
-        "rows_per_expert": {"max": int(counts.max()), "ge32": int((counts >= 32).sum()), "unused": int((counts == 0).sum())},
+        "rows_per_expert": {**row_count_profile(counts), "ge32": int((counts >= 32).sum())},
         "roofline": {"bound": "hbm", "achieved": round(wbytes / ev_s / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(wbytes / ev_s / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
                      "bytes_per_step": wbytes, "avg_step_ms": round(ev_s * 1e3, 4),

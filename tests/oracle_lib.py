@@ -258,15 +258,13 @@ class LayerWeights:
         self.down = np.ascontiguousarray(qd.reshape(-1))
 
 
-def zipf_row_scales(E: int, s: float) -> np.ndarray:
-    """Per-expert router row scales that skew top-k popularity towards low ids.
-
-    Larger logit variance for popular experts makes them win the top-k more
-    often; the scale follows a Zipf(s) rank profile, normalised to mean 1.
-    """
-    ranks = np.arange(1, E + 1, dtype=np.float64)
-    w = ranks ** (-s)
-    return (1.0 + 1.5 * w / w.max()).astype(np.float32)
+def zipf_row_scales(E: int, s: float, k: int = 8, T: int = 512) -> np.ndarray:
+    """The benchmark's configs[2] skew (bench.zipf_router_scales): router row
+    scales under which expert popularity follows a Zipf(s) rank profile."""
+    import sys
+    sys.path.insert(0, str(ROOT))
+    from bench import zipf_router_scales
+    return zipf_router_scales(E, k, s, T)
 
 
 class SharedWeights:

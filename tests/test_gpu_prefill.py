@@ -215,6 +215,11 @@ def test_prefill_layer_30b_shape(orc, T):
     counts = np.bincount(r["ids"].reshape(-1), minlength=E)
     note(f"  rows per expert: max {counts.max()}, experts >= 32 rows: {int((counts >= 32).sum())}, "
          f"unused: {int((counts == 0).sum())}")
+    # the configured skew: counts from 0 to a few hundred, Zipf-like in between
+    from bench import row_count_profile
+    prof = row_count_profile(counts)
+    assert prof["max_rows"] >= 150 and prof["experts_with_no_rows"] >= 1, prof
+    assert -1.6 < prof["loglog_slope_rank5_100"] < -0.7, prof
     assert np.array_equal(ids, r["ids"])
     assert np.array_equal(bits(w), bits(r["weights"]))
     note(f"  output rel err {rel_err(out, r['out']):.3e}, rms_norm rel err {rel_err(xn, r['xnext']):.3e}")
@@ -274,6 +279,7 @@ def test_layer_config5_shape_permuted_slots(orc, T):
     to the oracle (whose slot handling the parity tests pin at smaller shapes)."""
     H, E, k, F, types = C5
     note(f"ffn_layer config-5 shape T={T}, permuted slots")
+    ops.device_status(clear=True)
     g = GpuLayerTyped(H, E, k, F, types, seed=900 + T, permute=True)
     x = np.random.default_rng(T + 50).standard_normal((T, H)).astype(np.float32)
     out, xn, ids, w = ops.ffn_layer(g.layer, dev(x), rms_eps=1e-6)
