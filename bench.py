@@ -119,7 +119,7 @@ def cpu_reference_stack(layers, xs, n_warmup: int, gpu_out, gpu_ids, gpu_layer=N
     stay within 1e-3."""
     import numpy as np
     sys.path.insert(0, str(ROOT / "tests"))
-    from oracle_lib import Q4_K, REF_SO, REF_SO_AVX512, LayerWeights, RefGGML
+    from oracle_lib import Q4_K, REF_SO, REF_SO_AVX512, LayerWeights, RefGGML, have_ref_avx512
     if not REF_SO.exists():
         return None, None
     cpu = host_cpu()
@@ -135,10 +135,7 @@ def cpu_reference_stack(layers, xs, n_warmup: int, gpu_out, gpu_ids, gpu_layer=N
         lw.n_slots, lw.slot_of = E, None
         lws.append(lw)
     t_copy = time.perf_counter() - t0
-    flags = Path("/proc/cpuinfo").read_text() if Path("/proc/cpuinfo").exists() else ""
-    need = ("avx512f", "avx512cd", "avx512vl", "avx512dq", "avx512bw", "avx512vbmi", "avx512_vnni", "avx512_bf16",
-            "avx_vnni")
-    has512 = REF_SO_AVX512.exists() and all(f" {f}" in flags for f in need)
+    has512 = have_ref_avx512()
     runs = {}
     for name, path in (("avx2", REF_SO), ("avx512", REF_SO_AVX512 if has512 else None)):
         if path is None:
@@ -282,8 +279,8 @@ def prefill(args) -> int:
     ops.randn_(x, args.seed + 555, 0.0, 1.0)
     torch.cuda.synchronize()
 
-    def timed(min_rows: int):
-        prev = ops.set_mfma_min_rows(min_rows)
+    def timed(min_rows: int, form: int = ops.MFMA_AUTO):
+        prev, prev_f = ops.set_mfma_min_rows(min_rows), ops.set_mfma_form(form)
         try:
             for _ in range(args.warmup):
                 ops.ffn_layer(L, x, rms_eps=RMS_EPS)
@@ -300,10 +297,17 @@ def prefill(args) -> int:
             return wall / args.steps, sum(a.elapsed_time(b) for a, b in evs) / args.steps / 1000.0, r
         finally:
             ops.set_mfma_min_rows(prev)
+            ops.set_mfma_form(prev_f)
 
     step_s, ev_s, (out, xn, ids, w) = timed(args.mfma_min_rows)
+    exact_s, _, (out_x, _, _, _) = timed(args.mfma_min_rows, ops.MFMA_EXACT)
+    bs_s, _, (out_b, _, _, _) = timed(args.mfma_min_rows, ops.MFMA_BLOCK_SUM)
     gemv_s, _, (out_g, _, _, _) = timed(0)
-    same = bool(torch.equal(out.view(torch.int32), out_g.view(torch.int32)))
+
+    def rel(a):   # vs the GEMV, which (like the exact matrix-core form) replays ggml's float steps
+        return float(f"{float((a.double() - out_g.double()).abs().max() / out_g.double().abs().max().clamp_min(1e-30)):.3e}")
+
+    same = bool(torch.equal(out_x.view(torch.int32), out_g.view(torch.int32)))
     counts = np.bincount(ids.cpu().numpy().reshape(-1), minlength=E)
     expert_bytes = 2 * F * row_size(Q4_K, H) + H * row_size(Q4_K, F)
     wbytes = int((counts > 0).sum()) * expert_bytes + E * H * 4          # unique weights touched + router
@@ -318,15 +322,20 @@ def prefill(args) -> int:
         "dtype": "q4_K x q8_K -> int32 (MFMA i8) -> f32", "data": "synthetic (seeded, router Zipf(1.1)-skewed)",
         "config": {"workload": "Qwen3-30B-A3B MoE FFN layer, prefill T=512 (configs[2])", "n_embd": H,
                    "n_expert": E, "n_expert_used": K_USED, "n_ff_exp": F, "tokens": T, "weights": "Q4_K",
-                   "path": f"qwmoe_ffn_layer (mfma_min_rows {args.mfma_min_rows})"},
+                   "path": f"qwmoe_ffn_layer (mfma_min_rows {args.mfma_min_rows}, auto matrix-core form: "
+                           "gate/up lane-exact, down block sums)"},
         "rows_per_expert": {**row_count_profile(counts), "ge32": int((counts >= 32).sum())},
         "roofline": {"bound": "hbm", "achieved": round(wbytes / ev_s / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(wbytes / ev_s / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
                      "bytes_per_step": wbytes, "avg_step_ms": round(ev_s * 1e3, 4),
                      "int8_mac_rate_tops": round(macs / ev_s / 1e12, 2),
                      "int8_mac_frac_of_2500_tmacs": round(macs / ev_s / 2.5e15, 4)},
+        "rel_err_vs_gemv": rel(out),
+        "exact_mfma_ms_per_step": round(exact_s * 1e3, 4),
+        "exact_mfma_equals_gemv_bitwise": same,
+        "block_sum_everywhere_ms_per_step": round(bs_s * 1e3, 4),
+        "block_sum_everywhere_rel_err_vs_gemv": rel(out_b),
         "gemv_only_ms_per_step": round(gemv_s * 1e3, 4),
-        "mfma_equals_gemv_bitwise": same,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

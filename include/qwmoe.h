@@ -72,13 +72,34 @@ const char * qwmoe_strerror(int status);
 /* Experts that receive at least `rows` rows in one mul_mat_id (prefill and
  * large verify batches) are computed on the int8 matrix cores
  * (v_mfma_i32_16x16x32_i8 / 16x16x64_i8) when the weight type is Q4_K; lighter
- * experts, and every expert when rows == 0, use the LDS-tiled GEMV.  Both are
- * bit-identical to ggml (the matrix-core kernel forms the eight AVX2 lane sums
- * and four min lanes exactly and replays their float steps).  Default 8.  No
- * reference counterpart: ggml's CPU backend has one dot product per type
- * (ggml-cpu.c:1463-1524); this only selects the GPU kernel. */
+ * experts, and every expert when rows == 0, use the LDS-tiled GEMV, which is
+ * bit-identical to ggml.  Default 8.  No reference counterpart: ggml's CPU
+ * backend has one dot product per type (ggml-cpu.c:1463-1524); this only
+ * selects the GPU kernel. */
 int qwmoe_set_mfma_min_rows(int rows);
 int qwmoe_get_mfma_min_rows(void);
+/* How the matrix-core kernel forms its floats (no reference counterpart).
+ * Every form computes ggml's integers exactly: per super-block the eight AVX2
+ * lane sums and the four min lanes of ggml_vec_dot_q4_K_q8_K.
+ *   QWMOE_MFMA_EXACT: replays ggml's float steps lane for lane (eight fp32 fma
+ *       chains and hsum_float_8): bit-identical to the CPU backend;
+ *   QWMOE_MFMA_BLOCK_SUM: adds each super-block's exact integer sums in one
+ *       fp32 chain (and one for the mins): the same integers, floats rounded in
+ *       another order (~1e-6 of the output's magnitude), ~2.5x faster per
+ *       projection.  A projection whose output is re-quantized downstream (gate
+ *       and up: SwiGLU, then Q8_K for the down projection) can then move a Q8_K
+ *       value that sat at a rounding boundary by one step, which moves that
+ *       token's layer output by up to ~1.5e-3 of its magnitude;
+ *   QWMOE_MFMA_AUTO (default): the exact form wherever the output may be
+ *       re-quantized -- qwmoe_mul_mat_id (its consumer is the caller's) and the
+ *       gate/up projections of qwmoe_ffn_layer, qwmoe_shared_expert_add and the
+ *       layer stacks -- and the block-sum form for their down projections, whose
+ *       fp32 outputs only reach the weighted sum.  Layer outputs stay within
+ *       ~1e-6 of ggml's.
+ * Captured layer-stack graphs are re-captured when the setting changes. */
+enum { QWMOE_MFMA_BLOCK_SUM = 0, QWMOE_MFMA_EXACT = 1, QWMOE_MFMA_AUTO = 2 };
+int qwmoe_set_mfma_form(int form);
+int qwmoe_get_mfma_form(void);
 /* Bytes used by the workspace of the most demanding call so far. */
 size_t qwmoe_workspace_high_water(void);
 

@@ -61,6 +61,8 @@ SIGNATURES = {
     "qwmoe_workspace_high_water": (SZ, []),
     "qwmoe_set_mfma_min_rows": (I, [I]),
     "qwmoe_get_mfma_min_rows": (I, []),
+    "qwmoe_set_mfma_form": (I, [I]),
+    "qwmoe_get_mfma_form": (I, []),
     "qwmoe_row_size": (SZ, [I, I64]),
     "qwmoe_vec_dot_type": (I, [I]),
     "qwmoe_device_status": (I, [P, P, I]),

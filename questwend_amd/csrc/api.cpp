@@ -27,6 +27,7 @@ struct Library {
     size_t high_water = 0;
     int32_t* status = nullptr;   // device status word (first 256 bytes of the arena)
     int mfma_min_rows = 8;       // experts with this many routed rows use the matrix-core kernel (0: never)
+    int mfma_form = QWMOE_MFMA_AUTO;   // matrix cores' float tail (QWMOE_MFMA_*)
 };
 
 Library g_lib;
@@ -103,8 +104,13 @@ qw::MmidArgs mmid_args(int type, const void* as, int64_t K, int64_t N, int64_t n
     m.max_rows = max_rows;
     const bool mfma = g_lib.mfma_min_rows > 0 && max_rows >= g_lib.mfma_min_rows && qw::mmid_mfma_supported(m);
     if (mfma) m.mfma_min_rows = g_lib.mfma_min_rows;
+    m.mfma_exact = g_lib.mfma_form != QWMOE_MFMA_BLOCK_SUM;
     return m;
 }
+
+// The matrix-core form of a down projection inside a layer entry point: its
+// fp32 output only reaches the weighted sum, so QWMOE_MFMA_AUTO takes block sums.
+int down_mfma_exact() { return g_lib.mfma_form == QWMOE_MFMA_EXACT; }
 
 int mmid_launch(const qw::MmidArgs& m, hipStream_t st) {
     int rc = qw::launch_mmid_gemv(m, st);
@@ -173,12 +179,13 @@ extern "C" {
 
 int qwmoe_init(int device, size_t workspace_bytes) {
     std::lock_guard<std::mutex> lk(g_mu);
-    const int mfma_min_rows = g_lib.mfma_min_rows;   // a setting, kept across re-initialisation
+    const int mfma_min_rows = g_lib.mfma_min_rows, mfma_form = g_lib.mfma_form;   // settings, kept across re-init
     if (g_lib.ready) {
         if (g_lib.device == device && (workspace_bytes == 0 || workspace_bytes <= g_lib.ws_bytes)) return QWMOE_OK;
         (void) hipFree(g_lib.ws);
         g_lib = Library{};
         g_lib.mfma_min_rows = mfma_min_rows;
+        g_lib.mfma_form = mfma_form;
     }
     if (hipSetDevice(device) != hipSuccess) return QWMOE_ERR_HIP;
     const size_t bytes = workspace_bytes ? workspace_bytes : ((size_t) 256 << 20);
@@ -203,9 +210,10 @@ int qwmoe_shutdown(void) {
     if (!g_lib.ready) return QWMOE_OK;
     (void) hipDeviceSynchronize();
     (void) hipFree(g_lib.ws);
-    const int mfma_min_rows = g_lib.mfma_min_rows;
+    const int mfma_min_rows = g_lib.mfma_min_rows, mfma_form = g_lib.mfma_form;
     g_lib = Library{};
     g_lib.mfma_min_rows = mfma_min_rows;
+    g_lib.mfma_form = mfma_form;
     g_ws_generation.fetch_add(1);
     return QWMOE_OK;
 }
@@ -237,6 +245,19 @@ int qwmoe_set_mfma_min_rows(int rows) {
 }
 
 int qwmoe_get_mfma_min_rows(void) { return g_lib.mfma_min_rows; }
+
+int qwmoe_set_mfma_form(int form) {
+    if (form != QWMOE_MFMA_BLOCK_SUM && form != QWMOE_MFMA_EXACT && form != QWMOE_MFMA_AUTO)
+        return QWMOE_ERR_INVALID_ARG;
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (g_lib.mfma_form != form) {
+        g_lib.mfma_form = form;
+        g_ws_generation.fetch_add(1);   // captured graphs chose the kernel with the old setting
+    }
+    return QWMOE_OK;
+}
+
+int qwmoe_get_mfma_form(void) { return g_lib.mfma_form; }
 
 size_t qwmoe_workspace_high_water(void) { return g_lib.high_water; }
 
@@ -467,6 +488,7 @@ int qwmoe_shared_expert_add(void* stream, const qwmoe_shared_expert* se, int64_t
     // ggml_mul(ggml_silu(g), u) rounds as swiglu_split does: silu, then one multiply
     qw::MmidArgs md = mmid_args(se->type_down, se->down, F, H, 1, se->down_nb1, se->down_nb1 * (size_t) H, aq, 1, qd,
                                 rows, active, active_off, n_active, 1, nullptr, 0, sh, (size_t) H * 4, (size_t) H * 4, T);
+    md.mfma_exact = down_mfma_exact();
     md.swiglu_gate = gateo;
     md.swiglu_up = upo;
     if (vd == qw::T_Q8_K && qw::mmid_gemv_swiglu_ok(md)) {
@@ -578,6 +600,7 @@ int qwmoe_ffn_layer(void* stream, const qwmoe_layer* L, const float* x, int64_t 
     qw::MmidArgs md = mmid_args(L->type_down, L->down, F, H, L->n_slots_down, L->down_nb1, L->down_nb2, aq, k, qd,
                                 G.rows, G.active, G.active_off, G.n_active, G.max_active, L->slot_down,
                                 L->slot_down ? E : 0, ex, (size_t) H * 4, (size_t) H * 4 * (size_t) k, T);
+    md.mfma_exact = down_mfma_exact();
     md.swiglu_gate = gateo;
     md.swiglu_up = upo;
     if (vd == qw::T_Q8_K && qw::mmid_gemv_swiglu_ok(md)) {

@@ -227,6 +227,187 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
 }
 
+// The block-sum form (mfma_exact == 0).  Same integers, fewer float steps:
+// per (weight row, activation row, super-block) the eight AVX lanes' sums add up
+// in the MFMA's own int32 accumulator (sumi = sum_L sumi_L, the block's exact
+// integer dot with its scales; |sumi| < 2^25), the mins likewise (prod = sum_m
+// prod_m), and the float steps are acc = fma(d_i, sumi, acc) and
+// accm = fma(dmin_i, prod, accm) over the super-blocks, then acc + accm.  The
+// integers are ggml's exactly; the floats round in another order (relative
+// difference ~1e-7 of the terms), inside the 1e-3 bar.  Each wave keeps four
+// 16-row activation tiles per pass (64 rows), so a weight row's operand is
+// formed once for all of them and the tile is streamed a quarter as often.
+constexpr int MF_NB = 4;                               // activation tiles per pass
+constexpr int MF_N4 = 16 * MF_NB;                      // activation rows per pass
+
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) k_mmid_mfma_q4k_bs(MmidArgs m) {
+    __shared__ __align__(16) uint8_t s_w[2][MF_M * MF_WS];
+    __shared__ __align__(16) uint8_t s_a[2][MF_N4 * MF_AS];
+    __shared__ int32_t s_arow[MF_N4];
+    __shared__ int32_t s_et[MF_N4][2];
+    const int tiles = (int) (m.N / MF_M);
+    const int tile = (int) (blockIdx.x % (uint32_t) tiles);
+    const int g = (int) (blockIdx.x / (uint32_t) tiles);
+    if (g >= *m.n_active) return;
+    const int p0 = m.active_off[g], p1 = m.active_off[g + 1];
+    if (p1 - p0 < m.mfma_min_rows) return;   // light expert: the GEMV kernel's
+    const int bin = m.active[g];
+    int64_t mat = bin;
+    if (m.slot_of) mat = (bin < m.n_slot_of) ? m.slot_of[bin] : -1;
+    if (mat < 0 || mat >= m.n_as) {
+        if (threadIdx.x == 0 && m.status) atomicOr(m.status, 4);
+        return;
+    }
+    const int64_t r0 = (int64_t) tile * MF_M;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int lr = lane & 15, gq = lane >> 4;
+    const int nb = (int) (m.K / QK_K);
+    const uint8_t* wtile = m.w + (size_t) mat * m.nb2 + (size_t) r0 * m.nb1;
+    const __amdgpu_buffer_rsrc_t wrsrc = buffer_rsrc(wtile, (uint32_t) (MF_M * m.nb1));
+    const __amdgpu_buffer_rsrc_t arsrc = buffer_rsrc(m.act_q, 0x7fffffffu);
+    const int arow_l = 16 * wave + lr;
+    for (int pass = 0;; ++pass) {
+    const int pc = p0 + MF_N4 * pass;
+    if (pc >= p1) break;
+    const int ntok = (p1 - pc) < MF_N4 ? (p1 - pc) : MF_N4;
+    lds_barrier();
+    if (tid < MF_N4) {
+        const int pp = pc + (tid < ntok ? tid : 0);
+        const int e = m.rows[2 * pp], t = m.rows[2 * pp + 1];
+        s_et[tid][0] = e;
+        s_et[tid][1] = t;
+        s_arow[tid] = (int) ((int64_t) (e % m.b_ne1) + (int64_t) t * m.b_ne1);
+    }
+    lds_barrier();
+    // staging: thread (row n = tid / 4, sub = tid % 4) copies dwords c = sub + 4 j of
+    // activation row n (65: d, then the 64 of qs) and 16-byte chunks c = sub + 4 j of
+    // weight row n (9 per row): one base offset per thread, the rest immediates
+    const int sn = tid >> 2, sub = tid & 3;
+    const uint32_t abase = (uint32_t) s_arow[sn < ntok ? sn : 0] * (uint32_t) m.act_row_bytes + 4u * (uint32_t) sub;
+    const uint32_t adst = (uint32_t) (sn * MF_AS + 12 + 4 * sub);   // dword c >= 1 at adst + 16 j; c = 0 (the d) at sn * MF_AS
+    const uint32_t wbase = (uint32_t) sn * (uint32_t) m.nb1 + 16u * (uint32_t) sub;
+    const uint32_t wdst = (uint32_t) (sn * MF_WS + 16 * sub);
+    constexpr int AJ = 17, WJ = 3;   // c = sub + 4 j <= 64 (activations), <= 8 (weights)
+    u32x4m wreg[WJ];
+    uint32_t areg[AJ];
+    auto load = [&](int i) {
+        const uint32_t wi = wbase + (uint32_t) i * 144u, ai = abase + (uint32_t) i * 292u;
+#pragma unroll
+        for (int jj = 0; jj < WJ; ++jj)
+            if (sub + 4 * jj <= 8)
+                wreg[jj] = __builtin_bit_cast(u32x4m, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, wi + 64u * jj, 0, 0));
+#pragma unroll
+        for (int jj = 0; jj < AJ; ++jj)
+            if (sub + 4 * jj <= 64) areg[jj] = __builtin_amdgcn_raw_buffer_load_b32(arsrc, ai + 16u * jj, 0, 0);
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int jj = 0; jj < WJ; ++jj)
+            if (sub + 4 * jj <= 8) *(u32x4m*) (s_w[buf] + wdst + 64 * jj) = wreg[jj];
+        *(uint32_t*) (s_a[buf] + (sub == 0 ? (uint32_t) (sn * MF_AS) : adst)) = areg[0];
+#pragma unroll
+        for (int jj = 1; jj < AJ; ++jj)
+            if (sub + 4 * jj <= 64) *(uint32_t*) (s_a[buf] + adst + 16 * jj) = areg[jj];
+    };
+    // rows of activation tile bt past ntok are staged from row 0 and never written out
+    float acc[MF_NB][4], accm[MF_NB][4];
+#pragma unroll
+    for (int bt = 0; bt < MF_NB; ++bt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            acc[bt][r] = 0.0f;
+            accm[bt][r] = 0.0f;
+        }
+    const int nbt = (ntok + 15) / 16;   // activation tiles holding rows this pass (uniform)
+    load(0);
+    store(0);
+    lds_barrier();
+    for (int i = 0; i < nb; ++i) {
+        const int buf = i & 1;
+        if (i + 1 < nb) load(i + 1);
+        const uint8_t* sw = s_w[buf];
+        const uint8_t* sa = s_a[buf];
+        const u32x4m hdr = *(const u32x4m*) (sw + arow_l * MF_WS);
+        const uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;
+        const uint32_t sc_lo = s0 & 0x3f3f3f3fu;
+        const uint32_t sc_hi = (s2 & 0x0f0f0f0fu) | (((s0 >> 6) & 0x03030303u) << 4);
+        const uint32_t mn_lo = s1 & 0x3f3f3f3fu;
+        const uint32_t mn_hi = ((s2 >> 4) & 0x0f0f0f0fu) | (((s1 >> 6) & 0x03030303u) << 4);
+        const uint32_t scw = gq < 2 ? sc_lo : sc_hi;
+        const uint32_t sa_ = (scw >> (16 * (gq & 1))) & 0xffu, sb_ = (scw >> (16 * (gq & 1) + 8)) & 0xffu;
+        float xd[4], xdm[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t h0 = *(const uint32_t*) (sw + (16 * wave + 4 * gq + r) * MF_WS);
+            xd[r] = h2f((uint16_t) (h0 & 0xffff));
+            xdm[r] = h2f((uint16_t) (h0 >> 16));
+        }
+        // this lane's A operands for the eight AVX lanes (scale digits times the
+        // nibbles), and the four min operands, formed once for all activation tiles
+        long alo[8], ahi[8];
+#pragma unroll
+        for (int L = 0; L < 8; ++L) {
+            const uint32_t w = *(const uint32_t*) (sw + arow_l * MF_WS + 16 + 32 * gq + 4 * L);
+            const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+            alo[L] = pack2(mul_bytes(lo, sa_ & 7u), mul_bytes(hi, sb_ & 7u));
+            ahi[L] = pack2(mul_bytes(lo, sa_ >> 3), mul_bytes(hi, sb_ >> 3));
+        }
+        int mbq[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int sbk = 2 * q + (gq >> 1);
+            const uint32_t mnw = sbk < 4 ? mn_lo : mn_hi;
+            mbq[q] = (int) (((mnw >> (8 * (sbk & 3))) & 0xffu) * 0x01010101u);
+        }
+        // activation tiles in pairs: two independent MFMA accumulation chains
+#pragma unroll
+        for (int bp = 0; bp < MF_NB; bp += 2) {
+            if (bp >= nbt) break;
+            v4i slo[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}}, shi[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
+            v4i sm[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
+#pragma unroll
+            for (int L = 0; L < 8; ++L)
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const uint8_t* ab = sa + (16 * (bp + u) + lr) * MF_AS + 16 + 64 * gq + 4 * L;
+                    const long bq = pack2(*(const uint32_t*) ab, *(const uint32_t*) (ab + 32));
+                    slo[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(alo[L], bq, slo[u], 0, 0, 0);
+                    shi[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ahi[L], bq, shi[u], 0, 0, 0);
+                }
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const v4i bq = *(const v4i*) (sa + (16 * (bp + u) + lr) * MF_AS + 16 + 64 * q + 16 * gq);
+                    sm[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(v4i{mbq[q], mbq[q], mbq[q], mbq[q]}, bq, sm[u], 0, 0, 0);
+                }
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const float dy = *(const float*) (sa + (16 * (bp + u) + lr) * MF_AS);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    acc[bp + u][r] = __builtin_fmaf(dy * xd[r], (float) (8 * shi[u][r] + slo[u][r]), acc[bp + u][r]);
+                    accm[bp + u][r] = __builtin_fmaf(-dy * xdm[r], (float) sm[u][r], accm[bp + u][r]);
+                }
+            }
+        }
+        if (i + 1 < nb) store(buf ^ 1);
+        lds_barrier();
+    }
+#pragma unroll
+    for (int bt = 0; bt < MF_NB; ++bt) {
+        const int row = 16 * bt + lr;
+        if (bt < nbt && row < ntok) {
+            const int e = s_et[row][0], tt = s_et[row][1];
+            float* dp = (float*) ((char*) m.dst + (size_t) e * m.dst_nb1 + (size_t) tt * m.dst_nb2) + r0 + 16 * wave +
+                        4 * gq;
+            *(float4*) dp = float4{acc[bt][0] + accm[bt][0], acc[bt][1] + accm[bt][1], acc[bt][2] + accm[bt][2],
+                                   acc[bt][3] + accm[bt][3]};
+        }
+    }
+    }
+}
+
 // Whether the matrix-core kernel can take (type, shape, strides): Q4_K rows of
 // 16-byte aligned super-blocks, 64-row tiles, 16-byte aligned output rows.
 bool mmid_mfma_supported(const MmidArgs& m) {
@@ -242,7 +423,8 @@ int launch_mmid_mfma(const MmidArgs& m, hipStream_t stream) {
     if (groups == 0) return 0;
     if (groups > (int64_t(1) << 30)) return -2;
     const unsigned grid = (unsigned) groups;
-    hipLaunchKernelGGL(k_mmid_mfma_q4k, dim3(grid), dim3(256), 0, stream, m);
+    if (m.mfma_exact) hipLaunchKernelGGL(k_mmid_mfma_q4k, dim3(grid), dim3(256), 0, stream, m);
+    else hipLaunchKernelGGL(k_mmid_mfma_q4k_bs, dim3(grid), dim3(256), 0, stream, m);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 

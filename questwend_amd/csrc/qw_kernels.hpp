@@ -76,6 +76,8 @@ struct MmidArgs {
     int32_t* status;          // bit 2 set on an out-of-range slot
     int64_t max_active;       // grid bound on active bins
     int mfma_min_rows;        // bins with at least this many rows go to the matrix-core kernel (0: none do)
+    int mfma_exact;           // matrix cores: 1 replays ggml's eight fp32 AVX-lane chains (bit-identical);
+                              // 0 adds each super-block's exact integer sum in one fp32 chain
     int64_t max_rows;         // bound on the rows of one bin
     // optional (Q8_K activations only): activation row r is the Q8_K of
     // silu(swiglu_gate[r]) * swiglu_up[r] (f32 rows of K values), formed inside

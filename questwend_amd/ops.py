@@ -40,6 +40,20 @@ def set_mfma_min_rows(rows: int) -> int:
     return prev
 
 
+MFMA_BLOCK_SUM, MFMA_EXACT, MFMA_AUTO = 0, 1, 2
+
+
+def set_mfma_form(form: int) -> int:
+    """The matrix-core kernel's float tail: MFMA_EXACT replays ggml's fp32 lane
+    chains (bit-identical), MFMA_BLOCK_SUM adds exact integer block sums in one
+    fp32 chain per output, MFMA_AUTO (default) is exact where the output may be
+    re-quantized and block-sum for the down projections of the layer entry
+    points.  Returns the previous setting."""
+    prev = int(lib().qwmoe_get_mfma_form())
+    check(lib().qwmoe_set_mfma_form(int(form)), "set_mfma_form")
+    return prev
+
+
 def device_status(clear: bool = True) -> int:
     v = C.c_int32(0)
     check(lib().qwmoe_device_status(stream(), C.byref(v), int(clear)), "qwmoe_device_status")

@@ -423,3 +423,15 @@ class RefLayer:
 
 def have_ref() -> bool:
     return REF_SO.exists()
+
+
+def have_ref_avx512() -> bool:
+    """The AVX-512 reference build exists and this host has every ISA extension
+    its flags enable (ggml's AVX-512 branch runs; elsewhere it would SIGILL)."""
+    try:
+        flags = open("/proc/cpuinfo").read()
+    except OSError:
+        return False
+    need = ("avx512f", "avx512cd", "avx512vl", "avx512dq", "avx512bw", "avx512vbmi", "avx512_vnni", "avx512_bf16",
+            "avx_vnni")
+    return REF_SO_AVX512.exists() and all(f" {f}" in flags for f in need)

@@ -32,8 +32,10 @@ def lib_init():
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     ops.init(0, 256 << 20)
+    prev = ops.set_mfma_form(ops.MFMA_EXACT)   # bit-exact tests: heavy bins on the matrix cores replay ggml's float steps
     yield
     torch.cuda.synchronize()
+    ops.set_mfma_form(prev)
 
 
 @pytest.fixture(scope="module")

@@ -50,8 +50,10 @@ def lib_init():
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     ops.init(0, 512 << 20)
+    prev = ops.set_mfma_form(ops.MFMA_EXACT)   # bit-exact tests: the matrix cores (T = 17) replay ggml's float steps
     yield
     torch.cuda.synchronize()
+    ops.set_mfma_form(prev)
 
 
 @pytest.fixture(scope="module")
@@ -84,7 +86,8 @@ def test_router_input_norm(orc, n, rows):
 @pytest.mark.parametrize("T", [1, 3, 17])
 def test_shared_expert_add(orc, types, T):
     """T = 17 puts 17 rows in the one bin: the matrix cores take the
-    projections (min rows 8); smaller batches stay on the GEMV."""
+    projections (min rows 8); smaller batches stay on the GEMV.  Bit for bit
+    under the exact matrix-core form; the default form at T = 17 within 1e-5."""
     note(f"shared expert types={types} T={T} (H=2048, F_sh=512)")
     se = SharedWeights(2048, 512, *types, seed=70 + T, oracle=orc)
     g, keep = gpu_shared(se)
@@ -102,6 +105,16 @@ def test_shared_expert_add(orc, types, T):
         mo_d = dev(mo)
         ops.shared_expert_add(g, dev(x), mo_d, out=mo_d)
         assert np.array_equal(bits(host(mo_d)), bits(orc.shared_expert_add(se, x, mo)))
+        if T == 17:
+            # the default form: gate/up exact, the down projection's matrix cores on
+            # block sums (same integers, another fp32 order): within 1e-5 of max|out|
+            prev_f = ops.set_mfma_form(ops.MFMA_AUTO)
+            try:
+                got = host(ops.shared_expert_add(g, dev(x), dev(mo)))
+            finally:
+                ops.set_mfma_form(prev_f)
+            want = orc.shared_expert_add(se, x, mo).astype(np.float64)
+            assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max()
     finally:
         ops.set_mfma_min_rows(prev)
     status_clean()

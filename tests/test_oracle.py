@@ -133,23 +133,13 @@ def test_layer_matches_ggml_all_intermediates(orc, T):
         assert np.array_equal(bits(a[key]), bits(b[key])), key
 
 
-def _host_has_avx512_branch() -> bool:
-    try:
-        flags = open("/proc/cpuinfo").read()
-    except OSError:
-        return False
-    need = ("avx512f", "avx512cd", "avx512vl", "avx512dq", "avx512bw", "avx512vbmi", "avx512_vnni", "avx512_bf16",
-            "avx_vnni")
-    return all(f" {f}" in flags for f in need)
-
-
 @needs_ref
 def test_stack_run_avx2_bit_exact_and_avx512_within_tolerance(orc):
     """The chained-stack driver the benchmark times: the AVX2 build equals the
     restatement bit for bit through a 4-layer stack (ids, output); the AVX-512
     build (the timed CPU baseline) takes the AVX-512 branch, and teacher-forced
     per layer its ids agree and its output stays far inside 1e-3."""
-    from oracle_lib import REF_SO_AVX512
+    from oracle_lib import REF_SO_AVX512, have_ref_avx512
     lws = [LayerWeights(1024, 32, 8, 512, Q4_K, Q4_K, Q4_K, seed=70 + l, oracle=orc) for l in range(4)]
     xs = np.random.default_rng(8).standard_normal((5, 1024)).astype(np.float32)
     ref = RefGGML()
@@ -166,7 +156,7 @@ def test_stack_run_avx2_bit_exact_and_avx512_within_tolerance(orc):
             assert r["margin"][s, l] == p[7] - p[8]
             x = o["xnext"]
         assert np.array_equal(r["out"][s].view(np.int32), o["out"][0].view(np.int32))
-    if not (REF_SO_AVX512.exists() and _host_has_avx512_branch()):
+    if not have_ref_avx512():
         pytest.skip("AVX-512 reference build or host ISA absent")
     r5 = RefGGML(REF_SO_AVX512)
     assert r5.isa() == 512
