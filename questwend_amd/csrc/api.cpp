@@ -74,7 +74,7 @@ qw::MmidArgs mmid_args(int type, const void* as, int64_t K, int64_t N, int64_t n
                        const uint8_t* bq, int64_t ne11, size_t bq_row, const int32_t* rows, const int32_t* active,
                        const int32_t* active_off, const int32_t* n_active, int64_t max_active,
                        const int32_t* slot_of, int64_t n_slot_of, float* dst, size_t nb1, size_t nb2,
-                       int64_t max_rows) {
+                       int64_t max_rows, int64_t n_pairs) {
     qw::MmidArgs m{};
     m.type = type;
     m.w = (const uint8_t*) as;
@@ -102,6 +102,7 @@ qw::MmidArgs mmid_args(int type, const void* as, int64_t K, int64_t N, int64_t n
     // stay on the bit-exact GEMV
     m.mfma_min_rows = 0;
     m.max_rows = max_rows;
+    m.n_pairs = n_pairs;
     const bool mfma = g_lib.mfma_min_rows > 0 && max_rows >= g_lib.mfma_min_rows && qw::mmid_mfma_supported(m);
     if (mfma) m.mfma_min_rows = g_lib.mfma_min_rows;
     m.mfma_exact = g_lib.mfma_form != QWMOE_MFMA_BLOCK_SUM;
@@ -122,9 +123,10 @@ int mmid_launch(const qw::MmidArgs& m, hipStream_t st) {
 int mmid_grouped(hipStream_t st, int type, const void* as, int64_t K, int64_t N, int64_t n_as, size_t nb01,
                  size_t nb02, const uint8_t* bq, int64_t ne11, size_t bq_row, const int32_t* rows,
                  const int32_t* active, const int32_t* active_off, const int32_t* n_active, int64_t max_active,
-                 const int32_t* slot_of, int64_t n_slot_of, float* dst, size_t nb1, size_t nb2, int64_t max_rows) {
+                 const int32_t* slot_of, int64_t n_slot_of, float* dst, size_t nb1, size_t nb2, int64_t max_rows,
+                 int64_t n_pairs) {
     return mmid_launch(mmid_args(type, as, K, N, n_as, nb01, nb02, bq, ne11, bq_row, rows, active, active_off, n_active,
-                                 max_active, slot_of, n_slot_of, dst, nb1, nb2, max_rows),
+                                 max_active, slot_of, n_slot_of, dst, nb1, nb2, max_rows, n_pairs),
                        st);
 }
 
@@ -355,7 +357,7 @@ int mul_mat_id_in(Arena& ar, int err_space, void* stream, int type, const void* 
     if (rc) return rc;
     if (qw::launch_group(ga, st) != 0) return QWMOE_ERR_HIP;
     return mmid_grouped(st, type, as, ne00, ne01, ne02, nb01, nb02, bq, ne11, qrow, G.rows, G.active, G.active_off,
-                        G.n_active, G.max_active, slot_of, n_slot_of, dst, nb1, nb2, n_ids * ne12);
+                        G.n_active, G.max_active, slot_of, n_slot_of, dst, nb1, nb2, n_ids * ne12, n_ids * ne12);
 }
 
 }  // namespace
@@ -476,9 +478,9 @@ int qwmoe_shared_expert_add(void* stream, const qwmoe_shared_expert* se, int64_t
     if (xu != xg && (rc = qw::launch_quantize_act(vu, x, H, 1, T, (size_t) H * 4, (size_t) H * 4, xu, st))) return rc;
     const size_t fb = (size_t) F * 4;
     const qw::MmidArgs mu = mmid_args(se->type_up, se->up, H, F, 1, se->up_nb1, se->up_nb1 * (size_t) F, xu, 1, qu,
-                                      rows, active, active_off, n_active, 1, nullptr, 0, upo, fb, fb, T);
+                                      rows, active, active_off, n_active, 1, nullptr, 0, upo, fb, fb, T, T);
     const qw::MmidArgs mg = mmid_args(se->type_gate, se->gate, H, F, 1, se->gate_nb1, se->gate_nb1 * (size_t) F, xg, 1,
-                                      qg, rows, active, active_off, n_active, 1, nullptr, 0, gateo, fb, fb, T);
+                                      qg, rows, active, active_off, n_active, 1, nullptr, 0, gateo, fb, fb, T, T);
     if (mu.mfma_min_rows == 0 && mg.mfma_min_rows == 0 && mu.type == mg.type) {
         if ((rc = qw::launch_mmid_gemv2(mu, mg, st))) return rc;
     } else {
@@ -487,7 +489,7 @@ int qwmoe_shared_expert_add(void* stream, const qwmoe_shared_expert* se, int64_t
     }
     // ggml_mul(ggml_silu(g), u) rounds as swiglu_split does: silu, then one multiply
     qw::MmidArgs md = mmid_args(se->type_down, se->down, F, H, 1, se->down_nb1, se->down_nb1 * (size_t) H, aq, 1, qd,
-                                rows, active, active_off, n_active, 1, nullptr, 0, sh, (size_t) H * 4, (size_t) H * 4, T);
+                                rows, active, active_off, n_active, 1, nullptr, 0, sh, (size_t) H * 4, (size_t) H * 4, T, T);
     md.mfma_exact = down_mfma_exact();
     md.swiglu_gate = gateo;
     md.swiglu_up = upo;
@@ -582,10 +584,10 @@ int qwmoe_ffn_layer(void* stream, const qwmoe_layer* L, const float* x, int64_t 
     const size_t dnb1 = (size_t) F * 4, dnb2 = (size_t) F * 4 * (size_t) k;
     const qw::MmidArgs mu = mmid_args(L->type_up, L->up, H, F, L->n_slots_up, L->up_nb1, L->up_nb2, xu, 1, qu, G.rows,
                                       G.active, G.active_off, G.n_active, G.max_active, L->slot_up,
-                                      L->slot_up ? E : 0, upo, dnb1, dnb2, T);
+                                      L->slot_up ? E : 0, upo, dnb1, dnb2, T, k * T);
     const qw::MmidArgs mg = mmid_args(L->type_gate, L->gate, H, F, L->n_slots_gate, L->gate_nb1, L->gate_nb2, xg, 1, qg,
                                       G.rows, G.active, G.active_off, G.n_active, G.max_active, L->slot_gate,
-                                      L->slot_gate ? E : 0, gateo, dnb1, dnb2, T);
+                                      L->slot_gate ? E : 0, gateo, dnb1, dnb2, T, k * T);
     if (mu.mfma_min_rows == 0 && mg.mfma_min_rows == 0 && mu.type == mg.type) {
         // gate and up in one launch
         if ((rc = qw::launch_mmid_gemv2(mu, mg, st))) return rc;
@@ -599,7 +601,7 @@ int qwmoe_ffn_layer(void* stream, const qwmoe_layer* L, const float* x, int64_t 
     if (!aq) return QWMOE_ERR_WORKSPACE;
     qw::MmidArgs md = mmid_args(L->type_down, L->down, F, H, L->n_slots_down, L->down_nb1, L->down_nb2, aq, k, qd,
                                 G.rows, G.active, G.active_off, G.n_active, G.max_active, L->slot_down,
-                                L->slot_down ? E : 0, ex, (size_t) H * 4, (size_t) H * 4 * (size_t) k, T);
+                                L->slot_down ? E : 0, ex, (size_t) H * 4, (size_t) H * 4 * (size_t) k, T, k * T);
     md.mfma_exact = down_mfma_exact();
     md.swiglu_gate = gateo;
     md.swiglu_up = upo;

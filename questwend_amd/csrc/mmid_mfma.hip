@@ -40,6 +40,7 @@ constexpr uint32_t MF_WS = 144;   // LDS stride of a staged Q4_K block (9 x 16 B
 constexpr uint32_t MF_AS = 272;   // LDS stride of a staged Q8_K block: d at 0, qs at 16 (16-aligned)
 constexpr int MF_WCH = (MF_M * 9 + 255) / 256;    // 16-byte weight chunks per thread and super-block
 constexpr int MF_ACH = (MF_N * 65 + 255) / 256;   // activation dwords per thread and super-block
+constexpr int MF_RX = 32;         // rows per work item of the exact form (two passes)
 
 __device__ __forceinline__ long pack2(uint32_t lo, uint32_t hi) { return (long) (((uint64_t) hi << 32) | lo); }
 
@@ -57,13 +58,60 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short) 0, (int) bytes, 0x00020000);
 }
 
-// Workgroup b = (active expert g, row tile): weight rows r0 .. r0 + 63 of the
-// expert's matrix against all its routed activation rows, 16 per pass.  Super-
+// Work items: the routed rows of each heavy expert (at least mfma_min_rows)
+// cut into chunks of R rows; item i is chunk c of active expert g, items in
+// expert order.  Wave 0 scans the active experts' chunk counts 64 at a time and
+// leaves (g, c) in s_item, g = -1 past the last item.  Splitting an expert's
+// rows over workgroups keeps the longest workgroup at R rows whatever the skew
+// of the routing (one expert can hold every token of the batch).
+__device__ __forceinline__ void mf_item(const MmidArgs& m, int item, int R, int wave, int lane, int* s_item) {
+    if (wave == 0) {
+        const int n = *m.n_active;
+        int run = 0, fg = -1, fc = 0;
+        for (int base = 0; base < n; base += 64) {
+            const int j = base + lane;
+            int ch = 0;
+            if (j < n) {
+                const int cnt = m.active_off[j + 1] - m.active_off[j];
+                ch = cnt >= m.mfma_min_rows ? (cnt + R - 1) / R : 0;
+            }
+            int incl = ch;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int v = __shfl_up(incl, o);
+                if (lane >= o) incl += v;
+            }
+            const int excl = incl - ch;
+            const uint64_t hit = __ballot(item >= run + excl && item < run + incl);
+            if (hit) {   // uniform
+                const int src = __ffsll((unsigned long long) hit) - 1;
+                fg = base + src;
+                fc = item - run - __shfl(excl, src);
+                break;
+            }
+            run += __shfl(incl, 63);
+        }
+        if (lane == 0) {
+            s_item[0] = fg;
+            s_item[1] = fc;
+        }
+    }
+    __syncthreads();
+}
+
+// Upper bound on the items of a launch: at most min(max_active, n_pairs /
+// mfma_min_rows) heavy experts, each with at most one partial chunk.
+inline int64_t mf_max_items(const MmidArgs& m, int R) {
+    const int64_t heavy = std::min<int64_t>(m.max_active, m.n_pairs / std::max(m.mfma_min_rows, 1));
+    return heavy + m.n_pairs / R;
+}
+
+// Workgroup b = (work item, row tile): weight rows r0 .. r0 + 63 of the expert's
+// matrix against the item's MF_RX routed activation rows, 16 per pass.  Super-
 // block i + 1 is loaded into registers while super-block i is computed from LDS.
-// One workgroup walks all passes of its tile, so the workgroups in flight hold
-// distinct tiles and a tile's re-reads come from the caches of its CU.  (Measured
-// on the T=512 30B layer: 117 us per projection; one workgroup per pass: 124 us
-// with 2.6x the weight bytes fetched; a tile's passes placed on one XCD: 202 us.)
+// Items bound the longest workgroup: with one workgroup walking all of a tile's
+// rows, the heaviest expert of a skewed batch (266 rows of 512 tokens) set the
+// time of the whole launch.
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) k_mmid_mfma_q4k(MmidArgs m) {
     __shared__ __align__(16) uint8_t s_w[2][MF_M * MF_WS];
     __shared__ __align__(16) uint8_t s_a[2][MF_N * MF_AS];
@@ -71,10 +119,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     __shared__ int32_t s_et[MF_N][2];
     const int tiles = (int) (m.N / MF_M);
     const int tile = (int) (blockIdx.x % (uint32_t) tiles);
-    const int g = (int) (blockIdx.x / (uint32_t) tiles);
-    if (g >= *m.n_active) return;
-    const int p0 = m.active_off[g], p1 = m.active_off[g + 1];
-    if (p1 - p0 < m.mfma_min_rows) return;   // light expert: the GEMV kernel's
+    __shared__ int s_item[2];
+    mf_item(m, (int) (blockIdx.x / (uint32_t) tiles), MF_RX, threadIdx.x >> 6, threadIdx.x & 63, s_item);
+    const int g = s_item[0];
+    if (g < 0) return;   // past the last item (light experts have none: the GEMV kernel's)
+    const int p0 = m.active_off[g] + MF_RX * s_item[1], p1 = min(m.active_off[g + 1], p0 + MF_RX);
     const int bin = m.active[g];
     int64_t mat = bin;
     if (m.slot_of) mat = (bin < m.n_slot_of) ? m.slot_of[bin] : -1;
@@ -239,6 +288,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 // formed once for all of them and the tile is streamed a quarter as often.
 constexpr int MF_NB = 4;                               // activation tiles per pass
 constexpr int MF_N4 = 16 * MF_NB;                      // activation rows per pass
+constexpr int MF_RB = MF_N4;                           // rows per work item (one pass)
 
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) k_mmid_mfma_q4k_bs(MmidArgs m) {
     __shared__ __align__(16) uint8_t s_w[2][MF_M * MF_WS];
@@ -247,10 +297,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     __shared__ int32_t s_et[MF_N4][2];
     const int tiles = (int) (m.N / MF_M);
     const int tile = (int) (blockIdx.x % (uint32_t) tiles);
-    const int g = (int) (blockIdx.x / (uint32_t) tiles);
-    if (g >= *m.n_active) return;
-    const int p0 = m.active_off[g], p1 = m.active_off[g + 1];
-    if (p1 - p0 < m.mfma_min_rows) return;   // light expert: the GEMV kernel's
+    __shared__ int s_item[2];
+    mf_item(m, (int) (blockIdx.x / (uint32_t) tiles), MF_RB, threadIdx.x >> 6, threadIdx.x & 63, s_item);
+    const int g = s_item[0];
+    if (g < 0) return;   // past the last item (light experts have none: the GEMV kernel's)
+    const int p0 = m.active_off[g] + MF_RB * s_item[1], p1 = min(m.active_off[g + 1], p0 + MF_RB);
     const int bin = m.active[g];
     int64_t mat = bin;
     if (m.slot_of) mat = (bin < m.n_slot_of) ? m.slot_of[bin] : -1;
@@ -418,8 +469,8 @@ bool mmid_mfma_supported(const MmidArgs& m) {
 
 int launch_mmid_mfma(const MmidArgs& m, hipStream_t stream) {
     if (!mmid_mfma_supported(m)) return -2;
-    // one workgroup per (active expert, row tile)
-    const int64_t groups = m.max_active * (m.N / MF_M);
+    // one workgroup per (work item, row tile)
+    const int64_t groups = mf_max_items(m, m.mfma_exact ? MF_RX : MF_RB) * (m.N / MF_M);
     if (groups == 0) return 0;
     if (groups > (int64_t(1) << 30)) return -2;
     const unsigned grid = (unsigned) groups;

@@ -79,6 +79,7 @@ struct MmidArgs {
     int mfma_exact;           // matrix cores: 1 replays ggml's eight fp32 AVX-lane chains (bit-identical);
                               // 0 adds each super-block's exact integer sum in one fp32 chain
     int64_t max_rows;         // bound on the rows of one bin
+    int64_t n_pairs;          // bound on the grouped (e, t) pairs of all bins
     // optional (Q8_K activations only): activation row r is the Q8_K of
     // silu(swiglu_gate[r]) * swiglu_up[r] (f32 rows of K values), formed inside
     // the GEMV instead of read from act_q; see mmid_gemv_swiglu_ok
