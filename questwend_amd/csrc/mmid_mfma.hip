@@ -35,12 +35,47 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4m __attribute__((ext_vector_type(4)));
 
 constexpr int MF_M = 64;          // weight rows per workgroup (4 waves x 16)
-constexpr int MF_N = 16;          // activation rows per workgroup (one 16-row tile per wave)
 constexpr uint32_t MF_WS = 144;   // LDS stride of a staged Q4_K block (9 x 16 B)
-constexpr uint32_t MF_AS = 272;   // LDS stride of a staged Q8_K block: d at 0, qs at 16 (16-aligned)
-constexpr int MF_WCH = (MF_M * 9 + 255) / 256;    // 16-byte weight chunks per thread and super-block
-constexpr int MF_ACH = (MF_N * 65 + 255) / 256;   // activation dwords per thread and super-block
-constexpr int MF_RX = 32;         // rows per work item of the exact form (two passes)
+constexpr uint32_t MF_AS = 272;   // LDS stride of a staged Q8_K block (68 dwords): d at 0, qs at 16
+constexpr int MF_NB_X = 1;        // 16-row activation tiles per pass: exact form
+constexpr int MF_NB_B = 4;        // block-sum form
+
+// Waits until at most N of this wave's vector memory operations are in flight.
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Buffer resource words over [base, base + bytes) (the layout
+// __builtin_amdgcn_make_buffer_rsrc builds; loads past the end return zeros).
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4 rsrc_words(const void* base, uint32_t bytes) {
+    const uint64_t a = (uint64_t) base;
+    return i32x4{(int) (uint32_t) a, (int) ((uint32_t) (a >> 32) & 0xffffu), (int) bytes, 0x00020000};
+}
+
+// Buffer loads straight into LDS: lane l's 16 (4) bytes from voff + soff land at
+// LDS byte lds_base + 16 l (4 l).  Written as instructions, not through the
+// compiler's builtin: the compiler then inserts no wait of its own before the
+// LDS reads (it would wait for every copy in flight, the prefetched stages
+// included); the kernel waits with vm_wait and orders waves with a barrier.
+// M0 holds the LDS base for the instruction and is restored after it.
+__device__ __forceinline__ void dma_b128(i32x4 rsrc, uint32_t lds_base, uint32_t voff, uint32_t soff) {
+    uint32_t keep;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %2, %3, %4 offen lds\n\ts_mov_b32 m0, %0"
+        : "=&s"(keep)
+        : "s"(lds_base), "v"(voff), "s"(rsrc), "s"(soff)
+        : "memory");
+}
+__device__ __forceinline__ void dma_b32(i32x4 rsrc, uint32_t lds_base, uint32_t voff, uint32_t soff) {
+    uint32_t keep;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dword %2, %3, %4 offen lds\n\ts_mov_b32 m0, %0"
+        : "=&s"(keep)
+        : "s"(lds_base), "v"(voff), "s"(rsrc), "s"(soff)
+        : "memory");
+}
 
 __device__ __forceinline__ long pack2(uint32_t lo, uint32_t hi) { return (long) (((uint64_t) hi << 32) | lo); }
 
@@ -107,23 +142,48 @@ inline int64_t mf_max_items(const MmidArgs& m, int R) {
 }
 
 // Workgroup b = (work item, row tile): weight rows r0 .. r0 + 63 of the expert's
-// matrix against the item's MF_RX routed activation rows, 16 per pass.  Super-
-// block i + 1 is loaded into registers while super-block i is computed from LDS.
-// Items bound the longest workgroup: with one workgroup walking all of a tile's
-// rows, the heaviest expert of a skewed batch (266 rows of 512 tokens) set the
-// time of the whole launch.
+// matrix against one pass of 16 NB routed activation rows (the item).  Items
+// bound the longest workgroup: with one workgroup walking all of a tile's rows,
+// the heaviest expert of a skewed batch (266 rows of 512 tokens) set the time of
+// the whole launch.
+//
+// Pipeline.  Super-block i of the tile and of the pass's activation rows is
+// copied by buffer loads straight into LDS (no registers in between) into stage
+// buffer i % 3, two super-blocks ahead of the one being computed: a stage's
+// loads have two super-blocks of matrix-core work to land.  One barrier per
+// super-block: after it every wave has finished the previous super-block, whose
+// buffer then takes the loads of super-block i + 2.  A wave waits for its own
+// loads of super-block i (s_waitcnt vmcnt) before that barrier, so after it
+// every wave's copies are in LDS.
+//
+// Staging layout: weight chunk q (16 B; 9 per row) at byte 16 q, from row q / 9,
+// byte 16 (q % 9) of the super-block; activation dword slot u of row n (68 per
+// row) at byte 4 (68 n + u), from byte 0 (u < 4: the d, padded) or 4 u - 12 (the
+// qs) of the row's Q8_K block.  One DMA instruction covers 64 consecutive chunks
+// or slots, one per lane.
+template <int NB, bool EXACT>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) k_mmid_mfma_q4k(MmidArgs m) {
-    __shared__ __align__(16) uint8_t s_w[2][MF_M * MF_WS];
-    __shared__ __align__(16) uint8_t s_a[2][MF_N * MF_AS];
-    __shared__ int32_t s_arow[MF_N];
-    __shared__ int32_t s_et[MF_N][2];
+    constexpr int NR = 16 * NB;               // activation rows per pass (and per item)
+    constexpr int AW = NR * 68 / 64;          // activation DMA instructions per stage
+    constexpr int AWW = (AW + 3) / 4;         // ... per wave, at most
+    constexpr int VM_STAGE = 2 + AW / 4;      // fewest DMA instructions any wave issues per stage
+    static_assert(NR * 68 % 64 == 0 && VM_STAGE <= 63, "staging shape");
+    __shared__ __align__(16) uint8_t s_w0[MF_M * MF_WS];
+    __shared__ __align__(16) uint8_t s_w1[MF_M * MF_WS];
+    __shared__ __align__(16) uint8_t s_w2[MF_M * MF_WS];
+    __shared__ __align__(16) uint8_t s_a0[NR * MF_AS];
+    __shared__ __align__(16) uint8_t s_a1[NR * MF_AS];
+    __shared__ __align__(16) uint8_t s_a2[NR * MF_AS];
+    __shared__ int32_t s_arow[NR];
+    __shared__ int32_t s_et[NR][2];
+    __shared__ int s_item[2];
     const int tiles = (int) (m.N / MF_M);
     const int tile = (int) (blockIdx.x % (uint32_t) tiles);
-    __shared__ int s_item[2];
-    mf_item(m, (int) (blockIdx.x / (uint32_t) tiles), MF_RX, threadIdx.x >> 6, threadIdx.x & 63, s_item);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    mf_item(m, (int) (blockIdx.x / (uint32_t) tiles), NR, wave, lane, s_item);
     const int g = s_item[0];
     if (g < 0) return;   // past the last item (light experts have none: the GEMV kernel's)
-    const int p0 = m.active_off[g] + MF_RX * s_item[1], p1 = min(m.active_off[g + 1], p0 + MF_RX);
+    const int p0 = m.active_off[g] + NR * s_item[1], p1 = min(m.active_off[g + 1], p0 + NR);
     const int bin = m.active[g];
     int64_t mat = bin;
     if (m.slot_of) mat = (bin < m.n_slot_of) ? m.slot_of[bin] : -1;
@@ -132,83 +192,62 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
         return;
     }
     const int64_t r0 = (int64_t) tile * MF_M;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int lr = lane & 15, gq = lane >> 4;   // A row / B row within the tile; k-slot group
+    const int lr = lane & 15, gq = lane >> 4;   // A row / B row within a 16 x 16 tile; k-slot group
     const int nb = (int) (m.K / QK_K);
     const uint8_t* wtile = m.w + (size_t) mat * m.nb2 + (size_t) r0 * m.nb1;
-    const __amdgpu_buffer_rsrc_t wrsrc = buffer_rsrc(wtile, (uint32_t) (MF_M * m.nb1));
-    const __amdgpu_buffer_rsrc_t arsrc = buffer_rsrc(m.act_q, 0x7fffffffu);
+    const i32x4 wrsrc = rsrc_words(wtile, (uint32_t) (MF_M * m.nb1));
+    const i32x4 arsrc = rsrc_words(m.act_q, 0x7fffffffu);
     const int arow_l = 16 * wave + lr;          // this lane's A row in the staged tile
-    for (int pass = 0;; ++pass) {
-    const int pc = p0 + MF_N * pass;
-    if (pc >= p1) break;
-    const int ntok = (p1 - pc) < MF_N ? (p1 - pc) : MF_N;
-    lds_barrier();   // the previous pass is done with the staged tiles
-    if (tid < MF_N) {
-        const int pp = pc + (tid < ntok ? tid : 0);
+    const int ntok = p1 - p0;                   // 1 .. NR
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    if (tid < NR) {
+        const int pp = p0 + (tid < ntok ? tid : 0);   // rows past ntok are staged from row 0, never written
         const int e = m.rows[2 * pp], t = m.rows[2 * pp + 1];
         s_et[tid][0] = e;
         s_et[tid][1] = t;
         s_arow[tid] = (int) ((int64_t) (e % m.b_ne1) + (int64_t) t * m.b_ne1);
     }
     lds_barrier();
-
-    // staging: this thread's weight chunks and activation dwords of super-block i,
-    // through buffer loads (32-bit offsets from a uniform base; a load past the
-    // buffer's end returns zeros instead of reading out of bounds).  Offsets and
-    // LDS destinations are fixed for the pass; a super-block adds i * 144 / i * 292.
-    uint32_t woff[MF_WCH], wdst[MF_WCH], aoff[MF_ACH], adst[MF_ACH];
+    // this lane's source offsets (the super-block adds i * 144 / i * 292 as the scalar offset)
+    uint32_t woff[3], aoff[AWW];
 #pragma unroll
-    for (int j = 0; j < MF_WCH; ++j) {
-        const int z = tid + 256 * j;
-        const int zc = min(z, MF_M * 9 - 1);
-        const int r = zc / 9, c = zc - r * 9;
-        woff[j] = (uint32_t) r * (uint32_t) m.nb1 + 16u * (uint32_t) c;
-        wdst[j] = z < MF_M * 9 ? (uint32_t) (r * MF_WS + 16 * c) : 0xffffffffu;
+    for (int k = 0; k < 3; ++k) {
+        const int q = 64 * (wave + 4 * k) + lane;
+        const int qc = q < MF_M * 9 ? q : 0;
+        woff[k] = (uint32_t) (qc / 9) * (uint32_t) m.nb1 + 16u * (uint32_t) (qc % 9);
     }
 #pragma unroll
-    for (int j = 0; j < MF_ACH; ++j) {
-        const int z = tid + 256 * j;
-        const int zc = min(z, ntok * 65 - 1);
-        const int n = zc / 65, c = zc - n * 65;
-        aoff[j] = (uint32_t) s_arow[n] * (uint32_t) m.act_row_bytes + 4u * (uint32_t) c;
-        adst[j] = z < ntok * 65 ? (uint32_t) (n * MF_AS + (c == 0 ? 0 : 12 + 4 * c)) : 0xffffffffu;
+    for (int k = 0; k < AWW; ++k) {
+        const int sl = 64 * (wave + 4 * k) + lane;
+        const int slc = sl < NR * 68 ? sl : 0;
+        const int n = slc / 68, u = slc - 68 * n;
+        aoff[k] = (uint32_t) s_arow[n] * (uint32_t) m.act_row_bytes + (u < 4 ? 0u : 4u * (uint32_t) u - 12u);
     }
-    u32x4m wreg[MF_WCH];
-    uint32_t areg[MF_ACH];
-    auto load = [&](int i) {
+    auto issue = [&](uint8_t* sw, uint8_t* sa, int i) __attribute__((always_inline)) {
+        // LDS bases recomputed per stage, not kept live across the loop (scalar registers)
+        uint32_t lw = (uint32_t) (uintptr_t) sw, la = (uint32_t) (uintptr_t) sa;
+        asm volatile("" : "+s"(lw), "+s"(la));
 #pragma unroll
-        for (int j = 0; j < MF_WCH; ++j)
-            wreg[j] = __builtin_bit_cast(u32x4m, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, woff[j] + (uint32_t) i * 144u, 0, 0));
+        for (int k = 0; k < 3; ++k)
+            if (wv + 4 * k < 9) dma_b128(wrsrc, lw + 1024u * (uint32_t) (wv + 4 * k), woff[k], 144u * (uint32_t) i);
 #pragma unroll
-        for (int j = 0; j < MF_ACH; ++j) areg[j] = __builtin_amdgcn_raw_buffer_load_b32(arsrc, aoff[j] + (uint32_t) i * 292u, 0, 0);
-    };
-    auto store = [&](int buf) {
-#pragma unroll
-        for (int j = 0; j < MF_WCH; ++j)
-            if (wdst[j] != 0xffffffffu) *(u32x4m*) (s_w[buf] + wdst[j]) = wreg[j];
-#pragma unroll
-        for (int j = 0; j < MF_ACH; ++j)
-            if (adst[j] != 0xffffffffu) *(uint32_t*) (s_a[buf] + adst[j]) = areg[j];
+        for (int k = 0; k < AWW; ++k)
+            if (wv + 4 * k < AW) dma_b32(arsrc, la + 256u * (uint32_t) (wv + 4 * k), aoff[k], 292u * (uint32_t) i);
     };
 
-    // per output (D register r): the eight AVX lanes and four min lanes
-    float acc[4][8], accm[4][4];
+    // EXACT: per output (D register r) the eight AVX lanes and four min lanes.
+    // Block sums: per activation tile and output, one chain and one for the mins.
+    constexpr int NACC = EXACT ? 8 : NB, NACCM = EXACT ? 4 : NB;
+    float acc[4][NACC], accm[4][NACCM];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
 #pragma unroll
-        for (int L = 0; L < 8; ++L) acc[r][L] = 0.0f;
+        for (int L = 0; L < NACC; ++L) acc[r][L] = 0.0f;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) accm[r][q] = 0.0f;
+        for (int q = 0; q < NACCM; ++q) accm[r][q] = 0.0f;
     }
-    load(0);
-    store(0);
-    lds_barrier();
-    for (int i = 0; i < nb; ++i) {
-        const int buf = i & 1;
-        if (i + 1 < nb) load(i + 1);
-        const uint8_t* sw = s_w[buf];
-        const uint8_t* sa = s_a[buf];
+
+    auto compute = [&](const uint8_t* sw, const uint8_t* sa) __attribute__((always_inline)) {
         // this lane's A row: the 6-bit scales and mins of the 8 sub-blocks
         // (the utmp shuffle of quants.c:2067-2072), as bytes
         const u32x4m hdr = *(const u32x4m*) (sw + arow_l * MF_WS);
@@ -220,172 +259,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
         // sub-blocks 2 gq (low nibbles) and 2 gq + 1 (high nibbles) of this lane's k-slots
         const uint32_t scw = gq < 2 ? sc_lo : sc_hi;
         const uint32_t sa_ = (scw >> (16 * (gq & 1))) & 0xffu, sb_ = (scw >> (16 * (gq & 1) + 8)) & 0xffu;
-        // block scales of the D rows 4 gq + r and of this lane's B row
-        float d[4], dmin[4];
-        const float dy = *(const float*) (sa + lr * MF_AS);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint32_t h0 = *(const uint32_t*) (sw + (16 * wave + 4 * gq + r) * MF_WS);
-            d[r] = dy * h2f((uint16_t) (h0 & 0xffff));
-            dmin[r] = -dy * h2f((uint16_t) (h0 >> 16));
-        }
-        // AVX lanes
-#pragma unroll
-        for (int L = 0; L < 8; ++L) {
-            const uint32_t w = *(const uint32_t*) (sw + arow_l * MF_WS + 16 + 32 * gq + 4 * L);
-            const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
-            const long a_lo = pack2(mul_bytes(lo, sa_ & 7u), mul_bytes(hi, sb_ & 7u));
-            const long a_hi = pack2(mul_bytes(lo, sa_ >> 3), mul_bytes(hi, sb_ >> 3));
-            const uint8_t* ab = sa + lr * MF_AS + 16 + 64 * gq + 4 * L;
-            const long bq = pack2(*(const uint32_t*) ab, *(const uint32_t*) (ab + 32));
-            const v4i z4 = v4i{0, 0, 0, 0};
-            const v4i dlo = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_lo, bq, z4, 0, 0, 0);
-            const v4i dhi = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_hi, bq, z4, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[r][L] = __builtin_fmaf(d[r], (float) (8 * dhi[r] + dlo[r]), acc[r][L]);
-        }
-        // min lanes: sub-blocks 2q (k-slots of lane groups 0, 1) and 2q + 1 (groups 2, 3)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int sbk = 2 * q + (gq >> 1);
-            const uint32_t mnw = sbk < 4 ? mn_lo : mn_hi;
-            const int mb = (int) (((mnw >> (8 * (sbk & 3))) & 0xffu) * 0x01010101u);
-            const v4i a_mn = v4i{mb, mb, mb, mb};
-            const v4i bq = *(const v4i*) (sa + lr * MF_AS + 16 + 64 * q + 16 * gq);
-            const v4i dm = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_mn, bq, v4i{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) accm[r][q] = __builtin_fmaf(dmin[r], (float) dm[r], accm[r][q]);
-        }
-        if (i + 1 < nb) store(buf ^ 1);   // the other buffer was last read before the previous barrier
-        lds_barrier();
-    }
-    // hsum_float_8(acc) + ((m0 + m2) + (m1 + m3)); rows r0 + 16 wave + 4 gq .. +3 of B row lr
-    float o[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const float* a = acc[r];
-        const float hs = ((a[4] + a[0]) + (a[6] + a[2])) + ((a[5] + a[1]) + (a[7] + a[3]));
-        const float* mm = accm[r];
-        o[r] = hs + ((mm[0] + mm[2]) + (mm[1] + mm[3]));
-    }
-    if (lr < ntok) {
-        const int e = s_et[lr][0], tt = s_et[lr][1];
-        float* dp = (float*) ((char*) m.dst + (size_t) e * m.dst_nb1 + (size_t) tt * m.dst_nb2) + r0 + 16 * wave + 4 * gq;
-        *(float4*) dp = float4{o[0], o[1], o[2], o[3]};
-    }
-    }
-}
-
-// The block-sum form (mfma_exact == 0).  Same integers, fewer float steps:
-// per (weight row, activation row, super-block) the eight AVX lanes' sums add up
-// in the MFMA's own int32 accumulator (sumi = sum_L sumi_L, the block's exact
-// integer dot with its scales; |sumi| < 2^25), the mins likewise (prod = sum_m
-// prod_m), and the float steps are acc = fma(d_i, sumi, acc) and
-// accm = fma(dmin_i, prod, accm) over the super-blocks, then acc + accm.  The
-// integers are ggml's exactly; the floats round in another order (relative
-// difference ~1e-7 of the terms), inside the 1e-3 bar.  Each wave keeps four
-// 16-row activation tiles per pass (64 rows), so a weight row's operand is
-// formed once for all of them and the tile is streamed a quarter as often.
-constexpr int MF_NB = 4;                               // activation tiles per pass
-constexpr int MF_N4 = 16 * MF_NB;                      // activation rows per pass
-constexpr int MF_RB = MF_N4;                           // rows per work item (one pass)
-
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) k_mmid_mfma_q4k_bs(MmidArgs m) {
-    __shared__ __align__(16) uint8_t s_w[2][MF_M * MF_WS];
-    __shared__ __align__(16) uint8_t s_a[2][MF_N4 * MF_AS];
-    __shared__ int32_t s_arow[MF_N4];
-    __shared__ int32_t s_et[MF_N4][2];
-    const int tiles = (int) (m.N / MF_M);
-    const int tile = (int) (blockIdx.x % (uint32_t) tiles);
-    __shared__ int s_item[2];
-    mf_item(m, (int) (blockIdx.x / (uint32_t) tiles), MF_RB, threadIdx.x >> 6, threadIdx.x & 63, s_item);
-    const int g = s_item[0];
-    if (g < 0) return;   // past the last item (light experts have none: the GEMV kernel's)
-    const int p0 = m.active_off[g] + MF_RB * s_item[1], p1 = min(m.active_off[g + 1], p0 + MF_RB);
-    const int bin = m.active[g];
-    int64_t mat = bin;
-    if (m.slot_of) mat = (bin < m.n_slot_of) ? m.slot_of[bin] : -1;
-    if (mat < 0 || mat >= m.n_as) {
-        if (threadIdx.x == 0 && m.status) atomicOr(m.status, 4);
-        return;
-    }
-    const int64_t r0 = (int64_t) tile * MF_M;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int lr = lane & 15, gq = lane >> 4;
-    const int nb = (int) (m.K / QK_K);
-    const uint8_t* wtile = m.w + (size_t) mat * m.nb2 + (size_t) r0 * m.nb1;
-    const __amdgpu_buffer_rsrc_t wrsrc = buffer_rsrc(wtile, (uint32_t) (MF_M * m.nb1));
-    const __amdgpu_buffer_rsrc_t arsrc = buffer_rsrc(m.act_q, 0x7fffffffu);
-    const int arow_l = 16 * wave + lr;
-    for (int pass = 0;; ++pass) {
-    const int pc = p0 + MF_N4 * pass;
-    if (pc >= p1) break;
-    const int ntok = (p1 - pc) < MF_N4 ? (p1 - pc) : MF_N4;
-    lds_barrier();
-    if (tid < MF_N4) {
-        const int pp = pc + (tid < ntok ? tid : 0);
-        const int e = m.rows[2 * pp], t = m.rows[2 * pp + 1];
-        s_et[tid][0] = e;
-        s_et[tid][1] = t;
-        s_arow[tid] = (int) ((int64_t) (e % m.b_ne1) + (int64_t) t * m.b_ne1);
-    }
-    lds_barrier();
-    // staging: thread (row n = tid / 4, sub = tid % 4) copies dwords c = sub + 4 j of
-    // activation row n (65: d, then the 64 of qs) and 16-byte chunks c = sub + 4 j of
-    // weight row n (9 per row): one base offset per thread, the rest immediates
-    const int sn = tid >> 2, sub = tid & 3;
-    const uint32_t abase = (uint32_t) s_arow[sn < ntok ? sn : 0] * (uint32_t) m.act_row_bytes + 4u * (uint32_t) sub;
-    const uint32_t adst = (uint32_t) (sn * MF_AS + 12 + 4 * sub);   // dword c >= 1 at adst + 16 j; c = 0 (the d) at sn * MF_AS
-    const uint32_t wbase = (uint32_t) sn * (uint32_t) m.nb1 + 16u * (uint32_t) sub;
-    const uint32_t wdst = (uint32_t) (sn * MF_WS + 16 * sub);
-    constexpr int AJ = 17, WJ = 3;   // c = sub + 4 j <= 64 (activations), <= 8 (weights)
-    u32x4m wreg[WJ];
-    uint32_t areg[AJ];
-    auto load = [&](int i) {
-        const uint32_t wi = wbase + (uint32_t) i * 144u, ai = abase + (uint32_t) i * 292u;
-#pragma unroll
-        for (int jj = 0; jj < WJ; ++jj)
-            if (sub + 4 * jj <= 8)
-                wreg[jj] = __builtin_bit_cast(u32x4m, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, wi + 64u * jj, 0, 0));
-#pragma unroll
-        for (int jj = 0; jj < AJ; ++jj)
-            if (sub + 4 * jj <= 64) areg[jj] = __builtin_amdgcn_raw_buffer_load_b32(arsrc, ai + 16u * jj, 0, 0);
-    };
-    auto store = [&](int buf) {
-#pragma unroll
-        for (int jj = 0; jj < WJ; ++jj)
-            if (sub + 4 * jj <= 8) *(u32x4m*) (s_w[buf] + wdst + 64 * jj) = wreg[jj];
-        *(uint32_t*) (s_a[buf] + (sub == 0 ? (uint32_t) (sn * MF_AS) : adst)) = areg[0];
-#pragma unroll
-        for (int jj = 1; jj < AJ; ++jj)
-            if (sub + 4 * jj <= 64) *(uint32_t*) (s_a[buf] + adst + 16 * jj) = areg[jj];
-    };
-    // rows of activation tile bt past ntok are staged from row 0 and never written out
-    float acc[MF_NB][4], accm[MF_NB][4];
-#pragma unroll
-    for (int bt = 0; bt < MF_NB; ++bt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            acc[bt][r] = 0.0f;
-            accm[bt][r] = 0.0f;
-        }
-    const int nbt = (ntok + 15) / 16;   // activation tiles holding rows this pass (uniform)
-    load(0);
-    store(0);
-    lds_barrier();
-    for (int i = 0; i < nb; ++i) {
-        const int buf = i & 1;
-        if (i + 1 < nb) load(i + 1);
-        const uint8_t* sw = s_w[buf];
-        const uint8_t* sa = s_a[buf];
-        const u32x4m hdr = *(const u32x4m*) (sw + arow_l * MF_WS);
-        const uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;
-        const uint32_t sc_lo = s0 & 0x3f3f3f3fu;
-        const uint32_t sc_hi = (s2 & 0x0f0f0f0fu) | (((s0 >> 6) & 0x03030303u) << 4);
-        const uint32_t mn_lo = s1 & 0x3f3f3f3fu;
-        const uint32_t mn_hi = ((s2 >> 4) & 0x0f0f0f0fu) | (((s1 >> 6) & 0x03030303u) << 4);
-        const uint32_t scw = gq < 2 ? sc_lo : sc_hi;
-        const uint32_t sa_ = (scw >> (16 * (gq & 1))) & 0xffu, sb_ = (scw >> (16 * (gq & 1) + 8)) & 0xffu;
+        // fp16 block scales of the D rows 4 gq + r
         float xd[4], xdm[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -393,71 +267,146 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
             xd[r] = h2f((uint16_t) (h0 & 0xffff));
             xdm[r] = h2f((uint16_t) (h0 >> 16));
         }
-        // this lane's A operands for the eight AVX lanes (scale digits times the
-        // nibbles), and the four min operands, formed once for all activation tiles
-        long alo[8], ahi[8];
-#pragma unroll
-        for (int L = 0; L < 8; ++L) {
-            const uint32_t w = *(const uint32_t*) (sw + arow_l * MF_WS + 16 + 32 * gq + 4 * L);
-            const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
-            alo[L] = pack2(mul_bytes(lo, sa_ & 7u), mul_bytes(hi, sb_ & 7u));
-            ahi[L] = pack2(mul_bytes(lo, sa_ >> 3), mul_bytes(hi, sb_ >> 3));
-        }
-        int mbq[4];
+        int mbq[4];   // min operands: sub-blocks 2q (k-slots of lane groups 0, 1) and 2q + 1 (groups 2, 3)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int sbk = 2 * q + (gq >> 1);
             const uint32_t mnw = sbk < 4 ? mn_lo : mn_hi;
             mbq[q] = (int) (((mnw >> (8 * (sbk & 3))) & 0xffu) * 0x01010101u);
         }
-        // activation tiles in pairs: two independent MFMA accumulation chains
+        if constexpr (EXACT) {
+            const float dy = *(const float*) (sa + lr * MF_AS);
+            float d[4], dmin[4];
 #pragma unroll
-        for (int bp = 0; bp < MF_NB; bp += 2) {
-            if (bp >= nbt) break;
-            v4i slo[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}}, shi[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
-            v4i sm[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
+            for (int r = 0; r < 4; ++r) {
+                d[r] = dy * xd[r];
+                dmin[r] = -dy * xdm[r];
+            }
 #pragma unroll
-            for (int L = 0; L < 8; ++L)
+            for (int L = 0; L < 8; ++L) {
+                const uint32_t w = *(const uint32_t*) (sw + arow_l * MF_WS + 16 + 32 * gq + 4 * L);
+                const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+                const long a_lo = pack2(mul_bytes(lo, sa_ & 7u), mul_bytes(hi, sb_ & 7u));
+                const long a_hi = pack2(mul_bytes(lo, sa_ >> 3), mul_bytes(hi, sb_ >> 3));
+                const uint8_t* ab = sa + lr * MF_AS + 16 + 64 * gq + 4 * L;
+                const long bq = pack2(*(const uint32_t*) ab, *(const uint32_t*) (ab + 32));
+                const v4i z4 = v4i{0, 0, 0, 0};
+                const v4i dlo = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_lo, bq, z4, 0, 0, 0);
+                const v4i dhi = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_hi, bq, z4, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[r][L] = __builtin_fmaf(d[r], (float) (8 * dhi[r] + dlo[r]), acc[r][L]);
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const v4i bq = *(const v4i*) (sa + lr * MF_AS + 16 + 64 * q + 16 * gq);
+                const v4i dm = __builtin_amdgcn_mfma_i32_16x16x64_i8(v4i{mbq[q], mbq[q], mbq[q], mbq[q]}, bq,
+                                                                     v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) accm[r][q] = __builtin_fmaf(dmin[r], (float) dm[r], accm[r][q]);
+            }
+        } else {
+            // this lane's A operands for the eight AVX lanes (scale digits times the
+            // nibbles), formed once for all activation tiles
+            long alo[8], ahi[8];
+#pragma unroll
+            for (int L = 0; L < 8; ++L) {
+                const uint32_t w = *(const uint32_t*) (sw + arow_l * MF_WS + 16 + 32 * gq + 4 * L);
+                const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+                alo[L] = pack2(mul_bytes(lo, sa_ & 7u), mul_bytes(hi, sb_ & 7u));
+                ahi[L] = pack2(mul_bytes(lo, sa_ >> 3), mul_bytes(hi, sb_ >> 3));
+            }
+            const int nbt = (ntok + 15) / 16;   // activation tiles holding rows (uniform)
+            // activation tiles in pairs: two independent MFMA accumulation chains
+#pragma unroll
+            for (int bp = 0; bp < NB; bp += 2) {
+                if (bp >= nbt) break;
+                v4i slo[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}}, shi[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
+                v4i sm[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
+#pragma unroll
+                for (int L = 0; L < 8; ++L)
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const uint8_t* ab = sa + (16 * (bp + u) + lr) * MF_AS + 16 + 64 * gq + 4 * L;
+                        const long bq = pack2(*(const uint32_t*) ab, *(const uint32_t*) (ab + 32));
+                        slo[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(alo[L], bq, slo[u], 0, 0, 0);
+                        shi[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ahi[L], bq, shi[u], 0, 0, 0);
+                    }
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const v4i bq = *(const v4i*) (sa + (16 * (bp + u) + lr) * MF_AS + 16 + 64 * q + 16 * gq);
+                        sm[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(v4i{mbq[q], mbq[q], mbq[q], mbq[q]}, bq, sm[u],
+                                                                      0, 0, 0);
+                    }
 #pragma unroll
                 for (int u = 0; u < 2; ++u) {
-                    const uint8_t* ab = sa + (16 * (bp + u) + lr) * MF_AS + 16 + 64 * gq + 4 * L;
-                    const long bq = pack2(*(const uint32_t*) ab, *(const uint32_t*) (ab + 32));
-                    slo[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(alo[L], bq, slo[u], 0, 0, 0);
-                    shi[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ahi[L], bq, shi[u], 0, 0, 0);
-                }
+                    const float dy = *(const float*) (sa + (16 * (bp + u) + lr) * MF_AS);
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-#pragma unroll
-                for (int u = 0; u < 2; ++u) {
-                    const v4i bq = *(const v4i*) (sa + (16 * (bp + u) + lr) * MF_AS + 16 + 64 * q + 16 * gq);
-                    sm[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(v4i{mbq[q], mbq[q], mbq[q], mbq[q]}, bq, sm[u], 0, 0, 0);
-                }
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const float dy = *(const float*) (sa + (16 * (bp + u) + lr) * MF_AS);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    acc[bp + u][r] = __builtin_fmaf(dy * xd[r], (float) (8 * shi[u][r] + slo[u][r]), acc[bp + u][r]);
-                    accm[bp + u][r] = __builtin_fmaf(-dy * xdm[r], (float) sm[u][r], accm[bp + u][r]);
+                    for (int r = 0; r < 4; ++r) {
+                        acc[r][bp + u] = __builtin_fmaf(dy * xd[r], (float) (8 * shi[u][r] + slo[u][r]), acc[r][bp + u]);
+                        accm[r][bp + u] = __builtin_fmaf(-dy * xdm[r], (float) sm[u][r], accm[r][bp + u]);
+                    }
                 }
             }
         }
-        if (i + 1 < nb) store(buf ^ 1);
+    };
+    auto stage = [&](int i, const uint8_t* cw, const uint8_t* ca, uint8_t* nw, uint8_t* na) __attribute__((always_inline)) {
+        if (i + 1 < nb) vm_wait<VM_STAGE>();   // super-block i + 1's loads may stay in flight
+        else vm_wait<0>();
         lds_barrier();
+        if (i + 2 < nb) issue(nw, na, i + 2);
+        compute(cw, ca);
+    };
+    issue(s_w0, s_a0, 0);
+    if (nb > 1) issue(s_w1, s_a1, 1);
+    for (int i = 0; i < nb; i += 3) {
+        stage(i, s_w0, s_a0, s_w2, s_a2);
+        if (i + 1 < nb) stage(i + 1, s_w1, s_a1, s_w0, s_a0);
+        if (i + 2 < nb) stage(i + 2, s_w2, s_a2, s_w1, s_a1);
     }
+    if constexpr (EXACT) {
+        // hsum_float_8(acc) + ((m0 + m2) + (m1 + m3)); rows r0 + 16 wave + 4 gq .. +3 of B row lr
+        float o[4];
 #pragma unroll
-    for (int bt = 0; bt < MF_NB; ++bt) {
-        const int row = 16 * bt + lr;
-        if (bt < nbt && row < ntok) {
-            const int e = s_et[row][0], tt = s_et[row][1];
+        for (int r = 0; r < 4; ++r) {
+            const float* a = acc[r];
+            const float hs = ((a[4] + a[0]) + (a[6] + a[2])) + ((a[5] + a[1]) + (a[7] + a[3]));
+            const float* mm = accm[r];
+            o[r] = hs + ((mm[0] + mm[2]) + (mm[1] + mm[3]));
+        }
+        if (lr < ntok) {
+            const int e = s_et[lr][0], tt = s_et[lr][1];
             float* dp = (float*) ((char*) m.dst + (size_t) e * m.dst_nb1 + (size_t) tt * m.dst_nb2) + r0 + 16 * wave +
                         4 * gq;
-            *(float4*) dp = float4{acc[bt][0] + accm[bt][0], acc[bt][1] + accm[bt][1], acc[bt][2] + accm[bt][2],
-                                   acc[bt][3] + accm[bt][3]};
+            *(float4*) dp = float4{o[0], o[1], o[2], o[3]};
+        }
+    } else {
+#pragma unroll
+        for (int bt = 0; bt < NB; ++bt) {
+            const int row = 16 * bt + lr;
+            if (row < ntok) {
+                const int e = s_et[row][0], tt = s_et[row][1];
+                float* dp = (float*) ((char*) m.dst + (size_t) e * m.dst_nb1 + (size_t) tt * m.dst_nb2) + r0 +
+                            16 * wave + 4 * gq;
+                *(float4*) dp = float4{acc[0][bt] + accm[0][bt], acc[1][bt] + accm[1][bt], acc[2][bt] + accm[2][bt],
+                                       acc[3][bt] + accm[3][bt]};
+            }
         }
     }
-    }
 }
+
+// The block-sum form (mfma_exact == 0) of the same kernel.  Same integers, fewer
+// float steps: per (weight row, activation row, super-block) the eight AVX
+// lanes' sums add up in the MFMA's own int32 accumulator (sumi = sum_L sumi_L,
+// the block's exact integer dot with its scales; |sumi| < 2^25), the mins
+// likewise (prod = sum_m prod_m), and the float steps are
+// acc = fma(y.d fp16(x.d), sumi, acc) and accm = fma(-y.d fp16(x.dmin), prod,
+// accm) over the super-blocks, then acc + accm.  The integers are ggml's
+// exactly; the floats round in another order (relative difference ~1e-7 of the
+// terms).  Each wave keeps four 16-row activation tiles per pass (64 rows), so a
+// weight row's operand is formed once for all of them and the tile is streamed
+// a quarter as often.
 
 // Whether the matrix-core kernel can take (type, shape, strides): Q4_K rows of
 // 16-byte aligned super-blocks, 64-row tiles, 16-byte aligned output rows.
@@ -470,12 +419,12 @@ bool mmid_mfma_supported(const MmidArgs& m) {
 int launch_mmid_mfma(const MmidArgs& m, hipStream_t stream) {
     if (!mmid_mfma_supported(m)) return -2;
     // one workgroup per (work item, row tile)
-    const int64_t groups = mf_max_items(m, m.mfma_exact ? MF_RX : MF_RB) * (m.N / MF_M);
+    const int64_t groups = mf_max_items(m, 16 * (m.mfma_exact ? MF_NB_X : MF_NB_B)) * (m.N / MF_M);
     if (groups == 0) return 0;
     if (groups > (int64_t(1) << 30)) return -2;
     const unsigned grid = (unsigned) groups;
-    if (m.mfma_exact) hipLaunchKernelGGL(k_mmid_mfma_q4k, dim3(grid), dim3(256), 0, stream, m);
-    else hipLaunchKernelGGL(k_mmid_mfma_q4k_bs, dim3(grid), dim3(256), 0, stream, m);
+    if (m.mfma_exact) hipLaunchKernelGGL((k_mmid_mfma_q4k<MF_NB_X, true>), dim3(grid), dim3(256), 0, stream, m);
+    else hipLaunchKernelGGL((k_mmid_mfma_q4k<MF_NB_B, false>), dim3(grid), dim3(256), 0, stream, m);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
