@@ -74,7 +74,7 @@ qw::MmidArgs mmid_args(int type, const void* as, int64_t K, int64_t N, int64_t n
                        const uint8_t* bq, int64_t ne11, size_t bq_row, const int32_t* rows, const int32_t* active,
                        const int32_t* active_off, const int32_t* n_active, int64_t max_active,
                        const int32_t* slot_of, int64_t n_slot_of, float* dst, size_t nb1, size_t nb2,
-                       int64_t max_rows, int64_t n_pairs) {
+                       int64_t max_rows, int64_t n_pairs, bool fp32_out = false) {
     qw::MmidArgs m{};
     m.type = type;
     m.w = (const uint8_t*) as;
@@ -103,15 +103,14 @@ qw::MmidArgs mmid_args(int type, const void* as, int64_t K, int64_t N, int64_t n
     m.mfma_min_rows = 0;
     m.max_rows = max_rows;
     m.n_pairs = n_pairs;
+    // the matrix cores' float tail: block sums where the form allows them -- under
+    // QWMOE_MFMA_AUTO only for fp32_out, the down projection of a layer entry
+    // point, whose output reaches nothing but the weighted sum
+    m.mfma_exact = g_lib.mfma_form == QWMOE_MFMA_EXACT || (g_lib.mfma_form == QWMOE_MFMA_AUTO && !fp32_out);
     const bool mfma = g_lib.mfma_min_rows > 0 && max_rows >= g_lib.mfma_min_rows && qw::mmid_mfma_supported(m);
     if (mfma) m.mfma_min_rows = g_lib.mfma_min_rows;
-    m.mfma_exact = g_lib.mfma_form != QWMOE_MFMA_BLOCK_SUM;
     return m;
 }
-
-// The matrix-core form of a down projection inside a layer entry point: its
-// fp32 output only reaches the weighted sum, so QWMOE_MFMA_AUTO takes block sums.
-int down_mfma_exact() { return g_lib.mfma_form == QWMOE_MFMA_EXACT; }
 
 int mmid_launch(const qw::MmidArgs& m, hipStream_t st) {
     int rc = qw::launch_mmid_gemv(m, st);
@@ -489,8 +488,7 @@ int qwmoe_shared_expert_add(void* stream, const qwmoe_shared_expert* se, int64_t
     }
     // ggml_mul(ggml_silu(g), u) rounds as swiglu_split does: silu, then one multiply
     qw::MmidArgs md = mmid_args(se->type_down, se->down, F, H, 1, se->down_nb1, se->down_nb1 * (size_t) H, aq, 1, qd,
-                                rows, active, active_off, n_active, 1, nullptr, 0, sh, (size_t) H * 4, (size_t) H * 4, T, T);
-    md.mfma_exact = down_mfma_exact();
+                                rows, active, active_off, n_active, 1, nullptr, 0, sh, (size_t) H * 4, (size_t) H * 4, T, T, true);
     md.swiglu_gate = gateo;
     md.swiglu_up = upo;
     if (vd == qw::T_Q8_K && qw::mmid_gemv_swiglu_ok(md)) {
@@ -601,8 +599,7 @@ int qwmoe_ffn_layer(void* stream, const qwmoe_layer* L, const float* x, int64_t 
     if (!aq) return QWMOE_ERR_WORKSPACE;
     qw::MmidArgs md = mmid_args(L->type_down, L->down, F, H, L->n_slots_down, L->down_nb1, L->down_nb2, aq, k, qd,
                                 G.rows, G.active, G.active_off, G.n_active, G.max_active, L->slot_down,
-                                L->slot_down ? E : 0, ex, (size_t) H * 4, (size_t) H * 4 * (size_t) k, T, k * T);
-    md.mfma_exact = down_mfma_exact();
+                                L->slot_down ? E : 0, ex, (size_t) H * 4, (size_t) H * 4 * (size_t) k, T, k * T, true);
     md.swiglu_gate = gateo;
     md.swiglu_up = upo;
     if (vd == qw::T_Q8_K && qw::mmid_gemv_swiglu_ok(md)) {

@@ -408,22 +408,238 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 // weight row's operand is formed once for all of them and the tile is streamed
 // a quarter as often.
 
-// Whether the matrix-core kernel can take (type, shape, strides): Q4_K rows of
-// 16-byte aligned super-blocks, 64-row tiles, 16-byte aligned output rows.
+// Q6_K x Q8_K on the matrix cores, block-sum form only: the down projections of
+// the layer entry points under QWMOE_MFMA_AUTO, every projection under
+// QWMOE_MFMA_BLOCK_SUM.  (Replaying ggml's eight float lanes for Q6_K is not
+// done on the matrix cores; the exact form keeps Q6_K on the GEMV.)
+//
+// Reference: ggml_vec_dot_q6_K_q8_K (ggml/src/ggml-cpu/arch/x86/quants.c:
+// 2426-2508).  Its integers, per (weight row, activation row, super-block):
+//     sumi = sum_{j<16} sc_j * sum_{e<16} (q6[16 j + e] - 32) * q8[16 j + e]
+// with q6 = ql nibble | qh 2-bit field << 4 (the dequantize_row_q6_K order:
+// element 128 n + 32 c + l of half n is nibble c >> 1 of ql[64 n + 32 (c & 1) +
+// l] and bits 2c of qh[32 n + l]); here acc = fma(y.d * fp16(x.d), sumi, acc).
+//
+// Matrix-core mapping: v_mfma_i32_32x32x16_i8, K = 16 = one sub-block, so D
+// holds each sub-block's dot and its scale multiplies after (sc_j * q6 does not
+// fit int8).  A = 32 activation rows (lane l: row l % 32, elements 8 (l / 32)
+// .. +8 of the sub-block), B = 32 weight rows (the same elements); D lane l,
+// register r: weight row l % 32, activation row 8 (r / 4) + 4 (l / 32) + r % 4.
+// Each lane thus owns one weight row of D and that row's scale.  The int32 sums
+// are exact (|sumi| < 2^28).
+//
+// Workgroup: 64 weight rows x 64 activation rows; wave w takes weight rows
+// 32 (w & 1) .. +32 and activation rows 32 (w >> 1) .. +32.  Two stage buffers:
+// super-block i + 1 is copied into LDS while i is computed.  A Q6_K block (210
+// B) starts 2 bytes past a dword boundary in every other super-block, so a row's
+// block is staged as the 53 dwords from the dword at or below its start (s = 0
+// or 2 bytes before it); with s = 0 the 53rd dword would reach past the block
+// (and, for the matrix's last block, past the tensor), so it repeats the 52nd
+// and the block's fp16 d comes from a separate 16-bit copy per row.
+constexpr int M6_M = 64;              // weight rows per workgroup
+constexpr int M6_N = 64;              // activation rows per pass (= rows per work item)
+constexpr uint32_t M6_WS = 212;       // LDS stride of a staged Q6_K block (53 dwords)
+
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) k_mmid_mfma_q6k(MmidArgs m) {
+    constexpr int WDMA = 53;                        // weight DMA instructions per stage (64 rows x 53 dwords)
+    constexpr int WDW = (WDMA + 3) / 4;             // ... per wave, at most
+    constexpr int ADMA = M6_N * 68 / 64;            // activation DMA instructions per stage
+    constexpr int ADW = (ADMA + 3) / 4;
+    __shared__ __align__(16) uint8_t s_w0[M6_M * M6_WS];
+    __shared__ __align__(16) uint8_t s_w1[M6_M * M6_WS];
+    __shared__ __align__(16) uint8_t s_a0[M6_N * MF_AS];
+    __shared__ __align__(16) uint8_t s_a1[M6_N * MF_AS];
+    __shared__ __align__(16) uint32_t s_d0[M6_M];   // fp16 d of each staged weight row (zero-extended)
+    __shared__ __align__(16) uint32_t s_d1[M6_M];
+    __shared__ int32_t s_arow[M6_N];
+    __shared__ int32_t s_et[M6_N][2];
+    __shared__ int s_item[2];
+    const int tiles = (int) (m.N / M6_M);
+    const int tile = (int) (blockIdx.x % (uint32_t) tiles);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    mf_item(m, (int) (blockIdx.x / (uint32_t) tiles), M6_N, wave, lane, s_item);
+    const int g = s_item[0];
+    if (g < 0) return;   // past the last item (light experts have none: the GEMV kernel's)
+    const int p0 = m.active_off[g] + M6_N * s_item[1], p1 = min(m.active_off[g + 1], p0 + M6_N);
+    const int bin = m.active[g];
+    int64_t mat = bin;
+    if (m.slot_of) mat = (bin < m.n_slot_of) ? m.slot_of[bin] : -1;
+    if (mat < 0 || mat >= m.n_as) {
+        if (threadIdx.x == 0 && m.status) atomicOr(m.status, 4);
+        return;
+    }
+    const int64_t r0 = (int64_t) tile * M6_M;
+    const int nb = (int) (m.K / QK_K);
+    const uint32_t nb1 = (uint32_t) m.nb1;
+    const uint8_t* wtile = m.w + (size_t) mat * m.nb2 + (size_t) r0 * m.nb1;
+    const i32x4 wrsrc = rsrc_words(wtile, (uint32_t) M6_M * nb1);
+    const i32x4 arsrc = rsrc_words(m.act_q, 0x7fffffffu);
+    const int ntok = p1 - p0;   // 1 .. M6_N
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    if (tid < M6_N) {
+        const int pp = p0 + (tid < ntok ? tid : 0);   // rows past ntok are staged from row 0, never written
+        const int e = m.rows[2 * pp], t = m.rows[2 * pp + 1];
+        s_et[tid][0] = e;
+        s_et[tid][1] = t;
+        s_arow[tid] = (int) ((int64_t) (e % m.b_ne1) + (int64_t) t * m.b_ne1);
+    }
+    lds_barrier();
+    // weight slot q = 64 j + lane: row q / 53, dword u = q % 53.  wbase = row * nb1 + 4 u,
+    // bit 0 set for u = 52 (row * nb1 is even); the stage's offset is
+    // (wbase + 210 i) & ~3, less 4 for u = 52 when the block starts on a dword
+    uint32_t wbase[WDW], aoff[ADW];
+#pragma unroll
+    for (int k = 0; k < WDW; ++k) {
+        const int q = 64 * (wave + 4 * k) + lane;
+        const int qc = q < M6_M * 53 ? q : 0;
+        const int row = qc / 53, u = qc - 53 * row;
+        wbase[k] = (uint32_t) row * nb1 + 4u * (uint32_t) u + (u == 52 ? 1u : 0u);
+    }
+#pragma unroll
+    for (int k = 0; k < ADW; ++k) {
+        const int sl = 64 * (wave + 4 * k) + lane;
+        const int slc = sl < M6_N * 68 ? sl : 0;
+        const int n = slc / 68, u = slc - 68 * n;
+        aoff[k] = (uint32_t) s_arow[n] * (uint32_t) m.act_row_bytes + (u < 4 ? 0u : 4u * (uint32_t) u - 12u);
+    }
+    const uint32_t dvoff = (uint32_t) lane * nb1 + 208u;   // wave 0: the fp16 d of row `lane`
+    auto issue = [&](uint8_t* sw, uint8_t* sa, uint32_t* sd, int i) __attribute__((always_inline)) {
+        // LDS bases recomputed per stage, not kept live across the loop (scalar registers)
+        uint32_t lw = (uint32_t) (uintptr_t) sw, la = (uint32_t) (uintptr_t) sa, ld = (uint32_t) (uintptr_t) sd;
+        int w = wv;
+        asm volatile("" : "+s"(lw), "+s"(la), "+s"(ld), "+s"(w));
+        const uint32_t si = 210u * (uint32_t) i;
+#pragma unroll
+        for (int k = 0; k < WDW; ++k)
+            if (w + 4 * k < WDMA) {
+                const uint32_t t = wbase[k] + si;
+                const uint32_t vo = (t & ~3u) - (((t & 1u) && !(t & 2u)) ? 4u : 0u);
+                dma_b32(wrsrc, lw + 256u * (uint32_t) (w + 4 * k), vo, 0u);
+            }
+        if (w == 0) {
+            uint32_t keep;
+            asm volatile(
+                "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_ushort %2, %3, %4 offen lds\n\t"
+                "s_mov_b32 m0, %0"
+                : "=&s"(keep)
+                : "s"(ld), "v"(dvoff), "s"(wrsrc), "s"(si)
+                : "memory");
+        }
+#pragma unroll
+        for (int k = 0; k < ADW; ++k)
+            if (w + 4 * k < ADMA) dma_b32(arsrc, la + 256u * (uint32_t) (w + 4 * k), aoff[k], 292u * (uint32_t) i);
+    };
+
+    const int lc = lane & 31, h = lane >> 5;
+    const int wrow = 32 * (wave & 1) + lc;         // this lane's weight row in the tile (D column)
+    const int arow0 = 32 * (wave >> 1);            // this wave's first activation row in the pass
+    const uint32_t par = ((uint32_t) wrow * nb1) & 2u;
+    float acc[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+
+    auto compute = [&](const uint8_t* sw, const uint8_t* sa, const uint32_t* sd, int i) __attribute__((always_inline)) {
+        const uint32_t sh = 8u * (par ^ (2u * ((uint32_t) i & 1u)));   // bit shift of the block in its staged dwords
+        const uint32_t* wr = (const uint32_t*) (sw + wrow * M6_WS);
+        // two dwords of the block at byte offset off (a multiple of 4) of this row
+        auto w2 = [&](int off, uint32_t& lo, uint32_t& hi) __attribute__((always_inline)) {
+            const uint32_t a = wr[off / 4], b = wr[off / 4 + 1], c = wr[off / 4 + 2];
+            lo = __builtin_amdgcn_alignbyte(b, a, sh / 8);
+            hi = __builtin_amdgcn_alignbyte(c, b, sh / 8);
+        };
+        uint32_t sc4[4];
+#pragma unroll
+        for (int k = 0; k < 4; k += 2) w2(192 + 4 * k, sc4[k], sc4[k + 1]);
+        int32_t isum[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) isum[r] = 0;
+#pragma unroll
+        for (int n = 0; n < 2; ++n) {
+            uint32_t ql[2][2][2], qh[2][2];   // [c & 1][p][dword], [p][dword]
+#pragma unroll
+            for (int c1 = 0; c1 < 2; ++c1)
+#pragma unroll
+                for (int p = 0; p < 2; ++p) w2(64 * n + 32 * c1 + 16 * p + 8 * h, ql[c1][p][0], ql[c1][p][1]);
+#pragma unroll
+            for (int p = 0; p < 2; ++p) w2(128 + 32 * n + 16 * p + 8 * h, qh[p][0], qh[p][1]);
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) {
+                const int j = 8 * n + jj, c = jj >> 1, p = jj & 1;
+                uint32_t bw[2];
+#pragma unroll
+                for (int d = 0; d < 2; ++d) {
+                    const uint32_t v = ((ql[c & 1][p][d] >> (4 * (c >> 1))) & 0x0F0F0F0Fu) |
+                                       (((qh[p][d] >> (2 * c)) & 0x03030303u) << 4);
+                    const uint32_t x = v ^ 0x20202020u;          // q6 - 32 as a 6-bit two's complement ...
+                    const uint32_t sg = x & 0x20202020u;
+                    bw[d] = x | (sg << 1) | (sg << 2);           // ... sign-extended to 8 bits
+                }
+                const uint8_t* ab = sa + (arow0 + lc) * MF_AS + 16 + 16 * j + 8 * h;
+                const long aq = pack2(*(const uint32_t*) ab, *(const uint32_t*) (ab + 4));
+                typedef int v16i __attribute__((ext_vector_type(16)));
+                v16i z16;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) z16[r] = 0;
+                const v16i dd = __builtin_amdgcn_mfma_i32_32x32x16_i8(aq, pack2(bw[0], bw[1]), z16, 0, 0, 0);
+                const int scj = (int) (int8_t) ((sc4[j >> 2] >> (8 * (j & 3))) & 0xffu);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) isum[r] += scj * dd[r];
+            }
+        }
+        const float dx = h2f((uint16_t) sd[wrow]);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int ar = arow0 + 8 * (r >> 2) + 4 * h + (r & 3);
+            const float dy = *(const float*) (sa + ar * MF_AS);
+            acc[r] = __builtin_fmaf(dy * dx, (float) isum[r], acc[r]);
+        }
+    };
+    // stage i: wait for its copies, barrier (every wave is done with stage i - 1,
+    // whose buffer then takes super-block i + 1), issue i + 1, compute i
+    issue(s_w0, s_a0, s_d0, 0);
+    for (int i = 0; i < nb; i += 2) {
+        vm_wait<0>();
+        lds_barrier();
+        if (i + 1 < nb) issue(s_w1, s_a1, s_d1, i + 1);
+        compute(s_w0, s_a0, s_d0, i);
+        if (i + 1 >= nb) break;
+        vm_wait<0>();
+        lds_barrier();
+        if (i + 2 < nb) issue(s_w0, s_a0, s_d0, i + 2);
+        compute(s_w1, s_a1, s_d1, i + 1);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int ar = arow0 + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (ar < ntok) {
+            const int e = s_et[ar][0], tt = s_et[ar][1];
+            float* dp = (float*) ((char*) m.dst + (size_t) e * m.dst_nb1 + (size_t) tt * m.dst_nb2);
+            dp[r0 + wrow] = acc[r];
+        }
+    }
+}
+
+// Whether a matrix-core kernel can take (type, form, shape, strides): Q4_K rows
+// of 16-byte aligned super-blocks, or (block-sum form) Q6_K rows on 4-byte
+// aligned tensors; 64-row tiles, 16-byte aligned output rows.
 bool mmid_mfma_supported(const MmidArgs& m) {
-    return m.type == T_Q4_K && m.N % MF_M == 0 && m.K % QK_K == 0 && m.nb1 % 16 == 0 && m.nb2 % 16 == 0 &&
-           ((uintptr_t) m.w & 15) == 0 && m.dst_nb1 % 16 == 0 && m.dst_nb2 % 16 == 0 && ((uintptr_t) m.dst & 15) == 0 &&
-           m.act_row_bytes % 4 == 0 && ((uintptr_t) m.act_q & 3) == 0;
+    const bool q4 = m.type == T_Q4_K && m.nb1 % 16 == 0 && m.nb2 % 16 == 0 && ((uintptr_t) m.w & 15) == 0;
+    const bool q6 = m.type == T_Q6_K && !m.mfma_exact && m.nb1 % 2 == 0 && m.nb2 % 4 == 0 && ((uintptr_t) m.w & 3) == 0 &&
+                    (uint64_t) M6_M * m.nb1 < (1ull << 31);
+    return (q4 || q6) && m.N % MF_M == 0 && m.K % QK_K == 0 && m.dst_nb1 % 16 == 0 && m.dst_nb2 % 16 == 0 &&
+           ((uintptr_t) m.dst & 15) == 0 && m.act_row_bytes % 4 == 0 && ((uintptr_t) m.act_q & 3) == 0;
 }
 
 int launch_mmid_mfma(const MmidArgs& m, hipStream_t stream) {
     if (!mmid_mfma_supported(m)) return -2;
     // one workgroup per (work item, row tile)
-    const int64_t groups = mf_max_items(m, 16 * (m.mfma_exact ? MF_NB_X : MF_NB_B)) * (m.N / MF_M);
+    const int rows = m.type == T_Q6_K ? M6_N : 16 * (m.mfma_exact ? MF_NB_X : MF_NB_B);
+    const int64_t groups = mf_max_items(m, rows) * (m.N / MF_M);
     if (groups == 0) return 0;
     if (groups > (int64_t(1) << 30)) return -2;
     const unsigned grid = (unsigned) groups;
-    if (m.mfma_exact) hipLaunchKernelGGL((k_mmid_mfma_q4k<MF_NB_X, true>), dim3(grid), dim3(256), 0, stream, m);
+    if (m.type == T_Q6_K) hipLaunchKernelGGL(k_mmid_mfma_q6k, dim3(grid), dim3(256), 0, stream, m);
+    else if (m.mfma_exact) hipLaunchKernelGGL((k_mmid_mfma_q4k<MF_NB_X, true>), dim3(grid), dim3(256), 0, stream, m);
     else hipLaunchKernelGGL((k_mmid_mfma_q4k<MF_NB_B, false>), dim3(grid), dim3(256), 0, stream, m);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }

@@ -114,6 +114,17 @@ def exact_acts(rng, shape, K: int) -> np.ndarray:
     return x
 
 
+def exact_q6k(rng, rows: int, K: int, max_scale: int) -> np.ndarray:
+    """Q6_K rows with d = 1.0 and scales in [-max_scale, max_scale]: dequantized
+    weights sc * (q6 - 32) are small integers, every fp32 operation exact."""
+    nb = K // 256
+    blk = np.zeros((rows, nb, 210), np.uint8)
+    blk[..., 0:192] = rng.integers(0, 256, (rows, nb, 192)).astype(np.uint8)       # ql, qh
+    blk[..., 192:208] = rng.integers(-max_scale, max_scale + 1, (rows, nb, 16)).astype(np.int8).view(np.uint8)
+    blk[..., 208:210] = np.array([0x00, 0x3C], np.uint8)                            # fp16 1.0
+    return blk.reshape(-1)
+
+
 def zipf_ids(rng, T: int, k: int, n_as: int, s: float = 1.1) -> np.ndarray:
     p = np.arange(1, n_as + 1, dtype=np.float64) ** -s
     p /= p.sum()
@@ -173,6 +184,64 @@ def test_mfma_random(orc, K, N, T, k, n_as, ne11):
     note(f"  heavy experts {int((counts >= 32).sum())}/{n_as}, max rows {counts.max()}, "
          f"block-sum rel err {rel_err(got, want):.3e}")
     assert prev == AUTO
+    assert np.array_equal(bits(got_auto), bits(want))
+    assert rel_err(got, want) < BS_TOL
+    assert ops.device_status(clear=True) == 0
+
+
+def test_exact_inputs_pin_the_crafted_q6k_blocks(orc):
+    """The crafted Q6_K blocks dequantize to sc * (q6 - 32) with d = 1 (the
+    oracle's dequantizer, pinned against ggml), i.e. small integers."""
+    rng = np.random.default_rng(1)
+    w = exact_q6k(rng, 4, 512, max_scale=4)
+    deq = orc.dequantize(Q6_K, w, 4 * 512)
+    assert np.all(deq == np.round(deq)) and np.max(np.abs(deq)) <= 4 * 32
+
+
+@pytest.mark.parametrize("K,N,min_rows", [(768, 128, 8), (1536, 64, 1), (512, 192, 16)])
+def test_mfma_q6k_integer_core_bit_exact(orc, K, N, min_rows):
+    """Q6_K heavy experts on the matrix cores (block-sum form; K = 768 puts every
+    other super-block 2 bytes past a dword boundary in odd rows) on exact inputs:
+    bit-identical to the reference."""
+    note(f"Q6_K matrix-core mul_mat_id, exact inputs: K={K} N={N} min_rows={min_rows}")
+    rng = np.random.default_rng(K + N + 6)
+    n_as, T = 5, 70
+    w = exact_q6k(rng, n_as * N, K, max_scale=4)
+    b = exact_acts(rng, (T, 1), K)
+    ids = np.stack([[0, 1 + (t % 4)] for t in range(T)]).astype(np.int32)   # expert 0 takes all 70 tokens
+    want = orc.mul_mat_id(Q6_K, K, N, n_as, w, b, ids)
+    prev, prev_f = ops.set_mfma_min_rows(min_rows), ops.set_mfma_form(BLOCK_SUM)
+    try:
+        got = host(ops.mul_mat_id(Q6_K, dev(w), K, N, n_as, dev(b), dev(ids)))
+    finally:
+        ops.set_mfma_min_rows(prev)
+        ops.set_mfma_form(prev_f)
+    assert np.array_equal(bits(got), bits(want))
+    assert ops.device_status(clear=True) == 0
+
+
+@pytest.mark.parametrize("K,N,T,k,n_as", [(1536, 256, 256, 8, 16), (768, 2048, 128, 8, 16), (512, 64, 97, 4, 8)])
+def test_mfma_q6k_random(orc, K, N, T, k, n_as):
+    """Random Q6_K weights and N(0,1) activations: block sums within BS_TOL of the
+    reference; the default form (exact for mul_mat_id, so Q6_K stays on the
+    GEMV) bit-identical."""
+    note(f"Q6_K matrix-core mul_mat_id, random data: K={K} N={N} T={T} k={k} n_as={n_as}")
+    rng = np.random.default_rng(T + N + 6)
+    w = orc.quantize(Q6_K, (rng.standard_normal((n_as * N, K)) * 0.02).astype(np.float32))
+    b = rng.standard_normal((T, 1, K)).astype(np.float32)
+    ids = zipf_ids(rng, T, k, n_as)
+    want = orc.mul_mat_id(Q6_K, K, N, n_as, w, b, ids)
+    counts = np.bincount(ids.reshape(-1), minlength=n_as)
+    assert counts.max() >= 32, "the case must route some expert to the matrix cores"
+    wd, bd, idd = dev(w), dev(b), dev(ids)
+    got_auto = host(ops.mul_mat_id(Q6_K, wd, K, N, n_as, bd, idd))
+    prev = ops.set_mfma_form(BLOCK_SUM)
+    try:
+        got = host(ops.mul_mat_id(Q6_K, wd, K, N, n_as, bd, idd))
+    finally:
+        ops.set_mfma_form(prev)
+    note(f"  heavy experts {int((counts >= 8).sum())}/{n_as}, max rows {counts.max()}, "
+         f"block-sum rel err {rel_err(got, want):.3e}")
     assert np.array_equal(bits(got_auto), bits(want))
     assert rel_err(got, want) < BS_TOL
     assert ops.device_status(clear=True) == 0
