@@ -36,9 +36,18 @@ typedef unsigned int u32x4m __attribute__((ext_vector_type(4)));
 
 constexpr int MF_M = 64;          // weight rows per workgroup (4 waves x 16)
 constexpr uint32_t MF_WS = 144;   // LDS stride of a staged Q4_K block (9 x 16 B)
-constexpr uint32_t MF_AS = 272;   // LDS stride of a staged Q8_K block (68 dwords): d at 0, qs at 16
-constexpr int MF_NB_X = 1;        // 16-row activation tiles per pass: exact form
+constexpr uint32_t MF_AS = 276;   // LDS stride of a staged Q8_K block (69 dwords): d at 0, qs at 16
+                                  // (an odd dword stride: 16 or 32 lanes reading one offset of their
+                                  // rows hit distinct banks)
+constexpr int MF_AD = 69;         // dwords per staged activation row
+constexpr int MF_NB_X = 1;        // 16-row activation tiles per pass: exact form (2 measured no faster)
 constexpr int MF_NB_B = 4;        // block-sum form
+
+// 16 bytes of LDS at a 4-byte aligned address.
+__device__ __forceinline__ v4i lds_v4i(const uint8_t* p) {
+    const uint32_t* q = (const uint32_t*) p;
+    return v4i{(int) q[0], (int) q[1], (int) q[2], (int) q[3]};
+}
 
 // Waits until at most N of this wave's vector memory operations are in flight.
 template <int N>
@@ -157,23 +166,24 @@ inline int64_t mf_max_items(const MmidArgs& m, int R) {
 // every wave's copies are in LDS.
 //
 // Staging layout: weight chunk q (16 B; 9 per row) at byte 16 q, from row q / 9,
-// byte 16 (q % 9) of the super-block; activation dword slot u of row n (68 per
-// row) at byte 4 (68 n + u), from byte 0 (u < 4: the d, padded) or 4 u - 12 (the
-// qs) of the row's Q8_K block.  One DMA instruction covers 64 consecutive chunks
-// or slots, one per lane.
+// byte 16 (q % 9) of the super-block; activation dword slot u of row n (69 per
+// row) at byte 4 (69 n + u), from byte 4 u - 12 (4 <= u < 68: the qs) or 0 (the
+// d, and the pads) of the row's Q8_K block.  One DMA instruction covers 64
+// consecutive chunks or slots, one per lane; the last activation instruction's
+// slots past the rows land in the buffer's slack.
 template <int NB, bool EXACT>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) k_mmid_mfma_q4k(MmidArgs m) {
     constexpr int NR = 16 * NB;               // activation rows per pass (and per item)
-    constexpr int AW = NR * 68 / 64;          // activation DMA instructions per stage
+    constexpr int AW = (NR * MF_AD + 63) / 64;   // activation DMA instructions per stage
     constexpr int AWW = (AW + 3) / 4;         // ... per wave, at most
     constexpr int VM_STAGE = 2 + AW / 4;      // fewest DMA instructions any wave issues per stage
-    static_assert(NR * 68 % 64 == 0 && VM_STAGE <= 63, "staging shape");
+    static_assert(VM_STAGE <= 63, "staging shape");
     __shared__ __align__(16) uint8_t s_w0[MF_M * MF_WS];
     __shared__ __align__(16) uint8_t s_w1[MF_M * MF_WS];
     __shared__ __align__(16) uint8_t s_w2[MF_M * MF_WS];
-    __shared__ __align__(16) uint8_t s_a0[NR * MF_AS];
-    __shared__ __align__(16) uint8_t s_a1[NR * MF_AS];
-    __shared__ __align__(16) uint8_t s_a2[NR * MF_AS];
+    __shared__ __align__(16) uint8_t s_a0[AW * 256];   // NR * MF_AS and the last instruction's slack
+    __shared__ __align__(16) uint8_t s_a1[AW * 256];
+    __shared__ __align__(16) uint8_t s_a2[AW * 256];
     __shared__ int32_t s_arow[NR];
     __shared__ int32_t s_et[NR][2];
     __shared__ int s_item[2];
@@ -219,9 +229,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
     for (int k = 0; k < AWW; ++k) {
         const int sl = 64 * (wave + 4 * k) + lane;
-        const int slc = sl < NR * 68 ? sl : 0;
-        const int n = slc / 68, u = slc - 68 * n;
-        aoff[k] = (uint32_t) s_arow[n] * (uint32_t) m.act_row_bytes + (u < 4 ? 0u : 4u * (uint32_t) u - 12u);
+        const int slc = sl < NR * MF_AD ? sl : 0;
+        const int n = slc / MF_AD, u = slc - MF_AD * n;
+        aoff[k] = (uint32_t) s_arow[n] * (uint32_t) m.act_row_bytes + (u < 4 || u >= 68 ? 0u : 4u * (uint32_t) u - 12u);
     }
     auto issue = [&](uint8_t* sw, uint8_t* sa, int i) __attribute__((always_inline)) {
         // LDS bases recomputed per stage, not kept live across the loop (scalar registers)
@@ -235,17 +245,21 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
             if (wv + 4 * k < AW) dma_b32(arsrc, la + 256u * (uint32_t) (wv + 4 * k), aoff[k], 292u * (uint32_t) i);
     };
 
-    // EXACT: per output (D register r) the eight AVX lanes and four min lanes.
-    // Block sums: per activation tile and output, one chain and one for the mins.
-    constexpr int NACC = EXACT ? 8 : NB, NACCM = EXACT ? 4 : NB;
-    float acc[4][NACC], accm[4][NACCM];
+    // EXACT: per activation tile and output (D register r) the eight AVX lanes
+    // and four min lanes.  Block sums: per output and tile, one chain and one
+    // for the mins.
+    constexpr int XT = EXACT ? NB : 1, NACC = EXACT ? 8 : NB, NACCM = EXACT ? 4 : NB;
+    float acc[XT][4][NACC], accm[XT][4][NACCM];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int t = 0; t < XT; ++t)
 #pragma unroll
-        for (int L = 0; L < NACC; ++L) acc[r][L] = 0.0f;
+        for (int r = 0; r < 4; ++r) {
 #pragma unroll
-        for (int q = 0; q < NACCM; ++q) accm[r][q] = 0.0f;
-    }
+            for (int L = 0; L < NACC; ++L) acc[t][r][L] = 0.0f;
+#pragma unroll
+            for (int q = 0; q < NACCM; ++q) accm[t][r][q] = 0.0f;
+        }
+    const int nbt = (ntok + 15) / 16;   // activation tiles holding rows (uniform)
 
     auto compute = [&](const uint8_t* sw, const uint8_t* sa) __attribute__((always_inline)) {
         // this lane's A row: the 6-bit scales and mins of the 8 sub-blocks
@@ -275,12 +289,16 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
             mbq[q] = (int) (((mnw >> (8 * (sbk & 3))) & 0xffu) * 0x01010101u);
         }
         if constexpr (EXACT) {
-            const float dy = *(const float*) (sa + lr * MF_AS);
-            float d[4], dmin[4];
+            // A operands formed once per AVX lane for all activation tiles
+            float d[NB][4], dmin[NB][4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                d[r] = dy * xd[r];
-                dmin[r] = -dy * xdm[r];
+            for (int t = 0; t < NB; ++t) {
+                const float dy = *(const float*) (sa + (16 * t + lr) * MF_AS);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    d[t][r] = dy * xd[r];
+                    dmin[t][r] = -dy * xdm[r];
+                }
             }
 #pragma unroll
             for (int L = 0; L < 8; ++L) {
@@ -288,22 +306,30 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
                 const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
                 const long a_lo = pack2(mul_bytes(lo, sa_ & 7u), mul_bytes(hi, sb_ & 7u));
                 const long a_hi = pack2(mul_bytes(lo, sa_ >> 3), mul_bytes(hi, sb_ >> 3));
-                const uint8_t* ab = sa + lr * MF_AS + 16 + 64 * gq + 4 * L;
-                const long bq = pack2(*(const uint32_t*) ab, *(const uint32_t*) (ab + 32));
-                const v4i z4 = v4i{0, 0, 0, 0};
-                const v4i dlo = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_lo, bq, z4, 0, 0, 0);
-                const v4i dhi = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_hi, bq, z4, 0, 0, 0);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) acc[r][L] = __builtin_fmaf(d[r], (float) (8 * dhi[r] + dlo[r]), acc[r][L]);
+                for (int t = 0; t < NB; ++t) {
+                    if (t >= nbt) break;
+                    const uint8_t* ab = sa + (16 * t + lr) * MF_AS + 16 + 64 * gq + 4 * L;
+                    const long bq = pack2(*(const uint32_t*) ab, *(const uint32_t*) (ab + 32));
+                    const v4i z4 = v4i{0, 0, 0, 0};
+                    const v4i dlo = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_lo, bq, z4, 0, 0, 0);
+                    const v4i dhi = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_hi, bq, z4, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        acc[t][r][L] = __builtin_fmaf(d[t][r], (float) (8 * dhi[r] + dlo[r]), acc[t][r][L]);
+                }
             }
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const v4i bq = *(const v4i*) (sa + lr * MF_AS + 16 + 64 * q + 16 * gq);
-                const v4i dm = __builtin_amdgcn_mfma_i32_16x16x64_i8(v4i{mbq[q], mbq[q], mbq[q], mbq[q]}, bq,
-                                                                     v4i{0, 0, 0, 0}, 0, 0, 0);
+            for (int q = 0; q < 4; ++q)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) accm[r][q] = __builtin_fmaf(dmin[r], (float) dm[r], accm[r][q]);
-            }
+                for (int t = 0; t < NB; ++t) {
+                    if (t >= nbt) break;
+                    const v4i bq = lds_v4i(sa + (16 * t + lr) * MF_AS + 16 + 64 * q + 16 * gq);
+                    const v4i dm = __builtin_amdgcn_mfma_i32_16x16x64_i8(v4i{mbq[q], mbq[q], mbq[q], mbq[q]}, bq,
+                                                                         v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) accm[t][r][q] = __builtin_fmaf(dmin[t][r], (float) dm[r], accm[t][r][q]);
+                }
         } else {
             // this lane's A operands for the eight AVX lanes (scale digits times the
             // nibbles), formed once for all activation tiles
@@ -315,7 +341,6 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
                 alo[L] = pack2(mul_bytes(lo, sa_ & 7u), mul_bytes(hi, sb_ & 7u));
                 ahi[L] = pack2(mul_bytes(lo, sa_ >> 3), mul_bytes(hi, sb_ >> 3));
             }
-            const int nbt = (ntok + 15) / 16;   // activation tiles holding rows (uniform)
             // activation tiles in pairs: two independent MFMA accumulation chains
 #pragma unroll
             for (int bp = 0; bp < NB; bp += 2) {
@@ -335,7 +360,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
                 for (int q = 0; q < 4; ++q)
 #pragma unroll
                     for (int u = 0; u < 2; ++u) {
-                        const v4i bq = *(const v4i*) (sa + (16 * (bp + u) + lr) * MF_AS + 16 + 64 * q + 16 * gq);
+                        const v4i bq = lds_v4i(sa + (16 * (bp + u) + lr) * MF_AS + 16 + 64 * q + 16 * gq);
                         sm[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(v4i{mbq[q], mbq[q], mbq[q], mbq[q]}, bq, sm[u],
                                                                       0, 0, 0);
                     }
@@ -344,8 +369,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
                     const float dy = *(const float*) (sa + (16 * (bp + u) + lr) * MF_AS);
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        acc[r][bp + u] = __builtin_fmaf(dy * xd[r], (float) (8 * shi[u][r] + slo[u][r]), acc[r][bp + u]);
-                        accm[r][bp + u] = __builtin_fmaf(-dy * xdm[r], (float) sm[u][r], accm[r][bp + u]);
+                        acc[0][r][bp + u] =
+                            __builtin_fmaf(dy * xd[r], (float) (8 * shi[u][r] + slo[u][r]), acc[0][r][bp + u]);
+                        accm[0][r][bp + u] = __builtin_fmaf(-dy * xdm[r], (float) sm[u][r], accm[0][r][bp + u]);
                     }
                 }
             }
@@ -366,20 +392,24 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
         if (i + 2 < nb) stage(i + 2, s_w2, s_a2, s_w1, s_a1);
     }
     if constexpr (EXACT) {
-        // hsum_float_8(acc) + ((m0 + m2) + (m1 + m3)); rows r0 + 16 wave + 4 gq .. +3 of B row lr
-        float o[4];
+        // hsum_float_8(acc) + ((m0 + m2) + (m1 + m3)); rows r0 + 16 wave + 4 gq .. +3 of B row 16 t + lr
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float* a = acc[r];
-            const float hs = ((a[4] + a[0]) + (a[6] + a[2])) + ((a[5] + a[1]) + (a[7] + a[3]));
-            const float* mm = accm[r];
-            o[r] = hs + ((mm[0] + mm[2]) + (mm[1] + mm[3]));
-        }
-        if (lr < ntok) {
-            const int e = s_et[lr][0], tt = s_et[lr][1];
-            float* dp = (float*) ((char*) m.dst + (size_t) e * m.dst_nb1 + (size_t) tt * m.dst_nb2) + r0 + 16 * wave +
-                        4 * gq;
-            *(float4*) dp = float4{o[0], o[1], o[2], o[3]};
+        for (int t = 0; t < NB; ++t) {
+            float o[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float* a = acc[t][r];
+                const float hs = ((a[4] + a[0]) + (a[6] + a[2])) + ((a[5] + a[1]) + (a[7] + a[3]));
+                const float* mm = accm[t][r];
+                o[r] = hs + ((mm[0] + mm[2]) + (mm[1] + mm[3]));
+            }
+            const int row = 16 * t + lr;
+            if (row < ntok) {
+                const int e = s_et[row][0], tt = s_et[row][1];
+                float* dp = (float*) ((char*) m.dst + (size_t) e * m.dst_nb1 + (size_t) tt * m.dst_nb2) + r0 +
+                            16 * wave + 4 * gq;
+                *(float4*) dp = float4{o[0], o[1], o[2], o[3]};
+            }
         }
     } else {
 #pragma unroll
@@ -389,8 +419,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
                 const int e = s_et[row][0], tt = s_et[row][1];
                 float* dp = (float*) ((char*) m.dst + (size_t) e * m.dst_nb1 + (size_t) tt * m.dst_nb2) + r0 +
                             16 * wave + 4 * gq;
-                *(float4*) dp = float4{acc[0][bt] + accm[0][bt], acc[1][bt] + accm[1][bt], acc[2][bt] + accm[2][bt],
-                                       acc[3][bt] + accm[3][bt]};
+                *(float4*) dp = float4{acc[0][0][bt] + accm[0][0][bt], acc[0][1][bt] + accm[0][1][bt],
+                                       acc[0][2][bt] + accm[0][2][bt], acc[0][3][bt] + accm[0][3][bt]};
             }
         }
     }
@@ -428,33 +458,34 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 // Each lane thus owns one weight row of D and that row's scale.  The int32 sums
 // are exact (|sumi| < 2^28).
 //
-// Workgroup: 64 weight rows x 64 activation rows; wave w takes weight rows
-// 32 (w & 1) .. +32 and activation rows 32 (w >> 1) .. +32.  Two stage buffers:
+// Workgroup: 128 weight rows x 32 activation rows (one work item), wave w takes
+// weight rows 32 w .. +32 (a tile past N leaves its last waves idle; 32-row
+// items keep the padding of partly filled items small).  Two stage buffers:
 // super-block i + 1 is copied into LDS while i is computed.  A Q6_K block (210
 // B) starts 2 bytes past a dword boundary in every other super-block, so a row's
 // block is staged as the 53 dwords from the dword at or below its start (s = 0
 // or 2 bytes before it); with s = 0 the 53rd dword would reach past the block
 // (and, for the matrix's last block, past the tensor), so it repeats the 52nd
 // and the block's fp16 d comes from a separate 16-bit copy per row.
-constexpr int M6_M = 64;              // weight rows per workgroup
-constexpr int M6_N = 64;              // activation rows per pass (= rows per work item)
+constexpr int M6_M = 128;             // weight rows per workgroup
+constexpr int M6_N = 32;              // activation rows per pass (= rows per work item)
 constexpr uint32_t M6_WS = 212;       // LDS stride of a staged Q6_K block (53 dwords)
 
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) k_mmid_mfma_q6k(MmidArgs m) {
-    constexpr int WDMA = 53;                        // weight DMA instructions per stage (64 rows x 53 dwords)
+    constexpr int WDMA = M6_M * 53 / 64;            // weight DMA instructions per stage (M6_M rows x 53 dwords)
     constexpr int WDW = (WDMA + 3) / 4;             // ... per wave, at most
-    constexpr int ADMA = M6_N * 68 / 64;            // activation DMA instructions per stage
+    constexpr int ADMA = (M6_N * MF_AD + 63) / 64;  // activation DMA instructions per stage
     constexpr int ADW = (ADMA + 3) / 4;
     __shared__ __align__(16) uint8_t s_w0[M6_M * M6_WS];
     __shared__ __align__(16) uint8_t s_w1[M6_M * M6_WS];
-    __shared__ __align__(16) uint8_t s_a0[M6_N * MF_AS];
-    __shared__ __align__(16) uint8_t s_a1[M6_N * MF_AS];
-    __shared__ __align__(16) uint32_t s_d0[M6_M];   // fp16 d of each staged weight row (zero-extended)
+    __shared__ __align__(16) uint8_t s_a0[ADMA * 256];   // M6_N * MF_AS and the last instruction's slack
+    __shared__ __align__(16) uint8_t s_a1[ADMA * 256];
+    __shared__ __align__(16) uint32_t s_d0[M6_M];   // fp16 d of each staged weight row (zero-extended dword)
     __shared__ __align__(16) uint32_t s_d1[M6_M];
     __shared__ int32_t s_arow[M6_N];
     __shared__ int32_t s_et[M6_N][2];
     __shared__ int s_item[2];
-    const int tiles = (int) (m.N / M6_M);
+    const int tiles = (int) ((m.N + M6_M - 1) / M6_M);
     const int tile = (int) (blockIdx.x % (uint32_t) tiles);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     mf_item(m, (int) (blockIdx.x / (uint32_t) tiles), M6_N, wave, lane, s_item);
@@ -469,10 +500,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
         return;
     }
     const int64_t r0 = (int64_t) tile * M6_M;
+    const int trows = (int) min((int64_t) M6_M, m.N - r0);   // 64 or 128 (N % 64 == 0)
     const int nb = (int) (m.K / QK_K);
     const uint32_t nb1 = (uint32_t) m.nb1;
     const uint8_t* wtile = m.w + (size_t) mat * m.nb2 + (size_t) r0 * m.nb1;
-    const i32x4 wrsrc = rsrc_words(wtile, (uint32_t) M6_M * nb1);
+    const i32x4 wrsrc = rsrc_words(wtile, (uint32_t) trows * nb1);   // rows past trows read as zeros
     const i32x4 arsrc = rsrc_words(m.act_q, 0x7fffffffu);
     const int ntok = p1 - p0;   // 1 .. M6_N
     const int wv = __builtin_amdgcn_readfirstlane(wave);
@@ -498,11 +530,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
     for (int k = 0; k < ADW; ++k) {
         const int sl = 64 * (wave + 4 * k) + lane;
-        const int slc = sl < M6_N * 68 ? sl : 0;
-        const int n = slc / 68, u = slc - 68 * n;
-        aoff[k] = (uint32_t) s_arow[n] * (uint32_t) m.act_row_bytes + (u < 4 ? 0u : 4u * (uint32_t) u - 12u);
+        const int slc = sl < M6_N * MF_AD ? sl : 0;
+        const int n = slc / MF_AD, u = slc - MF_AD * n;
+        aoff[k] = (uint32_t) s_arow[n] * (uint32_t) m.act_row_bytes + (u < 4 || u >= 68 ? 0u : 4u * (uint32_t) u - 12u);
     }
-    const uint32_t dvoff = (uint32_t) lane * nb1 + 208u;   // wave 0: the fp16 d of row `lane`
+    const uint32_t dvoff = (uint32_t) lane * nb1 + 208u;   // the fp16 d of row `lane` (+ 64 for the second copy)
     auto issue = [&](uint8_t* sw, uint8_t* sa, uint32_t* sd, int i) __attribute__((always_inline)) {
         // LDS bases recomputed per stage, not kept live across the loop (scalar registers)
         uint32_t lw = (uint32_t) (uintptr_t) sw, la = (uint32_t) (uintptr_t) sa, ld = (uint32_t) (uintptr_t) sd;
@@ -516,13 +548,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
                 const uint32_t vo = (t & ~3u) - (((t & 1u) && !(t & 2u)) ? 4u : 0u);
                 dma_b32(wrsrc, lw + 256u * (uint32_t) (w + 4 * k), vo, 0u);
             }
-        if (w == 0) {
+        if (w < M6_M / 64) {   // waves 0, 1: rows 64 w + lane
             uint32_t keep;
+            const uint32_t ldw = ld + 256u * (uint32_t) w, sio = si + 64u * nb1 * (uint32_t) w;
             asm volatile(
                 "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_ushort %2, %3, %4 offen lds\n\t"
                 "s_mov_b32 m0, %0"
                 : "=&s"(keep)
-                : "s"(ld), "v"(dvoff), "s"(wrsrc), "s"(si)
+                : "s"(ldw), "v"(dvoff), "s"(wrsrc), "s"(sio)
                 : "memory");
         }
 #pragma unroll
@@ -531,8 +564,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     };
 
     const int lc = lane & 31, h = lane >> 5;
-    const int wrow = 32 * (wave & 1) + lc;         // this lane's weight row in the tile (D column)
-    const int arow0 = 32 * (wave >> 1);            // this wave's first activation row in the pass
+    const int wrow = 32 * wave + lc;               // this lane's weight row in the tile (D column)
+    constexpr int arow0 = 0;                       // the wave's activation rows: the whole pass
+    const bool active = 32 * wv < trows;           // uniform: the wave's weight rows exist
     const uint32_t par = ((uint32_t) wrow * nb1) & 2u;
     float acc[16];
 #pragma unroll
@@ -582,8 +616,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
                 for (int r = 0; r < 16; ++r) z16[r] = 0;
                 const v16i dd = __builtin_amdgcn_mfma_i32_32x32x16_i8(aq, pack2(bw[0], bw[1]), z16, 0, 0, 0);
                 const int scj = (int) (int8_t) ((sc4[j >> 2] >> (8 * (j & 3))) & 0xffu);
+                // |dd| <= 16 * 32 * 128 < 2^23: the 24-bit multiply-add (full rate) is exact.
+                // The empty asm keeps each sum's adds one per sub-block, so they fuse
+                // with the multiplies (v_mad_i32_i24) instead of pairing into add3s.
 #pragma unroll
-                for (int r = 0; r < 16; ++r) isum[r] += scj * dd[r];
+                for (int r = 0; r < 16; ++r) {
+                    isum[r] += mul24(scj, dd[r]);
+                    asm("" : "+v"(isum[r]));
+                }
             }
         }
         const float dx = h2f((uint16_t) sd[wrow]);
@@ -601,13 +641,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
         vm_wait<0>();
         lds_barrier();
         if (i + 1 < nb) issue(s_w1, s_a1, s_d1, i + 1);
-        compute(s_w0, s_a0, s_d0, i);
+        if (active) compute(s_w0, s_a0, s_d0, i);
         if (i + 1 >= nb) break;
         vm_wait<0>();
         lds_barrier();
         if (i + 2 < nb) issue(s_w0, s_a0, s_d0, i + 2);
-        compute(s_w1, s_a1, s_d1, i + 1);
+        if (active) compute(s_w1, s_a1, s_d1, i + 1);
     }
+    if (!active) return;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const int ar = arow0 + 8 * (r >> 2) + 4 * h + (r & 3);
@@ -625,7 +666,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 bool mmid_mfma_supported(const MmidArgs& m) {
     const bool q4 = m.type == T_Q4_K && m.nb1 % 16 == 0 && m.nb2 % 16 == 0 && ((uintptr_t) m.w & 15) == 0;
     const bool q6 = m.type == T_Q6_K && !m.mfma_exact && m.nb1 % 2 == 0 && m.nb2 % 4 == 0 && ((uintptr_t) m.w & 3) == 0 &&
-                    (uint64_t) M6_M * m.nb1 < (1ull << 31);
+                    (uint64_t) M6_M * m.nb1 + 64ull * m.nb1 < (1ull << 31);
     return (q4 || q6) && m.N % MF_M == 0 && m.K % QK_K == 0 && m.dst_nb1 % 16 == 0 && m.dst_nb2 % 16 == 0 &&
            ((uintptr_t) m.dst & 15) == 0 && m.act_row_bytes % 4 == 0 && ((uintptr_t) m.act_q & 3) == 0;
 }
@@ -634,7 +675,7 @@ int launch_mmid_mfma(const MmidArgs& m, hipStream_t stream) {
     if (!mmid_mfma_supported(m)) return -2;
     // one workgroup per (work item, row tile)
     const int rows = m.type == T_Q6_K ? M6_N : 16 * (m.mfma_exact ? MF_NB_X : MF_NB_B);
-    const int64_t groups = mf_max_items(m, rows) * (m.N / MF_M);
+    const int64_t groups = mf_max_items(m, rows) * (m.type == T_Q6_K ? (m.N + M6_M - 1) / M6_M : m.N / MF_M);
     if (groups == 0) return 0;
     if (groups > (int64_t(1) << 30)) return -2;
     const unsigned grid = (unsigned) groups;
