@@ -189,6 +189,16 @@ int qwmoe_group_by_expert(void * stream, const int32_t * ids, int64_t n_ids, int
 int qwmoe_router_topk(void * stream, const float * W, const float * x, int64_t H, int64_t E, int64_t k,
                       int64_t T, size_t x_nb1, float clamp_min, float scale, int32_t * ids, float * weights,
                       float * probs);
+/* The router of a resident-only decode (core/runtime.cpp:870-881, under
+ * cache_fast_build && resident_decode): want = argsort_top_k(logits, k), the
+ * experts the unmasked router prefers, recorded for the host's background
+ * refill; then logits = logits + mask (the layer's row of resmask_all: 0 for a
+ * resident expert, -inf for an absent one) before the softmax, so top-k can
+ * never pick an absent expert.  mask: f32 [E] added to every token's logits (NULL:
+ * none); want: [k, T] (NULL: not recorded).  Otherwise as qwmoe_router_topk. */
+int qwmoe_router_topk_resident(void * stream, const float * W, const float * x, int64_t H, int64_t E, int64_t k,
+                               int64_t T, size_t x_nb1, float clamp_min, float scale, const float * mask,
+                               int32_t * want, int32_t * ids, float * weights, float * probs);
 
 /* ggml_swiglu_split(gate, up) = silu(gate) * up (ggml/src/ggml.c:3060-3065,
  * ggml/src/ggml-cpu/ops.cpp:3182-3238): `rows` rows of n values, n % 8 == 0. */
@@ -257,6 +267,12 @@ typedef struct qwmoe_layer {
     const int32_t * slot_gate; /* [E] or NULL */
     const int32_t * slot_up;
     const int32_t * slot_down;
+    /* Resident-only routing (core/runtime.cpp:870-881; see
+     * qwmoe_router_topk_resident): resmask f32 [E] added to the router logits
+     * before the softmax, want_ids [k, T] the top k of the raw logits.  Both
+     * NULL for the plain router. */
+    const float * resmask;
+    int32_t * want_ids;
 } qwmoe_layer;
 
 /* The whole layer for T tokens: router -> 3x mul_mat_id + swiglu -> weighted

@@ -914,14 +914,23 @@ int orc_mul_mat_id(int type, int64_t K, int64_t N, int64_t n_as, const void * as
 
 // Router of core/runtime.cpp:869-897: logits = W x (mul_mat, vec_dot_f32),
 // soft_max, argsort_top_k, get_rows, sum_rows, clamp(6.103515625e-5, inf), div,
-// optional scale.  W: [E][H]; x: [T][H]; ids/weights: [T][k].
-void orc_router(int64_t H, int64_t E, int64_t k, int64_t T, const float * W, const float * x,
-                float scale, int32_t * ids, float * weights, float * logits_out, float * probs_out) {
-    std::vector<float> logits((size_t) E), probs((size_t) E);
+// optional scale.  W: [E][H]; x: [T][H]; ids/weights: [T][k].  With resident-
+// only routing (870-881): want = argsort_top_k of the raw logits ([T][k]; NULL:
+// not recorded), then logits + mask ([E], ggml_add broadcast over the tokens;
+// NULL: none) before the softmax.  logits_out holds the raw logits.
+void orc_router_resident(int64_t H, int64_t E, int64_t k, int64_t T, const float * W, const float * x,
+                         float scale, const float * mask, int32_t * want, int32_t * ids, float * weights,
+                         float * logits_out, float * probs_out) {
+    std::vector<float> logits((size_t) E), masked((size_t) E), probs((size_t) E);
     std::vector<int32_t> order((size_t) E);
     for (int64_t t = 0; t < T; ++t) {
         for (int64_t e = 0; e < E; ++e) logits[(size_t) e] = vec_dot_f32((int) H, W + e * H, x + t * H, 2);
-        soft_max_row((int) E, logits.data(), probs.data());
+        if (want) {
+            argsort_desc((int) E, logits.data(), order.data());
+            for (int64_t i = 0; i < k; ++i) want[t * k + i] = order[(size_t) i];
+        }
+        for (int64_t e = 0; e < E; ++e) masked[(size_t) e] = mask ? logits[(size_t) e] + mask[e] : logits[(size_t) e];
+        soft_max_row((int) E, masked.data(), probs.data());
         argsort_desc((int) E, probs.data(), order.data());
         double s = 0.0;  // ggml_vec_sum_f32: double accumulation
         for (int64_t i = 0; i < k; ++i) {
@@ -940,8 +949,14 @@ void orc_router(int64_t H, int64_t E, int64_t k, int64_t T, const float * W, con
     }
 }
 
+void orc_router(int64_t H, int64_t E, int64_t k, int64_t T, const float * W, const float * x,
+                float scale, int32_t * ids, float * weights, float * logits_out, float * probs_out) {
+    orc_router_resident(H, E, k, T, W, x, scale, nullptr, nullptr, ids, weights, logits_out, probs_out);
+}
+
 // One MoE FFN layer, core/runtime.cpp:861-974 (resident path), optionally
-// followed by RMS_NORM (rms_eps >= 0).  Weight tensors are [E] matrices of
+// followed by RMS_NORM (rms_eps >= 0); resmask / want_out: resident-only routing
+// as in orc_router_resident (both nullable).  Weight tensors are [E] matrices of
 // [N][row] bytes: gate/up [F rows of H], down [H rows of F]; slot tables
 // (nullable) remap logical expert -> slot for each role.  Any output may be NULL.
 int orc_moe_layer(int64_t H, int64_t E, int64_t k, int64_t F, int64_t T, int type_gate,
@@ -950,10 +965,10 @@ int orc_moe_layer(int64_t H, int64_t E, int64_t k, int64_t F, int64_t T, int typ
                   const int32_t * slot_gate, const int32_t * slot_up, const int32_t * slot_down,
                   float scale, float rms_eps, const float * x, float * out, float * xnext,
                   int32_t * ids_out, float * weights_out, float * gate_out, float * up_out,
-                  float * act_out, float * experts_out) {
+                  float * act_out, float * experts_out, const float * resmask, int32_t * want_out) {
     std::vector<int32_t> ids((size_t) (T * k));
     std::vector<float> w((size_t) (T * k));
-    orc_router(H, E, k, T, w_router, x, scale, ids.data(), w.data(), nullptr, nullptr);
+    orc_router_resident(H, E, k, T, w_router, x, scale, resmask, want_out, ids.data(), w.data(), nullptr, nullptr);
     std::vector<float> up((size_t) (T * k * F)), gate((size_t) (T * k * F)), act((size_t) (T * k * F)),
         ex((size_t) (T * k * H));
     const size_t rs_gu = row_size(type_gate, H), rs_u = row_size(type_up, H), rs_d = row_size(type_down, F);

@@ -195,6 +195,54 @@ static void copy_2d(const ggml_tensor * t, void * dst, size_t elt) {
     }
 }
 
+// The router of a resident-only decode, core/runtime.cpp:869-897 with the
+// cache_fast_build && resident_decode branch (870-881): want =
+// argsort_top_k(logits), logits = add(logits, mask [E] broadcast over the
+// tokens), then soft_max / argsort_top_k / get_rows / sum_rows / clamp / div
+// (/ scale).  W: f32 [H, E]; x [T, H]; want / ids / weights [T, k]; probs [T, E]
+// (nullable).
+int qwref_router_resident(int64_t H, int64_t E, int64_t k, int64_t T, const float * w_router, const float * x,
+                          const float * mask, float expert_weights_scale, int32_t * want, int32_t * ids,
+                          float * weights_out, float * probs_out, int n_threads) {
+    ensure_init();
+    ggml_init_params ip = { sizeof(float) * (size_t) T * (size_t) (H + 4 * E + 4 * k) + sizeof(float) * (size_t) E
+                                + ggml_tensor_overhead() * 64 + ggml_graph_overhead() + (1 << 20),
+                            nullptr, false };
+    ggml_context * ctx = ggml_init(ip);
+    ggml_tensor * Wr = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, H, E);
+    memcpy(Wr->data, w_router, sizeof(float) * H * E);
+    ggml_tensor * X = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, H, T);
+    memcpy(X->data, x, sizeof(float) * H * T);
+    ggml_tensor * M = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, E, 1);
+    memcpy(M->data, mask, sizeof(float) * E);
+    ggml_tensor * logits = ggml_mul_mat(ctx, Wr, X);
+    ggml_tensor * wnt = ggml_argsort_top_k(ctx, logits, (int) k);
+    ggml_tensor * probs = ggml_soft_max(ctx, ggml_add(ctx, logits, M));
+    ggml_tensor * selected = ggml_argsort_top_k(ctx, probs, (int) k);
+    ggml_tensor * weights = ggml_get_rows(ctx, ggml_reshape_3d(ctx, probs, 1, E, T), selected);
+    weights = ggml_reshape_2d(ctx, weights, k, T);
+    ggml_tensor * wsum = ggml_clamp(ctx, ggml_sum_rows(ctx, weights), 6.103515625e-5f, INFINITY);
+    weights = ggml_div(ctx, weights, wsum);
+    if (expert_weights_scale != 0.0f && expert_weights_scale != 1.0f)
+        weights = ggml_scale(ctx, weights, expert_weights_scale);
+    ggml_cgraph * gf = ggml_new_graph(ctx);
+    ggml_build_forward_expand(gf, wnt);
+    ggml_build_forward_expand(gf, weights);
+    ggml_build_forward_expand(gf, selected);
+    ggml_cplan plan = ggml_graph_plan(gf, n_threads, nullptr);
+    std::vector<uint8_t> work(plan.work_size + 64);
+    plan.work_data = work.data();
+    const int rc = ggml_graph_compute(gf, &plan) == GGML_STATUS_SUCCESS ? 0 : -1;
+    if (rc == 0) {
+        if (want) copy_2d(wnt, want, 4);
+        if (ids) copy_2d(selected, ids, 4);
+        if (weights_out) copy_2d(weights, weights_out, 4);
+        if (probs_out) copy_2d(probs, probs_out, 4);
+    }
+    ggml_free(ctx);
+    return rc;
+}
+
 // Evaluates the layer on x [T, H] (row-major == ggml [H, T]).  Any output
 // pointer may be NULL.  ids/weights are [T, k]; logits/probs [T, E];
 // gate/up/act [T, k, F]; experts [T, k, H]; out / xnext [T, H].

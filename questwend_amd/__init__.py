@@ -38,6 +38,7 @@ class Layer(C.Structure):
         ("down_nb1", C.c_size_t), ("down_nb2", C.c_size_t),
         ("n_slots_gate", C.c_int64), ("n_slots_up", C.c_int64), ("n_slots_down", C.c_int64),
         ("slot_gate", C.c_void_p), ("slot_up", C.c_void_p), ("slot_down", C.c_void_p),
+        ("resmask", C.c_void_p), ("want_ids", C.c_void_p),
     ]
 
 
@@ -74,6 +75,7 @@ SIGNATURES = {
     "qwmoe_mul_mat_id_noalloc": (I, [P, I, P, I64, I64, I64, SZ, SZ, P, I64, I64, SZ, SZ, P, I64, SZ, P, I64, P, SZ, SZ]),
     "qwmoe_group_by_expert": (I, [P, P, I64, I64, SZ, I64, P, P, P]),
     "qwmoe_router_topk": (I, [P, P, P, I64, I64, I64, I64, SZ, F, F, P, P, P]),
+    "qwmoe_router_topk_resident": (I, [P, P, P, I64, I64, I64, I64, SZ, F, F, P, P, P, P, P]),
     "qwmoe_swiglu": (I, [P, P, P, P, I64, I64]),
     "qwmoe_weighted_sum": (I, [P, P, P, P, I64, I64, I64]),
     "qwmoe_rms_norm": (I, [P, P, P, I64, I64, F]),

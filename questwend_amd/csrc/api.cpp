@@ -390,6 +390,13 @@ int qwmoe_mul_mat_id_noalloc(void* stream, int type, const void* as, int64_t ne0
 
 int qwmoe_router_topk(void* stream, const float* W, const float* x, int64_t H, int64_t E, int64_t k, int64_t T,
                       size_t x_nb1, float clamp_min, float scale, int32_t* ids, float* weights, float* probs) {
+    return qwmoe_router_topk_resident(stream, W, x, H, E, k, T, x_nb1, clamp_min, scale, nullptr, nullptr, ids, weights,
+                                      probs);
+}
+
+int qwmoe_router_topk_resident(void* stream, const float* W, const float* x, int64_t H, int64_t E, int64_t k,
+                               int64_t T, size_t x_nb1, float clamp_min, float scale, const float* mask,
+                               int32_t* want, int32_t* ids, float* weights, float* probs) {
     if (!g_lib.ready) return QWMOE_ERR_NOT_INITIALIZED;
     if (!W || !x || !ids || !weights || H <= 0 || E <= 0 || k <= 0 || k > E || T < 0) return QWMOE_ERR_INVALID_ARG;
     if (E % 8 || E > 512 || H % 4 || x_nb1 % 16 || ((uintptr_t) x & 15) || ((uintptr_t) W & 15) || x_nb1 < (size_t) H * 4)
@@ -412,6 +419,8 @@ int qwmoe_router_topk(void* stream, const float* W, const float* x, int64_t H, i
     a.probs = probs;
     a.logits = nullptr;
     a.status = g_lib.status;
+    a.mask = mask;
+    a.want = want;
     return qw::launch_router(a, logits, S(stream));
 }
 
@@ -553,6 +562,8 @@ int qwmoe_ffn_layer(void* stream, const qwmoe_layer* L, const float* x, int64_t 
     ra.ids = ids;
     ra.weights = w;
     ra.status = g_lib.status;
+    ra.mask = L->resmask;
+    ra.want = L->want_ids;
     if (E % 8 || E > 512 || H % 4) return QWMOE_ERR_UNSUPPORTED;
     // x quantized once per distinct activation type of gate / up; a small batch's
     // Q8_K copy is made by the router launch

@@ -290,7 +290,7 @@ __global__ void __launch_bounds__(GROUP_WAVES * 64) k_topk_group(RouterArgs ra, 
     const bool small = ra.T * ra.k <= 64;
     if (w < ra.T)
         topk_token<true>(logits, ra.E, ra.k, w, ra.clamp_min, ra.scale, small ? s_ids : ra.ids, ra.weights, ra.probs,
-                         ra.status, p, gsum, order, stack, need_sort, lane);
+                         ra.status, p, gsum, order, stack, need_sort, lane, ra.mask, ra.want);
     __syncthreads();   // every token's ids are written
     int32_t* hist = (int32_t*) ((uint8_t*) dyn + (size_t) GROUP_WAVES * ((per_wave + 15u) & ~15u));
     if (small) {

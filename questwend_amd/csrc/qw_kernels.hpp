@@ -28,6 +28,8 @@ struct RouterArgs {
     float* probs;         // optional [T][E]
     int32_t* status;      // optional device word: bit 0 set when a top-k tie needed the exact sort
     void* xq;             // optional [T][H/256] Q8_K of x, made in the same launch (T <= 16, dense x rows)
+    const float* mask;    // optional [E] added to every token's logits before the softmax
+    int32_t* want;        // optional [T][k]: top k of the raw (unmasked) logits
 };
 int launch_router(const RouterArgs& a, float* logits_ws, hipStream_t stream);
 

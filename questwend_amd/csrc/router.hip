@@ -105,14 +105,15 @@ constexpr int ROUTER_EPL = 8;
 __global__ void __launch_bounds__(64) k_router_topk(const float* __restrict__ logits, int64_t E, int64_t k,
                                                     int64_t T, float clamp_min, float scale, int32_t* __restrict__ ids,
                                                     float* __restrict__ weights, float* __restrict__ probs_out,
-                                                    int32_t* __restrict__ status) {
+                                                    int32_t* __restrict__ status, const float* __restrict__ mask,
+                                                    int32_t* __restrict__ want) {
     __shared__ __align__(16) float p[64 * ROUTER_EPL];
     __shared__ float gsum[64 * ROUTER_EPL / 8];
     __shared__ int32_t order[64 * ROUTER_EPL];
     __shared__ SortRange sort_stack[SORT_STACK];
     __shared__ int need_sort;
     topk_token<false>(logits, E, k, blockIdx.x, clamp_min, scale, ids, weights, probs_out, status, p, gsum, order,
-                      sort_stack, &need_sort, threadIdx.x);
+                      sort_stack, &need_sort, threadIdx.x, mask, want);
 }
 
 int launch_router(const RouterArgs& a, float* logits_ws, hipStream_t stream) {
@@ -132,7 +133,7 @@ int launch_router(const RouterArgs& a, float* logits_ws, hipStream_t stream) {
     }
     if (!a.ids) return hipGetLastError() == hipSuccess ? 0 : -3;   // logits only (top-k fused elsewhere)
     hipLaunchKernelGGL(k_router_topk, dim3((unsigned) a.T), dim3(64), 0, stream, logits, a.E, a.k, a.T, a.clamp_min,
-                       a.scale, a.ids, a.weights, a.probs, a.status);
+                       a.scale, a.ids, a.weights, a.probs, a.status, a.mask, a.want);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 

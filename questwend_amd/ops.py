@@ -148,6 +148,21 @@ def router_topk(W, x, k: int, clamp_min: float = 6.103515625e-5, scale: float = 
     return (ids, w, probs) if want_probs else (ids, w)
 
 
+def router_topk_resident(W, x, k: int, mask=None, want: bool = True, clamp_min: float = 6.103515625e-5,
+                         scale: float = 0.0):
+    """Resident-only routing: mask f32 [E] (0 / -inf) added to the logits before
+    the softmax; want = the unmasked top k.  Returns ids, weights (, want) [T, k]."""
+    torch = _torch()
+    E, H = W.shape
+    T = x.shape[0]
+    ids = torch.empty((T, k), dtype=torch.int32, device=x.device)
+    w = torch.empty((T, k), dtype=torch.float32, device=x.device)
+    wt = torch.empty((T, k), dtype=torch.int32, device=x.device) if want else None
+    check(lib().qwmoe_router_topk_resident(stream(), _ptr(W), _ptr(x), H, E, k, T, x.stride(0) * 4, clamp_min, scale,
+                                           _ptr(mask), _ptr(wt), _ptr(ids), _ptr(w), None), "router_topk_resident")
+    return (ids, w, wt) if want else (ids, w)
+
+
 def swiglu(gate, up):
     torch = _torch()
     n = gate.shape[-1]
@@ -196,8 +211,11 @@ def shared_expert_add(se: SharedExpert, x, moe_out, resid=None, out=None):
     return out
 
 
-def make_layer(H, E, k, F, router, gate, up, down, types, n_slots=None, slots=None, scale=0.0) -> Layer:
-    """Builds a ``qwmoe_layer`` from device tensors (dense expert matrices)."""
+def make_layer(H, E, k, F, router, gate, up, down, types, n_slots=None, slots=None, scale=0.0, resmask=None,
+               want_ids=None) -> Layer:
+    """Builds a ``qwmoe_layer`` from device tensors (dense expert matrices).
+    resmask: f32 [E] (0 / -inf) for resident-only routing; want_ids: i32 [T, k]
+    receiving the unmasked top k (both optional; the caller keeps them alive)."""
     tg, tu, td = types
     rg, ru, rd = row_size(tg, H), row_size(tu, H), row_size(td, F)
     ns = n_slots or (E, E, E)
@@ -213,6 +231,7 @@ def make_layer(H, E, k, F, router, gate, up, down, types, n_slots=None, slots=No
     L.down_nb1, L.down_nb2 = rd, rd * H
     L.n_slots_gate, L.n_slots_up, L.n_slots_down = ns
     L.slot_gate, L.slot_up, L.slot_down = _ptr(sg), _ptr(su), _ptr(sd)
+    L.resmask, L.want_ids = _ptr(resmask), _ptr(want_ids)
     return L
 
 

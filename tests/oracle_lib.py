@@ -73,8 +73,10 @@ class Oracle:
                                      C.c_int64, C.c_void_p, C.c_int64, C.c_void_p]
         L.orc_router.argtypes = [C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p,
                                  C.c_float, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
+        L.orc_router_resident.argtypes = [C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p,
+                                          C.c_float] + [C.c_void_p] * 6
         L.orc_moe_layer.argtypes = ([C.c_int64] * 5 + [C.c_int] * 3 + [C.c_void_p] * 4 + [C.c_int64]
-                                    + [C.c_void_p] * 3 + [C.c_float, C.c_float] + [C.c_void_p] * 9)
+                                    + [C.c_void_p] * 3 + [C.c_float, C.c_float] + [C.c_void_p] * 11)
 
     # -- quantization -------------------------------------------------------
     def quantize(self, t: int, x: np.ndarray) -> np.ndarray:
@@ -198,7 +200,24 @@ class Oracle:
                             _p(w), _p(logits), _p(probs))
         return ids, w, logits, probs
 
-    def moe_layer(self, layer: "LayerWeights", x: np.ndarray, rms_eps: float = -1.0, scale: float = 0.0):
+    def router_resident(self, W: np.ndarray, x: np.ndarray, k: int, mask: np.ndarray | None, scale: float = 0.0):
+        """Resident-only routing: returns ids, weights, want (the unmasked top k), probs."""
+        E, H = W.shape
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, H)
+        T = x.shape[0]
+        ids = np.zeros((T, k), np.int32)
+        w = np.zeros((T, k), np.float32)
+        want = np.zeros((T, k), np.int32)
+        probs = np.zeros((T, E), np.float32)
+        m = None if mask is None else np.ascontiguousarray(mask, np.float32)
+        self.lib.orc_router_resident(H, E, k, T, _p(np.ascontiguousarray(W, np.float32)), _p(x), scale, _p(m),
+                                     _p(want), _p(ids), _p(w), None, _p(probs))
+        return ids, w, want, probs
+
+    def moe_layer(self, layer: "LayerWeights", x: np.ndarray, rms_eps: float = -1.0, scale: float = 0.0,
+                  resmask: np.ndarray | None = None):
+        """resmask: f32 [E] (0 / -inf) for resident-only routing; the result then
+        also holds 'want', the unmasked top k."""
         H, E, k, F = layer.H, layer.E, layer.k, layer.F
         x = np.ascontiguousarray(x, np.float32).reshape(-1, H)
         T = x.shape[0]
@@ -211,12 +230,18 @@ class Oracle:
         act = np.zeros((T, k, F), np.float32)
         ex = np.zeros((T, k, H), np.float32)
         sg, su, sd = (None, None, None) if layer.slot_of is None else layer.slot_of
+        m = None if resmask is None else np.ascontiguousarray(resmask, np.float32)
+        want = np.zeros((T, k), np.int32)
         rc = self.lib.orc_moe_layer(H, E, k, F, T, layer.type_gate, layer.type_up, layer.type_down,
                                     _p(layer.router), _p(layer.gate), _p(layer.up), _p(layer.down),
                                     layer.n_slots, _p(sg), _p(su), _p(sd), scale, rms_eps, _p(x), _p(out),
-                                    _p(xnext), _p(ids), _p(w), _p(gate), _p(up), _p(act), _p(ex))
+                                    _p(xnext), _p(ids), _p(w), _p(gate), _p(up), _p(act), _p(ex), _p(m),
+                                    _p(want) if m is not None else None)
         assert rc == 0
-        return dict(out=out, xnext=xnext, ids=ids, weights=w, gate=gate, up=up, act=act, experts=ex)
+        r = dict(out=out, xnext=xnext, ids=ids, weights=w, gate=gate, up=up, act=act, experts=ex)
+        if m is not None:
+            r["want"] = want
+        return r
 
 
 class LayerWeights:
@@ -305,6 +330,22 @@ class RefGGML:
         L.qwref_isa.restype = C.c_int
         L.qwref_shared_expert_add.argtypes = ([C.c_int64, C.c_int64, C.c_int64] + [C.c_int] * 3 + [C.c_void_p] * 8
                                               + [C.c_int])
+        L.qwref_router_resident.argtypes = ([C.c_int64] * 4 + [C.c_void_p] * 3 + [C.c_float] + [C.c_void_p] * 4
+                                            + [C.c_int])
+
+    def router_resident(self, W, x, k: int, mask, scale: float = 0.0, n_threads: int = 2):
+        """ggml's resident-only router: ids, weights, want (unmasked top k), probs."""
+        E, H = W.shape
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, H)
+        T = x.shape[0]
+        ids = np.zeros((T, k), np.int32)
+        w = np.zeros((T, k), np.float32)
+        want = np.zeros((T, k), np.int32)
+        probs = np.zeros((T, E), np.float32)
+        assert self.lib.qwref_router_resident(H, E, k, T, _p(np.ascontiguousarray(W, np.float32)), _p(x),
+                                              _p(np.ascontiguousarray(mask, np.float32)), scale, _p(want), _p(ids),
+                                              _p(w), _p(probs), n_threads) == 0
+        return ids, w, want, probs
 
     def shared_expert_add(self, se: SharedWeights, x, moe_out, resid=None, n_threads=4):
         x = np.ascontiguousarray(x, np.float32)

@@ -171,6 +171,37 @@ def test_stack_run_avx2_bit_exact_and_avx512_within_tolerance(orc):
 
 
 @needs_ref
+@pytest.mark.parametrize("T,n_res", [(1, 40), (1, 8), (3, 64), (5, 128)])
+def test_router_resident_matches_ggml(orc, T, n_res):
+    """Resident-only routing (core/runtime.cpp:870-881) against ggml's graph of
+    the same ops: want = argsort_top_k(raw logits), then logits + mask (0 for
+    the n_res resident experts, -inf else) before soft_max / top-k / weights.
+    ids, weights, want and probabilities bit for bit; no absent expert is ever
+    picked; with every expert resident the ids equal the unmasked router's and
+    want equals them (softmax keeps the order)."""
+    rng = np.random.default_rng(T * 100 + n_res)
+    E, H, k = 128, 256, 8
+    W = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    res = np.sort(rng.choice(E, n_res, replace=False))
+    mask = np.full(E, -np.inf, np.float32)
+    mask[res] = 0.0
+    ids, w, want, probs = orc.router_resident(W, x, k, mask)
+    rids, rw, rwant, rprobs = RefGGML().router_resident(W, x, k, mask)
+    assert np.array_equal(ids, rids)
+    assert np.array_equal(want, rwant)
+    assert np.array_equal(w.view(np.int32), rw.view(np.int32))
+    assert np.array_equal(probs.view(np.int32), rprobs.view(np.int32))
+    assert np.isin(ids, res).all()
+    assert np.all(probs[:, np.setdiff1d(np.arange(E), res)] == 0.0)
+    pids, pw, logits, _ = orc.router(W, x, k)
+    assert np.array_equal(want, np.argsort(-logits, axis=1, kind="stable")[:, :k])   # no ties in random logits
+    if n_res == E:
+        assert np.array_equal(ids, pids) and np.array_equal(want, pids)
+        assert np.array_equal(w.view(np.int32), pw.view(np.int32))
+
+
+@needs_ref
 def test_rms_norm_mul_matches_ggml(orc):
     """The router input of a decoder layer: mul(rms_norm(x), w) bit for bit."""
     ref = RefGGML()
