@@ -740,6 +740,8 @@ int qwmoe_decode_stack_create(const qwmoe_layer* layers, int n_layer, float rms_
         D.n_slots_gate = L.n_slots_gate;
         D.n_slots_up = L.n_slots_up;
         D.n_slots_down = L.n_slots_down;
+        D.resmask = L.resmask;
+        D.want = L.want_ids;
     }
     uint8_t* base = (uint8_t*) blk;
     if (hipMemset(blk, 0, total) != hipSuccess ||

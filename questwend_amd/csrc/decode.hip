@@ -224,7 +224,7 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
     __shared__ SortRange s_stack[SORT_STACK];
     __shared__ int32_t s_spec[32];
     __shared__ uint64_t s_L[2][LAYER_WORDS];   // descriptors of layers l (slot l & 1) and l + 1
-    __shared__ int s_need_sort;
+    __shared__ int s_need_sort, s_wflag;
     __shared__ int s_bad;
     __shared__ int s_reload;
     __shared__ int s_fail;
@@ -321,6 +321,13 @@ __global__ void __launch_bounds__(DEC_THREADS) k_decode_stack(DecodeArgs a) {
         lds_barrier();
         if (s_fail) return;
         loads_returned();
+        // resident-only routing: workgroup 0 records the top k of the raw logits,
+        // then every workgroup adds the layer's mask row before ranking them
+        if (L.resmask) {
+            if (b == 0 && L.want) decode_want(s_p, E, k, L.want, s_order, s_stack, &s_wflag, tid, DEC_THREADS);
+            for (int i = tid; i < E; i += DEC_THREADS) s_p[i] = s_p[i] + L.resmask[i];
+            lds_barrier();
+        }
         // logit ranks: rank = number of strictly larger logits, TOPK_TPV lanes per
         // value, lane sub taking the float4 groups c = sub (mod TOPK_TPV).  Equal
         // logits share a rank, so the losing one fails the check below, as does a

@@ -455,7 +455,7 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
     __shared__ uint64_t s_L[2][XLW];
     __shared__ SortRange s_stack[SORT_STACK];
     __shared__ double s_red[XW];
-    __shared__ int s_fail, s_need_sort;
+    __shared__ int s_fail, s_need_sort, s_wflag;
 
     const int b = blockIdx.x, tid0 = threadIdx.x;
     // Roles: the XCD this workgroup runs on (XCC_ID) and j = b / 8.  The
@@ -540,6 +540,14 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
         if (tid < E && !gather<1>(a, a.xl + xcd * E, E, ep, s_p, tid, XW_LOGITS)) s_fail = 1;
         lds_barrier();
         if (s_fail) return;
+        // resident-only routing: workgroup 0 records the top k of the raw logits,
+        // then every workgroup adds the layer's mask row before ranking them
+        if (const float* const Lmask = (const float*) uni64((uint64_t) L.resmask)) {
+            int32_t* const Lwant = (int32_t*) uni64((uint64_t) L.want);
+            if (b == 0 && Lwant) decode_want(s_p, E, k, Lwant, s_order, s_stack, &s_wflag, tid, XT);
+            for (int i = tid; i < E; i += XT) s_p[i] = s_p[i] + Lmask[i];
+            lds_barrier();
+        }
         // logit ranks (strictly larger count; four lanes per value); the rank-c
         // expert is XCD c's speculative expert: {id, gate, up, down slots}
         {

@@ -4,6 +4,7 @@
 #include <stdint.h>
 
 #include "qw_common.hpp"
+#include "qw_sort.hpp"
 
 namespace qw {
 
@@ -18,7 +19,43 @@ struct DecodeLayer {
     const int32_t* slot_up;
     const int32_t* slot_down;
     int64_t n_slots_gate, n_slots_up, n_slots_down;
+    const float* resmask;         // [E] added to the logits before the softmax, or null
+    int32_t* want;                // [k] top k of the raw logits (with resmask), or null
 };
+
+// Resident-only routing in a decode kernel (core/runtime.cpp:870-881): want[0..k)
+// = ggml_argsort_top_k of the raw logits v[0..E) (ranks by strictly larger
+// count; std::sort's order on a tie inside the first k), computed by the nt
+// threads of one workgroup.  ord: E ints of LDS scratch; flag: an LDS word.
+// Ends synchronised.  Runs only for layers with a mask, so it is kept out of line.
+__device__ __attribute__((noinline)) inline void decode_want(const float* v, int E, int k, int32_t* want,
+                                                             int32_t* ord, SortRange* stack, int* flag, int tid,
+                                                             int nt) {
+    if (tid == 0) *flag = 0;
+    __syncthreads();
+    for (int i = tid; i < E; i += nt) {
+        const float vi = v[i];
+        int gt = 0, eq = 0;
+        for (int j = 0; j < E; ++j) {
+            gt += v[j] > vi;
+            eq += v[j] == vi;
+        }
+        if (gt < k) {
+            if (eq != 1) *flag = 1;
+            else ord[gt] = i;
+        }
+    }
+    __syncthreads();
+    if (*flag) {
+        if (tid == 0) {
+            for (int i = 0; i < E; ++i) ord[i] = i;
+            libstdcxx_sort_desc(ord, E, v, stack);
+        }
+        __syncthreads();
+    }
+    for (int i = tid; i < k; i += nt) want[i] = ord[i];
+    __syncthreads();
+}
 
 struct DecodeStackDesc {
     DecodeLayer* layers_dev = nullptr;

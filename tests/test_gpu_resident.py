@@ -124,3 +124,98 @@ def test_ffn_layer_resident(orc, T, n_res, types):
     assert np.array_equal(bits(host(w)), bits(r["weights"]))
     assert np.array_equal(bits(host(out)), bits(r["out"]))
     assert ops.device_status(clear=True) & (qa.STATUS_BAD_ID | qa.STATUS_BAD_SLOT) == 0
+
+
+def masked_layers(layers, n_res_list, seed, T=1):
+    """ctypes copies of GpuLayer descriptors with a resident mask row and a want
+    buffer each; returns (descriptors, masks (host), wants (device), keepalive)."""
+    rng = np.random.default_rng(seed)
+    descs, masks, wants, keep = [], [], [], []
+    for g, n_res in zip(layers, n_res_list):
+        E, k = g.layer.n_expert, g.layer.n_expert_used
+        mask, _ = resident_mask(rng, E, n_res)
+        md = dev(mask)
+        want = torch.full((T, k), -1, dtype=torch.int32, device=DEV)
+        L = qa.Layer.from_buffer_copy(g.layer)
+        L.resmask, L.want_ids = md.data_ptr(), want.data_ptr()
+        descs.append(L)
+        masks.append(mask)
+        wants.append(want)
+        keep += [md, want, g]
+    return descs, masks, wants, keep
+
+
+def chain_oracle(orc, layers, masks, x, eps=1e-6):
+    """The stack on the CPU: each layer's oracle (with its mask) on the previous
+    layer's RMSNorm output."""
+    rs, xr = [], x
+    for g, m in zip(layers, masks):
+        r = orc.moe_layer(g.host, xr, rms_eps=eps, resmask=m)
+        rs.append(r)
+        xr = r["xnext"]
+    return rs
+
+
+@pytest.mark.parametrize("kernel_env", ["xcd", "per_cu"])
+def test_decode_stack_resident(orc, kernel_env):
+    """The persistent decode stack with every layer's mask and want: per layer
+    ids / weights / want and the last layer's output bit-identical to the
+    oracle chain; masks from 9 resident experts (ranks past k tie at -inf) to all
+    128.  XCD kernel on a 256-CU device, else the per-CU kernel."""
+    import os
+    from test_gpu_decode import GpuLayer
+    if kernel_env == "xcd" and torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the XCD kernel needs a 256-CU device")
+    note(f"decode stack resident ({kernel_env}): 3 layers H=2048 E=128 k=8 F=768, 3 tokens")
+    layers = [GpuLayer(2048, 128, 8, 768, (Q4_K,) * 3, seed=700 + i, permute=(i == 1)) for i in range(3)]
+    descs, masks, wants, keep = masked_layers(layers, [9, 40, 128], seed=7)
+    old = os.environ.get("QWMOE_DECODE_XCD")
+    os.environ["QWMOE_DECODE_XCD"] = "1" if kernel_env == "xcd" else "0"
+    try:
+        stack = ops.DecodeStack(descs, 1e-6, keepalive=keep)
+    finally:
+        if old is None:
+            os.environ.pop("QWMOE_DECODE_XCD")
+        else:
+            os.environ["QWMOE_DECODE_XCD"] = old
+    assert stack.kernel() in ((1,) if kernel_env == "per_cu" else (2, 3))
+    rng = np.random.default_rng(3)
+    for t in range(3):
+        x = rng.standard_normal(2048).astype(np.float32)
+        out, xo, ids, w = stack(dev(x))
+        rs = chain_oracle(orc, layers, masks, x.reshape(1, -1))
+        ids_h, w_h = host(ids), host(w)
+        for l, r in enumerate(rs):
+            assert np.array_equal(host(wants[l])[0], r["want"][0]), f"token {t} layer {l} want"
+            assert np.array_equal(ids_h[l], r["ids"][0]), f"token {t} layer {l} ids"
+            assert np.array_equal(bits(w_h[l]), bits(r["weights"][0])), f"token {t} layer {l} weights"
+        assert np.array_equal(bits(host(out)), bits(rs[-1]["out"][0])), f"token {t} out"
+        assert np.array_equal(bits(host(xo)), bits(rs[-1]["xnext"][0])), f"token {t} x_out"
+    assert stack.status() & ~1 == 0
+    stack.close()
+
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_layer_stack_resident(orc, T):
+    """qwmoe_layer_stack (captured graph) with masks and wants: per layer ids,
+    want and the last layer's output bit-identical to the oracle chain; a mask
+    changed in place between runs is read by the replayed graph."""
+    from test_gpu_decode import GpuLayer
+    note(f"layer stack resident T={T}: 2 layers H=1024 E=32 k=4 F=512")
+    layers = [GpuLayer(1024, 32, 4, 512, (Q4_K,) * 3, seed=800 + i) for i in range(2)]
+    descs, masks, wants, keep = masked_layers(layers, [6, 20], seed=8, T=T)
+    stack = ops.LayerStack(descs, 1e-6, max_tokens=T, keepalive=keep)
+    rng = np.random.default_rng(T)
+    for rep in range(2):
+        if rep == 1:   # new palette: the mask tensors are updated in place
+            for m, d in zip(masks, keep[0::3]):
+                m[:] = resident_mask(rng, m.size, 10)[0]
+                d.copy_(torch.from_numpy(m))
+        x = rng.standard_normal((T, 1024)).astype(np.float32)
+        out, xo, ids, w = stack(dev(x))
+        rs = chain_oracle(orc, layers, masks, x)
+        for l, r in enumerate(rs):
+            assert np.array_equal(host(wants[l]), r["want"]), f"rep {rep} layer {l} want"
+            assert np.array_equal(host(ids)[l], r["ids"]), f"rep {rep} layer {l} ids"
+        assert np.array_equal(bits(host(out)), bits(rs[-1]["out"])), f"rep {rep} out"
+    stack.close()
