@@ -532,6 +532,22 @@ const int32_t * qwmoe_expert_cache_device_row(const qwmoe_expert_cache * c, int 
  * `touch` is set, touches every role of every entry (hits, LRU stamps,
  * counts).  Changes nothing otherwise. */
 int qwmoe_expert_cache_verify(qwmoe_expert_cache * c, const int32_t * ids, int n_layer, int k, int touch);
+/* The resident-decode mask (decode_cached_fast's fill_resmask, core/runtime.cpp:
+ * 2900-2919): mask [n_layer][n_expert] gets 0 for an expert resident in all
+ * three roles and -inf otherwise; a layer with fewer than floor_res residents
+ * is left unmasked (all 0).  Returns 1 when every layer is masked ("complete":
+ * the masked decode cannot miss), 0 otherwise.  mask_dev (optional, device):
+ * the same values copied there on the cache's stream before returning -- the
+ * layers' resmask rows point into it. */
+int qwmoe_expert_cache_resmask(const qwmoe_expert_cache * c, int floor_res, float * mask, float * mask_dev);
+/* The background refill after a masked decode (core/runtime.cpp:2976-3008):
+ * touches every selected expert sel [n_layer][k] in all roles, then, walking
+ * the layers round robin from *cursor, fetches (ensure_resident) wanted-but-
+ * absent experts of want [n_layer][k] (the layers' want_ids) until `budget`
+ * fetches are spent; *cursor advances by one layer.  Returns the fetches made.
+ * budget <= 0 does nothing, as in the reference. */
+int qwmoe_expert_cache_refill(qwmoe_expert_cache * c, const int32_t * sel, const int32_t * want, int n_layer, int k,
+                              int budget, int * cursor);
 /* Fills L's expert fields (types, pool bases, strides, slot counts, device
  * rows) for `layer`; the caller sets shapes, router and scale. */
 int qwmoe_expert_cache_layer(const qwmoe_expert_cache * c, int layer, qwmoe_layer * L);

@@ -145,6 +145,45 @@ class ExpertCachePolicy:
     def resident(self, role: int, layer: int, expert: int) -> bool:
         return layer * self.n_expert + expert in self.pool(role, layer).key2slot
 
+    def resmask(self, floor_res: int) -> tuple[list[list[float]], bool]:
+        """decode_cached_fast's fill_resmask (core/runtime.cpp:2900-2919): 0 for an
+        expert resident in all roles, -inf else; a layer with fewer than
+        floor_res residents routes unmasked.  Returns (rows, complete)."""
+        rows, complete = [], True
+        for l in range(self.n_layer):
+            res = [all(self.resident(r, l, e) for r in range(3)) for e in range(self.n_expert)]
+            if sum(res) < floor_res:
+                rows.append([0.0] * self.n_expert)
+                complete = False
+            else:
+                rows.append([0.0 if x else float("-inf") for x in res])
+        return rows, complete
+
+    def refill(self, sel, want, budget: int, cursor: int) -> tuple[int, int]:
+        """The background refill of a masked decode (core/runtime.cpp:2976-3008):
+        touch the used experts, then fetch wanted-but-absent ones round robin
+        from layer `cursor` within `budget`.  Returns (fetched, next cursor)."""
+        if budget <= 0:
+            return 0, cursor
+        for l, row in enumerate(sel):
+            for e in row:
+                for r in range(3):
+                    self.touch(r, l, e)
+        fetched = 0
+        for step in range(self.n_layer):
+            if budget <= 0:
+                break
+            l = (cursor + step) % self.n_layer
+            for e in want[l]:
+                if budget <= 0:
+                    break
+                if all(self.resident(r, l, e) for r in range(3)):
+                    continue
+                self.ensure_resident(l, e)
+                budget -= 1
+                fetched += 1
+        return fetched, (cursor + 1) % self.n_layer
+
     def slot_of_row(self, role: int, layer: int) -> list[int]:     # expert_cache.cpp:694-697
         return self.slot_of[role][layer * self.n_expert:(layer + 1) * self.n_expert]
 

@@ -129,6 +129,8 @@ SIGNATURES = {
     "qwmoe_expert_cache_touch": (I, [P, I, I, I]),
     "qwmoe_expert_cache_resident": (I, [P, I, I, I]),
     "qwmoe_expert_cache_verify": (I, [P, P, I, I, I]),
+    "qwmoe_expert_cache_resmask": (I, [P, I, P, P]),
+    "qwmoe_expert_cache_refill": (I, [P, P, P, I, I, I, P]),
     "qwmoe_expert_cache_slot_of_row": (P, [P, I, I]),
     "qwmoe_expert_cache_device_row": (P, [P, I, I]),
     "qwmoe_expert_cache_layer": (I, [P, I, P]),

@@ -31,6 +31,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <atomic>
 #include <chrono>
 #include <condition_variable>
@@ -230,6 +231,7 @@ struct qwmoe_expert_cache {
 
     size_t row_index(int role, int layer) const { return ((size_t) role * n_layer + layer) * (size_t) n_expert; }
     Pool& pool_of(int role, int layer) { return pools[layer_pool[role][layer]]; }
+    const Pool& pool_of(int role, int layer) const { return pools[layer_pool[role][layer]]; }
 
     void set_row(int role, int key, int32_t slot) {
         const size_t i = (size_t) role * n_layer * n_expert + (size_t) key;
@@ -821,6 +823,65 @@ int qwmoe_expert_cache_verify(qwmoe_expert_cache* c, const int32_t* ids, int n_l
             for (int i = 0; i < k; ++i)
                 for (int r = 0; r < N_ROLE; ++r) qwmoe_expert_cache_touch(c, r, l, ids[(size_t) l * k + i]);
     return missing;
+}
+
+int qwmoe_expert_cache_resmask(const qwmoe_expert_cache* c, int floor_res, float* mask, float* mask_dev) {
+    if (!c || !mask) return QWMOE_ERR_INVALID_ARG;
+    if (mask_dev && c->dry) return QWMOE_ERR_UNSUPPORTED;
+    bool complete = true;
+    for (int l = 0; l < c->n_layer; ++l) {
+        float* row = mask + (size_t) l * c->n_expert;
+        int n_res = 0;
+        for (int e = 0; e < c->n_expert; ++e) {
+            const int key = l * c->n_expert + e;
+            bool res = true;
+            for (int r = 0; r < N_ROLE; ++r) res = res && c->pool_of(r, l).holds(key);
+            row[e] = res ? 0.0f : -INFINITY;
+            n_res += res ? 1 : 0;
+        }
+        if (n_res < floor_res) {   // palette too thin: the layer routes unmasked
+            for (int e = 0; e < c->n_expert; ++e) row[e] = 0.0f;
+            complete = false;
+        }
+    }
+    if (mask_dev) {
+        const size_t bytes = sizeof(float) * (size_t) c->n_layer * (size_t) c->n_expert;
+        if (hipMemcpyAsync(mask_dev, mask, bytes, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
+            hipStreamSynchronize(c->stream) != hipSuccess)
+            return QWMOE_ERR_HIP;
+    }
+    return complete ? 1 : 0;
+}
+
+int qwmoe_expert_cache_refill(qwmoe_expert_cache* c, const int32_t* sel, const int32_t* want, int n_layer, int k,
+                              int budget, int* cursor) {
+    if (!c || !sel || !want || !cursor || n_layer != c->n_layer || k <= 0 || *cursor < 0 || *cursor >= n_layer)
+        return QWMOE_ERR_INVALID_ARG;
+    for (int i = 0; i < n_layer * k; ++i)
+        if (sel[i] < 0 || sel[i] >= c->n_expert || want[i] < 0 || want[i] >= c->n_expert) return QWMOE_ERR_INVALID_ARG;
+    if (budget <= 0) return 0;
+    // the actually used experts are touched first, so the refill's evictions
+    // land on stale entries
+    for (int l = 0; l < n_layer; ++l)
+        for (int i = 0; i < k; ++i)
+            for (int r = 0; r < N_ROLE; ++r) qwmoe_expert_cache_touch(c, r, l, sel[(size_t) l * k + i]);
+    int fetched = 0;
+    for (int step = 0; step < n_layer && budget > 0; ++step) {
+        const int l = (*cursor + step) % n_layer;
+        for (int i = 0; i < k && budget > 0; ++i) {
+            const int e = want[(size_t) l * k + i];
+            const int key = l * c->n_expert + e;
+            bool res = true;
+            for (int r = 0; r < N_ROLE; ++r) res = res && c->pool_of(r, l).holds(key);
+            if (res) continue;
+            const int rc = qwmoe_expert_cache_ensure_resident(c, l, e);
+            if (rc < 0) return rc;
+            --budget;
+            ++fetched;
+        }
+    }
+    *cursor = (*cursor + 1) % n_layer;
+    return fetched;
 }
 
 int qwmoe_expert_cache_resident(const qwmoe_expert_cache* c, int role, int layer, int expert) {

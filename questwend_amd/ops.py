@@ -576,6 +576,28 @@ class ExpertCache(_Handle):
         check(min(r, 0), "expert_cache_verify")
         return r
 
+    def resmask(self, floor_res: int, device_out=None):
+        """The resident-decode mask [n_layer, n_expert] (0 / -inf) as a numpy array
+        and whether every layer is masked; device_out (f32 tensor of that shape)
+        receives a copy on the cache's stream."""
+        import numpy as np
+        m = np.zeros((self.n_layer, self.n_expert), np.float32)
+        r = lib().qwmoe_expert_cache_resmask(self.h, floor_res, m.ctypes.data, _ptr(device_out))
+        check(min(r, 0), "expert_cache_resmask")
+        return m, r == 1
+
+    def refill(self, sel, want, budget: int, cursor: int) -> tuple[int, int]:
+        """Background refill after a masked decode: sel / want int32 [n_layer, k]
+        (host arrays or tensors).  Returns (fetched, next cursor)."""
+        import numpy as np
+        a = np.ascontiguousarray(sel.cpu().numpy() if hasattr(sel, "cpu") else sel, dtype=np.int32)
+        b = np.ascontiguousarray(want.cpu().numpy() if hasattr(want, "cpu") else want, dtype=np.int32)
+        cur = C.c_int(cursor)
+        r = lib().qwmoe_expert_cache_refill(self.h, a.ctypes.data, b.ctypes.data, a.shape[0], a.shape[1], budget,
+                                            C.byref(cur))
+        check(min(r, 0), "expert_cache_refill")
+        return r, cur.value
+
     def slot_of_row(self, role: int, layer: int) -> list[int]:
         p = lib().qwmoe_expert_cache_slot_of_row(self.h, role, layer)
         if not p:

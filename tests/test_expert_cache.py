@@ -422,3 +422,61 @@ def test_run_layer_needs_device_pools():
     assert rc != 0
     with pytest.raises(QwmoeError):
         ops.check(rc, "run_layer")
+
+
+# ---- resident-only decode: the mask and the background refill ----------------------
+
+def test_oracle_resmask_and_refill_by_hand():
+    """Pins the policy's fill_resmask / refill (core/runtime.cpp:2900-2919,
+    2976-3008) on a worked case: 2 layers x 4 experts, one pool per role with 4
+    slots shared by both layers (LRU across them)."""
+    sigs = uniform_sigs(2)
+    p = ExpertCachePolicy(2, 4, 2, sigs, sum(sigs[r][0][3] for r in range(3)) * 2 * 4 // 2)   # half of everything
+    assert [q.n_slots for q in p.pools] == [4, 4, 4]
+    p.ensure(0, [1, 3])
+    p.ensure(1, [2])
+    rows, complete = p.resmask(floor_res=1)
+    ninf = float("-inf")
+    assert rows == [[ninf, 0.0, ninf, 0.0], [ninf, ninf, 0.0, ninf]] and complete
+    rows, complete = p.resmask(floor_res=2)                   # layer 1 has one resident: left unmasked
+    assert rows[0] == [ninf, 0.0, ninf, 0.0] and rows[1] == [0.0] * 4 and not complete
+    # refill from layer 1 (cursor 1), budget 2: the used experts are touched in
+    # order (0,1), (0,3), (1,2); layer 1 wants 0 (a free slot) then 3 (evicts the
+    # least recently used, (0,1))
+    misses, evictions = p.misses, p.evictions
+    fetched, cur = p.refill(sel=[[1, 3], [2, 2]], want=[[0, 1], [0, 3]], budget=2, cursor=1)
+    assert (fetched, cur) == (2, 0)
+    assert (p.misses, p.evictions) == (misses + 6, evictions + 3)     # 2 experts x 3 roles; one eviction per pool
+    assert all(p.resident(r, 1, e) for r in range(3) for e in (0, 2, 3))
+    assert all(p.resident(r, 0, 3) for r in range(3)) and not any(p.resident(r, 0, 1) for r in range(3))
+    assert p.refill([[3, 3], [0, 3]], [[0, 1], [0, 3]], budget=0, cursor=0) == (0, 0)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_library_resident_helpers_match_oracle(seed):
+    """qwmoe_expert_cache_resmask / _refill (dry run) against the policy, call for
+    call, interleaved with the other operations; state compared after each."""
+    import numpy as np
+    ops = lib_or_skip()
+    rng = random.Random(5000 + seed)
+    n_layer, E, n_used, sigs, budget = random_setup(rng)
+    p = ExpertCachePolicy(n_layer, E, n_used, sigs, budget)
+    c = make_lib(ops, n_layer, E, n_used, sigs, budget)
+    cursor = 0
+    for _ in range(12):
+        for op in random_ops(rng, p, 20):
+            apply_both(c, p, op)
+        floor = rng.randint(0, E)
+        m, complete = c.resmask(floor)
+        rows, comp2 = p.resmask(floor)
+        assert complete == comp2
+        assert np.array_equal(m, np.array(rows, np.float32))
+        k = min(n_used, E)
+        sel = [zipf_ids(rng, E, k) for _ in range(n_layer)]
+        want = [zipf_ids(rng, E, k) for _ in range(n_layer)]
+        b = rng.randint(0, 6)
+        got = c.refill(np.array(sel, np.int32), np.array(want, np.int32), b, cursor)
+        exp = p.refill(sel, want, b, cursor)
+        assert got == exp
+        cursor = got[1]
+        assert_same(c, p)

@@ -368,3 +368,61 @@ def test_file_tier_read_failure_leaves_slots_empty(tmp_path):
         cache.sync()
         assert all(cache.resident(r, 1, e) for r in range(3) for e in (2, 3))
         cache.close()
+
+
+def test_resident_decode_through_cache():
+    """decode_cached_fast's resident mode (core/runtime.cpp:2895-3008): every
+    layer's router is masked to the experts the cache holds (mask rows from
+    qwmoe_expert_cache_resmask), the whole stack runs in one launch and cannot
+    miss, and the unmasked top k it records (want) drives the background refill
+    (qwmoe_expert_cache_refill, 8 fetches per token).  Each token's output is
+    bit-identical to the all-resident weights under the same masks, every
+    selected expert is resident, and the refill brings wanted experts in."""
+    note("resident decode through the cache: 3 layers H=1024 E=16 k=4 F=512 Q4_K, 50% resident, 16 tokens")
+    n_layer, H, E, k, F = 3, 1024, 16, 4, 512
+    eps = 1e-6
+    cl = CachedLayers(n_layer, H, E, k, F, (Q4_K,) * 3, 0.5, seed=13)
+    mask_dev = torch.zeros((n_layer, E), dtype=torch.float32, device=DEV)
+    want_dev = torch.zeros((n_layer, k), dtype=torch.int32, device=DEV)
+
+    def masked(descs):
+        out = []
+        for l, L0 in enumerate(descs):
+            L = qa.Layer.from_buffer_copy(L0)
+            L.resmask, L.want_ids = mask_dev[l].data_ptr(), want_dev[l].data_ptr()
+            out.append(L)
+        return out
+
+    stack = ops.DecodeStack(masked(cl.cached), eps, keepalive=(cl, mask_dev, want_dev))
+    ref = ops.DecodeStack(masked(cl.resident), eps, keepalive=(cl, mask_dev, want_dev))
+    rng = np.random.default_rng(5)
+    for l in range(n_layer):   # a warm palette: 8 experts per layer (the pools' 24 slots)
+        cl.cache.ensure(l, list(rng.choice(E, 8, replace=False)))
+    cursor, stamp, fetched_total = 0, None, 0
+    for t in range(16):
+        st = cl.cache.stats()
+        if (st["misses"], st["evictions"]) != stamp:      # residency changed: new mask rows
+            m, complete = cl.cache.resmask(k, mask_dev)
+            stamp = (st["misses"], st["evictions"])
+            assert complete
+            for l in range(n_layer):
+                assert all((m[l, e] == 0.0) == cl.resident_all(l, [e]) for e in range(E))
+        x = torch.from_numpy(rng.standard_normal(H).astype(np.float32)).to(DEV)
+        r_out, r_xo, r_ids, _ = ref(x)
+        out, xo, ids, _ = stack(x)
+        torch.cuda.synchronize()
+        assert torch.equal(ids, r_ids), f"token {t} ids"
+        assert np.array_equal(bits(out), bits(r_out)), f"token {t} out"
+        assert np.array_equal(bits(xo), bits(r_xo)), f"token {t} x_out"
+        ids_h, want_h = ids.cpu().numpy(), want_dev.cpu().numpy()
+        assert cl.cache.verify(ids_h, touch=False) == 0, f"token {t}: the masked stack picked an absent expert"
+        absent = sum(not cl.resident_all(l, [e]) for l in range(n_layer) for e in want_h[l])
+        fetched, cursor = cl.cache.refill(ids_h, want_h, 8, cursor)
+        assert 0 <= fetched <= 8 and (absent == 0) == (fetched == 0)
+        fetched_total += fetched
+    note(f"refill fetched {fetched_total} experts over 16 tokens")
+    assert fetched_total > 0
+    assert stack.status() & ~1 == 0
+    stack.close()
+    ref.close()
+    cl.cache.close()
