@@ -571,6 +571,28 @@ int qwmoe_expert_cache_sync(qwmoe_expert_cache * c);
  * call; outputs as qwmoe_ffn_layer's.  The first call allocates a small id buffer. */
 int qwmoe_expert_cache_run_layer(qwmoe_expert_cache * c, int layer, const qwmoe_layer * L, const float * x, int64_t T,
                                  float * out, float rms_eps, float * x_next, int32_t * ids_out, float * weights_out);
+/* plan_slices of the chunked prefill (core/runtime.cpp:2144-2170): tokens
+ * t = 0..T-1 with selections sel [T][n_used] are cut into slices (t0, len) so
+ * that no slice names more than `cap` distinct experts (one ensure() must not
+ * evict its own slots) nor runs longer than max_slice tokens (< 1: 1024); a
+ * token that would overflow opens the next slice.  slices: [T][2] capacity;
+ * union_list (optional, [n_expert]) receives the chunk's distinct experts in
+ * first-use order, n_union (optional) their count.  Host only. */
+int qwmoe_plan_slices(const int32_t * sel, int T, int n_used, int n_expert, int cap, int max_slice, int32_t * slices,
+                      int * n_slices, int32_t * union_list, int * n_union);
+/* The same for a cache layer, with the reference's cap = max(n_used,
+ * capacity(layer) - 8). */
+int qwmoe_expert_cache_plan_slices(const qwmoe_expert_cache * c, int layer, const int32_t * sel, int T, int max_slice,
+                                   int32_t * slices, int * n_slices);
+/* One layer of the chunked prefill through the cache (segment B of
+ * core/runtime.cpp:2100-2300): the router's ids for all T tokens are read back,
+ * planned into slices, and each slice's experts made resident (ensure) before
+ * qwmoe_ffn_layer runs on its tokens -- lossless, the FFN being per token.
+ * Any T; outputs as qwmoe_ffn_layer's; *n_slices_out (optional) the slices run.
+ * Grows the cache's id buffers when T needs more. */
+int qwmoe_expert_cache_run_batch(qwmoe_expert_cache * c, int layer, const qwmoe_layer * L, const float * x, int64_t T,
+                                 float * out, float rms_eps, float * x_next, int32_t * ids_out, float * weights_out,
+                                 int max_slice, int * n_slices_out);
 
 /* ---- host-side checks (no GPU needed) ---------------------------------------- */
 

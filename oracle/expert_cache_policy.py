@@ -218,3 +218,36 @@ class ExpertCachePolicy:
             self._install(r, l, e)
             n += 1
         return n
+
+
+def plan_slices(sel, n_used: int, n_expert: int, cap: int, max_slice: int = 1024):
+    """plan_slices of the chunked prefill (core/runtime.cpp:2144-2170): cut the
+    tokens' selections into slices naming at most cap distinct experts and at
+    most max_slice tokens; returns ([(t0, len)], union in first-use order)."""
+    if max_slice < 1:
+        max_slice = 1024
+    T = len(sel)
+    slices, union, in_union = [], [], set()
+    seen, distinct, t0 = set(), 0, 0
+    for t in range(T):
+        nnew = 0
+        for e in sel[t]:
+            if e not in in_union:
+                in_union.add(e)
+                union.append(e)
+            if e not in seen:
+                seen.add(e)
+                nnew += 1
+        if (distinct + nnew > cap or t - t0 >= max_slice) and t > t0:
+            slices.append((t0, t - t0))
+            seen, distinct = set(), 0
+            nnew = 0
+            for e in sel[t]:
+                if e not in seen:
+                    seen.add(e)
+                    nnew += 1
+            t0 = t
+        distinct += nnew
+    if T:
+        slices.append((t0, T - t0))
+    return slices, union

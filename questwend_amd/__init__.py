@@ -131,6 +131,9 @@ SIGNATURES = {
     "qwmoe_expert_cache_verify": (I, [P, P, I, I, I]),
     "qwmoe_expert_cache_resmask": (I, [P, I, P, P]),
     "qwmoe_expert_cache_refill": (I, [P, P, P, I, I, I, P]),
+    "qwmoe_plan_slices": (I, [P, I, I, I, I, I, P, P, P, P]),
+    "qwmoe_expert_cache_plan_slices": (I, [P, I, P, I, I, P, P]),
+    "qwmoe_expert_cache_run_batch": (I, [P, I, P, P, I64, P, F, P, P, P, I, P]),
     "qwmoe_expert_cache_slot_of_row": (P, [P, I, I]),
     "qwmoe_expert_cache_device_row": (P, [P, I, I]),
     "qwmoe_expert_cache_layer": (I, [P, I, P]),

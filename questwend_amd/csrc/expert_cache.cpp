@@ -229,6 +229,28 @@ struct qwmoe_expert_cache {
         if (dev_block) (void) hipFree(dev_block);
     }
 
+    // The run paths' router ids / weights (device) and id read-back (pinned
+    // host), grown to hold n ids; the old buffers are freed once the stream has
+    // finished with them.
+    int grow_run_buffers(size_t n) {
+        if (n <= run_cap) return QWMOE_OK;
+        if (hipStreamSynchronize(stream) != hipSuccess) return QWMOE_ERR_HIP;
+        if (run_ids_dev) (void) hipFree(run_ids_dev);
+        if (run_ids_host) (void) hipHostFree(run_ids_host);
+        run_ids_dev = nullptr;
+        run_ids_host = nullptr;
+        run_w_dev = nullptr;
+        run_cap = 0;
+        if (hipMalloc(&run_ids_dev, n * 8) != hipSuccess ||
+            hipHostMalloc(&run_ids_host, n * 4, hipHostMallocDefault) != hipSuccess) {
+            (void) hipGetLastError();
+            return QWMOE_ERR_HIP;
+        }
+        run_w_dev = (float*) (run_ids_dev + n);
+        run_cap = n;
+        return QWMOE_OK;
+    }
+
     size_t row_index(int role, int layer) const { return ((size_t) role * n_layer + layer) * (size_t) n_expert; }
     Pool& pool_of(int role, int layer) { return pools[layer_pool[role][layer]]; }
     const Pool& pool_of(int role, int layer) const { return pools[layer_pool[role][layer]]; }
@@ -988,23 +1010,10 @@ int qwmoe_expert_cache_run_layer(qwmoe_expert_cache* c, int layer, const qwmoe_l
     if (L->n_expert != c->n_expert || L->n_expert_used <= 0 || T > 64) return QWMOE_ERR_INVALID_ARG;
     if (T == 0) return QWMOE_OK;
     const size_t n = (size_t) T * (size_t) L->n_expert_used;
-    if (n > c->run_cap) {
-        if (c->run_ids_dev) (void) hipFree(c->run_ids_dev);
-        if (c->run_ids_host) (void) hipHostFree(c->run_ids_host);
-        c->run_ids_dev = nullptr;
-        c->run_ids_host = nullptr;
-        c->run_cap = 0;
-        const size_t cap = (size_t) 64 * (size_t) L->n_expert_used;
-        if (hipMalloc(&c->run_ids_dev, cap * 8) != hipSuccess ||
-            hipHostMalloc(&c->run_ids_host, cap * 4, hipHostMallocDefault) != hipSuccess) {
-            (void) hipGetLastError();
-            return QWMOE_ERR_HIP;
-        }
-        c->run_w_dev = (float*) (c->run_ids_dev + cap);
-        c->run_cap = cap;
-    }
+    int rc = c->grow_run_buffers(std::max(n, (size_t) 64 * (size_t) L->n_expert_used));
+    if (rc != QWMOE_OK) return rc;
     // the router's selection, read back (the reference's ensure_layer)
-    int rc = qwmoe_router_topk(c->stream, L->router, x, L->n_embd, L->n_expert, L->n_expert_used, T,
+    rc = qwmoe_router_topk(c->stream, L->router, x, L->n_embd, L->n_expert, L->n_expert_used, T,
                                (size_t) L->n_embd * 4, 6.103515625e-5f, L->expert_weights_scale, c->run_ids_dev,
                                c->run_w_dev, nullptr);
     if (rc != QWMOE_OK) return rc;
@@ -1016,6 +1025,106 @@ int qwmoe_expert_cache_run_layer(qwmoe_expert_cache* c, int layer, const qwmoe_l
     qwmoe_layer Lc = *L;
     if ((rc = qwmoe_expert_cache_layer(c, layer, &Lc)) != QWMOE_OK) return rc;
     return qwmoe_ffn_layer(c->stream, &Lc, x, T, out, rms_eps, x_next, ids_out, weights_out);
+}
+
+int qwmoe_plan_slices(const int32_t* sel, int T, int n_used, int n_expert, int cap, int max_slice, int32_t* slices,
+                      int* n_slices, int32_t* union_list, int* n_union) {
+    if (!sel || !slices || !n_slices || T < 0 || n_used <= 0 || n_expert <= 0 || cap < n_used)
+        return QWMOE_ERR_INVALID_ARG;
+    for (int64_t i = 0; i < (int64_t) T * n_used; ++i)
+        if (sel[i] < 0 || sel[i] >= n_expert) return QWMOE_ERR_INVALID_ARG;
+    if (max_slice < 1) max_slice = 1024;
+    std::vector<uint8_t> in_slice((size_t) n_expert, 0), in_union((size_t) n_expert, 0);
+    int ns = 0, nu = 0, distinct = 0, t0 = 0;
+    for (int t = 0; t < T; ++t) {
+        const int32_t* row = sel + (size_t) t * n_used;
+        int fresh = 0;
+        for (int j = 0; j < n_used; ++j) {
+            if (!in_union[(size_t) row[j]]) {
+                in_union[(size_t) row[j]] = 1;
+                if (union_list) union_list[nu] = row[j];
+                ++nu;
+            }
+            if (!in_slice[(size_t) row[j]]) {
+                in_slice[(size_t) row[j]] = 1;
+                ++fresh;
+            }
+        }
+        // token t would take the slice past the pool's capacity (or its length
+        // past max_slice): the slice ends before t, and t opens the next one
+        if ((distinct + fresh > cap || t - t0 >= max_slice) && t > t0) {
+            slices[2 * ns] = t0;
+            slices[2 * ns + 1] = t - t0;
+            ++ns;
+            std::fill(in_slice.begin(), in_slice.end(), 0);
+            fresh = 0;
+            for (int j = 0; j < n_used; ++j)
+                if (!in_slice[(size_t) row[j]]) {
+                    in_slice[(size_t) row[j]] = 1;
+                    ++fresh;
+                }
+            distinct = 0;
+            t0 = t;
+        }
+        distinct += fresh;
+    }
+    if (T > 0) {
+        slices[2 * ns] = t0;
+        slices[2 * ns + 1] = T - t0;
+        ++ns;
+    }
+    *n_slices = ns;
+    if (n_union) *n_union = nu;
+    return QWMOE_OK;
+}
+
+int qwmoe_expert_cache_plan_slices(const qwmoe_expert_cache* c, int layer, const int32_t* sel, int T, int max_slice,
+                                   int32_t* slices, int* n_slices) {
+    if (!valid_role_layer(c, 0, layer)) return QWMOE_ERR_INVALID_ARG;
+    const int cap = std::max(c->n_used, qwmoe_expert_cache_capacity(c, layer) - 8);
+    return qwmoe_plan_slices(sel, T, c->n_used, c->n_expert, cap, max_slice, slices, n_slices, nullptr, nullptr);
+}
+
+int qwmoe_expert_cache_run_batch(qwmoe_expert_cache* c, int layer, const qwmoe_layer* L, const float* x, int64_t T,
+                                 float* out, float rms_eps, float* x_next, int32_t* ids_out, float* weights_out,
+                                 int max_slice, int* n_slices_out) {
+    if (!valid_role_layer(c, 0, layer) || !L || !x || !out || T < 0 || T > INT32_MAX / 64) return QWMOE_ERR_INVALID_ARG;
+    if (c->dry) return QWMOE_ERR_UNSUPPORTED;
+    if (L->n_expert != c->n_expert || L->n_expert_used != c->n_used) return QWMOE_ERR_INVALID_ARG;
+    if (n_slices_out) *n_slices_out = 0;
+    if (T == 0) return QWMOE_OK;
+    const int k = (int) L->n_expert_used;
+    const int64_t H = L->n_embd;
+    int rc = c->grow_run_buffers((size_t) T * (size_t) k);
+    if (rc != QWMOE_OK) return rc;
+    // the router's selection for the whole batch, read back
+    rc = qwmoe_router_topk(c->stream, L->router, x, H, L->n_expert, k, T, (size_t) H * 4, 6.103515625e-5f,
+                           L->expert_weights_scale, c->run_ids_dev, c->run_w_dev, nullptr);
+    if (rc != QWMOE_OK) return rc;
+    const size_t n = (size_t) T * (size_t) k;
+    if (hipMemcpyAsync(c->run_ids_host, c->run_ids_dev, n * 4, hipMemcpyDeviceToHost, c->stream) != hipSuccess ||
+        hipStreamSynchronize(c->stream) != hipSuccess)
+        return QWMOE_ERR_HIP;
+    std::vector<int32_t> slices((size_t) (2 * T));
+    int ns = 0;
+    if ((rc = qwmoe_expert_cache_plan_slices(c, layer, c->run_ids_host, (int) T, max_slice, slices.data(), &ns)))
+        return rc;
+    // each slice: its experts made resident (evictions land after the previous
+    // slice's kernels on the same stream), then the layer on its tokens
+    for (int s = 0; s < ns; ++s) {
+        const int t0 = slices[(size_t) (2 * s)], len = slices[(size_t) (2 * s + 1)];
+        if ((rc = qwmoe_expert_cache_ensure(c, layer, c->run_ids_host + (size_t) t0 * k, len * k, nullptr, nullptr,
+                                            nullptr)) != QWMOE_OK)
+            return rc;
+        qwmoe_layer Lc = *L;
+        if ((rc = qwmoe_expert_cache_layer(c, layer, &Lc)) != QWMOE_OK) return rc;
+        const size_t o = (size_t) t0 * (size_t) H, oi = (size_t) t0 * (size_t) k;
+        if ((rc = qwmoe_ffn_layer(c->stream, &Lc, x + o, len, out + o, rms_eps, x_next ? x_next + o : nullptr,
+                                  ids_out ? ids_out + oi : nullptr, weights_out ? weights_out + oi : nullptr)))
+            return rc;
+    }
+    if (n_slices_out) *n_slices_out = ns;
+    return QWMOE_OK;
 }
 
 int qwmoe_expert_cache_sync(qwmoe_expert_cache* c) {

@@ -148,6 +148,20 @@ def router_topk(W, x, k: int, clamp_min: float = 6.103515625e-5, scale: float = 
     return (ids, w, probs) if want_probs else (ids, w)
 
 
+def plan_slices(sel, n_expert: int, cap: int, max_slice: int = 1024):
+    """plan_slices (core/runtime.cpp:2144-2170) on the host: sel int32 [T, n_used]
+    -> ([(t0, len)], union in first-use order)."""
+    import numpy as np
+    a = np.ascontiguousarray(sel, dtype=np.int32)
+    T, n_used = a.shape
+    out = np.zeros(2 * max(T, 1), np.int32)
+    un = np.zeros(n_expert, np.int32)
+    ns, nu = C.c_int(0), C.c_int(0)
+    check(lib().qwmoe_plan_slices(a.ctypes.data, T, n_used, n_expert, cap, max_slice, out.ctypes.data, C.byref(ns),
+                                  un.ctypes.data, C.byref(nu)), "plan_slices")
+    return [(int(out[2 * i]), int(out[2 * i + 1])) for i in range(ns.value)], un[:nu.value].tolist()
+
+
 def router_topk_resident(W, x, k: int, mask=None, want: bool = True, clamp_min: float = 6.103515625e-5,
                          scale: float = 0.0):
     """Resident-only routing: mask f32 [E] (0 / -inf) added to the logits before
@@ -642,3 +656,29 @@ class ExpertCache(_Handle):
         check(lib().qwmoe_expert_cache_run_layer(self.h, layer, C.byref(L), _ptr(x), T, _ptr(out), rms_eps, _ptr(xn),
                                                  _ptr(ids), _ptr(w)), "expert_cache_run_layer")
         return out, xn, ids, w
+
+    def run_batch(self, layer: int, L: Layer, x, rms_eps: float = -1.0, max_slice: int = 1024):
+        """The chunked prefill's layer through the cache: ids read back, planned
+        into slices within the pools' capacity, ensure() + the layer per slice.
+        x: f32 [T, H] -> (out, x_next or None, ids, weights, n_slices)."""
+        torch = _torch()
+        T, H = x.shape
+        k = L.n_expert_used
+        out = torch.empty((T, H), dtype=torch.float32, device=x.device)
+        xn = torch.empty((T, H), dtype=torch.float32, device=x.device) if rms_eps >= 0 else None
+        ids = torch.empty((T, k), dtype=torch.int32, device=x.device)
+        w = torch.empty((T, k), dtype=torch.float32, device=x.device)
+        ns = C.c_int(0)
+        check(lib().qwmoe_expert_cache_run_batch(self.h, layer, C.byref(L), _ptr(x), T, _ptr(out), rms_eps, _ptr(xn),
+                                                 _ptr(ids), _ptr(w), max_slice, C.byref(ns)), "expert_cache_run_batch")
+        return out, xn, ids, w, ns.value
+
+    def plan_slices(self, layer: int, sel, max_slice: int = 1024) -> list[tuple[int, int]]:
+        import numpy as np
+        a = np.ascontiguousarray(sel, dtype=np.int32)
+        T = a.shape[0]
+        out = np.zeros(2 * max(T, 1), np.int32)
+        ns = C.c_int(0)
+        check(lib().qwmoe_expert_cache_plan_slices(self.h, layer, a.ctypes.data, T, max_slice, out.ctypes.data,
+                                                   C.byref(ns)), "expert_cache_plan_slices")
+        return [(int(out[2 * i]), int(out[2 * i + 1])) for i in range(ns.value)]

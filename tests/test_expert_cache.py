@@ -480,3 +480,38 @@ def test_library_resident_helpers_match_oracle(seed):
         assert got == exp
         cursor = got[1]
         assert_same(c, p)
+
+
+# ---- batch slicing against pool capacity -----------------------------------------
+
+def test_oracle_plan_slices_by_hand():
+    """plan_slices (core/runtime.cpp:2144-2170) on a worked case: n_used 2, cap 3.
+    t0 {0,1} -> 2 distinct; t1 {1,2} -> 3; t2 {3,0} would make 5 > 3: slice
+    (0, 2) closes, t2 opens with {3,0}; t3 {0,3} -> still 2; t4 {4,5} -> 4 > 3:
+    (2, 2) closes; t4 alone -> (4, 1).  max_slice 2 caps lengths instead."""
+    from expert_cache_policy import plan_slices
+    sel = [[0, 1], [1, 2], [3, 0], [0, 3], [4, 5]]
+    assert plan_slices(sel, 2, 6, 3) == ([(0, 2), (2, 2), (4, 1)], [0, 1, 2, 3, 4, 5])
+    assert plan_slices(sel, 2, 6, 10, max_slice=2) == ([(0, 2), (2, 2), (4, 1)], [0, 1, 2, 3, 4, 5])
+    assert plan_slices(sel, 2, 6, 10) == ([(0, 5)], [0, 1, 2, 3, 4, 5])
+    assert plan_slices([], 2, 6, 3) == ([], [])
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_library_plan_slices_matches_oracle(seed):
+    import numpy as np
+    from expert_cache_policy import plan_slices
+    ops = lib_or_skip()
+    rng = random.Random(7000 + seed)
+    E = rng.choice([8, 16, 32, 128])
+    n_used = rng.randint(1, min(8, E))
+    T = rng.randint(0, 300)
+    cap = rng.randint(n_used, E + 4)
+    max_slice = rng.choice([0, 1, 3, 17, 1024])
+    sel = [zipf_ids(rng, E, n_used) for _ in range(T)]
+    got = ops.plan_slices(np.array(sel, np.int32).reshape(T, n_used), E, cap, max_slice)
+    assert got == plan_slices(sel, n_used, E, cap, max_slice)
+    # every slice fits the cap and the max length, and they tile the tokens
+    sl, _ = got
+    assert sum(n for _, n in sl) == T and all(n <= (max_slice if max_slice >= 1 else 1024) for _, n in sl)
+    assert all(len({e for t in range(t0, t0 + n) for e in sel[t]}) <= cap for t0, n in sl)

@@ -426,3 +426,27 @@ def test_resident_decode_through_cache():
     stack.close()
     ref.close()
     cl.cache.close()
+
+
+def test_run_batch_slices_within_capacity():
+    """The chunked prefill's layer through the cache (qwmoe_expert_cache_run_batch):
+    a 200-token batch naming every expert, pools at 75 % -- the slices planned
+    against capacity(layer) run one after another; outputs, ids and weights
+    bit-identical to the all-resident layer on the whole batch."""
+    note("run_batch: 1 layer H=1024 E=32 k=4 F=512 (Q4_K, Q4_K, Q6_K), 75% resident, T=200 and T=3")
+    cl = CachedLayers(1, 1024, 32, 4, 512, (Q4_K, Q4_K, Q6_K), 0.75, seed=17)
+    cap = cl.cache.capacity(0)
+    rng = np.random.default_rng(9)
+    for T, max_slice in ((200, 1024), (200, 16), (3, 1024)):
+        x = torch.from_numpy(rng.standard_normal((T, 1024)).astype(np.float32)).to(DEV)
+        ref_out, ref_xn, ref_ids, ref_w = ops.ffn_layer(cl.resident[0], x, rms_eps=1e-6)
+        plan = cl.cache.plan_slices(0, ref_ids.cpu().numpy(), max_slice)
+        out, xn, ids, w, ns = cl.cache.run_batch(0, cl.cached[0], x, rms_eps=1e-6, max_slice=max_slice)
+        torch.cuda.synchronize()
+        note(f"  T={T} max_slice={max_slice}: capacity {cap}, {ns} slices {plan[:4]}...")
+        assert ns == len(plan) and (T < 20 or 1 < ns < T)
+        assert torch.equal(ids, ref_ids)
+        assert np.array_equal(bits(w), bits(ref_w))
+        assert np.array_equal(bits(out), bits(ref_out))
+        assert np.array_equal(bits(xn), bits(ref_xn))
+    cl.cache.close()
