@@ -107,3 +107,21 @@ def test_slot_table_semantics():
         assert lib.qwmoe_slot_table_set(t, 0, 4, 0, 0) == -1
     finally:
         lib.qwmoe_slot_table_free(t)
+
+
+@pytest.mark.skipif(not Path("/root/reference/third_party/ggml/include/ggml.h").exists(),
+                    reason="ggml headers (reference tree) absent")
+@pytest.mark.parametrize("lang", ["c", "c++"])
+def test_ggml_glue_header_compiles(tmp_path, lang):
+    """include/qwmoe_ggml.h, included after ggml.h, compiles as C and as C++."""
+    import shutil
+    import subprocess
+    cc = shutil.which("gcc" if lang == "c" else "g++")
+    if cc is None:
+        pytest.skip("no host compiler")
+    src = tmp_path / ("glue.c" if lang == "c" else "glue.cpp")
+    src.write_text('#include "ggml.h"\n#include "qwmoe_ggml.h"\n'
+                   "int probe(const struct ggml_tensor * t) { return qwmoe_ggml_supports_mul_mat_id(t); }\n")
+    root = Path(__file__).resolve().parents[1]
+    subprocess.run([cc, "-fsyntax-only", "-Wall", "-Werror", "-x", lang, "-I", "/root/reference/third_party/ggml/include",
+                    "-I", str(root / "include"), str(src)], check=True)
