@@ -342,6 +342,55 @@ def prefill(args) -> int:
     return 0
 
 
+def cpu_chain_baseline(host_layers, xs, T: int, n_layer_total: int, budget_s: float = 15.0):
+    """The reference ggml CPU backend (oracle/_ref, AVX-512 branch when the host
+    has it) running a chain of layers at T tokens: each step pushes T tokens
+    through every layer of host_layers (x -> layer -> RMSNorm -> next layer),
+    timed per step; one warm-up step, then steps until budget_s of CPU work.
+    When host_layers is a sample of the workload's n_layer_total layers, the
+    per-step time is scaled by n_layer_total / len(host_layers).  Threads: the
+    physical cores of one socket.  None without the reference build."""
+    import numpy as np
+    sys.path.insert(0, str(ROOT / "tests"))
+    from oracle_lib import REF_SO, REF_SO_AVX512, RefGGML, have_ref_avx512
+    if not REF_SO.exists():
+        return None
+    cpu = host_cpu()
+    n_thr = max(1, min(cpu["cores_per_socket"], cpu["cpus_available"]))
+    ref = RefGGML(REF_SO_AVX512 if have_ref_avx512() else REF_SO)
+    RL = [ref.layer(lw, T, rms_eps=RMS_EPS, n_threads=n_thr) for lw in host_layers]
+    times, t_all, i = [], time.perf_counter(), 0
+    while True:
+        x = np.ascontiguousarray(xs[i % len(xs)][:T], np.float32)
+        t0 = time.perf_counter()
+        for R in RL:
+            x = R(x)["xnext"]
+        dt = time.perf_counter() - t0
+        if i > 0:
+            times.append(dt)
+        i += 1
+        if (time.perf_counter() - t_all > budget_s and len(times) >= 3) or len(times) >= 2000:
+            break
+    med = float(np.median(times)) * n_layer_total / len(host_layers)
+    return {"value": round(T / med, 2), "unit": "tok/s", "cores": n_thr, "kind": "reference",
+            "sample": f"{len(times)} steps of T={T} through {len(host_layers)} of the {n_layer_total} layers "
+                      f"(per-step time scaled by {n_layer_total}/{len(host_layers)}); tok/s = T / median step",
+            "median_ms_per_step": round(med * 1e3, 3), "isa": "AVX-512" if ref.isa() == 512 else "AVX2",
+            "threads": n_thr, "cpu": cpu["model"]}
+
+
+def host_layer_weights(router, gate, up, down, types, H_, E_, k_, F_):
+    sys.path.insert(0, str(ROOT / "tests"))
+    from oracle_lib import LayerWeights
+    lw = LayerWeights.__new__(LayerWeights)
+    lw.H, lw.E, lw.k, lw.F = H_, E_, k_, F_
+    lw.type_gate, lw.type_up, lw.type_down = types
+    lw.router = router.cpu().numpy()
+    lw.gate, lw.up, lw.down = (m.cpu().numpy().reshape(-1) for m in (gate, up, down))
+    lw.n_slots, lw.slot_of = E_, None
+    return lw
+
+
 def prefill_cpu_baseline(L, mats, router, x, T: int):
     """The reference ggml CPU backend (oracle/_ref) on the same layer and batch:
     one evaluation of the T-token graph on 16 host threads."""
@@ -552,6 +601,10 @@ def verify_bench(args) -> int:
                      "unique_experts_per_layer": round(uniq / N_LAYER, 2),
                      "weight_gbps": round(wbytes / g_s / 1e9, 1)})
     last = rows[-1]
+    cpu = None
+    if not args.no_cpu_baseline:
+        lws = [host_layer_weights(*ly, (Q4_K,) * 3, H, E, K_USED, F) for ly in layers]
+        cpu = cpu_chain_baseline(lws, xs[:16].cpu().numpy(), Tmax, N_LAYER)
     line = {
         "metric": "verify-batch tok/s, 30B-A3B Q4_K MoE FFN stack (speculative-decoding verify forward, FFN half)",
         "value": last["verify_tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -565,7 +618,7 @@ def verify_bench(args) -> int:
         "roofline": {"bound": "hbm", "achieved": last["weight_gbps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(last["weight_gbps"] / HBM_PEAK_GBS, 4), "traffic": None,
                      "note": "unique experts' weights + routers per step / step time"},
-        "cpu_baseline": None,
+        "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
     stack.close()
@@ -657,6 +710,18 @@ def config5_bench(args) -> int:
     pre_exact_s, (out_x, _, _, _) = prefill_s(ops.MFMA_EXACT)
     pre_rel = float((out.double() - out_x.double()).abs().max() / out_x.double().abs().max().clamp_min(1e-30))
     used = int((np.bincount(ids.cpu().numpy().reshape(-1), minlength=E5) > 0).sum())
+    cpu = None
+    if not args.no_cpu_baseline:
+        # decode on the CPU: a sample of 4 of the 94 layers (logical expert order:
+        # the slot permutation undone), their per-token time scaled to 94
+        lws = []
+        for l in range(4):
+            router_l, mats_l, slots_l = keep[l]
+            logical = [m.view(E5, -1)[sl.long()] for m, sl in zip(mats_l, slots_l)]
+            lws.append(host_layer_weights(router_l, *logical, types, H5, E5, K5, F5))
+            del logical
+        cpu = cpu_chain_baseline(lws, xs[:16].view(-1, 1, H5).cpu().numpy(), 1, NL5)
+        del lws
     pre_bytes = used * expert5 + E5 * H5 * 4
     line = {
         "metric": "configs[4] decode tok/s (94-layer stack, batch 1) and prefill tok/s (T=1024, one layer)",
@@ -677,7 +742,7 @@ def config5_bench(args) -> int:
                      "frac": round(dec_bytes / dec_s / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
                      "note": "decode: selected experts' weights + routers per token / token time"},
         "weight_gen_s": round(t_gen, 1),
-        "cpu_baseline": None,
+        "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
     stack.close()
