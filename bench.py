@@ -30,7 +30,9 @@ RMS_EPS = 1e-6
 HBM_PEAK_GBS = 8000.0
 TRAFFIC_FILE = ROOT / "profiles" / "decode_xcd_q4k_30b_pmc.txt"
 KERNEL_NAMES = {1: "k_decode_stack<8,3,Q4_K>", 2: "k_decode_xcd<8,3,4> (XCD-local exchange words)",
-                3: "k_decode_xcd<8,3,4> (device-scope exchange words)"}
+                3: "k_decode_xcd<8,3,4> (device-scope exchange words)",
+                4: "k_decode_xcd_wide<16,6,4,Q6_K> (XCD-local exchange words)",
+                5: "k_decode_xcd_wide<16,6,4,Q6_K> (device-scope exchange words)"}
 
 
 def measured_traffic(path: str):
@@ -631,8 +633,8 @@ def config5_bench(args) -> int:
     """the large-expert regime, 94 MoE layers (H=4096, E=128, top-8,
     F=1536), Q4_K gate/up and Q6_K down, every layer's experts stored at a seeded
     random slot permutation read through the slot rows.  Decode at batch 1
-    through all 94 layers (qwmoe_layer_stack at T = 1, its captured graph; the
-    persistent decode kernel's LDS plan does not cover this shape) and prefill of
+    through all 94 layers (the persistent decode kernel's wide XCD form, one
+    launch per token; the layer stack at T = 1 timed beside it) and prefill of
     1024 tokens through one layer (qwmoe_ffn_layer, Zipf(1.1)-skewed router)."""
     import numpy as np
     import torch
@@ -669,10 +671,36 @@ def config5_bench(args) -> int:
     del tmp
     t_gen = time.perf_counter() - t_gen
 
-    # decode: one token through all 94 layers per step
+    # decode: one token through all 94 layers per step, on the persistent decode
+    # kernel (its wide XCD form: one launch per token) and, beside it, on the
+    # layer stack at T = 1 (five launches per layer, one captured graph)
+    dstack = ops.DecodeStack(layers, RMS_EPS, keepalive=keep)
     stack = ops.LayerStack(layers, RMS_EPS, max_tokens=1, keepalive=keep)
     xs = torch.empty((args.steps + args.warmup, 1, H5), dtype=torch.float32, device=dev)
     ops.randn_(xs, args.seed + 4242, 0.0, 1.0)
+    # the two paths on the first 8 tokens: ids, weights and outputs bitwise
+    same = True
+    for i in range(min(8, args.steps + args.warmup)):
+        a_ = dstack(xs[i].view(-1))
+        b_ = stack(xs[i])
+        same = same and torch.equal(a_[2].view(-1), b_[2].reshape(-1)) and all(
+            torch.equal(u.reshape(-1).view(torch.int32), v.reshape(-1).view(torch.int32))
+            for u, v in ((a_[0], b_[0]), (a_[1], b_[1]), (a_[3], b_[3])))
+    dout = torch.empty(H5, dtype=torch.float32, device=dev)
+    dxo = torch.empty(H5, dtype=torch.float32, device=dev)
+    for i in range(args.warmup):
+        dstack.run(xs[i].view(-1), dout, dxo)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        evs[i][0].record()
+        dstack.run(xs[args.warmup + i].view(-1), dout, dxo)
+        evs[i][1].record()
+    torch.cuda.synchronize()
+    dec_s = (time.perf_counter() - t0) / args.steps
+    kern_ms = sum(a_.elapsed_time(b_) for a_, b_ in evs) / args.steps
+    dstatus = dstack.status()
     for i in range(args.warmup):
         stack(xs[i], want_ids=False)
     torch.cuda.synchronize()
@@ -680,7 +708,7 @@ def config5_bench(args) -> int:
     for i in range(args.steps):
         stack(xs[args.warmup + i], want_ids=False)
     torch.cuda.synchronize()
-    dec_s = (time.perf_counter() - t0) / args.steps
+    ls_s = (time.perf_counter() - t0) / args.steps
     expert5 = 2 * F5 * row_size(Q4_K, H5) + H5 * row_size(Q6_K, F5)
     dec_bytes = NL5 * (K5 * expert5 + E5 * H5 * 4)
 
@@ -729,23 +757,32 @@ def config5_bench(args) -> int:
         "ms_per_step": round(dec_s * 1e3, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "q4_K/q6_K x q8_K -> f32", "data": "synthetic (seeded; slot permutation seeded; prefill router Zipf(1.1))",
         "config": {"workload": "configs[4]: 94 layers H=4096 E=128 k=8 F=1536, Q4_K gate/up, Q6_K down, permuted slots",
-                   "decode_path": "qwmoe_layer_stack T=1 (captured graph)", "prefill_path": "qwmoe_ffn_layer T=1024"},
+                   "decode_path": "qwmoe_decode_stack_run: " + KERNEL_NAMES.get(dstack.kernel(), "?") +
+                                  ", one launch per token through 94 layers",
+                   "prefill_path": "qwmoe_ffn_layer T=1024"},
         "decode": {"tok_s": round(1.0 / dec_s, 2), "ms_per_token": round(dec_s * 1e3, 3),
+                   "avg_launch_ms": round(kern_ms, 4),
                    "weight_bytes_per_token": dec_bytes, "gbps": round(dec_bytes / dec_s / 1e9, 1),
-                   "frac_of_8tbs": round(dec_bytes / dec_s / 1e9 / HBM_PEAK_GBS, 4)},
+                   "frac_of_8tbs": round(dec_bytes / dec_s / 1e9 / HBM_PEAK_GBS, 4),
+                   "device_status": dstatus,
+                   "layer_stack_t1_tok_s": round(1.0 / ls_s, 2),
+                   "equals_layer_stack_bitwise_8_tokens": bool(same)},
         "prefill": {"tokens": T5, "ms_per_layer": round(pre_s * 1e3, 3), "tok_s": round(T5 / pre_s, 1),
                     "used_experts": used, "weight_gbps": round(pre_bytes / pre_s / 1e9, 1),
                     "form": "auto (gate/up lane-exact, down block sums on the matrix cores)",
                     "exact_form_ms_per_layer": round(pre_exact_s * 1e3, 3),
                     "rel_err_vs_exact_form": float(f"{pre_rel:.3e}")},
-        "roofline": {"bound": "hbm", "achieved": round(dec_bytes / dec_s / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dec_bytes / dec_s / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
-                     "note": "decode: selected experts' weights + routers per token / token time"},
+        "roofline": {"bound": "hbm", "achieved": round(dec_bytes / kern_ms / 1e6, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(dec_bytes / kern_ms / 1e6 / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": KERNEL_NAMES.get(dstack.kernel(), "?") + " (one launch = one token through 94 layers)",
+                     "bytes_per_launch": dec_bytes, "avg_launch_ms": round(kern_ms, 4),
+                     "note": "selected experts' weights + routers per token / average launch time (HIP events)"},
         "weight_gen_s": round(t_gen, 1),
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
     stack.close()
+    dstack.close()
     return 0
 
 

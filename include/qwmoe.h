@@ -304,7 +304,7 @@ int qwmoe_decode_stack_run(void * stream, qwmoe_decode_stack * s, const float * 
                            int32_t * ids_out, float * weights_out);
 /* Synchronises `stream`; status bits: 1 top-k tie replayed, 8 a wait timed out
  * (launch abandoned), 16 a slot table entry was out of range.  With 8, the
- * XCD kernel (qwmoe_decode_stack_kernel 2 or 3) names the exchange it waited
+ * XCD kernels (qwmoe_decode_stack_kernel 2 to 5) name the exchange they waited
  * for: 256 router logits, 512 act, 1024 down outputs, 2048 y, 4096 top-k. */
 int qwmoe_decode_stack_status(void * stream, qwmoe_decode_stack * s, int32_t * status_out, int clear);
 void qwmoe_decode_stack_free(qwmoe_decode_stack * s);
@@ -312,10 +312,12 @@ void qwmoe_decode_stack_free(qwmoe_decode_stack * s);
  * 1 = one workgroup per CU over every selected expert; 2 = one selected expert
  * per XCD (256-CU devices, k <= 8, H = 2048, Q4_K down), exchanges inside an XCD
  * through its L2; 3 = the same with every exchange word stored at device scope
- * (used when creation finds the workgroups not dealt to the XCDs round robin).
- * Creation picks 2 or 3 where the shape allows, else 1; QWMOE_DECODE_XCD=0 in
- * the environment at creation forces 1, QWMOE_DECODE_XCD_LOCAL=0 forces 3 over 2.
- * Results are identical. */
+ * (used when creation finds the workgroups not dealt to the XCDs round robin);
+ * 4 and 5 = the forms of 2 and 3 for wide layers (H = 4096, F = 1536, E = 128,
+ * Q6_K or Q4_K down with 4- / 16-byte aligned rows; router logits exchanged
+ * across XCDs).  Creation picks 2 to 5 where the shape allows, else 1;
+ * QWMOE_DECODE_XCD=0 in the environment at creation forces 1,
+ * QWMOE_DECODE_XCD_LOCAL=0 forces device-scope words.  Results are identical. */
 int qwmoe_decode_stack_kernel(const qwmoe_decode_stack * s);
 
 /* ---- T-token batches through a layer stack (speculative-decoding verify) ------ */

@@ -684,7 +684,15 @@ int qwmoe_decode_stack_create(const qwmoe_layer* layers, int n_layer, float rms_
     if (allow_xcd && qw::check_decode_xcd(d, cus) == 0) {
         d.use_xcd = 1;
         d.grid = cus;
-    } else {
+        // the wide form loads whole down blocks per lane: Q6_K rows 4-byte, Q4_K
+        // rows 16-byte aligned
+        d.xcd_wide = qw::decode_xcd_wide_kernel(d) != nullptr;
+        const uintptr_t dal = d.type_down == qw::T_Q6_K ? 3 : 15;
+        for (int l = 0; d.xcd_wide && l < n_layer; ++l)
+            if (((uintptr_t) layers[l].down | (uintptr_t) layers[l].down_nb1 | (uintptr_t) layers[l].down_nb2) & dal)
+                d.use_xcd = d.xcd_wide = 0;
+    }
+    if (!d.use_xcd) {
         rc = qw::plan_decode_stack(d, cus);
         if (rc == 0) rc = qw::check_decode_residency(d);
     }
@@ -778,7 +786,7 @@ int qwmoe_decode_stack_run(void* stream, qwmoe_decode_stack* s, const float* x, 
 
 int qwmoe_decode_stack_kernel(const qwmoe_decode_stack* s) {
     if (!s) return QWMOE_ERR_INVALID_ARG;
-    return s->d.use_xcd ? (s->d.xcd_local ? 2 : 3) : 1;
+    return s->d.use_xcd ? (s->d.xcd_local ? 2 : 3) + (s->d.xcd_wide ? 2 : 0) : 1;
 }
 
 int qwmoe_decode_stack_status(void* stream, qwmoe_decode_stack* s, int32_t* status_out, int clear) {

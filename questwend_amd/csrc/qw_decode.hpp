@@ -69,6 +69,7 @@ struct DecodeStackDesc {
     uint64_t* xd = nullptr;       // XCD kernel: down outputs crossing XCDs
     int use_xcd = 0;              // 1: k_decode_xcd (one expert per XCD), 0: k_decode_stack
     int xcd_local = 0;            // XCD kernel: XCD-local words stored with workgroup scope
+    int xcd_wide = 0;             // XCD kernel: the wide form (decode_xcd_wide.hip)
     int32_t* status = nullptr;
     int32_t* abort_flag = nullptr;
     uint32_t epoch = 1;           // next launch's first layer epoch
@@ -84,8 +85,10 @@ int plan_decode_stack(DecodeStackDesc& d, int grid);
 const void* decode_kernel(const DecodeStackDesc& d);
 // 0 if one WG of the planned kernel fits on a CU (grid = CU count => all resident).
 int check_decode_residency(const DecodeStackDesc& d);
-// decode_xcd.hip: the kernel with one selected expert per XCD (grid = 8 XCDs x 32 CUs)
+// decode_xcd.hip: the kernel with one selected expert per XCD (grid = 8 XCDs x 32 CUs);
+// decode_xcd_wide.hip: its form for wide layers (H = 4096, F = 1536), or null
 const void* decode_xcd_kernel(const DecodeStackDesc& d);
+const void* decode_xcd_wide_kernel(const DecodeStackDesc& d);
 // 0 if the shape has an XCD kernel and the device has 256 CUs
 int check_decode_xcd(const DecodeStackDesc& d, int cus);
 // writes each workgroup's XCD id to dev_buf[0..n) and sets *ok when workgroup b runs on XCD b % 8

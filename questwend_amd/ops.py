@@ -318,7 +318,8 @@ class DecodeStack(_Handle):
         return out, xo, ids, w
 
     def kernel(self) -> int:
-        """1: one workgroup per CU; 2: one expert per XCD; 3: the same, device-scope words."""
+        """1: one workgroup per CU; 2: one expert per XCD; 3: the same, device-scope words;
+        4, 5: the forms of 2, 3 for wide layers (H = 4096, F = 1536)."""
         return int(lib().qwmoe_decode_stack_kernel(self.h))
 
     def status(self, clear: bool = True) -> int:
