@@ -337,43 +337,6 @@ __global__ void __launch_bounds__(XT) k_decode_xcd_wide(XcdArgs a) {
             }
         };
 
-        // ---- A: gate/up blocks -> integers (the speculative expert) ---------------
-        if (expert_xcd) {
-            issue((uint32_t) __builtin_amdgcn_readfirstlane(spec.y), (uint32_t) __builtin_amdgcn_readfirstlane(spec.z));
-            topk_fast();
-            gate_up_parts();
-        } else {
-            topk_fast();
-        }
-        lds_barrier();
-        if (s_exact) {
-            topk_exact();
-            lds_barrier();
-            const int my_e = __builtin_amdgcn_readfirstlane(s_my.x);
-            if (expert_xcd && my_e != spec_e) {
-                // misspeculated: the right rows, one block at a time (a rare path; its
-                // own registers keep the fast path's blocks out of scratch memory)
-                const int4 my = s_my;
-                uint32_t sg = (uint32_t) __builtin_amdgcn_readfirstlane(my.y), su = (uint32_t) __builtin_amdgcn_readfirstlane(my.z);
-                sg = sg < nsg ? sg : 0u;
-                su = su < nsu ? su : 0u;
-#pragma unroll
-                for (int m = 0; m < UGL; ++m) {
-                    const uint8_t* p = (gup[m] ? Lup + (uint64_t) su * unb2 : Lgate + (uint64_t) sg * gnb2) + og[m];
-                    u32x4 w1[9];
-#pragma unroll
-                    for (int i = 0; i < 9; ++i) w1[i] = ldg16(p + 16 * i);
-                    const int u = tid + XT * m;
-                    uint32_t part[NPG];
-                    bp_q4k_block([&](uint32_t o) { return w1[o / 16][(o / 4) % 4]; }, s_xq,
-                                 BP_ABLK * (uint32_t) (u % NBH) + 12u, part);
-#pragma unroll
-                    for (int i = 0; i < NPG; ++i) s_part[u * NPG + i] = part[i];
-                }
-            }
-            lds_barrier();
-        }
-
         // next layer's slot rows and the descriptor of layer l + 2 (stored after the y exchange)
         const bool nxt = l + 1 < a.n_layer;
         const DecodeLayer& L1 = *(const DecodeLayer*) s_L[(l + 1) & 1];
@@ -385,9 +348,93 @@ __global__ void __launch_bounds__(XT) k_decode_xcd_wide(XcdArgs a) {
         const bool next2 = l + 2 < a.n_layer && tid < XLW;
         const uint64_t lw = ldg64((const uint64_t*) (a.layers + (next2 ? l + 2 : l)) + (tid % XLW));
 
+        // Down block u (row NH j + u / NBF, block u % NBF) of slot sd into w (Q6_K:
+        // the aligned words holding its 210 bytes, sh its byte offset in the first);
+        // zeros for u >= UD (uniform per wave).
+        uint32_t wd0[DW], wd1[DW], dsh0, dsh1;   // this lane's down blocks u = tid, tid + XT
+        auto load_down = [&](uint32_t sd, int u, uint32_t (&w)[DW], uint32_t& sh) {
+            sd = sd < nsd ? sd : 0u;
+            if (u < UD) {
+                const uint8_t* bp = Ldown + (uint64_t) sd * dnb2 + (uint32_t) (NH * j + u / NBF) * dnb1 +
+                                    (uint32_t) block_bytes(TD) * (uint32_t) (u % NBF);
+                if constexpr (TD == T_Q6_K) {
+                    sh = (uint32_t) ((uintptr_t) bp & 3);
+                    gu32_t* src = (gu32_t*) ((uintptr_t) bp & ~(uintptr_t) 3);
+#pragma unroll
+                    for (int i = 0; i < DW; ++i) w[i] = src[i];
+                } else {
+                    sh = 0;
+#pragma unroll
+                    for (int i = 0; i < 9; ++i) {
+                        const u32x4 v = ldg16(bp + 16 * i);
+                        w[4 * i] = v[0];
+                        w[4 * i + 1] = v[1];
+                        w[4 * i + 2] = v[2];
+                        w[4 * i + 3] = v[3];
+                    }
+                }
+            } else {
+                sh = 0;
+#pragma unroll
+                for (int i = 0; i < DW; ++i) w[i] = 0u;
+            }
+        };
+        // the integers of down block u from w (Q6_K: aligned in place first) into s_part
+        auto down_parts = [&](int u, uint32_t (&w)[DW], uint32_t sh) {
+            if (u >= UD) return;
+            uint32_t part[NPD];
+            const uint32_t yb = BP_ABLK * (uint32_t) (u % NBF) + 12u;
+            if constexpr (TD == T_Q6_K) {
+                const uint16_t d16 = (uint16_t) (sh ? w[52] >> 16 : w[52] & 0xffff);
+#pragma unroll
+                for (int i = 0; i < 52; ++i) w[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], sh);
+                bp_q6k_block<true>([&](uint32_t o) { return w[o / 4]; }, d16, s_aq, yb, part);
+            } else {
+                bp_q4k_block([&](uint32_t o) { return w[o / 4]; }, s_aq, yb, part);
+            }
+#pragma unroll
+            for (int i = 0; i < NPD; ++i) s_part[u * NPD + i] = part[i];
+        };
+
         if (expert_xcd) {
-            // ---- chains -> rows -> SwiGLU ---------------------------------------------
+            // ---- A: the speculative expert's gate/up blocks and the first down block
+            // of each lane, issued together; the gate/up integers
+            issue((uint32_t) __builtin_amdgcn_readfirstlane(spec.y), (uint32_t) __builtin_amdgcn_readfirstlane(spec.z));
+            load_down((uint32_t) __builtin_amdgcn_readfirstlane(spec.w), tid, wd0, dsh0);
+            topk_fast();
+            gate_up_parts();
+            lds_barrier();
+            if (s_exact) {
+                topk_exact();
+                lds_barrier();
+                const int4 my = s_my;
+                if (__builtin_amdgcn_readfirstlane(my.x) != spec_e) {
+                    // misspeculated: the right rows, one gate/up block at a time (a rare
+                    // path; its own registers keep the fast path's blocks out of scratch)
+                    uint32_t sg = (uint32_t) __builtin_amdgcn_readfirstlane(my.y);
+                    uint32_t su = (uint32_t) __builtin_amdgcn_readfirstlane(my.z);
+                    sg = sg < nsg ? sg : 0u;
+                    su = su < nsu ? su : 0u;
+#pragma unroll
+                    for (int m = 0; m < UGL; ++m) {
+                        const uint8_t* p = (gup[m] ? Lup + (uint64_t) su * unb2 : Lgate + (uint64_t) sg * gnb2) + og[m];
+                        u32x4 w1[9];
+#pragma unroll
+                        for (int i = 0; i < 9; ++i) w1[i] = ldg16(p + 16 * i);
+                        const int u = tid + XT * m;
+                        uint32_t part[NPG];
+                        bp_q4k_block([&](uint32_t o) { return w1[o / 16][(o / 4) % 4]; }, s_xq,
+                                     BP_ABLK * (uint32_t) (u % NBH) + 12u, part);
+#pragma unroll
+                        for (int i = 0; i < NPG; ++i) s_part[u * NPG + i] = part[i];
+                    }
+                    load_down((uint32_t) __builtin_amdgcn_readfirstlane(my.w), tid, wd0, dsh0);
+                }
+                lds_barrier();
+            }
             const int4 my = s_my;
+            load_down((uint32_t) __builtin_amdgcn_readfirstlane(my.w), tid + XT, wd1, dsh1);
+            // ---- chains -> rows -> SwiGLU ---------------------------------------------
             // chain (row, c): c < 8 -> AVX lane c of acc over the blocks in order, c >= 8
             // -> min lane c - 8 of acc_m
             for (int q = tid; q < NR * NCG; q += XT) {
@@ -410,42 +457,6 @@ __global__ void __launch_bounds__(XT) k_decode_xcd_wide(XcdArgs a) {
             lds_barrier();
             if (tid < NP) st_local(a.xa + xcd * F + NP * j + tid, tag(v_silu(s_g[tid]) * s_g[NP + tid], ep), local);
 
-            // ---- down blocks of this XCD's expert: rows NH j .. NH j + NH - 1 ---------
-            uint32_t wd[UDL][DW];   // (Q6_K: the aligned words holding each block)
-            uint32_t dsh[UDL];      // Q6_K: each block's byte offset in its first word (0 or 2)
-            {
-                uint32_t sd = (uint32_t) __builtin_amdgcn_readfirstlane(my.w);
-                sd = sd < nsd ? sd : 0u;
-                const uint8_t* base = Ldown + (uint64_t) sd * dnb2;
-#pragma unroll
-                for (int m = 0; m < UDL; ++m) {
-                    const int u = tid + XT * m;
-                    if (u < UD) {   // (uniform per wave)
-                        const uint8_t* bp = base + (uint32_t) (NH * j + u / NBF) * dnb1 +
-                                            (uint32_t) block_bytes(TD) * (uint32_t) (u % NBF);
-                        if constexpr (TD == T_Q6_K) {
-                            dsh[m] = (uint32_t) ((uintptr_t) bp & 3);
-                            gu32_t* w = (gu32_t*) ((uintptr_t) bp & ~(uintptr_t) 3);
-#pragma unroll
-                            for (int i = 0; i < DW; ++i) wd[m][i] = w[i];
-                        } else {
-                            dsh[m] = 0;
-#pragma unroll
-                            for (int i = 0; i < 9; ++i) {
-                                const u32x4 v = ldg16(bp + 16 * i);
-                                wd[m][4 * i] = v[0];
-                                wd[m][4 * i + 1] = v[1];
-                                wd[m][4 * i + 2] = v[2];
-                                wd[m][4 * i + 3] = v[3];
-                            }
-                        }
-                    } else {
-                        dsh[m] = 0;
-#pragma unroll
-                        for (int i = 0; i < DW; ++i) wd[m][i] = 0u;
-                    }
-                }
-            }
             weights();
 
             // ---- act of this XCD's expert -> Q8_K -> D: down blocks -> rows ------------
@@ -458,26 +469,8 @@ __global__ void __launch_bounds__(XT) k_decode_xcd_wide(XcdArgs a) {
                 quant_q8K_w64<4, 0>(v, lane, (uint8_t*) s_aq + BP_ABLK * wave + 12);
             }
             lds_barrier();
-#pragma unroll
-            for (int m = 0; m < UDL; ++m) {
-                const int u = tid + XT * m;
-                if (u < UD) {
-                    uint32_t part[NPD];
-                    const uint32_t yb = BP_ABLK * (uint32_t) (u % NBF) + 12u;
-                    if constexpr (TD == T_Q6_K) {
-                        // the block's words aligned in place (one register set, not two)
-                        const uint32_t sh = dsh[m];
-                        const uint16_t d16 = (uint16_t) (sh ? wd[m][52] >> 16 : wd[m][52] & 0xffff);
-#pragma unroll
-                        for (int i = 0; i < 52; ++i) wd[m][i] = __builtin_amdgcn_alignbyte(wd[m][i + 1], wd[m][i], sh);
-                        bp_q6k_block<true>([&, m](uint32_t o) { return wd[m][o / 4]; }, d16, s_aq, yb, part);
-                    } else {
-                        bp_q4k_block([&, m](uint32_t o) { return wd[m][o / 4]; }, s_aq, yb, part);
-                    }
-#pragma unroll
-                    for (int i = 0; i < NPD; ++i) s_part[u * NPD + i] = part[i];
-                }
-            }
+            down_parts(tid, wd0, dsh0);
+            down_parts(tid + XT, wd1, dsh1);
             lds_barrier();
             for (int q = tid; q < NH * NCD; q += XT) {
                 const int r = q / NCD, c = q - r * NCD;
@@ -498,6 +491,13 @@ __global__ void __launch_bounds__(XT) k_decode_xcd_wide(XcdArgs a) {
                 st_cross(a.xd + (((size_t) (l & 1) * NXCD + xcd) * NJ + j) * NH + tid, tag(v, ep));
             }
         } else {
+            topk_fast();
+            lds_barrier();
+            if (s_exact) {
+                topk_exact();
+                lds_barrier();
+                lds_barrier();
+            }
             weights();
         }
         // the next layer's router row, into registers (stored to LDS after the y exchange)
