@@ -640,7 +640,8 @@ def config5_bench(args) -> int:
     import torch
     from questwend_amd import Q4_K, Q6_K, ops, row_size
 
-    H5, E5, K5, F5, NL5 = 4096, 128, 8, 1536, 94
+    H5, E5, K5, F5 = 4096, 128, 8, 1536
+    NL5 = args.c5_layers   # 94; fewer only to profile the prefill kernels
     types = (Q4_K, Q4_K, Q6_K)
     ops.init(0, 1 << 30)
     dev = "cuda:0"
@@ -743,7 +744,7 @@ def config5_bench(args) -> int:
         # decode on the CPU: a sample of 4 of the 94 layers (logical expert order:
         # the slot permutation undone), their per-token time scaled to 94
         lws = []
-        for l in range(4):
+        for l in range(min(4, NL5)):
             router_l, mats_l, slots_l = keep[l]
             logical = [m.view(E5, -1)[sl.long()] for m, sl in zip(mats_l, slots_l)]
             lws.append(host_layer_weights(router_l, *logical, types, H5, E5, K5, F5))
@@ -756,9 +757,9 @@ def config5_bench(args) -> int:
         "value": round(1.0 / dec_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(dec_s * 1e3, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "q4_K/q6_K x q8_K -> f32", "data": "synthetic (seeded; slot permutation seeded; prefill router Zipf(1.1))",
-        "config": {"workload": "configs[4]: 94 layers H=4096 E=128 k=8 F=1536, Q4_K gate/up, Q6_K down, permuted slots",
+        "config": {"workload": f"configs[4]: {NL5} layers H=4096 E=128 k=8 F=1536, Q4_K gate/up, Q6_K down, permuted slots",
                    "decode_path": "qwmoe_decode_stack_run: " + KERNEL_NAMES.get(dstack.kernel(), "?") +
-                                  ", one launch per token through 94 layers",
+                                  f", one launch per token through {NL5} layers",
                    "prefill_path": "qwmoe_ffn_layer T=1024"},
         "decode": {"tok_s": round(1.0 / dec_s, 2), "ms_per_token": round(dec_s * 1e3, 3),
                    "avg_launch_ms": round(kern_ms, 4),
@@ -774,7 +775,7 @@ def config5_bench(args) -> int:
                     "rel_err_vs_exact_form": float(f"{pre_rel:.3e}")},
         "roofline": {"bound": "hbm", "achieved": round(dec_bytes / kern_ms / 1e6, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(dec_bytes / kern_ms / 1e6 / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": KERNEL_NAMES.get(dstack.kernel(), "?") + " (one launch = one token through 94 layers)",
+                     "kernel": KERNEL_NAMES.get(dstack.kernel(), "?") + f" (one launch = one token through {NL5} layers)",
                      "bytes_per_launch": dec_bytes, "avg_launch_ms": round(kern_ms, 4),
                      "note": "selected experts' weights + routers per token / average launch time (HIP events)"},
         "weight_gen_s": round(t_gen, 1),
@@ -809,6 +810,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--c5-layers", type=int, default=94,
+                    help="config5: layers in the decode stack (configs[4] has 94; fewer only for counter runs)")
     ap.add_argument("--traffic", default=str(TRAFFIC_FILE),
                     help="text file whose 'hbm_bytes_per_launch = N' line is the HBM traffic of one decode "
                          "launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (copy-calibrated)")

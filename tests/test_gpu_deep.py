@@ -9,8 +9,9 @@ layer's RMSNorm output as the GPU computed it.
   configs[3]  1000 seeded verify batches (T = 5, tokens correlated at rho = 0.8)
               through one 30B-A3B Q4_K layer: ids, weights, output, RMSNorm.
   configs[4]  94 layers at H = 4096, E = 128, F = 1536 (Q4_K gate/up, Q6_K
-              down) through the layer stack's captured graph at T = 1, every
-              layer read through a seeded slot permutation.  The routers are
+              down) through the layer stack's captured graph at T = 1 and
+              through the persistent decode kernel, every layer read through a
+              seeded slot permutation.  The routers are
               distinct per layer; the expert tensors come from 4 distinct sets,
               layer l using set l % 4 (all 94 distinct would need 147 GB).
 """
@@ -181,19 +182,32 @@ def test_config4_94_layers_slot_tables():
         lw.n_slots, lw.slot_of = E, None
         lws.append(lw)
     xs = np.random.default_rng(94).standard_normal((warm + steps, H)).astype(np.float32)
-    stack = ops.LayerStack(layers, EPS, max_tokens=1, keepalive=keep)
     xd = torch.from_numpy(xs).to(DEV)
-    g_out, g_ids = [], []
-    for s in range(warm + steps):
-        out, _, ids, _ = stack(xd[s:s + 1])
-        if s >= warm:
-            g_out.append(out.cpu().numpy()[0])
-            g_ids.append(ids.cpu().numpy()[:, 0])
-    stack.close()
+    runs = {}
+    # the layer stack (five launches per layer) and the persistent decode kernel
+    # (one launch per token; its wide XCD form on a 256-CU device)
+    for name in ("layer stack", "decode stack"):
+        if name == "layer stack":
+            stack = ops.LayerStack(layers, EPS, max_tokens=1, keepalive=keep)
+        else:
+            stack = ops.DecodeStack(layers, EPS, keepalive=keep)
+            note(f"  decode stack kernel {stack.kernel()}")
+        g_out, g_ids = [], []
+        for s in range(warm + steps):
+            out, _, ids, _ = stack(xd[s:s + 1] if name == "layer stack" else xd[s])
+            if s >= warm:
+                g_out.append(out.cpu().numpy().reshape(-1))
+                g_ids.append(ids.cpu().numpy().reshape(NL, k))
+        if name == "decode stack":
+            assert stack.status() & ~1 == 0
+        stack.close()
+        runs[name] = (g_out, g_ids)
     ref = RefGGML()
     RL = [ref.layer(lw, 1, rms_eps=EPS, n_threads=n_threads()) for lw in lws]
     r = ref.stack_run(RL, xs, warm, n_threads())
-    for s in range(steps):
-        assert np.array_equal(g_ids[s], r["ids"][s]), f"step {s} ids"
-        assert np.array_equal(bits(g_out[s]), bits(r["out"][s])), f"step {s} out"
-    note(f"  {steps} steps x {NL} layers equal; smallest top-k margin {float(r['margin'].min()):.3e}")
+    for name, (g_out, g_ids) in runs.items():
+        for s in range(steps):
+            assert np.array_equal(g_ids[s], r["ids"][s]), f"{name}: step {s} ids"
+            assert np.array_equal(bits(g_out[s]), bits(r["out"][s])), f"{name}: step {s} out"
+    note(f"  {steps} steps x {NL} layers equal (layer stack and decode stack); "
+         f"smallest top-k margin {float(r['margin'].min()):.3e}")
