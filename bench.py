@@ -17,6 +17,7 @@ from __future__ import annotations
 import argparse
 import ctypes as C
 import json
+import math
 import os
 import sys
 import time
@@ -553,11 +554,14 @@ def expert_cache_bench(args) -> int:
 
 
 def verify_bench(args) -> int:
-    """The configs[1] stack (48 Q4_K layers of the 30B-A3B shape) on the verify
-    batch of speculative decoding: T = 1..--tokens tokens (n_draft + 1) per step
-    through every layer (qwmoe_layer_stack: qwmoe_ffn_layer per layer, the chain
-    for each T replayed from one captured HIP graph), beside the same T tokens
-    decoded one launch each by the persistent decode stack."""
+    """the verify batch of speculative decoding, T = n_draft + 1
+    tokens (1..--tokens) per step through the configs[1] stack (48 Q4_K layers of
+    the 30B-A3B shape), the T tokens' activations N(0,1) correlated at rho = 0.8
+    so that their experts partly overlap.  qwmoe_layer_stack runs 2 <= T <= 8 as
+    one persistent launch (verify_xcd.hip) where the device allows; beside it the
+    per-layer chain (the same stack created with QWMOE_VERIFY_XCD=0: one captured
+    graph of five launches per layer, bitwise compared) and the T tokens decoded
+    one launch each by the persistent decode stack."""
     import numpy as np
     import torch
     from questwend_amd import Q4_K, ops, row_size
@@ -567,21 +571,39 @@ def verify_bench(args) -> int:
     Ls = [ops.make_layer(H, E, K_USED, F, r, g, u, d, (Q4_K,) * 3) for (r, g, u, d) in layers]
     Tmax = max(1, args.tokens)
     stack = ops.LayerStack(Ls, RMS_EPS, max_tokens=Tmax, keepalive=layers)
-    eager = ops.LayerStack(Ls, RMS_EPS, max_tokens=Tmax, graphs=False, keepalive=layers)
+    old = os.environ.get("QWMOE_VERIFY_XCD")
+    os.environ["QWMOE_VERIFY_XCD"] = "0"
+    try:
+        chain = ops.LayerStack(Ls, RMS_EPS, max_tokens=Tmax, keepalive=layers)
+    finally:
+        if old is None:
+            os.environ.pop("QWMOE_VERIFY_XCD")
+        else:
+            os.environ["QWMOE_VERIFY_XCD"] = old
     dstack = ops.DecodeStack(Ls, RMS_EPS, keepalive=layers)
-    xs = torch.empty((args.steps + args.warmup, Tmax, H), dtype=torch.float32, device="cuda:0")
-    ops.randn_(xs, args.seed + 999, 0.0, 1.0)
+    n = args.steps + args.warmup
+    c = torch.empty((n, 1, H), dtype=torch.float32, device="cuda:0")
+    z = torch.empty((n, Tmax, H), dtype=torch.float32, device="cuda:0")
+    ops.randn_(c, args.seed + 998, 0.0, 1.0)
+    ops.randn_(z, args.seed + 999, 0.0, 1.0)
+    xs = (c * math.sqrt(0.8) + z * math.sqrt(0.2)).contiguous()
     expert = 2 * F * row_size(Q4_K, H) + H * row_size(Q4_K, F)
 
-    def timed(fn, T):
+    def timed(fn, T, events=False):
         for i in range(args.warmup):
             fn(xs[i, :T])
         torch.cuda.synchronize()
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
         t0 = time.perf_counter()
         for i in range(args.steps):
+            if events:
+                evs[i][0].record()
             fn(xs[args.warmup + i, :T])
+            if events:
+                evs[i][1].record()
         torch.cuda.synchronize()
-        return (time.perf_counter() - t0) / args.steps
+        wall = (time.perf_counter() - t0) / args.steps
+        return wall, (sum(a_.elapsed_time(b_) for a_, b_ in evs) / args.steps / 1e3 if events else None)
 
     def dec(x):
         for t in range(x.shape[0]):
@@ -589,42 +611,51 @@ def verify_bench(args) -> int:
 
     rows, same = [], True
     for T in range(1, Tmax + 1):
-        g_s = timed(lambda x: stack(x, want_ids=False), T)
-        e_s = timed(lambda x: eager(x, want_ids=False), T)
-        d_s = timed(dec, T)
-        o, _, ids, _ = stack(xs[0, :T])
-        o2, _, _, _ = eager(xs[0, :T])
-        torch.cuda.synchronize()
-        same &= bool(torch.equal(o.view(torch.int32), o2.view(torch.int32)))
-        uniq = sum(len(np.unique(ids[l].cpu().numpy())) for l in range(N_LAYER))
+        g_s, k_s = timed(lambda x: stack(x, want_ids=False), T, events=True)
+        c_s, _ = timed(lambda x: chain(x, want_ids=False), T)
+        d_s, _ = timed(dec, T)
+        uniq = 0
+        for i in range(min(4, n)):
+            o, xo, ids, w = stack(xs[i, :T])
+            o2, xo2, ids2, w2 = chain(xs[i, :T])
+            torch.cuda.synchronize()
+            same &= bool(torch.equal(ids, ids2)) and all(
+                torch.equal(u.view(torch.int32), v.view(torch.int32)) for u, v in ((o, o2), (xo, xo2), (w, w2)))
+            uniq += sum(len(np.unique(ids[l].cpu().numpy())) for l in range(N_LAYER))
+        uniq /= min(4, n)
         wbytes = uniq * expert + N_LAYER * E * H * 4
-        rows.append({"T": T, "graph_ms": round(g_s * 1e3, 3), "eager_ms": round(e_s * 1e3, 3),
+        rows.append({"T": T, "ms": round(g_s * 1e3, 3), "avg_launch_ms": round(k_s * 1e3, 4),
+                     "per_layer_chain_ms": round(c_s * 1e3, 3),
                      "decode_stack_x_T_ms": round(d_s * 1e3, 3), "verify_tok_s": round(T / g_s, 1),
                      "unique_experts_per_layer": round(uniq / N_LAYER, 2),
-                     "weight_gbps": round(wbytes / g_s / 1e9, 1)})
+                     "weight_gbps": round(wbytes / k_s / 1e9, 1), "weight_bytes_per_step": int(wbytes)})
     last = rows[-1]
     cpu = None
     if not args.no_cpu_baseline:
         lws = [host_layer_weights(*ly, (Q4_K,) * 3, H, E, K_USED, F) for ly in layers]
         cpu = cpu_chain_baseline(lws, xs[:16].cpu().numpy(), Tmax, N_LAYER)
+    kname = {1: "the per-layer chain (captured graph)", 2: "k_verify_xcd<8,3,4> (XCD-local exchange words)",
+             3: "k_verify_xcd<8,3,4> (device-scope exchange words)"}.get(stack.kernel(), "?")
     line = {
         "metric": "verify-batch tok/s, 30B-A3B Q4_K MoE FFN stack (speculative-decoding verify forward, FFN half)",
         "value": last["verify_tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": last["graph_ms"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "q4_K x q8_K -> f32", "data": "synthetic (seeded)",
-        "config": {"workload": "configs[1] stack, T tokens per step through qwmoe_layer_stack", "n_layer": N_LAYER,
-                   "n_embd": H, "n_expert": E, "n_expert_used": K_USED, "n_ff_exp": F, "weights": "Q4_K",
-                   "tokens": Tmax},
+        "ms_per_step": last["ms"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q4_K x q8_K -> f32", "data": "synthetic (seeded; tokens N(0,1) correlated at rho = 0.8)",
+        "config": {"workload": "configs[3]: T tokens per step through the configs[1] stack (qwmoe_layer_stack)",
+                   "n_layer": N_LAYER, "n_embd": H, "n_expert": E, "n_expert_used": K_USED, "n_ff_exp": F,
+                   "weights": "Q4_K", "tokens": Tmax, "path_T_ge_2": kname},
         "per_T": rows,
-        "graph_equals_eager_bitwise": same,
+        "equals_per_layer_chain_bitwise": same,
         "roofline": {"bound": "hbm", "achieved": last["weight_gbps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(last["weight_gbps"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "note": "unique experts' weights + routers per step / step time"},
+                     "bytes_per_launch": last["weight_bytes_per_step"], "avg_launch_ms": last["avg_launch_ms"],
+                     "kernel": kname,
+                     "note": "the batch's distinct experts' weights + routers per step / average launch time (HIP events)"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
     stack.close()
-    eager.close()
+    chain.close()
     dstack.close()
     return 0
 

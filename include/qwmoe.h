@@ -348,6 +348,20 @@ void qwmoe_layer_stack_free(qwmoe_layer_stack * s);
  * diagnostic): a run captures again after qwmoe_init reallocated the workspace
  * or qwmoe_set_mfma_min_rows changed the threshold. */
 int64_t qwmoe_layer_stack_captures(const qwmoe_layer_stack * s);
+/* Which path a stack's runs at 2 <= T <= 8 take (no reference counterpart; the
+ * kernel choice only): 1 = the per-layer chain above (every T); 2 = one
+ * persistent launch for all layers (verify_xcd.hip: the batch's distinct experts
+ * dealt to the XCDs, each expert's rows loaded once for all its tokens), picked
+ * at creation on 256-CU devices when every layer has H = 2048, F = 768, E of 32,
+ * 64 or 128, k <= 8, Q4_K gate/up/down with 16-byte aligned rows, no resident
+ * mask and one expert_weights_scale; 3 = the same with every exchange word at
+ * device scope.  T = 1 always takes the per-layer chain.  QWMOE_VERIFY_XCD=0 in
+ * the environment at creation forces 1.  Results are identical. */
+int qwmoe_layer_stack_kernel(const qwmoe_layer_stack * s);
+/* Synchronises `stream`; the persistent launch's status bits (as
+ * qwmoe_decode_stack_status: 1 top-k tie replayed, 8 a wait timed out plus the
+ * exchange, 16 a slot out of range), 0 for the per-layer chain. */
+int qwmoe_layer_stack_status(void * stream, qwmoe_layer_stack * s, int32_t * status_out, int clear);
 
 /* ---- expert slot table (host) ------------------------------------------------ */
 

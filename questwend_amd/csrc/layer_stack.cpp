@@ -17,8 +17,11 @@
 #include <new>
 #include <vector>
 
+#include <cstdlib>
+
 #include "../../include/qwmoe.h"
 #include "qw_kernels.hpp"
+#include "qw_verify.hpp"
 
 struct qwmoe_layer_stack {
     std::vector<qwmoe_layer> layers;
@@ -35,12 +38,110 @@ struct qwmoe_layer_stack {
     std::vector<hipGraphExec_t> exec;    // [T]: the captured chain, or null
     std::vector<uint64_t> exec_gen;      // [T]: the library generation it was captured with
     int64_t captures = 0;                // graphs captured so far (a diagnostic)
+    // The persistent verify kernel (verify_xcd.hip) for 2 <= T <= VERIFY_TMAX, where
+    // the shape and device allow it: one launch for all layers.
+    const void* vfn = nullptr;
+    qw::VerifyArgs va{};                 // its arguments but the per-run ones
+    uint8_t* vblk = nullptr;             // layer table | exchange words | status, abort
+    uint32_t vepoch = 1;                 // next launch's first layer epoch
 
     ~qwmoe_layer_stack() {
         for (hipGraphExec_t e : exec)
             if (e) (void) hipGraphExecDestroy(e);
         if (cap) (void) hipStreamDestroy(cap);
         if (blk) (void) hipFree(blk);
+        if (vblk) (void) hipFree(vblk);
+    }
+
+    // Sets up the persistent verify kernel when every layer has the shape it
+    // takes (H = 2048, F = 768, E of 32, 64 or 128, k <= 8, Q4_K gate/up/down with
+    // 16-byte aligned rows, no resident mask, one expert_weights_scale) and the
+    // device has 256 CUs; QWMOE_VERIFY_XCD=0 in the environment turns it off.
+    // Leaves vfn null otherwise (the per-layer path serves every T).
+    int setup_verify() {
+        const char* env = getenv("QWMOE_VERIFY_XCD");
+        if (env && env[0] == '0') return QWMOE_OK;
+        const qwmoe_layer& L0 = layers[0];
+        for (const qwmoe_layer& L : layers) {
+            if (L.n_embd != L0.n_embd || L.n_ff != L0.n_ff || L.n_expert != L0.n_expert ||
+                L.n_expert_used != L0.n_expert_used || L.expert_weights_scale != L0.expert_weights_scale)
+                return QWMOE_OK;
+            if (L.type_gate != qw::T_Q4_K || L.type_up != qw::T_Q4_K || L.type_down != qw::T_Q4_K) return QWMOE_OK;
+            if (!L.router || !L.gate || !L.up || !L.down || L.resmask) return QWMOE_OK;
+            const uintptr_t al = (uintptr_t) L.gate | (uintptr_t) L.up | (uintptr_t) L.down | (uintptr_t) L.router |
+                                 (uintptr_t) L.gate_nb1 | (uintptr_t) L.gate_nb2 | (uintptr_t) L.up_nb1 |
+                                 (uintptr_t) L.up_nb2 | (uintptr_t) L.down_nb1 | (uintptr_t) L.down_nb2;
+            if (al & 15) return QWMOE_OK;
+            if (L.n_slots_gate <= 0 || L.n_slots_up <= 0 || L.n_slots_down <= 0) return QWMOE_OK;
+        }
+        if (L0.n_expert_used > 8 || max_T < 2) return QWMOE_OK;
+        const void* fn = qw::verify_xcd_kernel(L0.n_embd, L0.n_ff, L0.n_expert);
+        if (!fn) return QWMOE_OK;
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return QWMOE_ERR_HIP;
+        if (cus != 256 || qw::verify_xcd_occupancy(fn) != 0) return QWMOE_OK;
+        const int n = (int) layers.size();
+        auto a256 = [](size_t v) { return (v + 255) & ~(size_t) 255; };
+        const size_t o_xl = a256(sizeof(qw::DecodeLayer) * (size_t) n);
+        const size_t o_xa = o_xl + a256(8 * qw::verify_words_xl(L0.n_expert));
+        const size_t o_xd = o_xa + a256(8 * qw::verify_words_xa(L0.n_ff));
+        const size_t o_xy = o_xd + a256(8 * qw::verify_words_xd(L0.n_embd));
+        const size_t o_st = o_xy + a256(8 * qw::verify_words_xy(L0.n_embd));
+        const size_t total = o_st + 256;
+        if (hipMalloc(&vblk, total) != hipSuccess) {
+            vblk = nullptr;
+            (void) hipGetLastError();
+            return QWMOE_ERR_HIP;
+        }
+        std::vector<qw::DecodeLayer> host((size_t) n);
+        for (int l = 0; l < n; ++l) {
+            const qwmoe_layer& L = layers[(size_t) l];
+            qw::DecodeLayer& D = host[(size_t) l];
+            D = qw::DecodeLayer{};
+            D.router = L.router;
+            D.gate = (const uint8_t*) L.gate;
+            D.up = (const uint8_t*) L.up;
+            D.down = (const uint8_t*) L.down;
+            D.gate_nb1 = L.gate_nb1;
+            D.gate_nb2 = L.gate_nb2;
+            D.up_nb1 = L.up_nb1;
+            D.up_nb2 = L.up_nb2;
+            D.down_nb1 = L.down_nb1;
+            D.down_nb2 = L.down_nb2;
+            D.slot_gate = L.slot_gate;
+            D.slot_up = L.slot_up;
+            D.slot_down = L.slot_down;
+            D.n_slots_gate = L.n_slots_gate;
+            D.n_slots_up = L.n_slots_up;
+            D.n_slots_down = L.n_slots_down;
+        }
+        if (hipMemset(vblk, 0, total) != hipSuccess ||
+            hipMemcpy(vblk, host.data(), sizeof(qw::DecodeLayer) * (size_t) n, hipMemcpyHostToDevice) != hipSuccess)
+            return QWMOE_ERR_HIP;
+        // XCD-local words with workgroup scope only where the launch's workgroups
+        // are dealt to the XCDs round robin (the probe writes into the down words)
+        int ok = 0;
+        if (qw::probe_xcd_mapping((int32_t*) (vblk + o_xd), 256, nullptr, &ok) != 0) return QWMOE_ERR_HIP;
+        if (hipMemset(vblk + o_xd, 0, 256 * sizeof(int32_t)) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
+            return QWMOE_ERR_HIP;
+        const char* le = getenv("QWMOE_DECODE_XCD_LOCAL");
+        va = qw::VerifyArgs{};
+        va.layers = (const qw::DecodeLayer*) vblk;
+        va.n_layer = n;
+        va.k = (int) L0.n_expert_used;
+        va.scale = L0.expert_weights_scale;
+        va.rms_eps = rms_eps;
+        va.xl = (uint64_t*) (vblk + o_xl);
+        va.xa = (uint64_t*) (vblk + o_xa);
+        va.xd = (uint64_t*) (vblk + o_xd);
+        va.xy = (uint64_t*) (vblk + o_xy);
+        va.status = (int32_t*) (vblk + o_st);
+        va.abort_flag = (int32_t*) (vblk + o_st + 128);
+        va.local_st = (ok && !(le && le[0] == '0')) ? 1 : 0;
+        vfn = fn;
+        return QWMOE_OK;
     }
 
     // The chain for T tokens on stream st (eager, or recorded while capturing).
@@ -114,6 +215,11 @@ int qwmoe_layer_stack_create(const qwmoe_layer* layers, int n_layer, float rms_e
     s->ob = (float*) (s->blk + 2 * xs);
     s->ids = (int32_t*) (s->blk + 3 * xs);
     s->w = (float*) (s->blk + 3 * xs + is);
+    const int rc = s->setup_verify();
+    if (rc != QWMOE_OK) {
+        delete s;
+        return rc;
+    }
     *out = s;
     return QWMOE_OK;
 }
@@ -125,6 +231,20 @@ int qwmoe_layer_stack_run(void* stream, qwmoe_layer_stack* s, const float* x, in
     hipStream_t st = (hipStream_t) stream;
     const size_t xbytes = (size_t) T * (size_t) s->H * 4;
     const int n = (int) s->layers.size();
+    if (s->vfn && T >= 2 && T <= qw::VERIFY_TMAX) {
+        // the persistent kernel: the caller's buffers directly, one launch
+        if (s->vepoch > 0x7fffffffu - (uint32_t) n) return QWMOE_ERR_UNSUPPORTED;   // epoch space exhausted
+        qw::VerifyArgs a = s->va;
+        a.T = (int) T;
+        a.x_in = x;
+        a.out = out;
+        a.x_out = x_out;
+        a.ids_out = ids_out;
+        a.w_out = weights_out;
+        a.epoch0 = s->vepoch;
+        s->vepoch += (uint32_t) n;
+        return qw::launch_verify_xcd(s->vfn, a, st) == 0 ? QWMOE_OK : QWMOE_ERR_HIP;
+    }
     if (hipMemcpyAsync(s->xb[0], x, xbytes, hipMemcpyDeviceToDevice, st) != hipSuccess) return QWMOE_ERR_HIP;
     int rc;
     if (s->graphs) {
@@ -154,6 +274,23 @@ int qwmoe_layer_stack_run(void* stream, qwmoe_layer_stack* s, const float* x, in
 }
 
 int64_t qwmoe_layer_stack_captures(const qwmoe_layer_stack* s) { return s ? s->captures : -1; }
+
+int qwmoe_layer_stack_kernel(const qwmoe_layer_stack* s) {
+    if (!s) return QWMOE_ERR_INVALID_ARG;
+    return s->vfn ? (s->va.local_st ? 2 : 3) : 1;
+}
+
+int qwmoe_layer_stack_status(void* stream, qwmoe_layer_stack* s, int32_t* status_out, int clear) {
+    if (!s) return QWMOE_ERR_INVALID_ARG;
+    int32_t v = 0;
+    if (hipStreamSynchronize((hipStream_t) stream) != hipSuccess) return QWMOE_ERR_HIP;
+    if (s->vfn) {
+        if (hipMemcpy(&v, s->va.status, sizeof(v), hipMemcpyDeviceToHost) != hipSuccess) return QWMOE_ERR_HIP;
+        if (clear && hipMemset(s->va.status, 0, sizeof(int32_t)) != hipSuccess) return QWMOE_ERR_HIP;
+    }
+    if (status_out) *status_out = v;
+    return QWMOE_OK;
+}
 
 void qwmoe_layer_stack_free(qwmoe_layer_stack* s) {
     if (!s) return;

@@ -63,10 +63,12 @@ __device__ __forceinline__ void st_local(uint64_t* p, uint64_t v, int local) {
 }
 __device__ __forceinline__ uint64_t tag(float v, uint32_t ep) { return ((uint64_t) ep << 32) | (uint64_t) fbits(v); }
 
-__device__ __forceinline__ bool x_aborted(const XcdArgs& a) {
+template <class A>
+__device__ __forceinline__ bool x_aborted(const A& a) {
     return (uint32_t) __hip_atomic_load(a.abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= a.epoch0;
 }
-__device__ __forceinline__ void x_abort(const XcdArgs& a, int bit) {
+template <class A>
+__device__ __forceinline__ void x_abort(const A& a, int bit) {
     atomicOr(a.status, bit);
     __hip_atomic_store(a.abort_flag, (int32_t) a.epoch0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -92,8 +94,8 @@ __device__ __forceinline__ void all_loads_returned() { __builtin_amdgcn_s_waitcn
 // carries epoch ep, then stores the payloads to dst[i] (LDS).  A sweep reloads
 // every word of the thread and keeps the first payload seen with the epoch.
 // Returns false if the wait gave up.
-template <int MAXJ>
-__device__ __forceinline__ bool gather(const XcdArgs& a, const uint64_t* src, int n, uint32_t ep, float* dst,
+template <int MAXJ, class A>
+__device__ __forceinline__ bool gather(const A& a, const uint64_t* src, int n, uint32_t ep, float* dst,
                                        int tid, int where) {
     uint32_t got = 0;
     uint32_t val[MAXJ];

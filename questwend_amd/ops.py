@@ -360,6 +360,15 @@ class LayerStack(_Handle):
     def captures(self) -> int:
         return lib().qwmoe_layer_stack_captures(self.h)
 
+    def kernel(self) -> int:
+        """1: the per-layer chain; 2: one persistent launch for 2 <= T <= 8 (3: device-scope words)."""
+        return int(lib().qwmoe_layer_stack_kernel(self.h))
+
+    def status(self, clear: bool = True) -> int:
+        v = C.c_int32(0)
+        check(lib().qwmoe_layer_stack_status(stream(), self.h, C.byref(v), int(clear)), "layer_stack_status")
+        return v.value
+
     def _free(self) -> None:
         lib().qwmoe_layer_stack_free(self.h)
 
