@@ -440,7 +440,7 @@ def expert_cache_bench(args) -> int:
     dev = "cuda:0"
     layers = make_weights(torch, ops, Q4_K, args.seed)
     if args.zipf > 0:
-        sc = torch.from_numpy(zipf_row_scales(E, args.zipf)).to(dev)[:, None]
+        sc = torch.from_numpy(zipf_router_scales(E, K_USED, args.zipf)).to(dev)[:, None]
         for lay in layers:
             lay[0].mul_(sc)
     # the RAM tier: every expert tensor in pinned host memory
