@@ -325,15 +325,15 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
             int e_cur = spec_e;
             int4 my;
             float res, up;
+            const Q8KLane yv = q8k_lane(s_xq + QB * g, t);   // block g of Q8_K(x): the same for every row
             for (;;) {
 #pragma unroll
                 for (int r = 0; r < 2 * PPW; ++r) {
                     int p[4];
-                    const uint8_t* yb = s_xq + QB * g;
                     const Q4KLane w = q4k_lane(gh[r], gq[r], t);
-                    q4k_dot(w, yb, t, p);
+                    q4k_dot(w, yv, p);
                     reduce_chunks(p);
-                    const int pm = q4k_min_dot(w, yb, t);
+                    const int pm = q4k_min_dot(w, yv);
                     uint32_t* rec = s_tr[wave][r][g];
                     if ((t & 3) == 0) *(u32x4*) (rec + t) = u32x4{(uint32_t) p[0], (uint32_t) p[1], (uint32_t) p[2], (uint32_t) p[3]};
                     if (t < 4) rec[8 + t] = (uint32_t) pm;

@@ -342,6 +342,32 @@ __device__ __forceinline__ int q4k_min_dot(const Q4KLane& w, const uint8_t* yb, 
     return mul24(w.m0, q8s0) + mul24(w.m1, q8s1);
 }
 
+// The activation side of q4k_dot / q4k_min_dot in registers: lane t's 32 quant
+// bytes of a Q8_K block and its min lane's two sub-block sums.  Rows that share
+// the activation block (every gate/up row of a wave) read LDS once for all.
+struct Q8KLane {
+    u32x4 alo, ahi;
+    int q8s0, q8s1;
+};
+__device__ __forceinline__ Q8KLane q8k_lane(const uint8_t* yb, int t) {
+    Q8KLane y;
+    const int j = t & 3, hb = t >> 2, n = t & 3;
+    y.alo = *(const u32x4*) (yb + 64 * j + 16 * hb);
+    y.ahi = *(const u32x4*) (yb + 64 * j + 32 + 16 * hb);
+    const uint32_t bs01 = *(const uint32_t*) (yb + 260 + 8 * n), bs23 = *(const uint32_t*) (yb + 264 + 8 * n);
+    y.q8s0 = (int) (int16_t) (bs01 & 0xffff) + (int) (int16_t) (bs01 >> 16);
+    y.q8s1 = (int) (int16_t) (bs23 & 0xffff) + (int) (int16_t) (bs23 >> 16);
+    return y;
+}
+__device__ __forceinline__ void q4k_dot(const Q4KLane& w, const Q8KLane& y, int p[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        p[i] = mul24(w.scl, sdot4((int) w.lo[i], (int) y.alo[i], 0)) + mul24(w.sch, sdot4((int) w.hi[i], (int) y.ahi[i], 0));
+}
+__device__ __forceinline__ int q4k_min_dot(const Q4KLane& w, const Q8KLane& y) {
+    return mul24(w.m0, y.q8s0) + mul24(w.m1, y.q8s1);
+}
+
 // Sum over the four 64-element chunks: lanes t ^ 1, then t ^ 2 (quad_perm; the
 // sums are exact integers).  Every lane of a half ends with the sums of its AVX
 // lanes 4 hb .. 4 hb + 3.

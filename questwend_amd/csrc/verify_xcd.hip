@@ -343,14 +343,14 @@ __global__ void __launch_bounds__(XT) k_verify_xcd(VerifyArgs a) {
             for (uint32_t rem = tm; rem; rem &= rem - 1u) {
                 const int tk = __builtin_ctz(rem);
                 const uint8_t* xq = s_xq[tk];
+                const Q8KLane yv = q8k_lane(xq + QB * g, t8);   // block g of the token's Q8_K(x), for every row
 #pragma unroll
                 for (int r = 0; r < 2 * PPW; ++r) {
                     int p[4];
-                    const uint8_t* yb = xq + QB * g;
                     const Q4KLane w = q4k_lane(gh[r], gq[r], t8);
-                    q4k_dot(w, yb, t8, p);
+                    q4k_dot(w, yv, p);
                     reduce_chunks(p);
-                    const int pm = q4k_min_dot(w, yb, t8);
+                    const int pm = q4k_min_dot(w, yv);
                     uint32_t* rec = s_tr + ((wave * 2 * PPW + r) * NBH + g) * 16;
                     if ((t8 & 3) == 0) *(u32x4*) (rec + t8) = u32x4{(uint32_t) p[0], (uint32_t) p[1], (uint32_t) p[2], (uint32_t) p[3]};
                     if (t8 < 4) rec[8 + t8] = (uint32_t) pm;
