@@ -99,6 +99,88 @@ __global__ void __launch_bounds__(32 * EPW) k_router_logits(const float* __restr
     }
 }
 
+// The same logits for large batches (prefill): lane c of a 32-lane group runs
+// chain c for EL experts x TL tokens at once, so one step's EL + TL loads feed
+// EL * TL fmas (k_router_logits loads x once per expert and W once per ROUTER_TT
+// tokens).  Eight groups per workgroup: two expert subtiles x four token
+// subtiles, a tile of 2 EL experts x 4 TL tokens.  Each chain's fmas run in
+// step order as before, so the logits are the same bits.
+template <int EL, int TL, int STEPS>
+__global__ void __launch_bounds__(256) k_router_logits_tile(const float* __restrict__ W, const float* __restrict__ x,
+                                                            int64_t x_stride, int64_t H, int64_t E, int64_t T,
+                                                            float* __restrict__ logits) {
+    const int c = threadIdx.x & 31, gi = threadIdx.x >> 5;
+    const int64_t e0 = (int64_t) blockIdx.x * (2 * EL) + (gi & 1) * EL;
+    const int64_t t0 = (int64_t) blockIdx.y * (4 * TL) + (gi >> 1) * TL;
+    const int64_t np = H & ~(int64_t) 31;
+    const int64_t ns = np / 32;
+    const float* wr[EL];
+    const float* xr[TL];
+#pragma unroll
+    for (int i = 0; i < EL; ++i) wr[i] = W + (e0 + i < E ? e0 + i : 0) * H + c;
+#pragma unroll
+    for (int j = 0; j < TL; ++j) xr[j] = x + (t0 + j < T ? t0 + j : T - 1) * x_stride + c;
+    float acc[EL][TL];
+#pragma unroll
+    for (int i = 0; i < EL; ++i)
+#pragma unroll
+        for (int j = 0; j < TL; ++j) acc[i][j] = 0.0f;
+    float wv[STEPS][EL], xv[STEPS][TL];
+    auto load = [&](int64_t s0, float (*wd)[EL], float (*xd)[TL]) {
+#pragma unroll
+        for (int u = 0; u < STEPS; ++u) {
+            const int64_t s = (s0 + u < ns ? s0 + u : ns - 1) * 32;   // (past the end: never accumulated)
+#pragma unroll
+            for (int i = 0; i < EL; ++i) wd[u][i] = wr[i][s];
+#pragma unroll
+            for (int j = 0; j < TL; ++j) xd[u][j] = xr[j][s];
+        }
+    };
+    if (ns > 0) load(0, wv, xv);
+    for (int64_t s0 = 0; s0 < ns; s0 += STEPS) {
+        float wn[STEPS][EL], xn[STEPS][TL];
+        const bool more = s0 + STEPS < ns;
+        if (more) load(s0 + STEPS, wn, xn);
+#pragma unroll
+        for (int u = 0; u < STEPS; ++u)
+            if (s0 + u < ns) {
+#pragma unroll
+                for (int i = 0; i < EL; ++i)
+#pragma unroll
+                    for (int j = 0; j < TL; ++j) acc[i][j] = __builtin_fmaf(wv[u][i], xv[u][j], acc[i][j]);
+            }
+        if (more) {
+#pragma unroll
+            for (int u = 0; u < STEPS; ++u) {
+#pragma unroll
+                for (int i = 0; i < EL; ++i) wv[u][i] = wn[u][i];
+#pragma unroll
+                for (int j = 0; j < TL; ++j) xv[u][j] = xn[u][j];
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < EL; ++i)
+#pragma unroll
+        for (int j = 0; j < TL; ++j) {
+            // GGML_F32x8_REDUCE and the scalar tail, as in k_router_logits
+            float v = acc[i][j] + __shfl_down(acc[i][j], 16, 32);
+            v = v + __shfl_down(v, 8, 32);
+            v = v + __shfl_down(v, 4, 32);
+            const float u = v + __shfl_down(v, 1, 32);
+            float sumf = u + __shfl_down(u, 2, 32);
+            const int64_t e = e0 + i, t = t0 + j;
+            if (c == 0 && e < E && t < T) {
+                const float* we = W + e * H;
+                const float* xt = x + t * x_stride;
+                const int64_t nv = np + ((H - np) & ~(int64_t) 3);
+                for (int64_t h = np; h < H; ++h)
+                    sumf = (h < nv) ? sumf + we[h] * xt[h] : __builtin_fmaf(we[h], xt[h], sumf);
+                logits[t * E + e] = sumf;
+            }
+        }
+}
+
 // Softmax, exact top-k and weight normalisation for one token per 64-thread
 // workgroup.  Supports E % 8 == 0 and E <= 64 * ROUTER_EPL.
 constexpr int ROUTER_EPL = 8;
@@ -127,9 +209,10 @@ int launch_router(const RouterArgs& a, float* logits_ws, hipStream_t stream) {
         hipLaunchKernelGGL((k_router_logits<1, 2, 32>), g1, dim3(64), 0, stream, a.W, a.x, a.x_stride, a.H, a.E, a.T,
                            logits, (BlockQ8_K*) a.xq);
     } else {
-        dim3 g1((unsigned) ((a.E + 7) / 8), (unsigned) ((a.T + 3) / 4));
-        hipLaunchKernelGGL((k_router_logits<4, 8, 16>), g1, dim3(256), 0, stream, a.W, a.x, a.x_stride, a.H, a.E, a.T,
-                           logits, (BlockQ8_K*) nullptr);
+        constexpr int EL = 4, TL = 4;
+        dim3 g1((unsigned) ((a.E + 2 * EL - 1) / (2 * EL)), (unsigned) ((a.T + 4 * TL - 1) / (4 * TL)));
+        hipLaunchKernelGGL((k_router_logits_tile<EL, TL, 8>), g1, dim3(256), 0, stream, a.W, a.x, a.x_stride, a.H, a.E,
+                           a.T, logits);
     }
     if (!a.ids) return hipGetLastError() == hipSuccess ? 0 : -3;   // logits only (top-k fused elsewhere)
     hipLaunchKernelGGL(k_router_topk, dim3((unsigned) a.T), dim3(64), 0, stream, logits, a.E, a.k, a.T, a.clamp_min,
