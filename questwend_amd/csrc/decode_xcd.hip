@@ -335,9 +335,13 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
                     reduce_chunks(p);
                     const int pm = q4k_min_dot(w, yv);
                     uint32_t* rec = s_tr[wave][r][g];
-                    if ((t & 3) == 0) *(u32x4*) (rec + t) = u32x4{(uint32_t) p[0], (uint32_t) p[1], (uint32_t) p[2], (uint32_t) p[3]};
-                    if (t < 4) rec[8 + t] = (uint32_t) pm;
-                    if (t == 0) *(uint2*) (rec + 12) = uint2{fbits(w.d), fbits(w.dmin)};
+                    // every lane stores two words, no lane-conditional stores: rec[t] = AVX
+                    // lane t's sum, rec[8 + t] = min lane t's term (t < 4), d (t = 4), dmin (t = 5)
+                    const int q = t & 3;
+                    const int pt = q == 0 ? p[0] : q == 1 ? p[1] : q == 2 ? p[2] : p[3];
+                    const uint32_t w2 = t < 4 ? (uint32_t) pm : t == 4 ? fbits(w.d) : fbits(w.dmin);
+                    rec[t] = (uint32_t) pt;
+                    rec[8 + t] = w2;
                 }
                 wave_lds_sync();
                 // chain lanes: row r = lane >> 3 (< 2 * PPW), AVX lane n = lane & 7

@@ -352,9 +352,12 @@ __global__ void __launch_bounds__(XT) k_verify_xcd(VerifyArgs a) {
                     reduce_chunks(p);
                     const int pm = q4k_min_dot(w, yv);
                     uint32_t* rec = s_tr + ((wave * 2 * PPW + r) * NBH + g) * 16;
-                    if ((t8 & 3) == 0) *(u32x4*) (rec + t8) = u32x4{(uint32_t) p[0], (uint32_t) p[1], (uint32_t) p[2], (uint32_t) p[3]};
-                    if (t8 < 4) rec[8 + t8] = (uint32_t) pm;
-                    if (t8 == 0) *(uint2*) (rec + 12) = uint2{fbits(w.d), fbits(w.dmin)};
+                    // every lane stores two words (rec[t8] = AVX lane t8's sum, rec[8 + t8] = min
+                    // lane t8's term, d, dmin): no lane-conditional stores
+                    const int q = t8 & 3;
+                    const int pt = q == 0 ? p[0] : q == 1 ? p[1] : q == 2 ? p[2] : p[3];
+                    rec[t8] = (uint32_t) pt;
+                    rec[8 + t8] = t8 < 4 ? (uint32_t) pm : t8 == 4 ? fbits(w.d) : fbits(w.dmin);
                 }
                 wave_lds_sync();
                 // chain lanes: row r = lane >> 3 (< 2 PPW), AVX lane n = lane & 7
