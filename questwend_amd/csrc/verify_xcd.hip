@@ -74,7 +74,8 @@ __global__ void __launch_bounds__(XT) k_verify_xcd(VerifyArgs a) {
     constexpr int NH = H / NJ;            // down rows per workgroup
     constexpr int RW = NH / XW;           // down rows per wave (one per 8-lane group)
     constexpr int RW0 = XW - (NLOG + 1) / 2;   // first router wave (two logits per router wave)
-    constexpr int NTR = XW * 2 * PPW * NBH * 16;    // words of the gate/up block records
+    constexpr int TRS = NBH * 16 + 8;               // words per record row (8 past a multiple of the 64 banks)
+    constexpr int NTR = XW * 2 * PPW * TRS;         // words of the gate/up block records
     static_assert(NBH == 8, "gate/up rows: one super-block per 8-lane group");
     static_assert(PPW >= 1 && PPW * XW == NP && 2 * PPW * 8 <= 64, "pairs per wave");
     static_assert(RW == 8 && NH == 64, "down rows: one row per 8-lane group; y: one row per lane");
@@ -86,7 +87,7 @@ __global__ void __launch_bounds__(XT) k_verify_xcd(VerifyArgs a) {
     // during a layer the same memory holds the gate/up block records, the act rows
     // of one slot and their Q8_K
     __shared__ __align__(16) float s_big[VTM * H];
-    uint32_t* const s_tr = (uint32_t*) s_big;                     // [XW][2 PPW][NBH][16]
+    uint32_t* const s_tr = (uint32_t*) s_big;                     // [XW][2 PPW][TRS]: 16 words per block
     float* const s_act = s_big + NTR;                             // [VTM][F] (the slot's tokens in order)
     uint8_t* const s_aq = (uint8_t*) (s_act + VTM * F);           // [VTM][NBF * QB]
     __shared__ __align__(16) uint8_t s_xq[VTM][NBH * QB];         // Q8_K(x) per token
@@ -351,7 +352,7 @@ __global__ void __launch_bounds__(XT) k_verify_xcd(VerifyArgs a) {
                     q4k_dot(w, yv, p);
                     reduce_chunks(p);
                     const int pm = q4k_min_dot(w, yv);
-                    uint32_t* rec = s_tr + ((wave * 2 * PPW + r) * NBH + g) * 16;
+                    uint32_t* rec = s_tr + (wave * 2 * PPW + r) * TRS + 16 * g;
                     // every lane stores two words (rec[t8] = AVX lane t8's sum, rec[8 + t8] = min
                     // lane t8's term, d, dmin): no lane-conditional stores
                     const int q = t8 & 3;
@@ -367,7 +368,7 @@ __global__ void __launch_bounds__(XT) k_verify_xcd(VerifyArgs a) {
                     float acc = 0.0f, accm = 0.0f;
 #pragma unroll
                     for (int bb = 0; bb < NBH; ++bb) {
-                        const uint32_t* rec = s_tr + ((wave * 2 * PPW + r) * NBH + bb) * 16;
+                        const uint32_t* rec = s_tr + (wave * 2 * PPW + r) * TRS + 16 * bb;
                         const int S = (int) rec[n];
                         const int pm = (int) rec[8 + (n & 3)];
                         const float wd = bitsf(rec[12]), wdm = bitsf(rec[13]);
