@@ -707,7 +707,11 @@ def config5_bench(args) -> int:
     # kernel (its wide XCD form: one launch per token) and, beside it, on the
     # layer stack at T = 1 (five launches per layer, one captured graph)
     dstack = ops.DecodeStack(layers, RMS_EPS, keepalive=keep)
-    stack = ops.LayerStack(layers, RMS_EPS, max_tokens=1, keepalive=keep)
+    os.environ["QWMOE_VERIFY_XCD"] = "0"   # the chain (by default the layer stack hands T = 1 to the decode kernel)
+    try:
+        stack = ops.LayerStack(layers, RMS_EPS, max_tokens=1, keepalive=keep)
+    finally:
+        os.environ.pop("QWMOE_VERIFY_XCD", None)
     xs = torch.empty((args.steps + args.warmup, 1, H5), dtype=torch.float32, device=dev)
     ops.randn_(xs, args.seed + 4242, 0.0, 1.0)
     # the two paths on the first 8 tokens: ids, weights and outputs bitwise

@@ -355,10 +355,14 @@ int64_t qwmoe_layer_stack_captures(const qwmoe_layer_stack * s);
  * at creation on 256-CU devices when every layer has H = 2048, F = 768, E of 32,
  * 64 or 128, k <= 8, Q4_K gate/up/down with 16-byte aligned rows, no resident
  * mask and one expert_weights_scale; 3 = the same with every exchange word at
- * device scope.  T = 1 always takes the per-layer chain.  QWMOE_VERIFY_XCD=0 in
- * the environment at creation forces 1.  Results are identical. */
+ * device scope.  T = 1 runs on the whole-stack decode kernel
+ * (qwmoe_decode_stack_*, one launch per token) wherever qwmoe_decode_stack_create
+ * takes the stack's layers, else on the per-layer chain.  QWMOE_VERIFY_XCD=0 in
+ * the environment at creation forces the per-layer chain for every T (1).
+ * Results are identical. */
 int qwmoe_layer_stack_kernel(const qwmoe_layer_stack * s);
-/* Synchronises `stream`; the persistent launch's status bits (as
+/* Synchronises `stream`; the persistent launches' status bits (those of the
+ * T >= 2 kernel or'ed with the T = 1 decode kernel's, as
  * qwmoe_decode_stack_status: 1 top-k tie replayed, 8 a wait timed out plus the
  * exchange, 16 a slot out of range), 0 for the per-layer chain. */
 int qwmoe_layer_stack_status(void * stream, qwmoe_layer_stack * s, int32_t * status_out, int clear);

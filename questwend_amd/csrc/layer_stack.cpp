@@ -44,8 +44,12 @@ struct qwmoe_layer_stack {
     qw::VerifyArgs va{};                 // its arguments but the per-run ones
     uint8_t* vblk = nullptr;             // layer table | exchange words | status, abort
     uint32_t vepoch = 1;                 // next launch's first layer epoch
+    // T = 1: the whole-stack decode kernel (qwmoe_decode_stack_*), one launch per
+    // token, where it takes this stack's layers; the same bits as the chain
+    qwmoe_decode_stack* ds = nullptr;
 
     ~qwmoe_layer_stack() {
+        if (ds) qwmoe_decode_stack_free(ds);
         for (hipGraphExec_t e : exec)
             if (e) (void) hipGraphExecDestroy(e);
         if (cap) (void) hipStreamDestroy(cap);
@@ -220,6 +224,14 @@ int qwmoe_layer_stack_create(const qwmoe_layer* layers, int n_layer, float rms_e
         delete s;
         return rc;
     }
+    // runs at T = 1 go to the decode stack where it takes these layers (it leaves
+    // *out null otherwise, and the chain serves T = 1); QWMOE_VERIFY_XCD=0 keeps
+    // the chain for every T
+    const char* env = getenv("QWMOE_VERIFY_XCD");
+    if (!(env && env[0] == '0') && qwmoe_decode_stack_create(layers, n_layer, rms_eps, &s->ds) != QWMOE_OK) {
+        s->ds = nullptr;
+        (void) hipGetLastError();
+    }
     *out = s;
     return QWMOE_OK;
 }
@@ -228,6 +240,7 @@ int qwmoe_layer_stack_run(void* stream, qwmoe_layer_stack* s, const float* x, in
                           int32_t* ids_out, float* weights_out) {
     if (!s || !x || !out || T <= 0 || T > s->max_T) return QWMOE_ERR_INVALID_ARG;
     if ((ids_out == nullptr) != (weights_out == nullptr)) return QWMOE_ERR_INVALID_ARG;
+    if (T == 1 && s->ds) return qwmoe_decode_stack_run(stream, s->ds, x, out, x_out, ids_out, weights_out);
     hipStream_t st = (hipStream_t) stream;
     const size_t xbytes = (size_t) T * (size_t) s->H * 4;
     const int n = (int) s->layers.size();
@@ -287,6 +300,12 @@ int qwmoe_layer_stack_status(void* stream, qwmoe_layer_stack* s, int32_t* status
     if (s->vfn) {
         if (hipMemcpy(&v, s->va.status, sizeof(v), hipMemcpyDeviceToHost) != hipSuccess) return QWMOE_ERR_HIP;
         if (clear && hipMemset(s->va.status, 0, sizeof(int32_t)) != hipSuccess) return QWMOE_ERR_HIP;
+    }
+    if (s->ds) {
+        int32_t vd = 0;
+        const int rc = qwmoe_decode_stack_status(stream, s->ds, &vd, clear);
+        if (rc != QWMOE_OK) return rc;
+        v |= vd;
     }
     if (status_out) *status_out = v;
     return QWMOE_OK;

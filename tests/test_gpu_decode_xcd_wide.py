@@ -129,7 +129,11 @@ def test_wide_kernel_device_scope_and_layer_stack_same_bits():
     s4 = make_stack(descs, layers)
     s5 = make_stack(descs, layers, {"QWMOE_DECODE_XCD_LOCAL": "0"})
     assert (s4.kernel(), s5.kernel()) == (4, 5)
-    ls = ops.LayerStack(descs, 1e-6, max_tokens=1, keepalive=layers)
+    os.environ["QWMOE_VERIFY_XCD"] = "0"   # the per-layer chain at T = 1, not the decode kernel again
+    try:
+        ls = ops.LayerStack(descs, 1e-6, max_tokens=1, keepalive=layers)
+    finally:
+        os.environ.pop("QWMOE_VERIFY_XCD", None)
     for t, x in enumerate(tokens(24, 4)):
         xd = torch.from_numpy(x).to(DEV)
         r4, r5 = s4(xd), s5(xd)

@@ -17,6 +17,7 @@ layer's RMSNorm output as the GPU computed it.
 """
 from __future__ import annotations
 
+import os
 import sys
 
 import numpy as np
@@ -188,7 +189,11 @@ def test_config4_94_layers_slot_tables():
     # (one launch per token; its wide XCD form on a 256-CU device)
     for name in ("layer stack", "decode stack"):
         if name == "layer stack":
-            stack = ops.LayerStack(layers, EPS, max_tokens=1, keepalive=keep)
+            os.environ["QWMOE_VERIFY_XCD"] = "0"   # the per-layer chain (T = 1 otherwise runs on the decode kernel)
+            try:
+                stack = ops.LayerStack(layers, EPS, max_tokens=1, keepalive=keep)
+            finally:
+                os.environ.pop("QWMOE_VERIFY_XCD", None)
         else:
             stack = ops.DecodeStack(layers, EPS, keepalive=keep)
             note(f"  decode stack kernel {stack.kernel()}")

@@ -15,6 +15,8 @@ the FFN half of speculative decoding's verify forward (core/runtime.cpp:1495-156
 """
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 
@@ -102,7 +104,11 @@ def test_layer_stack_t1_equals_decode_stack():
     note("layer stack T=1 vs decode stack: 2 layers of the 30B shape (H=2048 E=128 k=8 F=768 Q4_K)")
     layers = [GpuLayer(2048, 128, 8, 768, (Q4_K,) * 3, seed=800 + i) for i in range(2)]
     Ls = [g.layer for g in layers]
-    stack = ops.LayerStack(Ls, 1e-6, max_tokens=1, keepalive=layers)
+    os.environ["QWMOE_VERIFY_XCD"] = "0"   # the per-layer chain at T = 1 (the default hands T = 1 to the decode stack)
+    try:
+        stack = ops.LayerStack(Ls, 1e-6, max_tokens=1, keepalive=layers)
+    finally:
+        os.environ.pop("QWMOE_VERIFY_XCD", None)
     dstack = ops.DecodeStack(Ls, 1e-6, keepalive=layers)
     rng = np.random.default_rng(3)
     for t in range(4):

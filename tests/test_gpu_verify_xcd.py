@@ -130,7 +130,7 @@ def test_verify_kernel_k4_scale_e32(orc):
 def test_verify_kernel_equals_per_layer_chain():
     """8 layers of the 30B shape, T = 5 correlated tokens, 6 steps: the
     persistent kernel (XCD-local and device-scope words) and the per-layer chain
-    give the same bits, and T = 1 (always the chain) still runs."""
+    give the same bits, and at T = 1 the stack (on the decode kernel) equals the chain."""
     note("verify kernel vs device-scope form vs per-layer chain: 8 layers, T=5, 6 steps")
     layers = [GpuLayer(H, 128, 8, F, (Q4_K,) * 3, seed=1160 + i, permute=(i % 3 == 0)) for i in range(8)]
     s2 = make_stack(layers)
