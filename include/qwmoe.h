@@ -90,12 +90,16 @@ int qwmoe_get_mfma_min_rows(void);
  *       and up: SwiGLU, then Q8_K for the down projection) can then move a Q8_K
  *       value that sat at a rounding boundary by one step, which moves that
  *       token's layer output by up to ~1.5e-3 of its magnitude;
- *   QWMOE_MFMA_AUTO (default): the exact form wherever the output may be
- *       re-quantized -- qwmoe_mul_mat_id (its consumer is the caller's) and the
- *       gate/up projections of qwmoe_ffn_layer, qwmoe_shared_expert_add and the
- *       layer stacks -- and the block-sum form for their down projections, whose
- *       fp32 outputs only reach the weighted sum.  Layer outputs stay within
- *       ~1e-6 of ggml's.
+ *   QWMOE_MFMA_AUTO: the exact form for qwmoe_mul_mat_id and for the gate/up
+ *       projections of qwmoe_ffn_layer, qwmoe_shared_expert_add and the layer
+ *       stacks; the block-sum form for their down projections.  The layer
+ *       output then differs from ggml's in the last bits (~1e-6 of its
+ *       magnitude), and since the next layer and its router re-quantize that
+ *       output to Q8_K, the difference can move a Q8_K value, and over many
+ *       layers a top-k choice, as in QWMOE_MFMA_BLOCK_SUM.
+ * The default is QWMOE_MFMA_EXACT: every result is ggml's bits.  The other
+ * forms are opt-in speed settings for callers that accept that drift (a T = 8
+ * verify batch under them need not give the bits of eight T = 1 decodes).
  * Captured layer-stack graphs are re-captured when the setting changes. */
 enum { QWMOE_MFMA_BLOCK_SUM = 0, QWMOE_MFMA_EXACT = 1, QWMOE_MFMA_AUTO = 2 };
 int qwmoe_set_mfma_form(int form);
@@ -299,7 +303,14 @@ int qwmoe_ffn_layer(void * stream, const qwmoe_layer * layer, const float * x, i
 typedef struct qwmoe_decode_stack qwmoe_decode_stack;
 int qwmoe_decode_stack_create(const qwmoe_layer * layers, int n_layer, float rms_eps, qwmoe_decode_stack ** out);
 /* One token: x [H] -> out [H] (MoE output of the last layer) and, when
- * non-NULL, x_out [H] = rms_norm(out); ids_out / weights_out [n_layer][k]. */
+ * non-NULL, x_out [H] = rms_norm(out); ids_out / weights_out [n_layer][k].
+ * The kernel is persistent: every workgroup must be resident at once, so the
+ * launch must not share the device with other work that holds CUs (a
+ * workgroup that waits too long gives up: status bit 8, outputs invalid, the
+ * call itself still returns QWMOE_OK -- check qwmoe_decode_stack_status).
+ * Each launch takes a fresh exchange epoch from the host, so a launch recorded
+ * under stream capture could not be replayed: on a capturing stream the call
+ * returns QWMOE_ERR_UNSUPPORTED and enqueues nothing. */
 int qwmoe_decode_stack_run(void * stream, qwmoe_decode_stack * s, const float * x, float * out, float * x_out,
                            int32_t * ids_out, float * weights_out);
 /* Synchronises `stream`; status bits: 1 top-k tie replayed, 8 a wait timed out
@@ -340,7 +351,15 @@ int qwmoe_layer_stack_create(const qwmoe_layer * layers, int n_layer, float rms_
                              qwmoe_layer_stack ** out);
 /* x [T][H] -> out [T][H] (MoE output of the last layer), x_out [T][H] (its
  * RMSNorm, may be NULL), ids_out / weights_out [n_layer][T][k] (both or none).
- * 1 <= T <= max_tokens. */
+ * 1 <= T <= max_tokens.  Runs at T = 1 and 2 <= T <= 8 may take persistent
+ * kernels (qwmoe_layer_stack_kernel, qwmoe_layer_stack_kernel_t1), with the
+ * decode stack's rule: they need every CU, and a wait that gives up leaves the
+ * outputs invalid while the call returns QWMOE_OK -- the status bits then
+ * appear in qwmoe_layer_stack_status (not in qwmoe_device_status, which the
+ * per-layer chain uses for bad slots).  The T = 1 decode stack is created at
+ * the first T = 1 run.  On a capturing stream (HIP graph capture) every T runs
+ * the per-layer chain, which the caller's graph records; that recording holds
+ * the library workspace's addresses, so re-capture after qwmoe_init. */
 int qwmoe_layer_stack_run(void * stream, qwmoe_layer_stack * s, const float * x, int64_t T, float * out,
                           float * x_out, int32_t * ids_out, float * weights_out);
 void qwmoe_layer_stack_free(qwmoe_layer_stack * s);
@@ -361,6 +380,11 @@ int64_t qwmoe_layer_stack_captures(const qwmoe_layer_stack * s);
  * the environment at creation forces the per-layer chain for every T (1).
  * Results are identical. */
 int qwmoe_layer_stack_kernel(const qwmoe_layer_stack * s);
+/* The kernel a T = 1 run takes outside capture (no reference counterpart):
+ * qwmoe_decode_stack_kernel's value for the stack's private decode stack
+ * (created here if no T = 1 run has created it yet), or 0 for the per-layer
+ * chain (shapes the decode stack does not take, or QWMOE_VERIFY_XCD=0). */
+int qwmoe_layer_stack_kernel_t1(qwmoe_layer_stack * s);
 /* Synchronises `stream`; the persistent launches' status bits (those of the
  * T >= 2 kernel or'ed with the T = 1 decode kernel's, as
  * qwmoe_decode_stack_status: 1 top-k tie replayed, 8 a wait timed out plus the
@@ -555,7 +579,8 @@ int qwmoe_expert_cache_verify(qwmoe_expert_cache * c, const int32_t * ids, int n
 /* The resident-decode mask (decode_cached_fast's fill_resmask, core/runtime.cpp:
  * 2900-2919): mask [n_layer][n_expert] gets 0 for an expert resident in all
  * three roles and -inf otherwise; a layer with fewer than floor_res residents
- * is left unmasked (all 0).  Returns 1 when every layer is masked ("complete":
+ * is left unmasked (all 0).  floor_res below n_expert_used counts as n_expert_used
+ * (a thinner mask would let top-k pick absent experts).  Returns 1 when every layer is masked ("complete":
  * the masked decode cannot miss), 0 otherwise.  mask_dev (optional, device):
  * the same values copied there on the cache's stream before returning -- the
  * layers' resmask rows point into it. */

@@ -13,19 +13,33 @@
 #ifndef QWMOE_GGML_H
 #define QWMOE_GGML_H
 
+#include <stdint.h>
+
 #include "qwmoe.h"
 
-/* Whether the op is a mul_mat_id libqwmoe takes: Q4_K / Q6_K / Q8_0 experts
- * with whole blocks per row, f32 activations and output with contiguous rows,
- * i32 ids, no fourth dimension. */
+/* Whether the op is a mul_mat_id libqwmoe takes -- exactly the nodes
+ * qwmoe_mul_mat_id accepts, so a scheduler that asks first never sees the call
+ * fail: Q4_K / Q6_K experts with K a multiple of 256 or Q8_0 with K a multiple
+ * of 64, f32 activations whose rows broadcast as ggml's e % ne11 with
+ * ne11 = 1 or n_ids, 16-byte aligned activation data and row / matrix strides
+ * (the activation quantizer's loads), i32 ids with contiguous rows, an f32
+ * output whose strides cover its rows, no fourth dimension. */
 static inline int qwmoe_ggml_supports_mul_mat_id(const struct ggml_tensor * op) {
     if (op->op != GGML_OP_MUL_MAT_ID) return 0;
     const struct ggml_tensor * as = op->src[0], * b = op->src[1], * ids = op->src[2];
+    if (!as || !b || !ids) return 0;
     const int wtype = as->type == GGML_TYPE_Q4_K || as->type == GGML_TYPE_Q6_K || as->type == GGML_TYPE_Q8_0;
     const int64_t blk = as->type == GGML_TYPE_Q8_0 ? 64 : 256;
-    return wtype && b->type == GGML_TYPE_F32 && ids->type == GGML_TYPE_I32 && op->type == GGML_TYPE_F32 &&
-           as->ne[0] % blk == 0 && as->ne[3] == 1 && b->ne[3] == 1 && b->nb[0] == sizeof(float) &&
-           ids->nb[0] == sizeof(int32_t) && op->nb[0] == sizeof(float);
+    const int64_t n_ids = ids->ne[0];
+    if (!wtype || b->type != GGML_TYPE_F32 || ids->type != GGML_TYPE_I32 || op->type != GGML_TYPE_F32) return 0;
+    if (as->ne[0] <= 0 || as->ne[0] % blk != 0 || as->ne[3] != 1 || b->ne[3] != 1 || ids->ne[2] != 1) return 0;
+    if (as->nb[2] < as->nb[1] * (size_t) as->ne[1]) return 0;
+    if (b->ne[1] != 1 && b->ne[1] != n_ids) return 0;
+    if (b->nb[0] != sizeof(float) || b->nb[1] % 16 != 0 || b->nb[2] % 16 != 0 || ((uintptr_t) b->data & 15)) return 0;
+    if (ids->nb[0] != sizeof(int32_t) || ids->nb[1] < (size_t) n_ids * 4 || ids->nb[1] % 4 != 0) return 0;
+    if (op->nb[0] != sizeof(float) || op->nb[1] < (size_t) as->ne[1] * 4 || op->nb[2] < op->nb[1] * (size_t) n_ids)
+        return 0;
+    return 1;
 }
 
 /* Runs the node on `stream` (a hipStream_t).  slot_row: optional logical id ->

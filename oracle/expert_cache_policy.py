@@ -32,7 +32,7 @@ class ExpertCachePolicy:
     """sigs: [role][layer] -> (type, ne0, ne1, slab bytes)."""
 
     def __init__(self, n_layer: int, n_expert: int, n_used: int, sigs, vram_budget: int):
-        self.n_layer, self.n_expert = n_layer, n_expert
+        self.n_layer, self.n_expert, self.n_used = n_layer, n_expert, n_used
         self.pools: list[Pool] = []
         self.layer_pool = [[-1] * n_layer for _ in range(3)]
         # signature discovery: role outer, layer inner (expert_cache.cpp:128-152)
@@ -148,7 +148,10 @@ class ExpertCachePolicy:
     def resmask(self, floor_res: int) -> tuple[list[list[float]], bool]:
         """decode_cached_fast's fill_resmask (core/runtime.cpp:2900-2919): 0 for an
         expert resident in all roles, -inf else; a layer with fewer than
-        floor_res residents routes unmasked.  Returns (rows, complete)."""
+        floor_res residents routes unmasked.  The floor is at least n_used (the
+        reference's floor_res = max(n_used, ...), core/runtime.cpp:2896-2898).
+        Returns (rows, complete)."""
+        floor_res = max(floor_res, self.n_used)
         rows, complete = [], True
         for l in range(self.n_layer):
             res = [all(self.resident(r, l, e) for r in range(3)) for e in range(self.n_expert)]

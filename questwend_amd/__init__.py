@@ -92,6 +92,7 @@ SIGNATURES = {
     "qwmoe_layer_stack_free": (None, [P]),
     "qwmoe_layer_stack_captures": (I64, [P]),
     "qwmoe_layer_stack_kernel": (I, [P]),
+    "qwmoe_layer_stack_kernel_t1": (I, [P]),
     "qwmoe_layer_stack_status": (I, [P, P, P, I]),
     "qwmoe_slot_table_create": (P, [I, I]),
     "qwmoe_slot_table_free": (None, [P]),

@@ -27,7 +27,7 @@ struct Library {
     size_t high_water = 0;
     int32_t* status = nullptr;   // device status word (first 256 bytes of the arena)
     int mfma_min_rows = 8;       // experts with this many routed rows use the matrix-core kernel (0: never)
-    int mfma_form = QWMOE_MFMA_AUTO;   // matrix cores' float tail (QWMOE_MFMA_*)
+    int mfma_form = QWMOE_MFMA_EXACT;  // matrix cores' float tail (QWMOE_MFMA_*): ggml's bits unless a caller opts out
 };
 
 Library g_lib;
@@ -103,9 +103,9 @@ qw::MmidArgs mmid_args(int type, const void* as, int64_t K, int64_t N, int64_t n
     m.mfma_min_rows = 0;
     m.max_rows = max_rows;
     m.n_pairs = n_pairs;
-    // the matrix cores' float tail: block sums where the form allows them -- under
-    // QWMOE_MFMA_AUTO only for fp32_out, the down projection of a layer entry
-    // point, whose output reaches nothing but the weighted sum
+    // the matrix cores' float tail: block sums only where the caller opted in --
+    // QWMOE_MFMA_BLOCK_SUM everywhere, QWMOE_MFMA_AUTO for fp32_out (the down
+    // projection of a layer entry point)
     m.mfma_exact = g_lib.mfma_form == QWMOE_MFMA_EXACT || (g_lib.mfma_form == QWMOE_MFMA_AUTO && !fp32_out);
     const bool mfma = g_lib.mfma_min_rows > 0 && max_rows >= g_lib.mfma_min_rows && qw::mmid_mfma_supported(m);
     if (mfma) m.mfma_min_rows = g_lib.mfma_min_rows;
@@ -777,6 +777,11 @@ int qwmoe_decode_stack_run(void* stream, qwmoe_decode_stack* s, const float* x, 
     if (!s || !x || !out) return QWMOE_ERR_INVALID_ARG;
     if ((ids_out == nullptr) != (weights_out == nullptr)) return QWMOE_ERR_INVALID_ARG;
     qw::DecodeStackDesc& d = s->d;
+    // the launch carries its exchange epoch from the host: a captured launch would
+    // replay the same epoch and accept the previous replay's words
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(S(stream), &cs) != hipSuccess) return QWMOE_ERR_HIP;
+    if (cs != hipStreamCaptureStatusNone) return QWMOE_ERR_UNSUPPORTED;
     if (d.epoch > 0x7fffffffu - (uint32_t) d.n_layer) return QWMOE_ERR_UNSUPPORTED;  // epoch space exhausted
     const uint32_t e0 = d.epoch;
     d.epoch += (uint32_t) d.n_layer;

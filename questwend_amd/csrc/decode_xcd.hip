@@ -359,16 +359,18 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
                         const float pmv = __builtin_fmaf(-yd * wdm, (float) pm, accm);
                         accm = n < 4 ? pmv : accm;
                     }
+                    // hsum_float_8 and the min lanes into lane 8r: row_shl inside the 16-lane
+                    // row (DPP), the same pairs as ggml's tree
                     float s2 = acc;
-                    s2 = s2 + __shfl_down(s2, 4, 8);
-                    s2 = s2 + __shfl_down(s2, 2, 8);
-                    s2 = s2 + __shfl_down(s2, 1, 8);
+                    s2 = s2 + dpp_f<0x104>(s2);
+                    s2 = s2 + dpp_f<0x102>(s2);
+                    s2 = s2 + dpp_f<0x101>(s2);
                     float m = accm;
-                    m = m + __shfl_down(m, 2, 8);
-                    m = m + __shfl_down(m, 1, 8);
+                    m = m + dpp_f<0x102>(m);
+                    m = m + dpp_f<0x101>(m);
                     res = s2 + m;
                 }
-                up = __shfl_down(res, 8);   // lane 16p: gate of pair p; lane 16p + 8: its up
+                up = dpp_f<0x108>(res);     // lane 16p: gate of pair p; lane 16p + 8: its up
                 // the exact expert of this XCD (posted by wave 0)
                 long spins = 0;
                 while (__hip_atomic_load(&s_topk_ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != ep) {

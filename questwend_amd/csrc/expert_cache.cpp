@@ -849,6 +849,10 @@ int qwmoe_expert_cache_verify(qwmoe_expert_cache* c, const int32_t* ids, int n_l
 
 int qwmoe_expert_cache_resmask(const qwmoe_expert_cache* c, int floor_res, float* mask, float* mask_dev) {
     if (!c || !mask) return QWMOE_ERR_INVALID_ARG;
+    // a layer masked to fewer than n_used residents would let top-k pick masked
+    // (absent) experts, which read slot 0's weights: the floor is at least n_used,
+    // as the reference's (core/runtime.cpp:2896-2898)
+    if (floor_res < c->n_used) floor_res = c->n_used;
     if (mask_dev && c->dry) return QWMOE_ERR_UNSUPPORTED;
     bool complete = true;
     for (int l = 0; l < c->n_layer; ++l) {

@@ -45,8 +45,10 @@ struct qwmoe_layer_stack {
     uint8_t* vblk = nullptr;             // layer table | exchange words | status, abort
     uint32_t vepoch = 1;                 // next launch's first layer epoch
     // T = 1: the whole-stack decode kernel (qwmoe_decode_stack_*), one launch per
-    // token, where it takes this stack's layers; the same bits as the chain
+    // token, where it takes this stack's layers; the same bits as the chain.
+    // Created at the first T = 1 run outside stream capture (ds_tried).
     qwmoe_decode_stack* ds = nullptr;
+    bool ds_allowed = true, ds_tried = false;
 
     ~qwmoe_layer_stack() {
         if (ds) qwmoe_decode_stack_free(ds);
@@ -224,14 +226,10 @@ int qwmoe_layer_stack_create(const qwmoe_layer* layers, int n_layer, float rms_e
         delete s;
         return rc;
     }
-    // runs at T = 1 go to the decode stack where it takes these layers (it leaves
-    // *out null otherwise, and the chain serves T = 1); QWMOE_VERIFY_XCD=0 keeps
-    // the chain for every T
+    // runs at T = 1 go to the decode stack where it takes these layers, created at
+    // the first such run; QWMOE_VERIFY_XCD=0 keeps the chain for every T
     const char* env = getenv("QWMOE_VERIFY_XCD");
-    if (!(env && env[0] == '0') && qwmoe_decode_stack_create(layers, n_layer, rms_eps, &s->ds) != QWMOE_OK) {
-        s->ds = nullptr;
-        (void) hipGetLastError();
-    }
+    s->ds_allowed = !(env && env[0] == '0');
     *out = s;
     return QWMOE_OK;
 }
@@ -240,11 +238,24 @@ int qwmoe_layer_stack_run(void* stream, qwmoe_layer_stack* s, const float* x, in
                           int32_t* ids_out, float* weights_out) {
     if (!s || !x || !out || T <= 0 || T > s->max_T) return QWMOE_ERR_INVALID_ARG;
     if ((ids_out == nullptr) != (weights_out == nullptr)) return QWMOE_ERR_INVALID_ARG;
-    if (T == 1 && s->ds) return qwmoe_decode_stack_run(stream, s->ds, x, out, x_out, ids_out, weights_out);
     hipStream_t st = (hipStream_t) stream;
+    // Under stream capture the persistent kernels cannot run (each launch takes a
+    // fresh exchange epoch from the host, which a replayed graph would repeat), and
+    // nothing may be allocated: the caller's capture records the per-layer chain.
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess) return QWMOE_ERR_HIP;
+    const bool capturing = cs != hipStreamCaptureStatusNone;
+    if (T == 1 && !capturing && s->ds_allowed && !s->ds_tried) {
+        s->ds_tried = true;
+        if (qwmoe_decode_stack_create(s->layers.data(), (int) s->layers.size(), s->rms_eps, &s->ds) != QWMOE_OK) {
+            s->ds = nullptr;
+            (void) hipGetLastError();
+        }
+    }
+    if (T == 1 && s->ds && !capturing) return qwmoe_decode_stack_run(stream, s->ds, x, out, x_out, ids_out, weights_out);
     const size_t xbytes = (size_t) T * (size_t) s->H * 4;
     const int n = (int) s->layers.size();
-    if (s->vfn && T >= 2 && T <= qw::VERIFY_TMAX) {
+    if (s->vfn && T >= 2 && T <= qw::VERIFY_TMAX && !capturing) {
         // the persistent kernel: the caller's buffers directly, one launch
         if (s->vepoch > 0x7fffffffu - (uint32_t) n) return QWMOE_ERR_UNSUPPORTED;   // epoch space exhausted
         qw::VerifyArgs a = s->va;
@@ -260,7 +271,9 @@ int qwmoe_layer_stack_run(void* stream, qwmoe_layer_stack* s, const float* x, in
     }
     if (hipMemcpyAsync(s->xb[0], x, xbytes, hipMemcpyDeviceToDevice, st) != hipSuccess) return QWMOE_ERR_HIP;
     int rc;
-    if (s->graphs) {
+    if (capturing) {
+        if ((rc = s->enqueue(st, T)) != QWMOE_OK) return rc;
+    } else if (s->graphs) {
         // a graph holds the workspace addresses and the kernel choices of its capture: capture again
         // after qwmoe_init reallocated the workspace or qwmoe_set_mfma_min_rows changed the threshold
         if (s->exec[(size_t) T] && s->exec_gen[(size_t) T] != qw::workspace_generation()) {
@@ -291,6 +304,18 @@ int64_t qwmoe_layer_stack_captures(const qwmoe_layer_stack* s) { return s ? s->c
 int qwmoe_layer_stack_kernel(const qwmoe_layer_stack* s) {
     if (!s) return QWMOE_ERR_INVALID_ARG;
     return s->vfn ? (s->va.local_st ? 2 : 3) : 1;
+}
+
+int qwmoe_layer_stack_kernel_t1(qwmoe_layer_stack* s) {
+    if (!s) return QWMOE_ERR_INVALID_ARG;
+    if (s->ds_allowed && !s->ds_tried) {
+        s->ds_tried = true;
+        if (qwmoe_decode_stack_create(s->layers.data(), (int) s->layers.size(), s->rms_eps, &s->ds) != QWMOE_OK) {
+            s->ds = nullptr;
+            (void) hipGetLastError();
+        }
+    }
+    return s->ds ? qwmoe_decode_stack_kernel(s->ds) : 0;
 }
 
 int qwmoe_layer_stack_status(void* stream, qwmoe_layer_stack* s, int32_t* status_out, int clear) {

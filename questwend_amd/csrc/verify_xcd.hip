@@ -377,16 +377,18 @@ __global__ void __launch_bounds__(XT) k_verify_xcd(VerifyArgs a) {
                         const float pmv = __builtin_fmaf(-yd * wdm, (float) pm, accm);
                         accm = n < 4 ? pmv : accm;
                     }
+                    // hsum_float_8 and the min lanes into lane 8r: row_shl inside the 16-lane
+                    // row (DPP), the same pairs as ggml's tree
                     float s2 = acc;
-                    s2 = s2 + __shfl_down(s2, 4, 8);
-                    s2 = s2 + __shfl_down(s2, 2, 8);
-                    s2 = s2 + __shfl_down(s2, 1, 8);
+                    s2 = s2 + dpp_f<0x104>(s2);
+                    s2 = s2 + dpp_f<0x102>(s2);
+                    s2 = s2 + dpp_f<0x101>(s2);
                     float m = accm;
-                    m = m + __shfl_down(m, 2, 8);
-                    m = m + __shfl_down(m, 1, 8);
+                    m = m + dpp_f<0x102>(m);
+                    m = m + dpp_f<0x101>(m);
                     res = s2 + m;
                 }
-                const float up = __shfl_down(res, 8);   // lane 16p: gate of pair p; lane 16p + 8: its up
+                const float up = dpp_f<0x108>(res);     // lane 16p: gate of pair p; lane 16p + 8: its up
                 if ((lane & 15) == 0 && (lane >> 4) < PPW) {
                     const int f = NP * j + PPW * wave + (lane >> 4);
                     st_local(a.xa + (((size_t) xcd * VSL + s) * VTM + tk) * F + f, tag(v_silu(res) * up, ep), local);

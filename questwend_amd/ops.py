@@ -46,9 +46,10 @@ MFMA_BLOCK_SUM, MFMA_EXACT, MFMA_AUTO = 0, 1, 2
 def set_mfma_form(form: int) -> int:
     """The matrix-core kernel's float tail: MFMA_EXACT replays ggml's fp32 lane
     chains (bit-identical), MFMA_BLOCK_SUM adds exact integer block sums in one
-    fp32 chain per output, MFMA_AUTO (default) is exact where the output may be
-    re-quantized and block-sum for the down projections of the layer entry
-    points.  Returns the previous setting."""
+    fp32 chain per output, MFMA_AUTO is exact except for the down projections
+    of the layer entry points.  The default is MFMA_EXACT; the other two are
+    opt-in speed settings whose outputs drift from ggml's in the last bits.
+    Returns the previous setting."""
     prev = int(lib().qwmoe_get_mfma_form())
     check(lib().qwmoe_set_mfma_form(int(form)), "set_mfma_form")
     return prev
@@ -363,6 +364,10 @@ class LayerStack(_Handle):
     def kernel(self) -> int:
         """1: the per-layer chain; 2: one persistent launch for 2 <= T <= 8 (3: device-scope words)."""
         return int(lib().qwmoe_layer_stack_kernel(self.h))
+
+    def kernel_t1(self) -> int:
+        """The decode kernel a T = 1 run takes (qwmoe_decode_stack_kernel's value), 0 for the chain."""
+        return int(lib().qwmoe_layer_stack_kernel_t1(self.h))
 
     def status(self, clear: bool = True) -> int:
         v = C.c_int32(0)

@@ -435,11 +435,14 @@ def test_oracle_resmask_and_refill_by_hand():
     assert [q.n_slots for q in p.pools] == [4, 4, 4]
     p.ensure(0, [1, 3])
     p.ensure(1, [2])
-    rows, complete = p.resmask(floor_res=1)
     ninf = float("-inf")
-    assert rows == [[ninf, 0.0, ninf, 0.0], [ninf, ninf, 0.0, ninf]] and complete
     rows, complete = p.resmask(floor_res=2)                   # layer 1 has one resident: left unmasked
     assert rows[0] == [ninf, 0.0, ninf, 0.0] and rows[1] == [0.0] * 4 and not complete
+    assert p.resmask(floor_res=1) == (rows, complete)         # the floor is at least n_used (2)
+    q = ExpertCachePolicy(2, 4, 2, sigs, sum(sigs[r][0][3] for r in range(3)) * 2 * 4 // 2)
+    q.ensure(0, [1, 3])
+    q.ensure(1, [2, 3])
+    assert q.resmask(floor_res=0) == ([[ninf, 0.0, ninf, 0.0], [ninf, ninf, 0.0, 0.0]], True)
     # refill from layer 1 (cursor 1), budget 2: the used experts are touched in
     # order (0,1), (0,3), (1,2); layer 1 wants 0 (a free slot) then 3 (evicts the
     # least recently used, (0,1))

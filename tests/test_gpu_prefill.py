@@ -13,9 +13,10 @@ The matrix cores have two forms of the float tail (qwmoe_set_mfma_form):
   * block-sum: each super-block's exact integer sums scaled and added in one
     fp32 chain per output -- the same products summed in another order, within
     BS_TOL of the reference per projection.
-The default (auto) takes the exact form wherever an output may be re-quantized
-(mul_mat_id, gate/up of a layer) and block sums for the layers' down
-projections, so layer outputs stay within BS_TOL too.  Block sums everywhere
+The default is the exact form.  The opt-in auto form takes the exact form
+wherever an output may be re-quantized (mul_mat_id, gate/up of a layer) and
+block sums for the layers' down projections, so layer outputs stay within
+BS_TOL too.  Block sums everywhere
 are reported beside it: there a last-bit change of gate/up can move a
 re-quantized Q8_K value by one step.  Both forms are pinned on inputs for which
 every fp32 operation is exact (block scales d = dmin = 1, activations that
@@ -163,9 +164,8 @@ def test_mfma_integer_core_bit_exact(orc, K, N, ne11, min_rows, exact):
 @pytest.mark.parametrize("K,N,T,k,n_as,ne11", [(2048, 768, 256, 8, 32, 1), (768, 2048, 128, 8, 16, 8),
                                               (2048, 512, 97, 4, 8, 1)])
 def test_mfma_random(orc, K, N, T, k, n_as, ne11):
-    """Random Q4_K weights and N(0,1) activations: the exact form (and the
-    default, which takes it for mul_mat_id) bit-identical to the reference, the
-    block-sum form within BS_TOL of it."""
+    """Random Q4_K weights and N(0,1) activations: the default (exact) form
+    bit-identical to the reference, the block-sum form within BS_TOL of it."""
     note(f"matrix-core mul_mat_id, random data: K={K} N={N} T={T} k={k} n_as={n_as} ne11={ne11}")
     rng = np.random.default_rng(T + N)
     w = orc.quantize(Q4_K, (rng.standard_normal((n_as * N, K)) * 0.02).astype(np.float32))
@@ -183,7 +183,7 @@ def test_mfma_random(orc, K, N, T, k, n_as, ne11):
         ops.set_mfma_form(prev)
     note(f"  heavy experts {int((counts >= 32).sum())}/{n_as}, max rows {counts.max()}, "
          f"block-sum rel err {rel_err(got, want):.3e}")
-    assert prev == AUTO
+    assert prev == EXACT   # the library's default
     assert np.array_equal(bits(got_auto), bits(want))
     assert rel_err(got, want) < BS_TOL
     assert ops.device_status(clear=True) == 0
@@ -263,8 +263,8 @@ def test_mfma_disabled_is_bit_exact(orc):
 
 
 def layer_forms(layer, x):
-    """ffn_layer under the exact form (all four outputs), the default auto form
-    and block sums everywhere (outputs only)."""
+    """ffn_layer under the exact form (the default; all four outputs), the
+    opt-in auto form and block sums everywhere (outputs only)."""
     prev = ops.set_mfma_form(EXACT)
     try:
         out, xn, ids, w = (host(t) for t in ops.ffn_layer(layer, dev(x), rms_eps=1e-6))
@@ -309,7 +309,7 @@ def test_prefill_layer_30b_shape(orc, T):
     """a Q4_K layer at the 30B-A3B shape, T tokens of N(0,1), Zipf-skewed
     routing: ids and weights bit-identical to the CPU reference; the layer output
     bit-identical with the exact matrix-core form and within BS_TOL with the
-    default form; its RMSNorm within 1e-3 (double sum in another order,
+    auto form; its RMSNorm within 1e-3 (double sum in another order,
     rounding identical except within ~2^-29 of a float boundary).
 
     With block sums everywhere the gate/up outputs can differ in the last bit,
@@ -419,7 +419,7 @@ def test_prefill_layer_config5_shape():
     the GEMV.  Against the reference ggml (16 threads) when it is built; else
     tokens are independent, so a sample of 24 tokens is checked against the
     oracle.  Output bit-identical with the exact matrix-core form, within
-    BS_TOL with the default form (block sums everywhere: reported, as in
+    BS_TOL with the auto form (block sums everywhere: reported, as in
     test_prefill_layer_30b_shape)."""
     H, E, k, F, types = C5
     T = 1024
