@@ -289,6 +289,61 @@ typedef struct qwmoe_layer {
 int qwmoe_ffn_layer(void * stream, const qwmoe_layer * layer, const float * x, int64_t T, float * out,
                     float rms_eps, float * x_next, int32_t * ids_out, float * weights_out);
 
+/* ---- the attention half of a decoder layer ------------------------------------ */
+
+/* One non-recurrent, non-gated Qwen3 attention block (Seg A of a MoE layer:
+ * build_segA, core/runtime.cpp:1976-2030; build_attn, 681-734; NEOX RoPE,
+ * apply_rope 290-300).  Weights as in the GGUF: attn_q [H, n_head * D],
+ * attn_k / attn_v [H, n_head_kv * D], attn_output [n_head * D, H] (rows of
+ * nb1 bytes, Q4_K / Q6_K / Q8_0), f32 norms.  The caches are ggml's k_cache /
+ * v_cache: f16 [n_ctx][n_head_kv * D] rows, 16-byte aligned, owned by the
+ * caller. */
+typedef struct qwmoe_attn_layer {
+    int64_t n_embd;            /* H */
+    int64_t n_head, n_head_kv; /* query and key/value heads (n_head % n_head_kv == 0) */
+    int64_t n_embd_head;       /* D = 128 */
+    int64_t n_rot;             /* RoPE dimensions = D */
+    float rope_freq_base;      /* 1e6 for Qwen3 */
+    const float * attn_norm;   /* [H]: blk.N.attn_norm.weight */
+    int type_q, type_k, type_v, type_o;
+    const void * wq; size_t wq_nb1;   /* blk.N.attn_q.weight */
+    const void * wk; size_t wk_nb1;   /* blk.N.attn_k.weight */
+    const void * wv; size_t wv_nb1;   /* blk.N.attn_v.weight */
+    const void * wo; size_t wo_nb1;   /* blk.N.attn_output.weight */
+    const float * q_norm;      /* [D]: blk.N.attn_q_norm.weight */
+    const float * k_norm;      /* [D]: blk.N.attn_k_norm.weight */
+    const float * ffn_norm;    /* [H]: blk.N.ffn_norm.weight (the router input's norm) */
+    uint16_t * k_cache;        /* f16 [n_ctx][n_head_kv * D] */
+    uint16_t * v_cache;
+    int64_t n_ctx;
+} qwmoe_attn_layer;
+
+/* T tokens at positions n_past .. n_past + T - 1 (a decode step, a verify batch
+ * or a prefill chunk), h f32 [T, H] the layer input (the residual stream):
+ *   cur = rms_norm(h) * attn_norm; Q, K, V = projections of cur;
+ *   Q = rope(rms_norm(Q) * q_norm), K = rope(rms_norm(K) * k_norm) per head;
+ *   K, V (f16) into cache rows n_past ..; causal attention over the n_past + T
+ *   cached keys, kq_scale = 1 / sqrt(D), ggml's soft_max_ext;
+ *   attn_resid = attn_output(att) + h; ffn_in = rms_norm(attn_resid) * ffn_norm
+ *   (ffn_in may be NULL).
+ * The projections are the quantized mul_mat row dots (activations quantized to
+ * the weight's vec_dot type, as ggml_mul_mat); Q and the probabilities are
+ * rounded to f16 before their products as ggml's f16 mul_mat does.  Outputs
+ * agree with the reference CPU graph within the fp32 rounding of the sums
+ * (1e-3), not bit for bit.  Requires D = n_rot = 128, n_head / n_head_kv <= 16,
+ * n_past + T <= n_ctx, h 16-byte aligned. */
+int qwmoe_attn_seg(void * stream, const qwmoe_attn_layer * layer, const float * h, int64_t T, int64_t n_past,
+                   float rms_eps, float * attn_resid, float * ffn_in);
+
+/* One whole decoder layer of a Qwen3-MoE model for T tokens: qwmoe_attn_seg,
+ * then qwmoe_ffn_layer on ffn_in (the router reads ffn_in; build_moe's T = 1 or
+ * T > 1 weighted sum), then h_out = moe_out + attn_resid (build_segB's residual,
+ * core/runtime.cpp:2087).  h, h_out f32 [T, H]; ids_out / weights_out
+ * optional [T, k]. */
+int qwmoe_decoder_layer(void * stream, const qwmoe_attn_layer * attn, const qwmoe_layer * moe, const float * h,
+                        int64_t T, int64_t n_past, float rms_eps, float * h_out, int32_t * ids_out,
+                        float * weights_out);
+
 /* ---- persistent multi-layer decode ------------------------------------------ */
 
 /* A stack of MoE FFN layers decoded one token per launch, all layers in a

@@ -458,3 +458,108 @@ int qwref_unary(int op, const float * a, const float * b, int64_t ne0, int64_t n
 }
 
 } // extern "C"
+
+extern "C" {
+
+// ---------------------------------------------------------------------------
+// Seg A's attention half for one non-recurrent, non-gated Qwen3 layer on the
+// CPU backend, the op sequence of core/runtime.cpp:1976-2030 (build_segA)
+// with build_attn's manual (non-flash) path, 681-734, and 1D NEOX RoPE
+// (apply_rope, 290-300):
+//   cur = rms_norm(h) * attn_norm; Q/K/V = mul_mat(W, cur), reshaped per head;
+//   Q = rms_norm(Q) * q_norm, K = rms_norm(K) * k_norm; rope_ext NEOX at
+//   positions n_past + i; K, V copied into the f16 caches at row n_past;
+//   kq = mul_mat(cont(permute(Kc)), permute(Q)); soft_max_ext(kq, mask, 1/sqrt(D));
+//   kqv = mul_mat(cont(transpose(Vc)) as [n_kv, D, n_head_kv], kq);
+//   att = cont_2d(permute(kqv)); cur = mul_mat(Wo, att);
+//   attn_resid = cur + h; ffn_in = rms_norm(attn_resid) * ffn_norm.
+// The causal f16 mask is filled as set_attn_inputs does (2108-2116).
+// h, attn_resid, ffn_in: [T, H]; k_cache / v_cache: f16 [n_ctx, n_head_kv * D],
+// read and written in place (rows n_past .. n_past + T - 1); q_out / att_out
+// ([T, n_head * D], the roped Q and the attention output) may be NULL.
+int qwref_attn_seg(int64_t H, int64_t n_head, int64_t n_head_kv, int64_t D, int64_t n_rot, float freq_base,
+                   float eps, int64_t T, int64_t n_past, int64_t n_ctx, const float * h, const float * attn_norm,
+                   int tq, const void * wq, int tk, const void * wk, int tv, const void * wv, int to,
+                   const void * wo, const float * q_norm, const float * k_norm, const float * ffn_norm,
+                   uint16_t * k_cache, uint16_t * v_cache, float * attn_resid, float * ffn_in, float * q_out,
+                   float * att_out, int n_threads) {
+    ensure_init();
+    if (n_past + T > n_ctx || n_head % n_head_kv) return -2;
+    const int64_t n_kv = n_past + T, gqa = n_head_kv * D;
+    const size_t cache_bytes = sizeof(uint16_t) * (size_t) (n_ctx * gqa);
+    const size_t act = sizeof(float) * (size_t) T * (size_t) (16 * H + 16 * n_head * D + 8 * gqa)
+                       + sizeof(float) * (size_t) (4 * n_head * T * n_kv + 2 * n_kv * gqa)
+                       + 2 * cache_bytes + sizeof(uint16_t) * (size_t) (n_kv * T);
+    const size_t wbytes = ggml_row_size((ggml_type) tq, H) * (size_t) (n_head * D) +
+                          ggml_row_size((ggml_type) tk, H) * (size_t) gqa +
+                          ggml_row_size((ggml_type) tv, H) * (size_t) gqa +
+                          ggml_row_size((ggml_type) to, n_head * D) * (size_t) H + sizeof(float) * (size_t) (4 * H + 4 * D);
+    ggml_init_params ip = { act + wbytes + ggml_tensor_overhead() * 128 + ggml_graph_overhead() + (4 << 20), nullptr,
+                            false };
+    ggml_context * ctx = ggml_init(ip);
+    auto wt = [&](int type, int64_t ne0, int64_t ne1, const void * data) {
+        ggml_tensor * t = ggml_new_tensor_2d(ctx, (ggml_type) type, ne0, ne1);
+        memcpy(t->data, data, ggml_nbytes(t));
+        return t;
+    };
+    auto vec = [&](const float * v, int64_t n) { return wt(GGML_TYPE_F32, n, 1, v); };
+    ggml_tensor * Wq = wt(tq, H, n_head * D, wq), * Wk = wt(tk, H, gqa, wk), * Wv = wt(tv, H, gqa, wv);
+    ggml_tensor * Wo = wt(to, n_head * D, H, wo);
+    ggml_tensor * An = ggml_reshape_1d(ctx, vec(attn_norm, H), H), * Fn = ggml_reshape_1d(ctx, vec(ffn_norm, H), H);
+    ggml_tensor * Qn = ggml_reshape_1d(ctx, vec(q_norm, D), D), * Kn = ggml_reshape_1d(ctx, vec(k_norm, D), D);
+    ggml_tensor * KC = wt(GGML_TYPE_F16, gqa, n_ctx, k_cache), * VC = wt(GGML_TYPE_F16, gqa, n_ctx, v_cache);
+    ggml_tensor * X = wt(GGML_TYPE_F32, H, T, h);
+    ggml_tensor * pos = ggml_new_tensor_1d(ctx, GGML_TYPE_I32, T);
+    for (int64_t i = 0; i < T; ++i) ((int32_t *) pos->data)[i] = (int32_t) (n_past + i);
+    ggml_tensor * mask = ggml_new_tensor_2d(ctx, GGML_TYPE_F16, n_kv, T);
+    const ggml_fp16_t z = ggml_fp32_to_fp16(0.0f), ninf = ggml_fp32_to_fp16(-INFINITY);
+    for (int64_t i = 0; i < T; ++i)
+        for (int64_t j = 0; j < n_kv; ++j) ((ggml_fp16_t *) mask->data)[i * n_kv + j] = j <= n_past + i ? z : ninf;
+
+    ggml_cgraph * gf = ggml_new_graph(ctx);
+    ggml_tensor * cur = ggml_mul(ctx, ggml_rms_norm(ctx, X, eps), An);
+    ggml_tensor * Q = ggml_reshape_3d(ctx, ggml_mul_mat(ctx, Wq, cur), D, n_head, T);
+    ggml_tensor * K = ggml_reshape_3d(ctx, ggml_mul_mat(ctx, Wk, cur), D, n_head_kv, T);
+    ggml_tensor * V = ggml_reshape_3d(ctx, ggml_mul_mat(ctx, Wv, cur), D, n_head_kv, T);
+    Q = ggml_mul(ctx, ggml_rms_norm(ctx, Q, eps), Qn);
+    K = ggml_mul(ctx, ggml_rms_norm(ctx, K, eps), Kn);
+    Q = ggml_rope_ext(ctx, Q, pos, nullptr, (int) n_rot, GGML_ROPE_TYPE_NEOX, 0, freq_base, 1.0f, 0.0f, 1.0f, 0.0f,
+                      0.0f);
+    K = ggml_rope_ext(ctx, K, pos, nullptr, (int) n_rot, GGML_ROPE_TYPE_NEOX, 0, freq_base, 1.0f, 0.0f, 1.0f, 0.0f,
+                      0.0f);
+    ggml_tensor * k_dst = ggml_view_2d(ctx, KC, gqa, T, KC->nb[1], (size_t) n_past * KC->nb[1]);
+    ggml_build_forward_expand(gf, ggml_cpy(ctx, ggml_reshape_2d(ctx, K, gqa, T), k_dst));
+    ggml_tensor * v_dst = ggml_view_2d(ctx, VC, gqa, T, VC->nb[1], (size_t) n_past * VC->nb[1]);
+    ggml_build_forward_expand(gf, ggml_cpy(ctx, ggml_reshape_2d(ctx, V, gqa, T), v_dst));
+    ggml_tensor * Kc = ggml_view_2d(ctx, KC, gqa, n_kv, KC->nb[1], 0);
+    Kc = ggml_permute(ctx, ggml_reshape_3d(ctx, Kc, D, n_head_kv, n_kv), 0, 2, 1, 3);
+    ggml_tensor * Qp = ggml_permute(ctx, Q, 0, 2, 1, 3);
+    ggml_tensor * kq = ggml_mul_mat(ctx, ggml_cont(ctx, Kc), Qp);
+    kq = ggml_soft_max_ext(ctx, kq, mask, 1.0f / sqrtf((float) D), 0.0f);
+    ggml_tensor * Vslice = ggml_view_2d(ctx, VC, gqa, n_kv, VC->nb[1], 0);
+    ggml_tensor * Vm = ggml_reshape_3d(ctx, ggml_cont(ctx, ggml_transpose(ctx, Vslice)), n_kv, D, n_head_kv);
+    ggml_tensor * kqv = ggml_mul_mat(ctx, Vm, kq);
+    ggml_tensor * att = ggml_cont_2d(ctx, ggml_permute(ctx, kqv, 0, 2, 1, 3), n_head * D, T);
+    ggml_tensor * resid = ggml_add(ctx, ggml_mul_mat(ctx, Wo, att), X);
+    ggml_tensor * fin = ggml_mul(ctx, ggml_rms_norm(ctx, resid, eps), Fn);
+    ggml_tensor * qc = ggml_cont(ctx, Q);
+    ggml_build_forward_expand(gf, qc);
+    ggml_build_forward_expand(gf, fin);
+
+    ggml_cplan plan = ggml_graph_plan(gf, n_threads, nullptr);
+    std::vector<uint8_t> work(plan.work_size + 64);
+    plan.work_data = work.data();
+    const int rc = ggml_graph_compute(gf, &plan) == GGML_STATUS_SUCCESS ? 0 : -1;
+    if (rc == 0) {
+        if (attn_resid) copy_2d(resid, attn_resid, 4);
+        if (ffn_in) copy_2d(fin, ffn_in, 4);
+        if (q_out) copy_2d(qc, q_out, 4);
+        if (att_out) copy_2d(att, att_out, 4);
+        memcpy(k_cache, KC->data, cache_bytes);
+        memcpy(v_cache, VC->data, cache_bytes);
+    }
+    ggml_free(ctx);
+    return rc;
+}
+
+}  // extern "C" (attention)

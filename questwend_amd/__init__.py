@@ -53,6 +53,20 @@ class SharedExpert(C.Structure):
     ]
 
 
+class AttnLayer(C.Structure):
+    """Mirror of ``qwmoe_attn_layer`` (include/qwmoe.h)."""
+
+    _fields_ = [
+        ("n_embd", C.c_int64), ("n_head", C.c_int64), ("n_head_kv", C.c_int64), ("n_embd_head", C.c_int64),
+        ("n_rot", C.c_int64), ("rope_freq_base", C.c_float), ("attn_norm", C.c_void_p),
+        ("type_q", C.c_int), ("type_k", C.c_int), ("type_v", C.c_int), ("type_o", C.c_int),
+        ("wq", C.c_void_p), ("wq_nb1", C.c_size_t), ("wk", C.c_void_p), ("wk_nb1", C.c_size_t),
+        ("wv", C.c_void_p), ("wv_nb1", C.c_size_t), ("wo", C.c_void_p), ("wo_nb1", C.c_size_t),
+        ("q_norm", C.c_void_p), ("k_norm", C.c_void_p), ("ffn_norm", C.c_void_p),
+        ("k_cache", C.c_void_p), ("v_cache", C.c_void_p), ("n_ctx", C.c_int64),
+    ]
+
+
 # name -> (restype, argtypes); every exported symbol of include/qwmoe.h
 P, I64, SZ, I, F, U64 = C.c_void_p, C.c_int64, C.c_size_t, C.c_int, C.c_float, C.c_uint64
 SIGNATURES = {
@@ -82,6 +96,8 @@ SIGNATURES = {
     "qwmoe_rms_norm_mul": (I, [P, P, P, P, I64, I64, F]),
     "qwmoe_shared_expert_add": (I, [P, P, I64, P, I64, P, P, P]),
     "qwmoe_ffn_layer": (I, [P, P, P, I64, P, F, P, P, P]),
+    "qwmoe_attn_seg": (I, [P, P, P, I64, I64, F, P, P]),
+    "qwmoe_decoder_layer": (I, [P, P, P, P, I64, I64, F, P, P, P]),
     "qwmoe_decode_stack_create": (I, [P, I, F, P]),
     "qwmoe_decode_stack_run": (I, [P, P, P, P, P, P, P]),
     "qwmoe_decode_stack_status": (I, [P, P, P, I]),

@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdint>
 #include <cstdlib>
 #include <cstring>
@@ -36,12 +37,17 @@ std::mutex g_mu;
 // workspace is (re)allocated or freed, or the matrix-core row threshold is set.
 std::atomic<uint64_t> g_ws_generation{1};
 
+// Lowest workspace offset a call's arena may use: raised while an entry point
+// that chains others keeps its own temporaries below it (ArenaFloor).
+size_t g_arena_floor = 0;
+
 // Bump allocator over the workspace for one call.
 struct Arena {
     uint8_t* base;
     size_t cap, off;
     bool track = true;   // record the high-water mark of the library workspace
-    explicit Arena(size_t reserved) : base(g_lib.ws), cap(g_lib.ws_bytes), off(reserved) {}
+    explicit Arena(size_t reserved)
+        : base(g_lib.ws), cap(g_lib.ws_bytes), off(reserved > g_arena_floor ? reserved : g_arena_floor) {}
     Arena(void* buf, size_t bytes) : base((uint8_t*) buf), cap(bytes), off(0), track(false) {}
     template <typename T>
     T* take(size_t count) {
@@ -57,6 +63,13 @@ struct Arena {
 };
 
 constexpr size_t kReserved = 256;  // status word lives here
+
+// Keeps the workspace below `off` for the enclosing call while it runs others.
+struct ArenaFloor {
+    size_t prev;
+    explicit ArenaFloor(size_t off) : prev(g_arena_floor) { g_arena_floor = off; }
+    ~ArenaFloor() { g_arena_floor = prev; }
+};
 
 inline hipStream_t S(void* s) { return (hipStream_t) s; }
 
@@ -512,6 +525,126 @@ int qwmoe_shared_expert_add(void* stream, const qwmoe_shared_expert* se, int64_t
     }
     if ((rc = mmid_launch(md, st))) return rc;
     return qw::launch_shared_gate_add(x, (size_t) H, se->gate_inp, sh, moe_out, resid, out, (size_t) H, H, T, st);
+}
+
+// The attention half of Seg A (core/runtime.cpp:1976-2030 with build_attn,
+// 681-734): projections as ggml_mul_mat of the quantized weights (every token
+// "expert" 0 of a one-bin grouping, so the mul_mat_id row dots apply), the
+// attention core in attn.hip, the residual and the FFN input norm.
+int qwmoe_attn_seg(void* stream, const qwmoe_attn_layer* L, const float* h, int64_t T, int64_t n_past,
+                   float rms_eps, float* attn_resid, float* ffn_in) {
+    if (!g_lib.ready) return QWMOE_ERR_NOT_INITIALIZED;
+    if (!L || !h || !attn_resid || T < 0 || n_past < 0 || !(rms_eps >= 0.0f)) return QWMOE_ERR_INVALID_ARG;
+    const int64_t H = L->n_embd, nq = L->n_head, nk = L->n_head_kv, D = L->n_embd_head;
+    if (H <= 0 || nq <= 0 || nk <= 0 || nq % nk || !L->attn_norm || !L->wq || !L->wk || !L->wv || !L->wo ||
+        !L->q_norm || !L->k_norm || !L->k_cache || !L->v_cache || (ffn_in && !L->ffn_norm))
+        return QWMOE_ERR_INVALID_ARG;
+    if (n_past + T > L->n_ctx) return QWMOE_ERR_INVALID_ARG;
+    if (D != 128 || L->n_rot != D || nq / nk > qw::ATT_RMAX || H % 4) return QWMOE_ERR_UNSUPPORTED;
+    if (((uintptr_t) L->k_cache & 15) || ((uintptr_t) L->v_cache & 15) || ((uintptr_t) h & 15))
+        return QWMOE_ERR_UNSUPPORTED;
+    const int types[4] = {L->type_q, L->type_k, L->type_v, L->type_o};
+    for (int t : types)
+        if (!weight_type_ok(t)) return QWMOE_ERR_UNSUPPORTED;
+    const int64_t NQ = nq * D, NK = nk * D;
+    int rc;
+    if ((rc = check_k(L->type_q, H)) || (rc = check_k(L->type_k, H)) || (rc = check_k(L->type_v, H)) ||
+        (rc = check_k(L->type_o, NQ)))
+        return rc;
+    if (L->wq_nb1 < qwmoe_row_size(L->type_q, H) || L->wk_nb1 < qwmoe_row_size(L->type_k, H) ||
+        L->wv_nb1 < qwmoe_row_size(L->type_v, H) || L->wo_nb1 < qwmoe_row_size(L->type_o, NQ))
+        return QWMOE_ERR_INVALID_ARG;
+    if (T == 0) return QWMOE_OK;
+    hipStream_t st = S(stream);
+    Arena ar(kReserved);
+    const int64_t n_kv = n_past + T, n_split = (n_kv + qw::ATT_SPLIT - 1) / qw::ATT_SPLIT;
+    int32_t* rows = ar.take<int32_t>((size_t) (2 * T + 2));
+    int32_t* active = ar.take<int32_t>(2);
+    int32_t* active_off = ar.take<int32_t>(3);
+    int32_t* n_active = ar.take<int32_t>(1);
+    float* cur = ar.take<float>((size_t) (H * T));
+    float* q = ar.take<float>((size_t) (NQ * T));
+    float* k = ar.take<float>((size_t) (NK * T));
+    float* v = ar.take<float>((size_t) (NK * T));
+    float* qr = ar.take<float>((size_t) (NQ * T));
+    float* sc = ar.take<float>((size_t) (nq * T * n_kv));
+    float* part = ar.take<float>((size_t) (n_split * T * NQ));
+    float* att = ar.take<float>((size_t) (NQ * T));
+    float* proj = ar.take<float>((size_t) (H * T));
+    if (!rows || !active || !active_off || !n_active || !cur || !q || !k || !v || !qr || !sc || !part || !att || !proj)
+        return QWMOE_ERR_WORKSPACE;
+    // quantized activations, one per vec_dot type in use
+    const int vqt = qw::vec_dot_type(L->type_q), vkt = qw::vec_dot_type(L->type_k), vvt = qw::vec_dot_type(L->type_v);
+    const int vot = qw::vec_dot_type(L->type_o);
+    const size_t rq = qwmoe_row_size(vqt, H), rk = qwmoe_row_size(vkt, H), rv = qwmoe_row_size(vvt, H);
+    const size_t ro = qwmoe_row_size(vot, NQ);
+    uint8_t* xq = ar.take<uint8_t>(rq * (size_t) T + 64);
+    uint8_t* xk = vkt == vqt ? xq : ar.take<uint8_t>(rk * (size_t) T + 64);
+    uint8_t* xv = vvt == vqt ? xq : vvt == vkt ? xk : ar.take<uint8_t>(rv * (size_t) T + 64);
+    uint8_t* aq = ar.take<uint8_t>(ro * (size_t) T + 64);
+    if (!xq || !xk || !xv || !aq) return QWMOE_ERR_WORKSPACE;
+    if ((rc = qw::launch_rms_norm(h, cur, H, T, rms_eps, st, L->attn_norm))) return rc;
+    if ((rc = qw::launch_group_dense(rows, active, active_off, n_active, T, st))) return rc;
+    const size_t hb = (size_t) H * 4;
+    if ((rc = qw::launch_quantize_act(vqt, cur, H, 1, T, hb, hb, xq, st))) return rc;
+    if (xk != xq && (rc = qw::launch_quantize_act(vkt, cur, H, 1, T, hb, hb, xk, st))) return rc;
+    if (xv != xq && xv != xk && (rc = qw::launch_quantize_act(vvt, cur, H, 1, T, hb, hb, xv, st))) return rc;
+    auto proj_launch = [&](int type, const void* w, size_t nb1, int64_t K, int64_t N, const uint8_t* xb, size_t xrow,
+                           float* dst) {
+        const size_t ob = (size_t) N * 4;
+        const qw::MmidArgs m = mmid_args(type, w, K, N, 1, nb1, nb1 * (size_t) N, xb, 1, xrow, rows, active,
+                                         active_off, n_active, 1, nullptr, 0, dst, ob, ob, T, T);
+        return mmid_launch(m, st);
+    };
+    if ((rc = proj_launch(L->type_q, L->wq, L->wq_nb1, H, NQ, xq, rq, q))) return rc;
+    if ((rc = proj_launch(L->type_k, L->wk, L->wk_nb1, H, NK, xk, rk, k))) return rc;
+    if ((rc = proj_launch(L->type_v, L->wv, L->wv_nb1, H, NK, xv, rv, v))) return rc;
+    qw::AttnArgs a{};
+    a.T = (int) T;
+    a.n_head = (int) nq;
+    a.n_head_kv = (int) nk;
+    a.n_past = n_past;
+    a.n_kv = n_kv;
+    a.eps = rms_eps;
+    a.theta_scale = powf(L->rope_freq_base, -2.0f / (float) L->n_rot);   // ggml_compute_forward_rope_flt
+    a.kq_scale = 1.0f / sqrtf((float) D);
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.q_norm = L->q_norm;
+    a.k_norm = L->k_norm;
+    a.qr = qr;
+    a.kc = L->k_cache;
+    a.vc = L->v_cache;
+    a.s = sc;
+    a.part = part;
+    a.att = att;
+    if ((rc = qw::launch_attn_core(a, st))) return rc;
+    const size_t qb = (size_t) NQ * 4;
+    if ((rc = qw::launch_quantize_act(vot, att, NQ, 1, T, qb, qb, aq, st))) return rc;
+    if ((rc = proj_launch(L->type_o, L->wo, L->wo_nb1, NQ, H, aq, ro, proj))) return rc;
+    return qw::launch_add_rms_norm_mul(proj, h, attn_resid, ffn_in, H, T, rms_eps, L->ffn_norm, st);
+}
+
+int qwmoe_decoder_layer(void* stream, const qwmoe_attn_layer* attn, const qwmoe_layer* moe, const float* h,
+                        int64_t T, int64_t n_past, float rms_eps, float* h_out, int32_t* ids_out,
+                        float* weights_out) {
+    if (!g_lib.ready) return QWMOE_ERR_NOT_INITIALIZED;
+    if (!attn || !moe || !h || !h_out || T < 0 || !(rms_eps >= 0.0f)) return QWMOE_ERR_INVALID_ARG;
+    if (moe->n_embd != attn->n_embd || !attn->ffn_norm) return QWMOE_ERR_INVALID_ARG;
+    if (T == 0) return QWMOE_OK;
+    const int64_t H = attn->n_embd;
+    Arena ar(kReserved);
+    float* resid = ar.take<float>((size_t) (H * T));
+    float* fin = ar.take<float>((size_t) (H * T));
+    float* moe_out = ar.take<float>((size_t) (H * T));
+    if (!resid || !fin || !moe_out) return QWMOE_ERR_WORKSPACE;
+    const ArenaFloor keep(ar.off);   // the calls below take their temporaries above these
+    int rc = qwmoe_attn_seg(stream, attn, h, T, n_past, rms_eps, resid, fin);
+    if (rc == QWMOE_OK) rc = qwmoe_ffn_layer(stream, moe, fin, T, moe_out, -1.0f, nullptr, ids_out, weights_out);
+    // h_new = moe_out + attn_resid (build_segB, core/runtime.cpp:2087)
+    if (rc == QWMOE_OK) rc = qw::launch_add_rms_norm_mul(moe_out, resid, h_out, nullptr, H, T, 0.0f, nullptr, S(stream));
+    return rc;
 }
 
 int qwmoe_ffn_layer(void* stream, const qwmoe_layer* L, const float* x, int64_t T, float* out, float rms_eps,

@@ -123,4 +123,30 @@ constexpr size_t kScratchBytes = (size_t) 8 << 20;
 int scratch_setup(int device);
 void* scratch_ptr(int device);
 
+// attn.hip: the attention half of Seg A (per-head norms, NEOX RoPE, f16 KV cache,
+// GQA scores, softmax, P.V), head dimension 128
+constexpr int ATT_RMAX = 16;      // query heads per kv head, at most
+constexpr int ATT_SPLIT = 512;    // keys per P.V partial sum
+struct AttnArgs {
+    int T, n_head, n_head_kv;
+    int64_t n_past, n_kv;         // n_kv = n_past + T keys after this call's rows are written
+    float eps, theta_scale, kq_scale;
+    const float* q;               // [T][n_head][128] projections
+    const float* k;               // [T][n_head_kv][128]
+    const float* v;               // [T][n_head_kv][128]
+    const float* q_norm;          // [128]
+    const float* k_norm;          // [128]
+    float* qr;                    // [T][n_head][128] Q after norm and RoPE
+    uint16_t* kc;                 // f16 caches [n_ctx][n_head_kv * 128], 16-byte aligned
+    uint16_t* vc;
+    float* s;                     // [T][n_head][n_kv] scores, then probabilities
+    float* part;                  // [ceil(n_kv / ATT_SPLIT)][T][n_head][128]
+    float* att;                   // [T][n_head * 128]
+};
+int launch_attn_core(const AttnArgs& a, hipStream_t stream);
+// resid = x + y; out = rms_norm(resid) * w (rows of n, dense), out may be null
+int launch_add_rms_norm_mul(const float* x, const float* y, float* resid, float* out, int64_t n, int64_t rows,
+                            float eps, const float* w, hipStream_t stream);
+int launch_fill_i32(int32_t* p, int64_t n, int32_t v, hipStream_t stream);
+
 }  // namespace qw

@@ -392,6 +392,53 @@ def ffn_layer(layer: Layer, x, rms_eps: float = -1.0):
     return out, xn, ids, w
 
 
+def make_attn_layer(H, n_head, n_head_kv, D, attn_norm, wq, wk, wv, wo, types, q_norm, k_norm, ffn_norm,
+                    k_cache, v_cache, rope_freq_base=1e6):
+    """Builds a ``qwmoe_attn_layer`` from device tensors (dense weight rows, f16
+    caches [n_ctx, n_head_kv * D] as int16/float16 tensors; the caller keeps
+    them alive).  types: (q, k, v, o) ggml type ids."""
+    from . import AttnLayer
+    tq, tk, tv, to = types
+    L = AttnLayer()
+    L.n_embd, L.n_head, L.n_head_kv, L.n_embd_head, L.n_rot = H, n_head, n_head_kv, D, D
+    L.rope_freq_base = rope_freq_base
+    L.attn_norm = _ptr(attn_norm)
+    L.type_q, L.type_k, L.type_v, L.type_o = tq, tk, tv, to
+    L.wq, L.wq_nb1 = _ptr(wq), row_size(tq, H)
+    L.wk, L.wk_nb1 = _ptr(wk), row_size(tk, H)
+    L.wv, L.wv_nb1 = _ptr(wv), row_size(tv, H)
+    L.wo, L.wo_nb1 = _ptr(wo), row_size(to, n_head * D)
+    L.q_norm, L.k_norm, L.ffn_norm = _ptr(q_norm), _ptr(k_norm), _ptr(ffn_norm)
+    L.k_cache, L.v_cache = _ptr(k_cache), _ptr(v_cache)
+    L.n_ctx = k_cache.shape[0]
+    return L
+
+
+def attn_seg(layer, h, n_past: int, rms_eps: float = 1e-6, want_ffn_in: bool = True):
+    """The attention half of Seg A for h f32 [T, H] at positions n_past ..:
+    (attn_resid, ffn_in or None); the layer's caches get rows n_past .. n_past + T - 1."""
+    torch = _torch()
+    T, H = h.shape
+    resid = torch.empty((T, H), dtype=torch.float32, device=h.device)
+    fin = torch.empty((T, H), dtype=torch.float32, device=h.device) if want_ffn_in else None
+    check(lib().qwmoe_attn_seg(stream(), C.byref(layer), _ptr(h), T, n_past, rms_eps, _ptr(resid), _ptr(fin)),
+          "attn_seg")
+    return resid, fin
+
+
+def decoder_layer(attn, moe: Layer, h, n_past: int, rms_eps: float = 1e-6):
+    """A whole Qwen3-MoE decoder layer for h f32 [T, H]: (h_out, ids, weights)."""
+    torch = _torch()
+    T, H = h.shape
+    k = moe.n_expert_used
+    out = torch.empty((T, H), dtype=torch.float32, device=h.device)
+    ids = torch.empty((T, k), dtype=torch.int32, device=h.device)
+    w = torch.empty((T, k), dtype=torch.float32, device=h.device)
+    check(lib().qwmoe_decoder_layer(stream(), C.byref(attn), C.byref(moe), _ptr(h), T, n_past, rms_eps, _ptr(out),
+                                    _ptr(ids), _ptr(w)), "decoder_layer")
+    return out, ids, w
+
+
 class Gguf(_Handle):
     """A GGUF model file (or shard set) opened through qwmoe_gguf_*: metadata on
     the host, MoE layers loaded into device memory on request."""

@@ -306,6 +306,83 @@ class SharedWeights:
         self.gate_inp = (rng.standard_normal(H) * 0.02).astype(np.float32)
 
 
+class AttnWeights:
+    """A Qwen3 attention block's weights, seeded: attn_q [n_head * D, H],
+    attn_k / attn_v [n_head_kv * D, H], attn_output [H, n_head * D] quantized
+    from N(0, 0.02) fp32 (types (q, k, v, o)); the f32 norms N(1, 0.1)."""
+
+    def __init__(self, H, n_head, n_head_kv, D, types, seed, oracle: Oracle, freq_base=1e6):
+        rng = np.random.default_rng(seed)
+        self.H, self.n_head, self.n_head_kv, self.D, self.types, self.freq_base = H, n_head, n_head_kv, D, types, freq_base
+        NQ, NK = n_head * D, n_head_kv * D
+        q = lambda t, r, c: oracle.quantize(t, (rng.standard_normal((r, c)) * 0.02).astype(np.float32))  # noqa: E731
+        self.wq, self.wk, self.wv = q(types[0], NQ, H), q(types[1], NK, H), q(types[2], NK, H)
+        self.wo = q(types[3], H, NQ)
+        nrm = lambda n: (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32)  # noqa: E731
+        self.attn_norm, self.ffn_norm, self.q_norm, self.k_norm = nrm(H), nrm(H), nrm(D), nrm(D)
+
+
+def attn_seg_restated(aw: AttnWeights, h, n_past: int, k_cache, v_cache, orc: Oracle, eps: float = 1e-6):
+    """Seg A's attention half (core/runtime.cpp:1976-2030, build_attn 681-734)
+    restated on the CPU: the projections are the oracle's quantized mul_mat (ggml's
+    row dots, bit for bit); the norms follow ggml_rms_norm (double sum); RoPE NEOX
+    with ggml_rope_cache_init's theta_{i+1} = theta_i * powf(base, -2/n_rot) in
+    fp32; K, V rounded to f16 into the caches; Q and the probabilities rounded to
+    f16 (the f16 mul_mat's vec_dot_type); the products and the softmax in float64.
+    Returns (attn_resid, ffn_in, q_roped, att); the caches are updated in place."""
+    h = np.ascontiguousarray(h, np.float32)
+    T, H = h.shape
+    nq, nk, D = aw.n_head, aw.n_head_kv, aw.D
+    R, NQ, NK = nq // nk, nq * D, nk * D
+
+    def mm(t, w, x, N):
+        return orc.mul_mat_id(t, x.shape[1], N, 1, w, x[:, None, :], np.zeros((x.shape[0], 1), np.int32))[:, 0, :]
+
+    cur = orc.rms_norm_mul(h, aw.attn_norm, eps)
+    Q = mm(aw.types[0], aw.wq, cur, NQ).reshape(T, nq, D)
+    K = mm(aw.types[1], aw.wk, cur, NK).reshape(T, nk, D)
+    V = mm(aw.types[2], aw.wv, cur, NK).reshape(T, nk, D)
+    Q = orc.rms_norm_mul(Q.reshape(-1, D), aw.q_norm, eps).reshape(T, nq, D)
+    K = orc.rms_norm_mul(K.reshape(-1, D), aw.k_norm, eps).reshape(T, nk, D)
+    scale = np.float32(np.power(np.float32(aw.freq_base), np.float32(-2.0) / np.float32(D), dtype=np.float32))
+    half = D // 2
+
+    def rope(x, pos):
+        th = np.zeros(half, np.float32)
+        t_ = np.float32(pos)
+        for i in range(half):
+            th[i] = t_
+            t_ = np.float32(t_ * scale)
+        c = np.cos(th.astype(np.float64)).astype(np.float32)
+        s_ = np.sin(th.astype(np.float64)).astype(np.float32)
+        x0, x1 = x[..., :half], x[..., half:]
+        return np.concatenate([x0 * c - x1 * s_, x0 * s_ + x1 * c], axis=-1).astype(np.float32)
+
+    Q = np.stack([rope(Q[t], n_past + t) for t in range(T)])
+    K = np.stack([rope(K[t], n_past + t) for t in range(T)])
+    k_cache[n_past:n_past + T] = K.reshape(T, NK).astype(np.float16).view(np.uint16)
+    v_cache[n_past:n_past + T] = V.reshape(T, NK).astype(np.float16).view(np.uint16)
+    n_kv = n_past + T
+    Kc = k_cache[:n_kv].view(np.float16).astype(np.float64).reshape(n_kv, nk, D)
+    Vc = v_cache[:n_kv].view(np.float16).astype(np.float64).reshape(n_kv, nk, D)
+    att = np.zeros((T, nq, D), np.float32)
+    kq_scale = np.float32(1.0 / np.sqrt(np.float32(D)))
+    for t in range(T):
+        for hh in range(nq):
+            g = hh // R
+            q16 = Q[t, hh].astype(np.float16).astype(np.float64)
+            sc = (Kc[:, g, :] @ q16).astype(np.float32) * kq_scale
+            sc[n_past + t + 1:] = -np.inf
+            e = np.exp(sc.astype(np.float64) - sc.max())
+            p = (e / e.sum()).astype(np.float32).astype(np.float16).astype(np.float64)
+            att[t, hh] = (p @ Vc[:, g, :]).astype(np.float32)
+    att = att.reshape(T, NQ)
+    proj = mm(aw.types[3], aw.wo, att, H)
+    resid = (proj + h).astype(np.float32)
+    fin = orc.rms_norm_mul(resid, aw.ffn_norm, eps)
+    return resid, fin, Q.reshape(T, NQ), att
+
+
 class RefGGML:
     def __init__(self, path: Path = REF_SO):
         if not path.exists():
@@ -332,6 +409,26 @@ class RefGGML:
                                               + [C.c_int])
         L.qwref_router_resident.argtypes = ([C.c_int64] * 4 + [C.c_void_p] * 3 + [C.c_float] + [C.c_void_p] * 4
                                             + [C.c_int])
+        L.qwref_attn_seg.argtypes = ([C.c_int64] * 5 + [C.c_float] * 2 + [C.c_int64] * 3 + [C.c_void_p] * 2
+                                     + [C.c_int, C.c_void_p] * 4 + [C.c_void_p] * 9 + [C.c_int])
+
+    def attn_seg(self, aw, h, n_past: int, k_cache, v_cache, eps: float = 1e-6, n_threads: int = 4):
+        """ggml's Seg A attention half (build_segA + build_attn, manual path) on
+        AttnWeights aw: (attn_resid, ffn_in, q_roped, att); k_cache / v_cache
+        (uint16 [n_ctx, n_head_kv * D]) are updated in place."""
+        h = np.ascontiguousarray(h, np.float32)
+        T, H = h.shape
+        NQ = aw.n_head * aw.D
+        resid, fin = np.zeros((T, H), np.float32), np.zeros((T, H), np.float32)
+        qo, att = np.zeros((T, NQ), np.float32), np.zeros((T, NQ), np.float32)
+        assert k_cache.flags.c_contiguous and v_cache.flags.c_contiguous
+        rc = self.lib.qwref_attn_seg(H, aw.n_head, aw.n_head_kv, aw.D, aw.D, aw.freq_base, eps, T, n_past,
+                                     k_cache.shape[0], _p(h), _p(aw.attn_norm), aw.types[0], _p(aw.wq), aw.types[1],
+                                     _p(aw.wk), aw.types[2], _p(aw.wv), aw.types[3], _p(aw.wo), _p(aw.q_norm),
+                                     _p(aw.k_norm), _p(aw.ffn_norm), _p(k_cache), _p(v_cache), _p(resid), _p(fin),
+                                     _p(qo), _p(att), n_threads)
+        assert rc == 0, rc
+        return resid, fin, qo, att
 
     def router_resident(self, W, x, k: int, mask, scale: float = 0.0, n_threads: int = 2):
         """ggml's resident-only router: ids, weights, want (unmasked top k), probs."""
