@@ -66,7 +66,32 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
+    build_ggml_backend()
     return LIB
+
+
+# The ggml backend plugin (ggml_backend/ggml-qwmoe.cpp) compiles against the
+# ggml headers of the tree it plugs into: QWMOE_GGML_DIR, by default the
+# reference's vendored ggml.  It links libqwmoe.so; ggml's own symbols are left
+# to the process's ggml, as for ggml's dynamically loaded backends.
+GGML_DIR = Path(os.environ.get("QWMOE_GGML_DIR", "/root/reference/third_party/ggml"))
+GGML_LIB = PKG / "libggml-qwmoe.so"
+
+
+def build_ggml_backend() -> Path | None:
+    if not (GGML_DIR / "src" / "ggml-backend-impl.h").exists():
+        return None
+    src = PKG / "ggml_backend" / "ggml-qwmoe.cpp"
+    inc = PKG.parent / "include"
+    tmp = GGML_LIB.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", f"-I{GGML_DIR / 'include'}",
+           f"-I{GGML_DIR / 'src'}", f"-I{inc}", str(src), "-o", str(tmp), f"-L{PKG}", "-lqwmoe",
+           "-Wl,-rpath,$ORIGIN"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"ggml backend build failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, GGML_LIB)
+    return GGML_LIB
 
 
 if __name__ == "__main__":

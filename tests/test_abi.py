@@ -125,3 +125,26 @@ def test_ggml_glue_header_compiles(tmp_path, lang):
     root = Path(__file__).resolve().parents[1]
     subprocess.run([cc, "-fsyntax-only", "-Wall", "-Werror", "-x", lang, "-I", "/root/reference/third_party/ggml/include",
                     "-I", str(root / "include"), str(src)], check=True)
+
+
+GGML_HEADER = Path(__file__).resolve().parents[1] / "include" / "ggml-qwmoe.h"
+GGML_PLUGIN = Path(__file__).resolve().parents[1] / "questwend_amd" / "libggml-qwmoe.so"
+
+
+def test_ggml_backend_plugin_exports_its_header():
+    """The ggml backend plugin exports what include/ggml-qwmoe.h declares and
+    leaves only ggml's own API to the host process (no GPU needed: the registry
+    reports the devices HIP sees, none here)."""
+    if not GGML_PLUGIN.exists():
+        pytest.skip("libggml-qwmoe.so is built only where the ggml headers are present")
+    text = re.sub(r"/\*.*?\*/", "", GGML_HEADER.read_text(), flags=re.S)
+    names = sorted(set(re.findall(r"\b(ggml_backend_(?:qwmoe|is_qwmoe)[a-z0-9_]*)\s*\(", text)))
+    assert names == ["ggml_backend_is_qwmoe", "ggml_backend_qwmoe_init", "ggml_backend_qwmoe_reg"]
+    qa.lib()
+    from oracle_lib import REF_SO, have_ref
+    if not have_ref():
+        pytest.skip("the plugin resolves ggml's symbols from a loaded ggml (oracle/_ref)")
+    C.CDLL(str(REF_SO), mode=C.RTLD_GLOBAL)
+    plugin = C.CDLL(str(GGML_PLUGIN))
+    for n in names:
+        assert hasattr(plugin, n)
