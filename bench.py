@@ -36,15 +36,42 @@ KERNEL_NAMES = {1: "k_decode_stack<8,3,Q4_K>", 2: "k_decode_xcd<8,3,4> (XCD-loca
                 5: "k_decode_xcd_wide<16,6,4,Q6_K> (device-scope exchange words)"}
 
 
+# The sources of the headline kernel: a counter summary under profiles/ holds
+# their SHA-256 beside its bytes, and its traffic is reported only for them.
+KERNEL_SOURCES = ["decode_xcd.hip", "qw_xcd.hpp", "qw_decode.hpp", "qw_kernels.hpp", "qw_common.hpp", "qw_sort.hpp"]
+
+
+def kernel_sources_sha256() -> str:
+    import hashlib
+    h = hashlib.sha256()
+    for name in KERNEL_SOURCES:
+        h.update((ROOT / "questwend_amd" / "csrc" / name).read_bytes())
+    return h.hexdigest()
+
+
 def measured_traffic(path: str):
-    """HBM bytes per decode launch from a committed rocprofv3 counter summary, or None."""
+    """(HBM bytes per decode launch, note) from a committed rocprofv3 counter
+    summary: the bytes only when the summary's kernel_sources_sha256 matches the
+    sources built here, else (None, why)."""
     try:
-        for line in Path(path).read_text().splitlines():
-            if line.strip().startswith("hbm_bytes_per_launch"):
-                return int(float(line.split("=", 1)[1].split()[0]))
-    except (OSError, ValueError, IndexError):
-        pass
-    return None
+        lines = Path(path).read_text().splitlines()
+    except OSError:
+        return None, f"no counter summary at {path}"
+    val, sha = None, None
+    for line in lines:
+        t = line.strip()
+        try:
+            if t.startswith("hbm_bytes_per_launch"):
+                val = int(float(t.split("=", 1)[1].split()[0]))
+            elif t.startswith("kernel_sources_sha256"):
+                sha = t.split("=", 1)[1].split()[0]
+        except (ValueError, IndexError):
+            pass
+    if val is None:
+        return None, "the counter summary holds no hbm_bytes_per_launch"
+    if sha != kernel_sources_sha256():
+        return None, "the counter summary was measured on other kernel sources (stale); re-measure"
+    return val, f"rocprofv3 FETCH_SIZE + WRITE_SIZE, scaled by the copy probe ({Path(path).name})"
 
 
 def algorithmic_bytes_per_token() -> int:
@@ -282,8 +309,9 @@ def prefill(args) -> int:
     ops.randn_(x, args.seed + 555, 0.0, 1.0)
     torch.cuda.synchronize()
 
-    def timed(min_rows: int, form: int = ops.MFMA_AUTO):
-        prev, prev_f = ops.set_mfma_min_rows(min_rows), ops.set_mfma_form(form)
+    def timed(min_rows: int, form: int | None = None):
+        prev = ops.set_mfma_min_rows(min_rows)
+        prev_f = ops.set_mfma_form(form) if form is not None else None
         try:
             for _ in range(args.warmup):
                 ops.ffn_layer(L, x, rms_eps=RMS_EPS)
@@ -300,24 +328,25 @@ def prefill(args) -> int:
             return wall / args.steps, sum(a.elapsed_time(b) for a, b in evs) / args.steps / 1000.0, r
         finally:
             ops.set_mfma_min_rows(prev)
-            ops.set_mfma_form(prev_f)
+            if prev_f is not None:
+                ops.set_mfma_form(prev_f)
 
-    step_s, ev_s, (out, xn, ids, w) = timed(args.mfma_min_rows)
-    exact_s, _, (out_x, _, _, _) = timed(args.mfma_min_rows, ops.MFMA_EXACT)
+    step_s, ev_s, (out, xn, ids, w) = timed(args.mfma_min_rows)          # the library default: exact
+    auto_s, _, (out_a, _, _, _) = timed(args.mfma_min_rows, ops.MFMA_AUTO)
     bs_s, _, (out_b, _, _, _) = timed(args.mfma_min_rows, ops.MFMA_BLOCK_SUM)
     gemv_s, _, (out_g, _, _, _) = timed(0)
 
     def rel(a):   # vs the GEMV, which (like the exact matrix-core form) replays ggml's float steps
         return float(f"{float((a.double() - out_g.double()).abs().max() / out_g.double().abs().max().clamp_min(1e-30)):.3e}")
 
-    same = bool(torch.equal(out_x.view(torch.int32), out_g.view(torch.int32)))
+    same = bool(torch.equal(out.view(torch.int32), out_g.view(torch.int32)))
     counts = np.bincount(ids.cpu().numpy().reshape(-1), minlength=E)
     expert_bytes = 2 * F * row_size(Q4_K, H) + H * row_size(Q4_K, F)
     wbytes = int((counts > 0).sum()) * expert_bytes + E * H * 4          # unique weights touched + router
     macs = T * K_USED * (2 * F * H + H * F)                               # int8 MACs of the three projections
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = prefill_cpu_baseline(L, mats, router, x, T)
+        cpu = prefill_cpu_baseline(host_layer_weights(router, *mats, (Q4_K,) * 3, H, E, K_USED, F), x, T)
     line = {
         "metric": "prefill tok/s + achieved HBM GB/s and int8 MFMA rate, Q4_K MoE FFN layer 30B-A3B",
         "value": round(T / step_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -325,17 +354,17 @@ def prefill(args) -> int:
         "dtype": "q4_K x q8_K -> int32 (MFMA i8) -> f32", "data": "synthetic (seeded, router Zipf(1.1)-skewed)",
         "config": {"workload": "Qwen3-30B-A3B MoE FFN layer, prefill T=512 (configs[2])", "n_embd": H,
                    "n_expert": E, "n_expert_used": K_USED, "n_ff_exp": F, "tokens": T, "weights": "Q4_K",
-                   "path": f"qwmoe_ffn_layer (mfma_min_rows {args.mfma_min_rows}, auto matrix-core form: "
-                           "gate/up lane-exact, down block sums)"},
+                   "path": f"qwmoe_ffn_layer (mfma_min_rows {args.mfma_min_rows}, the default exact matrix-core "
+                           "form: ggml's bits)"},
         "rows_per_expert": {**row_count_profile(counts), "ge32": int((counts >= 32).sum())},
         "roofline": {"bound": "hbm", "achieved": round(wbytes / ev_s / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(wbytes / ev_s / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
                      "bytes_per_step": wbytes, "avg_step_ms": round(ev_s * 1e3, 4),
                      "int8_mac_rate_tops": round(macs / ev_s / 1e12, 2),
                      "int8_mac_frac_of_2500_tmacs": round(macs / ev_s / 2.5e15, 4)},
-        "rel_err_vs_gemv": rel(out),
-        "exact_mfma_ms_per_step": round(exact_s * 1e3, 4),
         "exact_mfma_equals_gemv_bitwise": same,
+        "auto_form_ms_per_step": round(auto_s * 1e3, 4),
+        "auto_form_rel_err_vs_gemv": rel(out_a),
         "block_sum_everywhere_ms_per_step": round(bs_s * 1e3, 4),
         "block_sum_everywhere_rel_err_vs_gemv": rel(out_b),
         "gemv_only_ms_per_step": round(gemv_s * 1e3, 4),
@@ -394,21 +423,16 @@ def host_layer_weights(router, gate, up, down, types, H_, E_, k_, F_):
     return lw
 
 
-def prefill_cpu_baseline(L, mats, router, x, T: int):
-    """The reference ggml CPU backend (oracle/_ref) on the same layer and batch:
-    one evaluation of the T-token graph on 16 host threads."""
+def prefill_cpu_baseline(lw, x, T: int):
+    """The reference ggml CPU backend (oracle/_ref) on the same layer (host
+    weights lw) and batch: evaluations of the T-token graph for about 10 s on
+    the physical cores of one socket."""
     sys.path.insert(0, str(ROOT / "tests"))
-    from oracle_lib import REF_SO, LayerWeights, RefGGML
-    from questwend_amd import Q4_K
+    from oracle_lib import REF_SO, RefGGML
     if not REF_SO.exists():
         return None
-    lw = LayerWeights.__new__(LayerWeights)
-    lw.H, lw.E, lw.k, lw.F = H, E, K_USED, F
-    lw.type_gate = lw.type_up = lw.type_down = Q4_K
-    lw.router = router.cpu().numpy()
-    lw.gate, lw.up, lw.down = (m.cpu().numpy().reshape(-1) for m in mats)
-    lw.n_slots, lw.slot_of = E, None
-    n_thr = min(16, os.cpu_count() or 1)
+    cpu = host_cpu()
+    n_thr = max(1, min(cpu["cores_per_socket"], cpu["cpus_available"]))
     run = RefGGML().layer(lw, T, rms_eps=RMS_EPS, n_threads=n_thr)
     xh = x.cpu().numpy()
     run(xh, n_threads=n_thr)
@@ -419,7 +443,34 @@ def prefill_cpu_baseline(L, mats, router, x, T: int):
         reps += 1
     dt = (time.perf_counter() - t0) / reps
     return {"value": round(T / dt, 2), "unit": "tok/s", "cores": n_thr, "kind": "reference",
-            "sample": f"{reps} evaluations of the T={T} layer graph in {dt * reps:.1f}s"}
+            "sample": f"{reps} evaluations of the T={T} layer graph in {dt * reps:.1f}s", "ms_per_layer": round(dt * 1e3, 3)}
+
+
+def verify_cpu_protocol(lw, T: int, n_steps: int, rho: float, seed: int):
+    """configs[3]'s protocol on the reference ggml CPU backend: n_steps seeded
+    batches of T tokens, N(0,1) correlated at rho, through one layer (lw); each
+    step timed with perf_counter; median and p90 per step."""
+    import numpy as np
+    sys.path.insert(0, str(ROOT / "tests"))
+    from oracle_lib import REF_SO, REF_SO_AVX512, RefGGML, have_ref_avx512
+    if not REF_SO.exists():
+        return None
+    cpu = host_cpu()
+    n_thr = max(1, min(cpu["cores_per_socket"], cpu["cpus_available"]))
+    ref = RefGGML(REF_SO_AVX512 if have_ref_avx512() else REF_SO)
+    run = ref.layer(lw, T, rms_eps=RMS_EPS, n_threads=n_thr)
+    rng = np.random.default_rng(seed)
+    times = []
+    for i in range(n_steps + 8):
+        c = rng.standard_normal(lw.H)
+        x = (np.sqrt(rho) * c + np.sqrt(1.0 - rho) * rng.standard_normal((T, lw.H))).astype(np.float32)
+        t0 = time.perf_counter()
+        run(x)
+        if i >= 8:
+            times.append(time.perf_counter() - t0)
+    med, p90 = float(np.median(times)), float(np.percentile(times, 90))
+    return {"median_ms_per_layer": round(med * 1e3, 4), "p90_ms_per_layer": round(p90 * 1e3, 4), "cores": n_thr,
+            "isa": "AVX-512" if ref.isa() == 512 else "AVX2", "steps": n_steps, "T": T}
 
 
 def expert_cache_bench(args) -> int:
@@ -632,8 +683,16 @@ def verify_bench(args) -> int:
     last = rows[-1]
     cpu = None
     if not args.no_cpu_baseline:
-        lws = [host_layer_weights(*ly, (Q4_K,) * 3, H, E, K_USED, F) for ly in layers]
-        cpu = cpu_chain_baseline(lws, xs[:16].cpu().numpy(), Tmax, N_LAYER)
+        # 1000 seeded T-token batches through one layer, on the reference
+        # CPU backend; the line's tok/s for the 48-layer stack from its median
+        proto = verify_cpu_protocol(host_layer_weights(*layers[0], (Q4_K,) * 3, H, E, K_USED, F), Tmax, 1000, 0.8,
+                                    args.seed)
+        if proto:
+            med = proto["median_ms_per_layer"] * N_LAYER / 1e3
+            cpu = {"value": round(Tmax / med, 2), "unit": "tok/s", "cores": proto["cores"], "kind": "reference",
+                   "sample": f"configs[3]: 1000 seeded batches of T={Tmax} correlated tokens (rho 0.8) through one "
+                             f"layer, 8 warm-up; tok/s = T / ({N_LAYER} x median layer time)",
+                   "protocol": proto}
     kname = {1: "the per-layer chain (captured graph)", 2: "k_verify_xcd<8,3,4> (XCD-local exchange words)",
              3: "k_verify_xcd<8,3,4> (device-scope exchange words)"}.get(stack.kernel(), "?")
     line = {
@@ -770,23 +829,28 @@ def config5_bench(args) -> int:
         finally:
             ops.set_mfma_form(prev)
 
-    pre_s, (out, _, ids, _) = prefill_s(ops.MFMA_AUTO)
-    pre_exact_s, (out_x, _, _, _) = prefill_s(ops.MFMA_EXACT)
+    pre_s, (out_x, _, ids, _) = prefill_s(ops.MFMA_EXACT)          # the library default
+    pre_auto_s, (out, _, _, _) = prefill_s(ops.MFMA_AUTO)
+    pre_bs_s, (out_b, _, _, _) = prefill_s(ops.MFMA_BLOCK_SUM)
     pre_rel = float((out.double() - out_x.double()).abs().max() / out_x.double().abs().max().clamp_min(1e-30))
-    used = int((np.bincount(ids.cpu().numpy().reshape(-1), minlength=E5) > 0).sum())
-    cpu = None
+    pre_rel_bs = float((out_b.double() - out_x.double()).abs().max() / out_x.double().abs().max().clamp_min(1e-30))
+    counts5 = np.bincount(ids.cpu().numpy().reshape(-1), minlength=E5)
+    used = int((counts5 > 0).sum())
+    cpu = pre_cpu = None
     if not args.no_cpu_baseline:
-        # decode on the CPU: a sample of 4 of the 94 layers (logical expert order:
-        # the slot permutation undone), their per-token time scaled to 94
-        lws = []
-        for l in range(min(4, NL5)):
+        # decode on the CPU: a sample of 24 of the 94 layers, 1..24 (logical expert
+        # order: the slot permutation undone; 37 GB of host memory), their per-token
+        # time scaled to 94.  (Layer 0's router now carries the prefill's Zipf skew.)
+        def host_logical(l):
             router_l, mats_l, slots_l = keep[l]
             logical = [m.view(E5, -1)[sl.long()] for m, sl in zip(mats_l, slots_l)]
-            lws.append(host_layer_weights(router_l, *logical, types, H5, E5, K5, F5))
-            del logical
+            return host_layer_weights(router_l, *logical, types, H5, E5, K5, F5)
+        lws = [host_logical(l) for l in range(1, min(25, NL5))] if NL5 > 1 else [host_logical(0)]
         cpu = cpu_chain_baseline(lws, xs[:16].view(-1, 1, H5).cpu().numpy(), 1, NL5)
         del lws
+        pre_cpu = prefill_cpu_baseline(host_logical(0), x, T5)   # layer 0 (Zipf router) at T = 1024
     pre_bytes = used * expert5 + E5 * H5 * 4
+    pre_macs = T5 * K5 * (2 * F5 * H5 + H5 * F5)
     line = {
         "metric": "configs[4] decode tok/s (94-layer stack, batch 1) and prefill tok/s (T=1024, one layer)",
         "value": round(1.0 / dec_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -804,10 +868,20 @@ def config5_bench(args) -> int:
                    "layer_stack_t1_tok_s": round(1.0 / ls_s, 2),
                    "equals_layer_stack_bitwise_8_tokens": bool(same)},
         "prefill": {"tokens": T5, "ms_per_layer": round(pre_s * 1e3, 3), "tok_s": round(T5 / pre_s, 1),
-                    "used_experts": used, "weight_gbps": round(pre_bytes / pre_s / 1e9, 1),
-                    "form": "auto (gate/up lane-exact, down block sums on the matrix cores)",
-                    "exact_form_ms_per_layer": round(pre_exact_s * 1e3, 3),
-                    "rel_err_vs_exact_form": float(f"{pre_rel:.3e}")},
+                    "used_experts": used, "rows_per_expert": row_count_profile(counts5),
+                    "form": "exact (the library default: ggml's bits)",
+                    "auto_form_ms_per_layer": round(pre_auto_s * 1e3, 3),
+                    "auto_form_rel_err_vs_exact": float(f"{pre_rel:.3e}"),
+                    "block_sum_form_ms_per_layer": round(pre_bs_s * 1e3, 3),
+                    "block_sum_form_rel_err_vs_exact": float(f"{pre_rel_bs:.3e}"),
+                    "roofline": {"bound": "hbm", "achieved": round(pre_bytes / pre_s / 1e9, 1), "peak": HBM_PEAK_GBS,
+                                 "unit": "GB/s", "frac": round(pre_bytes / pre_s / 1e9 / HBM_PEAK_GBS, 4),
+                                 "traffic": None, "bytes_per_layer": pre_bytes,
+                                 "int8_mac_rate_tops": round(pre_macs / pre_s / 1e12, 2),
+                                 "int8_mac_frac_of_2500_tmacs": round(pre_macs / pre_s / 2.5e15, 4),
+                                 "note": "used experts' weights + router once per layer / wall time per layer; "
+                                         "MACs of the three projections (int8 MFMA peak 5.0 POP/s = 2.5 P MAC/s)"},
+                    "cpu_baseline": pre_cpu},
         "roofline": {"bound": "hbm", "achieved": round(dec_bytes / kern_ms / 1e6, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(dec_bytes / kern_ms / 1e6 / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": KERNEL_NAMES.get(dstack.kernel(), "?") + f" (one launch = one token through {NL5} layers)",
@@ -923,6 +997,7 @@ def main() -> int:
     tok_s = args.steps / wall
     abytes = algorithmic_bytes_per_token()
     achieved = abytes / (kern_ms / 1000.0) / 1e9
+    traffic, traffic_note = measured_traffic(args.traffic)
 
     cpu, parity = None, None
     if not args.no_cpu_baseline:
@@ -953,9 +1028,10 @@ def main() -> int:
         "hbm_gbs": round(abytes * tok_s / 1e9, 1),
         "hbm_frac": round(abytes * tok_s / 1e9 / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.traffic),
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": KERNEL_NAMES.get(stack.kernel(), "?") + " (one launch = one token through 48 layers)",
-                     "bytes_per_launch": abytes, "avg_launch_ms": round(kern_ms, 4)},
+                     "bytes_per_launch": abytes, "avg_launch_ms": round(kern_ms, 4),
+                     "traffic_source": traffic_note, "kernel_sources_sha256": kernel_sources_sha256()[:16]},
         "cpu_baseline": cpu,
         "parity_vs_reference_cpu": parity,
         "device_status": status,
