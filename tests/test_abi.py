@@ -5,6 +5,8 @@ from __future__ import annotations
 
 import ctypes as C
 import re
+import subprocess
+import sys
 from pathlib import Path
 
 import numpy as np
@@ -144,7 +146,11 @@ def test_ggml_backend_plugin_exports_its_header():
     from oracle_lib import REF_SO, have_ref
     if not have_ref():
         pytest.skip("the plugin resolves ggml's symbols from a loaded ggml (oracle/_ref)")
-    C.CDLL(str(REF_SO), mode=C.RTLD_GLOBAL)
-    plugin = C.CDLL(str(GGML_PLUGIN))
-    for n in names:
-        assert hasattr(plugin, n)
+    # In a child process: a ggml loaded RTLD_GLOBAL here would interpose its
+    # symbols on every ggml build the later tests load (the AVX-512 one).
+    code = ("import ctypes as C, sys\n"
+            f"C.CDLL({str(REF_SO)!r}, mode=C.RTLD_GLOBAL)\n"
+            f"p = C.CDLL({str(GGML_PLUGIN)!r})\n"
+            f"sys.exit(0 if all(hasattr(p, n) for n in {names!r}) else 3)\n")
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr[-2000:]
