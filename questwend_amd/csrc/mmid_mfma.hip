@@ -660,12 +660,256 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
 }
 
+// Q6_K x Q8_K on the matrix cores, bit-identical to ggml: the exact form.
+//
+// ggml_vec_dot_q6_K_q8_K's AVX2 branch (quants.c:2426-2508) keeps eight int32
+// lanes per (weight row, activation row, super-block),
+//     sumi_L = sum_{g<8} sc[2 g + (L >= 4)] * sum_{e<4} q6[32 g + 4 L + e] * q8[32 g + 4 L + e]
+//              - 32 (sc[2 L] bsum[2 L] + sc[2 L + 1] bsum[2 L + 1])
+// with q6 in [0, 63] (maddubs on the unsigned 6-bit values, madd with the
+// sub-block scale; q8sclsub), then acc_L = fma(y.d * fp16(x.d), (float) sumi_L,
+// acc_L) over the super-blocks and hsum_float_8(acc).  Element 32 g + l of a
+// block is the dequantize_row_q6_K element 128 n + 32 c + l with g = 4 n + c.
+//
+// sc * q6 does not fit int8, so each product v enters A as two base-64 digits:
+// v = 64 hi + lo, lo in [-32, 31], hi in [-126, 125].  The bsum term is a
+// contraction over the 32 elements of sub-blocks 2 L, 2 L + 1 (storage order)
+// with -32 sc = 64 h + l, h = floor(-sc / 2) in [-64, 64], l = 32 (sc & 1).
+// Per AVX lane L and 16 x 16 tile, two v_mfma_i32_16x16x64_i8:
+//     D_hi = [hi of lane L's 32 products | h] . [q8 of lane L's elements | q8 of 32 L .. 32 L + 31]
+//     D_lo = [lo | l] . (same B)
+//     sumi_L = 64 D_hi + D_lo
+// (Two independent contractions from zero: no matrix-core result feeds another
+// of a different shape.)
+// A lane l holds weight row l % 16, B lane l activation row l % 16; byte
+// positions 0..7 of both are lane L's elements of segments g = 2 gq, 2 gq + 1
+// (gq = l / 16: the k-slots of the Q4_K exact form), positions 8..15 the
+// elements 32 L + 8 gq .. +8 of the bsum term (sub-block 2 L + gq / 2).  Any
+// assignment of elements to (lane group, byte) that A and B share gives the
+// same contraction.  The float steps then follow ggml lane for lane.
+//
+// Workgroup: 64 weight rows (a wave per 16) x one work item of 16 NB routed
+// activation rows; staging as k_mmid_mfma_q4k (three stage buffers, two
+// super-blocks ahead), blocks staged as in k_mmid_mfma_q6k (53 dwords from the
+// dword at or below the block's start; the fp16 d from a 16-bit copy).
+constexpr int MX_NB = 2;   // activation tiles per pass of the exact Q6_K form
+
+// Base-64 digits of v = s * q for the four bytes q of w (each 0..63), s in
+// [-128, 127]: v = 64 hi + lo with lo in [-32, 31], hi in [-126, 125]
+// (hi = (v + 32) >> 6), returned as four signed bytes each.  Packed 16-bit
+// multiply-adds: the low 16 bits of v + 32 are exact (|v| < 2^13).
+__device__ __forceinline__ void q6_digits(uint32_t w, int s, uint32_t& hi, uint32_t& lo) {
+    typedef short s16x2m __attribute__((ext_vector_type(2)));
+    const u16x2m ss = {(unsigned short) s, (unsigned short) s}, c32 = {32, 32}, m63 = {63, 63};
+    const u16x2m e = __builtin_bit_cast(u16x2m, w & 0x00FF00FFu) * ss + c32;
+    const u16x2m o = __builtin_bit_cast(u16x2m, (w >> 8) & 0x00FF00FFu) * ss + c32;
+    const uint32_t he = __builtin_bit_cast(uint32_t, __builtin_bit_cast(s16x2m, e) >> (short) 6);
+    const uint32_t ho = __builtin_bit_cast(uint32_t, __builtin_bit_cast(s16x2m, o) >> (short) 6);
+    const uint32_t le = __builtin_bit_cast(uint32_t, (u16x2m) ((e & m63) - c32));
+    const uint32_t lo_ = __builtin_bit_cast(uint32_t, (u16x2m) ((o & m63) - c32));
+    hi = (he & 0x00FF00FFu) | ((ho & 0x00FF00FFu) << 8);
+    lo = (le & 0x00FF00FFu) | ((lo_ & 0x00FF00FFu) << 8);
+}
+
+template <int NB>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) k_mmid_mfma_q6k_x(MmidArgs m) {
+    constexpr int NR = 16 * NB;                  // activation rows per pass (and per item)
+    constexpr int WDMA = MF_M * 53 / 64;         // weight DMA instructions per stage (64 rows x 53 dwords)
+    constexpr int WDW = (WDMA + 3) / 4;          // ... per wave, at most
+    constexpr int AW = (NR * MF_AD + 63) / 64;   // activation DMA instructions per stage
+    constexpr int AWW = (AW + 3) / 4;
+    constexpr int VM_STAGE = WDMA / 4 + AW / 4;  // fewest DMA instructions any wave issues per stage
+    static_assert(MF_M * 53 % 64 == 0 && 2 * (WDW + 1 + AWW) <= 63, "staging shape");
+    __shared__ __align__(16) uint8_t s_w0[MF_M * M6_WS];
+    __shared__ __align__(16) uint8_t s_w1[MF_M * M6_WS];
+    __shared__ __align__(16) uint8_t s_w2[MF_M * M6_WS];
+    __shared__ __align__(16) uint8_t s_a0[AW * 256];   // NR * MF_AS and the last instruction's slack
+    __shared__ __align__(16) uint8_t s_a1[AW * 256];
+    __shared__ __align__(16) uint8_t s_a2[AW * 256];
+    __shared__ __align__(16) uint32_t s_d0[MF_M];      // fp16 d of each staged weight row (zero-extended dword)
+    __shared__ __align__(16) uint32_t s_d1[MF_M];
+    __shared__ __align__(16) uint32_t s_d2[MF_M];
+    __shared__ int32_t s_arow[NR];
+    __shared__ int32_t s_et[NR][2];
+    __shared__ int s_item[2];
+    const int tiles = (int) (m.N / MF_M);
+    const int tile = (int) (blockIdx.x % (uint32_t) tiles);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    mf_item(m, (int) (blockIdx.x / (uint32_t) tiles), NR, wave, lane, s_item);
+    const int g = s_item[0];
+    if (g < 0) return;   // past the last item (light experts have none: the GEMV kernel's)
+    const int p0 = m.active_off[g] + NR * s_item[1], p1 = min(m.active_off[g + 1], p0 + NR);
+    const int bin = m.active[g];
+    int64_t mat = bin;
+    if (m.slot_of) mat = (bin < m.n_slot_of) ? m.slot_of[bin] : -1;
+    if (mat < 0 || mat >= m.n_as) {
+        if (threadIdx.x == 0 && m.status) atomicOr(m.status, 4);
+        return;
+    }
+    const int64_t r0 = (int64_t) tile * MF_M;
+    const int nb = (int) (m.K / QK_K);
+    const uint32_t nb1 = (uint32_t) m.nb1;
+    const uint8_t* wtile = m.w + (size_t) mat * m.nb2 + (size_t) r0 * m.nb1;
+    const i32x4 wrsrc = rsrc_words(wtile, (uint32_t) MF_M * nb1);
+    const i32x4 arsrc = rsrc_words(m.act_q, 0x7fffffffu);
+    const int ntok = p1 - p0;   // 1 .. NR
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    if (tid < NR) {
+        const int pp = p0 + (tid < ntok ? tid : 0);   // rows past ntok are staged from row 0, never written
+        const int e = m.rows[2 * pp], t = m.rows[2 * pp + 1];
+        s_et[tid][0] = e;
+        s_et[tid][1] = t;
+        s_arow[tid] = (int) ((int64_t) (e % m.b_ne1) + (int64_t) t * m.b_ne1);
+    }
+    lds_barrier();
+    // weight slot q = 64 j + lane: row q / 53, dword u = q % 53 (as k_mmid_mfma_q6k)
+    uint32_t wbase[WDW], aoff[AWW];
+#pragma unroll
+    for (int k = 0; k < WDW; ++k) {
+        const int q = 64 * (wave + 4 * k) + lane;
+        const int qc = q < MF_M * 53 ? q : 0;
+        const int row = qc / 53, u = qc - 53 * row;
+        wbase[k] = (uint32_t) row * nb1 + 4u * (uint32_t) u + (u == 52 ? 1u : 0u);
+    }
+#pragma unroll
+    for (int k = 0; k < AWW; ++k) {
+        const int sl = 64 * (wave + 4 * k) + lane;
+        const int slc = sl < NR * MF_AD ? sl : 0;
+        const int n = slc / MF_AD, u = slc - MF_AD * n;
+        aoff[k] = (uint32_t) s_arow[n] * (uint32_t) m.act_row_bytes + (u < 4 || u >= 68 ? 0u : 4u * (uint32_t) u - 12u);
+    }
+    const uint32_t dvoff = (uint32_t) lane * nb1 + 208u;   // the fp16 d of row `lane`
+    auto issue = [&](uint8_t* sw, uint8_t* sa, uint32_t* sd, int i) __attribute__((always_inline)) {
+        uint32_t lw = (uint32_t) (uintptr_t) sw, la = (uint32_t) (uintptr_t) sa, ld = (uint32_t) (uintptr_t) sd;
+        int w = wv;
+        asm volatile("" : "+s"(lw), "+s"(la), "+s"(ld), "+s"(w));
+        const uint32_t si = 210u * (uint32_t) i;
+#pragma unroll
+        for (int k = 0; k < WDW; ++k)
+            if (w + 4 * k < WDMA) {
+                const uint32_t t = wbase[k] + si;
+                const uint32_t vo = (t & ~3u) - (((t & 1u) && !(t & 2u)) ? 4u : 0u);
+                dma_b32(wrsrc, lw + 256u * (uint32_t) (w + 4 * k), vo, 0u);
+            }
+        if (w == 0) {
+            uint32_t keep;
+            asm volatile(
+                "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_ushort %2, %3, %4 offen lds\n\t"
+                "s_mov_b32 m0, %0"
+                : "=&s"(keep)
+                : "s"(ld), "v"(dvoff), "s"(wrsrc), "s"(si)
+                : "memory");
+        }
+#pragma unroll
+        for (int k = 0; k < AWW; ++k)
+            if (w + 4 * k < AW) dma_b32(arsrc, la + 256u * (uint32_t) (w + 4 * k), aoff[k], 292u * (uint32_t) i);
+    };
+
+    const int lr = lane & 15, gq = lane >> 4;   // A row / B row within a 16 x 16 tile; k-slot group
+    const int arow_l = 16 * wave + lr;          // this lane's A row in the staged tile
+    const int nh = gq >> 1, nib = gq & 1;       // half n of this lane's segments, their ql nibble
+    const uint32_t par = ((uint32_t) arow_l * nb1) & 2u;
+    float acc[NB][4][8];
+#pragma unroll
+    for (int t = 0; t < NB; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int L = 0; L < 8; ++L) acc[t][r][L] = 0.0f;
+
+    auto compute = [&](const uint8_t* sw, const uint8_t* sa, const uint32_t* sd, int i) __attribute__((always_inline)) {
+        const uint32_t sh = par ^ (2u * ((uint32_t) i & 1u));   // byte offset of the block in its staged dwords
+        const uint32_t* wr = (const uint32_t*) (sw + arow_l * M6_WS);
+        auto wd = [&](int off) __attribute__((always_inline)) {   // the block's dword at byte off (multiple of 4)
+            return __builtin_amdgcn_alignbyte(wr[off / 4 + 1], wr[off / 4], sh);
+        };
+        uint32_t scw[4];   // the 16 sub-block scales
+#pragma unroll
+        for (int k = 0; k < 4; ++k) scw[k] = wd(192 + 4 * k);
+        const uint32_t scm = wd(192 + 4 * gq);   // scales of sub-blocks 4 gq .. 4 gq + 3 (this lane's segments)
+        float d[NB][4];
+#pragma unroll
+        for (int t = 0; t < NB; ++t) {
+            const float dy = *(const float*) (sa + (16 * t + lr) * MF_AS);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) d[t][r] = dy * h2f((uint16_t) sd[16 * wave + 4 * gq + r]);
+        }
+#pragma unroll
+        for (int L = 0; L < 8; ++L) {
+            const uint32_t qa = wd(64 * nh + 4 * L), qb = wd(64 * nh + 32 + 4 * L), qhw = wd(128 + 32 * nh + 4 * L);
+            const uint32_t c0 = 4u * (uint32_t) nib;   // qh shift of segment 2 gq (2 c, c = 2 nib); + 2 for 2 gq + 1
+            const uint32_t q0 = ((qa >> (4u * nib)) & 0x0F0F0F0Fu) | (((qhw >> c0) & 0x03030303u) << 4);
+            const uint32_t q1 = ((qb >> (4u * nib)) & 0x0F0F0F0Fu) | (((qhw >> (c0 + 2u)) & 0x03030303u) << 4);
+            const int hs = L >= 4 ? 8 : 0;
+            uint32_t h0, l0, h1, l1;
+            q6_digits(q0, (int) (int8_t) (scm >> hs), h0, l0);
+            q6_digits(q1, (int) (int8_t) (scm >> (16 + hs)), h1, l1);
+            // the bsum term's scale: sub-block 2 L + nh
+            const int sm = (int) (int8_t) (scw[L >> 1] >> (8 * (2 * (L & 1)) + 8 * nh));
+            const uint32_t hb = __builtin_amdgcn_perm((uint32_t) ((-sm) >> 1), (uint32_t) ((-sm) >> 1), 0u);   // byte 0 x 4
+            const uint32_t lb = (sm & 1) ? 0x20202020u : 0u;
+            const v4i ahi = v4i{(int) h0, (int) h1, (int) hb, (int) hb};
+            const v4i alo = v4i{(int) l0, (int) l1, (int) lb, (int) lb};
+            // every tile of the pass, whether or not it holds routed rows (a
+            // branch here would keep the matrix-core results from overlapping
+            // the next lane's operand work); rows past ntok are never stored
+#pragma unroll
+            for (int t = 0; t < NB; ++t) {
+                const uint8_t* ab = sa + (16 * t + lr) * MF_AS + 16;
+                const uint32_t bm0 = *(const uint32_t*) (ab + 64 * gq + 4 * L);
+                const uint32_t bm1 = *(const uint32_t*) (ab + 64 * gq + 32 + 4 * L);
+                const uint32_t bn0 = *(const uint32_t*) (ab + 32 * L + 8 * gq);
+                const uint32_t bn1 = *(const uint32_t*) (ab + 32 * L + 8 * gq + 4);
+                const v4i bq = v4i{(int) bm0, (int) bm1, (int) bn0, (int) bn1};
+                const v4i z4 = v4i{0, 0, 0, 0};
+                const v4i dhi = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi, bq, z4, 0, 0, 0);
+                const v4i dlo = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo, bq, z4, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    acc[t][r][L] = __builtin_fmaf(d[t][r], (float) (64 * dhi[r] + dlo[r]), acc[t][r][L]);
+            }
+        }
+    };
+    auto stage = [&](int i, const uint8_t* cw, const uint8_t* ca, const uint32_t* cd, uint8_t* nw, uint8_t* na,
+                     uint32_t* nd) __attribute__((always_inline)) {
+        if (i + 1 < nb) vm_wait<VM_STAGE>();   // super-block i + 1's loads may stay in flight
+        else vm_wait<0>();
+        lds_barrier();
+        if (i + 2 < nb) issue(nw, na, nd, i + 2);
+        compute(cw, ca, cd, i);
+    };
+    issue(s_w0, s_a0, s_d0, 0);
+    if (nb > 1) issue(s_w1, s_a1, s_d1, 1);
+    for (int i = 0; i < nb; i += 3) {
+        stage(i, s_w0, s_a0, s_d0, s_w2, s_a2, s_d2);
+        if (i + 1 < nb) stage(i + 1, s_w1, s_a1, s_d1, s_w0, s_a0, s_d0);
+        if (i + 2 < nb) stage(i + 2, s_w2, s_a2, s_d2, s_w1, s_a1, s_d1);
+    }
+    // hsum_float_8(acc); rows r0 + 16 wave + 4 gq .. +3 of B row 16 t + lr
+#pragma unroll
+    for (int t = 0; t < NB; ++t) {
+        float o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float* a = acc[t][r];
+            o[r] = ((a[4] + a[0]) + (a[6] + a[2])) + ((a[5] + a[1]) + (a[7] + a[3]));
+        }
+        const int row = 16 * t + lr;
+        if (row < ntok) {
+            const int e = s_et[row][0], tt = s_et[row][1];
+            float* dp = (float*) ((char*) m.dst + (size_t) e * m.dst_nb1 + (size_t) tt * m.dst_nb2) + r0 +
+                        16 * wave + 4 * gq;
+            *(float4*) dp = float4{o[0], o[1], o[2], o[3]};
+        }
+    }
+}
+
 // Whether a matrix-core kernel can take (type, form, shape, strides): Q4_K rows
-// of 16-byte aligned super-blocks, or (block-sum form) Q6_K rows on 4-byte
-// aligned tensors; 64-row tiles, 16-byte aligned output rows.
+// of 16-byte aligned super-blocks, or Q6_K rows on 4-byte aligned tensors;
+// 64-row tiles, 16-byte aligned output rows.
 bool mmid_mfma_supported(const MmidArgs& m) {
     const bool q4 = m.type == T_Q4_K && m.nb1 % 16 == 0 && m.nb2 % 16 == 0 && ((uintptr_t) m.w & 15) == 0;
-    const bool q6 = m.type == T_Q6_K && !m.mfma_exact && m.nb1 % 2 == 0 && m.nb2 % 4 == 0 && ((uintptr_t) m.w & 3) == 0 &&
+    const bool q6 = m.type == T_Q6_K && m.nb1 % 2 == 0 && m.nb2 % 4 == 0 && ((uintptr_t) m.w & 3) == 0 &&
                     (uint64_t) M6_M * m.nb1 + 64ull * m.nb1 < (1ull << 31);
     return (q4 || q6) && m.N % MF_M == 0 && m.K % QK_K == 0 && m.dst_nb1 % 16 == 0 && m.dst_nb2 % 16 == 0 &&
            ((uintptr_t) m.dst & 15) == 0 && m.act_row_bytes % 4 == 0 && ((uintptr_t) m.act_q & 3) == 0;
@@ -674,12 +918,14 @@ bool mmid_mfma_supported(const MmidArgs& m) {
 int launch_mmid_mfma(const MmidArgs& m, hipStream_t stream) {
     if (!mmid_mfma_supported(m)) return -2;
     // one workgroup per (work item, row tile)
-    const int rows = m.type == T_Q6_K ? M6_N : 16 * (m.mfma_exact ? MF_NB_X : MF_NB_B);
-    const int64_t groups = mf_max_items(m, rows) * (m.type == T_Q6_K ? (m.N + M6_M - 1) / M6_M : m.N / MF_M);
+    const bool q6x = m.type == T_Q6_K && m.mfma_exact, q6b = m.type == T_Q6_K && !m.mfma_exact;
+    const int rows = q6b ? M6_N : 16 * (q6x ? MX_NB : m.mfma_exact ? MF_NB_X : MF_NB_B);
+    const int64_t groups = mf_max_items(m, rows) * (q6b ? (m.N + M6_M - 1) / M6_M : m.N / MF_M);
     if (groups == 0) return 0;
     if (groups > (int64_t(1) << 30)) return -2;
     const unsigned grid = (unsigned) groups;
-    if (m.type == T_Q6_K) hipLaunchKernelGGL(k_mmid_mfma_q6k, dim3(grid), dim3(256), 0, stream, m);
+    if (q6b) hipLaunchKernelGGL(k_mmid_mfma_q6k, dim3(grid), dim3(256), 0, stream, m);
+    else if (q6x) hipLaunchKernelGGL((k_mmid_mfma_q6k_x<MX_NB>), dim3(grid), dim3(256), 0, stream, m);
     else if (m.mfma_exact) hipLaunchKernelGGL((k_mmid_mfma_q4k<MF_NB_X, true>), dim3(grid), dim3(256), 0, stream, m);
     else hipLaunchKernelGGL((k_mmid_mfma_q4k<MF_NB_B, false>), dim3(grid), dim3(256), 0, stream, m);
     return hipGetLastError() == hipSuccess ? 0 : -3;

@@ -198,19 +198,26 @@ def test_exact_inputs_pin_the_crafted_q6k_blocks(orc):
     assert np.all(deq == np.round(deq)) and np.max(np.abs(deq)) <= 4 * 32
 
 
+@pytest.mark.parametrize("form", ["block_sum", "exact"])
 @pytest.mark.parametrize("K,N,min_rows", [(768, 128, 8), (1536, 64, 1), (512, 192, 16)])
-def test_mfma_q6k_integer_core_bit_exact(orc, K, N, min_rows):
-    """Q6_K heavy experts on the matrix cores (block-sum form; K = 768 puts every
-    other super-block 2 bytes past a dword boundary in odd rows) on exact inputs:
-    bit-identical to the reference."""
-    note(f"Q6_K matrix-core mul_mat_id, exact inputs: K={K} N={N} min_rows={min_rows}")
+def test_mfma_q6k_integer_core_bit_exact(orc, K, N, min_rows, form):
+    """Q6_K heavy experts on the matrix cores (K = 768 puts every other
+    super-block 2 bytes past a dword boundary in odd rows) on exact inputs:
+    bit-identical to the reference in both forms (the exact form's base-64
+    digits of sc * q6 and its bsum term included: scales span [-128, 127])."""
+    note(f"Q6_K matrix-core mul_mat_id ({form} form), exact inputs: K={K} N={N} min_rows={min_rows}")
     rng = np.random.default_rng(K + N + 6)
     n_as, T = 5, 70
     w = exact_q6k(rng, n_as * N, K, max_scale=4)
+    if form == "exact":   # the extreme scales and 6-bit values: the digits' range ends
+        wb = w.reshape(n_as * N, K // 256, 210)
+        wb[:, :, 192:208] = rng.choice(np.array([-128, -127, -1, 0, 1, 126, 127], np.int8),
+                                       wb[:, :, 192:208].shape).view(np.uint8)
+        wb[0, :, 0:192] = 0xFF                    # row 0: every q6 = 63
     b = exact_acts(rng, (T, 1), K)
     ids = np.stack([[0, 1 + (t % 4)] for t in range(T)]).astype(np.int32)   # expert 0 takes all 70 tokens
     want = orc.mul_mat_id(Q6_K, K, N, n_as, w, b, ids)
-    prev, prev_f = ops.set_mfma_min_rows(min_rows), ops.set_mfma_form(BLOCK_SUM)
+    prev, prev_f = ops.set_mfma_min_rows(min_rows), ops.set_mfma_form(BLOCK_SUM if form == "block_sum" else EXACT)
     try:
         got = host(ops.mul_mat_id(Q6_K, dev(w), K, N, n_as, dev(b), dev(ids)))
     finally:
