@@ -171,8 +171,11 @@ inline int64_t mf_max_items(const MmidArgs& m, int R) {
 // d, and the pads) of the row's Q8_K block.  One DMA instruction covers 64
 // consecutive chunks or slots, one per lane; the last activation instruction's
 // slots past the rows land in the buffer's slack.
+// Occupancy: the exact form (41.7 KB of LDS, ~128 VGPRs) runs three
+// workgroups per CU, the block-sum form (81 KB, ~206 VGPRs) two.
 template <int NB, bool EXACT>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) k_mmid_mfma_q4k(MmidArgs m) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(EXACT ? 3 : 2, EXACT ? 3 : 2)))
+k_mmid_mfma_q4k(MmidArgs m) {
     constexpr int NR = 16 * NB;               // activation rows per pass (and per item)
     constexpr int AW = (NR * MF_AD + 63) / 64;   // activation DMA instructions per stage
     constexpr int AWW = (AW + 3) / 4;         // ... per wave, at most
@@ -689,9 +692,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 // same contraction.  The float steps then follow ggml lane for lane.
 //
 // Workgroup: 64 weight rows (a wave per 16) x one work item of 16 NB routed
-// activation rows; staging as k_mmid_mfma_q4k (three stage buffers, two
-// super-blocks ahead), blocks staged as in k_mmid_mfma_q6k (53 dwords from the
-// dword at or below the block's start; the fp16 d from a 16-bit copy).
+// activation rows; super-blocks staged by DMA as in k_mmid_mfma_q6k (53 dwords
+// from the dword at or below the block's start; the fp16 d from a 16-bit copy),
+// one super-block ahead.
 constexpr int MX_NB = 2;   // activation tiles per pass of the exact Q6_K form
 
 // Base-64 digits of v = s * q for the four bytes q of w (each 0..63), s in
@@ -712,23 +715,19 @@ __device__ __forceinline__ void q6_digits(uint32_t w, int s, uint32_t& hi, uint3
 }
 
 template <int NB>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) k_mmid_mfma_q6k_x(MmidArgs m) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) k_mmid_mfma_q6k_x(MmidArgs m) {
     constexpr int NR = 16 * NB;                  // activation rows per pass (and per item)
     constexpr int WDMA = MF_M * 53 / 64;         // weight DMA instructions per stage (64 rows x 53 dwords)
     constexpr int WDW = (WDMA + 3) / 4;          // ... per wave, at most
     constexpr int AW = (NR * MF_AD + 63) / 64;   // activation DMA instructions per stage
     constexpr int AWW = (AW + 3) / 4;
-    constexpr int VM_STAGE = WDMA / 4 + AW / 4;  // fewest DMA instructions any wave issues per stage
-    static_assert(MF_M * 53 % 64 == 0 && 2 * (WDW + 1 + AWW) <= 63, "staging shape");
+    static_assert(MF_M * 53 % 64 == 0 && WDW + 1 + AWW <= 63, "staging shape");
     __shared__ __align__(16) uint8_t s_w0[MF_M * M6_WS];
     __shared__ __align__(16) uint8_t s_w1[MF_M * M6_WS];
-    __shared__ __align__(16) uint8_t s_w2[MF_M * M6_WS];
     __shared__ __align__(16) uint8_t s_a0[AW * 256];   // NR * MF_AS and the last instruction's slack
     __shared__ __align__(16) uint8_t s_a1[AW * 256];
-    __shared__ __align__(16) uint8_t s_a2[AW * 256];
     __shared__ __align__(16) uint32_t s_d0[MF_M];      // fp16 d of each staged weight row (zero-extended dword)
     __shared__ __align__(16) uint32_t s_d1[MF_M];
-    __shared__ __align__(16) uint32_t s_d2[MF_M];
     __shared__ int32_t s_arow[NR];
     __shared__ int32_t s_et[NR][2];
     __shared__ int s_item[2];
@@ -809,6 +808,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int arow_l = 16 * wave + lr;          // this lane's A row in the staged tile
     const int nh = gq >> 1, nib = gq & 1;       // half n of this lane's segments, their ql nibble
     const uint32_t par = ((uint32_t) arow_l * nb1) & 2u;
+    const int nbt = (ntok + 15) / 16;           // activation tiles holding rows (uniform)
     float acc[NB][4][8];
 #pragma unroll
     for (int t = 0; t < NB; ++t)
@@ -850,11 +850,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
             const uint32_t lb = (sm & 1) ? 0x20202020u : 0u;
             const v4i ahi = v4i{(int) h0, (int) h1, (int) hb, (int) hb};
             const v4i alo = v4i{(int) l0, (int) l1, (int) lb, (int) lb};
-            // every tile of the pass, whether or not it holds routed rows (a
-            // branch here would keep the matrix-core results from overlapping
-            // the next lane's operand work); rows past ntok are never stored
 #pragma unroll
             for (int t = 0; t < NB; ++t) {
+                if (t >= nbt) break;   // (computing empty tiles too measured slower: 5 VGPRs spilled)
                 const uint8_t* ab = sa + (16 * t + lr) * MF_AS + 16;
                 const uint32_t bm0 = *(const uint32_t*) (ab + 64 * gq + 4 * L);
                 const uint32_t bm1 = *(const uint32_t*) (ab + 64 * gq + 32 + 4 * L);
@@ -870,20 +868,20 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
             }
         }
     };
-    auto stage = [&](int i, const uint8_t* cw, const uint8_t* ca, const uint32_t* cd, uint8_t* nw, uint8_t* na,
-                     uint32_t* nd) __attribute__((always_inline)) {
-        if (i + 1 < nb) vm_wait<VM_STAGE>();   // super-block i + 1's loads may stay in flight
-        else vm_wait<0>();
-        lds_barrier();
-        if (i + 2 < nb) issue(nw, na, nd, i + 2);
-        compute(cw, ca, cd, i);
-    };
+    // stage i: wait for its copies, barrier (every wave is done with stage i - 1,
+    // whose buffer then takes super-block i + 1), issue i + 1, compute i.  Two
+    // stage buffers (45 KB of LDS) let three workgroups share a CU.
     issue(s_w0, s_a0, s_d0, 0);
-    if (nb > 1) issue(s_w1, s_a1, s_d1, 1);
-    for (int i = 0; i < nb; i += 3) {
-        stage(i, s_w0, s_a0, s_d0, s_w2, s_a2, s_d2);
-        if (i + 1 < nb) stage(i + 1, s_w1, s_a1, s_d1, s_w0, s_a0, s_d0);
-        if (i + 2 < nb) stage(i + 2, s_w2, s_a2, s_d2, s_w1, s_a1, s_d1);
+    for (int i = 0; i < nb; i += 2) {
+        vm_wait<0>();
+        lds_barrier();
+        if (i + 1 < nb) issue(s_w1, s_a1, s_d1, i + 1);
+        compute(s_w0, s_a0, s_d0, i);
+        if (i + 1 >= nb) break;
+        vm_wait<0>();
+        lds_barrier();
+        if (i + 2 < nb) issue(s_w0, s_a0, s_d0, i + 2);
+        compute(s_w1, s_a1, s_d1, i + 1);
     }
     // hsum_float_8(acc); rows r0 + 16 wave + 4 gq .. +3 of B row 16 t + lr
 #pragma unroll
