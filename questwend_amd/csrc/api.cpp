@@ -126,9 +126,25 @@ qw::MmidArgs mmid_args(int type, const void* as, int64_t K, int64_t N, int64_t n
 }
 
 int mmid_launch(const qw::MmidArgs& m, hipStream_t st) {
-    int rc = qw::launch_mmid_gemv(m, st);
+    // with mfma_min_rows == 1 the matrix cores take every bin that holds a row:
+    // the GEMV's workgroups would only return
+    int rc = m.mfma_min_rows == 1 ? 0 : qw::launch_mmid_gemv(m, st);
     if (rc == 0 && m.mfma_min_rows > 0) rc = qw::launch_mmid_mfma(m, st);
     return rc;
+}
+
+// Gate and up of a layer (same type, shape and grouping): one GEMV launch and
+// one matrix-core launch for both, else each on its own.
+int mmid_launch_pair(const qw::MmidArgs& mu, const qw::MmidArgs& mg, hipStream_t st) {
+    const bool same = mu.type == mg.type && mu.K == mg.K && mu.N == mg.N && mu.mfma_min_rows == mg.mfma_min_rows &&
+                      mu.mfma_exact == mg.mfma_exact;
+    if (same) {
+        int rc = mu.mfma_min_rows == 1 ? 0 : qw::launch_mmid_gemv2(mu, mg, st);
+        if (rc == 0 && mu.mfma_min_rows > 0) rc = qw::launch_mmid_mfma2(mu, mg, st);
+        if (rc != -2) return rc;
+    }
+    const int rc = mmid_launch(mu, st);
+    return rc ? rc : mmid_launch(mg, st);
 }
 
 // Shared implementation of mul_mat_id once b is quantized and ids are grouped.
@@ -502,12 +518,7 @@ int qwmoe_shared_expert_add(void* stream, const qwmoe_shared_expert* se, int64_t
                                       rows, active, active_off, n_active, 1, nullptr, 0, upo, fb, fb, T, T);
     const qw::MmidArgs mg = mmid_args(se->type_gate, se->gate, H, F, 1, se->gate_nb1, se->gate_nb1 * (size_t) F, xg, 1,
                                       qg, rows, active, active_off, n_active, 1, nullptr, 0, gateo, fb, fb, T, T);
-    if (mu.mfma_min_rows == 0 && mg.mfma_min_rows == 0 && mu.type == mg.type) {
-        if ((rc = qw::launch_mmid_gemv2(mu, mg, st))) return rc;
-    } else {
-        if ((rc = mmid_launch(mu, st))) return rc;
-        if ((rc = mmid_launch(mg, st))) return rc;
-    }
+    if ((rc = mmid_launch_pair(mu, mg, st))) return rc;
     // ggml_mul(ggml_silu(g), u) rounds as swiglu_split does: silu, then one multiply
     qw::MmidArgs md = mmid_args(se->type_down, se->down, F, H, 1, se->down_nb1, se->down_nb1 * (size_t) H, aq, 1, qd,
                                 rows, active, active_off, n_active, 1, nullptr, 0, sh, (size_t) H * 4, (size_t) H * 4, T, T, true);
@@ -730,13 +741,7 @@ int qwmoe_ffn_layer(void* stream, const qwmoe_layer* L, const float* x, int64_t 
     const qw::MmidArgs mg = mmid_args(L->type_gate, L->gate, H, F, L->n_slots_gate, L->gate_nb1, L->gate_nb2, xg, 1, qg,
                                       G.rows, G.active, G.active_off, G.n_active, G.max_active, L->slot_gate,
                                       L->slot_gate ? E : 0, gateo, dnb1, dnb2, T, k * T);
-    if (mu.mfma_min_rows == 0 && mg.mfma_min_rows == 0 && mu.type == mg.type) {
-        // gate and up in one launch
-        if ((rc = qw::launch_mmid_gemv2(mu, mg, st))) return rc;
-    } else {
-        if ((rc = mmid_launch(mu, st))) return rc;
-        if ((rc = mmid_launch(mg, st))) return rc;
-    }
+    if ((rc = mmid_launch_pair(mu, mg, st))) return rc;   // gate and up in one launch each
     const int vd = qw::vec_dot_type(L->type_down);
     const size_t qd = qwmoe_row_size(vd, F);
     uint8_t* aq = ar.take<uint8_t>(qd * (size_t) (k * T) + 64);

@@ -150,6 +150,15 @@ inline int64_t mf_max_items(const MmidArgs& m, int R) {
     return heavy + m.n_pairs / R;
 }
 
+// One launch runs the matrix-core part of one mul_mat_id, or of two of the same
+// type, shape and grouping (gate and up of an FFN): workgroups [0, groups) take
+// m[0], [groups, 2 groups) m[1], so the second matrix's workgroups fill the CUs
+// the first one's last round leaves idle.
+struct MfLaunch {
+    MmidArgs m[2];
+    uint32_t groups;   // workgroups per matrix
+};
+
 // Workgroup b = (work item, row tile): weight rows r0 .. r0 + 63 of the expert's
 // matrix against one pass of 16 NB routed activation rows (the item).  Items
 // bound the longest workgroup: with one workgroup walking all of a tile's rows,
@@ -175,7 +184,10 @@ inline int64_t mf_max_items(const MmidArgs& m, int R) {
 // workgroups per CU, the block-sum form (81 KB, ~206 VGPRs) two.
 template <int NB, bool EXACT>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(EXACT ? 3 : 2, EXACT ? 3 : 2)))
-k_mmid_mfma_q4k(MmidArgs m) {
+k_mmid_mfma_q4k(MfLaunch lp) {
+    const uint32_t zm = blockIdx.x >= lp.groups ? 1u : 0u;   // uniform: which matrix
+    const MmidArgs& m = lp.m[zm];
+    const uint32_t bid = blockIdx.x - zm * lp.groups;
     constexpr int NR = 16 * NB;               // activation rows per pass (and per item)
     constexpr int AW = (NR * MF_AD + 63) / 64;   // activation DMA instructions per stage
     constexpr int AWW = (AW + 3) / 4;         // ... per wave, at most
@@ -191,9 +203,9 @@ k_mmid_mfma_q4k(MmidArgs m) {
     __shared__ int32_t s_et[NR][2];
     __shared__ int s_item[2];
     const int tiles = (int) (m.N / MF_M);
-    const int tile = (int) (blockIdx.x % (uint32_t) tiles);
+    const int tile = (int) (bid % (uint32_t) tiles);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    mf_item(m, (int) (blockIdx.x / (uint32_t) tiles), NR, wave, lane, s_item);
+    mf_item(m, (int) (bid / (uint32_t) tiles), NR, wave, lane, s_item);
     const int g = s_item[0];
     if (g < 0) return;   // past the last item (light experts have none: the GEMV kernel's)
     const int p0 = m.active_off[g] + NR * s_item[1], p1 = min(m.active_off[g + 1], p0 + NR);
@@ -474,7 +486,10 @@ constexpr int M6_M = 128;             // weight rows per workgroup
 constexpr int M6_N = 32;              // activation rows per pass (= rows per work item)
 constexpr uint32_t M6_WS = 212;       // LDS stride of a staged Q6_K block (53 dwords)
 
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) k_mmid_mfma_q6k(MmidArgs m) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) k_mmid_mfma_q6k(MfLaunch lp) {
+    const uint32_t zm = blockIdx.x >= lp.groups ? 1u : 0u;   // uniform: which matrix
+    const MmidArgs& m = lp.m[zm];
+    const uint32_t bid = blockIdx.x - zm * lp.groups;
     constexpr int WDMA = M6_M * 53 / 64;            // weight DMA instructions per stage (M6_M rows x 53 dwords)
     constexpr int WDW = (WDMA + 3) / 4;             // ... per wave, at most
     constexpr int ADMA = (M6_N * MF_AD + 63) / 64;  // activation DMA instructions per stage
@@ -489,9 +504,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     __shared__ int32_t s_et[M6_N][2];
     __shared__ int s_item[2];
     const int tiles = (int) ((m.N + M6_M - 1) / M6_M);
-    const int tile = (int) (blockIdx.x % (uint32_t) tiles);
+    const int tile = (int) (bid % (uint32_t) tiles);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    mf_item(m, (int) (blockIdx.x / (uint32_t) tiles), M6_N, wave, lane, s_item);
+    mf_item(m, (int) (bid / (uint32_t) tiles), M6_N, wave, lane, s_item);
     const int g = s_item[0];
     if (g < 0) return;   // past the last item (light experts have none: the GEMV kernel's)
     const int p0 = m.active_off[g] + M6_N * s_item[1], p1 = min(m.active_off[g + 1], p0 + M6_N);
@@ -715,7 +730,10 @@ __device__ __forceinline__ void q6_digits(uint32_t w, int s, uint32_t& hi, uint3
 }
 
 template <int NB>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) k_mmid_mfma_q6k_x(MmidArgs m) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) k_mmid_mfma_q6k_x(MfLaunch lp) {
+    const uint32_t zm = blockIdx.x >= lp.groups ? 1u : 0u;   // uniform: which matrix
+    const MmidArgs& m = lp.m[zm];
+    const uint32_t bid = blockIdx.x - zm * lp.groups;
     constexpr int NR = 16 * NB;                  // activation rows per pass (and per item)
     constexpr int WDMA = MF_M * 53 / 64;         // weight DMA instructions per stage (64 rows x 53 dwords)
     constexpr int WDW = (WDMA + 3) / 4;          // ... per wave, at most
@@ -732,9 +750,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))
     __shared__ int32_t s_et[NR][2];
     __shared__ int s_item[2];
     const int tiles = (int) (m.N / MF_M);
-    const int tile = (int) (blockIdx.x % (uint32_t) tiles);
+    const int tile = (int) (bid % (uint32_t) tiles);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    mf_item(m, (int) (blockIdx.x / (uint32_t) tiles), NR, wave, lane, s_item);
+    mf_item(m, (int) (bid / (uint32_t) tiles), NR, wave, lane, s_item);
     const int g = s_item[0];
     if (g < 0) return;   // past the last item (light experts have none: the GEMV kernel's)
     const int p0 = m.active_off[g] + NR * s_item[1], p1 = min(m.active_off[g + 1], p0 + NR);
@@ -913,20 +931,46 @@ bool mmid_mfma_supported(const MmidArgs& m) {
            ((uintptr_t) m.dst & 15) == 0 && m.act_row_bytes % 4 == 0 && ((uintptr_t) m.act_q & 3) == 0;
 }
 
+static int launch_mf(const MfLaunch& lp, int nz, hipStream_t stream) {
+    const MmidArgs& m = lp.m[0];
+    if (lp.groups == 0) return 0;
+    const unsigned grid = lp.groups * (unsigned) nz;
+    const bool q6x = m.type == T_Q6_K && m.mfma_exact, q6b = m.type == T_Q6_K && !m.mfma_exact;
+    if (q6b) hipLaunchKernelGGL(k_mmid_mfma_q6k, dim3(grid), dim3(256), 0, stream, lp);
+    else if (q6x) hipLaunchKernelGGL((k_mmid_mfma_q6k_x<MX_NB>), dim3(grid), dim3(256), 0, stream, lp);
+    else if (m.mfma_exact) hipLaunchKernelGGL((k_mmid_mfma_q4k<MF_NB_X, true>), dim3(grid), dim3(256), 0, stream, lp);
+    else hipLaunchKernelGGL((k_mmid_mfma_q4k<MF_NB_B, false>), dim3(grid), dim3(256), 0, stream, lp);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+// Workgroups of one matrix: (work item, row tile) pairs.
+static int64_t mf_groups(const MmidArgs& m) {
+    const bool q6b = m.type == T_Q6_K && !m.mfma_exact;
+    const int rows = q6b ? M6_N : 16 * (m.type == T_Q6_K ? MX_NB : m.mfma_exact ? MF_NB_X : MF_NB_B);
+    return mf_max_items(m, rows) * (q6b ? (m.N + M6_M - 1) / M6_M : m.N / MF_M);
+}
+
 int launch_mmid_mfma(const MmidArgs& m, hipStream_t stream) {
     if (!mmid_mfma_supported(m)) return -2;
-    // one workgroup per (work item, row tile)
-    const bool q6x = m.type == T_Q6_K && m.mfma_exact, q6b = m.type == T_Q6_K && !m.mfma_exact;
-    const int rows = q6b ? M6_N : 16 * (q6x ? MX_NB : m.mfma_exact ? MF_NB_X : MF_NB_B);
-    const int64_t groups = mf_max_items(m, rows) * (q6b ? (m.N + M6_M - 1) / M6_M : m.N / MF_M);
-    if (groups == 0) return 0;
+    const int64_t groups = mf_groups(m);
     if (groups > (int64_t(1) << 30)) return -2;
-    const unsigned grid = (unsigned) groups;
-    if (q6b) hipLaunchKernelGGL(k_mmid_mfma_q6k, dim3(grid), dim3(256), 0, stream, m);
-    else if (q6x) hipLaunchKernelGGL((k_mmid_mfma_q6k_x<MX_NB>), dim3(grid), dim3(256), 0, stream, m);
-    else if (m.mfma_exact) hipLaunchKernelGGL((k_mmid_mfma_q4k<MF_NB_X, true>), dim3(grid), dim3(256), 0, stream, m);
-    else hipLaunchKernelGGL((k_mmid_mfma_q4k<MF_NB_B, false>), dim3(grid), dim3(256), 0, stream, m);
-    return hipGetLastError() == hipSuccess ? 0 : -3;
+    MfLaunch lp;
+    lp.m[0] = lp.m[1] = m;
+    lp.groups = (uint32_t) groups;
+    return launch_mf(lp, 1, stream);
+}
+
+int launch_mmid_mfma2(const MmidArgs& a, const MmidArgs& b, hipStream_t stream) {
+    if (!mmid_mfma_supported(a) || !mmid_mfma_supported(b) || a.type != b.type || a.mfma_exact != b.mfma_exact ||
+        a.K != b.K || a.N != b.N)
+        return -2;
+    const int64_t groups = mf_groups(a);
+    if (groups != mf_groups(b) || groups > (int64_t(1) << 29)) return -2;
+    MfLaunch lp;
+    lp.m[0] = a;
+    lp.m[1] = b;
+    lp.groups = (uint32_t) groups;
+    return launch_mf(lp, 2, stream);
 }
 
 }  // namespace qw

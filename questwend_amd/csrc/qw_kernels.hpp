@@ -97,6 +97,9 @@ int launch_mmid_gemv2(const MmidArgs& a, const MmidArgs& b, hipStream_t stream);
 // mmid_mfma.hip
 bool mmid_mfma_supported(const MmidArgs& m);
 int launch_mmid_mfma(const MmidArgs& m, hipStream_t stream);
+// the matrix-core parts of two mul_mat_ids of the same type, form, shape and
+// grouping (gate and up) in one launch
+int launch_mmid_mfma2(const MmidArgs& a, const MmidArgs& b, hipStream_t stream);
 
 // ffn.hip
 int launch_swiglu(const float* gate, const float* up, float* out, int64_t n_rows, int64_t n, size_t g_stride,
