@@ -725,8 +725,10 @@ __device__ __forceinline__ void q6_digits(uint32_t w, int s, uint32_t& hi, uint3
     const uint32_t ho = __builtin_bit_cast(uint32_t, __builtin_bit_cast(s16x2m, o) >> (short) 6);
     const uint32_t le = __builtin_bit_cast(uint32_t, (u16x2m) ((e & m63) - c32));
     const uint32_t lo_ = __builtin_bit_cast(uint32_t, (u16x2m) ((o & m63) - c32));
-    hi = (he & 0x00FF00FFu) | ((ho & 0x00FF00FFu) << 8);
-    lo = (le & 0x00FF00FFu) | ((lo_ & 0x00FF00FFu) << 8);
+    // bytes 0 and 2 of each (v_perm_b32: selector 0-3 picks the second operand's
+    // bytes, 4-7 the first's)
+    hi = __builtin_amdgcn_perm(ho, he, 0x06020400u);
+    lo = __builtin_amdgcn_perm(lo_, le, 0x06020400u);
 }
 
 template <int NB>
