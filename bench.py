@@ -332,14 +332,22 @@ def prefill(args) -> int:
                 ops.set_mfma_form(prev_f)
 
     step_s, ev_s, (out, xn, ids, w) = timed(args.mfma_min_rows)          # the library default: exact
-    auto_s, _, (out_a, _, _, _) = timed(args.mfma_min_rows, ops.MFMA_AUTO)
-    bs_s, _, (out_b, _, _, _) = timed(args.mfma_min_rows, ops.MFMA_BLOCK_SUM)
-    gemv_s, _, (out_g, _, _, _) = timed(0)
+    if args.exact_only:   # (kernel traces of the default form alone)
+        auto_s = bs_s = gemv_s = out_a = out_b = out_g = None
+    else:
+        auto_s, _, (out_a, _, _, _) = timed(args.mfma_min_rows, ops.MFMA_AUTO)
+        bs_s, _, (out_b, _, _, _) = timed(args.mfma_min_rows, ops.MFMA_BLOCK_SUM)
+        gemv_s, _, (out_g, _, _, _) = timed(0)
 
     def rel(a):   # vs the GEMV, which (like the exact matrix-core form) replays ggml's float steps
+        if a is None:
+            return None
         return float(f"{float((a.double() - out_g.double()).abs().max() / out_g.double().abs().max().clamp_min(1e-30)):.3e}")
 
-    same = bool(torch.equal(out.view(torch.int32), out_g.view(torch.int32)))
+    def ms(t):
+        return None if t is None else round(t * 1e3, 4)
+
+    same = None if out_g is None else bool(torch.equal(out.view(torch.int32), out_g.view(torch.int32)))
     counts = np.bincount(ids.cpu().numpy().reshape(-1), minlength=E)
     expert_bytes = 2 * F * row_size(Q4_K, H) + H * row_size(Q4_K, F)
     wbytes = int((counts > 0).sum()) * expert_bytes + E * H * 4          # unique weights touched + router
@@ -363,11 +371,11 @@ def prefill(args) -> int:
                      "int8_mac_rate_tops": round(macs / ev_s / 1e12, 2),
                      "int8_mac_frac_of_2500_tmacs": round(macs / ev_s / 2.5e15, 4)},
         "exact_mfma_equals_gemv_bitwise": same,
-        "auto_form_ms_per_step": round(auto_s * 1e3, 4),
+        "auto_form_ms_per_step": ms(auto_s),
         "auto_form_rel_err_vs_gemv": rel(out_a),
-        "block_sum_everywhere_ms_per_step": round(bs_s * 1e3, 4),
+        "block_sum_everywhere_ms_per_step": ms(bs_s),
         "block_sum_everywhere_rel_err_vs_gemv": rel(out_b),
-        "gemv_only_ms_per_step": round(gemv_s * 1e3, 4),
+        "gemv_only_ms_per_step": ms(gemv_s),
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
@@ -817,6 +825,7 @@ def config5_bench(args) -> int:
 
     def prefill_s(form):
         prev = ops.set_mfma_form(form)
+        prev_rows = ops.set_mfma_min_rows(args.mfma_min_rows)   # as the configs[2] prefill line
         try:
             for _ in range(2):
                 ops.ffn_layer(L0, x, rms_eps=RMS_EPS)
@@ -828,12 +837,16 @@ def config5_bench(args) -> int:
             return (time.perf_counter() - t0) / reps, r
         finally:
             ops.set_mfma_form(prev)
+            ops.set_mfma_min_rows(prev_rows)
 
     pre_s, (out_x, _, ids, _) = prefill_s(ops.MFMA_EXACT)          # the library default
-    pre_auto_s, (out, _, _, _) = prefill_s(ops.MFMA_AUTO)
-    pre_bs_s, (out_b, _, _, _) = prefill_s(ops.MFMA_BLOCK_SUM)
-    pre_rel = float((out.double() - out_x.double()).abs().max() / out_x.double().abs().max().clamp_min(1e-30))
-    pre_rel_bs = float((out_b.double() - out_x.double()).abs().max() / out_x.double().abs().max().clamp_min(1e-30))
+    if args.exact_only:   # (kernel traces of the default form alone)
+        pre_auto_s = pre_bs_s = pre_rel = pre_rel_bs = None
+    else:
+        pre_auto_s, (out, _, _, _) = prefill_s(ops.MFMA_AUTO)
+        pre_bs_s, (out_b, _, _, _) = prefill_s(ops.MFMA_BLOCK_SUM)
+        pre_rel = float((out.double() - out_x.double()).abs().max() / out_x.double().abs().max().clamp_min(1e-30))
+        pre_rel_bs = float((out_b.double() - out_x.double()).abs().max() / out_x.double().abs().max().clamp_min(1e-30))
     counts5 = np.bincount(ids.cpu().numpy().reshape(-1), minlength=E5)
     used = int((counts5 > 0).sum())
     cpu = pre_cpu = None
@@ -859,7 +872,7 @@ def config5_bench(args) -> int:
         "config": {"workload": f"configs[4]: {NL5} layers H=4096 E=128 k=8 F=1536, Q4_K gate/up, Q6_K down, permuted slots",
                    "decode_path": "qwmoe_decode_stack_run: " + KERNEL_NAMES.get(dstack.kernel(), "?") +
                                   f", one launch per token through {NL5} layers",
-                   "prefill_path": "qwmoe_ffn_layer T=1024"},
+                   "prefill_path": f"qwmoe_ffn_layer T=1024 (mfma_min_rows {args.mfma_min_rows})"},
         "decode": {"tok_s": round(1.0 / dec_s, 2), "ms_per_token": round(dec_s * 1e3, 3),
                    "avg_launch_ms": round(kern_ms, 4),
                    "weight_bytes_per_token": dec_bytes, "gbps": round(dec_bytes / dec_s / 1e9, 1),
@@ -870,10 +883,10 @@ def config5_bench(args) -> int:
         "prefill": {"tokens": T5, "ms_per_layer": round(pre_s * 1e3, 3), "tok_s": round(T5 / pre_s, 1),
                     "used_experts": used, "rows_per_expert": row_count_profile(counts5),
                     "form": "exact (the library default: ggml's bits)",
-                    "auto_form_ms_per_layer": round(pre_auto_s * 1e3, 3),
-                    "auto_form_rel_err_vs_exact": float(f"{pre_rel:.3e}"),
-                    "block_sum_form_ms_per_layer": round(pre_bs_s * 1e3, 3),
-                    "block_sum_form_rel_err_vs_exact": float(f"{pre_rel_bs:.3e}"),
+                    "auto_form_ms_per_layer": None if pre_auto_s is None else round(pre_auto_s * 1e3, 3),
+                    "auto_form_rel_err_vs_exact": None if pre_rel is None else float(f"{pre_rel:.3e}"),
+                    "block_sum_form_ms_per_layer": None if pre_bs_s is None else round(pre_bs_s * 1e3, 3),
+                    "block_sum_form_rel_err_vs_exact": None if pre_rel_bs is None else float(f"{pre_rel_bs:.3e}"),
                     "roofline": {"bound": "hbm", "achieved": round(pre_bytes / pre_s / 1e9, 1), "peak": HBM_PEAK_GBS,
                                  "unit": "GB/s", "frac": round(pre_bytes / pre_s / 1e9 / HBM_PEAK_GBS, 4),
                                  "traffic": None, "bytes_per_layer": pre_bytes,
@@ -935,6 +948,8 @@ def main() -> int:
                     help="expert_cache: every fetch by hipMemcpyAsync (no slab gather kernel)")
     ap.add_argument("--tokens", type=int, default=None, help="prefill batch size (512); verify: largest T (4)")
     ap.add_argument("--mfma-min-rows", type=int, default=1, help="prefill: experts with this many rows use MFMA")
+    ap.add_argument("--exact-only", action="store_true",
+                    help="prefill / config5: time only the default (exact) form, for kernel traces")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the sharding plan is "

@@ -80,9 +80,11 @@ int qwmoe_set_mfma_min_rows(int rows);
 int qwmoe_get_mfma_min_rows(void);
 /* How the matrix-core kernel forms its floats (no reference counterpart).
  * Every form computes ggml's integers exactly: per super-block the eight AVX2
- * lane sums and the four min lanes of ggml_vec_dot_q4_K_q8_K.
+ * lane sums (and, for Q4_K, the four min lanes) of ggml_vec_dot_q4_K_q8_K and
+ * ggml_vec_dot_q6_K_q8_K.
  *   QWMOE_MFMA_EXACT: replays ggml's float steps lane for lane (eight fp32 fma
- *       chains and hsum_float_8): bit-identical to the CPU backend;
+ *       chains and hsum_float_8): bit-identical to the CPU backend, for Q4_K and
+ *       Q6_K experts alike;
  *   QWMOE_MFMA_BLOCK_SUM: adds each super-block's exact integer sums in one
  *       fp32 chain (and one for the mins): the same integers, floats rounded in
  *       another order (~1e-6 of the output's magnitude), ~2.5x faster per
