@@ -925,6 +925,137 @@ def copy_probe(mib: int = 1024, reps: int = 4) -> int:
     return 0
 
 
+def attn_bench(args) -> int:
+    """The attention half of Seg A (qwmoe_attn_seg, core/runtime.cpp:1976-2030) and
+    a whole decoder layer (qwmoe_decoder_layer) at the Qwen3-30B-A3B attention
+    shape: H = 2048, 32 query / 4 kv heads of D = 128, Q4_K q/k/o and Q6_K v
+    (seeded synthetic weights quantized on the GPU), f16 KV cache of n_ctx = 4096
+    rows.  Timed: decode (T = 1) at n_past = 4095 -- the line's value, tokens per
+    second of the attention segment -- a prefill chunk of 512 tokens at n_past 0
+    and at n_past 3584, and one decoder layer (attention + the 30B MoE FFN) at
+    decode.  roofline: the weight rows and KV-cache rows one decode call reads,
+    over its time (HIP events).  cpu_baseline: ggml's own graph for the same
+    segment (oracle/_ref, AVX-512 build where the host has it) on the same
+    weights and cache at decode."""
+    import numpy as np
+    import torch
+    from questwend_amd import Q4_K, Q6_K, ops, row_size
+
+    NH, NKV, D, N_CTX = 32, 4, 128, 4096
+    NQ, NK = NH * D, NKV * D
+    types = (Q4_K, Q4_K, Q6_K, Q4_K)
+    dev = "cuda:0"
+    ops.init(0, 512 << 20)
+
+    def qmat(rows, cols, t, seed):
+        f = torch.empty((rows, cols), dtype=torch.float32, device=dev)
+        ops.randn_(f, seed, 0.0, 0.02)
+        return ops.quantize_chunk(t, f)
+
+    def vec(n, seed, mean=1.0, std=0.1):
+        v = torch.empty(n, dtype=torch.float32, device=dev)
+        return ops.randn_(v, seed, mean, std)
+
+    sd = args.seed * 1000 + 900
+    wq, wk = qmat(NQ, H, types[0], sd + 1), qmat(NK, H, types[1], sd + 2)
+    wv, wo = qmat(NK, H, types[2], sd + 3), qmat(H, NQ, types[3], sd + 4)
+    an, fn, qn, kn = vec(H, sd + 5), vec(H, sd + 6), vec(D, sd + 7), vec(D, sd + 8)
+    kc = torch.empty((N_CTX, NK), dtype=torch.float32, device=dev)
+    vc = torch.empty((N_CTX, NK), dtype=torch.float32, device=dev)
+    ops.randn_(kc, sd + 9, 0.0, 0.5)
+    ops.randn_(vc, sd + 10, 0.0, 0.5)
+    kc, vc = kc.half(), vc.half()
+    AL = ops.make_attn_layer(H, NH, NKV, D, an, wq, wk, wv, wo, types, qn, kn, fn, kc, vc)
+    # the MoE FFN of the decoder layer: one 30B layer (as the decode stack's)
+    router = torch.empty((E, H), dtype=torch.float32, device=dev)
+    ops.randn_(router, sd + 11, 0.0, 0.02)
+    mats = [qmat(E * F, H, Q4_K, sd + 12), qmat(E * F, H, Q4_K, sd + 13), qmat(E * H, F, Q4_K, sd + 14)]
+    ML = ops.make_layer(H, E, K_USED, F, router, *mats, (Q4_K,) * 3)
+    torch.cuda.synchronize()
+
+    def timed(fn_, n):
+        for _ in range(max(2, args.warmup)):
+            fn_()
+        torch.cuda.synchronize()
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+        t0 = time.perf_counter()
+        for a, b in evs:
+            a.record()
+            fn_()
+            b.record()
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) / n
+        return wall, sum(a.elapsed_time(b) for a, b in evs) / n / 1000.0
+
+    h1 = torch.empty((1, H), dtype=torch.float32, device=dev)
+    ops.randn_(h1, sd + 20, 0.0, 1.0)
+    hp = torch.empty((512, H), dtype=torch.float32, device=dev)
+    ops.randn_(hp, sd + 21, 0.0, 1.0)
+    n_past = N_CTX - 1
+    dec_wall, dec_ev = timed(lambda: ops.attn_seg(AL, h1, n_past), args.steps)
+    pre0_wall, pre0_ev = timed(lambda: ops.attn_seg(AL, hp, 0), max(4, args.steps // 16))
+    pre1_wall, pre1_ev = timed(lambda: ops.attn_seg(AL, hp, N_CTX - 512), max(4, args.steps // 16))
+    lay_wall, lay_ev = timed(lambda: ops.decoder_layer(AL, ML, h1, n_past), args.steps)
+    status = ops.device_status(clear=True)
+
+    wbytes = NQ * row_size(types[0], H) + NK * row_size(types[1], H) + NK * row_size(types[2], H) + \
+        H * row_size(types[3], NQ)
+    kvbytes = 2 * (n_past + 1) * NK * 2
+    abytes = wbytes + kvbytes + (3 * H + 2 * D) * 4
+    moe_bytes = algorithmic_bytes_per_token() // N_LAYER
+    cpu = None
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, str(ROOT / "tests"))
+        from oracle_lib import REF_SO, REF_SO_AVX512, AttnWeights, RefGGML, have_ref_avx512
+        if REF_SO.exists():
+            aw = AttnWeights.__new__(AttnWeights)
+            aw.H, aw.n_head, aw.n_head_kv, aw.D, aw.types, aw.freq_base = H, NH, NKV, D, types, 1e6
+            aw.wq, aw.wk, aw.wv, aw.wo = (t.cpu().numpy().reshape(-1) for t in (wq, wk, wv, wo))
+            aw.attn_norm, aw.ffn_norm, aw.q_norm, aw.k_norm = (t.cpu().numpy() for t in (an, fn, qn, kn))
+            kch = kc.cpu().numpy().view(np.uint16).copy()
+            vch = vc.cpu().numpy().view(np.uint16).copy()
+            x = h1.cpu().numpy()
+            cpuinfo = host_cpu()
+            n_thr = max(1, min(cpuinfo["cores_per_socket"], cpuinfo["cpus_available"]))
+            ref = RefGGML(REF_SO_AVX512 if have_ref_avx512() else REF_SO)
+            ref.attn_seg(aw, x, n_past, kch, vch, n_threads=n_thr)
+            times, t_all = [], time.perf_counter()
+            while (time.perf_counter() - t_all < 10.0 or len(times) < 5) and len(times) < 5000:
+                t0 = time.perf_counter()
+                ref.attn_seg(aw, x, n_past, kch, vch, n_threads=n_thr)
+                times.append(time.perf_counter() - t0)
+            med = float(np.median(times))
+            cpu = {"value": round(1.0 / med, 1), "unit": "tok/s", "cores": n_thr, "kind": "reference",
+                   "sample": f"{len(times)} decode steps (T=1 at n_past {n_past}) of ggml's attention graph in "
+                             f"{time.perf_counter() - t_all:.1f}s",
+                   "median_ms_per_step": round(med * 1e3, 4), "isa": "AVX-512" if ref.isa() == 512 else "AVX2",
+                   "threads": n_thr, "cpu": cpuinfo["model"]}
+    line = {
+        "metric": "attention decode tok/s + achieved HBM GB/s, Qwen3-30B-A3B attention at 4096 context",
+        "value": round(1.0 / dec_wall, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(dec_wall * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "q4_K/q6_K x q8_K -> f32; f16 KV cache",
+        "data": "synthetic (seeded N(0,0.02) weights quantized on the GPU; N(0,0.5) f16 cache; N(0,1) inputs)",
+        "config": {"workload": "Qwen3-30B-A3B attention half of Seg A (qwmoe_attn_seg)", "n_embd": H,
+                   "n_head": NH, "n_head_kv": NKV, "head_dim": D, "n_ctx": N_CTX, "n_past": n_past,
+                   "types_qkvo": ["Q4_K", "Q4_K", "Q6_K", "Q4_K"]},
+        "roofline": {"bound": "hbm", "achieved": round(abytes / dec_ev / 1e9, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(abytes / dec_ev / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "qwmoe_attn_seg at T=1 (the segment's kernels together)",
+                     "bytes_per_call": abytes, "weight_bytes": wbytes, "kv_bytes": kvbytes,
+                     "avg_call_ms": round(dec_ev * 1e3, 4)},
+        "prefill_chunk_512": {"n_past_0_ms": round(pre0_wall * 1e3, 4), "n_past_3584_ms": round(pre1_wall * 1e3, 4),
+                              "tok_s_at_n_past_3584": round(512 / pre1_wall, 1)},
+        "decoder_layer_decode": {"ms": round(lay_wall * 1e3, 4), "avg_call_ms": round(lay_ev * 1e3, 4),
+                                 "bytes_per_call": abytes + moe_bytes,
+                                 "achieved_gbs": round((abytes + moe_bytes) / lay_ev / 1e9, 1)},
+        "cpu_baseline": cpu,
+        "device_status": status,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -938,10 +1069,12 @@ def main() -> int:
                     help="text file whose 'hbm_bytes_per_launch = N' line is the HBM traffic of one decode "
                          "launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (copy-calibrated)")
     ap.add_argument("--copy-probe", action="store_true", help="run only the copy-kernel calibration probe")
-    ap.add_argument("--workload", choices=["decode", "prefill", "expert_cache", "verify", "config5"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "prefill", "expert_cache", "verify", "config5", "attn"],
+                    default="decode",
                     help="decode: configs[1] (the headline line); prefill: configs[2]; expert_cache: configs[1] "
                          "decode with the experts offloaded to pinned host memory; verify: configs[1] stack on "
-                         "T = 1..--tokens verify batches; config5: configs[4] decode and prefill")
+                         "T = 1..--tokens verify batches; config5: configs[4] decode and prefill; attn: the "
+                         "attention half of Seg A and a whole decoder layer at the 30B shape")
     ap.add_argument("--resident", type=float, default=0.5, help="expert_cache: fraction of experts in HBM")
     ap.add_argument("--zipf", type=float, default=1.1, help="expert_cache: router skew (0: none)")
     ap.add_argument("--copy-engine", action="store_true",
@@ -967,6 +1100,8 @@ def main() -> int:
         return verify_bench(args)
     if args.workload == "config5":
         return config5_bench(args)
+    if args.workload == "attn":
+        return attn_bench(args)
 
     import numpy as np
     import torch

@@ -568,7 +568,7 @@ int qwmoe_attn_seg(void* stream, const qwmoe_attn_layer* L, const float* h, int6
     if (T == 0) return QWMOE_OK;
     hipStream_t st = S(stream);
     Arena ar(kReserved);
-    const int64_t n_kv = n_past + T, n_split = (n_kv + qw::ATT_SPLIT - 1) / qw::ATT_SPLIT;
+    const int64_t n_kv = n_past + T, split = qw::attn_split(T, nk, n_kv), n_split = (n_kv + split - 1) / split;
     int32_t* rows = ar.take<int32_t>((size_t) (2 * T + 2));
     int32_t* active = ar.take<int32_t>(2);
     int32_t* active_off = ar.take<int32_t>(3);
@@ -628,6 +628,7 @@ int qwmoe_attn_seg(void* stream, const qwmoe_attn_layer* L, const float* h, int6
     a.kc = L->k_cache;
     a.vc = L->v_cache;
     a.s = sc;
+    a.split = split;
     a.part = part;
     a.att = att;
     if ((rc = qw::launch_attn_core(a, st))) return rc;

@@ -68,50 +68,58 @@ __global__ void __launch_bounds__(64) k_attn_qk_rope(AttnArgs a) {
     }
 }
 
-// Scores of 256 keys per block, one key per thread, for the R = n_head /
-// n_head_kv query heads of kv head g and token t: s = (f16(q) . k) * kq_scale
-// + mask, mask = 0 for key j <= n_past + t, -inf after (the causal mask
-// set_attn_inputs fills, core/runtime.cpp:2108-2116).  The key row is held in
-// registers; the query rows are read from LDS by every thread (broadcast).
+// Scores for the R = n_head / n_head_kv query heads of kv head g and token t:
+// s = (f16(q) . k) * kq_scale + mask, mask = 0 for key j <= n_past + t, -inf
+// after (the causal mask set_attn_inputs fills, core/runtime.cpp:2108-2116).
+// 64 keys per 256-thread block, four lanes per key: lane p of a key's quad
+// loads dims 32 p .. 32 p + 31 of the key row (four 16-byte loads) and forms
+// their part of each head's dot; the quad's parts are added by DPP.  The query
+// rows sit in LDS with one float of padding per 32, so the quad's four lanes
+// read four banks.
+constexpr int SQS = AD + AD / 32;   // padded query row
 __global__ void __launch_bounds__(256) k_attn_scores(AttnArgs a) {
-    __shared__ __align__(16) float sq[ATT_RMAX][AD];
+    __shared__ __align__(16) float sq[ATT_RMAX][SQS];
     const int g = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
     const int nq = a.n_head, R = nq / a.n_head_kv, gqa = a.n_head_kv * AD;
+    // the key row's loads first: their latency overlaps the query staging
+    const int p = tid & 3;
+    const int64_t j = (int64_t) blockIdx.x * 64 + (tid >> 2);
+    const bool valid = j < a.n_kv;
+    const uint4* krow = (const uint4*) ((const __half*) a.kc + (valid ? j : 0) * gqa + g * AD + 32 * p);
+    uint4 kv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) kv[i] = krow[i];
     for (int i = tid; i < R * AD; i += 256) {
         const int h = i / AD, d = i % AD;
-        sq[h][d] = to_f16_and_back(a.qr[((int64_t) t * nq + g * R + h) * AD + d]);
+        sq[h][d + d / 32] = to_f16_and_back(a.qr[((int64_t) t * nq + g * R + h) * AD + d]);
     }
     __syncthreads();
-    const int64_t j = (int64_t) blockIdx.x * 256 + tid;
-    if (j >= a.n_kv) return;
-    const uint4* krow = (const uint4*) ((const __half*) a.kc + j * gqa + g * AD);
-    uint4 kv[AD / 8];
+    float kf[32];
 #pragma unroll
-    for (int i = 0; i < AD / 8; ++i) kv[i] = krow[i];
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t w4[4] = {kv[i].x, kv[i].y, kv[i].z, kv[i].w};
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const __half2 hv = *(const __half2*) &w4[m];
+            kf[8 * i + 2 * m] = __low2float(hv);
+            kf[8 * i + 2 * m + 1] = __high2float(hv);
+        }
+    }
     const bool masked = j > a.n_past + t;
+    const float* qb = &sq[0][33 * p];
     for (int h = 0; h < R; ++h) {
         float acc = 0.0f;
 #pragma unroll
-        for (int i = 0; i < AD / 8; ++i) {
-            const float4 qa = *(const float4*) &sq[h][8 * i], qb = *(const float4*) &sq[h][8 * i + 4];
-            const uint32_t w4[4] = {kv[i].x, kv[i].y, kv[i].z, kv[i].w};
-            float kf[8];
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                const __half2 hv = *(const __half2*) &w4[m];
-                kf[2 * m] = __low2float(hv);
-                kf[2 * m + 1] = __high2float(hv);
-            }
-            acc = __builtin_fmaf(qa.x, kf[0], acc);
-            acc = __builtin_fmaf(qa.y, kf[1], acc);
-            acc = __builtin_fmaf(qa.z, kf[2], acc);
-            acc = __builtin_fmaf(qa.w, kf[3], acc);
-            acc = __builtin_fmaf(qb.x, kf[4], acc);
-            acc = __builtin_fmaf(qb.y, kf[5], acc);
-            acc = __builtin_fmaf(qb.z, kf[6], acc);
-            acc = __builtin_fmaf(qb.w, kf[7], acc);
+        for (int i = 0; i < 32; i += 4) {
+            const float4 q4 = *(const float4*) (qb + h * SQS + i);
+            acc = __builtin_fmaf(q4.x, kf[i], acc);
+            acc = __builtin_fmaf(q4.y, kf[i + 1], acc);
+            acc = __builtin_fmaf(q4.z, kf[i + 2], acc);
+            acc = __builtin_fmaf(q4.w, kf[i + 3], acc);
         }
-        a.s[((int64_t) t * nq + g * R + h) * a.n_kv + j] = masked ? -INFINITY : acc * a.kq_scale;
+        acc = acc + dpp_f<DPP_XOR1>(acc);
+        acc = acc + dpp_f<DPP_XOR2>(acc);
+        if (p == 0 && valid) a.s[((int64_t) t * nq + g * R + h) * a.n_kv + j] = masked ? -INFINITY : acc * a.kq_scale;
     }
 }
 
@@ -152,41 +160,262 @@ __global__ void __launch_bounds__(256) k_attn_softmax(AttnArgs a) {
     for (int64_t i = tid; i < n; i += 256) row[i] = row[i] * inv;
 }
 
-// P.V partial sums over the keys [split * ATT_SPLIT, ...) for kv head g and
-// token t: thread (d = tid % 128, half = tid / 128) accumulates output element
-// d of query heads g R + half, g R + half + 2, ...; the probabilities of a
-// 256-key chunk are staged in LDS, rounded to f16.
+// The same softmax with the row held in registers (one read and one write of
+// the row): thread tid holds the groups of eight tid, tid + 256, ... (NG of
+// them, rows of up to 2048 NG elements); the tail past the last whole group is
+// taken by the first threads, as in the loop form above.
+template <int NG>
+__global__ void __launch_bounds__(256) k_attn_softmax_r(AttnArgs a) {
+    __shared__ float red[4];
+    __shared__ double dred[4];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    float* row = a.s + ((int64_t) blockIdx.y * a.n_head + blockIdx.x) * a.n_kv;
+    const int64_t n = a.n_kv, ng = n / 8;
+    float e[NG][8];   // (rows start at any multiple of 4 bytes: scalar loads)
+#pragma unroll
+    for (int u = 0; u < NG; ++u) {
+        const int64_t q = tid + 256 * u;
+#pragma unroll
+        for (int m = 0; m < 8; ++m) e[u][m] = q < ng ? row[8 * q + m] : -INFINITY;
+    }
+    const int64_t it = 8 * ng + tid;   // this thread's tail element, if any
+    const float tv = it < n ? row[it] : -INFINITY;
+    float mx = tv;
+#pragma unroll
+    for (int u = 0; u < NG; ++u)
+#pragma unroll
+        for (int m = 0; m < 8; ++m) mx = fmaxf(mx, e[u][m]);
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if (lane == 0) red[wv] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    double sum = 0.0;
+#pragma unroll
+    for (int u = 0; u < NG; ++u)
+        if (tid + 256 * u < ng) {
+#pragma unroll
+            for (int m = 0; m < 8; ++m) e[u][m] = v_expf(e[u][m] - mx);
+            sum += (double) hsum8(e[u]);
+        }
+    float te = 0.0f;
+    if (it < n) {
+        te = (float) exp((double) (tv - mx));
+        sum += (double) te;
+    }
+    for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off);
+    if (lane == 0) dred[wv] = sum;
+    __syncthreads();
+    const double tot = (dred[0] + dred[1]) + (dred[2] + dred[3]);
+    const float inv = (float) (1.0 / tot);
+#pragma unroll
+    for (int u = 0; u < NG; ++u) {
+        const int64_t q = tid + 256 * u;
+        if (q < ng) {
+#pragma unroll
+            for (int m = 0; m < 8; ++m) row[8 * q + m] = e[u][m] * inv;
+        }
+    }
+    if (it < n) row[it] = te * inv;
+}
+
+// P.V partial sums over the keys [sp_i * split, ...) for kv head g and token
+// t: four 64-lane groups take every fourth key; lane l of a group holds output
+// elements 2 l, 2 l + 1 of each of the R query heads (one 4-byte load of V per
+// key); the groups' sums are added in group order through LDS.  The
+// probabilities of a chunk of up to 256 keys are staged in LDS, rounded to f16
+// (ggml's f16 vec_dot_type for the V product).
 __global__ void __launch_bounds__(256) k_attn_pv(AttnArgs a) {
     __shared__ float sp[ATT_RMAX][256];
+    __shared__ float2 sred[3][ATT_RMAX][64];
     const int g = blockIdx.x, t = blockIdx.y, sp_i = blockIdx.z, tid = threadIdx.x;
+    const int lane = tid & 63, grp = tid >> 6;
     const int nq = a.n_head, R = nq / a.n_head_kv, gqa = a.n_head_kv * AD;
-    const int d = tid & (AD - 1), half = tid >> 7;
-    const int64_t k0 = (int64_t) sp_i * ATT_SPLIT, k1 = min((int64_t) a.n_kv, k0 + ATT_SPLIT);
-    float acc[ATT_RMAX / 2];
+    const int64_t k0 = (int64_t) sp_i * a.split, k1 = min((int64_t) a.n_kv, k0 + a.split);
+    float2 acc[ATT_RMAX];
 #pragma unroll
-    for (int u = 0; u < ATT_RMAX / 2; ++u) acc[u] = 0.0f;
+    for (int h = 0; h < ATT_RMAX; ++h) acc[h] = float2{0.0f, 0.0f};
     for (int64_t c0 = k0; c0 < k1; c0 += 256) {
         const int nc = (int) min((int64_t) 256, k1 - c0);
+        const __half2* vb = (const __half2*) ((const __half*) a.vc + c0 * gqa + g * AD) + lane;
+        // the first keys' V before the staging barrier (a 64-key split is one
+        // round of 16 per group: all of its loads overlap the staging)
+        __half2 v16[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int jj = grp + 4 * u;
+            v16[u] = jj < nc ? vb[(int64_t) jj * (gqa / 2)] : __half2{};
+        }
         __syncthreads();
         for (int i = tid; i < R * 256; i += 256) {
             const int h = i / 256, jj = i % 256;
             sp[h][jj] = jj < nc ? to_f16_and_back(a.s[((int64_t) t * nq + g * R + h) * a.n_kv + c0 + jj]) : 0.0f;
         }
         __syncthreads();
-        const __half* vcol = (const __half*) a.vc + c0 * gqa + g * AD + d;
-        for (int jj = 0; jj < nc; ++jj) {
-            const float v = __half2float(vcol[(int64_t) jj * gqa]);
 #pragma unroll
-            for (int u = 0; u < ATT_RMAX / 2; ++u) {
-                const int h = half + 2 * u;
-                if (h < R) acc[u] = __builtin_fmaf(sp[h][jj], v, acc[u]);
+        for (int u = 0; u < 16; ++u) {
+            const int jj = grp + 4 * u;
+            if (jj >= nc) break;
+            const float2 v = __half22float2(v16[u]);
+#pragma unroll
+            for (int h = 0; h < ATT_RMAX; ++h)
+                if (h < R) {
+                    const float p = sp[h][jj];
+                    acc[h].x = __builtin_fmaf(p, v.x, acc[h].x);
+                    acc[h].y = __builtin_fmaf(p, v.y, acc[h].y);
+                }
+        }
+#pragma unroll 4
+        for (int jj = grp + 64; jj < nc; jj += 4) {
+            const float2 v = __half22float2(vb[(int64_t) jj * (gqa / 2)]);
+#pragma unroll
+            for (int h = 0; h < ATT_RMAX; ++h)
+                if (h < R) {
+                    const float p = sp[h][jj];
+                    acc[h].x = __builtin_fmaf(p, v.x, acc[h].x);
+                    acc[h].y = __builtin_fmaf(p, v.y, acc[h].y);
+                }
+        }
+    }
+    if (grp > 0) {
+#pragma unroll
+        for (int h = 0; h < ATT_RMAX; ++h)
+            if (h < R) sred[grp - 1][h][lane] = acc[h];
+    }
+    __syncthreads();
+    if (grp == 0) {
+#pragma unroll
+        for (int h = 0; h < ATT_RMAX; ++h)
+            if (h < R) {
+                float2 s2 = acc[h];
+#pragma unroll
+                for (int q = 0; q < 3; ++q) {
+                    const float2 o = sred[q][h][lane];
+                    s2.x = s2.x + o.x;
+                    s2.y = s2.y + o.y;
+                }
+                *(float2*) &a.part[(((int64_t) sp_i * a.T + t) * nq + g * R + h) * AD + 2 * lane] = s2;
+            }
+    }
+}
+
+// ---- batches of at least 64 query rows: the two products on the matrix cores ----
+//
+// Rows r = t R + h (token-major) of kv head g.  v_mfma_f32_16x16x16_f16: lane l
+// of A holds row l % 16, k = 4 (l / 16) .. +3; lane l of B holds column l % 16,
+// the same k; lane l, register i of D is row 4 (l / 16) + i, column l % 16.
+// The f16 operands are the values ggml rounds to f16 (Q, and the normalized
+// probabilities), so every product is exact in fp32; only the order of the
+// fp32 sums differs from the CPU backend's.
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ h4 f4_to_h4(float x0, float x1, float x2, float x3) {
+    return h4{(_Float16) x0, (_Float16) x1, (_Float16) x2, (_Float16) x3};
+}
+
+// Scores: a workgroup takes 64 rows (a wave per 16) and 64 keys (four 16-key
+// tiles), eight MFMAs over the 128 dims per tile.  B is read straight from the
+// cache rows (8 bytes per lane and dim step).
+__global__ void __launch_bounds__(256) k_attn_scores_mf(AttnArgs a) {
+    const int g = blockIdx.y, tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, q = l >> 4;
+    const int nq = a.n_head, R = nq / a.n_head_kv, gqa = a.n_head_kv * AD;
+    const int64_t rows = (int64_t) a.T * R, key0 = (int64_t) blockIdx.x * 64;
+    const int64_t ra = (int64_t) blockIdx.z * 64 + 16 * w + li;   // this lane's A row
+    h4 qa[8];
+    if (ra < rows) {
+        const int t = (int) (ra / R), h = (int) (ra % R);
+        const float* qrow = a.qr + ((int64_t) t * nq + g * R + h) * AD + 4 * q;
+#pragma unroll
+        for (int st = 0; st < 8; ++st) {
+            const float4 v = *(const float4*) (qrow + 16 * st);
+            qa[st] = f4_to_h4(v.x, v.y, v.z, v.w);
+        }
+    } else {
+#pragma unroll
+        for (int st = 0; st < 8; ++st) qa[st] = h4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+        const int64_t jb = key0 + 16 * kt + li;   // this lane's B column (key)
+        const bool kv_ok = jb < a.n_kv;
+        const _Float16* krow = (const _Float16*) a.kc + (kv_ok ? jb : 0) * gqa + g * AD + 4 * q;
+        f4 acc = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int st = 0; st < 8; ++st) {
+            const h4 kb = kv_ok ? *(const h4*) (krow + 16 * st) : h4{0, 0, 0, 0};
+            acc = __builtin_amdgcn_mfma_f32_16x16x16f16(qa[st], kb, acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int64_t r = (int64_t) blockIdx.z * 64 + 16 * w + 4 * q + i;
+            if (r < rows && kv_ok) {
+                const int t = (int) (r / R), h = (int) (r % R);
+                a.s[((int64_t) t * nq + g * R + h) * a.n_kv + jb] = jb > a.n_past + t ? -INFINITY : acc[i] * a.kq_scale;
+            }
+        }
+    }
+}
+
+// P.V: a workgroup takes 64 rows (a wave per 16) and all 128 dims (eight 16-dim
+// tiles), over the keys its rows may see (<= n_past + their last token), 64 keys
+// at a time: the V chunk is staged in LDS transposed ([dim][key], f16) so that
+// a B operand is one 8-byte read; A (the probabilities, rounded to f16) is read
+// straight from the score rows.  Writes att, no partial sums.
+constexpr int SVS = 64 + 4;   // padded key stride of the staged V chunk (halves)
+__global__ void __launch_bounds__(256) k_attn_pv_mf(AttnArgs a) {
+    __shared__ __align__(16) _Float16 sv[AD][SVS];
+    const int g = blockIdx.x, tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, q = l >> 4;
+    const int nq = a.n_head, R = nq / a.n_head_kv, gqa = a.n_head_kv * AD;
+    const int64_t rows = (int64_t) a.T * R, row0 = (int64_t) blockIdx.y * 64;
+    const int t_last = (int) (min(rows, row0 + 64) - 1) / R;
+    const int64_t klim = min((int64_t) a.n_kv, a.n_past + t_last + 1);   // keys past it are masked for every row
+    const int64_t ra = row0 + 16 * w + li;                                // this lane's A row
+    const bool row_ok = ra < rows;
+    const float* prow = a.s + (row_ok ? ((int64_t) (ra / R) * nq + g * R + ra % R) * a.n_kv : 0);
+    f4 acc[8];
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) acc[nt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int sk = tid & 63, sdq = tid >> 6;   // staging: key sk of the chunk, dims 32 sdq .. +32
+    for (int64_t c0 = 0; c0 < klim; c0 += 64) {
+        const int64_t kj = c0 + sk;
+        uint4 vv[4];
+        const uint4* vrow = (const uint4*) ((const _Float16*) a.vc + (kj < klim ? kj : 0) * gqa + g * AD + 32 * sdq);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) vv[i] = kj < klim ? vrow[i] : uint4{0u, 0u, 0u, 0u};
+        __syncthreads();   // the previous chunk's B reads are done
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t w4[4] = {vv[i].x, vv[i].y, vv[i].z, vv[i].w};
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const int d = 32 * sdq + 8 * i + 2 * m;
+                sv[d][sk] = __builtin_bit_cast(_Float16, (uint16_t) (w4[m] & 0xffffu));
+                sv[d + 1][sk] = __builtin_bit_cast(_Float16, (uint16_t) (w4[m] >> 16));
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+            const int64_t k4 = c0 + 16 * kt + 4 * q;   // this lane's four keys of the A operand
+            float p4[4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) p4[m] = row_ok && k4 + m < klim ? prow[k4 + m] : 0.0f;
+            const h4 pa = f4_to_h4(p4[0], p4[1], p4[2], p4[3]);
+#pragma unroll
+            for (int nt = 0; nt < 8; ++nt) {
+                const h4 vb = *(const h4*) &sv[16 * nt + li][16 * kt + 4 * q];
+                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, vb, acc[nt], 0, 0, 0);
             }
         }
     }
 #pragma unroll
-    for (int u = 0; u < ATT_RMAX / 2; ++u) {
-        const int h = half + 2 * u;
-        if (h < R) a.part[(((int64_t) sp_i * a.T + t) * nq + g * R + h) * AD + d] = acc[u];
+    for (int i = 0; i < 4; ++i) {
+        const int64_t r = row0 + 16 * w + 4 * q + i;
+        if (r < rows) {
+            float* dst = a.att + ((int64_t) (r / R) * nq + g * R + r % R) * AD + li;
+#pragma unroll
+            for (int nt = 0; nt < 8; ++nt) dst[16 * nt] = acc[nt][i];
+        }
     }
 }
 
@@ -196,6 +425,7 @@ __global__ void __launch_bounds__(256) k_attn_combine(AttnArgs a, int n_split) {
     const int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x;
     if (i >= n) return;
     float s = a.part[i];
+#pragma unroll 8
     for (int k = 1; k < n_split; ++k) s = s + a.part[(int64_t) k * n + i];
     a.att[i] = s;
 }
@@ -234,10 +464,27 @@ int launch_attn_core(const AttnArgs& a, hipStream_t st) {
     if (a.T <= 0) return 0;
     const int nq = a.n_head, nk = a.n_head_kv;
     hipLaunchKernelGGL(k_attn_qk_rope, dim3((unsigned) a.T, (unsigned) (nq + 2 * nk)), dim3(64), 0, st, a);
-    hipLaunchKernelGGL(k_attn_scores, dim3((unsigned) ((a.n_kv + 255) / 256), (unsigned) nk, (unsigned) a.T),
-                       dim3(256), 0, st, a);
-    hipLaunchKernelGGL(k_attn_softmax, dim3((unsigned) nq, (unsigned) a.T), dim3(256), 0, st, a);
-    const int n_split = (int) ((a.n_kv + ATT_SPLIT - 1) / ATT_SPLIT);
+    const int64_t rows = (int64_t) a.T * (nq / nk);
+    const bool mf = rows >= 64;   // the matrix-core products (prefill chunks, large batches)
+    if (mf)
+        hipLaunchKernelGGL(k_attn_scores_mf, dim3((unsigned) ((a.n_kv + 63) / 64), (unsigned) nk,
+                                                  (unsigned) ((rows + 63) / 64)), dim3(256), 0, st, a);
+    else
+        hipLaunchKernelGGL(k_attn_scores, dim3((unsigned) ((a.n_kv + 63) / 64), (unsigned) nk, (unsigned) a.T),
+                           dim3(256), 0, st, a);
+    const dim3 sm_grid((unsigned) nq, (unsigned) a.T);
+    const int64_t ng = a.n_kv / 8;   // whole groups of eight per row
+    if (ng <= 256) hipLaunchKernelGGL(k_attn_softmax_r<1>, sm_grid, dim3(256), 0, st, a);
+    else if (ng <= 512) hipLaunchKernelGGL(k_attn_softmax_r<2>, sm_grid, dim3(256), 0, st, a);
+    else if (ng <= 1024) hipLaunchKernelGGL(k_attn_softmax_r<4>, sm_grid, dim3(256), 0, st, a);
+    else if (ng <= 2048) hipLaunchKernelGGL(k_attn_softmax_r<8>, sm_grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(k_attn_softmax, sm_grid, dim3(256), 0, st, a);
+    if (mf) {
+        hipLaunchKernelGGL(k_attn_pv_mf, dim3((unsigned) nk, (unsigned) ((rows + 63) / 64)), dim3(256), 0, st, a);
+        return hipGetLastError() == hipSuccess ? 0 : -3;
+    }
+    if (a.split <= 0) return -2;
+    const int n_split = (int) ((a.n_kv + a.split - 1) / a.split);
     hipLaunchKernelGGL(k_attn_pv, dim3((unsigned) nk, (unsigned) a.T, (unsigned) n_split), dim3(256), 0, st, a);
     const int64_t n = (int64_t) a.T * nq * AD;
     hipLaunchKernelGGL(k_attn_combine, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, st, a, n_split);

@@ -129,7 +129,11 @@ void* scratch_ptr(int device);
 // attn.hip: the attention half of Seg A (per-head norms, NEOX RoPE, f16 KV cache,
 // GQA scores, softmax, P.V), head dimension 128
 constexpr int ATT_RMAX = 16;      // query heads per kv head, at most
-constexpr int ATT_SPLIT = 512;    // keys per P.V partial sum
+// Keys per P.V partial sum: 64 while the (kv head, token) pairs alone would
+// leave most CUs idle (decode, verify batches), else 512.
+inline int64_t attn_split(int64_t T, int64_t n_head_kv, int64_t n_kv) {
+    return T * n_head_kv * ((n_kv + 511) / 512) >= 512 ? 512 : 64;
+}
 struct AttnArgs {
     int T, n_head, n_head_kv;
     int64_t n_past, n_kv;         // n_kv = n_past + T keys after this call's rows are written
@@ -143,7 +147,8 @@ struct AttnArgs {
     uint16_t* kc;                 // f16 caches [n_ctx][n_head_kv * 128], 16-byte aligned
     uint16_t* vc;
     float* s;                     // [T][n_head][n_kv] scores, then probabilities
-    float* part;                  // [ceil(n_kv / ATT_SPLIT)][T][n_head][128]
+    int64_t split;                // keys per P.V partial sum (attn_split)
+    float* part;                  // [ceil(n_kv / split)][T][n_head][128]
     float* att;                   // [T][n_head * 128]
 };
 int launch_attn_core(const AttnArgs& a, hipStream_t stream);

@@ -9,7 +9,8 @@ cache rows the call writes: V bit for bit, K within one f16 step.
 
 * the 30B-A3B attention shape (H = 2048, 32 query / 4 kv heads, D = 128,
   Q4_K q/k/o, Q6_K v): decode at n_past 0, 37 and 700, a T = 5 verify batch,
-  a T = 64 prefill chunk, and decode at n_past 3000 (several P.V splits);
+  T = 64 and T = 37 prefill chunks (the matrix-core products), and decode at
+  n_past 3000 (many P.V partial sums);
 * the decoder layer equals its parts (attn_seg -> ffn_layer -> residual add)
   bit for bit, and the whole layer matches ggml's attention graph followed by
   ggml's MoE layer within 1e-3 where both route the same experts.
@@ -125,12 +126,14 @@ def test_attn_seg_30b_shape_steps(orc):
     kc, vc = filled_caches(1024, 700, seed=9)
     g = GpuAttn(aw, 1024, kc, vc)
     rng = np.random.default_rng(1)
-    for T, n_past in ((1, 0), (1, 37), (5, 40), (64, 100), (1, 700)):
+    # T = 64 and 37 take the matrix-core products (at least 64 query rows), 37 with
+    # a ragged last row block; the others the decode kernels
+    for T, n_past in ((1, 0), (1, 37), (5, 40), (64, 100), (37, 164), (1, 700)):
         check_step(orc, g, rng.standard_normal((T, H)).astype(np.float32), n_past, f"T={T} n_past={n_past}")
 
 
 def test_attn_seg_long_context(orc):
-    note("attn_seg 30B shape, decode at n_past=3000 (P.V in 6 splits)")
+    note("attn_seg 30B shape, decode at n_past=3000 (P.V in 47 partial sums)")
     aw = AttnWeights(H, NH, NKV, D, TYPES, seed=4, oracle=orc)
     kc, vc = filled_caches(4096, 3000, seed=10)
     g = GpuAttn(aw, 4096, kc, vc)
