@@ -313,13 +313,15 @@ __device__ __forceinline__ h4 f4_to_h4(float x0, float x1, float x2, float x3) {
     return h4{(_Float16) x0, (_Float16) x1, (_Float16) x2, (_Float16) x3};
 }
 
-// Scores: a workgroup takes 64 rows (a wave per 16) and 64 keys (four 16-key
-// tiles), eight MFMAs over the 128 dims per tile.  B is read straight from the
-// cache rows (8 bytes per lane and dim step).
+// Scores: a workgroup takes 64 rows (a wave per 16, their Q in registers) and
+// MF_SK keys, 16 at a time: eight MFMAs over the 128 dims per 16-key tile, the
+// next tile's key rows loaded while the current one is multiplied.  B is read
+// straight from the cache rows (8 bytes per lane and dim step).
+constexpr int MF_SK = 512;   // keys per workgroup of k_attn_scores_mf
 __global__ void __launch_bounds__(256) k_attn_scores_mf(AttnArgs a) {
     const int g = blockIdx.y, tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, q = l >> 4;
     const int nq = a.n_head, R = nq / a.n_head_kv, gqa = a.n_head_kv * AD;
-    const int64_t rows = (int64_t) a.T * R, key0 = (int64_t) blockIdx.x * 64;
+    const int64_t rows = (int64_t) a.T * R, key0 = (int64_t) blockIdx.x * MF_SK;
     const int64_t ra = (int64_t) blockIdx.z * 64 + 16 * w + li;   // this lane's A row
     h4 qa[8];
     if (ra < rows) {
@@ -334,25 +336,35 @@ __global__ void __launch_bounds__(256) k_attn_scores_mf(AttnArgs a) {
 #pragma unroll
         for (int st = 0; st < 8; ++st) qa[st] = h4{0, 0, 0, 0};
     }
+    // rows of this wave: the last token they hold bounds the keys that are not masked for all of them
+    const int64_t rw0 = (int64_t) blockIdx.z * 64 + 16 * w;
+    const int64_t kend = min(min((int64_t) a.n_kv, key0 + MF_SK), a.n_kv);
+    auto load_b = [&](int64_t j0, h4 (&kb)[8]) __attribute__((always_inline)) {
+        const int64_t jb = j0 + li;
+        const bool ok = jb < kend;
+        const _Float16* krow = (const _Float16*) a.kc + (ok ? jb : 0) * gqa + g * AD + 4 * q;
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-        const int64_t jb = key0 + 16 * kt + li;   // this lane's B column (key)
-        const bool kv_ok = jb < a.n_kv;
-        const _Float16* krow = (const _Float16*) a.kc + (kv_ok ? jb : 0) * gqa + g * AD + 4 * q;
+        for (int st = 0; st < 8; ++st) kb[st] = ok ? *(const h4*) (krow + 16 * st) : h4{0, 0, 0, 0};
+    };
+    if (rw0 >= rows) return;
+    h4 kc[8], kn[8];
+    load_b(key0, kc);
+    for (int64_t j0 = key0; j0 < kend; j0 += 16) {
+        if (j0 + 16 < kend) load_b(j0 + 16, kn);
         f4 acc = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int st = 0; st < 8; ++st) {
-            const h4 kb = kv_ok ? *(const h4*) (krow + 16 * st) : h4{0, 0, 0, 0};
-            acc = __builtin_amdgcn_mfma_f32_16x16x16f16(qa[st], kb, acc, 0, 0, 0);
-        }
+        for (int st = 0; st < 8; ++st) acc = __builtin_amdgcn_mfma_f32_16x16x16f16(qa[st], kc[st], acc, 0, 0, 0);
+        const int64_t jb = j0 + li;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int64_t r = (int64_t) blockIdx.z * 64 + 16 * w + 4 * q + i;
-            if (r < rows && kv_ok) {
+            const int64_t r = rw0 + 4 * q + i;
+            if (r < rows && jb < kend) {
                 const int t = (int) (r / R), h = (int) (r % R);
                 a.s[((int64_t) t * nq + g * R + h) * a.n_kv + jb] = jb > a.n_past + t ? -INFINITY : acc[i] * a.kq_scale;
             }
         }
+#pragma unroll
+        for (int st = 0; st < 8; ++st) kc[st] = kn[st];
     }
 }
 
@@ -376,12 +388,16 @@ __global__ void __launch_bounds__(256) k_attn_pv_mf(AttnArgs a) {
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt) acc[nt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     const int sk = tid & 63, sdq = tid >> 6;   // staging: key sk of the chunk, dims 32 sdq .. +32
-    for (int64_t c0 = 0; c0 < klim; c0 += 64) {
+    auto load_v = [&](int64_t c0, uint4 (&vv)[4]) __attribute__((always_inline)) {
         const int64_t kj = c0 + sk;
-        uint4 vv[4];
         const uint4* vrow = (const uint4*) ((const _Float16*) a.vc + (kj < klim ? kj : 0) * gqa + g * AD + 32 * sdq);
 #pragma unroll
         for (int i = 0; i < 4; ++i) vv[i] = kj < klim ? vrow[i] : uint4{0u, 0u, 0u, 0u};
+    };
+    uint4 vv[4], vn[4];
+    load_v(0, vv);
+    for (int64_t c0 = 0; c0 < klim; c0 += 64) {
+        if (c0 + 64 < klim) load_v(c0 + 64, vn);   // the next chunk's rows, in flight during this one
         __syncthreads();   // the previous chunk's B reads are done
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -407,6 +423,8 @@ __global__ void __launch_bounds__(256) k_attn_pv_mf(AttnArgs a) {
                 acc[nt] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, vb, acc[nt], 0, 0, 0);
             }
         }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) vv[i] = vn[i];
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -467,7 +485,7 @@ int launch_attn_core(const AttnArgs& a, hipStream_t st) {
     const int64_t rows = (int64_t) a.T * (nq / nk);
     const bool mf = rows >= 64;   // the matrix-core products (prefill chunks, large batches)
     if (mf)
-        hipLaunchKernelGGL(k_attn_scores_mf, dim3((unsigned) ((a.n_kv + 63) / 64), (unsigned) nk,
+        hipLaunchKernelGGL(k_attn_scores_mf, dim3((unsigned) ((a.n_kv + MF_SK - 1) / MF_SK), (unsigned) nk,
                                                   (unsigned) ((rows + 63) / 64)), dim3(256), 0, st, a);
     else
         hipLaunchKernelGGL(k_attn_scores, dim3((unsigned) ((a.n_kv + 63) / 64), (unsigned) nk, (unsigned) a.T),
