@@ -594,12 +594,18 @@ int qwmoe_attn_seg(void* stream, const qwmoe_attn_layer* L, const float* h, int6
     uint8_t* xv = vvt == vqt ? xq : vvt == vkt ? xk : ar.take<uint8_t>(rv * (size_t) T + 64);
     uint8_t* aq = ar.take<uint8_t>(ro * (size_t) T + 64);
     if (!xq || !xk || !xv || !aq) return QWMOE_ERR_WORKSPACE;
-    if ((rc = qw::launch_rms_norm(h, cur, H, T, rms_eps, st, L->attn_norm))) return rc;
     if ((rc = qw::launch_group_dense(rows, active, active_off, n_active, T, st))) return rc;
     const size_t hb = (size_t) H * 4;
-    if ((rc = qw::launch_quantize_act(vqt, cur, H, 1, T, hb, hb, xq, st))) return rc;
-    if (xk != xq && (rc = qw::launch_quantize_act(vkt, cur, H, 1, T, hb, hb, xk, st))) return rc;
-    if (xv != xq && xv != xk && (rc = qw::launch_quantize_act(vvt, cur, H, 1, T, hb, hb, xv, st))) return rc;
+    // attn_norm, then the projections' input quantized: one launch when every
+    // projection reads Q8_K (the K-quants), the same bits as the two steps
+    const bool fused_norm = vqt == qw::T_Q8_K && xk == xq && xv == xq &&
+                            qw::launch_rms_norm_q8K(h, H, T, rms_eps, L->attn_norm, xq, st) == 0;
+    if (!fused_norm) {
+        if ((rc = qw::launch_rms_norm(h, cur, H, T, rms_eps, st, L->attn_norm))) return rc;
+        if ((rc = qw::launch_quantize_act(vqt, cur, H, 1, T, hb, hb, xq, st))) return rc;
+        if (xk != xq && (rc = qw::launch_quantize_act(vkt, cur, H, 1, T, hb, hb, xk, st))) return rc;
+        if (xv != xq && xv != xk && (rc = qw::launch_quantize_act(vvt, cur, H, 1, T, hb, hb, xv, st))) return rc;
+    }
     auto proj_launch = [&](int type, const void* w, size_t nb1, int64_t K, int64_t N, const uint8_t* xb, size_t xrow,
                            float* dst) {
         const size_t ob = (size_t) N * 4;
@@ -607,8 +613,20 @@ int qwmoe_attn_seg(void* stream, const qwmoe_attn_layer* L, const float* h, int6
                                          active_off, n_active, 1, nullptr, 0, dst, ob, ob, T, T);
         return mmid_launch(m, st);
     };
-    if ((rc = proj_launch(L->type_q, L->wq, L->wq_nb1, H, NQ, xq, rq, q))) return rc;
-    if ((rc = proj_launch(L->type_k, L->wk, L->wk_nb1, H, NK, xk, rk, k))) return rc;
+    {   // Q and K in one GEMV launch when they share a type and neither takes the matrix cores
+        const qw::MmidArgs mq = mmid_args(L->type_q, L->wq, H, NQ, 1, L->wq_nb1, L->wq_nb1 * (size_t) NQ, xq, 1, rq,
+                                          rows, active, active_off, n_active, 1, nullptr, 0, q, (size_t) NQ * 4,
+                                          (size_t) NQ * 4, T, T);
+        const qw::MmidArgs mk = mmid_args(L->type_k, L->wk, H, NK, 1, L->wk_nb1, L->wk_nb1 * (size_t) NK, xk, 1, rk,
+                                          rows, active, active_off, n_active, 1, nullptr, 0, k, (size_t) NK * 4,
+                                          (size_t) NK * 4, T, T);
+        const bool pair = mq.type == mk.type && mq.mfma_min_rows == 0 && mk.mfma_min_rows == 0 && NQ >= NK &&
+                          qw::launch_mmid_gemv2(mq, mk, st) == 0;
+        if (!pair) {
+            if ((rc = mmid_launch(mq, st))) return rc;
+            if ((rc = mmid_launch(mk, st))) return rc;
+        }
+    }
     if ((rc = proj_launch(L->type_v, L->wv, L->wv_nb1, H, NK, xv, rv, v))) return rc;
     qw::AttnArgs a{};
     a.T = (int) T;
@@ -631,9 +649,10 @@ int qwmoe_attn_seg(void* stream, const qwmoe_attn_layer* L, const float* h, int6
     a.split = split;
     a.part = part;
     a.att = att;
+    a.att_q8K = vot == qw::T_Q8_K ? aq : nullptr;   // the split path quantizes att as it sums it
     if ((rc = qw::launch_attn_core(a, st))) return rc;
     const size_t qb = (size_t) NQ * 4;
-    if ((rc = qw::launch_quantize_act(vot, att, NQ, 1, T, qb, qb, aq, st))) return rc;
+    if (!qw::attn_writes_q8K(a) && (rc = qw::launch_quantize_act(vot, att, NQ, 1, T, qb, qb, aq, st))) return rc;
     if ((rc = proj_launch(L->type_o, L->wo, L->wo_nb1, NQ, H, aq, ro, proj))) return rc;
     return qw::launch_add_rms_norm_mul(proj, h, attn_resid, ffn_in, H, T, rms_eps, L->ffn_norm, st);
 }

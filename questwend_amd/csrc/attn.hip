@@ -471,6 +471,57 @@ __global__ void __launch_bounds__(256) k_add_rms_norm_mul(const float* __restric
     for (int64_t i = threadIdx.x; i < n; i += 256) out[o + i] = (resid[o + i] * scale) * w[i];
 }
 
+// attn_norm and the Q8_K quantisation of its output in one launch, one
+// 256-thread block per row of n (a multiple of 256): the sum of squares and
+// scale exactly as k_rms_norm, each value (x * scale) * w as it writes them, and
+// each 256-value block quantized by one wave as k_quant_q8K does.
+__global__ void __launch_bounds__(256) k_rms_norm_q8K(const float* __restrict__ x, int64_t n, float eps,
+                                                      const float* __restrict__ w, BlockQ8_K* __restrict__ dst) {
+    __shared__ double part[4];
+    const float* xr = x + (int64_t) blockIdx.x * n;
+    double s = 0.0;
+    for (int64_t i = threadIdx.x; i < n; i += 256) {
+        const float v = xr[i];
+        s += (double) (v * v);
+    }
+    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    const double tot = (part[0] + part[1]) + (part[2] + part[3]);
+    const float mean = (float) (tot / (double) n);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int64_t nb = n / QK_K;
+    for (int64_t ib = wv; ib < nb; ib += 4) {
+        const float4 q = *(const float4*) (xr + ib * QK_K + 4 * lane);
+        const float4 ww = *(const float4*) (w + ib * QK_K + 4 * lane);
+        const float v[4] = {(q.x * scale) * ww.x, (q.y * scale) * ww.y, (q.z * scale) * ww.z, (q.w * scale) * ww.w};
+        quant_q8K_wave(v, lane, dst + (int64_t) blockIdx.x * nb + ib);
+    }
+}
+
+// The P.V split sums (k_attn_combine's order) and the Q8_K quantisation of the
+// result (the attn_output projection's input) in one launch: one wave per
+// 256-value block of a token's row.
+__global__ void __launch_bounds__(256) k_attn_combine_q8K(AttnArgs a, int n_split, BlockQ8_K* __restrict__ dst) {
+    const int lane = threadIdx.x & 63;
+    const int64_t n = (int64_t) a.T * a.n_head * AD, nblk = n / QK_K;
+    const int64_t blk = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (blk >= nblk) return;
+    const int64_t i0 = blk * QK_K + 4 * lane;
+    float4 s4 = *(const float4*) (a.part + i0);
+#pragma unroll 4
+    for (int k = 1; k < n_split; ++k) {
+        const float4 o = *(const float4*) (a.part + (int64_t) k * n + i0);
+        s4.x = s4.x + o.x;
+        s4.y = s4.y + o.y;
+        s4.z = s4.z + o.z;
+        s4.w = s4.w + o.w;
+    }
+    const float v[4] = {s4.x, s4.y, s4.z, s4.w};
+    quant_q8K_wave(v, lane, dst + blk);
+}
+
 __global__ void k_fill_i32(int32_t* p, int64_t n, int32_t v) {
     const int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x;
     if (i < n) p[i] = v;
@@ -497,7 +548,7 @@ int launch_attn_core(const AttnArgs& a, hipStream_t st) {
     else if (ng <= 1024) hipLaunchKernelGGL(k_attn_softmax_r<4>, sm_grid, dim3(256), 0, st, a);
     else if (ng <= 2048) hipLaunchKernelGGL(k_attn_softmax_r<8>, sm_grid, dim3(256), 0, st, a);
     else hipLaunchKernelGGL(k_attn_softmax, sm_grid, dim3(256), 0, st, a);
-    if (mf) {
+    if (mf) {   // writes att (a.att_q8K is left to the caller)
         hipLaunchKernelGGL(k_attn_pv_mf, dim3((unsigned) nk, (unsigned) ((rows + 63) / 64)), dim3(256), 0, st, a);
         return hipGetLastError() == hipSuccess ? 0 : -3;
     }
@@ -505,7 +556,21 @@ int launch_attn_core(const AttnArgs& a, hipStream_t st) {
     const int n_split = (int) ((a.n_kv + a.split - 1) / a.split);
     hipLaunchKernelGGL(k_attn_pv, dim3((unsigned) nk, (unsigned) a.T, (unsigned) n_split), dim3(256), 0, st, a);
     const int64_t n = (int64_t) a.T * nq * AD;
-    hipLaunchKernelGGL(k_attn_combine, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, st, a, n_split);
+    if (a.att_q8K) {   // the split sums straight into the attn_output projection's Q8_K rows
+        const int64_t nblk = n / QK_K;
+        hipLaunchKernelGGL(k_attn_combine_q8K, dim3((unsigned) ((nblk + 3) / 4)), dim3(256), 0, st, a, n_split,
+                           (BlockQ8_K*) a.att_q8K);
+    } else {
+        hipLaunchKernelGGL(k_attn_combine, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, st, a, n_split);
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+int launch_rms_norm_q8K(const float* x, int64_t n, int64_t rows, float eps, const float* w, void* dst,
+                        hipStream_t st) {
+    if (n % QK_K || !w || (((uintptr_t) x | (uintptr_t) w) & 15)) return -2;
+    if (rows == 0) return 0;
+    hipLaunchKernelGGL(k_rms_norm_q8K, dim3((unsigned) rows), dim3(256), 0, st, x, n, eps, w, (BlockQ8_K*) dst);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 

@@ -825,7 +825,8 @@ int launch_mmid_gemv(const MmidArgs& m, hipStream_t stream) {
 }
 
 int launch_mmid_gemv2(const MmidArgs& a, const MmidArgs& b, hipStream_t stream) {
-    if (a.type != b.type || a.K != b.K || a.N != b.N || a.max_active != b.max_active || a.max_rows != b.max_rows ||
+    // the grid covers a's rows; b may have fewer (its workgroups past b.N return)
+    if (a.type != b.type || a.K != b.K || a.N < b.N || a.max_active != b.max_active || a.max_rows != b.max_rows ||
         a.act_row_bytes != b.act_row_bytes)
         return -2;
     MmidPair pr;

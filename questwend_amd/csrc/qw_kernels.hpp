@@ -92,7 +92,7 @@ int launch_mmid_gemv(const MmidArgs& m, hipStream_t stream);
 // whether launch_mmid_gemv forms the activations itself for these arguments with
 // swiglu_gate / swiglu_up set (small bins on the block-parallel kernel)
 bool mmid_gemv_swiglu_ok(const MmidArgs& m);
-// two GEMVs of the same type, shape and grouping in one launch (mfma_min_rows must be 0 in both)
+// two GEMVs of the same type, K and grouping in one launch (a.N >= b.N; gate and up, or Q and K)
 int launch_mmid_gemv2(const MmidArgs& a, const MmidArgs& b, hipStream_t stream);
 // mmid_mfma.hip
 bool mmid_mfma_supported(const MmidArgs& m);
@@ -150,8 +150,16 @@ struct AttnArgs {
     int64_t split;                // keys per P.V partial sum (attn_split)
     float* part;                  // [ceil(n_kv / split)][T][n_head][128]
     float* att;                   // [T][n_head * 128]
+    void* att_q8K;                // optional: Q8_K rows of att (the split path writes these instead of att)
 };
 int launch_attn_core(const AttnArgs& a, hipStream_t stream);
+// whether launch_attn_core writes a.att_q8K (and not att) for these arguments
+inline bool attn_writes_q8K(const AttnArgs& a) {
+    return a.att_q8K && (int64_t) a.T * (a.n_head / a.n_head_kv) < 64;
+}
+// attn_norm and its Q8_K quantisation in one launch (n % 256 == 0, x and w 16-byte aligned)
+int launch_rms_norm_q8K(const float* x, int64_t n, int64_t rows, float eps, const float* w, void* dst,
+                        hipStream_t stream);
 // resid = x + y; out = rms_norm(resid) * w (rows of n, dense), out may be null
 int launch_add_rms_norm_mul(const float* x, const float* y, float* resid, float* out, int64_t n, int64_t rows,
                             float eps, const float* w, hipStream_t stream);
