@@ -580,9 +580,11 @@ int qwmoe_attn_seg(void* stream, const qwmoe_attn_layer* L, const float* h, int6
     float* qr = ar.take<float>((size_t) (NQ * T));
     float* sc = ar.take<float>((size_t) (nq * T * n_kv));
     float* part = ar.take<float>((size_t) (n_split * T * NQ));
+    float* stat = ar.take<float>((size_t) (n_split * T * nq * 2));
     float* att = ar.take<float>((size_t) (NQ * T));
     float* proj = ar.take<float>((size_t) (H * T));
-    if (!rows || !active || !active_off || !n_active || !cur || !q || !k || !v || !qr || !sc || !part || !att || !proj)
+    if (!rows || !active || !active_off || !n_active || !cur || !q || !k || !v || !qr || !sc || !part || !stat || !att ||
+        !proj)
         return QWMOE_ERR_WORKSPACE;
     // quantized activations, one per vec_dot type in use
     const int vqt = qw::vec_dot_type(L->type_q), vkt = qw::vec_dot_type(L->type_k), vvt = qw::vec_dot_type(L->type_v);
@@ -648,6 +650,7 @@ int qwmoe_attn_seg(void* stream, const qwmoe_attn_layer* L, const float* h, int6
     a.s = sc;
     a.split = split;
     a.part = part;
+    a.stat = stat;
     a.att = att;
     a.att_q8K = vot == qw::T_Q8_K ? aq : nullptr;   // the split path quantizes att as it sums it
     if ((rc = qw::launch_attn_core(a, st))) return rc;

@@ -68,61 +68,6 @@ __global__ void __launch_bounds__(64) k_attn_qk_rope(AttnArgs a) {
     }
 }
 
-// Scores for the R = n_head / n_head_kv query heads of kv head g and token t:
-// s = (f16(q) . k) * kq_scale + mask, mask = 0 for key j <= n_past + t, -inf
-// after (the causal mask set_attn_inputs fills, core/runtime.cpp:2108-2116).
-// 64 keys per 256-thread block, four lanes per key: lane p of a key's quad
-// loads dims 32 p .. 32 p + 31 of the key row (four 16-byte loads) and forms
-// their part of each head's dot; the quad's parts are added by DPP.  The query
-// rows sit in LDS with one float of padding per 32, so the quad's four lanes
-// read four banks.
-constexpr int SQS = AD + AD / 32;   // padded query row
-__global__ void __launch_bounds__(256) k_attn_scores(AttnArgs a) {
-    __shared__ __align__(16) float sq[ATT_RMAX][SQS];
-    const int g = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
-    const int nq = a.n_head, R = nq / a.n_head_kv, gqa = a.n_head_kv * AD;
-    // the key row's loads first: their latency overlaps the query staging
-    const int p = tid & 3;
-    const int64_t j = (int64_t) blockIdx.x * 64 + (tid >> 2);
-    const bool valid = j < a.n_kv;
-    const uint4* krow = (const uint4*) ((const __half*) a.kc + (valid ? j : 0) * gqa + g * AD + 32 * p);
-    uint4 kv[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) kv[i] = krow[i];
-    for (int i = tid; i < R * AD; i += 256) {
-        const int h = i / AD, d = i % AD;
-        sq[h][d + d / 32] = to_f16_and_back(a.qr[((int64_t) t * nq + g * R + h) * AD + d]);
-    }
-    __syncthreads();
-    float kf[32];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t w4[4] = {kv[i].x, kv[i].y, kv[i].z, kv[i].w};
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const __half2 hv = *(const __half2*) &w4[m];
-            kf[8 * i + 2 * m] = __low2float(hv);
-            kf[8 * i + 2 * m + 1] = __high2float(hv);
-        }
-    }
-    const bool masked = j > a.n_past + t;
-    const float* qb = &sq[0][33 * p];
-    for (int h = 0; h < R; ++h) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 32; i += 4) {
-            const float4 q4 = *(const float4*) (qb + h * SQS + i);
-            acc = __builtin_fmaf(q4.x, kf[i], acc);
-            acc = __builtin_fmaf(q4.y, kf[i + 1], acc);
-            acc = __builtin_fmaf(q4.z, kf[i + 2], acc);
-            acc = __builtin_fmaf(q4.w, kf[i + 3], acc);
-        }
-        acc = acc + dpp_f<DPP_XOR1>(acc);
-        acc = acc + dpp_f<DPP_XOR2>(acc);
-        if (p == 0 && valid) a.s[((int64_t) t * nq + g * R + h) * a.n_kv + j] = masked ? -INFINITY : acc * a.kq_scale;
-    }
-}
-
 // ggml_compute_forward_soft_max_f32 on one (token, head) row of n_kv scores,
 // in place: max; v_expf(x - max) in groups of eight with each group's
 // hsum_float_8 added in double, expf on the tail; times (float) (1 / sum).
@@ -218,61 +163,183 @@ __global__ void __launch_bounds__(256) k_attn_softmax_r(AttnArgs a) {
     if (it < n) row[it] = te * inv;
 }
 
-// P.V partial sums over the keys [sp_i * split, ...) for kv head g and token
-// t: four 64-lane groups take every fourth key; lane l of a group holds output
-// elements 2 l, 2 l + 1 of each of the R query heads (one 4-byte load of V per
-// key); the groups' sums are added in group order through LDS.  The
-// probabilities of a chunk of up to 256 keys are staged in LDS, rounded to f16
-// (ggml's f16 vec_dot_type for the V product).
-__global__ void __launch_bounds__(256) k_attn_pv(AttnArgs a) {
-    __shared__ float sp[ATT_RMAX][256];
-    __shared__ float2 sred[3][ATT_RMAX][64];
+// ---- decode and small batches (fewer than 64 query rows): split softmax ----
+//
+// k_attn_split_scores: one workgroup per (kv head g, token t, key split): the
+// scores of its keys, 64 at a time with four lanes per key (each loads a quarter
+// of the f16 key row and forms its part of each head's dot; the quad's parts
+// added by DPP), written to the score rows, and per head the split's max m_s and
+// sum l_s = sum_j v_expf(s_j - m_s) (double; chunks rescaled by exp(m_old - m)).
+// k_attn_split_pv: per split, M = max_s m_s and S = sum_s exp(m_s - M) l_s (a
+// fixed order), then ggml's probabilities p_j = v_expf(s_j - M) * (float) (1 / S)
+// rounded to f16 (the f16 vec_dot_type of the V product) and the split's P.V
+// partial sums.  The e_j are ggml's (the same M and ggml_v_expf); S differs from
+// ggml's double sum only in the order of its terms, so p can move by one f16
+// step at a rounding boundary.  k_attn_combine(_q8K) adds the splits.
+constexpr int SQS = AD + AD / 32;   // padded query row in LDS (a key's four lanes read four banks)
+
+__global__ void __launch_bounds__(256) k_attn_split_scores(AttnArgs a) {
+    __shared__ __align__(16) float sq[ATT_RMAX][SQS];
+    __shared__ float ss[ATT_RMAX][64];
+    __shared__ float sm[ATT_RMAX];
+    __shared__ double sl[ATT_RMAX];
     const int g = blockIdx.x, t = blockIdx.y, sp_i = blockIdx.z, tid = threadIdx.x;
     const int lane = tid & 63, grp = tid >> 6;
     const int nq = a.n_head, R = nq / a.n_head_kv, gqa = a.n_head_kv * AD;
     const int64_t k0 = (int64_t) sp_i * a.split, k1 = min((int64_t) a.n_kv, k0 + a.split);
+    const int64_t vis = a.n_past + t;   // last key this token sees
+    for (int i = tid; i < R * AD; i += 256) {
+        const int h = i / AD, d = i % AD;
+        sq[h][d + d / 32] = to_f16_and_back(a.qr[((int64_t) t * nq + g * R + h) * AD + d]);
+    }
+    if (tid < ATT_RMAX) {
+        sm[tid] = -INFINITY;
+        sl[tid] = 0.0;
+    }
+    const int p = tid & 3, kq = tid >> 2;
+    for (int64_t c0 = k0; c0 < k1; c0 += 64) {
+        const int nc = (int) min((int64_t) 64, k1 - c0);
+        const int64_t j = c0 + kq;
+        const bool kok = kq < nc;
+        const uint4* krow = (const uint4*) ((const __half*) a.kc + (kok ? j : c0) * gqa + g * AD + 32 * p);
+        uint4 kv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kv[i] = krow[i];
+        __syncthreads();   // sq staged (first chunk); the previous chunk's ss reads are done
+        float kf[32];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t w4[4] = {kv[i].x, kv[i].y, kv[i].z, kv[i].w};
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const __half2 hv = *(const __half2*) &w4[m];
+                kf[8 * i + 2 * m] = __low2float(hv);
+                kf[8 * i + 2 * m + 1] = __high2float(hv);
+            }
+        }
+        const float* qb = &sq[0][33 * p];
+        for (int h = 0; h < R; ++h) {
+            float sd = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 32; i += 4) {
+                const float4 q4 = *(const float4*) (qb + h * SQS + i);
+                sd = __builtin_fmaf(q4.x, kf[i], sd);
+                sd = __builtin_fmaf(q4.y, kf[i + 1], sd);
+                sd = __builtin_fmaf(q4.z, kf[i + 2], sd);
+                sd = __builtin_fmaf(q4.w, kf[i + 3], sd);
+            }
+            sd = sd + dpp_f<DPP_XOR1>(sd);
+            sd = sd + dpp_f<DPP_XOR2>(sd);
+            if (p == 0) {
+                const float sv = j <= vis ? sd * a.kq_scale : -INFINITY;
+                if (kok) a.s[((int64_t) t * nq + g * R + h) * a.n_kv + j] = sv;
+                ss[h][kq] = kok ? sv : -INFINITY;
+            }
+        }
+        __syncthreads();
+        for (int h = grp; h < R; h += 4) {   // wave grp: heads grp, grp + 4, ...
+            const float sv = ss[h][lane];
+            float mc = sv;
+            for (int off = 32; off >= 1; off >>= 1) mc = fmaxf(mc, __shfl_xor(mc, off));
+            const float mo = sm[h], mn = fmaxf(mo, mc);
+            double es = sv == -INFINITY ? 0.0 : (double) v_expf(sv - mn);
+            for (int off = 32; off >= 1; off >>= 1) es += __shfl_xor(es, off);
+            if (lane == 0) {
+                const double al = mo == -INFINITY ? 0.0 : exp((double) mo - (double) mn);
+                sm[h] = mn;
+                sl[h] = sl[h] * al + es;
+            }
+        }
+    }
+    __syncthreads();
+    if (tid < R) {
+        const int64_t row = ((int64_t) sp_i * a.T + t) * nq + g * R + tid;
+        a.stat[2 * row] = sm[tid];
+        a.stat[2 * row + 1] = (float) sl[tid];
+    }
+}
+
+// P.V partial sums over the split's keys for kv head g and token t: four 64-lane
+// groups take every fourth key; lane l of a group holds output elements 2 l,
+// 2 l + 1 of each of the R query heads (one 4-byte V load per key); the groups'
+// sums are added in group order through LDS.
+__global__ void __launch_bounds__(256) k_attn_split_pv(AttnArgs a, int n_split) {
+    __shared__ float sp[ATT_RMAX][256];
+    __shared__ float2 sred[3][ATT_RMAX][64];
+    __shared__ float sM[ATT_RMAX], sI[ATT_RMAX];
+    const int g = blockIdx.x, t = blockIdx.y, sp_i = blockIdx.z, tid = threadIdx.x;
+    const int lane = tid & 63, grp = tid >> 6;
+    const int nq = a.n_head, R = nq / a.n_head_kv, gqa = a.n_head_kv * AD;
+    const int64_t k0 = (int64_t) sp_i * a.split, k1 = min((int64_t) a.n_kv, k0 + a.split);
+    // the first keys' V before the statistics and the staging (their latency overlaps them)
+    const __half2* vb0 = (const __half2*) ((const __half*) a.vc + k0 * gqa + g * AD) + lane;
+    const int nc0 = (int) min((int64_t) 256, k1 - k0);
+    __half2 v16[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+        const int jj = grp + 4 * u;
+        v16[u] = jj < nc0 ? vb0[(int64_t) jj * (gqa / 2)] : __half2{};
+    }
+    // M and S of each head over all splits (wave grp: heads grp, grp + 4, ...; lane s0
+    // takes splits s0, s0 + 64, ...; the lanes' sums added in a fixed tree order)
+    for (int h = grp; h < R; h += 4) {
+        float mx = -INFINITY;
+        for (int s0 = lane; s0 < n_split; s0 += 64)
+            mx = fmaxf(mx, a.stat[2 * (((int64_t) s0 * a.T + t) * nq + g * R + h)]);
+        for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+        double S = 0.0;
+        for (int s0 = lane; s0 < n_split; s0 += 64) {
+            const int64_t r = ((int64_t) s0 * a.T + t) * nq + g * R + h;
+            const float ms = a.stat[2 * r];
+            if (ms != -INFINITY) S += exp((double) ms - (double) mx) * (double) a.stat[2 * r + 1];
+        }
+        for (int off = 32; off >= 1; off >>= 1) S += __shfl_xor(S, off);
+        if (lane == 0) {
+            sM[h] = mx;
+            sI[h] = (float) (1.0 / S);
+        }
+    }
     float2 acc[ATT_RMAX];
 #pragma unroll
     for (int h = 0; h < ATT_RMAX; ++h) acc[h] = float2{0.0f, 0.0f};
     for (int64_t c0 = k0; c0 < k1; c0 += 256) {
         const int nc = (int) min((int64_t) 256, k1 - c0);
-        const __half2* vb = (const __half2*) ((const __half*) a.vc + c0 * gqa + g * AD) + lane;
-        // the first keys' V before the staging barrier (a 64-key split is one
-        // round of 16 per group: all of its loads overlap the staging)
-        __half2 v16[16];
-#pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            const int jj = grp + 4 * u;
-            v16[u] = jj < nc ? vb[(int64_t) jj * (gqa / 2)] : __half2{};
-        }
-        __syncthreads();
+        __syncthreads();   // sM / sI written; the previous chunk's sp reads are done
         for (int i = tid; i < R * 256; i += 256) {
             const int h = i / 256, jj = i % 256;
-            sp[h][jj] = jj < nc ? to_f16_and_back(a.s[((int64_t) t * nq + g * R + h) * a.n_kv + c0 + jj]) : 0.0f;
+            float pv = 0.0f;
+            if (jj < nc) {
+                const float sv = a.s[((int64_t) t * nq + g * R + h) * a.n_kv + c0 + jj];
+                pv = sv == -INFINITY ? 0.0f : to_f16_and_back(v_expf(sv - sM[h]) * sI[h]);
+            }
+            sp[h][jj] = pv;
         }
         __syncthreads();
+        const __half2* vb = (const __half2*) ((const __half*) a.vc + c0 * gqa + g * AD) + lane;
+        if (c0 == k0) {
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            const int jj = grp + 4 * u;
-            if (jj >= nc) break;
-            const float2 v = __half22float2(v16[u]);
+            for (int u = 0; u < 16; ++u) {
+                const int jj = grp + 4 * u;
+                if (jj >= nc) break;
+                const float2 v = __half22float2(v16[u]);
 #pragma unroll
-            for (int h = 0; h < ATT_RMAX; ++h)
-                if (h < R) {
-                    const float p = sp[h][jj];
-                    acc[h].x = __builtin_fmaf(p, v.x, acc[h].x);
-                    acc[h].y = __builtin_fmaf(p, v.y, acc[h].y);
-                }
+                for (int h = 0; h < ATT_RMAX; ++h)
+                    if (h < R) {
+                        const float pe = sp[h][jj];
+                        acc[h].x = __builtin_fmaf(pe, v.x, acc[h].x);
+                        acc[h].y = __builtin_fmaf(pe, v.y, acc[h].y);
+                    }
+            }
         }
 #pragma unroll 4
-        for (int jj = grp + 64; jj < nc; jj += 4) {
+        for (int jj = grp + (c0 == k0 ? 64 : 0); jj < nc; jj += 4) {
             const float2 v = __half22float2(vb[(int64_t) jj * (gqa / 2)]);
 #pragma unroll
             for (int h = 0; h < ATT_RMAX; ++h)
                 if (h < R) {
-                    const float p = sp[h][jj];
-                    acc[h].x = __builtin_fmaf(p, v.x, acc[h].x);
-                    acc[h].y = __builtin_fmaf(p, v.y, acc[h].y);
+                    const float pe = sp[h][jj];
+                    acc[h].x = __builtin_fmaf(pe, v.x, acc[h].x);
+                    acc[h].y = __builtin_fmaf(pe, v.y, acc[h].y);
                 }
         }
     }
@@ -296,6 +363,39 @@ __global__ void __launch_bounds__(256) k_attn_pv(AttnArgs a) {
                 *(float2*) &a.part[(((int64_t) sp_i * a.T + t) * nq + g * R + h) * AD + 2 * lane] = s2;
             }
     }
+}
+
+// att[t][h][d] = the sum of the splits' partials, in split order.
+__global__ void __launch_bounds__(256) k_attn_combine(AttnArgs a, int n_split) {
+    const int64_t n = (int64_t) a.T * a.n_head * AD;
+    const int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    float s = a.part[i];
+#pragma unroll 8
+    for (int k = 1; k < n_split; ++k) s = s + a.part[(int64_t) k * n + i];
+    a.att[i] = s;
+}
+
+// The P.V split sums (k_attn_combine's order) and the Q8_K quantisation of the
+// result (the attn_output projection's input) in one launch: one wave per
+// 256-value block of a token's row.
+__global__ void __launch_bounds__(256) k_attn_combine_q8K(AttnArgs a, int n_split, BlockQ8_K* __restrict__ dst) {
+    const int lane = threadIdx.x & 63;
+    const int64_t n = (int64_t) a.T * a.n_head * AD, nblk = n / QK_K;
+    const int64_t blk = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (blk >= nblk) return;
+    const int64_t i0 = blk * QK_K + 4 * lane;
+    float4 s4 = *(const float4*) (a.part + i0);
+#pragma unroll 4
+    for (int k = 1; k < n_split; ++k) {
+        const float4 o = *(const float4*) (a.part + (int64_t) k * n + i0);
+        s4.x = s4.x + o.x;
+        s4.y = s4.y + o.y;
+        s4.z = s4.z + o.z;
+        s4.w = s4.w + o.w;
+    }
+    const float v[4] = {s4.x, s4.y, s4.z, s4.w};
+    quant_q8K_wave(v, lane, dst + blk);
 }
 
 // ---- batches of at least 64 query rows: the two products on the matrix cores ----
@@ -437,17 +537,6 @@ __global__ void __launch_bounds__(256) k_attn_pv_mf(AttnArgs a) {
     }
 }
 
-// att[t][h][d] = the sum of the splits' partials, in split order.
-__global__ void __launch_bounds__(256) k_attn_combine(AttnArgs a, int n_split) {
-    const int64_t n = (int64_t) a.T * a.n_head * AD;
-    const int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x;
-    if (i >= n) return;
-    float s = a.part[i];
-#pragma unroll 8
-    for (int k = 1; k < n_split; ++k) s = s + a.part[(int64_t) k * n + i];
-    a.att[i] = s;
-}
-
 // resid = x + y (ggml_add), out = rms_norm(resid) * w (k_rms_norm's order); one
 // 256-thread block per row of n.
 __global__ void __launch_bounds__(256) k_add_rms_norm_mul(const float* __restrict__ x, const float* __restrict__ y,
@@ -500,28 +589,6 @@ __global__ void __launch_bounds__(256) k_rms_norm_q8K(const float* __restrict__ 
     }
 }
 
-// The P.V split sums (k_attn_combine's order) and the Q8_K quantisation of the
-// result (the attn_output projection's input) in one launch: one wave per
-// 256-value block of a token's row.
-__global__ void __launch_bounds__(256) k_attn_combine_q8K(AttnArgs a, int n_split, BlockQ8_K* __restrict__ dst) {
-    const int lane = threadIdx.x & 63;
-    const int64_t n = (int64_t) a.T * a.n_head * AD, nblk = n / QK_K;
-    const int64_t blk = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (blk >= nblk) return;
-    const int64_t i0 = blk * QK_K + 4 * lane;
-    float4 s4 = *(const float4*) (a.part + i0);
-#pragma unroll 4
-    for (int k = 1; k < n_split; ++k) {
-        const float4 o = *(const float4*) (a.part + (int64_t) k * n + i0);
-        s4.x = s4.x + o.x;
-        s4.y = s4.y + o.y;
-        s4.z = s4.z + o.z;
-        s4.w = s4.w + o.w;
-    }
-    const float v[4] = {s4.x, s4.y, s4.z, s4.w};
-    quant_q8K_wave(v, lane, dst + blk);
-}
-
 __global__ void k_fill_i32(int32_t* p, int64_t n, int32_t v) {
     const int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x;
     if (i < n) p[i] = v;
@@ -535,12 +602,22 @@ int launch_attn_core(const AttnArgs& a, hipStream_t st) {
     hipLaunchKernelGGL(k_attn_qk_rope, dim3((unsigned) a.T, (unsigned) (nq + 2 * nk)), dim3(64), 0, st, a);
     const int64_t rows = (int64_t) a.T * (nq / nk);
     const bool mf = rows >= 64;   // the matrix-core products (prefill chunks, large batches)
-    if (mf)
-        hipLaunchKernelGGL(k_attn_scores_mf, dim3((unsigned) ((a.n_kv + MF_SK - 1) / MF_SK), (unsigned) nk,
-                                                  (unsigned) ((rows + 63) / 64)), dim3(256), 0, st, a);
-    else
-        hipLaunchKernelGGL(k_attn_scores, dim3((unsigned) ((a.n_kv + 63) / 64), (unsigned) nk, (unsigned) a.T),
-                           dim3(256), 0, st, a);
+    if (!mf) {   // decode and small batches: split softmax, three launches
+        if (a.split <= 0 || !a.stat) return -2;
+        const int n_split = (int) ((a.n_kv + a.split - 1) / a.split);
+        const dim3 grid((unsigned) nk, (unsigned) a.T, (unsigned) n_split);
+        hipLaunchKernelGGL(k_attn_split_scores, grid, dim3(256), 0, st, a);
+        hipLaunchKernelGGL(k_attn_split_pv, grid, dim3(256), 0, st, a, n_split);
+        const int64_t n = (int64_t) a.T * nq * AD;
+        if (a.att_q8K)   // the split sums straight into the attn_output projection's Q8_K rows
+            hipLaunchKernelGGL(k_attn_combine_q8K, dim3((unsigned) ((n / QK_K + 3) / 4)), dim3(256), 0, st, a, n_split,
+                               (BlockQ8_K*) a.att_q8K);
+        else
+            hipLaunchKernelGGL(k_attn_combine, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, st, a, n_split);
+        return hipGetLastError() == hipSuccess ? 0 : -3;
+    }
+    hipLaunchKernelGGL(k_attn_scores_mf, dim3((unsigned) ((a.n_kv + MF_SK - 1) / MF_SK), (unsigned) nk,
+                                              (unsigned) ((rows + 63) / 64)), dim3(256), 0, st, a);
     const dim3 sm_grid((unsigned) nq, (unsigned) a.T);
     const int64_t ng = a.n_kv / 8;   // whole groups of eight per row
     if (ng <= 256) hipLaunchKernelGGL(k_attn_softmax_r<1>, sm_grid, dim3(256), 0, st, a);
@@ -548,21 +625,8 @@ int launch_attn_core(const AttnArgs& a, hipStream_t st) {
     else if (ng <= 1024) hipLaunchKernelGGL(k_attn_softmax_r<4>, sm_grid, dim3(256), 0, st, a);
     else if (ng <= 2048) hipLaunchKernelGGL(k_attn_softmax_r<8>, sm_grid, dim3(256), 0, st, a);
     else hipLaunchKernelGGL(k_attn_softmax, sm_grid, dim3(256), 0, st, a);
-    if (mf) {   // writes att (a.att_q8K is left to the caller)
-        hipLaunchKernelGGL(k_attn_pv_mf, dim3((unsigned) nk, (unsigned) ((rows + 63) / 64)), dim3(256), 0, st, a);
-        return hipGetLastError() == hipSuccess ? 0 : -3;
-    }
-    if (a.split <= 0) return -2;
-    const int n_split = (int) ((a.n_kv + a.split - 1) / a.split);
-    hipLaunchKernelGGL(k_attn_pv, dim3((unsigned) nk, (unsigned) a.T, (unsigned) n_split), dim3(256), 0, st, a);
-    const int64_t n = (int64_t) a.T * nq * AD;
-    if (a.att_q8K) {   // the split sums straight into the attn_output projection's Q8_K rows
-        const int64_t nblk = n / QK_K;
-        hipLaunchKernelGGL(k_attn_combine_q8K, dim3((unsigned) ((nblk + 3) / 4)), dim3(256), 0, st, a, n_split,
-                           (BlockQ8_K*) a.att_q8K);
-    } else {
-        hipLaunchKernelGGL(k_attn_combine, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, st, a, n_split);
-    }
+    // writes att (a.att_q8K is left to the caller)
+    hipLaunchKernelGGL(k_attn_pv_mf, dim3((unsigned) nk, (unsigned) ((rows + 63) / 64)), dim3(256), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 

@@ -129,10 +129,14 @@ void* scratch_ptr(int device);
 // attn.hip: the attention half of Seg A (per-head norms, NEOX RoPE, f16 KV cache,
 // GQA scores, softmax, P.V), head dimension 128
 constexpr int ATT_RMAX = 16;      // query heads per kv head, at most
-// Keys per P.V partial sum: 64 while the (kv head, token) pairs alone would
-// leave most CUs idle (decode, verify batches), else 512.
+// Keys per split of the split-softmax path (fewer than 64 query rows): a
+// multiple of 64 that gives the (kv head, token, split) workgroups about 512 in
+// all (64 keys at the 30B decode shape up to 8 k keys of context).
 inline int64_t attn_split(int64_t T, int64_t n_head_kv, int64_t n_kv) {
-    return T * n_head_kv * ((n_kv + 511) / 512) >= 512 ? 512 : 64;
+    const int64_t pairs = T * n_head_kv > 0 ? T * n_head_kv : 1;
+    const int64_t want = 512 / pairs > 1 ? 512 / pairs : 1;   // splits per (kv head, token)
+    const int64_t keys = (n_kv + want - 1) / want;
+    return 64 * ((keys + 63) / 64 > 0 ? (keys + 63) / 64 : 1);
 }
 struct AttnArgs {
     int T, n_head, n_head_kv;
@@ -147,8 +151,9 @@ struct AttnArgs {
     uint16_t* kc;                 // f16 caches [n_ctx][n_head_kv * 128], 16-byte aligned
     uint16_t* vc;
     float* s;                     // [T][n_head][n_kv] scores, then probabilities
-    int64_t split;                // keys per P.V partial sum (attn_split)
-    float* part;                  // [ceil(n_kv / split)][T][n_head][128]
+    int64_t split;                // keys per split (attn_split; fewer than 64 query rows)
+    float* part;                  // [ceil(n_kv / split)][T][n_head][128] partial products
+    float* stat;                  // [ceil(n_kv / split)][T][n_head][2]: each split's max and sum
     float* att;                   // [T][n_head * 128]
     void* att_q8K;                // optional: Q8_K rows of att (the split path writes these instead of att)
 };
