@@ -580,7 +580,7 @@ int qwmoe_attn_seg(void* stream, const qwmoe_attn_layer* L, const float* h, int6
     float* qr = ar.take<float>((size_t) (NQ * T));
     float* sc = ar.take<float>((size_t) (nq * T * n_kv));
     float* part = ar.take<float>((size_t) (n_split * T * NQ));
-    float* stat = ar.take<float>((size_t) (n_split * T * nq * 2));
+    float* stat = ar.take<float>((size_t) (qw::attn_stat_blocks(T, nk, n_kv) * T * nq * 2));
     float* att = ar.take<float>((size_t) (NQ * T));
     float* proj = ar.take<float>((size_t) (H * T));
     if (!rows || !active || !active_off || !n_active || !cur || !q || !k || !v || !qr || !sc || !part || !stat || !att ||

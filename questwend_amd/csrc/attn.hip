@@ -68,101 +68,6 @@ __global__ void __launch_bounds__(64) k_attn_qk_rope(AttnArgs a) {
     }
 }
 
-// ggml_compute_forward_soft_max_f32 on one (token, head) row of n_kv scores,
-// in place: max; v_expf(x - max) in groups of eight with each group's
-// hsum_float_8 added in double, expf on the tail; times (float) (1 / sum).
-__global__ void __launch_bounds__(256) k_attn_softmax(AttnArgs a) {
-    __shared__ float red[4];
-    __shared__ double dred[4];
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    float* row = a.s + ((int64_t) blockIdx.y * a.n_head + blockIdx.x) * a.n_kv;
-    const int64_t n = a.n_kv, ng = n / 8;
-    float mx = -INFINITY;
-    for (int64_t i = tid; i < n; i += 256) mx = fmaxf(mx, row[i]);
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-    if (lane == 0) red[wv] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    double sum = 0.0;
-    for (int64_t q = tid; q < ng; q += 256) {
-        float e[8];
-#pragma unroll
-        for (int m = 0; m < 8; ++m) e[m] = v_expf(row[8 * q + m] - mx);
-#pragma unroll
-        for (int m = 0; m < 8; ++m) row[8 * q + m] = e[m];
-        sum += (double) hsum8(e);
-    }
-    for (int64_t i = 8 * ng + tid; i < n; i += 256) {
-        const float e = (float) exp((double) (row[i] - mx));
-        row[i] = e;
-        sum += (double) e;
-    }
-    for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off);
-    if (lane == 0) dred[wv] = sum;
-    __syncthreads();
-    const double tot = (dred[0] + dred[1]) + (dred[2] + dred[3]);
-    const float inv = (float) (1.0 / tot);
-    for (int64_t i = tid; i < n; i += 256) row[i] = row[i] * inv;
-}
-
-// The same softmax with the row held in registers (one read and one write of
-// the row): thread tid holds the groups of eight tid, tid + 256, ... (NG of
-// them, rows of up to 2048 NG elements); the tail past the last whole group is
-// taken by the first threads, as in the loop form above.
-template <int NG>
-__global__ void __launch_bounds__(256) k_attn_softmax_r(AttnArgs a) {
-    __shared__ float red[4];
-    __shared__ double dred[4];
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    float* row = a.s + ((int64_t) blockIdx.y * a.n_head + blockIdx.x) * a.n_kv;
-    const int64_t n = a.n_kv, ng = n / 8;
-    float e[NG][8];   // (rows start at any multiple of 4 bytes: scalar loads)
-#pragma unroll
-    for (int u = 0; u < NG; ++u) {
-        const int64_t q = tid + 256 * u;
-#pragma unroll
-        for (int m = 0; m < 8; ++m) e[u][m] = q < ng ? row[8 * q + m] : -INFINITY;
-    }
-    const int64_t it = 8 * ng + tid;   // this thread's tail element, if any
-    const float tv = it < n ? row[it] : -INFINITY;
-    float mx = tv;
-#pragma unroll
-    for (int u = 0; u < NG; ++u)
-#pragma unroll
-        for (int m = 0; m < 8; ++m) mx = fmaxf(mx, e[u][m]);
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-    if (lane == 0) red[wv] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    double sum = 0.0;
-#pragma unroll
-    for (int u = 0; u < NG; ++u)
-        if (tid + 256 * u < ng) {
-#pragma unroll
-            for (int m = 0; m < 8; ++m) e[u][m] = v_expf(e[u][m] - mx);
-            sum += (double) hsum8(e[u]);
-        }
-    float te = 0.0f;
-    if (it < n) {
-        te = (float) exp((double) (tv - mx));
-        sum += (double) te;
-    }
-    for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off);
-    if (lane == 0) dred[wv] = sum;
-    __syncthreads();
-    const double tot = (dred[0] + dred[1]) + (dred[2] + dred[3]);
-    const float inv = (float) (1.0 / tot);
-#pragma unroll
-    for (int u = 0; u < NG; ++u) {
-        const int64_t q = tid + 256 * u;
-        if (q < ng) {
-#pragma unroll
-            for (int m = 0; m < 8; ++m) row[8 * q + m] = e[u][m] * inv;
-        }
-    }
-    if (it < n) row[it] = te * inv;
-}
-
 // ---- decode and small batches (fewer than 64 query rows): split softmax ----
 //
 // k_attn_split_scores: one workgroup per (kv head g, token t, key split): the
@@ -417,7 +322,7 @@ __device__ __forceinline__ h4 f4_to_h4(float x0, float x1, float x2, float x3) {
 // MF_SK keys, 16 at a time: eight MFMAs over the 128 dims per 16-key tile, the
 // next tile's key rows loaded while the current one is multiplied.  B is read
 // straight from the cache rows (8 bytes per lane and dim step).
-constexpr int MF_SK = 512;   // keys per workgroup of k_attn_scores_mf
+constexpr int MF_SK = ATT_MF_SK;   // keys per workgroup of k_attn_scores_mf
 __global__ void __launch_bounds__(256) k_attn_scores_mf(AttnArgs a) {
     const int g = blockIdx.y, tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, q = l >> 4;
     const int nq = a.n_head, R = nq / a.n_head_kv, gqa = a.n_head_kv * AD;
@@ -447,6 +352,9 @@ __global__ void __launch_bounds__(256) k_attn_scores_mf(AttnArgs a) {
         for (int st = 0; st < 8; ++st) kb[st] = ok ? *(const h4*) (krow + 16 * st) : h4{0, 0, 0, 0};
     };
     if (rw0 >= rows) return;
+    // this lane's running max and sum of v_expf(s - max) for its four D rows over its keys
+    float mrow[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    double lrow[4] = {0.0, 0.0, 0.0, 0.0};
     h4 kc[8], kn[8];
     load_b(key0, kc);
     for (int64_t j0 = key0; j0 < kend; j0 += 16) {
@@ -460,11 +368,39 @@ __global__ void __launch_bounds__(256) k_attn_scores_mf(AttnArgs a) {
             const int64_t r = rw0 + 4 * q + i;
             if (r < rows && jb < kend) {
                 const int t = (int) (r / R), h = (int) (r % R);
-                a.s[((int64_t) t * nq + g * R + h) * a.n_kv + jb] = jb > a.n_past + t ? -INFINITY : acc[i] * a.kq_scale;
+                const float sv = jb > a.n_past + t ? -INFINITY : acc[i] * a.kq_scale;
+                a.s[((int64_t) t * nq + g * R + h) * a.n_kv + jb] = sv;
+                if (sv > mrow[i]) {
+                    lrow[i] = (mrow[i] == -INFINITY ? 0.0 : lrow[i] * exp((double) mrow[i] - (double) sv)) + 1.0;
+                    mrow[i] = sv;
+                } else if (sv != -INFINITY) {
+                    lrow[i] += (double) v_expf(sv - mrow[i]);
+                }
             }
         }
 #pragma unroll
         for (int st = 0; st < 8; ++st) kc[st] = kn[st];
+    }
+    // the 16 lanes of a row group hold different keys of the same rows: combine them
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) {
+            const float mo = __shfl_xor(mrow[i], off);
+            const double lo = __shfl_xor(lrow[i], off);
+            const float mn = fmaxf(mrow[i], mo);
+            const double a0 = mrow[i] == -INFINITY ? 0.0 : lrow[i] * exp((double) mrow[i] - (double) mn);
+            const double a1 = mo == -INFINITY ? 0.0 : lo * exp((double) mo - (double) mn);
+            mrow[i] = mn;
+            lrow[i] = a0 + a1;
+        }
+        const int64_t r = rw0 + 4 * q + i;
+        if (li == 0 && r < rows) {
+            const int t = (int) (r / R), h = (int) (r % R);
+            const int64_t sr = (int64_t) blockIdx.x * a.T * nq + (int64_t) t * nq + g * R + h;
+            a.stat[2 * sr] = mrow[i];
+            a.stat[2 * sr + 1] = (float) lrow[i];
+        }
     }
 }
 
@@ -483,7 +419,19 @@ __global__ void __launch_bounds__(256) k_attn_pv_mf(AttnArgs a) {
     const int64_t klim = min((int64_t) a.n_kv, a.n_past + t_last + 1);   // keys past it are masked for every row
     const int64_t ra = row0 + 16 * w + li;                                // this lane's A row
     const bool row_ok = ra < rows;
-    const float* prow = a.s + (row_ok ? ((int64_t) (ra / R) * nq + g * R + ra % R) * a.n_kv : 0);
+    const int64_t rid = row_ok ? (int64_t) (ra / R) * nq + g * R + ra % R : 0;
+    const float* prow = a.s + rid * a.n_kv;
+    // the row's max M and sum S = sum_b exp(m_b - M) l_b over the 512-key blocks, then
+    // p = f16(v_expf(s - M) * (float) (1 / S)): ggml's normalized probabilities
+    const int nkb = (int) ((a.n_kv + MF_SK - 1) / MF_SK);
+    float M = -INFINITY;
+    for (int b = 0; b < nkb; ++b) M = fmaxf(M, row_ok ? a.stat[2 * ((int64_t) b * a.T * nq + rid)] : -INFINITY);
+    double S = 0.0;
+    for (int b = 0; b < nkb && row_ok; ++b) {
+        const float mb = a.stat[2 * ((int64_t) b * a.T * nq + rid)];
+        if (mb != -INFINITY) S += exp((double) mb - (double) M) * (double) a.stat[2 * ((int64_t) b * a.T * nq + rid) + 1];
+    }
+    const float inv = row_ok ? (float) (1.0 / S) : 0.0f;
     f4 acc[8];
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt) acc[nt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -515,7 +463,10 @@ __global__ void __launch_bounds__(256) k_attn_pv_mf(AttnArgs a) {
             const int64_t k4 = c0 + 16 * kt + 4 * q;   // this lane's four keys of the A operand
             float p4[4];
 #pragma unroll
-            for (int m = 0; m < 4; ++m) p4[m] = row_ok && k4 + m < klim ? prow[k4 + m] : 0.0f;
+            for (int m = 0; m < 4; ++m) {
+                const float sv = row_ok && k4 + m < klim ? prow[k4 + m] : -INFINITY;
+                p4[m] = sv == -INFINITY ? 0.0f : v_expf(sv - M) * inv;
+            }
             const h4 pa = f4_to_h4(p4[0], p4[1], p4[2], p4[3]);
 #pragma unroll
             for (int nt = 0; nt < 8; ++nt) {
@@ -618,14 +569,8 @@ int launch_attn_core(const AttnArgs& a, hipStream_t st) {
     }
     hipLaunchKernelGGL(k_attn_scores_mf, dim3((unsigned) ((a.n_kv + MF_SK - 1) / MF_SK), (unsigned) nk,
                                               (unsigned) ((rows + 63) / 64)), dim3(256), 0, st, a);
-    const dim3 sm_grid((unsigned) nq, (unsigned) a.T);
-    const int64_t ng = a.n_kv / 8;   // whole groups of eight per row
-    if (ng <= 256) hipLaunchKernelGGL(k_attn_softmax_r<1>, sm_grid, dim3(256), 0, st, a);
-    else if (ng <= 512) hipLaunchKernelGGL(k_attn_softmax_r<2>, sm_grid, dim3(256), 0, st, a);
-    else if (ng <= 1024) hipLaunchKernelGGL(k_attn_softmax_r<4>, sm_grid, dim3(256), 0, st, a);
-    else if (ng <= 2048) hipLaunchKernelGGL(k_attn_softmax_r<8>, sm_grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL(k_attn_softmax, sm_grid, dim3(256), 0, st, a);
-    // writes att (a.att_q8K is left to the caller)
+    // the softmax is formed inside the P.V kernel from the scores' block statistics;
+    // it writes att (a.att_q8K is left to the caller)
     hipLaunchKernelGGL(k_attn_pv_mf, dim3((unsigned) nk, (unsigned) ((rows + 63) / 64)), dim3(256), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }

@@ -129,6 +129,7 @@ void* scratch_ptr(int device);
 // attn.hip: the attention half of Seg A (per-head norms, NEOX RoPE, f16 KV cache,
 // GQA scores, softmax, P.V), head dimension 128
 constexpr int ATT_RMAX = 16;      // query heads per kv head, at most
+constexpr int ATT_MF_SK = 512;   // keys per block of the matrix-core scores (and of their softmax statistics)
 // Keys per split of the split-softmax path (fewer than 64 query rows): a
 // multiple of 64 that gives the (kv head, token, split) workgroups about 512 in
 // all (64 keys at the 30B decode shape up to 8 k keys of context).
@@ -153,10 +154,17 @@ struct AttnArgs {
     float* s;                     // [T][n_head][n_kv] scores, then probabilities
     int64_t split;                // keys per split (attn_split; fewer than 64 query rows)
     float* part;                  // [ceil(n_kv / split)][T][n_head][128] partial products
-    float* stat;                  // [ceil(n_kv / split)][T][n_head][2]: each split's max and sum
+    float* stat;                  // [blocks][T][n_head][2]: each key split's / 512-key block's max and sum
+                                  // (attn_stat_blocks blocks)
     float* att;                   // [T][n_head * 128]
     void* att_q8K;                // optional: Q8_K rows of att (the split path writes these instead of att)
 };
+// blocks of softmax statistics launch_attn_core writes: one per key split (fewer
+// than 64 query rows) or per 512-key block of the matrix-core scores
+inline int64_t attn_stat_blocks(int64_t T, int64_t n_head_kv, int64_t n_kv) {
+    const int64_t sp = attn_split(T, n_head_kv, n_kv), ns = (n_kv + sp - 1) / sp, nb = (n_kv + ATT_MF_SK - 1) / ATT_MF_SK;
+    return ns > nb ? ns : nb;
+}
 int launch_attn_core(const AttnArgs& a, hipStream_t stream);
 // whether launch_attn_core writes a.att_q8K (and not att) for these arguments
 inline bool attn_writes_q8K(const AttnArgs& a) {
