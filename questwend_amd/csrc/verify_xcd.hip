@@ -119,7 +119,7 @@ __global__ void __launch_bounds__(XT) k_verify_xcd(VerifyArgs a) {
     auto load_router = [&](const float* router, int tid) {
         const int wave = tid >> 6, lane = tid & 63;
         const int hw = 2 * (wave - RW0) + ((lane >> 5) & 1), c = lane & 31;
-        if (wave >= RW0 && hw < NLOG) {
+        if (router && wave >= RW0 && hw < NLOG) {
             const float* src = router + (size_t) (NLOG * j + hw) * H + c;
 #pragma unroll
             for (int s2 = 0; s2 < H / 32; ++s2) rw[s2] = *(const __attribute__((address_space(1))) float*) (src + 32 * s2);
@@ -233,7 +233,7 @@ __global__ void __launch_bounds__(XT) k_verify_xcd(VerifyArgs a) {
 #pragma unroll 1
                 for (int m = 0; m < 2; ++m) {
                     const int i = lane + 64 * m;
-                    const float pi = i < E ? pv[m] : 0.0f;
+                    const float pi = i < E ? (m ? pv[1] : pv[0]) : 0.0f;   // (no dynamic index: it would live in scratch)
                     int gt = 0, eq = 0;
 #pragma unroll 2
                     for (int jj = 0; jj < E; jj += 4) {
@@ -528,7 +528,7 @@ __global__ void __launch_bounds__(XT) k_verify_xcd(VerifyArgs a) {
         }
         const bool next2 = l + 2 < a.n_layer && tid < XLW;
         const uint64_t lw = ldg64((const uint64_t*) (a.layers + (next2 ? l + 2 : l)) + (tid % XLW));
-        if (nxt) load_router(L1.router, tid);
+        load_router(nxt ? L1.router : nullptr, tid);   // (rw defined on both paths: see load_router)
 
         // ---- D -> y[t][h]: wave t, lane h; build_moe's T > 1 sum: products, then an add
         // chain in slot order ------------------------------------------------------------
