@@ -91,10 +91,14 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
     auto load_router = [&](const float* router, int tid) {
         const int wave = tid >> 6, lane = tid & 63;
         const int hw = 2 * (wave - RW0) + ((lane >> 5) & 1), c = lane & 31;
-        if (wave >= RW0 && hw < NLOG) {
+        if (router && wave >= RW0 && hw < NLOG) {
             const float* src = router + (size_t) (NLOG * j + hw) * H + c;
 #pragma unroll
             for (int s2 = 0; s2 < H / 32; ++s2) rw[s2] = *(const __attribute__((address_space(1))) float*) (src + 32 * s2);
+        } else {
+            // (defined on every path, so the registers are not carried around the layer loop)
+#pragma unroll
+            for (int s2 = 0; s2 < H / 32; ++s2) rw[s2] = 0.0f;
         }
     };
     auto next_x = [&](int tid, float sc, uint32_t ep_next) {
@@ -473,7 +477,7 @@ __global__ void __launch_bounds__(XT) k_decode_xcd(XcdArgs a) {
         }
         // next layer's router weights, into the router lanes' registers (the gate/up
         // and down rows are consumed; they arrive while y is exchanged and normed)
-        if (nxt) load_router(L1.router, tid);
+        load_router(nxt ? L1.router : nullptr, tid);
 
         // ---- D -> y[h]: wave 0, lane h; the k expert XCDs' down outputs of row h --------
         if (wave == 0) {
