@@ -125,6 +125,32 @@ qw::MmidArgs mmid_args(int type, const void* as, int64_t K, int64_t N, int64_t n
     return m;
 }
 
+// The exact Q4_K matrix-core form on the f16 matrix cores: an f16 copy of the
+// n_rows activation rows in act_q, in the call's workspace.  Without room for it
+// the int8 form runs (the same bits).
+// QWMOE_MFMA_F16=0 in the environment keeps the int8 form (a test switch).
+int mfma_f16_prep(Arena& ar, qw::MmidArgs& m, int64_t n_rows, hipStream_t st) {
+    if (!qw::mmid_mfma_h_ok(m, n_rows)) return 0;
+    const char* env = getenv("QWMOE_MFMA_F16");
+    if (env && env[0] == '0') return 0;
+    uint16_t* h = ar.take<uint16_t>((size_t) (n_rows * m.K));
+    if (!h) return 0;
+    if (int rc = qw::launch_q8K_to_f16(m.act_q, m.act_row_bytes, m.K, n_rows, h, st)) return rc == -2 ? 0 : rc;
+    m.act_h = h;
+    return 0;
+}
+
+// Gate and up reading one activation buffer share its f16 copy.
+int mfma_f16_prep_pair(Arena& ar, qw::MmidArgs& mu, qw::MmidArgs& mg, int64_t n_rows, hipStream_t st) {
+    if (int rc = mfma_f16_prep(ar, mu, n_rows, st)) return rc;
+    if (mg.act_q == mu.act_q && mg.act_row_bytes == mu.act_row_bytes && mg.K == mu.K &&
+        qw::mmid_mfma_h_ok(mg, n_rows)) {
+        mg.act_h = mu.act_h;
+        return 0;
+    }
+    return mfma_f16_prep(ar, mg, n_rows, st);
+}
+
 int mmid_launch(const qw::MmidArgs& m, hipStream_t st) {
     // with mfma_min_rows == 1 the matrix cores take every bin that holds a row:
     // the GEMV's workgroups would only return
@@ -145,17 +171,6 @@ int mmid_launch_pair(const qw::MmidArgs& mu, const qw::MmidArgs& mg, hipStream_t
     }
     const int rc = mmid_launch(mu, st);
     return rc ? rc : mmid_launch(mg, st);
-}
-
-// Shared implementation of mul_mat_id once b is quantized and ids are grouped.
-int mmid_grouped(hipStream_t st, int type, const void* as, int64_t K, int64_t N, int64_t n_as, size_t nb01,
-                 size_t nb02, const uint8_t* bq, int64_t ne11, size_t bq_row, const int32_t* rows,
-                 const int32_t* active, const int32_t* active_off, const int32_t* n_active, int64_t max_active,
-                 const int32_t* slot_of, int64_t n_slot_of, float* dst, size_t nb1, size_t nb2, int64_t max_rows,
-                 int64_t n_pairs) {
-    return mmid_launch(mmid_args(type, as, K, N, n_as, nb01, nb02, bq, ne11, bq_row, rows, active, active_off, n_active,
-                                 max_active, slot_of, n_slot_of, dst, nb1, nb2, max_rows, n_pairs),
-                       st);
 }
 
 struct Grouping {
@@ -384,8 +399,10 @@ int mul_mat_id_in(Arena& ar, int err_space, void* stream, int type, const void* 
     rc = qwmoe_quantize_act(stream, vdt, b, ne00, ne11, ne12, nb11, nb12, bq);
     if (rc) return rc;
     if (qw::launch_group(ga, st) != 0) return QWMOE_ERR_HIP;
-    return mmid_grouped(st, type, as, ne00, ne01, ne02, nb01, nb02, bq, ne11, qrow, G.rows, G.active, G.active_off,
-                        G.n_active, G.max_active, slot_of, n_slot_of, dst, nb1, nb2, n_ids * ne12, n_ids * ne12);
+    qw::MmidArgs m = mmid_args(type, as, ne00, ne01, ne02, nb01, nb02, bq, ne11, qrow, G.rows, G.active, G.active_off,
+                               G.n_active, G.max_active, slot_of, n_slot_of, dst, nb1, nb2, n_ids * ne12, n_ids * ne12);
+    if ((rc = mfma_f16_prep(ar, m, ne11 * ne12, st))) return rc;
+    return mmid_launch(m, st);
 }
 
 }  // namespace
@@ -514,10 +531,11 @@ int qwmoe_shared_expert_add(void* stream, const qwmoe_shared_expert* se, int64_t
     if ((rc = qw::launch_quantize_act(vg, x, H, 1, T, (size_t) H * 4, (size_t) H * 4, xg, st))) return rc;
     if (xu != xg && (rc = qw::launch_quantize_act(vu, x, H, 1, T, (size_t) H * 4, (size_t) H * 4, xu, st))) return rc;
     const size_t fb = (size_t) F * 4;
-    const qw::MmidArgs mu = mmid_args(se->type_up, se->up, H, F, 1, se->up_nb1, se->up_nb1 * (size_t) F, xu, 1, qu,
-                                      rows, active, active_off, n_active, 1, nullptr, 0, upo, fb, fb, T, T);
-    const qw::MmidArgs mg = mmid_args(se->type_gate, se->gate, H, F, 1, se->gate_nb1, se->gate_nb1 * (size_t) F, xg, 1,
-                                      qg, rows, active, active_off, n_active, 1, nullptr, 0, gateo, fb, fb, T, T);
+    qw::MmidArgs mu = mmid_args(se->type_up, se->up, H, F, 1, se->up_nb1, se->up_nb1 * (size_t) F, xu, 1, qu, rows,
+                                active, active_off, n_active, 1, nullptr, 0, upo, fb, fb, T, T);
+    qw::MmidArgs mg = mmid_args(se->type_gate, se->gate, H, F, 1, se->gate_nb1, se->gate_nb1 * (size_t) F, xg, 1, qg,
+                                rows, active, active_off, n_active, 1, nullptr, 0, gateo, fb, fb, T, T);
+    if ((rc = mfma_f16_prep_pair(ar, mu, mg, T, st))) return rc;
     if ((rc = mmid_launch_pair(mu, mg, st))) return rc;
     // ggml_mul(ggml_silu(g), u) rounds as swiglu_split does: silu, then one multiply
     qw::MmidArgs md = mmid_args(se->type_down, se->down, F, H, 1, se->down_nb1, se->down_nb1 * (size_t) H, aq, 1, qd,
@@ -534,6 +552,7 @@ int qwmoe_shared_expert_add(void* stream, const qwmoe_shared_expert* se, int64_t
         if ((rc = qw::launch_swiglu(gateo, upo, act, T, F, fb, fb, fb, st))) return rc;
         if ((rc = qw::launch_quantize_act(vd, act, F, 1, T, fb, fb, aq, st))) return rc;
     }
+    if (!md.swiglu_gate && (rc = mfma_f16_prep(ar, md, T, st))) return rc;
     if ((rc = mmid_launch(md, st))) return rc;
     return qw::launch_shared_gate_add(x, (size_t) H, se->gate_inp, sh, moe_out, resid, out, (size_t) H, H, T, st);
 }
@@ -758,12 +777,13 @@ int qwmoe_ffn_layer(void* stream, const qwmoe_layer* L, const float* x, int64_t 
     if (!xq_fused && (rc = qw::launch_quantize_act(vg, x, H, 1, T, (size_t) H * 4, (size_t) H * 4, xg, st))) return rc;
     if (xu != xg && (rc = qw::launch_quantize_act(vu, x, H, 1, T, (size_t) H * 4, (size_t) H * 4, xu, st))) return rc;
     const size_t dnb1 = (size_t) F * 4, dnb2 = (size_t) F * 4 * (size_t) k;
-    const qw::MmidArgs mu = mmid_args(L->type_up, L->up, H, F, L->n_slots_up, L->up_nb1, L->up_nb2, xu, 1, qu, G.rows,
+    qw::MmidArgs mu = mmid_args(L->type_up, L->up, H, F, L->n_slots_up, L->up_nb1, L->up_nb2, xu, 1, qu, G.rows,
                                       G.active, G.active_off, G.n_active, G.max_active, L->slot_up,
                                       L->slot_up ? E : 0, upo, dnb1, dnb2, T, k * T);
-    const qw::MmidArgs mg = mmid_args(L->type_gate, L->gate, H, F, L->n_slots_gate, L->gate_nb1, L->gate_nb2, xg, 1, qg,
+    qw::MmidArgs mg = mmid_args(L->type_gate, L->gate, H, F, L->n_slots_gate, L->gate_nb1, L->gate_nb2, xg, 1, qg,
                                       G.rows, G.active, G.active_off, G.n_active, G.max_active, L->slot_gate,
                                       L->slot_gate ? E : 0, gateo, dnb1, dnb2, T, k * T);
+    if ((rc = mfma_f16_prep_pair(ar, mu, mg, T, st))) return rc;
     if ((rc = mmid_launch_pair(mu, mg, st))) return rc;   // gate and up in one launch each
     const int vd = qw::vec_dot_type(L->type_down);
     const size_t qd = qwmoe_row_size(vd, F);
@@ -786,6 +806,7 @@ int qwmoe_ffn_layer(void* stream, const qwmoe_layer* L, const float* x, int64_t 
         if ((rc = qw::launch_quantize_act(vd, act, F, k, k * T, (size_t) F * 4, (size_t) F * 4 * (size_t) k, aq, st)))
             return rc;
     }
+    if (!md.swiglu_gate && (rc = mfma_f16_prep(ar, md, k * T, st))) return rc;
     if ((rc = mmid_launch(md, st))) return rc;
     if (rms_eps >= 0.0f && H <= 16384) {
         if ((rc = qw::launch_weighted_sum_rms(ex, w, out, x_next, H, k, T, rms_eps, st))) return rc;

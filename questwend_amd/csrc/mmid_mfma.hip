@@ -453,6 +453,270 @@ k_mmid_mfma_q4k(MfLaunch lp) {
 // weight row's operand is formed once for all of them and the tile is streamed
 // a quarter as often.
 
+// ---- exact Q4_K on the f16 matrix cores ------------------------------------
+// The integers of the int8 exact form above, from v_mfma_f32_16x16x32_f16.  For
+// AVX lane L, A lane (weight row, gq) holds sc * q4 of elements
+// 64 gq + 4 L + {0, 2, 1, 3} (sub-block 2 gq, low nibbles of qs dword 8 gq + L)
+// and 64 gq + 32 + 4 L + {0, 2, 1, 3} (sub-block 2 gq + 1, its high nibbles) as
+// f16 (at most 63 * 15 = 945: exact); B lane (activation row, gq) holds the q8 of
+// the same elements, one 16-byte chunk (gq, L) of an f16 copy of the Q8_K rows
+// laid out that way (k_q8K_to_h).  Every product and partial sum is an integer
+// below 2^24, so the f32 D is sumi_L exactly: one MFMA per AVX lane and tile in
+// place of two int8 ones, and the float chain takes D as it is (no shift-add, no
+// convert).  Min lane m: two MFMAs over chunks (m, 0..3) and (m, 4..7), A = the
+// mins of sub-blocks 2m (slots 0-3) and 2m + 1 (slots 4-7).
+//
+// A from a qs dword w: (w & 0x000F000F) | 0x64006400 is the f16 pair
+// (1024 + q4 of byte 0, 1024 + q4 of byte 2); an fma with (sc, sc) and -1024 sc
+// leaves sc * q4 (one rounding of an exact integer below 2048).  High nibbles
+// stay in place: 1024 + 16 q4, times sc / 16, minus 64 sc.
+//
+// Staging as in the int8 form, three super-blocks deep; the activation rows come
+// from the f16 copy (512 bytes per row and super-block), chunk c of row n stored
+// at chunk c ^ (n & 15) (16 rows read at one offset hit distinct banks), their d
+// from the Q8_K rows.  ~52 KB of LDS: three workgroups per CU.
+typedef _Float16 h8m __attribute__((ext_vector_type(8)));
+typedef _Float16 h2m __attribute__((ext_vector_type(2)));
+typedef float f4m __attribute__((ext_vector_type(4)));
+constexpr int MH_NB = 1;   // 16-row activation tiles per pass of the f16 form (two measured slower, 78 KB
+                           // of LDS and two workgroups per CU, and failed the bit-exact test: not used)
+
+__device__ __forceinline__ h2m h2_bits(uint32_t x) { return __builtin_bit_cast(h2m, x); }
+__device__ __forceinline__ uint32_t h2_u32(h2m x) { return __builtin_bit_cast(uint32_t, x); }
+
+template <int NB>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) k_mmid_mfma_q4k_h(MfLaunch lp) {
+    static_assert(NB == 1, "one 16-row activation tile per pass (the form that is tested)");
+    const uint32_t zm = blockIdx.x >= lp.groups ? 1u : 0u;   // uniform: which matrix
+    const MmidArgs& m = lp.m[zm];
+    const uint32_t bid = blockIdx.x - zm * lp.groups;
+    constexpr int NR = 16 * NB;               // activation rows per pass (and per item)
+    constexpr int AHI = NR / 2;               // f16 activation DMA instructions per stage (two rows each)
+    constexpr int AHW = (AHI + 3) / 4;        // ... per wave, at most
+    static_assert(AHI % 4 == 0, "activation copies spread evenly over the waves");
+    // fewest DMA instructions any wave issues per stage: 2 or 3 of the 9 weight
+    // ones, AHI / 4 activation ones, the d's (wave 3)
+    constexpr int VM_STAGE = 2 + AHI / 4;
+    __shared__ __align__(16) uint8_t s_w0[MF_M * MF_WS];
+    __shared__ __align__(16) uint8_t s_w1[MF_M * MF_WS];
+    __shared__ __align__(16) uint8_t s_w2[MF_M * MF_WS];
+    __shared__ __align__(16) uint8_t s_h0[NR * 512];
+    __shared__ __align__(16) uint8_t s_h1[NR * 512];
+    __shared__ __align__(16) uint8_t s_h2[NR * 512];
+    __shared__ __align__(16) float s_d0[64], s_d1[64], s_d2[64];   // NR d's (a DMA instruction's 64 slots)
+    __shared__ int32_t s_arow[NR];
+    __shared__ int32_t s_et[NR][2];
+    __shared__ int s_item[2];
+    const int tiles = (int) (m.N / MF_M);
+    const int tile = (int) (bid % (uint32_t) tiles);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    mf_item(m, (int) (bid / (uint32_t) tiles), NR, wave, lane, s_item);
+    const int g = s_item[0];
+    if (g < 0) return;   // past the last item
+    const int p0 = m.active_off[g] + NR * s_item[1], p1 = min(m.active_off[g + 1], p0 + NR);
+    const int bin = m.active[g];
+    int64_t mat = bin;
+    if (m.slot_of) mat = (bin < m.n_slot_of) ? m.slot_of[bin] : -1;
+    if (mat < 0 || mat >= m.n_as) {
+        if (threadIdx.x == 0 && m.status) atomicOr(m.status, 4);
+        return;
+    }
+    const int64_t r0 = (int64_t) tile * MF_M;
+    const int lr = lane & 15, gq = lane >> 4;
+    const int nb = (int) (m.K / QK_K);
+    const uint8_t* wtile = m.w + (size_t) mat * m.nb2 + (size_t) r0 * m.nb1;
+    const i32x4 wrsrc = rsrc_words(wtile, (uint32_t) (MF_M * m.nb1));
+    const i32x4 hrsrc = rsrc_words(m.act_h, 0x7fffffffu);
+    const i32x4 arsrc = rsrc_words(m.act_q, 0x7fffffffu);
+    const int arow_l = 16 * wave + lr;
+    const int ntok = p1 - p0;
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    if (tid < NR) {
+        const int pp = p0 + (tid < ntok ? tid : 0);   // rows past ntok are staged from row 0, never written
+        const int e = m.rows[2 * pp], t = m.rows[2 * pp + 1];
+        s_et[tid][0] = e;
+        s_et[tid][1] = t;
+        s_arow[tid] = (int) ((int64_t) (e % m.b_ne1) + (int64_t) t * m.b_ne1);
+    }
+    lds_barrier();
+    uint32_t woff[3], hoff[AHW], doff = 0;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const int q = 64 * (wave + 4 * k) + lane;
+        const int qc = q < MF_M * 9 ? q : 0;
+        woff[k] = (uint32_t) (qc / 9) * (uint32_t) m.nb1 + 16u * (uint32_t) (qc % 9);
+    }
+#pragma unroll
+    for (int k = 0; k < AHW; ++k) {
+        const int ii = wave + 4 * k;                      // instruction: rows 2 ii, 2 ii + 1
+        const int n = ii < AHI ? 2 * ii + (lane >> 5) : 0, c = lane & 31;
+        hoff[k] = (uint32_t) s_arow[n] * (uint32_t) (2 * m.K) + 16u * (uint32_t) (c ^ (n & 15));
+    }
+    if (lane < NR) doff = (uint32_t) s_arow[lane] * (uint32_t) m.act_row_bytes;
+    auto issue = [&](uint8_t* sw, uint8_t* sh, float* sd, int i) __attribute__((always_inline)) {
+        uint32_t lw = (uint32_t) (uintptr_t) sw, lh = (uint32_t) (uintptr_t) sh, ld = (uint32_t) (uintptr_t) sd;
+        asm volatile("" : "+s"(lw), "+s"(lh), "+s"(ld));
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+            if (wv + 4 * k < 9) dma_b128(wrsrc, lw + 1024u * (uint32_t) (wv + 4 * k), woff[k], 144u * (uint32_t) i);
+#pragma unroll
+        for (int k = 0; k < AHW; ++k)
+            if (wv + 4 * k < AHI) dma_b128(hrsrc, lh + 1024u * (uint32_t) (wv + 4 * k), hoff[k], 512u * (uint32_t) i);
+        if (wv == 3 && lane < NR) dma_b32(arsrc, ld, doff, 292u * (uint32_t) i);
+    };
+
+    float acc[NB][4][8], accm[NB][4][4];
+#pragma unroll
+    for (int t = 0; t < NB; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+#pragma unroll
+            for (int L = 0; L < 8; ++L) acc[t][r][L] = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) accm[t][r][q] = 0.0f;
+        }
+    const int nbt = (ntok + 15) / 16;   // activation tiles holding rows (uniform)
+
+    // 0x64006400 as a register operand, so that (w & mask) | it is one v_and_or_b32
+    uint32_t hmag = 0x64006400u;
+    asm volatile("" : "+v"(hmag));
+    auto compute = [&](const uint8_t* sw, const uint8_t* sh, const float* sd) __attribute__((always_inline)) {
+        // this lane's A row: the 6-bit scales and mins of the 8 sub-blocks (quants.c:2067-2072)
+        const u32x4m hdr = *(const u32x4m*) (sw + arow_l * MF_WS);
+        const uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;
+        const uint32_t sc_lo = s0 & 0x3f3f3f3fu;
+        const uint32_t sc_hi = (s2 & 0x0f0f0f0fu) | (((s0 >> 6) & 0x03030303u) << 4);
+        const uint32_t mn_lo = s1 & 0x3f3f3f3fu;
+        const uint32_t mn_hi = ((s2 >> 4) & 0x0f0f0f0fu) | (((s1 >> 6) & 0x03030303u) << 4);
+        // sub-blocks 2 gq (low nibbles) and 2 gq + 1 (high nibbles) of this lane's k-slots
+        const uint32_t scw = gq < 2 ? sc_lo : sc_hi;
+        const uint32_t sab = (scw >> (16 * (gq & 1))) & 0xffffu;        // sc_a | sc_b << 8
+        // (sc_a, sc_a), (sc_b / 16, sc_b / 16) and the offsets as f16 pairs
+        const h2m pa = h2_bits(__builtin_amdgcn_perm(0u, sab, 0x0c000c00u) | 0x64006400u) - h2m{1024, 1024};
+        const h2m pb = h2_bits(__builtin_amdgcn_perm(0u, sab, 0x0c010c01u) | 0x64006400u) - h2m{1024, 1024};
+        const h2m S_lo = pa, C_lo = pa * h2m{-1024, -1024};
+        const h2m S_hi = pb * h2m{0.0625, 0.0625}, C_hi = pb * h2m{-64, -64};
+        float xd[4], xdm[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t h0 = *(const uint32_t*) (sw + (16 * wave + 4 * gq + r) * MF_WS);
+            xd[r] = h2f((uint16_t) (h0 & 0xffff));
+            xdm[r] = h2f((uint16_t) (h0 >> 16));
+        }
+        float d[NB][4], dmin[NB][4];
+#pragma unroll
+        for (int t = 0; t < NB; ++t) {
+            const float dy = sd[16 * t + lr];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                d[t][r] = dy * xd[r];
+                dmin[t][r] = -dy * xdm[r];
+            }
+        }
+#pragma unroll
+        for (int L = 0; L < 8; ++L) {
+            const uint32_t w = *(const uint32_t*) (sw + arow_l * MF_WS + 16 + 32 * gq + 4 * L);
+            const uint32_t v = w >> 8;
+            const h2m a0 = __builtin_elementwise_fma(h2_bits((w & 0x000F000Fu) | hmag), S_lo, C_lo);
+            const h2m a1 = __builtin_elementwise_fma(h2_bits((v & 0x000F000Fu) | hmag), S_lo, C_lo);
+            const h2m a2 = __builtin_elementwise_fma(h2_bits((w & 0x00F000F0u) | hmag), S_hi, C_hi);
+            const h2m a3 = __builtin_elementwise_fma(h2_bits((v & 0x00F000F0u) | hmag), S_hi, C_hi);
+            const h8m A = __builtin_bit_cast(h8m, u32x4m{h2_u32(a0), h2_u32(a1), h2_u32(a2), h2_u32(a3)});
+#pragma unroll
+            for (int t = 0; t < NB; ++t) {
+                if (t >= nbt) break;
+                const int n = 16 * t + lr;
+                const h8m B = *(const h8m*) (sh + n * 512 + 16 * ((8 * gq + L) ^ (n & 15)));
+                const f4m D = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, f4m{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[t][r][L] = __builtin_fmaf(d[t][r], D[r], acc[t][r][L]);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            // (m_2q, m_2q) and (m_2q+1, m_2q+1) as f16 pairs
+            const uint32_t mnw = q < 2 ? mn_lo : mn_hi;
+            const uint32_t b0 = (uint32_t) (2 * (q & 1)), b1 = b0 + 1;
+            const h2m m0 = h2_bits(__builtin_amdgcn_perm(0u, mnw, 0x0c000c00u | b0 | (b0 << 16)) | 0x64006400u) -
+                           h2m{1024, 1024};
+            const h2m m1 = h2_bits(__builtin_amdgcn_perm(0u, mnw, 0x0c000c00u | b1 | (b1 << 16)) | 0x64006400u) -
+                           h2m{1024, 1024};
+            const h8m Am = __builtin_bit_cast(h8m, u32x4m{h2_u32(m0), h2_u32(m0), h2_u32(m1), h2_u32(m1)});
+#pragma unroll
+            for (int t = 0; t < NB; ++t) {
+                if (t >= nbt) break;
+                const int n = 16 * t + lr;
+                const h8m B0 = *(const h8m*) (sh + n * 512 + 16 * ((8 * q + gq) ^ (n & 15)));
+                const h8m B1 = *(const h8m*) (sh + n * 512 + 16 * ((8 * q + 4 + gq) ^ (n & 15)));
+                f4m Dm = __builtin_amdgcn_mfma_f32_16x16x32_f16(Am, B0, f4m{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                Dm = __builtin_amdgcn_mfma_f32_16x16x32_f16(Am, B1, Dm, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) accm[t][r][q] = __builtin_fmaf(dmin[t][r], Dm[r], accm[t][r][q]);
+            }
+        }
+    };
+    auto stage = [&](int i, const uint8_t* cw, const uint8_t* ch, const float* cd, uint8_t* nw, uint8_t* nh,
+                     float* nd) __attribute__((always_inline)) {
+        if (i + 1 < nb) vm_wait<VM_STAGE>();   // super-block i + 1's loads may stay in flight
+        else vm_wait<0>();
+        lds_barrier();
+        if (i + 2 < nb) issue(nw, nh, nd, i + 2);
+        compute(cw, ch, cd);
+    };
+    issue(s_w0, s_h0, s_d0, 0);
+    if (nb > 1) issue(s_w1, s_h1, s_d1, 1);
+    for (int i = 0; i < nb; i += 3) {
+        stage(i, s_w0, s_h0, s_d0, s_w2, s_h2, s_d2);
+        if (i + 1 < nb) stage(i + 1, s_w1, s_h1, s_d1, s_w0, s_h0, s_d0);
+        if (i + 2 < nb) stage(i + 2, s_w2, s_h2, s_d2, s_w1, s_h1, s_d1);
+    }
+    // hsum_float_8(acc) + ((m0 + m2) + (m1 + m3)); rows r0 + 16 wave + 4 gq .. +3 of B row 16 t + lr
+#pragma unroll
+    for (int t = 0; t < NB; ++t) {
+        float o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float* a = acc[t][r];
+            const float hs = ((a[4] + a[0]) + (a[6] + a[2])) + ((a[5] + a[1]) + (a[7] + a[3]));
+            const float* mm = accm[t][r];
+            o[r] = hs + ((mm[0] + mm[2]) + (mm[1] + mm[3]));
+        }
+        const int row = 16 * t + lr;
+        if (row < ntok) {
+            const int e = s_et[row][0], tt = s_et[row][1];
+            float* dp = (float*) ((char*) m.dst + (size_t) e * m.dst_nb1 + (size_t) tt * m.dst_nb2) + r0 +
+                        16 * wave + 4 * gq;
+            *(float4*) dp = float4{o[0], o[1], o[2], o[3]};
+        }
+    }
+}
+
+// The f16 copy k_mmid_mfma_q4k_h reads: per activation row (K values at out + r K)
+// and super-block, 32 chunks of 16 bytes; chunk 8 g + L holds the q8 of elements
+// 64 g + 4 L + {0, 2, 1, 3} and 64 g + 32 + 4 L + {0, 2, 1, 3} (the A operands'
+// order of qs dword 8 g + L's low and high nibbles).  A thread writes one chunk.
+__global__ void k_q8K_to_h(const uint8_t* __restrict__ q, size_t row_bytes, int64_t K, int64_t rows,
+                           _Float16* __restrict__ out) {
+    const int64_t per_row = K / 8;
+    const int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows * per_row) return;
+    const int64_t r = i / per_row, ci = i - r * per_row, bb = ci / 32;
+    const int c = (int) (ci % 32), g = c >> 3, L = c & 7;
+    const uint8_t* src = q + (size_t) r * row_bytes + 292 * (size_t) bb + 4 + 64 * g + 4 * L;
+    const uint32_t u0 = *(const uint32_t*) src, u1 = *(const uint32_t*) (src + 32);
+    auto b = [](uint32_t u, int k) { return (_Float16) (float) (int8_t) (u >> (8 * k)); };
+    *(h8m*) (out + (size_t) r * K + 8 * ci) = h8m{b(u0, 0), b(u0, 2), b(u0, 1), b(u0, 3), b(u1, 0), b(u1, 2), b(u1, 1), b(u1, 3)};
+}
+
+int launch_q8K_to_f16(const uint8_t* q, size_t row_bytes, int64_t K, int64_t rows, uint16_t* out, hipStream_t stream) {
+    if (K % QK_K != 0 || rows <= 0 || row_bytes % 4 != 0 || ((uintptr_t) q & 3) || ((uintptr_t) out & 15)) return -2;
+    const int64_t n = rows * (K / 8);
+    hipLaunchKernelGGL(k_q8K_to_h, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, stream, q, row_bytes, K, rows,
+                       (_Float16*) out);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+
 // Q6_K x Q8_K on the matrix cores, block-sum form only: the down projections of
 // the layer entry points under QWMOE_MFMA_AUTO, every projection under
 // QWMOE_MFMA_BLOCK_SUM.  (Replaying ggml's eight float lanes for Q6_K is not
@@ -933,6 +1197,13 @@ bool mmid_mfma_supported(const MmidArgs& m) {
            ((uintptr_t) m.dst & 15) == 0 && m.act_row_bytes % 4 == 0 && ((uintptr_t) m.act_q & 3) == 0;
 }
 
+// Whether the exact Q4_K form can run on the f16 matrix cores (act_h set from
+// launch_q8K_to_f16 over all n_rows activation rows).
+bool mmid_mfma_h_ok(const MmidArgs& m, int64_t n_rows) {
+    return m.type == T_Q4_K && m.mfma_exact && m.mfma_min_rows > 0 && mmid_mfma_supported(m) && n_rows > 0 &&
+           (uint64_t) n_rows * (uint64_t) m.K * 2u + 512u < (1ull << 31);
+}
+
 static int launch_mf(const MfLaunch& lp, int nz, hipStream_t stream) {
     const MmidArgs& m = lp.m[0];
     if (lp.groups == 0) return 0;
@@ -940,6 +1211,7 @@ static int launch_mf(const MfLaunch& lp, int nz, hipStream_t stream) {
     const bool q6x = m.type == T_Q6_K && m.mfma_exact, q6b = m.type == T_Q6_K && !m.mfma_exact;
     if (q6b) hipLaunchKernelGGL(k_mmid_mfma_q6k, dim3(grid), dim3(256), 0, stream, lp);
     else if (q6x) hipLaunchKernelGGL((k_mmid_mfma_q6k_x<MX_NB>), dim3(grid), dim3(256), 0, stream, lp);
+    else if (m.mfma_exact && m.act_h) hipLaunchKernelGGL((k_mmid_mfma_q4k_h<MH_NB>), dim3(grid), dim3(256), 0, stream, lp);
     else if (m.mfma_exact) hipLaunchKernelGGL((k_mmid_mfma_q4k<MF_NB_X, true>), dim3(grid), dim3(256), 0, stream, lp);
     else hipLaunchKernelGGL((k_mmid_mfma_q4k<MF_NB_B, false>), dim3(grid), dim3(256), 0, stream, lp);
     return hipGetLastError() == hipSuccess ? 0 : -3;
@@ -948,7 +1220,8 @@ static int launch_mf(const MfLaunch& lp, int nz, hipStream_t stream) {
 // Workgroups of one matrix: (work item, row tile) pairs.
 static int64_t mf_groups(const MmidArgs& m) {
     const bool q6b = m.type == T_Q6_K && !m.mfma_exact;
-    const int rows = q6b ? M6_N : 16 * (m.type == T_Q6_K ? MX_NB : m.mfma_exact ? MF_NB_X : MF_NB_B);
+    const int rows = q6b ? M6_N
+                         : 16 * (m.type == T_Q6_K ? MX_NB : !m.mfma_exact ? MF_NB_B : m.act_h ? MH_NB : MF_NB_X);
     return mf_max_items(m, rows) * (q6b ? (m.N + M6_M - 1) / M6_M : m.N / MF_M);
 }
 
@@ -964,7 +1237,7 @@ int launch_mmid_mfma(const MmidArgs& m, hipStream_t stream) {
 
 int launch_mmid_mfma2(const MmidArgs& a, const MmidArgs& b, hipStream_t stream) {
     if (!mmid_mfma_supported(a) || !mmid_mfma_supported(b) || a.type != b.type || a.mfma_exact != b.mfma_exact ||
-        a.K != b.K || a.N != b.N)
+        a.K != b.K || a.N != b.N || !a.act_h != !b.act_h)
         return -2;
     const int64_t groups = mf_groups(a);
     if (groups != mf_groups(b) || groups > (int64_t(1) << 29)) return -2;

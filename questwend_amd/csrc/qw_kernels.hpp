@@ -87,6 +87,9 @@ struct MmidArgs {
     // the GEMV instead of read from act_q; see mmid_gemv_swiglu_ok
     const float* swiglu_gate;
     const float* swiglu_up;
+    // optional (exact Q4_K matrix-core form): the f16 copy of act_q's quants made by
+    // launch_q8K_to_f16; with it the exact form runs on the f16 matrix cores (the same bits)
+    const uint16_t* act_h;
 };
 int launch_mmid_gemv(const MmidArgs& m, hipStream_t stream);
 // whether launch_mmid_gemv forms the activations itself for these arguments with
@@ -100,6 +103,12 @@ int launch_mmid_mfma(const MmidArgs& m, hipStream_t stream);
 // the matrix-core parts of two mul_mat_ids of the same type, form, shape and
 // grouping (gate and up) in one launch
 int launch_mmid_mfma2(const MmidArgs& a, const MmidArgs& b, hipStream_t stream);
+// f16 copy of n_rows Q8_K activation rows (row_bytes apart, K values each) for
+// the exact Q4_K form on the f16 matrix cores: row r at out + r * K, every group
+// of four quants in the order 0, 2, 1, 3
+int launch_q8K_to_f16(const uint8_t* q, size_t row_bytes, int64_t K, int64_t n_rows, uint16_t* out, hipStream_t stream);
+// whether m (with act_q holding n_rows rows) can take such a copy as act_h
+bool mmid_mfma_h_ok(const MmidArgs& m, int64_t n_rows);
 
 // ffn.hip
 int launch_swiglu(const float* gate, const float* up, float* out, int64_t n_rows, int64_t n, size_t g_stride,

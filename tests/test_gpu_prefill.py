@@ -161,6 +161,46 @@ def test_mfma_integer_core_bit_exact(orc, K, N, ne11, min_rows, exact):
     assert ops.device_status(clear=True) == 0
 
 
+def full_range_q4k(rng, rows: int, K: int) -> np.ndarray:
+    """Q4_K rows of random bytes (every 6-bit scale and min, every nibble) with
+    positive fp16 d and dmin; row 0 at the maxima (scales, mins and nibbles 15)."""
+    nb = K // 256
+    blk = rng.integers(0, 256, (rows, nb, 144)).astype(np.uint8)
+    blk[..., 0:2] = np.float16(rng.uniform(2.0 ** -10, 2.0 ** -6, (rows, nb))).view(np.uint8).reshape(rows, nb, 2)
+    blk[..., 2:4] = np.float16(rng.uniform(2.0 ** -12, 2.0 ** -8, (rows, nb))).view(np.uint8).reshape(rows, nb, 2)
+    blk[0, :, 4:] = 0xFF
+    return blk.reshape(-1)
+
+
+@pytest.mark.parametrize("kernel", ["f16", "int8"])
+@pytest.mark.parametrize("K,N,ne11,min_rows", [(2048, 128, 1, 1), (768, 256, 2, 8), (4096, 64, 1, 16)])
+def test_mfma_exact_full_range_bit_exact(orc, K, N, ne11, min_rows, kernel, monkeypatch):
+    """The exact Q4_K form on either matrix-core kernel -- the f16 one (one
+    v_mfma_f32_16x16x32_f16 per AVX lane on sc * q4 and an f16 copy of the Q8_K
+    quants) or, with QWMOE_MFMA_F16=0, the int8 one -- over blocks of random bytes
+    and activations whose Q8_K rows reach -128 and 127: bit-identical to ggml's
+    AVX2 order (the oracle).  Items of 16 rows with a partial last one (70 tokens
+    on expert 0)."""
+    note(f"exact Q4_K matrix cores, full-range blocks: kernel={kernel} K={K} N={N} ne11={ne11} min_rows={min_rows}")
+    monkeypatch.setenv("QWMOE_MFMA_F16", "1" if kernel == "f16" else "0")
+    rng = np.random.default_rng(3 * K + N)
+    n_as, T = 5, 70
+    w = full_range_q4k(rng, n_as * N, K)
+    b = (rng.standard_normal((T, ne11, K)) * 2.0).astype(np.float32)
+    b[:, :, 7::256] = 40.0                                   # the block maximum: q8 -128 there
+    b[0, :, :] = np.where(np.arange(K) % 2 == 0, 1.0, -1.0)  # every q8 -128 or 127
+    ids = np.stack([[0, 1 + (t % 4)] for t in range(T)]).astype(np.int32)
+    want = orc.mul_mat_id(Q4_K, K, N, n_as, w, b, ids)
+    prev, prev_f = ops.set_mfma_min_rows(min_rows), ops.set_mfma_form(EXACT)
+    try:
+        got = host(ops.mul_mat_id(Q4_K, dev(w), K, N, n_as, dev(b), dev(ids)))
+    finally:
+        ops.set_mfma_min_rows(prev)
+        ops.set_mfma_form(prev_f)
+    assert np.array_equal(bits(got), bits(want))
+    assert ops.device_status(clear=True) == 0
+
+
 @pytest.mark.parametrize("K,N,T,k,n_as,ne11", [(2048, 768, 256, 8, 32, 1), (768, 2048, 128, 8, 16, 8),
                                               (2048, 512, 97, 4, 8, 1)])
 def test_mfma_random(orc, K, N, T, k, n_as, ne11):
