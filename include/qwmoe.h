@@ -70,10 +70,12 @@ int qwmoe_init(int device, size_t workspace_bytes);
 int qwmoe_shutdown(void);
 const char * qwmoe_strerror(int status);
 /* Experts that receive at least `rows` rows in one mul_mat_id (prefill and
- * large verify batches) are computed on the int8 matrix cores
- * (v_mfma_i32_16x16x32_i8 / 16x16x64_i8) when the weight type is Q4_K; lighter
- * experts, and every expert when rows == 0, use the LDS-tiled GEMV, which is
- * bit-identical to ggml.  Default 8.  No reference counterpart: ggml's CPU
+ * large verify batches) are computed on the matrix cores when the weight type
+ * is Q4_K or Q6_K; lighter experts, and every expert when rows == 0, use the
+ * LDS-tiled GEMV, which is bit-identical to ggml.  Default 8.  The exact Q4_K
+ * form runs on the f16 matrix cores with an f16 copy of the activation quants
+ * (2 K bytes per activation row, taken from the workspace; without room for it
+ * the int8 matrix cores run, with the same bits).  No reference counterpart: ggml's CPU
  * backend has one dot product per type (ggml-cpu.c:1463-1524); this only
  * selects the GPU kernel. */
 int qwmoe_set_mfma_min_rows(int rows);
