@@ -352,9 +352,11 @@ __global__ void __launch_bounds__(256) k_attn_scores_mf(AttnArgs a) {
         for (int st = 0; st < 8; ++st) kb[st] = ok ? *(const h4*) (krow + 16 * st) : h4{0, 0, 0, 0};
     };
     if (rw0 >= rows) return;
-    // this lane's running max and sum of v_expf(s - max) for its four D rows over its keys
+    // this lane's running max and sum of exp(s - max) for its four D rows over its keys.
+    // The sums only normalize (P.V forms each probability with ggml_v_expf): the
+    // hardware exp here moves S by ~1e-7 of itself, far below the f16 step of p.
     float mrow[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-    double lrow[4] = {0.0, 0.0, 0.0, 0.0};
+    float lrow[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     h4 kc[8], kn[8];
     load_b(key0, kc);
     for (int64_t j0 = key0; j0 < kend; j0 += 16) {
@@ -371,10 +373,10 @@ __global__ void __launch_bounds__(256) k_attn_scores_mf(AttnArgs a) {
                 const float sv = jb > a.n_past + t ? -INFINITY : acc[i] * a.kq_scale;
                 a.s[((int64_t) t * nq + g * R + h) * a.n_kv + jb] = sv;
                 if (sv > mrow[i]) {
-                    lrow[i] = (mrow[i] == -INFINITY ? 0.0 : lrow[i] * exp((double) mrow[i] - (double) sv)) + 1.0;
+                    lrow[i] = (mrow[i] == -INFINITY ? 0.0f : lrow[i] * __expf(mrow[i] - sv)) + 1.0f;
                     mrow[i] = sv;
                 } else if (sv != -INFINITY) {
-                    lrow[i] += (double) v_expf(sv - mrow[i]);
+                    lrow[i] += __expf(sv - mrow[i]);
                 }
             }
         }
@@ -387,10 +389,10 @@ __global__ void __launch_bounds__(256) k_attn_scores_mf(AttnArgs a) {
 #pragma unroll
         for (int off = 1; off < 16; off <<= 1) {
             const float mo = __shfl_xor(mrow[i], off);
-            const double lo = __shfl_xor(lrow[i], off);
+            const float lo = __shfl_xor(lrow[i], off);
             const float mn = fmaxf(mrow[i], mo);
-            const double a0 = mrow[i] == -INFINITY ? 0.0 : lrow[i] * exp((double) mrow[i] - (double) mn);
-            const double a1 = mo == -INFINITY ? 0.0 : lo * exp((double) mo - (double) mn);
+            const float a0 = mrow[i] == -INFINITY ? 0.0f : lrow[i] * __expf(mrow[i] - mn);
+            const float a1 = mo == -INFINITY ? 0.0f : lo * __expf(mo - mn);
             mrow[i] = mn;
             lrow[i] = a0 + a1;
         }
@@ -399,7 +401,7 @@ __global__ void __launch_bounds__(256) k_attn_scores_mf(AttnArgs a) {
             const int t = (int) (r / R), h = (int) (r % R);
             const int64_t sr = (int64_t) blockIdx.x * a.T * nq + (int64_t) t * nq + g * R + h;
             a.stat[2 * sr] = mrow[i];
-            a.stat[2 * sr + 1] = (float) lrow[i];
+            a.stat[2 * sr + 1] = lrow[i];
         }
     }
 }
