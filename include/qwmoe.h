@@ -342,6 +342,51 @@ typedef struct qwmoe_attn_layer {
 int qwmoe_attn_seg(void * stream, const qwmoe_attn_layer * layer, const float * h, int64_t T, int64_t n_past,
                    float rms_eps, float * attn_resid, float * ffn_in);
 
+/* One gated-delta-net block (Seg A of a recurrent layer of qwen3next /
+ * qwen35moe: build_segA with build_gdn, core/runtime.cpp:1976-1995, 737-859).
+ * Weight rows are dense quantized rows (Q4_K / Q6_K / Q8_0); the f32 tensors are
+ * ggml's: conv1d [conv_ch][d_conv], the states in their ggml layouts.  d_inner =
+ * dt_rank * d_state, conv_ch = d_inner + 2 n_group d_state.  Requires d_state =
+ * 128, dt_rank a multiple of n_group, 2 <= d_conv <= 8. */
+typedef struct qwmoe_gdn_layer {
+    int64_t n_embd;            /* H */
+    int64_t d_state;           /* S: ssm.state_size (128) */
+    int64_t n_group;           /* H_k: ssm.group_count (key heads) */
+    int64_t dt_rank;           /* H_v: ssm.time_step_rank (value heads) */
+    int64_t d_conv;            /* ssm.conv_kernel (4) */
+    const float * attn_norm;   /* [H]: blk.N.attn_norm.weight */
+    int type_qkv, type_gate, type_beta, type_alpha, type_out;
+    const void * w_qkv; size_t w_qkv_nb1;       /* blk.N.attn_qkv.weight: conv_ch rows of H */
+    const void * w_gate; size_t w_gate_nb1;     /* blk.N.attn_gate.weight: d_inner rows (z) */
+    const void * w_beta; size_t w_beta_nb1;     /* blk.N.ssm_beta.weight: H_v rows */
+    const void * w_alpha; size_t w_alpha_nb1;   /* blk.N.ssm_alpha.weight: H_v rows */
+    const void * w_out; size_t w_out_nb1;       /* blk.N.ssm_out.weight: H rows of d_inner */
+    const float * dt_bias;     /* [H_v]: blk.N.ssm_dt.bias */
+    const float * ssm_a;       /* [H_v]: blk.N.ssm_a */
+    const float * conv1d;      /* [conv_ch][d_conv]: blk.N.ssm_conv1d.weight */
+    const float * ssm_norm;    /* [S]: blk.N.ssm_norm.weight */
+    const float * ffn_norm;    /* [H]: the router input's norm (ffn_norm / post_attention_norm) */
+    float * conv_state;        /* [conv_ch][d_conv - 1], read and written */
+    float * ssm_state;         /* [H_v][S][S] (S_h transposed per head, as ggml), read and written */
+} qwmoe_gdn_layer;
+
+/* T tokens through the block, h f32 [T, H] the layer input:
+ *   cur = rms_norm(h) * attn_norm; qkv, z, beta, alpha = projections of cur;
+ *   beta = sigmoid(beta); g = softplus(alpha + dt_bias) * ssm_a;
+ *   conv = silu(causal conv of [conv_state | qkv] with conv1d), the conv state
+ *   advanced by T; q, k (H_k heads), v (H_v heads) from conv, q and k l2-normed;
+ *   per value head h (key head h % H_k) and token: S *= exp(g),
+ *   S += k (beta (v - S^T k))^T, o = S^T q / sqrt(S) (ggml_gated_delta_net);
+ *   y = rms_norm(o) * ssm_norm * silu(z) per head; attn_resid = ssm_out(y) + h;
+ *   ffn_in = rms_norm(attn_resid) * ffn_norm (ffn_in may be NULL).
+ * The projections are the quantized mul_mat row dots (ggml's bits); the rest
+ * agrees with the reference CPU graph within float rounding (1e-3).  Calls
+ * carry the layer's states: one call of T tokens equals consecutive calls of
+ * its parts.  Workspace ~4 T (3 conv_ch + 5 d_inner + 2 H) bytes plus the
+ * quantized activations. */
+int qwmoe_gdn_seg(void * stream, const qwmoe_gdn_layer * layer, const float * h, int64_t T, float rms_eps,
+                  float * attn_resid, float * ffn_in);
+
 /* One whole decoder layer of a Qwen3-MoE model for T tokens: qwmoe_attn_seg,
  * then qwmoe_ffn_layer on ffn_in (the router reads ffn_in; build_moe's T = 1 or
  * T > 1 weighted sum), then h_out = moe_out + attn_resid (build_segB's residual,

@@ -563,3 +563,109 @@ int qwref_attn_seg(int64_t H, int64_t n_head, int64_t n_head_kv, int64_t D, int6
 }
 
 }  // extern "C" (attention)
+
+extern "C" {
+
+// ---------------------------------------------------------------------------
+// Seg A's recurrent half (a gated-delta-net layer of qwen3next / qwen35moe) on
+// the CPU backend, the op sequence of core/runtime.cpp:1976-1995 (build_segA)
+// with build_gdn, 737-859, in its one-pass (non-verify) form:
+//   cur = rms_norm(h) * attn_norm;
+//   qkv = mul_mat(attn_qkv, cur) [conv_ch]; z = mul_mat(attn_gate, cur) [d_inner];
+//   beta = sigmoid(mul_mat(ssm_beta, cur)); g = softplus(mul_mat(ssm_alpha, cur) + dt_bias) * ssm_a;
+//   conv_input = concat(conv_state, transpose(qkv)); conv_state <- its last d_conv - 1 steps;
+//   conv = silu(ssm_conv(conv_input, conv1d)); q, k, v = views of conv (H_k, H_k, H_v heads of S);
+//   q, k = l2_norm(.., eps); (out, state) = gated_delta_net(q, k, v, g, beta, ssm_state, 1);
+//   out = rms_norm(out) * ssm_norm * silu(z) per head; cur = mul_mat(ssm_out, out);
+//   attn_resid = cur + h; ffn_in = rms_norm(attn_resid) * ffn_norm.
+// h, attn_resid, ffn_in: [T, H]; conv_state f32 [conv_ch][d_conv - 1] and ssm_state
+// f32 [H_v][S][S] (ggml's layouts) are read and written in place; gdn_out
+// ([T, H_v * S], the gated norm's output) may be NULL.
+int qwref_gdn_seg(int64_t H, int64_t S, int64_t H_k, int64_t H_v, int64_t d_conv, float eps, int64_t T,
+                  const float * h, const float * attn_norm, int t_qkv, const void * w_qkv, int t_gate,
+                  const void * w_gate, int t_beta, const void * w_beta, int t_alpha, const void * w_alpha,
+                  const float * dt_bias, const float * ssm_a, const float * conv1d, const float * ssm_norm,
+                  int t_out, const void * w_out, const float * ffn_norm, float * conv_state, float * ssm_state,
+                  float * attn_resid, float * ffn_in, float * gdn_out, int n_threads) {
+    ensure_init();
+    if (H_v % H_k || d_conv < 2) return -2;
+    const int64_t d_inner = H_v * S, key_dim = H_k * S, conv_ch = d_inner + 2 * key_dim;
+    const size_t el = sizeof(float);
+    const size_t wbytes = ggml_row_size((ggml_type) t_qkv, H) * (size_t) conv_ch +
+                          ggml_row_size((ggml_type) t_gate, H) * (size_t) d_inner +
+                          ggml_row_size((ggml_type) t_beta, H) * (size_t) H_v +
+                          ggml_row_size((ggml_type) t_alpha, H) * (size_t) H_v +
+                          ggml_row_size((ggml_type) t_out, d_inner) * (size_t) H;
+    const size_t act = el * (size_t) T * (size_t) (12 * H + 8 * conv_ch + 12 * d_inner + 8 * H_v) +
+                       el * (size_t) (4 * conv_ch * (d_conv + T) + 3 * S * S * H_v + 4 * H + 2 * S + 4 * H_v) +
+                       el * (size_t) (S * H_v * T + S * S * H_v);
+    ggml_init_params ip = { act + wbytes + ggml_tensor_overhead() * 160 + ggml_graph_overhead() + (4 << 20), nullptr,
+                            false };
+    ggml_context * ctx = ggml_init(ip);
+    auto wt = [&](int type, int64_t ne0, int64_t ne1, const void * data) {
+        ggml_tensor * t = ggml_new_tensor_2d(ctx, (ggml_type) type, ne0, ne1);
+        memcpy(t->data, data, ggml_nbytes(t));
+        return t;
+    };
+    auto vec = [&](const float * v, int64_t n) { return ggml_reshape_1d(ctx, wt(GGML_TYPE_F32, n, 1, v), n); };
+    ggml_tensor * Wqkv = wt(t_qkv, H, conv_ch, w_qkv), * Wgate = wt(t_gate, H, d_inner, w_gate);
+    ggml_tensor * Wbeta = wt(t_beta, H, H_v, w_beta), * Walpha = wt(t_alpha, H, H_v, w_alpha);
+    ggml_tensor * Wout = wt(t_out, d_inner, H, w_out);
+    ggml_tensor * An = vec(attn_norm, H), * Fn = vec(ffn_norm, H), * Sn = vec(ssm_norm, S);
+    ggml_tensor * DTb = vec(dt_bias, H_v), * Aa = vec(ssm_a, H_v);
+    ggml_tensor * CK = wt(GGML_TYPE_F32, d_conv, conv_ch, conv1d);
+    ggml_tensor * CS = wt(GGML_TYPE_F32, d_conv - 1, conv_ch, conv_state);
+    ggml_tensor * SS = ggml_new_tensor_3d(ctx, GGML_TYPE_F32, S, S, H_v);
+    memcpy(SS->data, ssm_state, ggml_nbytes(SS));
+    ggml_tensor * X = wt(GGML_TYPE_F32, H, T, h);
+
+    ggml_cgraph * gf = ggml_new_graph(ctx);
+    ggml_tensor * cur = ggml_mul(ctx, ggml_rms_norm(ctx, X, eps), An);
+    ggml_tensor * qkv = ggml_mul_mat(ctx, Wqkv, cur);                                  // [conv_ch, T]
+    ggml_tensor * z = ggml_mul_mat(ctx, Wgate, cur);                                   // [d_inner, T]
+    ggml_tensor * beta = ggml_sigmoid(ctx, ggml_mul_mat(ctx, Wbeta, cur));
+    beta = ggml_reshape_4d(ctx, beta, 1, H_v, T, 1);
+    ggml_tensor * alpha = ggml_softplus(ctx, ggml_add(ctx, ggml_mul_mat(ctx, Walpha, cur), DTb));
+    ggml_tensor * g = ggml_reshape_4d(ctx, ggml_mul(ctx, alpha, Aa), 1, H_v, T, 1);
+    ggml_tensor * cs = ggml_reshape_3d(ctx, CS, d_conv - 1, conv_ch, 1);
+    ggml_tensor * conv_input = ggml_concat(ctx, cs, ggml_transpose(ctx, qkv), 0);   // [d_conv - 1 + T, conv_ch, 1]
+    ggml_tensor * cs_last = ggml_view_3d(ctx, conv_input, d_conv - 1, conv_ch, 1, conv_input->nb[1],
+                                         conv_input->nb[2], ggml_row_size(conv_input->type, T));
+    ggml_build_forward_expand(gf, ggml_cpy(ctx, cs_last, CS));
+    ggml_tensor * conv = ggml_silu(ctx, ggml_ssm_conv(ctx, conv_input, CK));          // [conv_ch, T, 1]
+    const size_t nb1q = ggml_row_size(conv->type, conv_ch);
+    ggml_tensor * q = ggml_view_4d(ctx, conv, S, H_k, T, 1, el * S, nb1q, nb1q * T, 0);
+    ggml_tensor * k = ggml_view_4d(ctx, conv, S, H_k, T, 1, el * S, nb1q, nb1q * T, el * key_dim);
+    ggml_tensor * v = ggml_view_4d(ctx, conv, S, H_v, T, 1, el * S, nb1q, nb1q * T, el * 2 * key_dim);
+    q = ggml_cont(ctx, ggml_l2_norm(ctx, q, eps));
+    k = ggml_cont(ctx, ggml_l2_norm(ctx, k, eps));
+    v = ggml_cont(ctx, v);
+    ggml_tensor * s_in = ggml_reshape_4d(ctx, SS, S, S, H_v, 1);
+    ggml_tensor * res = ggml_gated_delta_net(ctx, q, k, v, g, beta, s_in, 1);
+    ggml_tensor * out = ggml_view_4d(ctx, res, S, H_v, T, 1, el * S, el * S * H_v, el * S * H_v * T, 0);
+    ggml_tensor * st = ggml_view_4d(ctx, res, S, S, H_v, 1, el * S, el * S * S, el * S * S * H_v, el * S * H_v * T);
+    ggml_build_forward_expand(gf, ggml_cpy(ctx, st, ggml_reshape_3d(ctx, SS, S, S, H_v)));
+    out = ggml_mul(ctx, ggml_rms_norm(ctx, ggml_cont(ctx, out), eps), Sn);
+    out = ggml_mul(ctx, out, ggml_silu(ctx, ggml_reshape_4d(ctx, z, S, H_v, T, 1)));
+    out = ggml_reshape_2d(ctx, out, S * H_v, T);
+    ggml_tensor * resid = ggml_add(ctx, ggml_mul_mat(ctx, Wout, out), X);
+    ggml_tensor * fin = ggml_mul(ctx, ggml_rms_norm(ctx, resid, eps), Fn);
+    ggml_build_forward_expand(gf, out);
+    ggml_build_forward_expand(gf, fin);
+
+    ggml_cplan plan = ggml_graph_plan(gf, n_threads, nullptr);
+    std::vector<uint8_t> work(plan.work_size + 64);
+    plan.work_data = work.data();
+    const int rc = ggml_graph_compute(gf, &plan) == GGML_STATUS_SUCCESS ? 0 : -1;
+    if (rc == 0) {
+        if (attn_resid) copy_2d(resid, attn_resid, 4);
+        if (ffn_in) copy_2d(fin, ffn_in, 4);
+        if (gdn_out) copy_2d(out, gdn_out, 4);
+        memcpy(conv_state, CS->data, ggml_nbytes(CS));
+        memcpy(ssm_state, SS->data, ggml_nbytes(SS));
+    }
+    ggml_free(ctx);
+    return rc;
+}
+
+}  // extern "C" (gated delta net)

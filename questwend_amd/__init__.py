@@ -67,6 +67,22 @@ class AttnLayer(C.Structure):
     ]
 
 
+class GdnLayer(C.Structure):
+    """Mirror of ``qwmoe_gdn_layer`` (include/qwmoe.h)."""
+
+    _fields_ = [
+        ("n_embd", C.c_int64), ("d_state", C.c_int64), ("n_group", C.c_int64), ("dt_rank", C.c_int64),
+        ("d_conv", C.c_int64), ("attn_norm", C.c_void_p),
+        ("type_qkv", C.c_int), ("type_gate", C.c_int), ("type_beta", C.c_int), ("type_alpha", C.c_int),
+        ("type_out", C.c_int),
+        ("w_qkv", C.c_void_p), ("w_qkv_nb1", C.c_size_t), ("w_gate", C.c_void_p), ("w_gate_nb1", C.c_size_t),
+        ("w_beta", C.c_void_p), ("w_beta_nb1", C.c_size_t), ("w_alpha", C.c_void_p), ("w_alpha_nb1", C.c_size_t),
+        ("w_out", C.c_void_p), ("w_out_nb1", C.c_size_t),
+        ("dt_bias", C.c_void_p), ("ssm_a", C.c_void_p), ("conv1d", C.c_void_p), ("ssm_norm", C.c_void_p),
+        ("ffn_norm", C.c_void_p), ("conv_state", C.c_void_p), ("ssm_state", C.c_void_p),
+    ]
+
+
 # name -> (restype, argtypes); every exported symbol of include/qwmoe.h
 P, I64, SZ, I, F, U64 = C.c_void_p, C.c_int64, C.c_size_t, C.c_int, C.c_float, C.c_uint64
 SIGNATURES = {
@@ -97,6 +113,7 @@ SIGNATURES = {
     "qwmoe_shared_expert_add": (I, [P, P, I64, P, I64, P, P, P]),
     "qwmoe_ffn_layer": (I, [P, P, P, I64, P, F, P, P, P]),
     "qwmoe_attn_seg": (I, [P, P, P, I64, I64, F, P, P]),
+    "qwmoe_gdn_seg": (I, [P, P, P, I64, F, P, P]),
     "qwmoe_decoder_layer": (I, [P, P, P, P, I64, I64, F, P, P, P]),
     "qwmoe_decode_stack_create": (I, [P, I, F, P]),
     "qwmoe_decode_stack_run": (I, [P, P, P, P, P, P, P]),

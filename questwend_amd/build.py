@@ -22,7 +22,7 @@ BUILD = PKG / "_build"
 LIB = PKG / "libqwmoe.so"
 ARCH = os.environ.get("QWMOE_ARCH", "gfx950")
 
-SOURCES = ["quantize.hip", "router.hip", "mmid.hip", "mmid_mfma.hip", "ffn.hip", "decode.hip", "decode_xcd.hip", "decode_xcd_wide.hip", "verify_xcd.hip", "api.cpp", "slot_table.cpp", "gguf.cpp", "expert_cache.cpp", "slab_copy.hip", "layer_stack.cpp", "scratch.hip", "attn.hip"]
+SOURCES = ["quantize.hip", "router.hip", "mmid.hip", "mmid_mfma.hip", "ffn.hip", "decode.hip", "decode_xcd.hip", "decode_xcd_wide.hip", "verify_xcd.hip", "api.cpp", "slot_table.cpp", "gguf.cpp", "expert_cache.cpp", "slab_copy.hip", "layer_stack.cpp", "scratch.hip", "attn.hip", "gdn.hip"]
 
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Wall", "-Wno-unused-function",
           "-Wno-unused-variable", "-Wno-unused-but-set-variable"]

@@ -679,6 +679,121 @@ int qwmoe_attn_seg(void* stream, const qwmoe_attn_layer* L, const float* h, int6
     return qw::launch_add_rms_norm_mul(proj, h, attn_resid, ffn_in, H, T, rms_eps, L->ffn_norm, st);
 }
 
+// The recurrent half of Seg A for a gated-delta-net layer (build_segA with
+// build_gdn, core/runtime.cpp:1976-1995 and 737-859): the five projections as
+// one-expert mul_mat_ids (ggml's row dots), the conv, the recurrence and the
+// gated norm in gdn.hip, the residual and the FFN input norm.
+int qwmoe_gdn_seg(void* stream, const qwmoe_gdn_layer* L, const float* h, int64_t T, float rms_eps,
+                  float* attn_resid, float* ffn_in) {
+    if (!g_lib.ready) return QWMOE_ERR_NOT_INITIALIZED;
+    if (!L || !h || !attn_resid || T < 0 || !(rms_eps >= 0.0f)) return QWMOE_ERR_INVALID_ARG;
+    const int64_t H = L->n_embd, Sd = L->d_state, Hk = L->n_group, Hv = L->dt_rank, dc = L->d_conv;
+    if (H <= 0 || Sd <= 0 || Hk <= 0 || Hv <= 0 || dc <= 0 || !L->attn_norm || !L->w_qkv || !L->w_gate ||
+        !L->w_beta || !L->w_alpha || !L->w_out || !L->dt_bias || !L->ssm_a || !L->conv1d || !L->ssm_norm ||
+        !L->conv_state || !L->ssm_state || (ffn_in && !L->ffn_norm))
+        return QWMOE_ERR_INVALID_ARG;
+    if (!qw::gdn_shape_ok(Sd, Hk, Hv, dc) || H % 4 || ((uintptr_t) h & 15) || ((uintptr_t) L->ssm_state & 15))
+        return QWMOE_ERR_UNSUPPORTED;
+    const int64_t d_inner = Hv * Sd, key_dim = Hk * Sd, conv_ch = d_inner + 2 * key_dim;
+    const int types[5] = {L->type_qkv, L->type_gate, L->type_beta, L->type_alpha, L->type_out};
+    for (int t : types)
+        if (!weight_type_ok(t)) return QWMOE_ERR_UNSUPPORTED;
+    int rc;
+    if ((rc = check_k(L->type_qkv, H)) || (rc = check_k(L->type_gate, H)) || (rc = check_k(L->type_beta, H)) ||
+        (rc = check_k(L->type_alpha, H)) || (rc = check_k(L->type_out, d_inner)))
+        return rc;
+    if (L->w_qkv_nb1 < qwmoe_row_size(L->type_qkv, H) || L->w_gate_nb1 < qwmoe_row_size(L->type_gate, H) ||
+        L->w_beta_nb1 < qwmoe_row_size(L->type_beta, H) || L->w_alpha_nb1 < qwmoe_row_size(L->type_alpha, H) ||
+        L->w_out_nb1 < qwmoe_row_size(L->type_out, d_inner))
+        return QWMOE_ERR_INVALID_ARG;
+    if (T == 0) return QWMOE_OK;
+    if (T > INT32_MAX / 2) return QWMOE_ERR_UNSUPPORTED;
+    hipStream_t st = S(stream);
+    Arena ar(kReserved);
+    int32_t* rows = ar.take<int32_t>((size_t) (2 * T + 2));
+    int32_t* active = ar.take<int32_t>(2);
+    int32_t* active_off = ar.take<int32_t>(3);
+    int32_t* n_active = ar.take<int32_t>(1);
+    float* cur = ar.take<float>((size_t) (H * T));
+    float* qkv = ar.take<float>((size_t) (conv_ch * T));
+    float* z = ar.take<float>((size_t) (d_inner * T));
+    float* braw = ar.take<float>((size_t) (Hv * T));
+    float* araw = ar.take<float>((size_t) (Hv * T));
+    float* conv = ar.take<float>((size_t) (conv_ch * T));
+    float* qn = ar.take<float>((size_t) (key_dim * T));
+    float* kn = ar.take<float>((size_t) (key_dim * T));
+    float* bg = ar.take<float>((size_t) (2 * Hv * T));
+    float* o = ar.take<float>((size_t) (d_inner * T));
+    float* y = ar.take<float>((size_t) (d_inner * T));
+    float* proj = ar.take<float>((size_t) (H * T));
+    if (!rows || !active || !active_off || !n_active || !cur || !qkv || !z || !braw || !araw || !conv || !qn || !kn ||
+        !bg || !o || !y || !proj)
+        return QWMOE_ERR_WORKSPACE;
+    // the input quantized once per vec_dot type the four input projections use
+    int vt[4] = {qw::vec_dot_type(L->type_qkv), qw::vec_dot_type(L->type_gate), qw::vec_dot_type(L->type_beta),
+                 qw::vec_dot_type(L->type_alpha)};
+    uint8_t* xq[4] = {nullptr, nullptr, nullptr, nullptr};
+    size_t xr[4];
+    for (int i = 0; i < 4; ++i) {
+        xr[i] = qwmoe_row_size(vt[i], H);
+        for (int j = 0; j < i; ++j)
+            if (vt[j] == vt[i]) xq[i] = xq[j];
+        if (!xq[i] && !(xq[i] = ar.take<uint8_t>(xr[i] * (size_t) T + 64))) return QWMOE_ERR_WORKSPACE;
+    }
+    const int vot = qw::vec_dot_type(L->type_out);
+    const size_t ro = qwmoe_row_size(vot, d_inner);
+    uint8_t* yq = ar.take<uint8_t>(ro * (size_t) T + 64);
+    if (!yq) return QWMOE_ERR_WORKSPACE;
+    if ((rc = qw::launch_group_dense(rows, active, active_off, n_active, T, st))) return rc;
+    const size_t hb = (size_t) H * 4;
+    if ((rc = qw::launch_rms_norm(h, cur, H, T, rms_eps, st, L->attn_norm))) return rc;
+    for (int i = 0; i < 4; ++i) {
+        bool done = false;
+        for (int j = 0; j < i; ++j) done = done || xq[j] == xq[i];
+        if (!done && (rc = qw::launch_quantize_act(vt[i], cur, H, 1, T, hb, hb, xq[i], st))) return rc;
+    }
+    auto proj_launch = [&](int type, const void* w, size_t nb1, int64_t K, int64_t N, const uint8_t* xb, size_t xrow,
+                           float* dst) {
+        const size_t ob = (size_t) N * 4;
+        qw::MmidArgs m = mmid_args(type, w, K, N, 1, nb1, nb1 * (size_t) N, xb, 1, xrow, rows, active, active_off,
+                                   n_active, 1, nullptr, 0, dst, ob, ob, T, T);
+        if (int r = mfma_f16_prep(ar, m, T, st)) return r;
+        return mmid_launch(m, st);
+    };
+    if ((rc = proj_launch(L->type_qkv, L->w_qkv, L->w_qkv_nb1, H, conv_ch, xq[0], xr[0], qkv))) return rc;
+    if ((rc = proj_launch(L->type_gate, L->w_gate, L->w_gate_nb1, H, d_inner, xq[1], xr[1], z))) return rc;
+    if ((rc = proj_launch(L->type_beta, L->w_beta, L->w_beta_nb1, H, Hv, xq[2], xr[2], braw))) return rc;
+    if ((rc = proj_launch(L->type_alpha, L->w_alpha, L->w_alpha_nb1, H, Hv, xq[3], xr[3], araw))) return rc;
+    qw::GdnArgs a{};
+    a.T = (int) T;
+    a.H_k = (int) Hk;
+    a.H_v = (int) Hv;
+    a.d_conv = (int) dc;
+    a.conv_ch = conv_ch;
+    a.eps = rms_eps;
+    a.qkv = qkv;
+    a.z = z;
+    a.braw = braw;
+    a.araw = araw;
+    a.dt_bias = L->dt_bias;
+    a.ssm_a = L->ssm_a;
+    a.conv1d = L->conv1d;
+    a.ssm_norm = L->ssm_norm;
+    a.conv_state = L->conv_state;
+    a.state = L->ssm_state;
+    a.conv = conv;
+    a.qn = qn;
+    a.kn = kn;
+    a.bg = bg;
+    a.o = o;
+    a.y = y;
+    if ((rc = qw::launch_gdn_core(a, st))) return rc == -2 ? QWMOE_ERR_UNSUPPORTED : QWMOE_ERR_HIP;
+    const size_t yb = (size_t) d_inner * 4;
+    if ((rc = qw::launch_quantize_act(vot, y, d_inner, 1, T, yb, yb, yq, st))) return rc;
+    if ((rc = proj_launch(L->type_out, L->w_out, L->w_out_nb1, d_inner, H, yq, ro, proj))) return rc;
+    return qw::launch_add_rms_norm_mul(proj, h, attn_resid, ffn_in, H, T, rms_eps, L->ffn_norm, st);
+}
+
 int qwmoe_decoder_layer(void* stream, const qwmoe_attn_layer* attn, const qwmoe_layer* moe, const float* h,
                         int64_t T, int64_t n_past, float rms_eps, float* h_out, int32_t* ids_out,
                         float* weights_out) {

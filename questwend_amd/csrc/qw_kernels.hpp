@@ -187,4 +187,31 @@ int launch_add_rms_norm_mul(const float* x, const float* y, float* resid, float*
                             float eps, const float* w, hipStream_t stream);
 int launch_fill_i32(int32_t* p, int64_t n, int32_t v, hipStream_t stream);
 
+// gdn.hip -- the gated-delta-net half of Seg A (qwen3next / qwen35moe)
+constexpr int GDN_MAX_CONV = 8;   // conv taps (ssm.conv_kernel), at most
+struct GdnArgs {
+    int T, H_k, H_v, d_conv;
+    int64_t conv_ch;              // H_v S + 2 H_k S
+    float eps;
+    const float* qkv;             // [T][conv_ch] the attn_qkv projection
+    const float* z;               // [T][H_v S] the attn_gate projection
+    const float* braw;            // [T][H_v] ssm_beta projection
+    const float* araw;            // [T][H_v] ssm_alpha projection
+    const float* dt_bias;         // [H_v]
+    const float* ssm_a;           // [H_v]
+    const float* conv1d;          // [conv_ch][d_conv]
+    const float* ssm_norm;        // [S]
+    float* conv_state;            // [conv_ch][d_conv - 1], updated
+    float* state;                 // [H_v][S][S] (ggml's layout, S^T per head), updated
+    float* conv;                  // [T][conv_ch] silu(conv)
+    float* qn;                    // [T][H_k][S] l2-normed q
+    float* kn;                    // [T][H_k][S] l2-normed k
+    float* bg;                    // [T][H_v][2] beta, g
+    float* o;                     // [T][H_v][S] the recurrence's outputs
+    float* y;                     // [T][H_v S] the gated norm's outputs
+};
+// S = 128, H_v a multiple of H_k, 2 <= d_conv <= GDN_MAX_CONV
+bool gdn_shape_ok(int64_t S, int64_t H_k, int64_t H_v, int64_t d_conv);
+int launch_gdn_core(const GdnArgs& a, hipStream_t stream);
+
 }  // namespace qw

@@ -426,6 +426,39 @@ def attn_seg(layer, h, n_past: int, rms_eps: float = 1e-6, want_ffn_in: bool = T
     return resid, fin
 
 
+def make_gdn_layer(H, S, H_k, H_v, d_conv, types, attn_norm, w_qkv, w_gate, w_beta, w_alpha, w_out, dt_bias, ssm_a,
+                   conv1d, ssm_norm, ffn_norm, conv_state, ssm_state):
+    """Builds a ``qwmoe_gdn_layer`` from device tensors (dense weight rows; f32
+    conv1d [conv_ch, d_conv], conv_state [conv_ch, d_conv - 1], ssm_state
+    [H_v, S, S]; the caller keeps them alive).  types: (qkv, gate, beta, alpha,
+    out) ggml type ids."""
+    from . import GdnLayer
+    L = GdnLayer()
+    L.n_embd, L.d_state, L.n_group, L.dt_rank, L.d_conv = H, S, H_k, H_v, d_conv
+    L.attn_norm = _ptr(attn_norm)
+    L.type_qkv, L.type_gate, L.type_beta, L.type_alpha, L.type_out = types
+    L.w_qkv, L.w_qkv_nb1 = _ptr(w_qkv), row_size(types[0], H)
+    L.w_gate, L.w_gate_nb1 = _ptr(w_gate), row_size(types[1], H)
+    L.w_beta, L.w_beta_nb1 = _ptr(w_beta), row_size(types[2], H)
+    L.w_alpha, L.w_alpha_nb1 = _ptr(w_alpha), row_size(types[3], H)
+    L.w_out, L.w_out_nb1 = _ptr(w_out), row_size(types[4], H_v * S)
+    L.dt_bias, L.ssm_a, L.conv1d, L.ssm_norm, L.ffn_norm = (_ptr(dt_bias), _ptr(ssm_a), _ptr(conv1d),
+                                                             _ptr(ssm_norm), _ptr(ffn_norm))
+    L.conv_state, L.ssm_state = _ptr(conv_state), _ptr(ssm_state)
+    return L
+
+
+def gdn_seg(layer, h, rms_eps: float = 1e-6, want_ffn_in: bool = True):
+    """The gated-delta-net half of Seg A for h f32 [T, H]: (attn_resid, ffn_in or
+    None); the layer's conv and recurrent states advance by T tokens."""
+    torch = _torch()
+    T, H = h.shape
+    resid = torch.empty((T, H), dtype=torch.float32, device=h.device)
+    fin = torch.empty((T, H), dtype=torch.float32, device=h.device) if want_ffn_in else None
+    check(lib().qwmoe_gdn_seg(stream(), C.byref(layer), _ptr(h), T, rms_eps, _ptr(resid), _ptr(fin)), "gdn_seg")
+    return resid, fin
+
+
 def decoder_layer(attn, moe: Layer, h, n_past: int, rms_eps: float = 1e-6):
     """A whole Qwen3-MoE decoder layer for h f32 [T, H]: (h_out, ids, weights)."""
     torch = _torch()

@@ -383,6 +383,108 @@ def attn_seg_restated(aw: AttnWeights, h, n_past: int, k_cache, v_cache, orc: Or
     return resid, fin, Q.reshape(T, NQ), att
 
 
+class GdnWeights:
+    """A gated-delta-net block's weights (qwen3next / qwen35moe recurrent
+    layers), seeded: attn_qkv [conv_ch, H], attn_gate [d_inner, H], ssm_beta and
+    ssm_alpha [H_v, H], ssm_out [H, d_inner] quantized from N(0, 0.02) fp32
+    (types (qkv, gate, beta, alpha, out)); conv1d [conv_ch][d_conv] N(0, 0.3);
+    dt_bias N(0, 0.5); ssm_a = -U(0.5, 2) (decays below 1); the f32 norms
+    N(1, 0.1).  d_inner = H_v * S, conv_ch = d_inner + 2 H_k S."""
+
+    def __init__(self, H, S, H_k, H_v, d_conv, types, seed, oracle: Oracle):
+        rng = np.random.default_rng(seed)
+        self.H, self.S, self.H_k, self.H_v, self.d_conv, self.types = H, S, H_k, H_v, d_conv, types
+        self.d_inner, self.key_dim = H_v * S, H_k * S
+        self.conv_ch = self.d_inner + 2 * self.key_dim
+        q = lambda t, r, c: oracle.quantize(t, (rng.standard_normal((r, c)) * 0.02).astype(np.float32))  # noqa: E731
+        self.w_qkv, self.w_gate = q(types[0], self.conv_ch, H), q(types[1], self.d_inner, H)
+        self.w_beta, self.w_alpha = q(types[2], H_v, H), q(types[3], H_v, H)
+        self.w_out = q(types[4], H, self.d_inner)
+        self.conv1d = (rng.standard_normal((self.conv_ch, d_conv)) * 0.3).astype(np.float32)
+        self.dt_bias = (rng.standard_normal(H_v) * 0.5).astype(np.float32)
+        self.ssm_a = (-rng.uniform(0.5, 2.0, H_v)).astype(np.float32)
+        nrm = lambda n: (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32)  # noqa: E731
+        self.attn_norm, self.ffn_norm, self.ssm_norm = nrm(H), nrm(H), nrm(S)
+
+    def fresh_state(self, rng=None):
+        """(conv_state f32 [conv_ch][d_conv - 1], ssm_state f32 [H_v][S][S]):
+        zeros, or small seeded values when rng is given."""
+        if rng is None:
+            return (np.zeros((self.conv_ch, self.d_conv - 1), np.float32),
+                    np.zeros((self.H_v, self.S, self.S), np.float32))
+        return ((rng.standard_normal((self.conv_ch, self.d_conv - 1)) * 0.5).astype(np.float32),
+                (rng.standard_normal((self.H_v, self.S, self.S)) * 0.05).astype(np.float32))
+
+
+def gdn_seg_restated(gw: GdnWeights, h, conv_state, ssm_state, orc: Oracle, eps: float = 1e-6):
+    """Seg A's recurrent half (core/runtime.cpp:1976-1995 with build_gdn 737-859)
+    restated on the CPU: the projections are the oracle's quantized mul_mat
+    (ggml's row dots, bit for bit); rms_norm and l2_norm with ggml's double sums;
+    sigmoid / softplus (threshold 20) / silu in float32 as ggml's unary ops;
+    ggml_ssm_conv's window dot in float32; ggml_gated_delta_net's recurrence
+    (ops.cpp:10734-10887: per value head h with key head h % H_k, the state
+    M = S^T, M *= exp(g); delta = (v - M k) beta; M += delta k^T; out = M q / sqrt(S))
+    in float64.  Returns (attn_resid, ffn_in, gated_out); conv_state and
+    ssm_state are updated in place."""
+    h = np.ascontiguousarray(h, np.float32)
+    T, H = h.shape
+    S, Hk, Hv, dc = gw.S, gw.H_k, gw.H_v, gw.d_conv
+    d_inner, key_dim, conv_ch = gw.d_inner, gw.key_dim, gw.conv_ch
+    f32 = np.float32
+
+    def mm(t, w, x, N):
+        return orc.mul_mat_id(t, x.shape[1], N, 1, w, x[:, None, :], np.zeros((x.shape[0], 1), np.int32))[:, 0, :]
+
+    cur = orc.rms_norm_mul(h, gw.attn_norm, eps)
+    qkv = mm(gw.types[0], gw.w_qkv, cur, conv_ch)
+    z = mm(gw.types[1], gw.w_gate, cur, d_inner)
+    braw = mm(gw.types[2], gw.w_beta, cur, Hv)
+    beta = (f32(1.0) / (f32(1.0) + np.exp(-braw).astype(f32))).astype(f32)
+    a = (mm(gw.types[3], gw.w_alpha, cur, Hv) + gw.dt_bias).astype(f32)
+    sp = np.where(a > f32(20.0), a, np.log(f32(1.0) + np.exp(a).astype(f32)).astype(f32)).astype(f32)
+    g = (sp * gw.ssm_a).astype(f32)
+    # causal conv over [conv_state | qkv^T], d_conv taps, float32 in tap order
+    inp = np.concatenate([conv_state, qkv.T], axis=1).astype(f32)          # [conv_ch, dc - 1 + T]
+    conv = np.zeros((T, conv_ch), f32)
+    for t in range(T):
+        acc = np.zeros(conv_ch, f32)
+        for j in range(dc):
+            acc = (acc + inp[:, t + j] * gw.conv1d[:, j]).astype(f32)
+        conv[t] = acc
+    conv_state[:] = inp[:, T:T + dc - 1]
+    conv = (conv.astype(np.float64) / (1.0 + np.exp(-conv.astype(np.float64)))).astype(f32)
+
+    def l2(x):
+        ss = np.sum((x * x).astype(np.float64), axis=-1, keepdims=True)
+        return (x * (f32(1.0) / np.maximum(np.sqrt(ss).astype(f32), f32(eps)))).astype(f32)
+
+    q = l2(conv[:, :key_dim].reshape(T, Hk, S)).astype(np.float64)
+    k = l2(conv[:, key_dim:2 * key_dim].reshape(T, Hk, S)).astype(np.float64)
+    v = conv[:, 2 * key_dim:].reshape(T, Hv, S).astype(np.float64)
+    M = ssm_state.astype(np.float64)                                        # [Hv][j][i] = S[i][j]
+    o = np.zeros((T, Hv, S), np.float64)
+    scale = 1.0 / np.sqrt(np.float32(S))
+    for t in range(T):
+        for hv in range(Hv):
+            hk = hv % Hk
+            M[hv] *= np.exp(np.float64(g[t, hv]))
+            delta = (v[t, hv] - M[hv] @ k[t, hk]) * np.float64(beta[t, hv])
+            M[hv] += np.outer(delta, k[t, hk])
+            o[t, hv] = (M[hv] @ q[t, hk]) * scale
+    ssm_state[:] = M.astype(f32)
+    o = o.astype(f32)
+    ss = np.sum((o * o).astype(np.float64), axis=-1, keepdims=True)
+    sc = (f32(1.0) / np.sqrt((ss / S).astype(f32) + f32(eps))).astype(f32)
+    zz = z.reshape(T, Hv, S).astype(np.float64)
+    silu_z = (zz / (1.0 + np.exp(-zz))).astype(f32)
+    y = ((o * sc).astype(f32) * gw.ssm_norm).astype(f32)
+    y = (y * silu_z).astype(f32).reshape(T, d_inner)
+    proj = mm(gw.types[4], gw.w_out, y, H)
+    resid = (proj + h).astype(f32)
+    fin = orc.rms_norm_mul(resid, gw.ffn_norm, eps)
+    return resid, fin, y
+
+
 class RefGGML:
     def __init__(self, path: Path = REF_SO):
         if not path.exists():
@@ -409,6 +511,9 @@ class RefGGML:
                                               + [C.c_int])
         L.qwref_router_resident.argtypes = ([C.c_int64] * 4 + [C.c_void_p] * 3 + [C.c_float] + [C.c_void_p] * 4
                                             + [C.c_int])
+        L.qwref_gdn_seg.argtypes = ([C.c_int64] * 5 + [C.c_float, C.c_int64] + [C.c_void_p] * 2
+                                    + [C.c_int, C.c_void_p] * 4 + [C.c_void_p] * 4 + [C.c_int, C.c_void_p]
+                                    + [C.c_void_p] * 6 + [C.c_int])
         L.qwref_attn_seg.argtypes = ([C.c_int64] * 5 + [C.c_float] * 2 + [C.c_int64] * 3 + [C.c_void_p] * 2
                                      + [C.c_int, C.c_void_p] * 4 + [C.c_void_p] * 9 + [C.c_int])
 
@@ -429,6 +534,24 @@ class RefGGML:
                                      _p(qo), _p(att), n_threads)
         assert rc == 0, rc
         return resid, fin, qo, att
+
+    def gdn_seg(self, gw, h, conv_state, ssm_state, eps: float = 1e-6, n_threads: int = 4):
+        """ggml's Seg A recurrent half (build_segA + build_gdn) on GdnWeights gw:
+        (attn_resid, ffn_in, gated_out); conv_state / ssm_state are updated in place."""
+        h = np.ascontiguousarray(h, np.float32)
+        T, H = h.shape
+        resid, fin = np.zeros((T, H), np.float32), np.zeros((T, H), np.float32)
+        y = np.zeros((T, gw.d_inner), np.float32)
+        assert conv_state.flags.c_contiguous and ssm_state.flags.c_contiguous
+        assert conv_state.dtype == np.float32 and ssm_state.dtype == np.float32
+        t = gw.types
+        rc = self.lib.qwref_gdn_seg(H, gw.S, gw.H_k, gw.H_v, gw.d_conv, eps, T, _p(h), _p(gw.attn_norm), t[0],
+                                    _p(gw.w_qkv), t[1], _p(gw.w_gate), t[2], _p(gw.w_beta), t[3], _p(gw.w_alpha),
+                                    _p(gw.dt_bias), _p(gw.ssm_a), _p(gw.conv1d), _p(gw.ssm_norm), t[4],
+                                    _p(gw.w_out), _p(gw.ffn_norm), _p(conv_state), _p(ssm_state), _p(resid),
+                                    _p(fin), _p(y), n_threads)
+        assert rc == 0, rc
+        return resid, fin, y
 
     def router_resident(self, W, x, k: int, mask, scale: float = 0.0, n_threads: int = 2):
         """ggml's resident-only router: ids, weights, want (unmasked top k), probs."""
