@@ -1056,6 +1056,131 @@ def attn_bench(args) -> int:
     return 0
 
 
+def gdn_bench(args) -> int:
+    """The gated-delta-net half of Seg A (qwmoe_gdn_seg; build_gdn,
+    core/runtime.cpp:737-859) at the shape of the reference's build_gdn comments:
+    H = 2048, S = 128, 16 key and 16 value heads, d_conv = 4 (conv_ch 6144), Q4_K
+    attn_qkv / ssm_out, Q6_K attn_gate, Q8_0 ssm_beta / ssm_alpha (seeded synthetic
+    weights quantized on the GPU).  Timed: decode (T = 1, the states carried from
+    call to call) -- the line's value, tokens per second of the segment -- and a
+    prefill chunk of 512 tokens.  roofline: the weight rows one decode call reads
+    plus the recurrent and conv states it reads and writes, over its time (HIP
+    events).  cpu_baseline: ggml's own graph for the block (oracle/_ref, AVX-512
+    build where the host has it) on the same weights at decode."""
+    import numpy as np
+    import torch
+    from questwend_amd import Q4_K, Q6_K, Q8_0, ops, row_size
+
+    S, HK, HV, DC = 128, 16, 16, 4
+    d_inner, key_dim = HV * S, HK * S
+    conv_ch = d_inner + 2 * key_dim
+    types = (Q4_K, Q6_K, Q8_0, Q8_0, Q4_K)
+    dev = "cuda:0"
+    ops.init(0, 512 << 20)
+
+    def qmat(rows, cols, t, seed):
+        f = torch.empty((rows, cols), dtype=torch.float32, device=dev)
+        ops.randn_(f, seed, 0.0, 0.02)
+        return ops.quantize_chunk(t, f)
+
+    def vec(n, seed, mean=1.0, std=0.1):
+        v = torch.empty(n, dtype=torch.float32, device=dev)
+        return ops.randn_(v, seed, mean, std)
+
+    sd = args.seed * 1000 + 950
+    w_qkv, w_gate = qmat(conv_ch, H, types[0], sd + 1), qmat(d_inner, H, types[1], sd + 2)
+    w_beta, w_alpha = qmat(HV, H, types[2], sd + 3), qmat(HV, H, types[3], sd + 4)
+    w_out = qmat(H, d_inner, types[4], sd + 5)
+    an, fn, sn = vec(H, sd + 6), vec(H, sd + 7), vec(S, sd + 8)
+    dtb = vec(HV, sd + 9, 0.0, 0.5)
+    ssm_a = -(vec(HV, sd + 10, 1.25, 0.3).abs() + 0.1)
+    conv1d = torch.empty((conv_ch, DC), dtype=torch.float32, device=dev)
+    ops.randn_(conv1d, sd + 11, 0.0, 0.3)
+    cs = torch.zeros((conv_ch, DC - 1), dtype=torch.float32, device=dev)
+    ss = torch.zeros((HV, S, S), dtype=torch.float32, device=dev)
+    GL = ops.make_gdn_layer(H, S, HK, HV, DC, types, an, w_qkv, w_gate, w_beta, w_alpha, w_out, dtb, ssm_a, conv1d,
+                            sn, fn, cs, ss)
+    torch.cuda.synchronize()
+
+    def timed(fn_, n):
+        for _ in range(max(2, args.warmup)):
+            fn_()
+        torch.cuda.synchronize()
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+        t0 = time.perf_counter()
+        for a, b in evs:
+            a.record()
+            fn_()
+            b.record()
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) / n
+        return wall, sum(a.elapsed_time(b) for a, b in evs) / n / 1000.0
+
+    h1 = torch.empty((1, H), dtype=torch.float32, device=dev)
+    ops.randn_(h1, sd + 20, 0.0, 1.0)
+    hp = torch.empty((512, H), dtype=torch.float32, device=dev)
+    ops.randn_(hp, sd + 21, 0.0, 1.0)
+    dec_wall, dec_ev = timed(lambda: ops.gdn_seg(GL, h1), args.steps)
+    pre_wall, pre_ev = timed(lambda: ops.gdn_seg(GL, hp), max(4, args.steps // 16))
+    status = ops.device_status(clear=True)
+
+    wbytes = conv_ch * row_size(types[0], H) + d_inner * row_size(types[1], H) + HV * row_size(types[2], H) + \
+        HV * row_size(types[3], H) + H * row_size(types[4], d_inner)
+    sbytes = 2 * (HV * S * S + conv_ch * (DC - 1)) * 4
+    abytes = wbytes + sbytes + (4 * H + S + conv_ch * DC + 2 * HV) * 4
+    cpu = None
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, str(ROOT / "tests"))
+        from oracle_lib import REF_SO, REF_SO_AVX512, GdnWeights, RefGGML, have_ref_avx512
+        if REF_SO.exists():
+            gw = GdnWeights.__new__(GdnWeights)
+            gw.H, gw.S, gw.H_k, gw.H_v, gw.d_conv, gw.types = H, S, HK, HV, DC, types
+            gw.d_inner, gw.key_dim, gw.conv_ch = d_inner, key_dim, conv_ch
+            gw.w_qkv, gw.w_gate, gw.w_beta, gw.w_alpha, gw.w_out = (t.cpu().numpy().reshape(-1) for t in
+                                                                    (w_qkv, w_gate, w_beta, w_alpha, w_out))
+            gw.attn_norm, gw.ffn_norm, gw.ssm_norm, gw.dt_bias, gw.ssm_a = (t.cpu().numpy() for t in
+                                                                            (an, fn, sn, dtb, ssm_a))
+            gw.conv1d = conv1d.cpu().numpy()
+            csh, ssh = cs.cpu().numpy().copy(), ss.cpu().numpy().copy()
+            x = h1.cpu().numpy()
+            cpuinfo = host_cpu()
+            n_thr = max(1, min(cpuinfo["cores_per_socket"], cpuinfo["cpus_available"]))
+            ref = RefGGML(REF_SO_AVX512 if have_ref_avx512() else REF_SO)
+            ref.gdn_seg(gw, x, csh, ssh, n_threads=n_thr)
+            times, t_all = [], time.perf_counter()
+            while (time.perf_counter() - t_all < 10.0 or len(times) < 5) and len(times) < 5000:
+                t0 = time.perf_counter()
+                ref.gdn_seg(gw, x, csh, ssh, n_threads=n_thr)
+                times.append(time.perf_counter() - t0)
+            med = float(np.median(times))
+            cpu = {"value": round(1.0 / med, 1), "unit": "tok/s", "cores": n_thr, "kind": "reference",
+                   "sample": f"{len(times)} decode steps (T=1, states carried) of ggml's gated-delta-net graph in "
+                             f"{time.perf_counter() - t_all:.1f}s",
+                   "median_ms_per_step": round(med * 1e3, 4), "isa": "AVX-512" if ref.isa() == 512 else "AVX2",
+                   "threads": n_thr, "cpu": cpuinfo["model"]}
+    line = {
+        "metric": "gated-delta-net decode tok/s + achieved HBM GB/s, Seg A recurrent half (qwen3next / qwen35moe)",
+        "value": round(1.0 / dec_wall, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(dec_wall * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "q4_K/q6_K/q8_0 x q8_K/q8_0 -> f32; f32 states",
+        "data": "synthetic (seeded N(0,0.02) weights quantized on the GPU; N(0,1) inputs; states from zero)",
+        "config": {"workload": "gated-delta-net half of Seg A (qwmoe_gdn_seg)", "n_embd": H, "d_state": S,
+                   "n_group": HK, "dt_rank": HV, "d_conv": DC, "conv_ch": conv_ch,
+                   "types_qkv_gate_beta_alpha_out": ["Q4_K", "Q6_K", "Q8_0", "Q8_0", "Q4_K"]},
+        "roofline": {"bound": "hbm", "achieved": round(abytes / dec_ev / 1e9, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(abytes / dec_ev / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "qwmoe_gdn_seg at T=1 (the segment's kernels together)",
+                     "bytes_per_call": abytes, "weight_bytes": wbytes, "state_bytes": sbytes,
+                     "avg_call_ms": round(dec_ev * 1e3, 4)},
+        "prefill_chunk_512": {"ms": round(pre_wall * 1e3, 4), "avg_call_ms": round(pre_ev * 1e3, 4),
+                              "tok_s": round(512 / pre_wall, 1)},
+        "cpu_baseline": cpu,
+        "device_status": status,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -1069,12 +1194,12 @@ def main() -> int:
                     help="text file whose 'hbm_bytes_per_launch = N' line is the HBM traffic of one decode "
                          "launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (copy-calibrated)")
     ap.add_argument("--copy-probe", action="store_true", help="run only the copy-kernel calibration probe")
-    ap.add_argument("--workload", choices=["decode", "prefill", "expert_cache", "verify", "config5", "attn"],
+    ap.add_argument("--workload", choices=["decode", "prefill", "expert_cache", "verify", "config5", "attn", "gdn"],
                     default="decode",
                     help="decode: configs[1] (the headline line); prefill: configs[2]; expert_cache: configs[1] "
                          "decode with the experts offloaded to pinned host memory; verify: configs[1] stack on "
                          "T = 1..--tokens verify batches; config5: configs[4] decode and prefill; attn: the "
-                         "attention half of Seg A and a whole decoder layer at the 30B shape")
+                         "attention half of Seg A and a whole decoder layer at the 30B shape; gdn: the gated-delta-net half of Seg A")
     ap.add_argument("--resident", type=float, default=0.5, help="expert_cache: fraction of experts in HBM")
     ap.add_argument("--zipf", type=float, default=1.1, help="expert_cache: router skew (0: none)")
     ap.add_argument("--copy-engine", action="store_true",
@@ -1100,6 +1225,8 @@ def main() -> int:
         return verify_bench(args)
     if args.workload == "config5":
         return config5_bench(args)
+    if args.workload == "gdn":
+        return gdn_bench(args)
     if args.workload == "attn":
         return attn_bench(args)
 

@@ -726,8 +726,14 @@ int qwmoe_gdn_seg(void* stream, const qwmoe_gdn_layer* L, const float* h, int64_
     float* o = ar.take<float>((size_t) (d_inner * T));
     float* y = ar.take<float>((size_t) (d_inner * T));
     float* proj = ar.take<float>((size_t) (H * T));
+    // one bin per token for the H_v-row projections (beta, alpha)
+    int32_t* trows = ar.take<int32_t>((size_t) (2 * T));
+    int32_t* tactive = ar.take<int32_t>((size_t) T);
+    int32_t* toff = ar.take<int32_t>((size_t) (T + 1));
+    int32_t* tn = ar.take<int32_t>(1);
+    int32_t* tslot = ar.take<int32_t>((size_t) T);
     if (!rows || !active || !active_off || !n_active || !cur || !qkv || !z || !braw || !araw || !conv || !qn || !kn ||
-        !bg || !o || !y || !proj)
+        !bg || !o || !y || !proj || !trows || !tactive || !toff || !tn || !tslot)
         return QWMOE_ERR_WORKSPACE;
     // the input quantized once per vec_dot type the four input projections use
     int vt[4] = {qw::vec_dot_type(L->type_qkv), qw::vec_dot_type(L->type_gate), qw::vec_dot_type(L->type_beta),
@@ -745,6 +751,7 @@ int qwmoe_gdn_seg(void* stream, const qwmoe_gdn_layer* L, const float* h, int64_
     uint8_t* yq = ar.take<uint8_t>(ro * (size_t) T + 64);
     if (!yq) return QWMOE_ERR_WORKSPACE;
     if ((rc = qw::launch_group_dense(rows, active, active_off, n_active, T, st))) return rc;
+    if ((rc = qw::launch_gdn_group_tokens(trows, tactive, toff, tn, tslot, T, st))) return rc;
     const size_t hb = (size_t) H * 4;
     if ((rc = qw::launch_rms_norm(h, cur, H, T, rms_eps, st, L->attn_norm))) return rc;
     for (int i = 0; i < 4; ++i) {
@@ -762,8 +769,18 @@ int qwmoe_gdn_seg(void* stream, const qwmoe_gdn_layer* L, const float* h, int64_
     };
     if ((rc = proj_launch(L->type_qkv, L->w_qkv, L->w_qkv_nb1, H, conv_ch, xq[0], xr[0], qkv))) return rc;
     if ((rc = proj_launch(L->type_gate, L->w_gate, L->w_gate_nb1, H, d_inner, xq[1], xr[1], z))) return rc;
-    if ((rc = proj_launch(L->type_beta, L->w_beta, L->w_beta_nb1, H, Hv, xq[2], xr[2], braw))) return rc;
-    if ((rc = proj_launch(L->type_alpha, L->w_alpha, L->w_alpha_nb1, H, Hv, xq[3], xr[3], araw))) return rc;
+    {   // beta and alpha: a workgroup per token (and both in one launch when they share a type)
+        auto small = [&](int type, const void* w, size_t nb1, const uint8_t* xb, size_t xrow, float* dst) {
+            return mmid_args(type, w, H, Hv, 1, nb1, nb1 * (size_t) Hv, xb, 1, xrow, trows, tactive, toff, tn, T,
+                             tslot, T, dst, 0, (size_t) Hv * 4, 1, T);
+        };
+        const qw::MmidArgs mb = small(L->type_beta, L->w_beta, L->w_beta_nb1, xq[2], xr[2], braw);
+        const qw::MmidArgs ma = small(L->type_alpha, L->w_alpha, L->w_alpha_nb1, xq[3], xr[3], araw);
+        if (!(mb.type == ma.type && qw::launch_mmid_gemv2(mb, ma, st) == 0)) {
+            if ((rc = mmid_launch(mb, st))) return rc;
+            if ((rc = mmid_launch(ma, st))) return rc;
+        }
+    }
     qw::GdnArgs a{};
     a.T = (int) T;
     a.H_k = (int) Hk;

@@ -213,5 +213,9 @@ struct GdnArgs {
 // S = 128, H_v a multiple of H_k, 2 <= d_conv <= GDN_MAX_CONV
 bool gdn_shape_ok(int64_t S, int64_t H_k, int64_t H_v, int64_t d_conv);
 int launch_gdn_core(const GdnArgs& a, hipStream_t stream);
+// one bin per token (bin i = token i, slot rows all 0): rows[2 T], active[T],
+// active_off[T + 1], n_active[1], slot[T]
+int launch_gdn_group_tokens(int32_t* rows, int32_t* active, int32_t* active_off, int32_t* n_active, int32_t* slot,
+                            int64_t T, hipStream_t stream);
 
 }  // namespace qw
