@@ -925,6 +925,34 @@ def copy_probe(mib: int = 1024, reps: int = 4) -> int:
     return 0
 
 
+def graph_replay_ms(fn_, n: int):
+    """fn_ captured into one HIP graph (torch's stream capture: the library's
+    calls enqueue on the capturing stream and allocate nothing) and replayed n
+    times: (ms per replay, the captured call's outputs), or (None, None) when
+    capture fails."""
+    import torch
+    try:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn_()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            outs = fn_()
+        for _ in range(3):
+            g.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            g.replay()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n * 1e3, (g, outs)
+    except Exception:  # noqa: BLE001 -- capture is reported as unavailable
+        return None, None
+
+
 def attn_bench(args) -> int:
     """The attention half of Seg A (qwmoe_attn_seg, core/runtime.cpp:1976-2030) and
     a whole decoder layer (qwmoe_decoder_layer) at the Qwen3-30B-A3B attention
@@ -996,6 +1024,16 @@ def attn_bench(args) -> int:
     pre0_wall, pre0_ev = timed(lambda: ops.attn_seg(AL, hp, 0), max(4, args.steps // 16))
     pre1_wall, pre1_ev = timed(lambda: ops.attn_seg(AL, hp, N_CTX - 512), max(4, args.steps // 16))
     lay_wall, lay_ev = timed(lambda: ops.decoder_layer(AL, ML, h1, n_past), args.steps)
+    # the decode call captured into a HIP graph: the same kernels without the
+    # host's per-launch cost; the replay's outputs checked against an eager call
+    g_ms, g_hold = graph_replay_ms(lambda: ops.attn_seg(AL, h1, n_past), args.steps)
+    g_equal = None
+    if g_hold is not None:
+        g_hold[0].replay()
+        torch.cuda.synchronize()
+        e_out = ops.attn_seg(AL, h1, n_past)
+        torch.cuda.synchronize()
+        g_equal = bool(torch.equal(g_hold[1][0], e_out[0]) and torch.equal(g_hold[1][1], e_out[1]))
     status = ops.device_status(clear=True)
 
     wbytes = NQ * row_size(types[0], H) + NK * row_size(types[1], H) + NK * row_size(types[2], H) + \
@@ -1046,6 +1084,10 @@ def attn_bench(args) -> int:
                      "avg_call_ms": round(dec_ev * 1e3, 4)},
         "prefill_chunk_512": {"n_past_0_ms": round(pre0_wall * 1e3, 4), "n_past_3584_ms": round(pre1_wall * 1e3, 4),
                               "tok_s_at_n_past_3584": round(512 / pre1_wall, 1)},
+        "decode_hip_graph": {"ms_per_call": None if g_ms is None else round(g_ms, 4),
+                             "tok_s": None if g_ms is None else round(1e3 / g_ms, 1),
+                             "achieved_gbs": None if g_ms is None else round(abytes / g_ms / 1e6, 1),
+                             "replay_equals_eager_bitwise": g_equal},
         "decoder_layer_decode": {"ms": round(lay_wall * 1e3, 4), "avg_call_ms": round(lay_ev * 1e3, 4),
                                  "bytes_per_call": abytes + moe_bytes,
                                  "achieved_gbs": round((abytes + moe_bytes) / lay_ev / 1e9, 1)},
@@ -1122,6 +1164,21 @@ def gdn_bench(args) -> int:
     ops.randn_(hp, sd + 21, 0.0, 1.0)
     dec_wall, dec_ev = timed(lambda: ops.gdn_seg(GL, h1), args.steps)
     pre_wall, pre_ev = timed(lambda: ops.gdn_seg(GL, hp), max(4, args.steps // 16))
+    # the decode call captured into a HIP graph (the states advance on every
+    # replay, as on every eager call); one replay checked against an eager call
+    # from the same states
+    g_ms, g_hold = graph_replay_ms(lambda: ops.gdn_seg(GL, h1), args.steps)
+    g_equal = None
+    if g_hold is not None:
+        cs0, ss0 = cs.clone(), ss.clone()
+        g_hold[0].replay()
+        torch.cuda.synchronize()
+        r_out, r_cs, r_ss = g_hold[1][0].clone(), cs.clone(), ss.clone()
+        cs.copy_(cs0)
+        ss.copy_(ss0)
+        e_out = ops.gdn_seg(GL, h1)
+        torch.cuda.synchronize()
+        g_equal = bool(torch.equal(r_out, e_out[0]) and torch.equal(r_cs, cs) and torch.equal(r_ss, ss))
     status = ops.device_status(clear=True)
 
     wbytes = conv_ch * row_size(types[0], H) + d_inner * row_size(types[1], H) + HV * row_size(types[2], H) + \
@@ -1174,6 +1231,10 @@ def gdn_bench(args) -> int:
                      "avg_call_ms": round(dec_ev * 1e3, 4)},
         "prefill_chunk_512": {"ms": round(pre_wall * 1e3, 4), "avg_call_ms": round(pre_ev * 1e3, 4),
                               "tok_s": round(512 / pre_wall, 1)},
+        "decode_hip_graph": {"ms_per_call": None if g_ms is None else round(g_ms, 4),
+                             "tok_s": None if g_ms is None else round(1e3 / g_ms, 1),
+                             "achieved_gbs": None if g_ms is None else round(abytes / g_ms / 1e6, 1),
+                             "replay_equals_eager_bitwise": g_equal},
         "cpu_baseline": cpu,
         "device_status": status,
     }
