@@ -335,10 +335,12 @@ typedef struct qwmoe_attn_layer {
  * rounded to f16 before their products as ggml's f16 mul_mat does.  Outputs
  * agree with the reference CPU graph within the fp32 rounding of the sums
  * (1e-3), not bit for bit.  Requires D = n_rot = 128, n_head / n_head_kv <= 16,
- * n_past + T <= n_ctx, h 16-byte aligned.  The score rows live in the library
- * workspace (4 n_head T (n_past + T) bytes, plus ~40 T n_embd bytes of
- * projections): size qwmoe_init's workspace for the longest chunk, or call
- * with smaller T (QWMOE_ERR_WORKSPACE otherwise, nothing enqueued). */
+ * n_past + T <= n_ctx, h 16-byte aligned.  Workspace: ~40 T n_embd bytes of
+ * projections, plus, for batches of fewer than 64 query rows per kv head
+ * (T n_head / n_head_kv < 64: decode, verify), the score rows (4 n_head T
+ * (n_past + T) bytes); larger chunks keep only per-512-key softmax statistics
+ * and recompute the scores beside P.V (QWMOE_ERR_WORKSPACE when it does not
+ * fit, nothing enqueued). */
 int qwmoe_attn_seg(void * stream, const qwmoe_attn_layer * layer, const float * h, int64_t T, int64_t n_past,
                    float rms_eps, float * attn_resid, float * ffn_in);
 

@@ -597,13 +597,16 @@ int qwmoe_attn_seg(void* stream, const qwmoe_attn_layer* L, const float* h, int6
     float* k = ar.take<float>((size_t) (NK * T));
     float* v = ar.take<float>((size_t) (NK * T));
     float* qr = ar.take<float>((size_t) (NQ * T));
-    float* sc = ar.take<float>((size_t) (nq * T * n_kv));
-    float* part = ar.take<float>((size_t) (n_split * T * NQ));
+    // the score rows and P.V partials exist only on the split path (fewer than 64
+    // query rows per kv head); the matrix-core path recomputes scores beside P.V
+    const bool mf_path = T * (nq / nk) >= 64;
+    float* sc = mf_path ? nullptr : ar.take<float>((size_t) (nq * T * n_kv));
+    float* part = mf_path ? nullptr : ar.take<float>((size_t) (n_split * T * NQ));
     float* stat = ar.take<float>((size_t) (qw::attn_stat_blocks(T, nk, n_kv) * T * nq * 2));
     float* att = ar.take<float>((size_t) (NQ * T));
     float* proj = ar.take<float>((size_t) (H * T));
-    if (!rows || !active || !active_off || !n_active || !cur || !q || !k || !v || !qr || !sc || !part || !stat || !att ||
-        !proj)
+    if (!rows || !active || !active_off || !n_active || !cur || !q || !k || !v || !qr || (!mf_path && (!sc || !part)) ||
+        !stat || !att || !proj)
         return QWMOE_ERR_WORKSPACE;
     // quantized activations, one per vec_dot type in use
     const int vqt = qw::vec_dot_type(L->type_q), vkt = qw::vec_dot_type(L->type_k), vvt = qw::vec_dot_type(L->type_v);

@@ -318,10 +318,13 @@ __device__ __forceinline__ h4 f4_to_h4(float x0, float x1, float x2, float x3) {
     return h4{(_Float16) x0, (_Float16) x1, (_Float16) x2, (_Float16) x3};
 }
 
-// Scores: a workgroup takes 64 rows (a wave per 16, their Q in registers) and
-// MF_SK keys, 16 at a time: eight MFMAs over the 128 dims per 16-key tile, the
-// next tile's key rows loaded while the current one is multiplied.  B is read
-// straight from the cache rows (8 bytes per lane and dim step).
+// Softmax statistics of the scores: a workgroup takes 64 rows (a wave per 16,
+// their Q in registers) and MF_SK keys, 16 at a time: eight MFMAs over the 128
+// dims per 16-key tile, the next tile's key rows loaded while the current one is
+// multiplied (B straight from the cache rows, 8 bytes per lane and dim step).
+// Only each row's maximum and sum of exp(s - max) over its MF_SK keys are
+// written; k_attn_pv_mf forms the scores again beside P.V, so the score rows
+// (4 n_head T n_kv bytes) never reach memory.
 constexpr int MF_SK = ATT_MF_SK;   // keys per workgroup of k_attn_scores_mf
 __global__ void __launch_bounds__(256) k_attn_scores_mf(AttnArgs a) {
     const int g = blockIdx.y, tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, q = l >> 4;
@@ -371,7 +374,6 @@ __global__ void __launch_bounds__(256) k_attn_scores_mf(AttnArgs a) {
             if (r < rows && jb < kend) {
                 const int t = (int) (r / R), h = (int) (r % R);
                 const float sv = jb > a.n_past + t ? -INFINITY : acc[i] * a.kq_scale;
-                a.s[((int64_t) t * nq + g * R + h) * a.n_kv + jb] = sv;
                 if (sv > mrow[i]) {
                     lrow[i] = (mrow[i] == -INFINITY ? 0.0f : lrow[i] * __expf(mrow[i] - sv)) + 1.0f;
                     mrow[i] = sv;
@@ -414,6 +416,7 @@ __global__ void __launch_bounds__(256) k_attn_scores_mf(AttnArgs a) {
 constexpr int SVS = 64 + 4;   // padded key stride of the staged V chunk (halves)
 __global__ void __launch_bounds__(256) k_attn_pv_mf(AttnArgs a) {
     __shared__ __align__(16) _Float16 sv[AD][SVS];
+    __shared__ __align__(16) _Float16 skc[64][AD + 8];   // the chunk's key rows (16 bytes of pad per row)
     const int g = blockIdx.x, tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, q = l >> 4;
     const int nq = a.n_head, R = nq / a.n_head_kv, gqa = a.n_head_kv * AD;
     const int64_t rows = (int64_t) a.T * R, row0 = (int64_t) blockIdx.y * 64;
@@ -422,7 +425,21 @@ __global__ void __launch_bounds__(256) k_attn_pv_mf(AttnArgs a) {
     const int64_t ra = row0 + 16 * w + li;                                // this lane's A row
     const bool row_ok = ra < rows;
     const int64_t rid = row_ok ? (int64_t) (ra / R) * nq + g * R + ra % R : 0;
-    const float* prow = a.s + rid * a.n_kv;
+    const int64_t key_max = row_ok ? a.n_past + ra / R : -1;             // the row's last unmasked key
+    // the row's Q (f16, as ggml rounds it) as the B operand of S^T = K Q^T: lane
+    // (li, q) holds dims 4 q + 16 st .. +3 of row li, the layout of an A operand
+    h4 qb[8];
+    if (row_ok) {
+        const float* qrow = a.qr + rid * AD + 4 * q;
+#pragma unroll
+        for (int st = 0; st < 8; ++st) {
+            const float4 v = *(const float4*) (qrow + 16 * st);
+            qb[st] = f4_to_h4(v.x, v.y, v.z, v.w);
+        }
+    } else {
+#pragma unroll
+        for (int st = 0; st < 8; ++st) qb[st] = h4{0, 0, 0, 0};
+    }
     // the row's max M and sum S = sum_b exp(m_b - M) l_b over the 512-key blocks, then
     // p = f16(v_expf(s - M) * (float) (1 / S)): ggml's normalized probabilities
     const int nkb = (int) ((a.n_kv + MF_SK - 1) / MF_SK);
@@ -438,17 +455,22 @@ __global__ void __launch_bounds__(256) k_attn_pv_mf(AttnArgs a) {
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt) acc[nt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     const int sk = tid & 63, sdq = tid >> 6;   // staging: key sk of the chunk, dims 32 sdq .. +32
-    auto load_v = [&](int64_t c0, uint4 (&vv)[4]) __attribute__((always_inline)) {
+    auto load_kv = [&](int64_t c0, uint4 (&vv)[4], uint4 (&kk)[4]) __attribute__((always_inline)) {
         const int64_t kj = c0 + sk;
-        const uint4* vrow = (const uint4*) ((const _Float16*) a.vc + (kj < klim ? kj : 0) * gqa + g * AD + 32 * sdq);
+        const int64_t off = (kj < klim ? kj : 0) * gqa + g * AD + 32 * sdq;
+        const uint4* vrow = (const uint4*) ((const _Float16*) a.vc + off);
+        const uint4* krow = (const uint4*) ((const _Float16*) a.kc + off);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) vv[i] = kj < klim ? vrow[i] : uint4{0u, 0u, 0u, 0u};
+        for (int i = 0; i < 4; ++i) {
+            vv[i] = kj < klim ? vrow[i] : uint4{0u, 0u, 0u, 0u};
+            kk[i] = kj < klim ? krow[i] : uint4{0u, 0u, 0u, 0u};
+        }
     };
-    uint4 vv[4], vn[4];
-    load_v(0, vv);
+    uint4 vv[4], vn[4], kv4[4], kn4[4];
+    load_kv(0, vv, kv4);
     for (int64_t c0 = 0; c0 < klim; c0 += 64) {
-        if (c0 + 64 < klim) load_v(c0 + 64, vn);   // the next chunk's rows, in flight during this one
-        __syncthreads();   // the previous chunk's B reads are done
+        if (c0 + 64 < klim) load_kv(c0 + 64, vn, kn4);   // the next chunk's rows, in flight during this one
+        __syncthreads();   // the previous chunk's reads are done
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t w4[4] = {vv[i].x, vv[i].y, vv[i].z, vv[i].w};
@@ -458,15 +480,25 @@ __global__ void __launch_bounds__(256) k_attn_pv_mf(AttnArgs a) {
                 sv[d][sk] = __builtin_bit_cast(_Float16, (uint16_t) (w4[m] & 0xffffu));
                 sv[d + 1][sk] = __builtin_bit_cast(_Float16, (uint16_t) (w4[m] >> 16));
             }
+            *(uint4*) &skc[sk][32 * sdq + 8 * i] = kv4[i];
         }
         __syncthreads();
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) {
             const int64_t k4 = c0 + 16 * kt + 4 * q;   // this lane's four keys of the A operand
+            // S^T for keys c0 + 16 kt .. +15 and the wave's 16 rows: A = the key rows
+            // (lane (li, q): key li, dims 4 q + 16 st), B = Q; D lane (li, q) register m
+            // is the score of row li and key k4 + m, P.V's A layout
+            f4 sc = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int st = 0; st < 8; ++st) {
+                const h4 kb = *(const h4*) &skc[16 * kt + li][16 * st + 4 * q];   // zero rows past klim
+                sc = __builtin_amdgcn_mfma_f32_16x16x16f16(kb, qb[st], sc, 0, 0, 0);
+            }
             float p4[4];
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
-                const float sv = row_ok && k4 + m < klim ? prow[k4 + m] : -INFINITY;
+                const float sv = k4 + m <= key_max && k4 + m < klim ? sc[m] * a.kq_scale : -INFINITY;
                 p4[m] = sv == -INFINITY ? 0.0f : v_expf(sv - M) * inv;
             }
             const h4 pa = f4_to_h4(p4[0], p4[1], p4[2], p4[3]);
@@ -477,7 +509,10 @@ __global__ void __launch_bounds__(256) k_attn_pv_mf(AttnArgs a) {
             }
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) vv[i] = vn[i];
+        for (int i = 0; i < 4; ++i) {
+            vv[i] = vn[i];
+            kv4[i] = kn4[i];
+        }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
