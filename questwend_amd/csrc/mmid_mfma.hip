@@ -29,6 +29,8 @@
 // super-block.
 #include "qw_kernels.hpp"
 
+#include <type_traits>
+
 namespace qw {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -716,6 +718,351 @@ int launch_q8K_to_f16(const uint8_t* q, size_t row_bytes, int64_t K, int64_t row
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
+// ---- exact Q4_K on the f16 matrix cores, persistent -------------------------
+// k_mmid_mfma_q4k_hp computes what k_mmid_mfma_q4k_h computes -- the same A and
+// B operands, one v_mfma_f32_16x16x32_f16 per AVX lane and tile, the same fp32
+// steps in the same order, so the same bits -- with another schedule:
+//  - a grid of two workgroups per CU walks the work units u = b, b + grid, ...
+//    A unit is (item, 64-row weight tile) of one of the launch's one or two
+//    matrices; an item is up to 32 routed rows of one heavy expert.  Each
+//    workgroup builds the item table (first item of each active expert) once in
+//    LDS; a unit's expert is a count over that table.
+//  - the three-stage copy pipeline runs on across units: while the last
+//    super-blocks of a unit are computed, the first ones of the next unit are
+//    being copied.  The next unit's (e, t) pairs are copied into LDS by the same
+//    DMA path one super-block ahead, so they are counted by the same waits.
+//  - two 16-row activation tiles per item: each A operand (sc * q4 of 16 weight
+//    rows) serves 32 activation rows.  A last item of at most 16 rows computes
+//    one tile; those items are numbered after all others, so a workgroup runs
+//    its two-tile units, then its one-tile units, each as straight-line code
+//    (the tile count a compile-time constant: no branch between a matrix-core
+//    instruction and the reads of its result, and no register shuffling of the
+//    accumulators between two code paths at every super-block).
+//  - activation rows i and i + 16 share one DMA instruction and sit 1040 bytes
+//    per pair apart (16 bytes of pad): the 16 rows a tile reads at one chunk
+//    offset fall on distinct LDS banks, and every B read is the lane's base plus
+//    a constant.
+// ~81 KB of LDS: two workgroups per CU.  Needs K >= 768 (three super-blocks: the
+// next unit's pairs land one super-block before they are used) and at most
+// MP_MAXG active bins.  Measured at configs[2] (T = 512, Zipf-skewed routing):
+// gate + up 170 us, down 104 us per launch against 174 / 114 us for
+// k_mmid_mfma_q4k_h; counters put it at ~56 % VALU-busy and ~16 % MFMA-busy,
+// with waves waiting a third of their cycles (two waves per SIMD).
+constexpr int MP_NR = 32;             // activation rows per item (two 16-row tiles)
+constexpr uint32_t MP_HS = 1040;      // LDS bytes per activation DMA instruction (rows i, i + 16, pad)
+constexpr int MP_MAXG = 128;          // active bins the item table holds
+constexpr int MP_VM = 6;              // fewest DMA instructions a wave issues per stage (waves 1, 2: 2 + 4)
+
+struct MpUnit {
+    int z, ntok, ok, p0;
+    uint32_t r0;
+    i32x4 wrsrc;
+};
+
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+k_mmid_mfma_q4k_hp(MfLaunch lp, uint32_t nz) {
+    __shared__ __align__(16) uint8_t s_w[3][MF_M * MF_WS];
+    __shared__ __align__(16) uint8_t s_h[3][16 * MP_HS];
+    __shared__ __align__(16) float s_d[3][MP_NR];
+    __shared__ __align__(16) int32_t s_meta[2][2 * MP_NR];   // (e, t) of a unit's 32 rows
+    __shared__ int32_t s_if[MP_MAXG + 1], s_if1[MP_MAXG + 1], s_aoff[MP_MAXG + 1], s_mat[2][MP_MAXG];
+    const MmidArgs& m0 = lp.m[0];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    const int lr = lane & 15, gq = lane >> 4;
+    const int nb = (int) (m0.K / QK_K), tiles = (int) (m0.N / MF_M);
+
+    // ---- the item table.  An active bin's rows (at least mfma_min_rows) are cut
+    // into items of 32 rows; a last item of 17..31 rows counts with the full ones
+    // (two-tile items, s_if[g] = the bin's first), one of 1..16 rows is a one-tile
+    // item (s_if1[g] = its index among those).  Two-tile items come first.
+    int n = __builtin_amdgcn_readfirstlane(*(const volatile int32_t*) m0.n_active);
+    n = n < MP_MAXG ? n : MP_MAXG;   // (the host bounds max_active by MP_MAXG)
+    if (wave == 0) {
+        int run = 0, run1 = 0;
+        for (int base = 0; base <= n; base += 64) {
+            const int j = base + lane;
+            int ch = 0, c1 = 0;
+            if (j < n) {
+                const int cnt = m0.active_off[j + 1] - m0.active_off[j];
+                if (cnt >= m0.mfma_min_rows) {
+                    const int rem = cnt % MP_NR;
+                    ch = cnt / MP_NR + (rem > 16 ? 1 : 0);
+                    c1 = rem > 0 && rem <= 16 ? 1 : 0;
+                }
+            }
+            int incl = ch, incl1 = c1;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int v = __shfl_up(incl, o), v1 = __shfl_up(incl1, o);
+                if (lane >= o) {
+                    incl += v;
+                    incl1 += v1;
+                }
+            }
+            if (j <= n) {
+                s_if[j] = run + incl - ch;
+                s_if1[j] = run1 + incl1 - c1;
+                s_aoff[j] = m0.active_off[j];
+            }
+            run += __shfl(incl, 63);
+            run1 += __shfl(incl1, 63);
+        }
+    } else if (wave <= 2 && (uint32_t) (wave - 1) < nz) {
+        const MmidArgs& mz = lp.m[wave - 1];
+        for (int j = lane; j < n; j += 64) {
+            const int bin = mz.active[j];
+            int64_t mat = bin;
+            if (mz.slot_of) mat = bin < mz.n_slot_of ? mz.slot_of[bin] : -1;
+            s_mat[wave - 1][j] = (mat >= 0 && mat < mz.n_as) ? (int) mat : -1;
+        }
+    }
+    __syncthreads();
+    const int n2 = __builtin_amdgcn_readfirstlane(s_if[n]), n1 = __builtin_amdgcn_readfirstlane(s_if1[n]);
+    const int U2 = n2 * tiles * (int) nz, total = U2 + n1 * tiles * (int) nz;
+    const int P = (int) gridDim.x, b = (int) blockIdx.x;
+    const int my_units = total > b ? (total - b + P - 1) / P : 0;
+    if (my_units == 0) return;
+
+    const int64_t b_ne1 = m0.b_ne1;
+    const i32x4 hrsrc = rsrc_words(m0.act_h, 0x7fffffffu);
+    const i32x4 arsrc = rsrc_words(m0.act_q, 0x7fffffffu);
+    const i32x4 prsrc = rsrc_words(m0.rows, (uint32_t) (8 * m0.n_pairs));
+    // unit u: its matrix, rows and weight tile (uniform).  Units [0, U2) are the
+    // two-tile items' (matrix, item, tile), then the one-tile items'.  (Units
+    // dealt to the XCDs by item chunks, for L2 reuse, measured slower.)
+    auto decode = [&](int u) __attribute__((always_inline)) {
+        MpUnit r;
+        const bool one = u >= U2;
+        const int uc = one ? u - U2 : u, ni = one ? n1 : n2;
+        r.z = uc >= ni * tiles ? 1 : 0;
+        const int uu = uc - r.z * ni * tiles, item = uu / tiles, tile = uu - item * tiles;
+        const int32_t* tab = one ? s_if1 : s_if;
+        int g = 0;
+        for (int j0 = 1; j0 <= n; j0 += 64) {
+            const int j = j0 + lane;
+            g += __popcll(__ballot(j <= n && tab[j] <= item));
+        }
+        g = __builtin_amdgcn_readfirstlane(g);
+        const int a0 = s_aoff[g], a1 = s_aoff[g + 1];
+        r.p0 = __builtin_amdgcn_readfirstlane(one ? a0 + MP_NR * ((a1 - a0) / MP_NR) : a0 + MP_NR * (item - s_if[g]));
+        const int ntok = a1 - r.p0;
+        r.ntok = __builtin_amdgcn_readfirstlane(ntok < MP_NR ? ntok : MP_NR);
+        const int mat = __builtin_amdgcn_readfirstlane(s_mat[r.z][g]);
+        r.ok = mat >= 0;
+        r.r0 = (uint32_t) tile * MF_M;
+        const MmidArgs& mz = lp.m[r.z];
+        const uint8_t* wt = mz.w + (size_t) (mat >= 0 ? mat : 0) * mz.nb2 + (size_t) r.r0 * mz.nb1;
+        const i32x4 w4 = rsrc_words(wt, (uint32_t) (MF_M * mz.nb1));
+        r.wrsrc = i32x4{__builtin_amdgcn_readfirstlane(w4.x), __builtin_amdgcn_readfirstlane(w4.y),
+                        __builtin_amdgcn_readfirstlane(w4.z), __builtin_amdgcn_readfirstlane(w4.w)};
+        return r;
+    };
+    // this lane's copy offsets for a unit whose (e, t) pairs are in s_meta[mb]
+    uint32_t woff[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const int q = 64 * (wave + 4 * k) + lane;
+        const int qc = q < MF_M * 9 ? q : 0;
+        woff[k] = (uint32_t) (qc / 9) * (uint32_t) m0.nb1 + 16u * (uint32_t) (qc % 9);
+    }
+    auto arow = [&](int mb, int nn) __attribute__((always_inline)) {
+        const int e = s_meta[mb][2 * nn], t = s_meta[mb][2 * nn + 1];
+        const int64_t er = b_ne1 == 1 ? 0 : (int64_t) e % b_ne1;
+        return (uint32_t) (er + (int64_t) t * b_ne1);
+    };
+    auto lane_offs = [&](int mb, int ntok, uint32_t (&ho)[4], uint32_t& dof) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int nrow = wave + 4 * k + 16 * (lane >> 5);
+            ho[k] = arow(mb, nrow < ntok ? nrow : 0) * (uint32_t) (2 * m0.K) + 16u * (uint32_t) (lane & 31);
+        }
+        dof = arow(mb, lane < ntok && lane < MP_NR ? lane : 0) * (uint32_t) m0.act_row_bytes;
+    };
+    // copies of super-block i of a unit into stage buffer sb
+    auto issue = [&](int sb, const MpUnit& U, const uint32_t (&ho)[4], uint32_t dof, int i) __attribute__((always_inline)) {
+        uint32_t lw = (uint32_t) (uintptr_t) s_w[sb], lh = (uint32_t) (uintptr_t) s_h[sb];
+        uint32_t ld = (uint32_t) (uintptr_t) s_d[sb];
+        asm volatile("" : "+s"(lw), "+s"(lh), "+s"(ld));
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+            if (wv + 4 * k < 9) dma_b128(U.wrsrc, lw + 1024u * (uint32_t) (wv + 4 * k), woff[k], 144u * (uint32_t) i);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) dma_b128(hrsrc, lh + MP_HS * (uint32_t) (wv + 4 * k), ho[k], 512u * (uint32_t) i);
+        if (wv == 3 && lane < MP_NR) dma_b32(arsrc, ld, dof, 292u * (uint32_t) i);
+    };
+
+    float acc[2][4][8], accm[2][4][4];
+    auto zero = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+#pragma unroll
+                for (int L = 0; L < 8; ++L) acc[t][r][L] = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) accm[t][r][q] = 0.0f;
+            }
+    };
+    uint32_t hmag = 0x64006400u;
+    asm volatile("" : "+v"(hmag));
+    const int arow_l = 16 * wave + lr;
+    // NBT activation tiles (1 or 2, a compile-time constant): straight-line code
+    // from each matrix-core instruction to the reads of its result.  (With the tile
+    // count tested inside the unrolled loops, the compiler put its wait states for
+    // the matrix-core result only on the path that computes the second tile; the
+    // branch around it read the first tile's result too early.)
+    auto compute = [&](int sb, auto nbt_c) __attribute__((always_inline)) {
+        constexpr int NBT = decltype(nbt_c)::value;
+        const uint8_t* sw = s_w[sb];
+        const uint8_t* sh = s_h[sb] + MP_HS * (uint32_t) lr;   // this lane's rows: lr (tile 0), lr + 16 (tile 1)
+        const float* sd = s_d[sb];
+        // this lane's A row: the 6-bit scales and mins of the 8 sub-blocks (quants.c:2067-2072)
+        const u32x4m hdr = *(const u32x4m*) (sw + arow_l * MF_WS);
+        const uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;
+        const uint32_t sc_lo = s0 & 0x3f3f3f3fu;
+        const uint32_t sc_hi = (s2 & 0x0f0f0f0fu) | (((s0 >> 6) & 0x03030303u) << 4);
+        const uint32_t mn_lo = s1 & 0x3f3f3f3fu;
+        const uint32_t mn_hi = ((s2 >> 4) & 0x0f0f0f0fu) | (((s1 >> 6) & 0x03030303u) << 4);
+        const uint32_t scw = gq < 2 ? sc_lo : sc_hi;
+        const uint32_t sab = (scw >> (16 * (gq & 1))) & 0xffffu;
+        const h2m pa = h2_bits(__builtin_amdgcn_perm(0u, sab, 0x0c000c00u) | 0x64006400u) - h2m{1024, 1024};
+        const h2m pb = h2_bits(__builtin_amdgcn_perm(0u, sab, 0x0c010c01u) | 0x64006400u) - h2m{1024, 1024};
+        const h2m S_lo = pa, C_lo = pa * h2m{-1024, -1024};
+        const h2m S_hi = pb * h2m{0.0625, 0.0625}, C_hi = pb * h2m{-64, -64};
+        float xd[4], xdm[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t h0 = *(const uint32_t*) (sw + (16 * wave + 4 * gq + r) * MF_WS);
+            xd[r] = h2f((uint16_t) (h0 & 0xffff));
+            xdm[r] = h2f((uint16_t) (h0 >> 16));
+        }
+        float d[2][4], dmin[2][4];
+#pragma unroll
+        for (int t = 0; t < NBT; ++t) {
+            const float dy = sd[16 * t + lr];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                d[t][r] = dy * xd[r];
+                dmin[t][r] = -dy * xdm[r];
+            }
+        }
+#pragma unroll
+        for (int L = 0; L < 8; ++L) {
+            const uint32_t w = *(const uint32_t*) (sw + arow_l * MF_WS + 16 + 32 * gq + 4 * L);
+            const uint32_t v = w >> 8;
+            const h2m a0 = __builtin_elementwise_fma(h2_bits((w & 0x000F000Fu) | hmag), S_lo, C_lo);
+            const h2m a1 = __builtin_elementwise_fma(h2_bits((v & 0x000F000Fu) | hmag), S_lo, C_lo);
+            const h2m a2 = __builtin_elementwise_fma(h2_bits((w & 0x00F000F0u) | hmag), S_hi, C_hi);
+            const h2m a3 = __builtin_elementwise_fma(h2_bits((v & 0x00F000F0u) | hmag), S_hi, C_hi);
+            const h8m A = __builtin_bit_cast(h8m, u32x4m{h2_u32(a0), h2_u32(a1), h2_u32(a2), h2_u32(a3)});
+#pragma unroll
+            for (int t = 0; t < NBT; ++t) {
+                const h8m B = *(const h8m*) (sh + 512 * t + 16 * (8 * gq + L));
+                const f4m D = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, f4m{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[t][r][L] = __builtin_fmaf(d[t][r], D[r], acc[t][r][L]);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t mnw = q < 2 ? mn_lo : mn_hi;
+            const uint32_t b0 = (uint32_t) (2 * (q & 1)), b1 = b0 + 1;
+            const h2m mm0 = h2_bits(__builtin_amdgcn_perm(0u, mnw, 0x0c000c00u | b0 | (b0 << 16)) | 0x64006400u) -
+                            h2m{1024, 1024};
+            const h2m mm1 = h2_bits(__builtin_amdgcn_perm(0u, mnw, 0x0c000c00u | b1 | (b1 << 16)) | 0x64006400u) -
+                            h2m{1024, 1024};
+            const h8m Am = __builtin_bit_cast(h8m, u32x4m{h2_u32(mm0), h2_u32(mm0), h2_u32(mm1), h2_u32(mm1)});
+#pragma unroll
+            for (int t = 0; t < NBT; ++t) {
+                const h8m B0 = *(const h8m*) (sh + 512 * t + 16 * (8 * q + gq));
+                const h8m B1 = *(const h8m*) (sh + 512 * t + 16 * (8 * q + 4 + gq));
+                f4m Dm = __builtin_amdgcn_mfma_f32_16x16x32_f16(Am, B0, f4m{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                Dm = __builtin_amdgcn_mfma_f32_16x16x32_f16(Am, B1, Dm, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) accm[t][r][q] = __builtin_fmaf(dmin[t][r], Dm[r], accm[t][r][q]);
+            }
+        }
+    };
+    // hsum_float_8(acc) + ((m0 + m2) + (m1 + m3)) of a finished unit; weight rows
+    // r0 + 16 wave + 4 gq .. +3, activation rows lr and 16 + lr
+    auto finish = [&](const MpUnit& U, int mb, auto nbt_c) __attribute__((always_inline)) {
+        constexpr int NBT = decltype(nbt_c)::value;
+        const MmidArgs& mz = lp.m[U.z];
+        if (!U.ok) {
+            if (tid == 0 && mz.status) atomicOr(mz.status, 4);
+            return;
+        }
+#pragma unroll
+        for (int t = 0; t < NBT; ++t) {
+            const int row = 16 * t + lr;
+            float o[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float* a = acc[t][r];
+                const float hs = ((a[4] + a[0]) + (a[6] + a[2])) + ((a[5] + a[1]) + (a[7] + a[3]));
+                const float* mm = accm[t][r];
+                o[r] = hs + ((mm[0] + mm[2]) + (mm[1] + mm[3]));
+            }
+            if (row < U.ntok) {
+                const int e = s_meta[mb][2 * row], tt = s_meta[mb][2 * row + 1];
+                float* dp = (float*) ((char*) mz.dst + (size_t) e * mz.dst_nb1 + (size_t) tt * mz.dst_nb2) + U.r0 +
+                            16 * wave + 4 * gq;
+                *(float4*) dp = float4{o[0], o[1], o[2], o[3]};
+            }
+        }
+    };
+
+    // ---- prologue: the first unit's pairs, then its super-blocks 0 and 1
+    MpUnit cur = decode(b), nxt = cur;
+    if (wv == 0) dma_b32(prsrc, (uint32_t) (uintptr_t) s_meta[0], 4u * (uint32_t) lane, 8u * (uint32_t) cur.p0);
+    vm_wait<0>();
+    lds_barrier();
+    uint32_t ho[4], dof, hn[4], dn = 0;
+    lane_offs(0, cur.ntok, ho, dof);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) hn[k] = ho[k];
+    zero();
+    issue(0, cur, ho, dof, 0);
+    issue(1, cur, ho, dof, 1);
+    const int S = my_units * nb;
+    int i = 0, j = 0, sb = 0, s = 0;
+    // one step: super-block i of unit j.  The unit's tile count is a template
+    // argument: a workgroup meets its two-tile units first, then its one-tile ones.
+    auto step = [&](auto nbt_c) __attribute__((always_inline)) {
+        if (s + 1 < S) vm_wait<MP_VM>();   // super-block s + 1's copies may stay in flight
+        else vm_wait<0>();
+        lds_barrier();
+        const bool more = j + 1 < my_units;
+        if (i == 0 && more) {   // the next unit's pairs: copied before this step's super-block copies
+            nxt = decode(b + (j + 1) * P);
+            if (wv == 0)
+                dma_b32(prsrc, (uint32_t) (uintptr_t) s_meta[(j + 1) & 1], 4u * (uint32_t) lane, 8u * (uint32_t) nxt.p0);
+        }
+        if (i == 1 && more) lane_offs((j + 1) & 1, nxt.ntok, hn, dn);   // (landed: waited for above)
+        if (s + 2 < S) {
+            const int i2 = i + 2, sb2 = sb == 0 ? 2 : sb - 1;
+            if (i2 < nb) issue(sb2, cur, ho, dof, i2);
+            else issue(sb2, nxt, hn, dn, i2 - nb);
+        }
+        compute(sb, nbt_c);
+        if (++i == nb) {
+            finish(cur, j & 1, nbt_c);
+            zero();
+            cur = nxt;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) ho[k] = hn[k];
+            dof = dn;
+            i = 0;
+            ++j;
+        }
+        sb = sb == 2 ? 0 : sb + 1;
+        ++s;
+    };
+    while (s < S && cur.ntok > 16) step(std::integral_constant<int, 2>{});
+    while (s < S) step(std::integral_constant<int, 1>{});
+}
+
 
 // Q6_K x Q8_K on the matrix cores, block-sum form only: the down projections of
 // the layer entry points under QWMOE_MFMA_AUTO, every projection under
@@ -1204,9 +1551,50 @@ bool mmid_mfma_h_ok(const MmidArgs& m, int64_t n_rows) {
            (uint64_t) n_rows * (uint64_t) m.K * 2u + 512u < (1ull << 31);
 }
 
+// Whether the persistent f16 kernel takes the launch: the exact form with the f16
+// copy, at least three super-blocks per row, at most MP_MAXG active bins, and for
+// two matrices one grouping and one activation buffer.  QWMOE_MFMA_PERSIST=0 in
+// the environment keeps k_mmid_mfma_q4k_h (a test switch).
+static bool mp_ok(const MfLaunch& lp, int nz) {
+    const MmidArgs& a = lp.m[0];
+    if (a.type != T_Q4_K || !a.mfma_exact || !a.act_h || a.K < 3 * QK_K || a.max_active > MP_MAXG ||
+        a.n_pairs <= 0 || 8 * a.n_pairs >= (int64_t(1) << 31))
+        return false;
+    if (nz == 2) {
+        const MmidArgs& b = lp.m[1];
+        if (b.rows != a.rows || b.active != a.active || b.active_off != a.active_off || b.n_active != a.n_active ||
+            b.act_h != a.act_h || b.act_q != a.act_q || b.b_ne1 != a.b_ne1 || b.act_row_bytes != a.act_row_bytes ||
+            b.mfma_min_rows != a.mfma_min_rows || b.nb1 != a.nb1 || b.K != a.K || b.N != a.N)
+            return false;
+    }
+    const char* e = getenv("QWMOE_MFMA_PERSIST");
+    return !(e && e[0] == '0');
+}
+
+// Two workgroups per CU of the current device (cached per device).
+static unsigned mp_grid() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 512;
+    if (cus[dev] <= 0) {
+        int c = 0;
+        if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+        cus[dev] = c;
+    }
+    return 2u * (unsigned) cus[dev];
+}
+
 static int launch_mf(const MfLaunch& lp, int nz, hipStream_t stream) {
     const MmidArgs& m = lp.m[0];
     if (lp.groups == 0) return 0;
+    if (mp_ok(lp, nz)) {
+        // at most (items of 32 rows) x tiles x nz units: no more workgroups than that
+        const int64_t units = mf_max_items(m, MP_NR) * (m.N / MF_M) * nz;
+        const unsigned grid = (unsigned) std::min<int64_t>(units, (int64_t) mp_grid());
+        if (grid == 0) return 0;
+        hipLaunchKernelGGL(k_mmid_mfma_q4k_hp, dim3(grid), dim3(256), 0, stream, lp, (uint32_t) nz);
+        return hipGetLastError() == hipSuccess ? 0 : -3;
+    }
     const unsigned grid = lp.groups * (unsigned) nz;
     const bool q6x = m.type == T_Q6_K && m.mfma_exact, q6b = m.type == T_Q6_K && !m.mfma_exact;
     if (q6b) hipLaunchKernelGGL(k_mmid_mfma_q6k, dim3(grid), dim3(256), 0, stream, lp);

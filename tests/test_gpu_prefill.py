@@ -172,17 +172,21 @@ def full_range_q4k(rng, rows: int, K: int) -> np.ndarray:
     return blk.reshape(-1)
 
 
-@pytest.mark.parametrize("kernel", ["f16", "int8"])
+@pytest.mark.parametrize("kernel", ["f16p", "f16", "int8"])
 @pytest.mark.parametrize("K,N,ne11,min_rows", [(2048, 128, 1, 1), (768, 256, 2, 8), (4096, 64, 1, 16)])
 def test_mfma_exact_full_range_bit_exact(orc, K, N, ne11, min_rows, kernel, monkeypatch):
-    """The exact Q4_K form on either matrix-core kernel -- the f16 one (one
+    """The exact Q4_K form on each matrix-core kernel -- the persistent f16 one
+    (the default: 32-row items, two 16-row tiles per weight operand), the f16 one
+    with a workgroup per (16-row item, tile) (QWMOE_MFMA_PERSIST=0; both: one
     v_mfma_f32_16x16x32_f16 per AVX lane on sc * q4 and an f16 copy of the Q8_K
     quants) or, with QWMOE_MFMA_F16=0, the int8 one -- over blocks of random bytes
     and activations whose Q8_K rows reach -128 and 127: bit-identical to ggml's
-    AVX2 order (the oracle).  Items of 16 rows with a partial last one (70 tokens
-    on expert 0)."""
+    AVX2 order (the oracle).  Expert 0 holds 70 tokens (items of 32 rows: 32, 32,
+    6, the last with one tile; items of 16: a partial last one), experts 1-4 17
+    or 18 (a second tile of one or two rows)."""
     note(f"exact Q4_K matrix cores, full-range blocks: kernel={kernel} K={K} N={N} ne11={ne11} min_rows={min_rows}")
-    monkeypatch.setenv("QWMOE_MFMA_F16", "1" if kernel == "f16" else "0")
+    monkeypatch.setenv("QWMOE_MFMA_F16", "0" if kernel == "int8" else "1")
+    monkeypatch.setenv("QWMOE_MFMA_PERSIST", "1" if kernel == "f16p" else "0")
     rng = np.random.default_rng(3 * K + N)
     n_as, T = 5, 70
     w = full_range_q4k(rng, n_as * N, K)
