@@ -15,11 +15,15 @@
 //     written to LDS; lanes (row, AVX lane) then run the fp32 chains over the
 //     blocks in order and one lane per row the hsum tree (quants.c: q4_K
 //     2038-2115, q6_K 2426-2508);
-//   - the router logits cross XCDs: workgroup j < E/8 of XCD c computes logit
-//     8 j + c from its router row in LDS, so the E rows are read once per
-//     layer instead of once per XCD.
-// The exchanges are decode_xcd.hip's tagged words: logits (now across XCDs),
-// act inside the XCD, down outputs across XCDs, y inside the XCD.  Ids,
+//   - every XCD computes all E router logits, as decode_xcd.hip does:
+//     workgroup j computes logits 4 j .. 4 j + 3 (waves 6 and 7, 32 lanes per
+//     logit) from its router rows in LDS, kept in the block-integer buffer,
+//     which is idle from the down phase to the next layer's gate/up phase.
+//     (Each router row read once per device, its logit exchanged across XCDs,
+//     measured slower: the logit gather then waits for the slowest of 128
+//     workgroups chip-wide plus a cross-XCD hop.)
+// The exchanges are decode_xcd.hip's tagged words: logits and act inside the
+// XCD, down outputs across XCDs, y inside the XCD.  Ids,
 // weights and outputs are bit-identical to the reference CPU path.
 #include "qw_xcd.hpp"
 #include "qw_bp_block.hpp"
@@ -48,21 +52,20 @@ __global__ void __launch_bounds__(XT) k_decode_xcd_wide(XcdArgs a) {
     constexpr int NPD = BpType<TD>::NPW, NCD = BpType<TD>::NCH;
     constexpr int PART = UG * NPG > UD * NPD ? UG * NPG : UD * NPD;
     constexpr int CHN = NR * NCG > NH * NCD ? NR * NCG : NH * NCD;
-    constexpr int NLW = E / NXCD;                 // workgroups per XCD that compute a logit
     static_assert(UG % XT == 0 && NP % 4 == 0, "gate/up blocks: whole per lane, gate or up uniform per wave");
     static_assert((UD % XT) % 64 == 0, "down blocks: the last round covers whole waves");
     static_assert(NR <= XT && NH <= 128, "rows per workgroup");
-    static_assert(E <= 128 && E % NXCD == 0 && NLW <= NJ, "logits: one per workgroup, two per lane in the softmax");
+    static_assert(E == 4 * NJ && PART >= 4 * H, "logits: four per workgroup (rows in s_part), two per lane in the softmax");
     static_assert(NBF <= XW, "Q8_K of act: one wave per block");
     static_assert(NBH * 16 <= 4 * 64 && H % (2 * XT) == 0, "Q8_K of x: four waves; router row: two 16-byte loads per lane");
     static_assert(TD == T_Q6_K || TD == T_Q4_K, "down type");
 
     __shared__ __align__(16) float s_y[H];                  // y of the last layer (x = y * sc)
-    __shared__ __align__(16) float s_rw[H];                 // this workgroup's router row (the next layer's)
     __shared__ __align__(16) uint32_t s_xq[NBH * BP_ABLK / 4];   // Q8_K(x): block b at 304 b + 12
     __shared__ __align__(16) float s_act[F];
     __shared__ __align__(16) uint32_t s_aq[NBF * BP_ABLK / 4];   // Q8_K(act), same layout
-    __shared__ __align__(16) uint32_t s_part[PART];         // per-block integers and scales
+    __shared__ __align__(16) uint32_t s_part[PART];         // per-block integers and scales; from the y exchange
+                                                            // to the router chains, router rows 4 j .. 4 j + 3
     __shared__ __align__(16) float s_ch[CHN];               // per-(row, chain) fp32 sums
     __shared__ __align__(16) float s_g[NR];                 // gate / up outputs
     __shared__ __align__(16) float s_p[E];                  // logits
@@ -85,21 +88,20 @@ __global__ void __launch_bounds__(XT) k_decode_xcd_wide(XcdArgs a) {
     const int k = a.k;
     const bool expert_xcd = xcd < k;
     const int local = a.local_st;
-    const bool has_logit = j < NLW;
-    const int e_mine = has_logit ? NXCD * j + xcd : 0;
+    float* const s_rw = (float*) s_part;   // router rows 4 j .. 4 j + 3 of the next layer
 
-    // The end of a layer (and the prologue): this workgroup's logit of the next
-    // layer from x = y * sc (wave 7, lanes 0..31 = the 32 chains) and Q8_K(x)
-    // (waves 4..6 and 0, sixteen lanes per block).
+    // The end of a layer (and the prologue): this workgroup's four logits of the
+    // next layer from x = y * sc (waves 6 and 7: lanes 32 h .. 32 h + 31 = the 32
+    // chains of logit 4 j + 2 (wave - 6) + h), stored inside the XCD, and Q8_K(x)
+    // (waves 0, 1, 4, 5, sixteen lanes per block).
     auto next_x = [&](int tid, float sc, uint32_t ep_next) {
         const int wave = tid >> 6, lane = tid & 63;
-        if (wave == XW - 1 && lane < 32 && has_logit) {
-            const float lg = router_chain_lds<H>(s_rw, s_y, sc, lane);
-            // (logit words double-buffered by layer parity: with k < 8 an XCD without
-            // an expert may still be reading layer l's while layer l + 1's are written)
-            if (lane == 0) st_cross(a.xl + ((ep_next - a.epoch0) & 1) * E + e_mine, tag(lg, ep_next));
+        if (wave >= XW - 2) {
+            const int li = 2 * (wave - (XW - 2)) + (lane >> 5);
+            const float lg = router_chain_lds<H>(s_rw + H * li, s_y, sc, lane & 31);
+            if ((lane & 31) == 0) st_local(a.xl + xcd * E + 4 * j + li, tag(lg, ep_next), local);
         }
-        const int tt = wave >= 4 && wave < XW - 1 ? tid - 256 : wave == 0 ? tid + 192 : -1;
+        const int tt = wave < 2 ? tid : wave == 4 || wave == 5 ? tid - 128 : -1;
         if (tt >= 0) quant_q8K_r16<12, 4, 0>(s_y, sc, NBH, (uint8_t*) s_xq, tt);
     };
 
@@ -110,8 +112,7 @@ __global__ void __launch_bounds__(XT) k_decode_xcd_wide(XcdArgs a) {
     for (int i = tid0; i < H; i += XT) s_y[i] = a.x_in[i];   // layer 0 takes x_in as it is (sc = 1)
     {
         const DecodeLayer& L0 = a.layers[0];
-        if (has_logit)
-            for (int i = tid0; i < H; i += XT) s_rw[i] = L0.router[(size_t) e_mine * H + i];
+        for (int i = tid0; i < 4 * H; i += XT) s_rw[i] = L0.router[(size_t) 4 * j * H + i];
         for (int i = tid0; i < 3 * E; i += XT) {
             const int32_t* so = i < E ? L0.slot_gate : i < 2 * E ? L0.slot_up : L0.slot_down;
             ((int32_t*) &s_slotx[0][i % E])[i / E] = so ? ldg32(so + i % E) : i % E;
@@ -148,8 +149,8 @@ __global__ void __launch_bounds__(XT) k_decode_xcd_wide(XcdArgs a) {
             og[m] = (uint32_t) (NP * j + (gup[m] ? r - NP : r)) * (gup[m] ? unb1 : gnb1) + 144u * (uint32_t) bb;
         }
 
-        // ---- L: the layer's E logits (words across XCDs) ---------------------------
-        if (tid < E && !gather<1>(a, a.xl + (l & 1) * E, E, ep, s_p, tid, XW_LOGITS)) s_fail = 1;
+        // ---- L: the layer's E logits (this XCD's words) ----------------------------
+        if (tid < E && !gather<1>(a, a.xl + xcd * E, E, ep, s_p, tid, XW_LOGITS)) s_fail = 1;
         lds_barrier();
         if (s_fail) return;
         // resident-only routing: workgroup 0 records the top k of the raw logits,
@@ -500,12 +501,16 @@ __global__ void __launch_bounds__(XT) k_decode_xcd_wide(XcdArgs a) {
             }
             weights();
         }
-        // the next layer's router row, into registers (stored to LDS after the y exchange)
-        u32x4 rwv[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};
-        if (nxt && has_logit) {
-            const float* src = L1.router + (size_t) e_mine * H;
+        // the next layer's router rows 4 j .. 4 j + 3, into registers (stored to LDS
+        // after the y exchange)
+        u32x4 rwv[8];
+        if (nxt) {
+            const float* src = L1.router + (size_t) 4 * j * H;
 #pragma unroll
-            for (int i = 0; i < 2; ++i) rwv[i] = ldg16(src + 4 * (tid + XT * i));
+            for (int i = 0; i < 8; ++i) rwv[i] = ldg16(src + 4 * (tid + XT * i));
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) rwv[i] = u32x4{0u, 0u, 0u, 0u};
         }
         lds_barrier();   // s_selw posted by wave 0
 
@@ -590,9 +595,9 @@ __global__ void __launch_bounds__(XT) k_decode_xcd_wide(XcdArgs a) {
             for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
             if (lane == 0) s_red[wave] = s;
             if (!ok) s_fail = 1;
-            if (nxt && has_logit) {
+            if (nxt) {
 #pragma unroll
-                for (int i = 0; i < 2; ++i) *(u32x4*) (s_rw + 4 * (tid + XT * i)) = rwv[i];
+                for (int i = 0; i < 8; ++i) *(u32x4*) (s_rw + 4 * (tid + XT * i)) = rwv[i];
             }
         }
         lds_barrier();
