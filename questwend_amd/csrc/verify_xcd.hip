@@ -396,28 +396,31 @@ __global__ void __launch_bounds__(XT) k_verify_xcd(VerifyArgs a) {
                 wave_lds_sync();   // the records are read before the next token's are written
             }
         };
-        // The current slot's rows and the next slot's (in flight) are two register
-        // sets; after a slot the next set is copied into the current one.  Each set is
-        // defined on both arms of its condition (a set left undefined on one arm is
-        // carried around the loops by the compiler, and spills).
+        // Two register sets, A for even slots and B for odd ones (the loop unrolled by
+        // two): slot s + 2's rows are issued into the set slot s used as soon as slot s
+        // is computed, while slot s + 1's are still in flight, so two slots' rows are
+        // in flight at a time.  (Copying the next slot's set into the current one after
+        // each slot waited for the next slot's loads before the one after could be
+        // issued: one slot in flight.)  Each set is defined on both arms of its
+        // condition (a set left undefined on one arm is carried around the loops by the
+        // compiler, and spills).
         auto zero_gu = [&](u32x4 (&gh)[2 * PPW], u32x4 (&gq)[2 * PPW]) {
 #pragma unroll
             for (int r = 0; r < 2 * PPW; ++r) gh[r] = gq[r] = u32x4{0u, 0u, 0u, 0u};
         };
         if (nslot > 0) {
-            u32x4 ghc[2 * PPW], gqc[2 * PPW], ghn[2 * PPW], gqn[2 * PPW];
-            issue_gu(0, ghc, gqc);
-            if (nslot > 1) issue_gu(1, ghn, gqn);
-            else zero_gu(ghn, gqn);
-            for (int s = 0; s < nslot; ++s) {
-                compute_gu(s, ghc, gqc);
-#pragma unroll
-                for (int r = 0; r < 2 * PPW; ++r) {
-                    ghc[r] = ghn[r];
-                    gqc[r] = gqn[r];
-                }
-                if (s + 2 < nslot) issue_gu(s + 2, ghn, gqn);
-                else zero_gu(ghn, gqn);
+            u32x4 ghA[2 * PPW], gqA[2 * PPW], ghB[2 * PPW], gqB[2 * PPW];
+            issue_gu(0, ghA, gqA);
+            if (nslot > 1) issue_gu(1, ghB, gqB);
+            else zero_gu(ghB, gqB);
+            for (int s = 0; s < nslot; s += 2) {
+                compute_gu(s, ghA, gqA);
+                if (s + 2 < nslot) issue_gu(s + 2, ghA, gqA);
+                else zero_gu(ghA, gqA);
+                if (s + 1 >= nslot) break;
+                compute_gu(s + 1, ghB, gqB);
+                if (s + 3 < nslot) issue_gu(s + 3, ghB, gqB);
+                else zero_gu(ghB, gqB);
             }
         }
 
