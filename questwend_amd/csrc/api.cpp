@@ -140,6 +140,18 @@ int mfma_f16_prep(Arena& ar, qw::MmidArgs& m, int64_t n_rows, hipStream_t st) {
     return 0;
 }
 
+// The same copy, written by the launch that quantizes the rows (the returned
+// buffer goes to launch_quantize_act / launch_swiglu_q8K as h_out): reserved
+// and attached to m, nothing launched; null where the f16 form does not apply.
+uint16_t* mfma_f16_reserve(Arena& ar, qw::MmidArgs& m, int64_t n_rows) {
+    if (!qw::mmid_mfma_h_ok(m, n_rows)) return nullptr;
+    const char* env = getenv("QWMOE_MFMA_F16");
+    if (env && env[0] == '0') return nullptr;
+    uint16_t* h = ar.take<uint16_t>((size_t) (n_rows * m.K));
+    m.act_h = h;
+    return h;
+}
+
 // Gate and up reading one activation buffer share its f16 copy.
 int mfma_f16_prep_pair(Arena& ar, qw::MmidArgs& mu, qw::MmidArgs& mg, int64_t n_rows, hipStream_t st) {
     if (int rc = mfma_f16_prep(ar, mu, n_rows, st)) return rc;
@@ -909,8 +921,6 @@ int qwmoe_ffn_layer(void* stream, const qwmoe_layer* L, const float* x, int64_t 
         if ((rc = qw::launch_router(ra, logits, st))) return rc;
         if ((rc = group(st, ar, ids, k, T, (size_t) k * 4, E, nullptr, nullptr, nullptr, G))) return rc;
     }
-    if (!xq_fused && (rc = qw::launch_quantize_act(vg, x, H, 1, T, (size_t) H * 4, (size_t) H * 4, xg, st))) return rc;
-    if (xu != xg && (rc = qw::launch_quantize_act(vu, x, H, 1, T, (size_t) H * 4, (size_t) H * 4, xu, st))) return rc;
     const size_t dnb1 = (size_t) F * 4, dnb2 = (size_t) F * 4 * (size_t) k;
     qw::MmidArgs mu = mmid_args(L->type_up, L->up, H, F, L->n_slots_up, L->up_nb1, L->up_nb2, xu, 1, qu, G.rows,
                                       G.active, G.active_off, G.n_active, G.max_active, L->slot_up,
@@ -918,7 +928,21 @@ int qwmoe_ffn_layer(void* stream, const qwmoe_layer* L, const float* x, int64_t 
     qw::MmidArgs mg = mmid_args(L->type_gate, L->gate, H, F, L->n_slots_gate, L->gate_nb1, L->gate_nb2, xg, 1, qg,
                                       G.rows, G.active, G.active_off, G.n_active, G.max_active, L->slot_gate,
                                       L->slot_gate ? E : 0, gateo, dnb1, dnb2, T, k * T);
-    if ((rc = mfma_f16_prep_pair(ar, mu, mg, T, st))) return rc;
+    // x's f16 copy for the exact matrix-core form, written by the quantizing launch
+    // (gate and up share it when they read one buffer)
+    uint16_t* hx = nullptr;
+    if (!xq_fused && xu == xg && vg == qw::T_Q8_K) {
+        hx = mfma_f16_reserve(ar, mu, T);
+        if (hx && qw::mmid_mfma_h_ok(mg, T)) mg.act_h = hx;
+        else if (hx) {
+            mu.act_h = nullptr;
+            hx = nullptr;
+        }
+    }
+    if (!xq_fused && (rc = qw::launch_quantize_act(vg, x, H, 1, T, (size_t) H * 4, (size_t) H * 4, xg, st, hx)))
+        return rc;
+    if (xu != xg && (rc = qw::launch_quantize_act(vu, x, H, 1, T, (size_t) H * 4, (size_t) H * 4, xu, st))) return rc;
+    if (!hx && (rc = mfma_f16_prep_pair(ar, mu, mg, T, st))) return rc;
     if ((rc = mmid_launch_pair(mu, mg, st))) return rc;   // gate and up in one launch each
     const int vd = qw::vec_dot_type(L->type_down);
     const size_t qd = qwmoe_row_size(vd, F);
@@ -931,9 +955,10 @@ int qwmoe_ffn_layer(void* stream, const qwmoe_layer* L, const float* x, int64_t 
     md.swiglu_up = upo;
     if (vd == qw::T_Q8_K && qw::mmid_gemv_swiglu_ok(md)) {
         // small bins: the down GEMV forms SwiGLU's Q8_K rows itself
-    } else if (vd == qw::T_Q8_K) {   // SwiGLU straight into Q8_K
+    } else if (vd == qw::T_Q8_K) {   // SwiGLU straight into Q8_K (and the f16 copy the matrix cores read)
         md.swiglu_gate = md.swiglu_up = nullptr;
-        if ((rc = qw::launch_swiglu_q8K(gateo, upo, F, k * T, aq, st))) return rc;
+        uint16_t* ha = mfma_f16_reserve(ar, md, k * T);
+        if ((rc = qw::launch_swiglu_q8K(gateo, upo, F, k * T, aq, st, ha))) return rc;
     } else {
         md.swiglu_gate = md.swiglu_up = nullptr;
         if ((rc = qw::launch_swiglu(gateo, upo, act, k * T, F, (size_t) F * 4, (size_t) F * 4, (size_t) F * 4, st)))
@@ -941,7 +966,7 @@ int qwmoe_ffn_layer(void* stream, const qwmoe_layer* L, const float* x, int64_t 
         if ((rc = qw::launch_quantize_act(vd, act, F, k, k * T, (size_t) F * 4, (size_t) F * 4 * (size_t) k, aq, st)))
             return rc;
     }
-    if (!md.swiglu_gate && (rc = mfma_f16_prep(ar, md, k * T, st))) return rc;
+    if (!md.swiglu_gate && !md.act_h && (rc = mfma_f16_prep(ar, md, k * T, st))) return rc;
     if ((rc = mmid_launch(md, st))) return rc;
     if (rms_eps >= 0.0f && H <= 16384) {
         if ((rc = qw::launch_weighted_sum_rms(ex, w, out, x_next, H, k, T, rms_eps, st))) return rc;

@@ -18,7 +18,7 @@ namespace qw {
 // src rows may be strided (ggml nb1/nb2 in bytes); dst rows are dense.
 __global__ void __launch_bounds__(256) k_quant_q8K(const float* __restrict__ src, int64_t K, int64_t ne1,
                                                    int64_t nrows, size_t nb1, size_t nb2,
-                                                   BlockQ8_K* __restrict__ dst) {
+                                                   BlockQ8_K* __restrict__ dst, _Float16* __restrict__ hout) {
     const int lane = threadIdx.x & 63;
     const int64_t nb = K / QK_K;
     const int64_t blk = (int64_t) blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
@@ -28,7 +28,7 @@ __global__ void __launch_bounds__(256) k_quant_q8K(const float* __restrict__ src
     const float* x = (const float*) ((const char*) src + i1 * nb1 + i2 * nb2) + ib * QK_K;
     const float4 q = *(const float4*) (x + 4 * lane);
     const float v[4] = {q.x, q.y, q.z, q.w};
-    quant_q8K_wave(v, lane, dst + blk);
+    quant_q8K_wave(v, lane, dst + blk, hout ? hout + (size_t) blk * QK_K : nullptr);
 }
 
 // SwiGLU (ggml_swiglu_split: silu(gate) * up, ops.cpp:3182-3238) of n_rows dense
@@ -36,7 +36,8 @@ __global__ void __launch_bounds__(256) k_quant_q8K(const float* __restrict__ src
 // one wave per 256-value block, the same values and quantizer as k_swiglu then
 // k_quant_q8K, without the fp32 round trip.
 __global__ void __launch_bounds__(256) k_swiglu_q8K(const float* __restrict__ gate, const float* __restrict__ up,
-                                                    int64_t F, int64_t n_rows, BlockQ8_K* __restrict__ dst) {
+                                                    int64_t F, int64_t n_rows, BlockQ8_K* __restrict__ dst,
+                                                    _Float16* __restrict__ hout) {
     const int lane = threadIdx.x & 63;
     const int64_t nb = F / QK_K;
     const int64_t blk = (int64_t) blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
@@ -45,15 +46,16 @@ __global__ void __launch_bounds__(256) k_swiglu_q8K(const float* __restrict__ ga
     const float4 g = *(const float4*) (gate + off);
     const float4 u = *(const float4*) (up + off);
     const float v[4] = {v_silu(g.x) * u.x, v_silu(g.y) * u.y, v_silu(g.z) * u.z, v_silu(g.w) * u.w};
-    quant_q8K_wave(v, lane, dst + blk);
+    quant_q8K_wave(v, lane, dst + blk, hout ? hout + (size_t) blk * QK_K : nullptr);
 }
 
-int launch_swiglu_q8K(const float* gate, const float* up, int64_t F, int64_t n_rows, void* dst, hipStream_t stream) {
+int launch_swiglu_q8K(const float* gate, const float* up, int64_t F, int64_t n_rows, void* dst, hipStream_t stream,
+                      uint16_t* h_out) {
     if (F % QK_K) return -2;
     const int64_t nblk = (F / QK_K) * n_rows;
     if (nblk == 0) return 0;
     hipLaunchKernelGGL(k_swiglu_q8K, dim3((unsigned) ((nblk + 3) / 4)), dim3(256), 0, stream, gate, up, F, n_rows,
-                       (BlockQ8_K*) dst);
+                       (BlockQ8_K*) dst, (_Float16*) h_out);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
@@ -91,12 +93,13 @@ __global__ void __launch_bounds__(256) k_quant_q8_0_act(const float* __restrict_
 }
 
 int launch_quantize_act(int vdt, const float* src, int64_t K, int64_t ne1, int64_t nrows, size_t nb1, size_t nb2,
-                        void* dst, hipStream_t stream) {
+                        void* dst, hipStream_t stream, uint16_t* h_out) {
+    if (h_out && vdt != T_Q8_K) return -2;
     if (vdt == T_Q8_K) {
         const int64_t nblk = (K / QK_K) * nrows;
         if (nblk == 0) return 0;
         hipLaunchKernelGGL(k_quant_q8K, dim3((unsigned) ((nblk + 3) / 4)), dim3(256), 0, stream, src, K, ne1, nrows,
-                           nb1, nb2, (BlockQ8_K*) dst);
+                           nb1, nb2, (BlockQ8_K*) dst, (_Float16*) h_out);
     } else if (vdt == T_Q8_0) {
         const int64_t nthr = (K / QK8_0) * nrows * 8;
         if (nthr == 0) return 0;

@@ -145,8 +145,16 @@ __device__ __forceinline__ T ld_unaligned(const void* p) {
 }
 
 // quantize_row_q8_K_ref of one block held by a wave, 4 values per lane
-// (values 4*lane .. 4*lane+3).
-__device__ __forceinline__ void quant_q8K_wave(const float* v, int lane, BlockQ8_K* y) {
+// (values 4*lane .. 4*lane+3).  With h set (the block's 256 slots of an f16 copy
+// in the exact Q4_K matrix-core form's layout: 16-byte chunk 8 g + L holds the
+// quants of elements 64 g + 4 L + {0, 2, 1, 3} and 64 g + 32 + 4 L + {0, 2, 1, 3})
+// each lane also writes its four quants there as f16 (exact).
+__device__ __forceinline__ void q8K_h_store(_Float16* h, int lane, int q0, int q1, int q2, int q3) {
+    typedef _Float16 h4v __attribute__((ext_vector_type(4)));
+    const int c = 8 * (lane >> 4) + (lane & 7), half = (lane >> 3) & 1;
+    *(h4v*) (h + 8 * c + 4 * half) = h4v{(_Float16) q0, (_Float16) q2, (_Float16) q1, (_Float16) q3};
+}
+__device__ __forceinline__ void quant_q8K_wave(const float* v, int lane, BlockQ8_K* y, _Float16* h = nullptr) {
     // first index of the largest |x|: reduce (|x|, -index) lexicographically
     float am = 0.0f;
     int ai = 0x7fffffff;
@@ -163,6 +171,7 @@ __device__ __forceinline__ void quant_q8K_wave(const float* v, int lane, BlockQ8
         *(int*) &y->qs[4 * lane] = 0;
         if (lane < 16) y->bsums[lane] = 0;
         if (lane == 0) y->d = 0.0f;
+        if (h) q8K_h_store(h, lane, 0, 0, 0, 0);
         return;
     }
     // the signed value at that index, from the lane that holds it
@@ -184,6 +193,7 @@ __device__ __forceinline__ void quant_q8K_wave(const float* v, int lane, BlockQ8
     s += __shfl_xor(s, 2);
     if ((lane & 3) == 0) y->bsums[lane >> 2] = (int16_t) s;
     if (lane == 0) y->d = 1.0f / iscale;
+    if (h) q8K_h_store(h, lane, qv[0], qv[1], qv[2], qv[3]);
 }
 
 }  // namespace qw

@@ -8,8 +8,10 @@
 namespace qw {
 
 // quantize.hip
+// h_out (optional, Q8_K only): the f16 copy the exact Q4_K matrix-core form reads
+// (launch_q8K_to_f16's layout), written by the same launch
 int launch_quantize_act(int vdt, const float* src, int64_t K, int64_t ne1, int64_t nrows, size_t nb1, size_t nb2,
-                        void* dst, hipStream_t stream);
+                        void* dst, hipStream_t stream, uint16_t* h_out = nullptr);
 int launch_quantize_weights(int type, const float* src, int64_t n, void* dst, hipStream_t stream);
 int launch_dequantize(int type, const void* x, float* y, int64_t n, hipStream_t stream);
 int launch_randn(float* y, int64_t n, uint64_t seed, float mean, float stddev, hipStream_t stream);
@@ -126,7 +128,10 @@ int launch_shared_gate_add(const float* x, size_t x_stride, const float* gate_in
 int launch_weighted_sum_rms(const float* experts, const float* weights, float* out, float* x_next, int64_t H,
                             int64_t k, int64_t T, float eps, hipStream_t stream);
 // k_swiglu then k_quant_q8K of its output, in one launch (F % 256 == 0; rows dense)
-int launch_swiglu_q8K(const float* gate, const float* up, int64_t F, int64_t n_rows, void* dst, hipStream_t stream);
+// h_out (optional): the f16 copy of the Q8_K rows the exact Q4_K matrix-core form
+// reads (launch_q8K_to_f16's layout), written by the same launch
+int launch_swiglu_q8K(const float* gate, const float* up, int64_t F, int64_t n_rows, void* dst, hipStream_t stream,
+                      uint16_t* h_out = nullptr);
 
 // Static device scratch of the allocation-free entry point (scratch.hip):
 // kScratchBytes per GPU.  scratch_setup(device), with that device current,
