@@ -947,6 +947,10 @@ k_mmid_mfma_q4k_hp(MfLaunch lp, uint32_t nz) {
                 dmin[t][r] = -dy * xdm[r];
             }
         }
+        // software-pipelined over the AVX lanes: lane L's matrix-core products are
+        // issued before lane L - 1's fp32 steps, so each result is read an
+        // iteration after its instruction (the same operations per accumulator)
+        f4m Dp[NBT];
 #pragma unroll
         for (int L = 0; L < 8; ++L) {
             const uint32_t w = *(const uint32_t*) (sw + arow_l * MF_WS + 16 + 32 * gq + 4 * L);
@@ -956,14 +960,25 @@ k_mmid_mfma_q4k_hp(MfLaunch lp, uint32_t nz) {
             const h2m a2 = __builtin_elementwise_fma(h2_bits((w & 0x00F000F0u) | hmag), S_hi, C_hi);
             const h2m a3 = __builtin_elementwise_fma(h2_bits((v & 0x00F000F0u) | hmag), S_hi, C_hi);
             const h8m A = __builtin_bit_cast(h8m, u32x4m{h2_u32(a0), h2_u32(a1), h2_u32(a2), h2_u32(a3)});
+            f4m Dc[NBT];
 #pragma unroll
             for (int t = 0; t < NBT; ++t) {
                 const h8m B = *(const h8m*) (sh + 512 * t + 16 * (8 * gq + L));
-                const f4m D = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, f4m{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) acc[t][r][L] = __builtin_fmaf(d[t][r], D[r], acc[t][r][L]);
+                Dc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, f4m{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
             }
+            if (L > 0) {
+#pragma unroll
+                for (int t = 0; t < NBT; ++t)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[t][r][L - 1] = __builtin_fmaf(d[t][r], Dp[t][r], acc[t][r][L - 1]);
+            }
+#pragma unroll
+            for (int t = 0; t < NBT; ++t) Dp[t] = Dc[t];
         }
+#pragma unroll
+        for (int t = 0; t < NBT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[t][r][7] = __builtin_fmaf(d[t][r], Dp[t][r], acc[t][r][7]);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const uint32_t mnw = q < 2 ? mn_lo : mn_hi;
@@ -973,16 +988,28 @@ k_mmid_mfma_q4k_hp(MfLaunch lp, uint32_t nz) {
             const h2m mm1 = h2_bits(__builtin_amdgcn_perm(0u, mnw, 0x0c000c00u | b1 | (b1 << 16)) | 0x64006400u) -
                             h2m{1024, 1024};
             const h8m Am = __builtin_bit_cast(h8m, u32x4m{h2_u32(mm0), h2_u32(mm0), h2_u32(mm1), h2_u32(mm1)});
+            f4m Dc[NBT];
 #pragma unroll
             for (int t = 0; t < NBT; ++t) {
                 const h8m B0 = *(const h8m*) (sh + 512 * t + 16 * (8 * q + gq));
                 const h8m B1 = *(const h8m*) (sh + 512 * t + 16 * (8 * q + 4 + gq));
-                f4m Dm = __builtin_amdgcn_mfma_f32_16x16x32_f16(Am, B0, f4m{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-                Dm = __builtin_amdgcn_mfma_f32_16x16x32_f16(Am, B1, Dm, 0, 0, 0);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) accm[t][r][q] = __builtin_fmaf(dmin[t][r], Dm[r], accm[t][r][q]);
+                Dc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Am, B0, f4m{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                Dc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Am, B1, Dc[t], 0, 0, 0);
             }
+            if (q > 0) {   // (min lane q - 1's fp32 steps, pipelined as above)
+#pragma unroll
+                for (int t = 0; t < NBT; ++t)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        accm[t][r][q - 1] = __builtin_fmaf(dmin[t][r], Dp[t][r], accm[t][r][q - 1]);
+            }
+#pragma unroll
+            for (int t = 0; t < NBT; ++t) Dp[t] = Dc[t];
         }
+#pragma unroll
+        for (int t = 0; t < NBT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) accm[t][r][3] = __builtin_fmaf(dmin[t][r], Dp[t][r], accm[t][r][3]);
     };
     // hsum_float_8(acc) + ((m0 + m2) + (m1 + m3)) of a finished unit; weight rows
     // r0 + 16 wave + 4 gq .. +3, activation rows lr and 16 + lr
