@@ -950,10 +950,18 @@ k_mmid_mfma_q4k_hp(MfLaunch lp, uint32_t nz) {
         // software-pipelined over the AVX lanes: lane L's matrix-core products are
         // issued before lane L - 1's fp32 steps, so each result is read an
         // iteration after its instruction (the same operations per accumulator)
+        // (the B operands are read from LDS one step ahead of their products)
         f4m Dp[NBT];
+        h8m Bc[NBT];
+#pragma unroll
+        for (int t = 0; t < NBT; ++t) Bc[t] = *(const h8m*) (sh + 512 * t + 16 * (8 * gq));
 #pragma unroll
         for (int L = 0; L < 8; ++L) {
             const uint32_t w = *(const uint32_t*) (sw + arow_l * MF_WS + 16 + 32 * gq + 4 * L);
+            h8m Bn[NBT];
+#pragma unroll
+            for (int t = 0; t < NBT; ++t)
+                Bn[t] = *(const h8m*) (sh + 512 * t + 16 * (L < 7 ? 8 * gq + L + 1 : gq));
             const uint32_t v = w >> 8;
             const h2m a0 = __builtin_elementwise_fma(h2_bits((w & 0x000F000Fu) | hmag), S_lo, C_lo);
             const h2m a1 = __builtin_elementwise_fma(h2_bits((v & 0x000F000Fu) | hmag), S_lo, C_lo);
@@ -962,10 +970,8 @@ k_mmid_mfma_q4k_hp(MfLaunch lp, uint32_t nz) {
             const h8m A = __builtin_bit_cast(h8m, u32x4m{h2_u32(a0), h2_u32(a1), h2_u32(a2), h2_u32(a3)});
             f4m Dc[NBT];
 #pragma unroll
-            for (int t = 0; t < NBT; ++t) {
-                const h8m B = *(const h8m*) (sh + 512 * t + 16 * (8 * gq + L));
-                Dc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, f4m{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-            }
+            for (int t = 0; t < NBT; ++t)
+                Dc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bc[t], f4m{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
             if (L > 0) {
 #pragma unroll
                 for (int t = 0; t < NBT; ++t)
@@ -973,7 +979,10 @@ k_mmid_mfma_q4k_hp(MfLaunch lp, uint32_t nz) {
                     for (int r = 0; r < 4; ++r) acc[t][r][L - 1] = __builtin_fmaf(d[t][r], Dp[t][r], acc[t][r][L - 1]);
             }
 #pragma unroll
-            for (int t = 0; t < NBT; ++t) Dp[t] = Dc[t];
+            for (int t = 0; t < NBT; ++t) {
+                Dp[t] = Dc[t];
+                Bc[t] = Bn[t];   // (after lane 7: min lane 0's first operand, chunk gq)
+            }
         }
 #pragma unroll
         for (int t = 0; t < NBT; ++t)
@@ -988,13 +997,19 @@ k_mmid_mfma_q4k_hp(MfLaunch lp, uint32_t nz) {
             const h2m mm1 = h2_bits(__builtin_amdgcn_perm(0u, mnw, 0x0c000c00u | b1 | (b1 << 16)) | 0x64006400u) -
                             h2m{1024, 1024};
             const h8m Am = __builtin_bit_cast(h8m, u32x4m{h2_u32(mm0), h2_u32(mm0), h2_u32(mm1), h2_u32(mm1)});
+            // Bc holds chunk 8 q + gq of each tile (read a step ahead); chunk 8 q + 4 + gq
+            // is read here, and the next min lane's first chunk for the step after
+            h8m B1[NBT], Bn[NBT];
+#pragma unroll
+            for (int t = 0; t < NBT; ++t) {
+                B1[t] = *(const h8m*) (sh + 512 * t + 16 * (8 * q + 4 + gq));
+                Bn[t] = *(const h8m*) (sh + 512 * t + 16 * (q < 3 ? 8 * (q + 1) + gq : gq));
+            }
             f4m Dc[NBT];
 #pragma unroll
             for (int t = 0; t < NBT; ++t) {
-                const h8m B0 = *(const h8m*) (sh + 512 * t + 16 * (8 * q + gq));
-                const h8m B1 = *(const h8m*) (sh + 512 * t + 16 * (8 * q + 4 + gq));
-                Dc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Am, B0, f4m{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-                Dc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Am, B1, Dc[t], 0, 0, 0);
+                Dc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Am, Bc[t], f4m{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                Dc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Am, B1[t], Dc[t], 0, 0, 0);
             }
             if (q > 0) {   // (min lane q - 1's fp32 steps, pipelined as above)
 #pragma unroll
@@ -1004,7 +1019,10 @@ k_mmid_mfma_q4k_hp(MfLaunch lp, uint32_t nz) {
                         accm[t][r][q - 1] = __builtin_fmaf(dmin[t][r], Dp[t][r], accm[t][r][q - 1]);
             }
 #pragma unroll
-            for (int t = 0; t < NBT; ++t) Dp[t] = Dc[t];
+            for (int t = 0; t < NBT; ++t) {
+                Dp[t] = Dc[t];
+                Bc[t] = Bn[t];
+            }
         }
 #pragma unroll
         for (int t = 0; t < NBT; ++t)
