@@ -917,9 +917,19 @@ k_mmid_mfma_q4k_hp(MfLaunch lp, uint32_t nz) {
         const uint8_t* sw = s_w[sb];
         const uint8_t* sh = s_h[sb] + MP_HS * (uint32_t) lr;   // this lane's rows: lr (tile 0), lr + 16 (tile 1)
         const float* sd = s_d[sb];
-        // this lane's A row: the 6-bit scales and mins of the 8 sub-blocks (quants.c:2067-2072)
+        // this lane's A row: the 6-bit scales and mins of the 8 sub-blocks (quants.c:2067-2072);
+        // the fp16 d / dmin of the four rows of its D registers; the activation rows' d.
+        // All read before any is used (one LDS wait: the empty asm takes them all).
+        uint32_t hx0 = *(const uint32_t*) (sw + (16 * wave + 4 * gq + 0) * MF_WS);
+        uint32_t hx1 = *(const uint32_t*) (sw + (16 * wave + 4 * gq + 1) * MF_WS);
+        uint32_t hx2 = *(const uint32_t*) (sw + (16 * wave + 4 * gq + 2) * MF_WS);
+        uint32_t hx3 = *(const uint32_t*) (sw + (16 * wave + 4 * gq + 3) * MF_WS);
+        float dy0 = sd[lr], dy1 = NBT > 1 ? sd[16 + lr] : 0.0f;
         const u32x4m hdr = *(const u32x4m*) (sw + arow_l * MF_WS);
-        const uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;
+        uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w, sx = hdr.x;
+        asm volatile("" : "+v"(sx), "+v"(s0), "+v"(s1), "+v"(s2), "+v"(hx0), "+v"(hx1), "+v"(hx2), "+v"(hx3), "+v"(dy0),
+                     "+v"(dy1));
+        const uint32_t hxr[4] = {hx0, hx1, hx2, hx3};
         const uint32_t sc_lo = s0 & 0x3f3f3f3fu;
         const uint32_t sc_hi = (s2 & 0x0f0f0f0fu) | (((s0 >> 6) & 0x03030303u) << 4);
         const uint32_t mn_lo = s1 & 0x3f3f3f3fu;
@@ -933,14 +943,13 @@ k_mmid_mfma_q4k_hp(MfLaunch lp, uint32_t nz) {
         float xd[4], xdm[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const uint32_t h0 = *(const uint32_t*) (sw + (16 * wave + 4 * gq + r) * MF_WS);
-            xd[r] = h2f((uint16_t) (h0 & 0xffff));
-            xdm[r] = h2f((uint16_t) (h0 >> 16));
+            xd[r] = h2f((uint16_t) (hxr[r] & 0xffff));
+            xdm[r] = h2f((uint16_t) (hxr[r] >> 16));
         }
         float d[2][4], dmin[2][4];
 #pragma unroll
         for (int t = 0; t < NBT; ++t) {
-            const float dy = sd[16 * t + lr];
+            const float dy = t == 0 ? dy0 : dy1;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 d[t][r] = dy * xd[r];
