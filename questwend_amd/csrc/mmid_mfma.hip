@@ -927,8 +927,12 @@ k_mmid_mfma_q4k_hp(MfLaunch lp, uint32_t nz) {
         float dy0 = sd[lr], dy1 = NBT > 1 ? sd[16 + lr] : 0.0f;
         const u32x4m hdr = *(const u32x4m*) (sw + arow_l * MF_WS);
         uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w, sx = hdr.x;
+        // and the 8 quant words of its 32-byte group gq (one per AVX lane)
+        u32x4m wq0 = *(const u32x4m*) (sw + arow_l * MF_WS + 16 + 32 * gq);
+        u32x4m wq1 = *(const u32x4m*) (sw + arow_l * MF_WS + 32 + 32 * gq);
         asm volatile("" : "+v"(sx), "+v"(s0), "+v"(s1), "+v"(s2), "+v"(hx0), "+v"(hx1), "+v"(hx2), "+v"(hx3), "+v"(dy0),
-                     "+v"(dy1));
+                     "+v"(dy1), "+v"(wq0), "+v"(wq1));
+        const uint32_t wl[8] = {wq0.x, wq0.y, wq0.z, wq0.w, wq1.x, wq1.y, wq1.z, wq1.w};
         const uint32_t hxr[4] = {hx0, hx1, hx2, hx3};
         const uint32_t sc_lo = s0 & 0x3f3f3f3fu;
         const uint32_t sc_hi = (s2 & 0x0f0f0f0fu) | (((s0 >> 6) & 0x03030303u) << 4);
@@ -966,11 +970,12 @@ k_mmid_mfma_q4k_hp(MfLaunch lp, uint32_t nz) {
         for (int t = 0; t < NBT; ++t) Bc[t] = *(const h8m*) (sh + 512 * t + 16 * (8 * gq));
 #pragma unroll
         for (int L = 0; L < 8; ++L) {
-            const uint32_t w = *(const uint32_t*) (sw + arow_l * MF_WS + 16 + 32 * gq + 4 * L);
+            const uint32_t w = wl[L];
             h8m Bn[NBT];
 #pragma unroll
             for (int t = 0; t < NBT; ++t)
                 Bn[t] = *(const h8m*) (sh + 512 * t + 16 * (L < 7 ? 8 * gq + L + 1 : gq));
+            __builtin_amdgcn_sched_barrier(0);   // (keeps those reads issued here, a step ahead)
             const uint32_t v = w >> 8;
             const h2m a0 = __builtin_elementwise_fma(h2_bits((w & 0x000F000Fu) | hmag), S_lo, C_lo);
             const h2m a1 = __builtin_elementwise_fma(h2_bits((v & 0x000F000Fu) | hmag), S_lo, C_lo);
@@ -1014,6 +1019,7 @@ k_mmid_mfma_q4k_hp(MfLaunch lp, uint32_t nz) {
                 B1[t] = *(const h8m*) (sh + 512 * t + 16 * (8 * q + 4 + gq));
                 Bn[t] = *(const h8m*) (sh + 512 * t + 16 * (q < 3 ? 8 * (q + 1) + gq : gq));
             }
+            __builtin_amdgcn_sched_barrier(0);
             f4m Dc[NBT];
 #pragma unroll
             for (int t = 0; t < NBT; ++t) {
