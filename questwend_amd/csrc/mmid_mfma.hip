@@ -867,9 +867,12 @@ k_mmid_mfma_q4k_hp(MfLaunch lp, uint32_t nz) {
         woff[k] = (uint32_t) (qc / 9) * (uint32_t) m0.nb1 + 16u * (uint32_t) (qc % 9);
     }
     auto arow = [&](int mb, int nn) __attribute__((always_inline)) {
-        const int e = s_meta[mb][2 * nn], t = s_meta[mb][2 * nn + 1];
-        const int64_t er = b_ne1 == 1 ? 0 : (int64_t) e % b_ne1;
-        return (uint32_t) (er + (int64_t) t * b_ne1);
+        // (32-bit: slot e >= 0 and 1 <= b_ne1 <= 65535 -- mp_ok -- give e % b_ne1 without
+        // the 64-bit division's ~130 instructions per call)
+        const uint32_t e = (uint32_t) s_meta[mb][2 * nn], t = (uint32_t) s_meta[mb][2 * nn + 1];
+        const uint32_t bn = (uint32_t) b_ne1;
+        const uint32_t er = bn == 1u ? 0u : e < bn ? e : e % bn;
+        return er + t * bn;
     };
     auto lane_offs = [&](int mb, int ntok, uint32_t (&ho)[4], uint32_t& dof) __attribute__((always_inline)) {
 #pragma unroll
@@ -1618,7 +1621,7 @@ bool mmid_mfma_h_ok(const MmidArgs& m, int64_t n_rows) {
 static bool mp_ok(const MfLaunch& lp, int nz) {
     const MmidArgs& a = lp.m[0];
     if (a.type != T_Q4_K || !a.mfma_exact || !a.act_h || a.K < 3 * QK_K || a.max_active > MP_MAXG ||
-        a.n_pairs <= 0 || 8 * a.n_pairs >= (int64_t(1) << 31))
+        a.n_pairs <= 0 || 8 * a.n_pairs >= (int64_t(1) << 31) || a.b_ne1 < 1 || a.b_ne1 > 65535)
         return false;
     if (nz == 2) {
         const MmidArgs& b = lp.m[1];
