@@ -181,6 +181,120 @@ __global__ void __launch_bounds__(256) k_router_logits_tile(const float* __restr
         }
 }
 
+// The same logits for large batches through LDS (H % 512 == 0, E % 16 == 0):
+// a workgroup computes 16 experts x 16 tokens.  256-element chunks of the 16
+// router rows and 16 token rows are copied with 16-byte loads (loaded into
+// registers two chunks ahead of their use) into LDS, where lane c of a
+// 32-lane group reads element 32 u + c of its 4 experts and 8 tokens for step u
+// (consecutive words: no bank conflicts) and runs chain c of those 32 logits in
+// step order.  The chains then go to LDS, and thread l forms logit l with the
+// GGML_F32x8_REDUCE tree of k_router_logits: ((c + c16) + (c8 + c24)) ... as
+// (v3_0 + v3_1) + (v3_2 + v3_3).  Same bits as k_router_logits_tile.
+constexpr int RL_CH = 256;
+__global__ void __launch_bounds__(256) k_router_logits_lds(const float* __restrict__ W, const float* __restrict__ x,
+                                                           int64_t x_stride, int64_t H, int64_t E, int64_t T,
+                                                           float* __restrict__ logits) {
+    __shared__ __align__(16) float s_buf[2][2][16][RL_CH];   // [stage][W, x][row][element]: 64 KB
+    const int tid = threadIdx.x, c = tid & 31, g = tid >> 5;
+    const int64_t e0 = (int64_t) blockIdx.x * 16, t0 = (int64_t) blockIdx.y * 16;
+    const int eg = 4 * (g & 3), tg = 8 * (g >> 2);
+    // copy slots: float4 f = tid + 256 k of each 16 x 256 tile, row f / 64, column 4 (f % 64)
+    const int crow = tid >> 6, ccol = 4 * (tid & 63);
+    const float* wsrc = W + (e0 + crow) * H + ccol;   // rows crow + 4 k: + 4 k H
+    int64_t xoff[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int64_t t = t0 + crow + 4 * k;
+        xoff[k] = (t < T ? t : T - 1) * x_stride + ccol;
+    }
+    const int64_t nch = H / RL_CH;   // (even)
+    // chunk n's copies into registers: set A holds the next chunk to store, set B
+    // is loaded two chunks ahead of its use (the loop is unrolled by two so the
+    // sets swap roles without a register copy of a load in flight)
+    // (named registers, not arrays: an array here is moved to LDS by the compiler)
+    float4 aw0, aw1, aw2, aw3, ax0, ax1, ax2, ax3, bw0, bw1, bw2, bw3, bx0, bx1, bx2, bx3;
+#define RL_FETCH1(rw, rx, k, nn)                                                       \
+    rw = *(const float4*) (wsrc + 4 * (k) * H + (nn) * RL_CH);                          \
+    rx = *(const float4*) (x + xoff[k] + (nn) * RL_CH);
+#define RL_FETCH(p, n)                                                                 \
+    {                                                                                  \
+        const int64_t nn = (n) < nch ? (n) : nch - 1;                                  \
+        RL_FETCH1(p##w0, p##x0, 0, nn) RL_FETCH1(p##w1, p##x1, 1, nn)                  \
+        RL_FETCH1(p##w2, p##x2, 2, nn) RL_FETCH1(p##w3, p##x3, 3, nn)                  \
+    }
+#define RL_PUT1(rw, rx, k, sb)                                                         \
+    *(float4*) &s_buf[sb][0][crow + 4 * (k)][ccol] = rw;                                \
+    *(float4*) &s_buf[sb][1][crow + 4 * (k)][ccol] = rx;
+#define RL_PUT(p, sb)                                                                  \
+    {                                                                                  \
+        RL_PUT1(p##w0, p##x0, 0, sb) RL_PUT1(p##w1, p##x1, 1, sb)                      \
+        RL_PUT1(p##w2, p##x2, 2, sb) RL_PUT1(p##w3, p##x3, 3, sb)                      \
+    }
+    float acc[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = 0.0f;
+    // one chunk: step u + 1's operands are read before step u's fmas (kept there by
+    // the scheduling barrier), so the LDS latency hides under the fmas
+    auto chunk = [&](int sb) __attribute__((always_inline)) {
+        float wv[2][4], xv[2][8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) wv[0][i] = s_buf[sb][0][eg + i][c];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xv[0][j] = s_buf[sb][1][tg + j][c];
+#pragma unroll
+        for (int u = 0; u < RL_CH / 32; ++u) {
+            const int cu = u & 1, nu = cu ^ 1;
+            if (u + 1 < RL_CH / 32) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) wv[nu][i] = s_buf[sb][0][eg + i][32 * (u + 1) + c];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) xv[nu][j] = s_buf[sb][1][tg + j][32 * (u + 1) + c];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[i][j] = __builtin_fmaf(wv[cu][i], xv[cu][j], acc[i][j]);
+        }
+    };
+    RL_FETCH(a, 0)
+    RL_PUT(a, 0)
+    RL_FETCH(a, 1)
+    __syncthreads();
+    // (past the last chunk the copies repeat it into a stage nobody reads)
+    for (int64_t ch = 0; ch < nch; ch += 2) {
+        RL_FETCH(b, ch + 2)
+        chunk(0);
+        RL_PUT(a, 1)   // chunk ch + 1; stage 1 was last read before the previous barrier
+        __syncthreads();
+        RL_FETCH(a, ch + 3)
+        chunk(1);
+        RL_PUT(b, 0)   // chunk ch + 2
+        __syncthreads();
+    }
+#undef RL_FETCH1
+#undef RL_FETCH
+#undef RL_PUT1
+#undef RL_PUT
+    // chains to LDS: logit l = 16 (token) + expert, 33 words per logit
+    float* red = &s_buf[0][0][0][0];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) red[((tg + j) * 16 + eg + i) * 33 + c] = acc[i][j];
+    __syncthreads();
+    const float* a = red + tid * 33;
+    float v2[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) v2[q] = (a[q] + a[q + 16]) + (a[q + 8] + a[q + 24]);
+    const float v3_0 = v2[0] + v2[4], v3_1 = v2[1] + v2[5], v3_2 = v2[2] + v2[6], v3_3 = v2[3] + v2[7];
+    const float sumf = (v3_0 + v3_1) + (v3_2 + v3_3);
+    const int64_t t = t0 + (tid >> 4), e = e0 + (tid & 15);
+    if (t < T) logits[t * E + e] = sumf;
+}
+
 // Softmax, exact top-k and weight normalisation for one token per 64-thread
 // workgroup.  Supports E % 8 == 0 and E <= 64 * ROUTER_EPL.
 constexpr int ROUTER_EPL = 8;
@@ -208,6 +322,10 @@ int launch_router(const RouterArgs& a, float* logits_ws, hipStream_t stream) {
         dim3 g1((unsigned) ((a.E + 1) / 2 + nq), (unsigned) a.T);
         hipLaunchKernelGGL((k_router_logits<1, 2, 32>), g1, dim3(64), 0, stream, a.W, a.x, a.x_stride, a.H, a.E, a.T,
                            logits, (BlockQ8_K*) a.xq);
+    } else if (a.H % (2 * RL_CH) == 0 && a.E % 16 == 0 && a.x_stride % 4 == 0 && ((uintptr_t) a.x & 15) == 0 &&
+               ((uintptr_t) a.W & 15) == 0) {
+        dim3 g1((unsigned) (a.E / 16), (unsigned) ((a.T + 15) / 16));
+        hipLaunchKernelGGL(k_router_logits_lds, g1, dim3(256), 0, stream, a.W, a.x, a.x_stride, a.H, a.E, a.T, logits);
     } else {
         constexpr int EL = 4, TL = 4;
         dim3 g1((unsigned) ((a.E + 2 * EL - 1) / (2 * EL)), (unsigned) ((a.T + 4 * TL - 1) / (4 * TL)));

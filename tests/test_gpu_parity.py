@@ -223,7 +223,10 @@ def test_group_by_expert(orc, T, k, n_as, dup):
 @pytest.mark.parametrize("H,E,k,T", [(2048, 128, 8, 1), (2048, 128, 8, 5), (4096, 128, 8, 3), (2048, 128, 8, 64),
                                      (512, 16, 4, 9), (2052, 64, 6, 2), (8192, 64, 4, 2),
                                      # T > 16 (the tiled logits kernel): partial expert and token tiles, H tails
-                                     (1004, 24, 3, 70), (2052, 64, 6, 37), (4096, 128, 8, 100)])
+                                     (1004, 24, 3, 70), (2052, 64, 6, 37), (4096, 128, 8, 100),
+                                     # T > 16, H % 512 == 0, E % 16 == 0 (the LDS-staged logits kernel):
+                                     # one or more chunks, partial token tiles
+                                     (512, 32, 4, 33), (2048, 48, 6, 20)])
 def test_router_bit_exact(orc, H, E, k, T):
     note(f"router H={H} E={E} k={k} T={T}")
     rng = np.random.default_rng(H + E + T)
