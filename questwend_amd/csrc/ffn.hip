@@ -253,10 +253,68 @@ __global__ void __launch_bounds__(1024) k_weighted_sum_rms(const float* __restri
     for (int64_t h = threadIdx.x; h < H; h += 1024) xn[t * H + h] = ys[h] * scale;
 }
 
+// The same for T > 1 with H % 1024 == 0, one 256-thread block per token: thread i
+// forms outputs 4 i + 1024 m .. + 3 (16-byte loads, every expert's loads of a
+// group of eight issued together), each as k_weighted_sum_rms does for T > 1
+// (a multiply, then adds of the products in expert order).  The sum of squares
+// reads the outputs back from LDS in k_rms_norm's per-thread order.
+__global__ void __launch_bounds__(256) k_weighted_sum_rms4(const float* __restrict__ ex, const float* __restrict__ w,
+                                                           float* __restrict__ out, float* __restrict__ xn, int64_t H,
+                                                           int64_t k, float eps) {
+    extern __shared__ float ys[];
+    __shared__ double part[4];
+    const int64_t t = blockIdx.x;
+    const float* e0 = ex + t * k * H;
+    const float* wt = w + t * k;
+    const int tid = threadIdx.x;
+    for (int64_t h = 4 * tid; h < H; h += 1024) {
+        float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int64_t j0 = 0; j0 < k; j0 += 8) {
+            float4 ev[8];
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) ev[jj] = *(const float4*) (e0 + (j0 + jj < k ? j0 + jj : k - 1) * H + h);
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) {
+                const int64_t j = j0 + jj;
+                if (j >= k) break;
+                const float wj = wt[j];
+                if (j == 0) acc = float4{ev[jj].x * wj, ev[jj].y * wj, ev[jj].z * wj, ev[jj].w * wj};
+                else
+                    acc = float4{acc.x + ev[jj].x * wj, acc.y + ev[jj].y * wj, acc.z + ev[jj].z * wj,
+                                 acc.w + ev[jj].w * wj};
+            }
+        }
+        *(float4*) (out + t * H + h) = acc;
+        *(float4*) (ys + h) = acc;
+    }
+    __syncthreads();
+    double s = 0.0;
+    for (int64_t h = tid; h < H; h += 256) {
+        const float v = ys[h];
+        s += (double) (v * v);
+    }
+    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+    if ((tid & 63) == 0) part[tid >> 6] = s;
+    __syncthreads();
+    const double tot = (part[0] + part[1]) + (part[2] + part[3]);
+    const float mean = (float) (tot / (double) H);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    for (int64_t h = 4 * tid; h < H; h += 1024) {
+        const float4 v = *(const float4*) (ys + h);
+        *(float4*) (xn + t * H + h) = float4{v.x * scale, v.y * scale, v.z * scale, v.w * scale};
+    }
+}
+
 int launch_weighted_sum_rms(const float* experts, const float* weights, float* out, float* x_next, int64_t H,
                             int64_t k, int64_t T, float eps, hipStream_t stream) {
     if (T == 0) return 0;
     if ((size_t) H * 4 > 64 * 1024) return -2;
+    if (T > 1 && H % 1024 == 0 && k >= 1 && ((uintptr_t) experts & 15) == 0 && ((uintptr_t) out & 15) == 0 &&
+        ((uintptr_t) x_next & 15) == 0) {
+        hipLaunchKernelGGL(k_weighted_sum_rms4, dim3((unsigned) T), dim3(256), (size_t) H * 4, stream, experts, weights,
+                           out, x_next, H, k, eps);
+        return hipGetLastError() == hipSuccess ? 0 : -3;
+    }
     hipLaunchKernelGGL(k_weighted_sum_rms, dim3((unsigned) T), dim3(1024), (size_t) H * 4, stream, experts, weights,
                        out, x_next, H, k, T, eps);
     return hipGetLastError() == hipSuccess ? 0 : -3;
