@@ -104,15 +104,18 @@ __device__ __forceinline__ void group_body(const GroupArgs& g, int32_t* s_hist, 
     }
     __syncthreads();
     // phase A: per-slice histogram; the first lane of each key in a chunk adds
-    // the chunk's count for it
+    // the chunk's count for it.  A slice of at most GROUP_UNROLL chunks keeps its
+    // keys and in-chunk ranks in registers for phase C (one pass of each loop).
+    const bool one = f1 - f0 <= GROUP_UNROLL * 64;   // (uniform)
+    int t[GROUP_UNROLL], e[GROUP_UNROLL], key[GROUP_UNROLL];
+    ChunkRank rk[GROUP_UNROLL];
     for (int c = f0; c < f1; c += GROUP_UNROLL * 64) {
-        int t[GROUP_UNROLL], e[GROUP_UNROLL], key[GROUP_UNROLL];
 #pragma unroll
         for (int u = 0; u < GROUP_UNROLL; ++u) key[u] = pair_key(g, c + 64 * u + lane, f1, t[u], e[u], true);
 #pragma unroll
         for (int u = 0; u < GROUP_UNROLL; ++u) {
-            const ChunkRank r = chunk_rank(key[u], nbits);
-            if (key[u] >= 0 && r.rank == 0) hist_add<IN_LDS>(hist + key[u], r.cnt);
+            rk[u] = chunk_rank(key[u], nbits);
+            if (key[u] >= 0 && rk[u].rank == 0) hist_add<IN_LDS>(hist + key[u], rk[u].cnt);
         }
     }
     __syncthreads();
@@ -178,12 +181,15 @@ __device__ __forceinline__ void group_body(const GroupArgs& g, int32_t* s_hist, 
     // phase C: stable scatter of (e, t) pairs: the first lane of each key takes
     // the chunk's positions from the slice cursor, the others offset by rank
     for (int c = f0; c < f1; c += GROUP_UNROLL * 64) {
-        int t[GROUP_UNROLL], e[GROUP_UNROLL], key[GROUP_UNROLL];
+        if (!one) {
 #pragma unroll
-        for (int u = 0; u < GROUP_UNROLL; ++u) key[u] = pair_key(g, c + 64 * u + lane, f1, t[u], e[u], false);
+            for (int u = 0; u < GROUP_UNROLL; ++u) key[u] = pair_key(g, c + 64 * u + lane, f1, t[u], e[u], false);
+#pragma unroll
+            for (int u = 0; u < GROUP_UNROLL; ++u) rk[u] = chunk_rank(key[u], nbits);
+        }
 #pragma unroll
         for (int u = 0; u < GROUP_UNROLL; ++u) {
-            const ChunkRank r = chunk_rank(key[u], nbits);
+            const ChunkRank r = rk[u];
             int32_t base = 0;
             if (key[u] >= 0 && r.rank == 0) base = hist_add<IN_LDS>(hist + key[u], r.cnt);
             base = __shfl(base, r.first & 63);
